@@ -1,0 +1,232 @@
+/*
+ * nnhip.h — C ABI of libnn-hip.so, the MI355X (gfx950) engine for neuralnet.cpp's
+ * BitNet b1.58 BitLinear W1.58A8 hot path.
+ *
+ * Plain C: opaque handles, device pointers as void / scalar pointers, sizes as size_t,
+ * a status enum and a thread-local last-error string. No HIP or torch types appear here.
+ *
+ * The reference exposes this path as C++ virtual methods of nn::ComputeEngine (NVI public
+ * entry -> protected *_impl), implemented in the engine submodule (compute.neuralnet.cpp);
+ * the C++ layer of this library (nn::HipEngine, neuralnet.cpp_amd/host) implements that
+ * interface on top of these entry points. Each declaration names the reference interface
+ * it replaces (file:line of the reference call site / contract, relative to the reference
+ * repository root).
+ *
+ * Layouts at this boundary follow the reference exactly:
+ *   W      (N, K)            f32 row-major, one output channel per row
+ *   tau    (N, 1)            f32 per-row absmean scale
+ *   wq     (N, ceil(K/16))   u32 words, 16 trits per word LSB first, code = trit + 2, tail code 2
+ *   X      (K, M)            f32 row-major; one column = one token
+ *   s      (1, M)            f32 per-token scale (absmax * fl(1/127))
+ *   xq     (K, ceil(M/4))    u32 words, 4 int8 per word little-endian, tail bytes 0
+ *   Y      (N, M)            f32 row-major
+ * The engine-internal layouts (repacked weights, token-major int8 activations) are
+ * described with the functions that produce them.
+ *
+ * Threading: one context = one HIP stream; calls on one context must not overlap
+ * (the reference's "one engine per thread" rule, docs/usage/07-thread-safety.md:9-17).
+ * All compute entry points are asynchronous on the context's stream.
+ */
+#ifndef NNHIP_H
+#define NNHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum nnhip_status
+{
+    NNHIP_OK = 0,
+    NNHIP_ERR_INVALID_ARG = 1, /* bad pointer, shape, or size */
+    NNHIP_ERR_HIP = 2,         /* a HIP runtime call or kernel launch failed */
+    NNHIP_ERR_OOM = 3,         /* device allocation failed */
+    NNHIP_ERR_NO_DEVICE = 4,   /* no usable gfx950 device */
+    NNHIP_ERR_UNSUPPORTED = 5  /* shape or option outside what the kernels support */
+} nnhip_status;
+
+typedef struct nnhip_ctx nnhip_ctx;
+typedef struct nnhip_group nnhip_group;
+
+/* ------------------------------------------------------------ runtime */
+
+/* Message of the last failed call on this thread ("" if none).
+ * Replaces nn::last_error() (modules/nn.engine.cpp:36-48). */
+const char* nnhip_last_error(void);
+
+/* Library version string, e.g. "nnhip 0.1.0 gfx950". */
+const char* nnhip_version(void);
+
+/* Number of visible HIP devices. */
+nnhip_status nnhip_device_count(int* count);
+
+/* Create a context bound to `device` with its own stream (default priority).
+ * Replaces nn::create_gpu_engine(const char* device) (cli/cli_engine_factory.hpp:51-76). */
+nnhip_status nnhip_ctx_create(int device, nnhip_ctx** out);
+nnhip_status nnhip_ctx_destroy(nnhip_ctx* ctx);
+
+/* Use an external hipStream_t (passed as void*) for all later calls; NULL selects the
+ * device's null (legacy default) stream. The caller keeps the external stream alive.
+ * nnhip_ctx_reset_stream goes back to the context's own stream. */
+nnhip_status nnhip_ctx_set_stream(nnhip_ctx* ctx, void* stream);
+nnhip_status nnhip_ctx_reset_stream(nnhip_ctx* ctx);
+nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream);
+
+/* Block the host until all work queued on the context's stream has finished.
+ * Replaces ComputeEngine::end_batch()/flush_batch() waits (compute_layer_gpt.hpp:715-719). */
+nnhip_status nnhip_sync(nnhip_ctx* ctx);
+
+/* Device memory (hipMalloc/hipFree on the context's device). */
+nnhip_status nnhip_malloc(nnhip_ctx* ctx, size_t bytes, void** out);
+nnhip_status nnhip_free(nnhip_ctx* ctx, void* ptr);
+
+/* Copies, ordered on the context's stream. h2d/d2h return after the copy completed
+ * (the host buffer may be reused). Replace ComputeEngine::from_matrix/to_matrix transfers
+ * (src/test_common.hpp:68-92). */
+nnhip_status nnhip_memcpy_h2d(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes);
+nnhip_status nnhip_memcpy_d2h(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes);
+nnhip_status nnhip_memcpy_d2d(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* Fill `words` u32 words with `value` using a kernel (safe inside a captured graph). */
+nnhip_status nnhip_fill_u32(nnhip_ctx* ctx, void* dst, uint32_t value, size_t words);
+
+/* ------------------------------------------- reference-layout primitives */
+
+/* tau[n] = sum_k fl(|W[n,k]| * fl(1/K)), fixed order: 64 lanes, lane l sums k = l, l+64, ...
+ * ascending, then a xor butterfly 32,16,8,4,2,1.
+ * Replaces dsl::compute_reduce_into(row_reduce_sum(abs(W)*rparam(1/K)))
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:637-640). */
+nnhip_status nnhip_row_absmean(nnhip_ctx* ctx, const float* W, size_t N, size_t K, float* tau);
+
+/* wq = trit_pack(W, tau): code 3 if w > 0.5*tau[n], 1 if w < -0.5*tau[n], else 2.
+ * Replaces ComputeEngine::trit_pack / trit_pack_into
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:305, :650; src/ternary_gemm_test.cpp:224-251). */
+nnhip_status nnhip_trit_pack(nnhip_ctx* ctx, const float* W, const float* tau, size_t N, size_t K,
+                             uint32_t* wq);
+
+/* out[c] = max over rows of x[r,c] (NaN ignored; -inf for rows == 0).
+ * Replaces ComputeEngine::col_reduce_max (include/neuralnet.cpp/compute_layer_bitlinear.hpp:445). */
+nnhip_status nnhip_col_reduce_max(nnhip_ctx* ctx, const float* x, size_t rows, size_t cols,
+                                  float* out);
+
+/* out[i] = |x[i]| (out may alias x). Replaces dsl::compute(abs(X))
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:443). */
+nnhip_status nnhip_abs(nnhip_ctx* ctx, const float* x, size_t n, float* out);
+
+/* x[i] = x[i] * alpha. Replaces ComputeEngine::scale_inplace
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:446). */
+nnhip_status nnhip_scale_inplace(nnhip_ctx* ctx, float* x, size_t n, float alpha);
+
+/* s[m] = (max_k |X[k,m]|) * fl(1/127): the three calls above fused into one kernel. */
+nnhip_status nnhip_act_scale(nnhip_ctx* ctx, const float* X, size_t K, size_t M, float* s);
+
+/* out (rows, ceil(cols/4)) = quantize_i8(x (rows, cols), scale, col_scale):
+ * q = round_half_away(clamp(x/s, -127, 127)), NaN -> 0, s == 0 -> 0; scale is (1, cols)
+ * when col_scale != 0, else (rows, 1). Replaces ComputeEngine::quantize_i8
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:448; src/int8_act_test.cpp:86-137). */
+nnhip_status nnhip_quantize_i8(nnhip_ctx* ctx, const float* x, const float* scale, size_t rows,
+                               size_t cols, int col_scale, uint32_t* out);
+
+/* out (rows, cols) f32 integers from the int8 container (rows, ceil(cols/4)).
+ * Replaces ComputeEngine::unpack_i8 (include/neuralnet.cpp/compute_layer_bitlinear.hpp:516;
+ * src/int8_act_test.cpp:140-168). */
+nnhip_status nnhip_unpack_i8(nnhip_ctx* ctx, const uint32_t* packed, size_t rows, size_t cols,
+                             float* out);
+
+/* Y (N, M) = (tau[n] * s[m]) * float(sum_k trit(n,k) * q(k,m)), int32 accumulation.
+ * Reference-layout operands; internally repacks wq and transposes xq into workspace owned
+ * by the context (grown on demand), then runs the same kernels as nnhip_ternary_matmul.
+ * Replaces ComputeEngine::matmul_q_i8 (include/neuralnet.cpp/compute_layer_bitlinear.hpp:454;
+ * contract docs/internal/21-quantized-weights.md:978-980; src/int8_act_test.cpp:171-238). */
+nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* tau,
+                               const uint32_t* xq, const float* s, size_t N, size_t K, size_t M,
+                               float* Y);
+
+/* Y[n, m] = Y[n, m] + b[n]. Replaces dsl::compute(leaf(y) + row_broadcast(b))
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:455-456). */
+nnhip_status nnhip_add_row_broadcast(nnhip_ctx* ctx, float* Y, const float* b, size_t N, size_t M);
+
+/* out (F, M) = RMSNorm(X (F, M)) with gain gamma (F): rms_inv = 1/sqrt(sum_f x^2 * fl(1/F) + eps)
+ * (sum in the fixed 64-part butterfly order), out = (x * rms_inv) * gamma[f].
+ * Replaces RMSNorm::forward (include/neuralnet.cpp/compute_layer_mlp.hpp:686-707). */
+nnhip_status nnhip_rmsnorm(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t F,
+                           size_t M, float* out);
+
+/* --------------------------------------------- MI355X-native fast path */
+
+/* Repacked ternary weights, layout T16K256: rows padded to 16, k padded to 256; one
+ * 1 KiB tile per (16 rows x 256 k) in row-tile-major order, each tile holding in lane
+ * order the A operands of four 16x16x64 int8 MFMAs (see nn_oracle.c for the bit map).
+ * Bytes needed for N x K weights: */
+size_t nnhip_repacked_bytes(size_t N, size_t K);
+
+/* Load-time repacker: reference container wq (N, ceil(K/16)) -> T16K256 (rp, 16-byte
+ * aligned, nnhip_repacked_bytes(N, K) bytes). Lossless: nnhip_unrepack_ternary inverts it
+ * bit for bit (including the tail codes of the last word of each row). No reference
+ * counterpart (engine-internal layout; the reference consumes wq directly). */
+nnhip_status nnhip_repack_ternary(nnhip_ctx* ctx, const uint32_t* wq, size_t N, size_t K, void* rp);
+nnhip_status nnhip_unrepack_ternary(nnhip_ctx* ctx, const void* rp, size_t N, size_t K, uint32_t* wq);
+
+/* Token-major int8 activations ("xi"): M rows of Kp = roundup(K, 256) bytes, row m holds the
+ * quantized token m in natural k order, bytes K..Kp-1 are 0; plus rowsum[m] = sum_k q(k, m)
+ * (int32). Bytes needed for xi: */
+size_t nnhip_act_i8_bytes(size_t K, size_t M);
+
+/* Fused abs -> per-token absmax -> scale -> int8 quantization of X (K, M) (reference layout):
+ * s[m] = max_k |X[k,m]| * fl(1/127); xi, rowsum as above. xq_ref (nullable) also receives
+ * the reference container (K, ceil(M/4)). Replaces the sequence of
+ * include/neuralnet.cpp/compute_layer_bitlinear.hpp:443-448 with one kernel. */
+nnhip_status nnhip_act_quant_i8(nnhip_ctx* ctx, const float* X, size_t K, size_t M, int8_t* xi,
+                                float* s, int32_t* rowsum, uint32_t* xq_ref);
+
+/* Fused RMSNorm -> absmax -> int8: as nnhip_rmsnorm followed by nnhip_act_quant_i8 on its
+ * output, without materializing the normalized tensor (bit-identical to that sequence).
+ * Replaces RMSNorm::forward + the BitLinear int8 prologue
+ * (compute_layer_mlp.hpp:686-707 + compute_layer_bitlinear.hpp:443-448). */
+nnhip_status nnhip_rmsnorm_quant_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps,
+                                    size_t F, size_t M, int8_t* xi, float* s, int32_t* rowsum,
+                                    uint32_t* xq_ref);
+
+/* Reference int8 container xq (K, ceil(M/4)) -> xi + rowsum (and back). */
+nnhip_status nnhip_act_i8_from_container(nnhip_ctx* ctx, const uint32_t* xq, size_t K, size_t M,
+                                         int8_t* xi, int32_t* rowsum);
+nnhip_status nnhip_act_i8_to_container(nnhip_ctx* ctx, const int8_t* xi, size_t K, size_t M,
+                                       uint32_t* xq);
+
+/* Ternary x int8 product on the fast layouts: Y (N, M) = (tau[n]*s[m]) * float(acc) [+ bias[n]],
+ * acc = sum_k trit(n,k) q(k,m) in int32 (exact). The bias add is a separate rounding (no FMA).
+ * M <= 16 runs the weight-streaming decode GEMV, larger M the MFMA GEMM. bias may be NULL.
+ * Replaces ComputeEngine::matmul_q_i8 + bias (compute_layer_bitlinear.hpp:454-456). */
+nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                  const float* s, const int32_t* rowsum, const float* bias, size_t N,
+                                  size_t K, size_t M, float* Y);
+
+/* Grouped decode GEMV: many independent (weights, activations) problems with M <= 16 in one
+ * launch, e.g. the q/k/v or gate/up projections of a layer, or a whole layer stack. The
+ * descriptors are copied to the device once at creation; run() launches one kernel. */
+typedef struct nnhip_gemv_desc
+{
+    const void* rp;        /* repacked weights (T16K256) */
+    const float* tau;      /* (N) */
+    const int8_t* xi;      /* (M, roundup(K,256)) */
+    const float* s;        /* (M) */
+    const int32_t* rowsum; /* (M) */
+    const float* bias;     /* (N) or NULL */
+    float* y;              /* (N, M) */
+    uint64_t N, K, M;
+} nnhip_gemv_desc;
+
+nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, size_t count,
+                                nnhip_group** out);
+nnhip_status nnhip_group_run(nnhip_ctx* ctx, nnhip_group* group);
+nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group);
+
+/* Number of waves the decode GEMV launches for `items` row tiles (for roofline accounting). */
+size_t nnhip_gemv_grid_waves(nnhip_ctx* ctx, size_t items);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NNHIP_H */

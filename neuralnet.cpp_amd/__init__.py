@@ -1,0 +1,390 @@
+"""Python binding (ctypes) of libnn-hip.so — the MI355X BitLinear W1.58A8 engine.
+
+The product is the C ABI in include/nnhip.h and the C++ nn:: engine layer built into the
+same library; this module is plumbing for the tests and bench.py. Device memory comes from
+torch (CUDA/HIP tensors), and every call runs on torch's current stream, so it is ordered
+with torch's own work. There is no CPU fallback: if libnn-hip.so is missing or no gfx950
+device is visible, the calls raise.
+
+The directory name contains a dot, so load it by path:
+    spec = importlib.util.spec_from_file_location(
+        "nnhip_py", "neuralnet.cpp_amd/__init__.py",
+        submodule_search_locations=["neuralnet.cpp_amd"])
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(_HERE, "libnn-hip.so")
+HEADER_PATH = os.path.join(ROOT, "include", "nnhip.h")
+
+TILE_K = 256
+TILE_ROWS = 16
+GEMV_MAX_M = 16
+
+
+class NNHipError(RuntimeError):
+    """A libnn-hip.so call returned a status other than NNHIP_OK."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[status {status}] {message}")
+        self.status = status
+
+
+def build(jobs: int = 8) -> None:
+    """Compile libnn-hip.so in-tree with neuralnet.cpp_amd/Makefile (hipcc, gfx950)."""
+    subprocess.run(["make", "-s", "-C", _HERE, f"-j{jobs}"], check=True)
+
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_st = ctypes.c_int
+_f = ctypes.c_float
+
+
+class GemvDesc(ctypes.Structure):
+    _fields_ = [("rp", _vp), ("tau", _vp), ("xi", _vp), ("s", _vp), ("rowsum", _vp),
+                ("bias", _vp), ("y", _vp), ("N", ctypes.c_uint64), ("K", ctypes.c_uint64),
+                ("M", ctypes.c_uint64)]
+
+
+# name -> (restype, argtypes); every nnhip_* symbol of include/nnhip.h
+SIGNATURES = {
+    "nnhip_last_error": (ctypes.c_char_p, []),
+    "nnhip_version": (ctypes.c_char_p, []),
+    "nnhip_device_count": (_st, [ctypes.POINTER(ctypes.c_int)]),
+    "nnhip_ctx_create": (_st, [ctypes.c_int, ctypes.POINTER(_vp)]),
+    "nnhip_ctx_destroy": (_st, [_vp]),
+    "nnhip_ctx_set_stream": (_st, [_vp, _vp]),
+    "nnhip_ctx_reset_stream": (_st, [_vp]),
+    "nnhip_ctx_get_stream": (_st, [_vp, ctypes.POINTER(_vp)]),
+    "nnhip_sync": (_st, [_vp]),
+    "nnhip_malloc": (_st, [_vp, _sz, ctypes.POINTER(_vp)]),
+    "nnhip_free": (_st, [_vp, _vp]),
+    "nnhip_memcpy_h2d": (_st, [_vp, _vp, _vp, _sz]),
+    "nnhip_memcpy_d2h": (_st, [_vp, _vp, _vp, _sz]),
+    "nnhip_memcpy_d2d": (_st, [_vp, _vp, _vp, _sz]),
+    "nnhip_fill_u32": (_st, [_vp, _vp, ctypes.c_uint32, _sz]),
+    "nnhip_row_absmean": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_trit_pack": (_st, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "nnhip_col_reduce_max": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_abs": (_st, [_vp, _vp, _sz, _vp]),
+    "nnhip_scale_inplace": (_st, [_vp, _vp, _sz, _f]),
+    "nnhip_act_scale": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_quantize_i8": (_st, [_vp, _vp, _vp, _sz, _sz, ctypes.c_int, _vp]),
+    "nnhip_unpack_i8": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_matmul_q_i8": (_st, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_add_row_broadcast": (_st, [_vp, _vp, _vp, _sz, _sz]),
+    "nnhip_rmsnorm": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _vp]),
+    "nnhip_repacked_bytes": (_sz, [_sz, _sz]),
+    "nnhip_repack_ternary": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_unrepack_ternary": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_act_i8_bytes": (_sz, [_sz, _sz]),
+    "nnhip_act_quant_i8": (_st, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "nnhip_rmsnorm_quant_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "nnhip_act_i8_from_container": (_st, [_vp, _vp, _sz, _sz, _vp, _vp]),
+    "nnhip_act_i8_to_container": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_ternary_matmul": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_group_create": (_st, [_vp, ctypes.POINTER(GemvDesc), _sz, ctypes.POINTER(_vp)]),
+    "nnhip_group_run": (_st, [_vp, _vp]),
+    "nnhip_group_destroy": (_st, [_vp, _vp]),
+    "nnhip_gemv_grid_waves": (_sz, [_vp, _sz]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libnn-hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NNHipError(-1, f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                                 "(make -C neuralnet.cpp_amd)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(status: int, fn: str) -> None:
+    if status != 0:
+        msg = lib().nnhip_last_error().decode(errors="replace")
+        raise NNHipError(status, msg or fn)
+
+
+def repacked_bytes(N: int, K: int) -> int:
+    return int(lib().nnhip_repacked_bytes(N, K))
+
+
+def act_i8_bytes(K: int, M: int) -> int:
+    return int(lib().nnhip_act_i8_bytes(K, M))
+
+
+def kp(K: int) -> int:
+    return (K + TILE_K - 1) // TILE_K * TILE_K
+
+
+class Context:
+    """One nnhip context (device + stream). Arguments are torch CUDA tensors."""
+
+    def __init__(self, device: int = 0):
+        import torch
+
+        self._torch = torch
+        if not torch.cuda.is_available():
+            raise NNHipError(4, "no GPU visible to torch")
+        self.device = device
+        h = _vp()
+        _check(lib().nnhip_ctx_create(device, ctypes.byref(h)), "nnhip_ctx_create")
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().nnhip_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- helpers
+    def _bind_stream(self) -> None:
+        s = self._torch.cuda.current_stream(self.device).cuda_stream
+        _check(lib().nnhip_ctx_set_stream(self.h, _vp(s)), "nnhip_ctx_set_stream")
+
+    def _dev(self, t, dtype=None, name="tensor"):
+        torch = self._torch
+        if t is None:
+            return None
+        if not t.is_cuda:
+            raise NNHipError(1, f"{name} must be a device tensor")
+        if not t.is_contiguous():
+            raise NNHipError(1, f"{name} must be contiguous")
+        if dtype is not None and t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+            raise NNHipError(1, f"{name} has dtype {t.dtype}, expected {dtype}")
+        return _vp(t.data_ptr())
+
+    def _empty(self, shape, dtype):
+        return self._torch.empty(shape, dtype=dtype, device=f"cuda:{self.device}")
+
+    def sync(self) -> None:
+        self._bind_stream()
+        _check(lib().nnhip_sync(self.h), "nnhip_sync")
+
+    # -- reference-layout primitives
+    def row_absmean(self, W):
+        torch = self._torch
+        N, K = W.shape
+        tau = self._empty((N,), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_row_absmean(self.h, self._dev(W, torch.float32, "W"), N, K,
+                                       self._dev(tau)), "nnhip_row_absmean")
+        return tau
+
+    def trit_pack(self, W, tau):
+        torch = self._torch
+        N, K = W.shape
+        wq = self._empty((N, (K + 15) // 16), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_trit_pack(self.h, self._dev(W, torch.float32, "W"),
+                                     self._dev(tau, torch.float32, "tau"), N, K, self._dev(wq)),
+               "nnhip_trit_pack")
+        return wq
+
+    def col_reduce_max(self, x):
+        torch = self._torch
+        rows, cols = x.shape
+        out = self._empty((cols,), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_col_reduce_max(self.h, self._dev(x, torch.float32, "x"), rows, cols,
+                                          self._dev(out)), "nnhip_col_reduce_max")
+        return out
+
+    def abs(self, x, out=None):
+        torch = self._torch
+        out = self._empty(x.shape, torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_abs(self.h, self._dev(x, torch.float32, "x"), x.numel(), self._dev(out)),
+               "nnhip_abs")
+        return out
+
+    def scale_inplace(self, x, alpha: float):
+        self._bind_stream()
+        _check(lib().nnhip_scale_inplace(self.h, self._dev(x, self._torch.float32, "x"), x.numel(),
+                                         alpha), "nnhip_scale_inplace")
+        return x
+
+    def act_scale(self, X):
+        torch = self._torch
+        K, M = X.shape
+        s = self._empty((M,), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_act_scale(self.h, self._dev(X, torch.float32, "X"), K, M, self._dev(s)),
+               "nnhip_act_scale")
+        return s
+
+    def quantize_i8(self, x, scale, col_scale: bool = True):
+        torch = self._torch
+        rows, cols = x.shape
+        out = self._empty((rows, (cols + 3) // 4), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_quantize_i8(self.h, self._dev(x, torch.float32, "x"),
+                                       self._dev(scale, torch.float32, "scale"), rows, cols,
+                                       int(col_scale), self._dev(out)), "nnhip_quantize_i8")
+        return out
+
+    def unpack_i8(self, packed, cols: int):
+        torch = self._torch
+        rows = packed.shape[0]
+        out = self._empty((rows, cols), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_unpack_i8(self.h, self._dev(packed, torch.int32, "packed"), rows, cols,
+                                     self._dev(out)), "nnhip_unpack_i8")
+        return out
+
+    def matmul_q_i8(self, wq, tau, xq, s, K: int, M: int):
+        torch = self._torch
+        N = wq.shape[0]
+        Y = self._empty((N, M), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_matmul_q_i8(self.h, self._dev(wq, torch.int32, "wq"),
+                                       self._dev(tau, torch.float32, "tau"),
+                                       self._dev(xq, torch.int32, "xq"),
+                                       self._dev(s, torch.float32, "s"), N, K, M, self._dev(Y)),
+               "nnhip_matmul_q_i8")
+        return Y
+
+    def add_row_broadcast(self, Y, b):
+        torch = self._torch
+        N, M = Y.shape
+        self._bind_stream()
+        _check(lib().nnhip_add_row_broadcast(self.h, self._dev(Y, torch.float32, "Y"),
+                                             self._dev(b, torch.float32, "b"), N, M),
+               "nnhip_add_row_broadcast")
+        return Y
+
+    def rmsnorm(self, X, gamma, eps: float):
+        torch = self._torch
+        F, M = X.shape
+        out = self._empty((F, M), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_rmsnorm(self.h, self._dev(X, torch.float32, "X"),
+                                   self._dev(gamma, torch.float32, "gamma"), eps, F, M,
+                                   self._dev(out)), "nnhip_rmsnorm")
+        return out
+
+    # -- fast path
+    def repack(self, wq, K: int):
+        torch = self._torch
+        N = wq.shape[0]
+        rp = self._empty((repacked_bytes(N, K) // 4,), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_repack_ternary(self.h, self._dev(wq, torch.int32, "wq"), N, K,
+                                          self._dev(rp)), "nnhip_repack_ternary")
+        return rp
+
+    def unrepack(self, rp, N: int, K: int):
+        torch = self._torch
+        wq = self._empty((N, (K + 15) // 16), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_unrepack_ternary(self.h, self._dev(rp, torch.int32, "rp"), N, K,
+                                            self._dev(wq)), "nnhip_unrepack_ternary")
+        return wq
+
+    def _act_out(self, K: int, M: int):
+        torch = self._torch
+        xi = self._empty((M, kp(K)), torch.int8)
+        s = self._empty((M,), torch.float32)
+        rs = self._empty((M,), torch.int32)
+        return xi, s, rs
+
+    def act_quant_i8(self, X, want_container: bool = False):
+        torch = self._torch
+        K, M = X.shape
+        xi, s, rs = self._act_out(K, M)
+        xq = self._empty((K, (M + 3) // 4), torch.int32) if want_container else None
+        self._bind_stream()
+        _check(lib().nnhip_act_quant_i8(self.h, self._dev(X, torch.float32, "X"), K, M,
+                                        self._dev(xi), self._dev(s), self._dev(rs),
+                                        self._dev(xq) if xq is not None else None),
+               "nnhip_act_quant_i8")
+        return (xi, s, rs, xq) if want_container else (xi, s, rs)
+
+    def rmsnorm_quant_i8(self, X, gamma, eps: float, want_container: bool = False):
+        torch = self._torch
+        F, M = X.shape
+        xi, s, rs = self._act_out(F, M)
+        xq = self._empty((F, (M + 3) // 4), torch.int32) if want_container else None
+        self._bind_stream()
+        _check(lib().nnhip_rmsnorm_quant_i8(self.h, self._dev(X, torch.float32, "X"),
+                                            self._dev(gamma, torch.float32, "gamma"), eps, F, M,
+                                            self._dev(xi), self._dev(s), self._dev(rs),
+                                            self._dev(xq) if xq is not None else None),
+               "nnhip_rmsnorm_quant_i8")
+        return (xi, s, rs, xq) if want_container else (xi, s, rs)
+
+    def act_from_container(self, xq, K: int, M: int):
+        torch = self._torch
+        xi, _, rs = self._act_out(K, M)
+        self._bind_stream()
+        _check(lib().nnhip_act_i8_from_container(self.h, self._dev(xq, torch.int32, "xq"), K, M,
+                                                 self._dev(xi), self._dev(rs)),
+               "nnhip_act_i8_from_container")
+        return xi, rs
+
+    def act_to_container(self, xi, K: int, M: int):
+        torch = self._torch
+        xq = self._empty((K, (M + 3) // 4), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_act_i8_to_container(self.h, self._dev(xi, torch.int8, "xi"), K, M,
+                                               self._dev(xq)), "nnhip_act_i8_to_container")
+        return xq
+
+    def ternary_matmul(self, rp, tau, xi, s, rowsum, N: int, K: int, M: int, bias=None, out=None):
+        torch = self._torch
+        Y = self._empty((N, M), torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul(self.h, self._dev(rp, torch.int32, "rp"),
+                                          self._dev(tau, torch.float32, "tau"),
+                                          self._dev(xi, torch.int8, "xi"),
+                                          self._dev(s, torch.float32, "s"),
+                                          self._dev(rowsum, torch.int32, "rowsum"),
+                                          self._dev(bias, torch.float32, "bias"), N, K, M,
+                                          self._dev(Y, torch.float32, "Y")),
+               "nnhip_ternary_matmul")
+        return Y
+
+    def group_create(self, problems):
+        """problems: list of dicts with rp, tau, xi, s, rowsum, bias (or None), y, N, K, M."""
+        arr = (GemvDesc * len(problems))()
+        for i, p in enumerate(problems):
+            arr[i] = GemvDesc(p["rp"].data_ptr(), p["tau"].data_ptr(), p["xi"].data_ptr(),
+                              p["s"].data_ptr(), p["rowsum"].data_ptr(),
+                              p["bias"].data_ptr() if p.get("bias") is not None else None,
+                              p["y"].data_ptr(), p["N"], p["K"], p["M"])
+        h = _vp()
+        self._bind_stream()
+        _check(lib().nnhip_group_create(self.h, arr, len(problems), ctypes.byref(h)),
+               "nnhip_group_create")
+        return h
+
+    def group_run(self, h) -> None:
+        self._bind_stream()
+        _check(lib().nnhip_group_run(self.h, h), "nnhip_group_run")
+
+    def group_destroy(self, h) -> None:
+        self._bind_stream()
+        _check(lib().nnhip_group_destroy(self.h, h), "nnhip_group_destroy")
+
+    def gemv_grid_waves(self, items: int) -> int:
+        return int(lib().nnhip_gemv_grid_waves(self.h, items))

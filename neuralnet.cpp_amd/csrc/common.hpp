@@ -1,0 +1,78 @@
+// common.hpp — shared declarations of libnn-hip.so (gfx950 only).
+//
+// Kernel launchers are host functions that enqueue on a given stream and return the
+// hipError_t of the launch; the C ABI (runtime.hip) validates arguments before calling them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace nnhip
+{
+
+constexpr int kWave = 64;
+
+// T16K256 repacked-weight geometry (see include/nnhip.h and oracle/nn_oracle.c).
+constexpr int kTileRows = 16;
+constexpr int kTileK = 256;
+constexpr int kTileWords = 256;  // 1 KiB per tile
+
+__host__ __device__ inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+__host__ __device__ inline size_t ceil_div(size_t v, size_t m) { return (v + m - 1) / m; }
+
+// 16-byte vector of u32 (a native clang vector, usable with the nontemporal builtins)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Largest M handled by the weight-streaming decode GEMV (one 16-token MFMA column block).
+constexpr int kGemvMaxM = 16;
+
+struct GemvProblem
+{
+    const u32x4* rp;
+    const float* tau;
+    const int8_t* xi;
+    const float* s;
+    const int32_t* rowsum;
+    const float* bias;
+    float* y;
+    int32_t N, K, M, KT;  // KT = Kp / 256
+};
+
+// ---- reference-layout kernels (k_ref.hip)
+hipError_t launch_fill_u32(hipStream_t st, uint32_t* dst, uint32_t value, size_t words);
+hipError_t launch_row_absmean(hipStream_t st, const float* W, size_t N, size_t K, float* tau);
+hipError_t launch_trit_pack(hipStream_t st, const float* W, const float* tau, size_t N, size_t K,
+                            uint32_t* wq);
+hipError_t launch_col_reduce_max(hipStream_t st, const float* x, size_t rows, size_t cols,
+                                 float* out, bool absval, float post_scale);
+hipError_t launch_abs(hipStream_t st, const float* x, size_t n, float* out);
+hipError_t launch_scale(hipStream_t st, float* x, size_t n, float alpha);
+hipError_t launch_quantize_i8(hipStream_t st, const float* x, const float* scale, size_t rows,
+                              size_t cols, bool col_scale, uint32_t* out);
+hipError_t launch_unpack_i8(hipStream_t st, const uint32_t* packed, size_t rows, size_t cols,
+                            float* out);
+hipError_t launch_add_row_broadcast(hipStream_t st, float* Y, const float* b, size_t N, size_t M);
+
+// ---- activation kernels (k_act.hip)
+hipError_t launch_rmsnorm(hipStream_t st, const float* X, const float* gamma, float eps, size_t F,
+                          size_t M, float* out);
+hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, bool norm, float eps,
+                            size_t K, size_t M, int8_t* xi, float* s, int32_t* rowsum,
+                            uint32_t* xq_ref);
+hipError_t launch_act_from_container(hipStream_t st, const uint32_t* xq, size_t K, size_t M,
+                                     int8_t* xi, int32_t* rowsum);
+hipError_t launch_act_to_container(hipStream_t st, const int8_t* xi, size_t K, size_t M,
+                                   uint32_t* xq);
+
+// ---- ternary kernels (k_ternary.hip)
+hipError_t launch_repack(hipStream_t st, const uint32_t* wq, size_t N, size_t K, uint32_t* rp);
+hipError_t launch_unrepack(hipStream_t st, const uint32_t* rp, size_t N, size_t K, uint32_t* wq);
+hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus);
+hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const uint32_t* d_items,
+                               size_t n_items, int num_cus);
+size_t gemv_grid_waves(size_t n_items, int num_cus);
+hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus);
+
+}  // namespace nnhip

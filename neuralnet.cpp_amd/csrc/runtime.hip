@@ -1,0 +1,626 @@
+// runtime.hip — the C ABI of libnn-hip.so (include/nnhip.h): contexts, memory, argument
+// validation and dispatch to the gfx950 kernels. Every entry point validates its arguments
+// on the host (null pointers, shapes, alignment, the kernels' size limits) before any launch,
+// and reports failures through the status code and the thread-local last-error string.
+#include "nnhip.h"
+
+#include "common.hpp"
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace nnhip;
+
+struct nnhip_ctx
+{
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;  // workspace of the reference-layout matmul_q_i8 path
+    size_t ws_bytes = 0;
+};
+
+struct nnhip_group
+{
+    GemvProblem* d_probs = nullptr;
+    uint32_t* d_items = nullptr;
+    size_t n_items = 0;
+};
+
+namespace
+{
+
+thread_local std::string g_err;
+
+nnhip_status fail(nnhip_status st, const char* fn, const std::string& msg)
+{
+    g_err = std::string(fn) + ": " + msg;
+    return st;
+}
+
+nnhip_status hip_fail(const char* fn, const char* what, hipError_t e)
+{
+    return fail(NNHIP_ERR_HIP, fn, std::string(what) + " failed: " + hipGetErrorString(e));
+}
+
+#define NNHIP_CHECK_CTX(fn)                                                  \
+    do                                                                       \
+    {                                                                        \
+        if (!ctx) return fail(NNHIP_ERR_INVALID_ARG, fn, "null context");   \
+        const hipError_t se_ = hipSetDevice(ctx->device);                    \
+        if (se_ != hipSuccess) return hip_fail(fn, "hipSetDevice", se_);     \
+    } while (0)
+
+#define NNHIP_REQUIRE(cond, fn, msg)                                         \
+    do                                                                       \
+    {                                                                        \
+        if (!(cond)) return fail(NNHIP_ERR_INVALID_ARG, fn, msg);            \
+    } while (0)
+
+#define NNHIP_LAUNCH(fn, expr)                                               \
+    do                                                                       \
+    {                                                                        \
+        const hipError_t le_ = (expr);                                       \
+        if (le_ != hipSuccess) return hip_fail(fn, "kernel launch", le_);    \
+    } while (0)
+
+constexpr size_t kMaxDim = 0x7FFFFFFFull;  // kernels index rows/tokens with int32
+// The decode GEMV accumulates 16*sum(code*x) in int32: 16 * 381 * K < 2^31.
+constexpr size_t kMaxK = 262144;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool mul_ok(size_t a, size_t b) { return a == 0 || b <= SIZE_MAX / a; }
+
+nnhip_status ensure_ws(nnhip_ctx* ctx, size_t bytes, const char* fn)
+{
+    if (ctx->ws_bytes >= bytes) return NNHIP_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
+    if (ctx->ws)
+    {
+        e = hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+        if (e != hipSuccess) return hip_fail(fn, "hipFree", e);
+    }
+    e = hipMalloc(&ctx->ws, bytes);
+    if (e != hipSuccess)
+    {
+        ctx->ws = nullptr;
+        (void)hipGetLastError();
+        return fail(NNHIP_ERR_OOM, fn, "workspace allocation of " + std::to_string(bytes) + " bytes failed");
+    }
+    ctx->ws_bytes = bytes;
+    return NNHIP_OK;
+}
+
+nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
+{
+    NNHIP_REQUIRE(N <= kMaxDim && M <= kMaxDim, fn, "N and M must be below 2^31");
+    NNHIP_REQUIRE(K >= 1 && K <= kMaxK, fn, "K must be in [1, 262144]");
+    NNHIP_REQUIRE(ceil_div(N, 16) < (1u << 20), fn, "N must be below 2^24");
+    NNHIP_REQUIRE(mul_ok(round_up(K, kTileK), M) && mul_ok(N, M), fn, "size overflow");
+    return NNHIP_OK;
+}
+
+nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
+                        const int8_t* xi, const float* s, const int32_t* rowsum, const float* bias,
+                        size_t N, size_t K, size_t M, float* Y)
+{
+    GemvProblem p;
+    p.rp = static_cast<const u32x4*>(rp);
+    p.tau = tau;
+    p.xi = xi;
+    p.s = s;
+    p.rowsum = rowsum;
+    p.bias = bias;
+    p.y = Y;
+    p.N = (int32_t)N;
+    p.K = (int32_t)K;
+    p.M = (int32_t)M;
+    p.KT = (int32_t)ceil_div(K, kTileK);
+    if (M <= (size_t)kGemvMaxM)
+        NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
+    else
+        NNHIP_LAUNCH(fn, launch_gemm(ctx->stream, p, ctx->num_cus));
+    return NNHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* nnhip_last_error(void) { return g_err.c_str(); }
+
+const char* nnhip_version(void) { return "nnhip 0.1.0 gfx950"; }
+
+nnhip_status nnhip_device_count(int* count)
+{
+    if (!count) return fail(NNHIP_ERR_INVALID_ARG, "nnhip_device_count", "null output");
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess)
+    {
+        (void)hipGetLastError();
+        *count = 0;
+        return fail(NNHIP_ERR_NO_DEVICE, "nnhip_device_count", hipGetErrorString(e));
+    }
+    *count = n;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_create(int device, nnhip_ctx** out)
+{
+    const char* fn = "nnhip_ctx_create";
+    NNHIP_REQUIRE(out != nullptr, fn, "null output");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+    {
+        (void)hipGetLastError();
+        return fail(NNHIP_ERR_NO_DEVICE, fn, "no HIP device visible");
+    }
+    NNHIP_REQUIRE(device >= 0 && device < n, fn, "device index out of range");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(fn, "hipGetDeviceProperties", e);
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(NNHIP_ERR_NO_DEVICE, fn,
+                    std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950 only");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(fn, "hipSetDevice", e);
+    auto* ctx = new nnhip_ctx;
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+    if (e != hipSuccess)
+    {
+        delete ctx;
+        return hip_fail(fn, "hipStreamCreate", e);
+    }
+    ctx->stream = ctx->own;
+    *out = ctx;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_destroy(nnhip_ctx* ctx)
+{
+    const char* fn = "nnhip_ctx_destroy";
+    if (!ctx) return NNHIP_OK;
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+    if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_set_stream(nnhip_ctx* ctx, void* stream)
+{
+    NNHIP_CHECK_CTX("nnhip_ctx_set_stream");
+    ctx->stream = static_cast<hipStream_t>(stream);
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_reset_stream(nnhip_ctx* ctx)
+{
+    NNHIP_CHECK_CTX("nnhip_ctx_reset_stream");
+    ctx->stream = ctx->own;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream)
+{
+    NNHIP_CHECK_CTX("nnhip_ctx_get_stream");
+    NNHIP_REQUIRE(stream != nullptr, "nnhip_ctx_get_stream", "null output");
+    *stream = ctx->stream;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_sync(nnhip_ctx* ctx)
+{
+    NNHIP_CHECK_CTX("nnhip_sync");
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail("nnhip_sync", "hipStreamSynchronize", e);
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_malloc(nnhip_ctx* ctx, size_t bytes, void** out)
+{
+    const char* fn = "nnhip_malloc";
+    NNHIP_CHECK_CTX(fn);
+    NNHIP_REQUIRE(out != nullptr, fn, "null output");
+    *out = nullptr;
+    if (bytes == 0) return NNHIP_OK;
+    const hipError_t e = hipMalloc(out, bytes);
+    if (e != hipSuccess)
+    {
+        *out = nullptr;
+        (void)hipGetLastError();
+        return fail(NNHIP_ERR_OOM, fn, "allocation of " + std::to_string(bytes) + " bytes failed");
+    }
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_free(nnhip_ctx* ctx, void* ptr)
+{
+    NNHIP_CHECK_CTX("nnhip_free");
+    if (!ptr) return NNHIP_OK;
+    const hipError_t e = hipFree(ptr);
+    if (e != hipSuccess) return hip_fail("nnhip_free", "hipFree", e);
+    return NNHIP_OK;
+}
+
+static nnhip_status copy_sync(nnhip_ctx* ctx, const char* fn, void* dst, const void* src, size_t bytes,
+                              hipMemcpyKind kind)
+{
+    NNHIP_CHECK_CTX(fn);
+    if (bytes == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(dst && src, fn, "null pointer");
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, ctx->stream);
+    if (e != hipSuccess) return hip_fail(fn, "hipMemcpyAsync", e);
+    if (kind != hipMemcpyDeviceToDevice)
+    {
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
+    }
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_memcpy_h2d(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    return copy_sync(ctx, "nnhip_memcpy_h2d", dst, src, bytes, hipMemcpyHostToDevice);
+}
+
+nnhip_status nnhip_memcpy_d2h(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    return copy_sync(ctx, "nnhip_memcpy_d2h", dst, src, bytes, hipMemcpyDeviceToHost);
+}
+
+nnhip_status nnhip_memcpy_d2d(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    return copy_sync(ctx, "nnhip_memcpy_d2d", dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+nnhip_status nnhip_fill_u32(nnhip_ctx* ctx, void* dst, uint32_t value, size_t words)
+{
+    const char* fn = "nnhip_fill_u32";
+    NNHIP_CHECK_CTX(fn);
+    if (words == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(dst != nullptr, fn, "null pointer");
+    NNHIP_REQUIRE((reinterpret_cast<uintptr_t>(dst) & 3u) == 0, fn, "dst must be 4-byte aligned");
+    NNHIP_LAUNCH(fn, launch_fill_u32(ctx->stream, static_cast<uint32_t*>(dst), value, words));
+    return NNHIP_OK;
+}
+
+// ------------------------------------------------------------- reference-layout primitives
+
+nnhip_status nnhip_row_absmean(nnhip_ctx* ctx, const float* W, size_t N, size_t K, float* tau)
+{
+    const char* fn = "nnhip_row_absmean";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(K >= 1, fn, "K must be >= 1");
+    NNHIP_REQUIRE(W && tau, fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(N, K), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_row_absmean(ctx->stream, W, N, K, tau));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_trit_pack(nnhip_ctx* ctx, const float* W, const float* tau, size_t N, size_t K,
+                             uint32_t* wq)
+{
+    const char* fn = "nnhip_trit_pack";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || K == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(W && tau && wq, fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(N, K), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_trit_pack(ctx->stream, W, tau, N, K, wq));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_col_reduce_max(nnhip_ctx* ctx, const float* x, size_t rows, size_t cols, float* out)
+{
+    const char* fn = "nnhip_col_reduce_max";
+    NNHIP_CHECK_CTX(fn);
+    if (cols == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(out && (x || rows == 0), fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(rows, cols), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_col_reduce_max(ctx->stream, x, rows, cols, out, false, 1.0f));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_abs(nnhip_ctx* ctx, const float* x, size_t n, float* out)
+{
+    const char* fn = "nnhip_abs";
+    NNHIP_CHECK_CTX(fn);
+    if (n == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(x && out, fn, "null pointer");
+    NNHIP_LAUNCH(fn, launch_abs(ctx->stream, x, n, out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_scale_inplace(nnhip_ctx* ctx, float* x, size_t n, float alpha)
+{
+    const char* fn = "nnhip_scale_inplace";
+    NNHIP_CHECK_CTX(fn);
+    if (n == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(x != nullptr, fn, "null pointer");
+    NNHIP_LAUNCH(fn, launch_scale(ctx->stream, x, n, alpha));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_act_scale(nnhip_ctx* ctx, const float* X, size_t K, size_t M, float* s)
+{
+    const char* fn = "nnhip_act_scale";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(s && (X || K == 0), fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(K, M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_col_reduce_max(ctx->stream, X, K, M, s, true, 1.0f / 127.0f));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_quantize_i8(nnhip_ctx* ctx, const float* x, const float* scale, size_t rows,
+                               size_t cols, int col_scale, uint32_t* out)
+{
+    const char* fn = "nnhip_quantize_i8";
+    NNHIP_CHECK_CTX(fn);
+    if (rows == 0 || cols == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(x && scale && out, fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(rows, cols), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_quantize_i8(ctx->stream, x, scale, rows, cols, col_scale != 0, out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_unpack_i8(nnhip_ctx* ctx, const uint32_t* packed, size_t rows, size_t cols, float* out)
+{
+    const char* fn = "nnhip_unpack_i8";
+    NNHIP_CHECK_CTX(fn);
+    if (rows == 0 || cols == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(packed && out, fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(rows, cols), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_unpack_i8(ctx->stream, packed, rows, cols, out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* tau, const uint32_t* xq,
+                               const float* s, size_t N, size_t K, size_t M, float* Y)
+{
+    const char* fn = "nnhip_matmul_q_i8";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(wq && tau && xq && s && Y, fn, "null pointer");
+    const size_t rp_bytes = round_up(nnhip_repacked_bytes(N, K), 256);
+    const size_t xi_bytes = round_up(nnhip_act_i8_bytes(K, M), 256);
+    const size_t rs_bytes = round_up(M * sizeof(int32_t), 256);
+    st = ensure_ws(ctx, rp_bytes + xi_bytes + rs_bytes, fn);
+    if (st != NNHIP_OK) return st;
+    uint8_t* base = static_cast<uint8_t*>(ctx->ws);
+    uint32_t* rp = reinterpret_cast<uint32_t*>(base);
+    int8_t* xi = reinterpret_cast<int8_t*>(base + rp_bytes);
+    int32_t* rowsum = reinterpret_cast<int32_t*>(base + rp_bytes + xi_bytes);
+    NNHIP_LAUNCH(fn, launch_repack(ctx->stream, wq, N, K, rp));
+    NNHIP_LAUNCH(fn, launch_act_from_container(ctx->stream, xq, K, M, xi, rowsum));
+    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, nullptr, N, K, M, Y);
+}
+
+nnhip_status nnhip_add_row_broadcast(nnhip_ctx* ctx, float* Y, const float* b, size_t N, size_t M)
+{
+    const char* fn = "nnhip_add_row_broadcast";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(Y && b, fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(N, M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_add_row_broadcast(ctx->stream, Y, b, N, M));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_rmsnorm(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t F,
+                           size_t M, float* out)
+{
+    const char* fn = "nnhip_rmsnorm";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0 || F == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(X && gamma && out, fn, "null pointer");
+    NNHIP_REQUIRE(F <= kMaxDim && M <= kMaxDim && mul_ok(F, M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_rmsnorm(ctx->stream, X, gamma, eps, F, M, out));
+    return NNHIP_OK;
+}
+
+// ------------------------------------------------------------- MI355X-native fast path
+
+size_t nnhip_repacked_bytes(size_t N, size_t K)
+{
+    return round_up(N, kTileRows) * round_up(K, kTileK) / 4;
+}
+
+nnhip_status nnhip_repack_ternary(nnhip_ctx* ctx, const uint32_t* wq, size_t N, size_t K, void* rp)
+{
+    const char* fn = "nnhip_repack_ternary";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || K == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(wq && rp, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp), fn, "rp must be 16-byte aligned");
+    NNHIP_REQUIRE(mul_ok(round_up(N, 16), round_up(K, kTileK)), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_repack(ctx->stream, wq, N, K, static_cast<uint32_t*>(rp)));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_unrepack_ternary(nnhip_ctx* ctx, const void* rp, size_t N, size_t K, uint32_t* wq)
+{
+    const char* fn = "nnhip_unrepack_ternary";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || K == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(wq && rp, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp), fn, "rp must be 16-byte aligned");
+    NNHIP_LAUNCH(fn, launch_unrepack(ctx->stream, static_cast<const uint32_t*>(rp), N, K, wq));
+    return NNHIP_OK;
+}
+
+size_t nnhip_act_i8_bytes(size_t K, size_t M) { return round_up(K, kTileK) * M; }
+
+static nnhip_status act_quant_common(nnhip_ctx* ctx, const char* fn, const float* X, const float* gamma,
+                                     bool norm, float eps, size_t K, size_t M, int8_t* xi, float* s,
+                                     int32_t* rowsum, uint32_t* xq_ref)
+{
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(K >= 1 && K <= kMaxK && M <= kMaxDim, fn, "K must be in [1, 262144], M below 2^31");
+    NNHIP_REQUIRE(X && xi && s && rowsum && (gamma || !norm), fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
+    NNHIP_REQUIRE(mul_ok(round_up(K, kTileK), M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, norm, eps, K, M, xi, s, rowsum, xq_ref));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_act_quant_i8(nnhip_ctx* ctx, const float* X, size_t K, size_t M, int8_t* xi, float* s,
+                                int32_t* rowsum, uint32_t* xq_ref)
+{
+    return act_quant_common(ctx, "nnhip_act_quant_i8", X, nullptr, false, 0.0f, K, M, xi, s, rowsum,
+                            xq_ref);
+}
+
+nnhip_status nnhip_rmsnorm_quant_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps,
+                                    size_t F, size_t M, int8_t* xi, float* s, int32_t* rowsum,
+                                    uint32_t* xq_ref)
+{
+    return act_quant_common(ctx, "nnhip_rmsnorm_quant_i8", X, gamma, true, eps, F, M, xi, s, rowsum,
+                            xq_ref);
+}
+
+nnhip_status nnhip_act_i8_from_container(nnhip_ctx* ctx, const uint32_t* xq, size_t K, size_t M,
+                                         int8_t* xi, int32_t* rowsum)
+{
+    const char* fn = "nnhip_act_i8_from_container";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(K >= 1 && K <= kMaxK && M <= kMaxDim, fn, "K must be in [1, 262144], M below 2^31");
+    NNHIP_REQUIRE(xq && xi && rowsum, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
+    NNHIP_LAUNCH(fn, launch_act_from_container(ctx->stream, xq, K, M, xi, rowsum));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_act_i8_to_container(nnhip_ctx* ctx, const int8_t* xi, size_t K, size_t M, uint32_t* xq)
+{
+    const char* fn = "nnhip_act_i8_to_container";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0 || K == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(K <= kMaxK && M <= kMaxDim, fn, "K must be <= 262144, M below 2^31");
+    NNHIP_REQUIRE(xq && xi, fn, "null pointer");
+    NNHIP_LAUNCH(fn, launch_act_to_container(ctx->stream, xi, K, M, xq));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                  const float* s, const int32_t* rowsum, const float* bias, size_t N,
+                                  size_t K, size_t M, float* Y)
+{
+    const char* fn = "nnhip_ternary_matmul";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    const nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && tau && xi && s && rowsum && Y, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
+    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y);
+}
+
+nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, size_t count,
+                                nnhip_group** out)
+{
+    const char* fn = "nnhip_group_create";
+    NNHIP_CHECK_CTX(fn);
+    NNHIP_REQUIRE(out != nullptr, fn, "null output");
+    *out = nullptr;
+    NNHIP_REQUIRE(descs != nullptr || count == 0, fn, "null descriptors");
+    NNHIP_REQUIRE(count < (1u << 12), fn, "at most 4095 problems per group");
+    std::vector<GemvProblem> probs(count);
+    std::vector<uint32_t> items;
+    for (size_t i = 0; i < count; ++i)
+    {
+        const nnhip_gemv_desc& d = descs[i];
+        const nnhip_status st = check_matmul_shape(fn, d.N, d.K, d.M);
+        if (st != NNHIP_OK) return st;
+        NNHIP_REQUIRE(d.M >= 1 && d.M <= (uint64_t)kGemvMaxM, fn, "grouped GEMV needs 1 <= M <= 16");
+        NNHIP_REQUIRE(d.rp && d.tau && d.xi && d.s && d.rowsum && d.y, fn, "null pointer in descriptor");
+        NNHIP_REQUIRE(aligned16(d.rp) && aligned16(d.xi), fn, "rp and xi must be 16-byte aligned");
+        GemvProblem& p = probs[i];
+        p.rp = static_cast<const u32x4*>(d.rp);
+        p.tau = d.tau;
+        p.xi = d.xi;
+        p.s = d.s;
+        p.rowsum = d.rowsum;
+        p.bias = d.bias;
+        p.y = d.y;
+        p.N = (int32_t)d.N;
+        p.K = (int32_t)d.K;
+        p.M = (int32_t)d.M;
+        p.KT = (int32_t)ceil_div(d.K, kTileK);
+        const size_t rts = ceil_div(d.N, 16);
+        for (size_t rt = 0; rt < rts; ++rt) items.push_back((uint32_t)((i << 20) | rt));
+    }
+    NNHIP_REQUIRE(items.size() < 0x7FFFFFFFull, fn, "too many row tiles");
+    auto* grp = new nnhip_group;
+    grp->n_items = items.size();
+    if (count > 0)
+    {
+        hipError_t e = hipMalloc(&grp->d_probs, sizeof(GemvProblem) * count);
+        if (e == hipSuccess && !items.empty()) e = hipMalloc(&grp->d_items, sizeof(uint32_t) * items.size());
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(grp->d_probs, probs.data(), sizeof(GemvProblem) * count,
+                               hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess && !items.empty())
+            e = hipMemcpyAsync(grp->d_items, items.data(), sizeof(uint32_t) * items.size(),
+                               hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess)
+        {
+            if (grp->d_probs) (void)hipFree(grp->d_probs);
+            if (grp->d_items) (void)hipFree(grp->d_items);
+            delete grp;
+            return hip_fail(fn, "descriptor upload", e);
+        }
+    }
+    *out = grp;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_group_run(nnhip_ctx* ctx, nnhip_group* group)
+{
+    const char* fn = "nnhip_group_run";
+    NNHIP_CHECK_CTX(fn);
+    NNHIP_REQUIRE(group != nullptr, fn, "null group");
+    NNHIP_LAUNCH(fn, launch_gemv_grouped(ctx->stream, group->d_probs, group->d_items, group->n_items,
+                                         ctx->num_cus));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group)
+{
+    const char* fn = "nnhip_group_destroy";
+    NNHIP_CHECK_CTX(fn);
+    if (!group) return NNHIP_OK;
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (group->d_probs) (void)hipFree(group->d_probs);
+    if (group->d_items) (void)hipFree(group->d_items);
+    delete group;
+    if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
+    return NNHIP_OK;
+}
+
+size_t nnhip_gemv_grid_waves(nnhip_ctx* ctx, size_t items)
+{
+    return gemv_grid_waves(items, ctx ? ctx->num_cus : 256);
+}
+
+}  // extern "C"

@@ -1,0 +1,462 @@
+/*
+ * nn_oracle.c — CPU restatement of the BitLinear W1.58A8 path (TEST INFRASTRUCTURE).
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
+ * library, as the checker or as the timed CPU baseline. The shipped libnn-hip.so never
+ * links it. Citations are file:line in the reference repository (neuralnet.cpp v1.18.0).
+ *
+ * Build: oracle/Makefile, with -ffp-contract=off so that every fp32 multiply and add
+ * rounds on its own, as the reference's epilogue order requires.
+ */
+#include "nn_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ RNG */
+
+uint64_t orc_splitmix64(uint64_t* state)
+{
+    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static double orc_unit(uint64_t* st) /* (0, 1] */
+{
+    return ((double)(orc_splitmix64(st) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+
+static double orc_unit0(uint64_t* st) /* [0, 1) */
+{
+    return (double)(orc_splitmix64(st) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+void orc_fill_uniform(float* out, size_t n, uint64_t seed, float lo, float hi)
+{
+    uint64_t st = seed;
+    for (size_t i = 0; i < n; ++i)
+        out[i] = (float)((double)lo + ((double)hi - (double)lo) * orc_unit0(&st));
+}
+
+void orc_fill_normal(float* out, size_t n, uint64_t seed, float mean, float stddev)
+{
+    /* Box-Muller in double; one normal per pair of uniforms (simple and deterministic). */
+    uint64_t st = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; ++i)
+    {
+        const double u1 = orc_unit(&st);
+        const double u2 = orc_unit(&st);
+        const double z = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
+        out[i] = (float)((double)mean + (double)stddev * z);
+    }
+}
+
+/* ------------------------------------------------------- nn::trit_pack */
+
+/* words_per_row(K) = ceil(K/16): src/ternary_gemm_test.cpp:74-77 */
+size_t orc_trit_words_per_row(size_t K) { return (K + 15) / 16; }
+
+/* code_of(w, tau): 3 if w > 0.5*tau, 1 if w < -0.5*tau, else 2 (ties and NaN -> 2).
+ * src/ternary_gemm_test.cpp:79-89 (tau=1 KAT), include/neuralnet.cpp/compute_layer_bitlinear.hpp:657-667
+ * (strict |W| > 0.5 tau threshold). 0.5f*tau is exact in fp32. */
+uint32_t orc_trit_code(float w, float tau)
+{
+    const float h = 0.5f * tau;
+    if (w > h) return 3u;
+    if (w < -h) return 1u;
+    return 2u;
+}
+
+/* pack_row: trit j of the row at (word[j/16] >> 2*(j%16)) & 3, tail codes 2.
+ * src/ternary_gemm_test.cpp:79-99 and :224-251 (engine trit_pack == host pack_row). */
+void orc_trit_pack_row(const float* w, size_t K, float tau, uint32_t* words)
+{
+    const size_t wpr = orc_trit_words_per_row(K);
+    for (size_t wi = 0; wi < wpr; ++wi)
+    {
+        uint32_t word = 0;
+        for (size_t j = 0; j < 16; ++j)
+        {
+            const size_t k = wi * 16 + j;
+            const uint32_t code = (k < K) ? orc_trit_code(w[k], tau) : 2u;
+            word |= code << (2 * j);
+        }
+        words[wi] = word;
+    }
+}
+
+void orc_trit_pack(const float* W, const float* tau, size_t N, size_t K, uint32_t* out)
+{
+    const size_t wpr = orc_trit_words_per_row(K);
+    for (size_t n = 0; n < N; ++n) orc_trit_pack_row(W + n * K, K, tau[n], out + n * wpr);
+}
+
+/* at(words, i) = value_of(code) = code - 2: src/ternary_gemm_test.cpp:91-99 */
+int orc_trit_at(const uint32_t* words, size_t i)
+{
+    return (int)((words[i / 16] >> (2 * (i % 16))) & 3u) - 2;
+}
+
+/* --------------------------------------------------------- absmean tau */
+
+/* tau_o = sum_k fl(|W_ok| * fl(1/K)): include/neuralnet.cpp/compute_layer_bitlinear.hpp:627-640
+ * (row_reduce_sum(abs(W) * rparam(1/K))). The summation order inside the reference engine is
+ * not available; this build fixes one order, shared with the GPU kernel: 64 lanes, lane l sums
+ * k = l, l+64, ... in ascending order, then a xor butterfly over offsets 32,16,8,4,2,1. */
+void orc_row_absmean(const float* W, size_t N, size_t K, float* tau)
+{
+    const float inv_k = 1.0f / (float)K;
+    for (size_t n = 0; n < N; ++n)
+    {
+        float p[64];
+        for (int l = 0; l < 64; ++l)
+        {
+            float acc = 0.0f;
+            for (size_t k = (size_t)l; k < K; k += 64)
+            {
+                const float t = fabsf(W[n * K + k]) * inv_k;
+                acc = acc + t;
+            }
+            p[l] = acc;
+        }
+        for (int off = 32; off >= 1; off >>= 1)
+        {
+            float q[64];
+            for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ off];
+            memcpy(p, q, sizeof p);
+        }
+        tau[n] = p[0];
+    }
+}
+
+/* ---------------------------------------------------------- nn::i8_pack */
+
+size_t orc_i8_words_per_row(size_t cols) { return (cols + 3) / 4; }
+
+/* q = round_half_away(clamp(x/s, -127, 127)); NaN -> 0; s == 0 -> 0.
+ * docs/internal/21-quantized-weights.md:973-975; src/int8_act_test.cpp:86-137.
+ * x/s is a true IEEE division (the docs' formula). */
+int8_t orc_quantize_one(float x, float s)
+{
+    if (s == 0.0f || x != x) return 0;
+    float v = x / s;
+    if (v != v) return 0;
+    if (v > 127.0f) v = 127.0f;
+    if (v < -127.0f) v = -127.0f;
+    return (int8_t)roundf(v);
+}
+
+/* max_k |X[k][m]| per column, starting from 0 and ignoring NaN (a NaN never compares greater).
+ * src/int8_act_test.cpp:95-101 / src/layer_bench.cpp:609-615. */
+void orc_col_absmax(const float* X, size_t rows, size_t cols, float* mx)
+{
+    for (size_t c = 0; c < cols; ++c)
+    {
+        float m = 0.0f;
+        for (size_t r = 0; r < rows; ++r)
+        {
+            const float a = fabsf(X[r * cols + c]);
+            if (a > m) m = a;
+        }
+        mx[c] = m;
+    }
+}
+
+/* s = col_reduce_max(|X|) * fl(1/127): include/neuralnet.cpp/compute_layer_bitlinear.hpp:443-447
+ * (scale_inplace multiplies by the rounded reciprocal; it does not divide). */
+void orc_act_scale(const float* X, size_t rows, size_t cols, float* s)
+{
+    orc_col_absmax(X, rows, cols, s);
+    const float r127 = 1.0f / 127.0f;
+    for (size_t c = 0; c < cols; ++c) s[c] = s[c] * r127;
+}
+
+/* quantize_i8(x (rows, cols), scale, col_scale) -> (rows, ceil(cols/4)) words, byte c%4 of
+ * word c/4 (little-endian within the word), tail bytes 0. col_scale: scale is (1, cols),
+ * else (rows, 1). docs/internal/21-quantized-weights.md:973-975, src/int8_act_test.cpp:106-136 */
+void orc_quantize_i8(const float* x, const float* scale, size_t rows, size_t cols, int col_scale,
+                     uint32_t* out)
+{
+    const size_t wpr = orc_i8_words_per_row(cols);
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t wi = 0; wi < wpr; ++wi)
+        {
+            uint32_t word = 0;
+            for (size_t b = 0; b < 4; ++b)
+            {
+                const size_t c = wi * 4 + b;
+                if (c >= cols) break;
+                const float s = col_scale ? scale[c] : scale[r];
+                const int8_t q = orc_quantize_one(x[r * cols + c], s);
+                word |= (uint32_t)(uint8_t)q << (8 * b);
+            }
+            out[r * wpr + wi] = word;
+        }
+}
+
+int orc_i8_at(const uint32_t* words, size_t i)
+{
+    return (int)(int8_t)(uint8_t)((words[i / 4] >> (8 * (i % 4))) & 0xFFu);
+}
+
+/* unpack_i8(packed (rows, ceil(cols/4)), cols) -> f32 integers: src/int8_act_test.cpp:140-168 */
+void orc_unpack_i8(const uint32_t* packed, size_t rows, size_t cols, float* out)
+{
+    const size_t wpr = orc_i8_words_per_row(cols);
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) out[r * cols + c] = (float)orc_i8_at(packed + r * wpr, c);
+}
+
+/* ---------------------------------------------------------- matmul_q_i8 */
+
+/* acc[n][m] = sum_k value_of(code(n,k)) * q(k,m), k ascending, int32:
+ * src/int8_act_test.cpp:210-236 */
+void orc_matmul_q_i8_acc(const uint32_t* wq, const uint32_t* xq, size_t N, size_t K, size_t M,
+                         int32_t* acc)
+{
+    const size_t wpr_w = orc_trit_words_per_row(K);
+    const size_t wpr_q = orc_i8_words_per_row(M);
+    for (size_t n = 0; n < N; ++n)
+        for (size_t m = 0; m < M; ++m)
+        {
+            int32_t a = 0;
+            for (size_t k = 0; k < K; ++k)
+                a += orc_trit_at(wq + n * wpr_w, k) * orc_i8_at(xq + k * wpr_q, m);
+            acc[n * M + m] = a;
+        }
+}
+
+/* Y[n][m] = (tau_n * s_m) * float(acc): the epilogue order of src/int8_act_test.cpp:233
+ * (left-to-right: the two scales multiply first, then the converted accumulator). */
+void orc_matmul_q_i8(const uint32_t* wq, const float* tau, const uint32_t* xq, const float* s,
+                     size_t N, size_t K, size_t M, float* Y)
+{
+    int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * ((N * M) != 0 ? N * M : 1));
+    orc_matmul_q_i8_acc(wq, xq, N, K, M, acc);
+    for (size_t n = 0; n < N; ++n)
+        for (size_t m = 0; m < M; ++m)
+        {
+            const float ts = tau[n] * s[m];
+            Y[n * M + m] = ts * (float)acc[n * M + m];
+        }
+    free(acc);
+}
+
+/* CpuEngine restatement (AGENTS.md:178-179; docs/internal/21-quantized-weights.md:794-798):
+ * decode RB=64 weight rows into f32 scratch, decode the int8 activations once, then a dense
+ * f32 dot-product microkernel. Every partial sum is an integer of magnitude <= 127*K < 2^24,
+ * so the f32 arithmetic is exact and the result is bit-identical to the int32 loop.
+ * Returns 0, or -1 when 127*K >= 2^24 (exactness would not hold). */
+int orc_matmul_q_i8_rowblock(const uint32_t* wq, const float* tau, const uint32_t* xq,
+                             const float* s, size_t N, size_t K, size_t M, float* Y, int threads)
+{
+    if ((double)K * 127.0 >= 16777216.0) return -1;
+    enum { RB = 64 };
+    const size_t wpr_w = orc_trit_words_per_row(K);
+    const size_t wpr_q = orc_i8_words_per_row(M);
+    /* activations decoded token-major (M, K) so the microkernel is a unit-stride dot */
+    float* xd = (float*)malloc(sizeof(float) * ((M * K) != 0 ? M * K : 1));
+    for (size_t k = 0; k < K; ++k)
+        for (size_t m = 0; m < M; ++m) xd[m * K + k] = (float)orc_i8_at(xq + k * wpr_q, m);
+    const long nblocks = (long)((N + RB - 1) / RB);
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel
+#endif
+    {
+        float* wd = (float*)malloc(sizeof(float) * RB * (K ? K : 1));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (long blk = 0; blk < nblocks; ++blk)
+        {
+            const size_t n0 = (size_t)blk * RB;
+            const size_t nb = (N - n0 < RB) ? N - n0 : RB;
+            for (size_t r = 0; r < nb; ++r)
+            {
+                const uint32_t* row = wq + (n0 + r) * wpr_w;
+                float* dst = wd + r * K;
+                for (size_t wi = 0; wi < wpr_w; ++wi)
+                {
+                    const uint32_t word = row[wi];
+                    const size_t kend = (wi * 16 + 16 < K) ? 16 : K - wi * 16;
+                    for (size_t j = 0; j < kend; ++j)
+                        dst[wi * 16 + j] = (float)((int)((word >> (2 * j)) & 3u) - 2);
+                }
+            }
+            for (size_t r = 0; r < nb; ++r)
+            {
+                const float* wrow = wd + r * K;
+                for (size_t m = 0; m < M; ++m)
+                {
+                    const float* xrow = xd + m * K;
+                    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, a4 = 0.f, a5 = 0.f, a6 = 0.f,
+                          a7 = 0.f;
+                    size_t k = 0;
+                    for (; k + 8 <= K; k += 8)
+                    {
+                        a0 += wrow[k + 0] * xrow[k + 0];
+                        a1 += wrow[k + 1] * xrow[k + 1];
+                        a2 += wrow[k + 2] * xrow[k + 2];
+                        a3 += wrow[k + 3] * xrow[k + 3];
+                        a4 += wrow[k + 4] * xrow[k + 4];
+                        a5 += wrow[k + 5] * xrow[k + 5];
+                        a6 += wrow[k + 6] * xrow[k + 6];
+                        a7 += wrow[k + 7] * xrow[k + 7];
+                    }
+                    for (; k < K; ++k) a0 += wrow[k] * xrow[k];
+                    const float acc = ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7));
+                    const float ts = tau[n0 + r] * s[m];
+                    Y[(n0 + r) * M + m] = ts * acc;
+                }
+            }
+        }
+        free(wd);
+    }
+    free(xd);
+    return 0;
+}
+
+/* y + b (row broadcast): include/neuralnet.cpp/compute_layer_bitlinear.hpp:455-456 */
+void orc_add_row_broadcast(float* Y, const float* b, size_t N, size_t M)
+{
+    for (size_t n = 0; n < N; ++n)
+        for (size_t m = 0; m < M; ++m) Y[n * M + m] = Y[n * M + m] + b[n];
+}
+
+/* -------------------------------------------------------------- RMSNorm */
+
+/* The per-token sum of squares uses the same fixed order as the absmean above: 64 strided
+ * parts (feature f goes to part f % 64), each summed in ascending f, then the xor butterfly
+ * over offsets 32,16,8,4,2,1. Both GPU kernels (one wave per token, or 64 tokens per block
+ * with 8 parts per lane) evaluate exactly this tree. */
+static float orc_rms_inv(const float* X, float eps, size_t F, size_t M, size_t m)
+{
+    float p[64];
+    for (int l = 0; l < 64; ++l)
+    {
+        float part = 0.0f;
+        for (size_t f = (size_t)l; f < F; f += 64)
+        {
+            const float x = X[f * M + m];
+            const float sq = x * x;
+            part = part + sq;
+        }
+        p[l] = part;
+    }
+    for (int off = 32; off >= 1; off >>= 1)
+    {
+        float q[64];
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ off];
+        memcpy(p, q, sizeof p);
+    }
+    const float inv_f = 1.0f / (float)F;
+    const float ms = p[0] * inv_f;
+    const float v = ms + eps;
+    return 1.0f / sqrtf(v);
+}
+
+/* RMSNorm forward: include/neuralnet.cpp/compute_layer_mlp.hpp:615-619 and :686-707:
+ * rms_inv = 1/sqrt(sum_f x^2 * (1/F) + eps); normed = x * rms_inv; out = normed * gamma. */
+void orc_rmsnorm(const float* X, const float* gamma, float eps, size_t F, size_t M, float* out)
+{
+    for (size_t m = 0; m < M; ++m)
+    {
+        const float ri = orc_rms_inv(X, eps, F, M, m);
+        for (size_t f = 0; f < F; ++f)
+        {
+            const float nrm = X[f * M + m] * ri;
+            out[f * M + m] = nrm * gamma[f];
+        }
+    }
+}
+
+/* RMSNorm -> per-token absmax scale -> int8, the three steps of
+ * include/neuralnet.cpp/compute_layer_mlp.hpp:686-707 followed by
+ * include/neuralnet.cpp/compute_layer_bitlinear.hpp:443-448, on the normed values.
+ * xq in the reference container layout (F, ceil(M/4)); s is (1, M). */
+void orc_rmsnorm_quant_i8(const float* X, const float* gamma, float eps, size_t F, size_t M,
+                          uint32_t* xq, float* s)
+{
+    float* tmp = (float*)malloc(sizeof(float) * ((F * M) != 0 ? F * M : 1));
+    orc_rmsnorm(X, gamma, eps, F, M, tmp);
+    orc_act_scale(tmp, F, M, s);
+    orc_quantize_i8(tmp, s, F, M, 1, xq);
+    free(tmp);
+}
+
+/* ---------------------------------------------- MI355X tile layout (repack) */
+
+/* Layout T16K256 (this build's own format, no reference counterpart):
+ *   rows padded to Np = roundup(N,16), k padded to Kp = roundup(K,256);
+ *   tile (rt, kt) of 16 rows x 256 k = 256 words (1 KiB) at word offset (rt*KT + kt)*256;
+ *   inside a tile, lane l = 16*g + r (g in 0..3, r in 0..15) owns the 4 words 4*l + q;
+ *   bit 8*b + 2*j of word q of lane l holds the code of
+ *       row 16*rt + r,  k = 256*kt + 64*j + 16*g + 4*q + b      (j, q, b in 0..3).
+ * So (word_q >> 2j) & 0x03030303 gives, in byte b, the code for k = 256kt+64j+16g+4q+b:
+ * the four words shifted by 2j are the 16 A-operand bytes of one 16x16x64 int8 MFMA whose
+ * B operand is 16 consecutive activation bytes starting at k = 256kt + 64j + 16g.
+ * Codes for k in [K, roundup(K,16)) are copied from the source tail, codes beyond are 2. */
+size_t orc_repacked_words(size_t N, size_t K)
+{
+    const size_t Np = (N + 15) / 16 * 16, Kp = (K + 255) / 256 * 256;
+    return Np * Kp / 16;
+}
+
+static uint32_t orc_src_code(const uint32_t* wq, size_t N, size_t K, size_t n, size_t k)
+{
+    const size_t wpr = orc_trit_words_per_row(K);
+    if (n >= N || k >= wpr * 16) return 2u;
+    return (wq[n * wpr + k / 16] >> (2 * (k % 16))) & 3u;
+}
+
+void orc_repack(const uint32_t* wq, size_t N, size_t K, uint32_t* out)
+{
+    const size_t RT = (N + 15) / 16, KT = (K + 255) / 256;
+    for (size_t rt = 0; rt < RT; ++rt)
+        for (size_t kt = 0; kt < KT; ++kt)
+            for (size_t l = 0; l < 64; ++l)
+                for (size_t q = 0; q < 4; ++q)
+                {
+                    const size_t g = l / 16, r = l % 16;
+                    uint32_t word = 0;
+                    for (size_t j = 0; j < 4; ++j)
+                        for (size_t b = 0; b < 4; ++b)
+                        {
+                            const size_t k = 256 * kt + 64 * j + 16 * g + 4 * q + b;
+                            const uint32_t code = orc_src_code(wq, N, K, 16 * rt + r, k);
+                            word |= code << (8 * b + 2 * j);
+                        }
+                    out[(rt * KT + kt) * 256 + 4 * l + q] = word;
+                }
+}
+
+void orc_unrepack(const uint32_t* rp, size_t N, size_t K, uint32_t* wq)
+{
+    const size_t KT = (K + 255) / 256;
+    const size_t wpr = orc_trit_words_per_row(K);
+    for (size_t n = 0; n < N; ++n)
+        for (size_t wi = 0; wi < wpr; ++wi)
+        {
+            uint32_t word = 0;
+            for (size_t e = 0; e < 16; ++e)
+            {
+                const size_t k = wi * 16 + e;
+                const size_t rt = n / 16, r = n % 16, kt = k / 256, kk = k % 256;
+                const size_t j = kk / 64, g = (kk % 64) / 16, q = (kk % 16) / 4, b = kk % 4;
+                const size_t l = 16 * g + r;
+                const uint32_t src = rp[(rt * KT + kt) * 256 + 4 * l + q];
+                const uint32_t code = (src >> (8 * b + 2 * j)) & 3u;
+                word |= code << (2 * e);
+            }
+            wq[n * wpr + wi] = word;
+        }
+}

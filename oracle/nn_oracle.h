@@ -1,0 +1,88 @@
+/*
+ * nn_oracle.h — CPU restatement of neuralnet.cpp's BitLinear W1.58A8 path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links, loads or
+ * calls this code. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg use it, and only as the checker / the timed CPU baseline.
+ *
+ * The reference implementation lives in the un-vendored `engine` submodule
+ * (compute.neuralnet.cpp @ 2dc4986), so it cannot be built here. Every
+ * function below restates the algorithm from the reference's own host-side
+ * test loops and call sites; each one cites the file:line it follows
+ * (paths relative to the reference repository root).
+ *
+ * Pinning status per function (what checks it besides its own formula):
+ *   orc_trit_code / orc_trit_pack_row / orc_trit_at : KAT src/ternary_gemm_test.cpp:79-99
+ *   orc_row_absmean   : KAT src/t1_58_test.cpp:207-252 to 1e-6; ulp order is this
+ *                       build's documented order (the reference order is
+ *                       unpinned: it lives inside the absent CpuEngine)
+ *   orc_quantize_one  : closed form + special cases src/int8_act_test.cpp:86-137;
+ *                       tie arithmetic (x/s vs x*(1/s)) is parity unpinned
+ *   orc_matmul_q_i8*  : brute force in the tests (int64 numpy) + epilogue order
+ *                       src/int8_act_test.cpp:210-236
+ *   orc_rmsnorm*      : textbook formula include/neuralnet.cpp/compute_layer_mlp.hpp:615-619,
+ *                       checked against a float64 recomputation within tolerance
+ *   orc_repack*       : the MI355X tile layout is this build's own format; pinned by
+ *                       the round trip repack -> unrepack == identity
+ */
+#ifndef NN_ORACLE_H
+#define NN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- deterministic RNG (std::normal_distribution is implementation-defined,
+ *      so fixtures use this in-repo generator) ---- */
+uint64_t orc_splitmix64(uint64_t* state);
+void orc_fill_uniform(float* out, size_t n, uint64_t seed, float lo, float hi);
+void orc_fill_normal(float* out, size_t n, uint64_t seed, float mean, float stddev);
+
+/* ---- nn::trit_pack (2 bit / weight, 16 per u32, LSB first, code = trit + 2) ---- */
+size_t orc_trit_words_per_row(size_t K);
+uint32_t orc_trit_code(float w, float tau);
+void orc_trit_pack_row(const float* w, size_t K, float tau, uint32_t* words);
+void orc_trit_pack(const float* W, const float* tau, size_t N, size_t K, uint32_t* out);
+int orc_trit_at(const uint32_t* words, size_t i);
+
+/* ---- per-row absmean tau (fixed 64-lane order, see nn_oracle.c) ---- */
+void orc_row_absmean(const float* W, size_t N, size_t K, float* tau);
+
+/* ---- nn::i8_pack (4 int8 per u32, little-endian, tail bytes 0) ---- */
+size_t orc_i8_words_per_row(size_t cols);
+int8_t orc_quantize_one(float x, float s);
+void orc_col_absmax(const float* X, size_t rows, size_t cols, float* mx);
+void orc_act_scale(const float* X, size_t rows, size_t cols, float* s);
+void orc_quantize_i8(const float* x, const float* scale, size_t rows, size_t cols, int col_scale,
+                     uint32_t* out);
+void orc_unpack_i8(const uint32_t* packed, size_t rows, size_t cols, float* out);
+int orc_i8_at(const uint32_t* words, size_t i);
+
+/* ---- matmul_q_i8: Y[n,m] = (tau_n * s_m) * float(sum_k trit(n,k) * q(k,m)) ---- */
+void orc_matmul_q_i8_acc(const uint32_t* wq, const uint32_t* xq, size_t N, size_t K, size_t M,
+                         int32_t* acc);
+void orc_matmul_q_i8(const uint32_t* wq, const float* tau, const uint32_t* xq, const float* s,
+                     size_t N, size_t K, size_t M, float* Y);
+/* CpuEngine restatement: row-block (RB=64) decode to f32 scratch + dense f32
+ * microkernel; exact because every partial sum is an integer below 2^24. */
+int orc_matmul_q_i8_rowblock(const uint32_t* wq, const float* tau, const uint32_t* xq,
+                             const float* s, size_t N, size_t K, size_t M, float* Y, int threads);
+void orc_add_row_broadcast(float* Y, const float* b, size_t N, size_t M);
+
+/* ---- RMSNorm and the fused RMSNorm -> absmax -> int8 path ---- */
+void orc_rmsnorm(const float* X, const float* gamma, float eps, size_t F, size_t M, float* out);
+void orc_rmsnorm_quant_i8(const float* X, const float* gamma, float eps, size_t F, size_t M,
+                          uint32_t* xq, float* s);
+
+/* ---- MI355X tile layout of packed ternary weights (checker for the repacker) ---- */
+size_t orc_repacked_words(size_t N, size_t K);
+void orc_repack(const uint32_t* wq, size_t N, size_t K, uint32_t* out);
+void orc_unrepack(const uint32_t* rp, size_t N, size_t K, uint32_t* wq);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

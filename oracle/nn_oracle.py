@@ -1,0 +1,249 @@
+"""ctypes binding of oracle/libnnoracle.so (the CPU restatement in nn_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker or the timed CPU baseline. The shipped library never
+uses it. Arrays are numpy; packed containers are uint32 arrays.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnnoracle.so")
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_sz = ctypes.c_size_t
+
+_lib = None
+
+
+def build() -> None:
+    """Compile libnnoracle.so with oracle/Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_fill_uniform": (None, [_f32p, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+            "orc_fill_normal": (None, [_f32p, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+            "orc_trit_words_per_row": (_sz, [_sz]),
+            "orc_trit_code": (ctypes.c_uint32, [ctypes.c_float, ctypes.c_float]),
+            "orc_trit_pack": (None, [_f32p, _f32p, _sz, _sz, _u32p]),
+            "orc_trit_at": (ctypes.c_int, [_u32p, _sz]),
+            "orc_row_absmean": (None, [_f32p, _sz, _sz, _f32p]),
+            "orc_i8_words_per_row": (_sz, [_sz]),
+            "orc_quantize_one": (ctypes.c_int8, [ctypes.c_float, ctypes.c_float]),
+            "orc_col_absmax": (None, [_f32p, _sz, _sz, _f32p]),
+            "orc_act_scale": (None, [_f32p, _sz, _sz, _f32p]),
+            "orc_quantize_i8": (None, [_f32p, _f32p, _sz, _sz, ctypes.c_int, _u32p]),
+            "orc_unpack_i8": (None, [_u32p, _sz, _sz, _f32p]),
+            "orc_matmul_q_i8_acc": (None, [_u32p, _u32p, _sz, _sz, _sz, _i32p]),
+            "orc_matmul_q_i8": (None, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p]),
+            "orc_matmul_q_i8_rowblock": (ctypes.c_int, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]),
+            "orc_add_row_broadcast": (None, [_f32p, _f32p, _sz, _sz]),
+            "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
+            "orc_rmsnorm_quant_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _u32p, _f32p]),
+            "orc_repacked_words": (_sz, [_sz, _sz]),
+            "orc_repack": (None, [_u32p, _sz, _sz, _u32p]),
+            "orc_unrepack": (None, [_u32p, _sz, _sz, _u32p]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, ctype):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def fill_uniform(n: int, seed: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_uniform(_p(out, ctypes.c_float), n, seed, lo, hi)
+    return out
+
+
+def fill_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal(_p(out, ctypes.c_float), n, seed, mean, std)
+    return out
+
+
+def trit_words_per_row(K: int) -> int:
+    return (K + 15) // 16
+
+
+def i8_words_per_row(cols: int) -> int:
+    return (cols + 3) // 4
+
+
+def trit_pack(W: np.ndarray, tau: np.ndarray) -> np.ndarray:
+    W = _f32(W)
+    N, K = W.shape
+    tau = _f32(tau).reshape(N)
+    out = np.empty((N, trit_words_per_row(K)), np.uint32)
+    lib().orc_trit_pack(_p(W, ctypes.c_float), _p(tau, ctypes.c_float), N, K, _p(out, ctypes.c_uint32))
+    return out
+
+
+def row_absmean(W: np.ndarray) -> np.ndarray:
+    W = _f32(W)
+    N, K = W.shape
+    tau = np.empty(N, np.float32)
+    lib().orc_row_absmean(_p(W, ctypes.c_float), N, K, _p(tau, ctypes.c_float))
+    return tau
+
+
+def quantize_one(x: float, s: float) -> int:
+    return int(lib().orc_quantize_one(x, s))
+
+
+def col_absmax(X: np.ndarray) -> np.ndarray:
+    X = _f32(X)
+    r, c = X.shape
+    out = np.empty(c, np.float32)
+    lib().orc_col_absmax(_p(X, ctypes.c_float), r, c, _p(out, ctypes.c_float))
+    return out
+
+
+def act_scale(X: np.ndarray) -> np.ndarray:
+    X = _f32(X)
+    r, c = X.shape
+    out = np.empty(c, np.float32)
+    lib().orc_act_scale(_p(X, ctypes.c_float), r, c, _p(out, ctypes.c_float))
+    return out
+
+
+def quantize_i8(x: np.ndarray, scale: np.ndarray, col_scale: bool = True) -> np.ndarray:
+    x = _f32(x)
+    rows, cols = x.shape
+    scale = _f32(scale).reshape(-1)
+    out = np.empty((rows, i8_words_per_row(cols)), np.uint32)
+    lib().orc_quantize_i8(_p(x, ctypes.c_float), _p(scale, ctypes.c_float), rows, cols, int(col_scale),
+                          _p(out, ctypes.c_uint32))
+    return out
+
+
+def unpack_i8(packed: np.ndarray, cols: int) -> np.ndarray:
+    packed = _u32(packed)
+    rows = packed.shape[0]
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_unpack_i8(_p(packed, ctypes.c_uint32), rows, cols, _p(out, ctypes.c_float))
+    return out
+
+
+def matmul_q_i8_acc(wq: np.ndarray, xq: np.ndarray, K: int, M: int) -> np.ndarray:
+    wq, xq = _u32(wq), _u32(xq)
+    N = wq.shape[0]
+    acc = np.empty((N, M), np.int32)
+    lib().orc_matmul_q_i8_acc(_p(wq, ctypes.c_uint32), _p(xq, ctypes.c_uint32), N, K, M,
+                              _p(acc, ctypes.c_int32))
+    return acc
+
+
+def matmul_q_i8(wq, tau, xq, s, K: int, M: int) -> np.ndarray:
+    wq, xq = _u32(wq), _u32(xq)
+    N = wq.shape[0]
+    tau, s = _f32(tau).reshape(N), _f32(s).reshape(M)
+    Y = np.empty((N, M), np.float32)
+    lib().orc_matmul_q_i8(_p(wq, ctypes.c_uint32), _p(tau, ctypes.c_float), _p(xq, ctypes.c_uint32),
+                          _p(s, ctypes.c_float), N, K, M, _p(Y, ctypes.c_float))
+    return Y
+
+
+def matmul_q_i8_rowblock(wq, tau, xq, s, K: int, M: int, threads: int = 0) -> np.ndarray:
+    wq, xq = _u32(wq), _u32(xq)
+    N = wq.shape[0]
+    tau, s = _f32(tau).reshape(N), _f32(s).reshape(M)
+    Y = np.empty((N, M), np.float32)
+    rc = lib().orc_matmul_q_i8_rowblock(_p(wq, ctypes.c_uint32), _p(tau, ctypes.c_float),
+                                        _p(xq, ctypes.c_uint32), _p(s, ctypes.c_float), N, K, M,
+                                        _p(Y, ctypes.c_float), threads)
+    if rc != 0:
+        raise ValueError("rowblock path is exact only for 127*K < 2^24")
+    return Y
+
+
+def add_row_broadcast(Y: np.ndarray, b: np.ndarray) -> np.ndarray:
+    Y = _f32(Y).copy()
+    N, M = Y.shape
+    b = _f32(b).reshape(N)
+    lib().orc_add_row_broadcast(_p(Y, ctypes.c_float), _p(b, ctypes.c_float), N, M)
+    return Y
+
+
+def rmsnorm(X: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
+    X = _f32(X)
+    F, M = X.shape
+    gamma = _f32(gamma).reshape(F)
+    out = np.empty((F, M), np.float32)
+    lib().orc_rmsnorm(_p(X, ctypes.c_float), _p(gamma, ctypes.c_float), eps, F, M, _p(out, ctypes.c_float))
+    return out
+
+
+def rmsnorm_quant_i8(X: np.ndarray, gamma: np.ndarray, eps: float):
+    X = _f32(X)
+    F, M = X.shape
+    gamma = _f32(gamma).reshape(F)
+    xq = np.empty((F, i8_words_per_row(M)), np.uint32)
+    s = np.empty(M, np.float32)
+    lib().orc_rmsnorm_quant_i8(_p(X, ctypes.c_float), _p(gamma, ctypes.c_float), eps, F, M,
+                               _p(xq, ctypes.c_uint32), _p(s, ctypes.c_float))
+    return xq, s
+
+
+def repacked_words(N: int, K: int) -> int:
+    return int(lib().orc_repacked_words(N, K))
+
+
+def repack(wq: np.ndarray, K: int) -> np.ndarray:
+    wq = _u32(wq)
+    N = wq.shape[0]
+    out = np.empty(repacked_words(N, K), np.uint32)
+    lib().orc_repack(_p(wq, ctypes.c_uint32), N, K, _p(out, ctypes.c_uint32))
+    return out
+
+
+def unrepack(rp: np.ndarray, N: int, K: int) -> np.ndarray:
+    rp = _u32(rp)
+    out = np.empty((N, trit_words_per_row(K)), np.uint32)
+    lib().orc_unrepack(_p(rp, ctypes.c_uint32), N, K, _p(out, ctypes.c_uint32))
+    return out
+
+
+# ---- helpers on the reference containers (pure numpy; used by tests to cross-check) ----
+
+def container_to_int8(xq: np.ndarray, cols: int) -> np.ndarray:
+    """(rows, ceil(cols/4)) u32 container -> (rows, cols) int8."""
+    b = _u32(xq).view(np.uint8).reshape(xq.shape[0], -1)[:, :cols]
+    return b.view(np.int8).copy()
+
+
+def trits_of(wq: np.ndarray, K: int) -> np.ndarray:
+    """(N, ceil(K/16)) packed words -> (N, K) int8 trits (code - 2)."""
+    wq = _u32(wq)
+    shifts = (2 * np.arange(16, dtype=np.uint32))
+    codes = (wq[:, :, None] >> shifts[None, None, :]) & 3
+    return (codes.reshape(wq.shape[0], -1)[:, :K].astype(np.int8) - 2)

@@ -1,0 +1,279 @@
+"""GPU parity: every libnn-hip.so entry point of the BitLinear W1.58A8 path against the CPU
+oracle on the same seeded inputs, bit for bit (integer containers, int32 accumulators and
+the fp32 epilogue, whose order the kernels keep). Large shapes are checked on sampled rows
+(the oracle runs on the same rows) plus size-independent properties.
+
+Reference tests mirrored: src/int8_act_test.cpp [1]-[3], src/ternary_gemm_test.cpp [1]-[2],
+src/t1_58_test.cpp [5].
+"""
+import numpy as np
+import pytest
+
+from conftest import normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t, dtype=None):
+    a = t.cpu().numpy()
+    if dtype is not None:
+        a = a.view(dtype)
+    return a
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+# ------------------------------------------------------------------ trit_pack / tau
+
+@pytest.mark.parametrize("N,K", [(7, 40), (130, 17), (3, 4), (1024, 1024), (2560, 6912), (33, 1)])
+def test_trit_pack_and_tau(ctx, orc, N, K):
+    say(f"trit_pack/row_absmean N={N} K={K}")
+    W = normal((N, K), 1000 + N + K, 0.0, 0.02)
+    W[0, :min(K, 3)] = 0.0
+    tau_g = host(ctx.row_absmean(dev(W)))
+    tau_o = orc.row_absmean(W)
+    assert np.array_equal(tau_g, tau_o)
+    wq_g = host(ctx.trit_pack(dev(W), dev(tau_o)), np.uint32)
+    assert np.array_equal(wq_g, orc.trit_pack(W, tau_o))
+
+
+def test_tau_kat_on_gpu(ctx, orc):
+    # src/t1_58_test.cpp:207-217: tau = {0.475, 0.25, 0.475}
+    W = np.array([[1.0, 0.3, -0.3, 0.3], [0.4, -0.4, 0.1, -0.1], [0.7, 0.6, 0.5, 0.1]], np.float32)
+    tau = host(ctx.row_absmean(dev(W)))
+    assert np.all(np.abs(tau.astype(np.float64) - [0.475, 0.25, 0.475]) < 1e-6)
+    t = orc.trits_of(host(ctx.trit_pack(dev(W), dev(tau)), np.uint32), 4)
+    assert t.tolist() == [[1, 1, -1, 1], [1, -1, 0, 0], [1, 1, 1, 0]]
+
+
+def test_trit_pack_ties_and_nan(ctx, orc):
+    tau = np.array([1.0, 2.0], np.float32)
+    W = np.array([[0.5, -0.5, 0.50000006, -0.50000006, np.nan, np.inf, -np.inf, 0.0],
+                  [1.0, -1.0, 1.0000001, -1.0000001, 0.0, -0.0, 3.0, -3.0]], np.float32)
+    got = host(ctx.trit_pack(dev(W), dev(tau)), np.uint32)
+    assert np.array_equal(got, orc.trit_pack(W, tau))
+
+
+# ------------------------------------------------------------------ int8 quantization
+
+def test_quantize_i8_kat(ctx, orc):
+    # src/int8_act_test.cpp:86-137: 5x7, zero column (s == 0), one NaN
+    xm = uniform((5, 7), 11)
+    s = np.abs(xm).max(axis=0)
+    xm[:, 0] = 0.0
+    xm[1, 1] = np.nan
+    s[0] = 0.0
+    got = host(ctx.quantize_i8(dev(xm), dev(s), True), np.uint32)
+    assert np.array_equal(got, orc.quantize_i8(xm, s, True))
+
+
+@pytest.mark.parametrize("rows,cols,col_scale", [(256, 13, True), (1024, 8, True), (9, 33, False),
+                                                 (2560, 1, True)])
+def test_quantize_unpack(ctx, orc, rows, cols, col_scale):
+    say(f"quantize/unpack {rows}x{cols} col_scale={col_scale}")
+    x = normal((rows, cols), rows + cols, 0.0, 3.0)
+    x.flat[::97] *= 40.0
+    sc = orc.act_scale(x) if col_scale else (np.abs(x).max(axis=1) / 127.0).astype(np.float32)
+    q = host(ctx.quantize_i8(dev(x), dev(sc), col_scale), np.uint32)
+    assert np.array_equal(q, orc.quantize_i8(x, sc, col_scale))
+    u = host(ctx.unpack_i8(dev(q), cols))
+    assert np.array_equal(u, orc.unpack_i8(q, cols))
+
+
+def test_col_reduce_max_abs_scale(ctx, orc):
+    X = normal((777, 19), 5)
+    X[3, 4] = np.nan
+    a = ctx.abs(dev(X))
+    m = host(ctx.col_reduce_max(a))
+    assert np.array_equal(m, orc.col_absmax(X))
+    s_seq = ctx.col_reduce_max(a)
+    ctx.scale_inplace(s_seq, 1.0 / 127.0)
+    s_fused = host(ctx.act_scale(dev(X)))
+    assert np.array_equal(host(s_seq), orc.act_scale(X))
+    assert np.array_equal(s_fused, orc.act_scale(X))
+
+
+# ------------------------------------------------------------------ matmul_q_i8 (reference layout)
+
+def make_case(orc, N, K, M, seed, gaussian=False, outliers=False):
+    if gaussian:
+        W = normal((N, K), seed, 0.0, 0.02)
+        tau = np.full(N, np.abs(W.astype(np.float64)).mean(), np.float32)
+        X = normal((K, M), seed + 1)
+        if outliers:
+            rng = np.random.default_rng(seed)
+            idx = rng.choice(K * M, size=max(1, K * M // 1000), replace=False)
+            X.flat[idx] *= 20.0
+        s = orc.act_scale(X)
+    else:
+        W = uniform((N, K), seed)
+        tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+        X = uniform((K, M), seed + 1)
+        s = np.abs(X).max(axis=0).astype(np.float32)
+    return W, tau, X, s, orc.trit_pack(W, tau), orc.quantize_i8(X, s, True)
+
+
+@pytest.mark.parametrize("N,K,M,seed", [
+    (130, 17, 6, 31),      # int8_act_test [3]: K, N not multiples, crosses the RB=64 row block
+    (512, 256, 8, 41),     # int8_act_test [3] GPU: 2B4T order
+    (1024, 1024, 8, 0xB17A0001),
+    (65, 33, 1, 3), (9, 100, 3, 5), (256, 40, 1, 7),   # ternary_gemm_test [6] tails / N=1
+    (64, 16, 16, 9), (64, 16, 17, 9),               # GEMV/GEMM boundary
+    (192, 48, 320, 11), (130, 300, 130, 13),         # GEMM tails in both directions
+])
+def test_matmul_q_i8(ctx, orc, N, K, M, seed):
+    say(f"matmul_q_i8 N={N} K={K} M={M}")
+    gaussian = (seed == 0xB17A0001)
+    _, tau, _, s, wq, xq = make_case(orc, N, K, M, seed, gaussian=gaussian)
+    Y = host(ctx.matmul_q_i8(dev(wq), dev(tau), dev(xq), dev(s), K, M))
+    assert np.array_equal(Y, orc.matmul_q_i8(wq, tau, xq, s, K, M))
+
+
+def test_golden_fixtures_on_gpu(ctx):
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "matmul_q_i8.npz")
+    with np.load(path, allow_pickle=False) as z:
+        names = sorted({k.split("__")[0] for k in z.files})
+        for name in names:
+            g = {k.split("__")[1]: z[k] for k in z.files if k.startswith(name + "__")}
+            N, K, M = (int(v) for v in g["shape"])
+            say(f"golden {name}")
+            xq = host(ctx.quantize_i8(dev(g["X"]), dev(g["s"]), True), np.uint32)
+            assert np.array_equal(xq, g["xq"]), name
+            Y = host(ctx.matmul_q_i8(dev(g["wq"]), dev(g["tau"]), dev(g["xq"]), dev(g["s"]), K, M))
+            assert np.array_equal(Y, g["Y"]), name
+            if "W" in g:
+                assert np.array_equal(host(ctx.trit_pack(dev(g["W"]), dev(g["tau"])), np.uint32), g["wq"])
+
+
+# ------------------------------------------------------------------ repacker
+
+@pytest.mark.parametrize("N,K", [(1, 1), (17, 257), (130, 17), (2560, 2560), (640, 6912)])
+def test_repack_roundtrip(ctx, orc, N, K):
+    say(f"repack N={N} K={K}")
+    rng = np.random.default_rng(N + K)
+    wq = rng.integers(0, 2 ** 32, size=(N, (K + 15) // 16), dtype=np.uint64).astype(np.uint32)
+    rp = ctx.repack(dev(wq), K)
+    if N * K <= 640 * 6912:
+        assert np.array_equal(host(rp, np.uint32), orc.repack(wq, K))
+    assert np.array_equal(host(ctx.unrepack(rp, N, K), np.uint32), wq)
+
+
+# ------------------------------------------------------------------ fused activation quant
+
+@pytest.mark.parametrize("K,M", [(2560, 1), (6912, 16), (17, 5), (2560, 33), (4096, 300), (1024, 8)])
+def test_act_quant_i8(ctx, orc, nnhip, K, M):
+    say(f"act_quant K={K} M={M}")
+    X = normal((K, M), K * 7 + M, 0.0, 1.0)
+    X.flat[::1009] *= 20.0
+    xi, s, rs, xq = ctx.act_quant_i8(dev(X), want_container=True)
+    s_o = orc.act_scale(X)
+    xq_o = orc.quantize_i8(X, s_o, True)
+    assert np.array_equal(host(s), s_o)
+    assert np.array_equal(host(xq, np.uint32), xq_o)
+    q = orc.container_to_int8(xq_o, M).T  # (M, K)
+    xi_h = host(xi)
+    assert np.array_equal(xi_h[:, :K], q)
+    assert np.all(xi_h[:, K:] == 0)
+    assert np.array_equal(host(rs), q.astype(np.int64).sum(axis=1))
+    # container -> xi conversion and back
+    xi2, rs2 = ctx.act_from_container(dev(xq_o), K, M)
+    assert np.array_equal(host(xi2), xi_h) and np.array_equal(host(rs2), host(rs))
+    assert np.array_equal(host(ctx.act_to_container(xi, K, M), np.uint32), xq_o)
+
+
+@pytest.mark.parametrize("F,M,eps", [(2560, 1, 1e-6), (2560, 16, 1e-5), (2560, 100, 1e-6),
+                                     (6912, 64, 1e-6), (300, 3, 1e-6)])
+def test_rmsnorm_quant(ctx, orc, F, M, eps):
+    say(f"rmsnorm_quant F={F} M={M}")
+    X = normal((F, M), F + M, 0.0, 1.0)
+    g = normal((F,), 3, 1.0, 0.1)
+    out = host(ctx.rmsnorm(dev(X), dev(g), eps))
+    assert np.array_equal(out, orc.rmsnorm(X, g, eps))
+    xi, s, rs, xq = ctx.rmsnorm_quant_i8(dev(X), dev(g), eps, want_container=True)
+    xq_o, s_o = orc.rmsnorm_quant_i8(X, g, eps)
+    assert np.array_equal(host(s), s_o)
+    assert np.array_equal(host(xq, np.uint32), xq_o)
+    assert np.array_equal(host(xi)[:, :F], orc.container_to_int8(xq_o, M).T)
+
+
+# ------------------------------------------------------------------ fast-path GEMV / GEMM
+
+def fast_case(ctx, orc, N, K, M, seed, outliers=False):
+    W, tau, X, s, wq, xq = make_case(orc, N, K, M, seed, gaussian=True, outliers=outliers)
+    rp = ctx.repack(dev(wq), K)
+    xi, s_d, rs = ctx.act_quant_i8(dev(X))
+    assert np.array_equal(host(s_d), s)
+    return tau, s, wq, xq, rp, xi, s_d, rs
+
+
+@pytest.mark.parametrize("N,K,M", [(2560, 2560, 1), (6912, 2560, 1), (2560, 6912, 1),
+                                   (2560, 2560, 16), (640, 2560, 16), (6912, 2560, 7)])
+def test_decode_gemv_shapes(ctx, orc, N, K, M):
+    say(f"gemv N={N} K={K} M={M}")
+    tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, N + K + M)
+    b = normal((N,), 99)
+    Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M, bias=dev(b)))
+    ref = orc.add_row_broadcast(orc.matmul_q_i8_rowblock(wq, tau, xq, s, K, M), b)
+    assert np.array_equal(Y, ref)
+
+
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 256), (11008, 4096, 1024), (4096, 4096, 2048),
+                                   (2560, 2560, 100)])
+def test_prefill_gemm_shapes(ctx, orc, N, K, M):
+    """BASELINE config 2 shapes, 0.1% activation outliers at 20x; oracle on sampled rows."""
+    say(f"gemm N={N} K={K} M={M}")
+    tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, 5 + M, outliers=True)
+    Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M))
+    rows = np.unique(np.concatenate([np.arange(0, N, max(1, N // 48)), [N - 1]]))
+    ref = orc.matmul_q_i8_rowblock(wq[rows], tau[rows], xq, s, K, M)
+    assert np.array_equal(Y[rows], ref)
+    # size-independent property on every row: Y / (tau*s) is an integer accumulator
+    ts = (tau[:, None] * s[None, :]).astype(np.float32)
+    acc = Y / ts
+    assert np.all(np.abs(acc - np.rint(acc)) < 1e-3 * np.maximum(1, np.abs(acc)))
+
+
+def test_grouped_gemv_matches_single(ctx, orc):
+    say("grouped gemv")
+    import torch
+    shapes = [(2560, 2560), (640, 2560), (6912, 2560), (2560, 6912), (100, 300)]
+    probs, singles = [], []
+    for i, (N, K) in enumerate(shapes):
+        tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, 1 + (i % 2) * 15, 50 + i)
+        M = 1 + (i % 2) * 15
+        y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+        probs.append(dict(rp=rp, tau=dev(tau), xi=xi, s=s_d, rowsum=rs, bias=None, y=y, N=N, K=K, M=M))
+        singles.append(host(ctx.ternary_matmul(rp, probs[-1]["tau"], xi, s_d, rs, N, K, M)))
+    h = ctx.group_create(probs)
+    for _ in range(3):
+        ctx.group_run(h)
+    ctx.sync()
+    for p, ref in zip(probs, singles):
+        assert np.array_equal(host(p["y"]), ref)
+    ctx.group_destroy(h)
+
+
+def test_invalid_arguments_raise(ctx, nnhip):
+    import torch
+    rp = torch.zeros(64, dtype=torch.int32, device="cuda")
+    x = torch.zeros((1, 256), dtype=torch.int8, device="cuda")
+    f = torch.zeros(16, dtype=torch.float32, device="cuda")
+    i = torch.zeros(16, dtype=torch.int32, device="cuda")
+    with pytest.raises(nnhip.NNHipError):   # K = 0
+        ctx.ternary_matmul(rp, f, x, f, i, 16, 0, 1)
+    with pytest.raises(nnhip.NNHipError):   # K beyond the int32 accumulator bound
+        ctx.ternary_matmul(rp, f, x, f, i, 16, 300000, 1)
+    with pytest.raises(nnhip.NNHipError):   # misaligned xi
+        bad = torch.zeros(300, dtype=torch.int8, device="cuda")[1:257].view(1, 256)
+        ctx.ternary_matmul(rp, f, bad, f, i, 16, 256, 1)

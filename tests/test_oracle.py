@@ -1,0 +1,268 @@
+"""Pins the CPU oracle (oracle/nn_oracle.c) against what the reference fixes.
+
+Known-answer tests are the reference's own inline constants; everything else is checked
+against an independent computation (numpy int64 / float64, closed forms, invariants),
+never by retyping the oracle's loop. Reference citations are file:line in
+neuralnet-cpp-dev/neuralnet.cpp v1.18.0.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from conftest import normal, uniform
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- trit_pack layout
+
+def test_trit_layout_kat(orc):
+    # src/ternary_gemm_test.cpp:79-89: tau = 1 -> threshold 0.5, codes = trit + 2, LSB first
+    w = np.array([1.0, -1.0, 0.0, 0.4, -0.4, 1.0, -1.0, 0.0,
+                  0.9, -0.9, 0.1, -0.1, 0.6, -0.6, 0.0, 0.0], np.float32)
+    expect = [3, 1, 2, 2, 2, 3, 1, 2, 3, 1, 2, 2, 3, 1, 2, 2]
+    word = orc.trit_pack(w[None, :], np.array([1.0], np.float32))[0, 0]
+    assert [(int(word) >> (2 * j)) & 3 for j in range(16)] == expect
+
+
+def test_trit_tail_is_code2(orc):
+    # src/ternary_gemm_test.cpp:91-99: K=5 -> positions 5..15 hold code 2 (trit 0), not code 0
+    w = np.array([1.0, -1.0, 0.0, 0.4, -0.4], np.float32)
+    wq = orc.trit_pack(w[None, :], np.array([1.0], np.float32))
+    assert orc.trits_of(wq, 16)[0].tolist() == [1, -1, 0, 0, 0] + [0] * 11
+    assert int(wq[0, 0]) >> 10 == (0xAAAAAAAA >> 10)
+
+
+def test_words_per_row_constants(orc):
+    # src/ternary_gemm_test.cpp:74-77, :102-104
+    L = orc.lib()
+    assert (L.orc_trit_words_per_row(16), L.orc_trit_words_per_row(17), L.orc_trit_words_per_row(1)) == (1, 2, 1)
+    assert L.orc_trit_words_per_row(512) * 4 == 128  # 0.25 B / weight
+    assert (L.orc_i8_words_per_row(7), L.orc_i8_words_per_row(4), L.orc_i8_words_per_row(1)) == (2, 1, 1)
+
+
+def test_trit_pack_matches_threshold_rule(orc):
+    # ternary_gemm_test.cpp:224-251 (engine pack == host pack_row) with the double-precision
+    # threshold of t1_58_test.cpp:238-252 as the independent rule
+    W = uniform((33, 70), 7)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    wq = orc.trit_pack(W, tau)
+    t = orc.trits_of(wq, 70)
+    w64, h = W.astype(np.float64), 0.5 * tau.astype(np.float64)[:, None]
+    expect = np.where(w64 > h, 1, np.where(w64 < -h, -1, 0))
+    assert np.array_equal(t, expect)
+
+
+# ---------------------------------------------------------------- absmean tau (KAT)
+
+KRAW_W = np.array([[1.0, 0.3, -0.3, 0.3], [0.4, -0.4, 0.1, -0.1], [0.7, 0.6, 0.5, 0.1]], np.float32)
+KX = np.array([[1.0, -2.0], [0.5, 1.0], [-1.0, 0.25], [2.0, -0.5]], np.float32)
+
+
+def test_tau_kat(orc):
+    # src/t1_58_test.cpp:207-217, :291: tau = {0.475, 0.25, 0.475} to 1e-6
+    tau = orc.row_absmean(KRAW_W)
+    assert np.all(np.abs(tau.astype(np.float64) - [0.475, 0.25, 0.475]) < 1e-6)
+    # trits of t1_58_test.cpp:322-326: row0 keeps the 0.3s (absmean), row1 zeroes the 0.1s
+    t = orc.trits_of(orc.trit_pack(KRAW_W, tau), 4)
+    assert t.tolist() == [[1, 1, -1, 1], [1, -1, 0, 0], [1, 1, 1, 0]]
+
+
+def test_tau_close_to_float64(orc):
+    W = normal((64, 6912), 11, 0.0, 0.02)
+    tau = orc.row_absmean(W)
+    ref = np.abs(W.astype(np.float64)).mean(axis=1)
+    assert np.max(np.abs(tau - ref) / ref) < 1e-6
+
+
+def test_zero_fraction_gaussian_absmean(orc):
+    # sanity invariant: per-tensor absmean on N(0, 0.02) leaves P(|z| <= 0.5*sqrt(2/pi)) zeros
+    W = normal((1024, 1024), 0xB17A0001, 0.0, 0.02)
+    tau = np.full(1024, np.abs(W.astype(np.float64)).mean(), np.float32)
+    t = orc.trits_of(orc.trit_pack(W, tau), 1024)
+    expect = math.erf(0.5 * math.sqrt(2 / math.pi) / math.sqrt(2))
+    assert abs(float((t == 0).mean()) - expect) < 0.005
+    assert abs(expect - 0.310) < 0.001
+
+
+# ---------------------------------------------------------------- int8 quantization
+
+def test_quantize_special_cases(orc):
+    # docs/internal/21-quantized-weights.md:973-975; src/int8_act_test.cpp:86-137
+    q = orc.quantize_one
+    assert q(1.0, 0.0) == 0                       # s == 0 -> 0
+    assert q(float("nan"), 1.0) == 0              # NaN -> 0
+    assert q(2.5, 1.0) == 3 and q(-2.5, 1.0) == -3  # round half away from zero
+    assert q(0.5, 1.0) == 1 and q(-0.5, 1.0) == -1
+    assert q(0.49999997, 1.0) == 0
+    assert q(1000.0, 1.0) == 127 and q(-1000.0, 1.0) == -127  # clamp to +-127 (never -128)
+    assert q(float("inf"), 1.0) == 127 and q(float("-inf"), 1.0) == -127
+    assert q(1.0, float("inf")) == 0
+
+
+def test_quantize_layout_and_values(orc):
+    # src/int8_act_test.cpp:86-137: M=5, N=7 (tail word), a zero column and a NaN
+    xm = uniform((5, 7), 11)
+    s = np.abs(xm).max(axis=0)
+    xm[:, 0] = 0.0
+    xm[1, 1] = np.nan
+    out = orc.quantize_i8(xm, s, True)
+    assert out.shape == (5, 2)
+    b = out.view(np.uint8).reshape(5, 8)
+    assert np.all(b[:, 7] == 0)                  # tail byte
+    q = orc.container_to_int8(out, 7).astype(np.int64)
+    assert np.all(q[:, 0] == 0) and q[1, 1] == 0
+    v = xm.astype(np.float64) / s.astype(np.float64)
+    ok = ~np.isnan(v)
+    # q is the integer nearest to x/s (s = absmax -> |x/s| <= 1 -> q in {-1, 0, 1})
+    assert np.all(np.abs(q[ok] - v[ok]) <= 0.5 + 1e-6)
+    assert set(np.unique(q)) <= {-1, 0, 1}
+
+
+def test_quantize_row_scale_and_clamp(orc):
+    x = uniform((9, 13), 3, -300.0, 300.0)
+    sc = np.full(9, 1.3, np.float32)
+    q = orc.container_to_int8(orc.quantize_i8(x, sc, False), 13).astype(np.int64)
+    v = np.clip(x.astype(np.float64) / 1.3, -127, 127)
+    assert np.all(np.abs(q - v) <= 0.5 + 1e-6)
+    assert q.min() >= -127 and q.max() <= 127
+
+
+def test_act_scale_multiplies_reciprocal(orc):
+    # compute_layer_bitlinear.hpp:443-447: s = max|x| * fl(1/127), a multiply, not a divide
+    X = normal((300, 9), 5)
+    s = orc.act_scale(X)
+    mx = np.abs(X).max(axis=0)
+    assert np.array_equal(s, (mx * np.float32(1.0 / 127.0)).astype(np.float32))
+
+
+def test_unpack_roundtrip(orc):
+    # src/int8_act_test.cpp:140-168
+    x = uniform((3, 6), 23)
+    s = np.maximum(0.3, np.abs(x[0]) + 0.1).astype(np.float32)
+    packed = orc.quantize_i8(x, s, True)
+    u = orc.unpack_i8(packed, 6)
+    assert np.array_equal(u, orc.container_to_int8(packed, 6).astype(np.float32))
+    assert np.all(np.abs(u) <= 127)
+
+
+# ---------------------------------------------------------------- matmul_q_i8
+
+def _case(orc, N, K, M, seed):
+    """int8_act_test.cpp:171-205 inputs: uniform W, tau = per-row absmean (double), X, s = absmax."""
+    W = uniform((N, K), seed)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    X = uniform((K, M), seed + 1)
+    s = np.abs(X).max(axis=0).astype(np.float32)
+    wq = orc.trit_pack(W, tau)
+    xq = orc.quantize_i8(X, s, True)
+    return wq, tau, xq, s
+
+
+@pytest.mark.parametrize("N,K,M,seed", [(130, 17, 6, 31), (512, 256, 8, 41), (65, 33, 1, 3),
+                                        (9, 100, 3, 5)])
+def test_matmul_q_i8_bruteforce(orc, N, K, M, seed):
+    wq, tau, xq, s = _case(orc, N, K, M, seed)
+    acc = orc.matmul_q_i8_acc(wq, xq, K, M)
+    t = orc.trits_of(wq, K).astype(np.int64)
+    q = orc.container_to_int8(xq, M).astype(np.int64)
+    assert np.array_equal(acc.astype(np.int64), t @ q)
+    Y = orc.matmul_q_i8(wq, tau, xq, s, K, M)
+    # src/int8_act_test.cpp:233: (tau_m * s_n) * float(acc), numpy float32 ops are IEEE
+    ts = tau[:, None] * s[None, :]
+    assert np.array_equal(Y, ts * (t @ q).astype(np.float32))
+    # the epilogue order matters: tau * (s * acc) differs somewhere on this data
+    alt = tau[:, None] * (s[None, :] * acc.astype(np.float32))
+    if N * M > 500:
+        assert not np.array_equal(Y, alt)
+
+
+@pytest.mark.parametrize("N,K,M", [(130, 17, 6), (512, 256, 8), (1024, 1024, 8), (100, 6912, 3)])
+def test_rowblock_bit_identical(orc, N, K, M):
+    wq, tau, xq, s = _case(orc, N, K, M, 77)
+    assert np.array_equal(orc.matmul_q_i8_rowblock(wq, tau, xq, s, K, M),
+                          orc.matmul_q_i8(wq, tau, xq, s, K, M))
+
+
+def test_bias_add(orc):
+    Y = normal((5, 3), 1)
+    b = normal((5,), 2)
+    assert np.array_equal(orc.add_row_broadcast(Y, b), Y + b[:, None])
+
+
+# ---------------------------------------------------------------- RMSNorm
+
+def test_rmsnorm_close_to_float64(orc):
+    X = normal((2560, 33), 9)
+    g = normal((2560,), 10, 1.0, 0.1)
+    out = orc.rmsnorm(X, g, 1e-6)
+    x64 = X.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(axis=0) + 1e-6) * g.astype(np.float64)[:, None]
+    assert np.max(np.abs(out - ref) / np.maximum(np.abs(ref), 1e-3)) < 2e-6
+
+
+def test_rmsnorm_quant_is_the_sequence(orc):
+    X = normal((700, 21), 12)
+    g = np.ones(700, np.float32)
+    xq, s = orc.rmsnorm_quant_i8(X, g, 1e-6)
+    n = orc.rmsnorm(X, g, 1e-6)
+    s2 = orc.act_scale(n)
+    assert np.array_equal(s, s2)
+    assert np.array_equal(xq, orc.quantize_i8(n, s2, True))
+
+
+# ---------------------------------------------------------------- MI355X tile layout
+
+@pytest.mark.parametrize("N,K", [(1, 1), (16, 256), (17, 257), (33, 40), (130, 17), (64, 1000)])
+def test_repack_roundtrip(orc, N, K):
+    rng = np.random.default_rng(N * 1000 + K)
+    wq = rng.integers(0, 2 ** 32, size=(N, (K + 15) // 16), dtype=np.uint64).astype(np.uint32)
+    rp = orc.repack(wq, K)
+    assert rp.size == ((N + 15) // 16 * 16) * ((K + 255) // 256 * 256) // 16
+    assert np.array_equal(orc.unrepack(rp, N, K), wq)
+
+
+def test_repack_layout_feeds_the_mfma_mapping(orc):
+    """Decode the tiles the way the kernel's MFMAs consume them (numpy, vectorized) and
+    check the resulting code matrix and a product against the reference container."""
+    N, K = 40, 600
+    W = normal((N, K), 4)
+    tau = np.abs(W).mean(axis=1).astype(np.float32)
+    wq = orc.trit_pack(W, tau)
+    rp = orc.repack(wq, K)
+    RT, KT = (N + 15) // 16, (K + 255) // 256
+    t = rp.reshape(RT, KT, 4, 16, 4)  # [rt][kt][g][r][q]
+    codes = np.zeros((RT * 16, KT * 256), np.int64)
+    for j in range(4):
+        for b in range(4):
+            c = (t >> np.uint32(8 * b + 2 * j)) & np.uint32(3)  # [rt][kt][g][r][q]
+            # k = 256kt + 64j + 16g + 4q + b ; row = 16rt + r
+            for g in range(4):
+                for q in range(4):
+                    cols = np.arange(KT) * 256 + 64 * j + 16 * g + 4 * q + b
+                    codes[:, cols] = c[:, :, g, :, q].transpose(0, 2, 1).reshape(RT * 16, KT)
+    trit = orc.trits_of(wq, K).astype(np.int64)
+    assert np.array_equal(codes[:N, :K] - 2, trit)
+    assert np.all(codes[N:, :] == 2) and np.all(codes[:, ((K + 15) // 16) * 16:] == 2)
+    x = np.random.default_rng(1).integers(-127, 128, size=(KT * 256,))
+    x[K:] = 0
+    assert np.array_equal(codes[:N] @ x - 2 * x.sum(), trit @ x[:K])
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+def test_golden_fixtures(orc):
+    path = os.path.join(GOLDEN, "matmul_q_i8.npz")
+    with np.load(path, allow_pickle=False) as z:
+        names = sorted({k.split("__")[0] for k in z.files})
+        assert len(names) >= 3
+        for name in names:
+            g = {k.split("__")[1]: z[k] for k in z.files if k.startswith(name + "__")}
+            N, K, M = (int(v) for v in g["shape"])
+            if "W" in g:
+                assert np.array_equal(orc.trit_pack(g["W"], g["tau"]), g["wq"]), name
+            assert np.array_equal(orc.quantize_i8(g["X"], g["s"], True), g["xq"]), name
+            assert np.array_equal(orc.matmul_q_i8_acc(g["wq"], g["xq"], K, M), g["acc"]), name
+            assert np.array_equal(orc.matmul_q_i8(g["wq"], g["tau"], g["xq"], g["s"], K, M), g["Y"]), name
