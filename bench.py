@@ -4,12 +4,12 @@ Headline (BASELINE.json metric, config 1): the M=1 ternary x int8 decode GEMV ov
 BitNet-2B-class layer stack — 30 layers x {q 2560->2560, k 2560->640, v 2560->640,
 o 2560->2560, gate 2560->6912, up 2560->6912, down 6912->2560}, 521,011,200 bytes of packed
 ternary weights (more than twice the 256 MB MALL) — run as ONE grouped launch per step.
-value = algorithmic bytes of the whole sweep / step time, in GB/s.
+value = algorithmic bytes of the whole sweep / average launch time, in GB/s.
 
-Reported beside it: the same sweep at M=16, per-shape grouped sweeps, and the prefill
-GEMM (config 2: M=2048, K=4096, N in {4096, 11008}) in TOPS against the dense int8 MFMA
-peak. The CPU baseline is the oracle's CpuEngine restatement (row-block decode + dense f32
-microkernel) on a bounded sample of the same workload, timed on this host.
+Reported beside it: the same sweep at M=16, per-shape grouped sweeps, single-GEMV launches,
+and the prefill GEMM (config 2: M=2048, K=4096, N in {4096, 11008}) in TOPS against the
+dense int8 MFMA peak. The CPU baseline is the oracle's CpuEngine restatement (row-block
+decode + dense f32 microkernel) on a bounded sample of the same workload, timed on this host.
 
 Inputs are synthetic (seeded): W ~ N(0, 0.02) ternarized by per-tensor absmean, activations
 ~ N(0, 1) quantized per token by absmax. All inputs are resident in HBM before timing.
@@ -58,31 +58,33 @@ def gemv_bytes(N, K, M):
 
 
 class Weights:
-    """The layer stack's packed ternary weights, generated and packed on the GPU."""
+    """The layer stack's packed ternary weights, generated, packed and repacked on the GPU."""
 
-    def __init__(self, ctx, torch, layers, keep_ref_layer0=True):
+    def __init__(self, ctx, torch, layers):
         self.mats = []   # (layer, name, K, N, rp, tau)
-        self.ref0 = {}   # layer-0 reference containers for the CPU baseline
+        self.ref0 = {}   # layer-0 reference containers, for the CPU baseline
         gen = torch.Generator(device="cuda")
         for layer in range(layers):
-            for name, K, N in SHAPES:
-                gen.manual_seed(0xB17A0000 + layer * 16 + len(self.mats) % 7)
+            for idx, (name, K, N) in enumerate(SHAPES):
+                gen.manual_seed(0xB17A0000 + layer * 16 + idx)
                 W = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
-                tau_v = W.abs().double().mean().float()
-                tau = tau_v.expand(N).contiguous()
+                tau = W.abs().double().mean().float().expand(N).contiguous()   # per-tensor absmean
                 wq = ctx.trit_pack(W, tau)
                 rp = ctx.repack(wq, K)
-                if layer == 0 and keep_ref_layer0:
+                if layer == 0:
                     self.ref0[name] = (wq.cpu().numpy().view(np.uint32), tau.cpu().numpy())
                 del W, wq
                 self.mats.append((layer, name, K, N, rp, tau))
         torch.cuda.synchronize()
 
 
-def make_acts(ctx, torch, K, M, seed):
+def make_acts(ctx, torch, K, M, seed, outliers=False):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     X = torch.randn((K, M), generator=gen, device="cuda", dtype=torch.float32)
+    if outliers:   # config 2: 0.1% of the elements at 20x scale
+        idx = torch.randperm(K * M, generator=gen, device="cuda")[: max(1, K * M // 1000)]
+        X.view(-1)[idx] *= 20.0
     xi, s, rs = ctx.act_quant_i8(X)
     return X, xi, s, rs
 
@@ -100,8 +102,8 @@ def build_group(ctx, torch, weights, acts, M, select=None):
 
 
 def time_launches(torch, stream, fn, steps, warmup):
-    """Average duration of `fn` launches measured with events on the launch stream, plus
-    the wall-clock of the whole timed region."""
+    """Average duration of `fn` over `steps` back-to-back launches, from events recorded on
+    the launch stream, plus the wall clock of the timed region (synchronized both sides)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -117,12 +119,71 @@ def time_launches(torch, stream, fn, steps, warmup):
     return start.elapsed_time(end) / steps / 1e3, wall
 
 
-def cpu_baseline(orc, weights, acts_host, budget_s=15.0):
+def extra_gemv_lines(ctx, torch, stream, weights, acts1, out):
+    acts16 = {K: make_acts(ctx, torch, K, 16, 0xB17A0003 + K) for K in (D, FFN)}
+    grp16, _, nbytes16 = build_group(ctx, torch, weights, acts16, 16)
+    t16, _ = time_launches(torch, stream, lambda: ctx.group_run(grp16), 20, 3)
+    out["gemv_m16_sweep"] = {"GB/s": round(nbytes16 / t16 / 1e9, 1),
+                             "frac_hbm": round(nbytes16 / t16 / 1e9 / HBM_PEAK_GBS, 4),
+                             "us_per_launch": round(t16 * 1e6, 2), "bytes": nbytes16}
+    log(f"M=16 sweep: {nbytes16 / t16 / 1e9:.1f} GB/s")
+    ctx.group_destroy(grp16)
+
+    per_shape = {}
+    for name, K, N in SHAPES:
+        g, _, nb = build_group(ctx, torch, weights, acts1, 1, select={name})
+        t, _ = time_launches(torch, stream, lambda: ctx.group_run(g), 20, 3)
+        per_shape[f"{name} {K}->{N} x{len(weights.mats) // len(SHAPES)}"] = {
+            "GB/s": round(nb / t / 1e9, 1), "us": round(t * 1e6, 2)}
+        ctx.group_destroy(g)
+    out["gemv_m1_per_shape_stacks"] = per_shape
+
+    single = {}
+    for (layer, name, K, N, rp, tau) in weights.mats[:len(SHAPES)]:
+        _, xi, s, rs = acts1[K]
+        y = torch.empty((N, 1), dtype=torch.float32, device="cuda")
+        t, _ = time_launches(torch, stream,
+                             lambda: ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, 1, out=y), 50, 5)
+        single[f"{name} {K}->{N}"] = {"us": round(t * 1e6, 2),
+                                      "GB/s": round(gemv_bytes(N, K, 1) / t / 1e9, 1)}
+    out["gemv_m1_single_launch"] = single
+
+
+def gemm_lines(ctx, torch, stream, steps, out):
+    M, K = 2048, 4096
+    _, xi, s, rs = make_acts(ctx, torch, K, M, 0xB17A0004, outliers=True)
+    gemm = {}
+    for N in (4096, 11008):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0xB17A0005 + N)
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        tau = W.abs().double().mean().float().expand(N).contiguous()
+        rp = ctx.repack(ctx.trit_pack(W, tau), K)
+        del W
+        y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+        t, _ = time_launches(torch, stream,
+                             lambda: ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, out=y),
+                             max(10, steps // 2), 5)
+        tops = 2.0 * M * N * K / t / 1e12
+        gemm[f"M={M} K={K} N={N}"] = {"TOPS": round(tops, 1), "us": round(t * 1e6, 1),
+                                      "frac_int8_mfma": round(tops / INT8_PEAK_TOPS, 4)}
+        log(f"GEMM M={M} K={K} N={N}: {t * 1e6:.1f} us, {tops:.1f} TOPS "
+            f"({tops / INT8_PEAK_TOPS:.3f} of int8 MFMA peak)")
+    out["prefill_gemm"] = gemm
+
+
+def cpu_baseline(weights, acts1, budget_s=12.0):
     """Oracle CpuEngine restatement (row-block RB=64 decode + dense f32 microkernel) at M=1
-    on a bounded sample: layer 0's seven matrices, repeated until ~budget_s of CPU time."""
+    on a bounded sample: layer 0's seven matrices, repeated for about budget_s seconds."""
+    from oracle import nn_oracle as orc   # the CPU restatement, timed as the baseline
     threads = min(16, os.cpu_count() or 1)
+    acts_host = {}
+    for K in (D, FFN):
+        X, _, s, _ = acts1[K]
+        s_h = s.cpu().numpy()
+        acts_host[K] = (orc.quantize_i8(X.cpu().numpy(), s_h, True), s_h)
     nbytes, elapsed, reps = 0, 0.0, 0
-    while elapsed < budget_s and reps < 20:
+    while elapsed < budget_s and reps < 5000:
         for name, K, N in SHAPES:
             wq, tau = weights.ref0[name]
             xq, s = acts_host[K]
@@ -131,11 +192,12 @@ def cpu_baseline(orc, weights, acts_host, budget_s=15.0):
             elapsed += time.perf_counter() - t0
             nbytes += gemv_bytes(N, K, 1)
         reps += 1
+    layer_bytes = sum(gemv_bytes(N, K, 1) for _, K, N in SHAPES)
     return {"value": round(nbytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"layer 0 of the stack (7 GEMVs, {sum(gemv_bytes(N, K, 1) for _, K, N in SHAPES)} B) "
-                      f"x {reps} repetitions at M=1, {elapsed:.1f} s; oracle/nn_oracle.c "
-                      f"orc_matmul_q_i8_rowblock with {threads} OpenMP threads"}
+            "sample": f"layer 0 of the stack (7 GEMVs, {layer_bytes} B) x {reps} repetitions at "
+                      f"M=1 ({elapsed:.1f} s); oracle/nn_oracle.c orc_matmul_q_i8_rowblock, "
+                      f"{threads} OpenMP threads"}
 
 
 def main():
@@ -146,6 +208,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM lines")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the M=16 / per-shape / single-launch GEMV lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path "
@@ -161,7 +225,6 @@ def main():
     log(f"generating {args.layers} layers of packed ternary weights on the GPU")
     weights = Weights(ctx, torch, args.layers)
     acts1 = {K: make_acts(ctx, torch, K, 1, 0xB17A0002 + K) for K in (D, FFN)}
-    acts16 = {K: make_acts(ctx, torch, K, 16, 0xB17A0003 + K) for K in (D, FFN)}
 
     # ---- headline: M=1 layer-stack sweep, one grouped launch per step
     grp, probs, nbytes = build_group(ctx, torch, weights, acts1, 1)
@@ -173,7 +236,7 @@ def main():
     log(f"M=1 sweep: {t_launch * 1e6:.1f} us/launch (events), {ms_per_step * 1e3:.1f} us/step wall, "
         f"{gbs:.1f} GB/s = {gbs / HBM_PEAK_GBS:.3f} of HBM peak")
 
-    # bit-check one output of the sweep against the single-problem path
+    # the sweep's last output must equal the single-problem launch bit for bit
     p0 = probs[-1]
     y_single = ctx.ternary_matmul(p0["rp"], p0["tau"], p0["xi"], p0["s"], p0["rowsum"],
                                   p0["N"], p0["K"], 1)
@@ -181,72 +244,17 @@ def main():
     assert torch.equal(y_single, p0["y"]), "grouped GEMV differs from the single launch"
 
     extra = {}
-    # ---- M=16 sweep
-    grp16, probs16, nbytes16 = build_group(ctx, torch, weights, acts16, 16)
-    t16, _ = time_launches(torch, stream, lambda: ctx.group_run(grp16), max(5, args.steps // 2), 3)
-    extra["gemv_m16_sweep"] = {"GB/s": round(nbytes16 / t16 / 1e9, 1),
-                               "frac_hbm": round(nbytes16 / t16 / 1e9 / HBM_PEAK_GBS, 4),
-                               "us_per_launch": round(t16 * 1e6, 2), "bytes": nbytes16}
-    log(f"M=16 sweep: {nbytes16 / t16 / 1e9:.1f} GB/s")
-    ctx.group_destroy(grp16)
-
-    # ---- per-shape sweeps (all 30 layers of one projection in one launch)
-    per_shape = {}
-    for name, K, N in SHAPES:
-        g, pr, nb = build_group(ctx, torch, weights, acts1, 1, select={name})
-        t, _ = time_launches(torch, stream, lambda: ctx.group_run(g), 20, 3)
-        per_shape[f"{name} {K}->{N}"] = {"GB/s": round(nb / t / 1e9, 1), "us": round(t * 1e6, 2)}
-        ctx.group_destroy(g)
-    extra["gemv_m1_per_shape_stacks"] = per_shape
-    # single GEMV launches (one matrix per launch, MALL-resident after warmup)
-    single = {}
-    for (layer, name, K, N, rp, tau) in weights.mats[:7]:
-        _, xi, s, rs = acts1[K]
-        y = torch.empty((N, 1), dtype=torch.float32, device="cuda")
-        t, _ = time_launches(torch, stream,
-                             lambda: ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, 1, out=y), 50, 5)
-        single[f"{name} {K}->{N}"] = {"us": round(t * 1e6, 2),
-                                      "GB/s": round(gemv_bytes(N, K, 1) / t / 1e9, 1)}
-    extra["gemv_m1_single_launch"] = single
-
-    # ---- prefill GEMM (config 2)
-    gemm = {}
+    if not args.no_extra:
+        extra_gemv_lines(ctx, torch, stream, weights, acts1, extra)
     if not args.no_gemm:
-        M, K = 2048, 4096
-        X, xi, s, rs = make_acts(ctx, torch, K, M, 0xB17A0004)
-        for N in (4096, 11008):
-            gen = torch.Generator(device="cuda")
-            gen.manual_seed(0xB17A0005 + N)
-            W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
-            tau = W.abs().double().mean().float().expand(N).contiguous()
-            rp = ctx.repack(ctx.trit_pack(W, tau), K)
-            del W
-            y = torch.empty((N, M), dtype=torch.float32, device="cuda")
-            t, _ = time_launches(torch, stream,
-                                 lambda: ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, out=y),
-                                 max(10, args.steps // 2), 5)
-            tops = 2.0 * M * N * K / t / 1e12
-            gemm[f"M={M} K={K} N={N}"] = {"TOPS": round(tops, 1), "us": round(t * 1e6, 1),
-                                          "frac_int8_mfma": round(tops / INT8_PEAK_TOPS, 4)}
-            log(f"GEMM M={M} K={K} N={N}: {t * 1e6:.1f} us, {tops:.1f} TOPS "
-                f"({tops / INT8_PEAK_TOPS:.3f} of int8 MFMA peak)")
-            del rp, y
-        extra["prefill_gemm"] = gemm
-
-    # ---- CPU baseline (bounded sample, rank 0, N=1)
+        gemm_lines(ctx, torch, stream, args.steps, extra)
     cpu = None
     if not args.no_cpu:
-        from oracle import nn_oracle as orc   # the CPU restatement, timed as the baseline
-        acts_host = {}
-        for K in (D, FFN):
-            X, _, s, _ = acts1[K]
-            s_h = s.cpu().numpy()
-            acts_host[K] = (orc.quantize_i8(X.cpu().numpy(), s_h, True), s_h)
-        log("timing the CPU baseline (about 15 s)")
-        cpu = cpu_baseline(orc, weights, acts_host)
+        log("timing the CPU baseline (about 12 s)")
+        cpu = cpu_baseline(weights, acts1)
         log(f"CPU baseline: {cpu['value']} GB/s with {cpu['cores']} threads")
 
-    waves = ctx.gemv_grid_waves(sum((p["N"] + 15) // 16 for p in probs))
+    n_items = sum((p["N"] + 15) // 16 for p in probs)
     line = {
         "metric": "M=1 ternary GEMV GB/s (% HBM peak); M=2048 GEMM int8 TOPS (% MFMA peak)",
         "value": round(gbs, 1),
@@ -262,9 +270,9 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights, absmean ternary; N(0,1) activations, absmax int8)",
         "config": {"workload": "M=1 ternary x int8 GEMV layer-stack sweep, one grouped launch: "
                                f"{args.layers} layers x q/k/v/o/gate/up/down of d=2560, ffn=6912, kv=640",
-                   "M": 1, "layers": args.layers, "gemvs": len(probs),
+                   "M": 1, "layers": args.layers, "gemvs": len(probs), "row_tiles": n_items,
                    "packed_weight_bytes": wbytes, "algorithmic_bytes": nbytes,
-                   "grid_waves": waves},
+                   "grid_waves": ctx.gemv_grid_waves(n_items)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_gemv_grouped", "avg_launch_us": round(t_launch * 1e6, 2)},

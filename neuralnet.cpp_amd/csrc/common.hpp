@@ -27,6 +27,27 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Largest M handled by the weight-streaming decode GEMV (one 16-token MFMA column block).
 constexpr int kGemvMaxM = 16;
+// Decode GEMV geometry shared by the kernels and the host schedule. Two variants:
+//  * LDS: the group's activations are staged in LDS (they fit kGemvLdsBudget), one 16-row
+//    tile per wave item, 3 k-tile stages in flight, 16 waves per CU (M = 1 decode);
+//  * register: activations are loaded with the weights, 4 row tiles per item share them,
+//    4 stages, 8 waves per CU (larger M).
+// Tuned on MI355X with the 30-layer BitNet-2B sweep (M = 1 and M = 16).
+#ifndef NNHIP_GEMV_LDS_DEPTH
+#define NNHIP_GEMV_LDS_DEPTH 3
+#endif
+constexpr int kLdsRTW = 1, kLdsDepth = NNHIP_GEMV_LDS_DEPTH, kLdsWavesPerCu = 16;
+constexpr int kRegRTW = 4, kRegDepth = 4, kRegWavesPerCu = 8;
+
+struct GemvVariant
+{
+    int row_tiles;
+    int waves_per_cu;
+};
+inline GemvVariant gemv_variant(bool lds)
+{
+    return lds ? GemvVariant{kLdsRTW, kLdsWavesPerCu} : GemvVariant{kRegRTW, kRegWavesPerCu};
+}
 
 struct GemvProblem
 {
@@ -38,7 +59,20 @@ struct GemvProblem
     const float* bias;
     float* y;
     int32_t N, K, M, KT;  // KT = Kp / 256
+    int32_t xlds;         // byte offset of this problem's activations in LDS, or -1
+    int32_t pad_;
 };
+
+// One activation block the decode GEMV stages in LDS at block start (M * Kp bytes).
+struct XStage
+{
+    const int8_t* src;
+    uint32_t bytes;   // multiple of 256
+    uint32_t lds_off;
+};
+
+// LDS budget per block for staged activations (3 blocks of 4 waves fit one CU).
+constexpr uint32_t kGemvLdsBudget = 48 * 1024;
 
 // ---- reference-layout kernels (k_ref.hip)
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* dst, uint32_t value, size_t words);
@@ -66,13 +100,18 @@ hipError_t launch_act_from_container(hipStream_t st, const uint32_t* xq, size_t 
 hipError_t launch_act_to_container(hipStream_t st, const int8_t* xi, size_t K, size_t M,
                                    uint32_t* xq);
 
-// ---- ternary kernels (k_ternary.hip)
+// ---- ternary kernels (k_ternary.hip, k_gemv.hip)
 hipError_t launch_repack(hipStream_t st, const uint32_t* wq, size_t N, size_t K, uint32_t* rp);
 hipError_t launch_unrepack(hipStream_t st, const uint32_t* rp, size_t N, size_t K, uint32_t* wq);
 hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus);
-hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const uint32_t* d_items,
-                               size_t n_items, int num_cus);
-size_t gemv_grid_waves(size_t n_items, int num_cus);
+// Grouped GEMV over a precomputed per-wave schedule: wave w runs the items
+// d_wave_items[d_wave_start[w] .. d_wave_start[w+1]) (item = problem << 20 | row tile).
+// If n_xstage > 0, the listed activation blocks (lds_bytes in total) are staged in LDS at
+// block start and every problem reads its activations at its xlds offset.
+hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const uint32_t* d_wave_start,
+                               const uint32_t* d_wave_items, size_t n_waves, const XStage* d_xstage,
+                               int n_xstage, uint32_t lds_bytes);
+size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds);
 hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus);
 
 }  // namespace nnhip

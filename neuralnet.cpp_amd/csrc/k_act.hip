@@ -26,6 +26,23 @@ __device__ __forceinline__ int quantize_one(float x, float s)
     return (int)roundf(v);
 }
 
+// Correctly rounded fp32 square root. v_sqrt_f32 alone is accurate to 1 ulp; the two
+// fma residuals pick between its neighbours (the same correction LLVM's IEEE fsqrt
+// lowering applies), so the result matches a host sqrtf bit for bit. Inputs here are
+// ms + eps >= eps > 0 and far from the denormal range.
+__device__ __forceinline__ float sqrt_rn(float v)
+{
+    float s = __builtin_sqrtf(v);
+    if (!(v > 0.0f) || isinf(v)) return s;
+    const float s_dn = __int_as_float(__float_as_int(s) - 1);
+    const float s_up = __int_as_float(__float_as_int(s) + 1);
+    const float r_dn = __builtin_fmaf(-s_dn, s, v);
+    const float r_up = __builtin_fmaf(-s_up, s, v);
+    if (r_dn <= 0.0f) s = s_dn;
+    if (r_up > 0.0f) s = s_up;
+    return s;
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
 #pragma unroll
@@ -77,7 +94,7 @@ __global__ __launch_bounds__(kBlock) void k_token_wave(const float* __restrict__
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_xor(part, off, kWave));
-        ri = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fmul_rn(part, inv_f), eps)));
+        ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(part, inv_f), eps)));
     }
 
     if (mode == 1)
@@ -165,7 +182,7 @@ __global__ __launch_bounds__(kTW * kWave) void k_token_lanes(
         for (int off = 32; off >= 1; off >>= 1)
 #pragma unroll
             for (int p = 0; p < off; ++p) v[p] = __fadd_rn(v[p], v[p + off]);
-        ri = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fmul_rn(v[0], inv_f), eps)));
+        ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(v[0], inv_f), eps)));
     }
 
     if (mode == 1)

@@ -1,0 +1,326 @@
+// k_gemv.hip — weight-streaming decode GEMV (M <= 16 tokens) for gfx950.
+//
+// One wave computes RTW consecutive 16-row tiles of one problem against all its (<= 16)
+// tokens with v_mfma_i32_16x16x64_i8, streaming the tiles' K/256 weight tiles (T16K256
+// layout, 1 KiB each: one 16-byte load per lane) from HBM. The activation operands of a
+// k tile are loaded once per stage and shared by the RTW row tiles, so more weight bytes
+// are in flight per register. Codes are trit + 2, so the MFMAs accumulate sum(code * x)
+// and the epilogue subtracts 2 * rowsum. Four accumulators per row tile make the unpack
+// 5 VALU ops per weight word instead of 7:
+//   j=0: w & 0x03030303 (codes)          -> a0      j=1: w & 0x0C0C0C0C (4 * codes)  -> a1
+//   j=2: w & 0x30303030 (16 * codes)     -> a2      j=3: (w >> 6) & 0x03030303       -> a3
+//   acc = a0 + a3 + (a1 >> 2) + (a2 >> 4) - 2 * rowsum       (shifts divide exact multiples)
+//
+// Memory: raw buffer loads. Lanes of tokens t >= M and row tiles past the matrix use
+// out-of-range offsets/resources, which the buffer unit answers with zeros and no memory
+// traffic (no branches around loads). A rolling pipeline keeps kDepth k-tile stages in
+// flight per wave; with the k-tile count known at compile time (the common widths) the
+// loop is fully unrolled and the vmcnt waits only cover the stage being consumed.
+//
+// Epilogue (reference order, src/int8_act_test.cpp:233): y = (tau[n] * s[t]) * float(acc),
+// then y + bias[n] as a separate rounding (compiled with -ffp-contract=off).
+#include "common.hpp"
+
+
+namespace nnhip
+{
+namespace
+{
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kM3 = 0x03030303u;
+constexpr int kBlock = 256;                 // 4 waves
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kRsrcFlags = 0x00020000;      // gfx9-family buffer resource word 3 (raw, dword)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
+}
+
+__device__ __forceinline__ v4i ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c)
+{
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+struct Acc
+{
+    v4i a0, a1, a2, a3;
+};
+
+template <int kRTW>
+struct Stage
+{
+    v4i w[kRTW];  // 4 weight words of this lane, per row tile
+    v4i x[4];     // activation bytes for MFMA j = 0..3 (register path only)
+};
+
+template <int kRTW>
+struct Src
+{
+    __amdgpu_buffer_rsrc_t rw[kRTW];  // one resource per row tile (num_records = KT KiB, 0 past N)
+    __amdgpu_buffer_rsrc_t rx;
+    uint32_t voff_w, voff_x;
+    const uint8_t* xl;  // LDS path: this lane's activation row + 16 g
+};
+
+template <bool LDS, int kRTW>
+__device__ __forceinline__ void load_stage(Stage<kRTW>& st, const Src<kRTW>& s, int kt)
+{
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r) st.w[r] = ld16(s.rw[r], s.voff_w, (uint32_t)kt * 1024u);
+    if constexpr (!LDS)
+    {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) st.x[j] = ld16(s.rx, s.voff_x, (uint32_t)kt * 256u + 64u * j);
+    }
+}
+
+template <int kRTW>
+__device__ __forceinline__ void read_x_lds(v4i (&x)[4], const Src<kRTW>& s, int kt)
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(s.xl + kt * 256 + 64 * j);
+}
+
+template <int kRTW>
+__device__ __forceinline__ void compute_stage(const v4i (&w4)[kRTW], const v4i (&x)[4], Acc (&acc)[kRTW])
+{
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r)
+    {
+        const v4i w = w4[r];
+        acc[r].a0 = mfma16(w & (int)kM3, x[0], acc[r].a0);
+        acc[r].a1 = mfma16(w & (int)(kM3 << 2), x[1], acc[r].a1);
+        acc[r].a2 = mfma16(w & (int)(kM3 << 4), x[2], acc[r].a2);
+        acc[r].a3 = mfma16((v4i)((__builtin_bit_cast(u32x4, w) >> 6) & kM3), x[3], acc[r].a3);
+    }
+}
+
+// Loads are unconditional: a stage past the last k tile reads beyond its resource
+// (num_records = KT KiB), which returns zero words (code 0: no contribution). On the LDS
+// path the activations of stage kt+1 are read from LDS while stage kt computes (LDS reads
+// count on lgkmcnt, so they never wait behind the weight stream).
+template <bool LDS, int kRTW, int kDepth, int KT_FIXED>
+__device__ __forceinline__ void gemv_stream(int KT, const Src<kRTW>& s, Acc (&acc)[kRTW])
+{
+    Stage<kRTW> st[kDepth];
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) load_stage<LDS>(st[u], s, u);
+    v4i xc[4], xn[4];
+    if constexpr (LDS) read_x_lds(xc, s, 0);
+    if constexpr (KT_FIXED > 0)
+    {
+#pragma unroll
+        for (int kt = 0; kt < KT_FIXED; ++kt)
+        {
+            if constexpr (LDS)
+            {
+                if (kt + 1 < KT_FIXED) read_x_lds(xn, s, kt + 1);
+                compute_stage(st[kt % kDepth].w, xc, acc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xc[j] = xn[j];
+            }
+            else
+            {
+                compute_stage(st[kt % kDepth].w, st[kt % kDepth].x, acc);
+            }
+            if (kt + kDepth < KT_FIXED) load_stage<LDS>(st[kt % kDepth], s, kt + kDepth);
+            // keep the stage order: later stages' MFMAs must not be hoisted above these loads
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    else
+    {
+        for (int kt = 0; kt < KT; kt += kDepth)
+        {
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u)
+            {
+                // zero words past KT: adds nothing (the LDS read stays inside the staged row)
+                if constexpr (LDS)
+                {
+                    if (kt + u + 1 < KT) read_x_lds(xn, s, kt + u + 1);
+                    compute_stage(st[u].w, xc, acc);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xc[j] = xn[j];
+                }
+                else
+                {
+                    compute_stage(st[u].w, st[u].x, acc);
+                }
+                load_stage<LDS>(st[u], s, kt + u + kDepth);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+}
+
+// Item = row tiles rt0 .. rt0 + kRTW - 1 of problem p. LDS path: the problem's activations
+// were staged at lds + p.xlds; tokens t >= M read token 0's row (their columns are never
+// stored), so no lane needs zeros.
+template <bool LDS, int kRTW, int kDepth>
+__device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lane, const uint8_t* lds)
+{
+    const int g = lane >> 4, t = lane & 15;
+    const int RT = (p.N + 15) / 16;
+    const uint32_t Kp = (uint32_t)p.KT * kTileK;
+    Src<kRTW> s;
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r)
+    {
+        const int rt = rt0 + r < RT ? rt0 + r : RT - 1;
+        s.rw[r] = rsrc(p.rp + (size_t)rt * p.KT * 64, rt0 + r < RT ? (uint32_t)p.KT * 1024u : 0u);
+    }
+    s.voff_w = (uint32_t)lane * 16u;
+    if constexpr (LDS)
+    {
+        s.xl = lds + p.xlds + (t < p.M ? t : 0) * Kp + 16 * g;
+    }
+    else
+    {
+        s.rx = rsrc(p.xi, (uint32_t)p.M * Kp);
+        s.voff_x = t < p.M ? (uint32_t)t * Kp + 16u * g : kOOB;
+    }
+
+    Acc acc[kRTW];
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r) acc[r].a0 = acc[r].a1 = acc[r].a2 = acc[r].a3 = v4i{0, 0, 0, 0};
+    switch (p.KT)
+    {
+    case 4: gemv_stream<LDS, kRTW, kDepth, 4>(4, s, acc); break;
+    case 10: gemv_stream<LDS, kRTW, kDepth, 10>(10, s, acc); break;
+    case 16: gemv_stream<LDS, kRTW, kDepth, 16>(16, s, acc); break;
+    case 27: gemv_stream<LDS, kRTW, kDepth, 27>(27, s, acc); break;
+    default: gemv_stream<LDS, kRTW, kDepth, 0>(p.KT, s, acc); break;
+    }
+
+    if (t >= p.M) return;
+    const int rs2 = 2 * p.rowsum[t];
+    const float sv = p.s[t];
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int n = (rt0 + r) * 16 + 4 * g + i;
+            if (n < p.N)
+            {
+                const int a = acc[r].a0[i] + acc[r].a3[i] + (acc[r].a1[i] >> 2) + (acc[r].a2[i] >> 4) - rs2;
+                float y = (p.tau[n] * sv) * (float)a;
+                if (p.bias) y = y + p.bias[n];
+                p.y[(size_t)n * p.M + t] = y;
+            }
+        }
+    }
+}
+
+// Copy the listed activation blocks into LDS (whole block cooperates), then barrier.
+__device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__ xs, int n_x)
+{
+    for (int e = 0; e < n_x; ++e)
+    {
+        const XStage x = xs[e];
+        for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kBlock * 16u)
+            *reinterpret_cast<v4i*>(lds + x.lds_off + off) = *reinterpret_cast<const v4i*>(x.src + off);
+    }
+    __syncthreads();
+}
+
+// Single problem: static assignment of items to waves.
+template <bool LDS, int kRTW, int kDepth>
+__global__ __launch_bounds__(kBlock) void k_gemv(GemvProblem p, int n_items, XStage xs)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    if constexpr (LDS) stage_x(lds, &xs, 1);
+    const int lane = threadIdx.x & 63;
+    const int waves = gridDim.x * (kBlock / kWave);
+    const int first = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6));
+    for (int item = first; item < n_items; item += waves) gemv_item<LDS, kRTW, kDepth>(p, item * kRTW, lane, lds);
+}
+
+// Grouped: wave w processes the items wave_items[wave_start[w] .. wave_start[w+1]) (each
+// item = problem << 20 | first row tile). The host balances the per-wave lists by cost
+// once, at group creation, so the kernel needs no atomics or memset and can be replayed.
+template <bool LDS, int kRTW, int kDepth>
+__global__ __launch_bounds__(kBlock) void k_gemv_grouped(const GemvProblem* __restrict__ probs,
+                                                         const uint32_t* __restrict__ wave_start,
+                                                         const uint32_t* __restrict__ wave_items,
+                                                         int n_waves, const XStage* __restrict__ xs,
+                                                         int n_x)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    if constexpr (LDS) stage_x(lds, xs, n_x);
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6));
+    if (w >= n_waves) return;
+    const uint32_t b = wave_start[w], e = wave_start[w + 1];
+    for (uint32_t i = b; i < e; ++i)
+    {
+        const uint32_t it = wave_items[i];
+        const GemvProblem p = probs[it >> 20];
+        gemv_item<LDS, kRTW, kDepth>(p, (int)(it & 0xFFFFFu), lane, lds);
+    }
+}
+
+}  // namespace
+
+size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds)
+{
+    // resident waves per CU for the variant, never more waves than work items
+    const GemvVariant v = gemv_variant(lds);
+    size_t blocks = ceil_div(n_items, (size_t)(kBlock / kWave));
+    const size_t cap = (size_t)(num_cus > 0 ? num_cus : 256) * (v.waves_per_cu / (kBlock / kWave));
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    return blocks * (kBlock / kWave);
+}
+
+hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus)
+{
+    if (p.N == 0 || p.M == 0) return hipSuccess;
+    const uint32_t xbytes = (uint32_t)p.M * (uint32_t)p.KT * kTileK;
+    const bool lds = xbytes <= kGemvLdsBudget;
+    const GemvVariant v = gemv_variant(lds);
+    const size_t items = ceil_div(ceil_div((size_t)p.N, 16), (size_t)v.row_tiles);
+    const unsigned blocks = (unsigned)(gemv_grid_waves(items, num_cus, lds) / (kBlock / kWave));
+    GemvProblem q = p;
+    if (lds)
+    {
+        q.xlds = 0;
+        const XStage xs{p.xi, xbytes, 0};
+        hipLaunchKernelGGL((k_gemv<true, kLdsRTW, kLdsDepth>), dim3(blocks), dim3(kBlock), xbytes, st, q,
+                           (int)items, xs);
+    }
+    else
+    {
+        q.xlds = -1;
+        hipLaunchKernelGGL((k_gemv<false, kRegRTW, kRegDepth>), dim3(blocks), dim3(kBlock), 0, st, q,
+                           (int)items, XStage{});
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const uint32_t* d_wave_start,
+                               const uint32_t* d_wave_items, size_t n_waves, const XStage* d_xstage,
+                               int n_xstage, uint32_t lds_bytes)
+{
+    if (n_waves == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)ceil_div(n_waves, (size_t)(kBlock / kWave));
+    if (n_xstage > 0)
+        hipLaunchKernelGGL((k_gemv_grouped<true, kLdsRTW, kLdsDepth>), dim3(blocks), dim3(kBlock), lds_bytes,
+                           st, d_probs, d_wave_start, d_wave_items, (int)n_waves, d_xstage, n_xstage);
+    else
+        hipLaunchKernelGGL((k_gemv_grouped<false, kRegRTW, kRegDepth>), dim3(blocks), dim3(kBlock), 0, st,
+                           d_probs, d_wave_start, d_wave_items, (int)n_waves, d_xstage, 0);
+    return hipGetLastError();
+}
+
+}  // namespace nnhip

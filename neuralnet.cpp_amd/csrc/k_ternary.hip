@@ -1,5 +1,5 @@
-// k_ternary.hip — ternary x int8 kernels for gfx950: the load-time repacker, the
-// weight-streaming decode GEMV (M <= 16) and the MFMA prefill GEMM.
+// k_ternary.hip — ternary x int8 kernels for gfx950: the load-time repacker and the
+// MFMA prefill GEMM (the decode GEMV is in k_gemv.hip).
 //
 // Weights use the T16K256 layout (see include/nnhip.h, oracle/nn_oracle.c): one 1 KiB tile
 // per 16 rows x 256 k, whose 64 lanes x 16 bytes are exactly the A operands of four
@@ -81,109 +81,6 @@ __global__ __launch_bounds__(256) void k_unrepack(const uint32_t* __restrict__ r
             word |= code << (2 * e);
         }
         wq[idx] = word;
-    }
-}
-
-// ------------------------------------------------------------------ decode GEMV (M <= 16)
-//
-// One wave computes a whole 16-row tile against all (<= 16) tokens, streaming the row
-// tile's K/256 weight tiles (1 KiB each, one 16-byte load per lane) from HBM. Four
-// accumulators let the unpack cost 5 VALU ops per word instead of 7:
-//   j=0: w & 0x03030303 (codes)           -> acc0
-//   j=1: w & 0x0C0C0C0C (4 * codes)       -> acc1
-//   j=2: w & 0x30303030 (16 * codes)      -> acc2
-//   j=3: (w >> 6) & 0x03030303 (codes)    -> acc3
-// acc = acc0 + acc3 + (acc1 >> 2) + (acc2 >> 4); the shifts divide exact multiples.
-// The B operand of lane (g, t) is 16 bytes of token t (zero for t >= M).
-
-constexpr int kGemvBlock = 256;  // 4 waves
-constexpr int kGemvUnroll = 4;
-
-__device__ __forceinline__ void gemv_ktile(const u32x4 w, const int8_t* __restrict__ xk, bool tok_ok,
-                                           v4i& a0, v4i& a1, v4i& a2, v4i& a3)
-{
-    const v4i zero = {0, 0, 0, 0};
-    const v4i b0 = tok_ok ? *reinterpret_cast<const v4i*>(xk) : zero;
-    const v4i b1 = tok_ok ? *reinterpret_cast<const v4i*>(xk + 64) : zero;
-    const v4i b2 = tok_ok ? *reinterpret_cast<const v4i*>(xk + 128) : zero;
-    const v4i b3 = tok_ok ? *reinterpret_cast<const v4i*>(xk + 192) : zero;
-    v4i a;
-    a = v4i{(int)(w.x & kM3), (int)(w.y & kM3), (int)(w.z & kM3), (int)(w.w & kM3)};
-    a0 = mfma16(a, b0, a0);
-    a = v4i{(int)(w.x & (kM3 << 2)), (int)(w.y & (kM3 << 2)), (int)(w.z & (kM3 << 2)),
-            (int)(w.w & (kM3 << 2))};
-    a1 = mfma16(a, b1, a1);
-    a = v4i{(int)(w.x & (kM3 << 4)), (int)(w.y & (kM3 << 4)), (int)(w.z & (kM3 << 4)),
-            (int)(w.w & (kM3 << 4))};
-    a2 = mfma16(a, b2, a2);
-    a = v4i{(int)((w.x >> 6) & kM3), (int)((w.y >> 6) & kM3), (int)((w.z >> 6) & kM3),
-            (int)((w.w >> 6) & kM3)};
-    a3 = mfma16(a, b3, a3);
-}
-
-__device__ __forceinline__ void gemv_row_tile(const GemvProblem& p, int rt, int lane)
-{
-    const int g = lane >> 4, t = lane & 15;
-    const bool tok_ok = t < p.M;
-    const size_t Kp = (size_t)p.KT * kTileK;
-    const u32x4* wp = p.rp + (size_t)rt * p.KT * 64 + lane;
-    const int8_t* xrow = p.xi + (tok_ok ? (size_t)t * Kp : 0) + 16 * g;
-
-    v4i a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
-    int kt = 0;
-    for (; kt + kGemvUnroll <= p.KT; kt += kGemvUnroll)
-    {
-        u32x4 w[kGemvUnroll];
-#pragma unroll
-        for (int u = 0; u < kGemvUnroll; ++u) w[u] = __builtin_nontemporal_load(wp + (size_t)(kt + u) * 64);
-#pragma unroll
-        for (int u = 0; u < kGemvUnroll; ++u)
-            gemv_ktile(w[u], xrow + (size_t)(kt + u) * kTileK, tok_ok, a0, a1, a2, a3);
-    }
-    for (; kt < p.KT; ++kt)
-    {
-        const u32x4 w = __builtin_nontemporal_load(wp + (size_t)kt * 64);
-        gemv_ktile(w, xrow + (size_t)kt * kTileK, tok_ok, a0, a1, a2, a3);
-    }
-
-    if (!tok_ok) return;
-    const int rs2 = 2 * p.rowsum[t];
-    const float sv = p.s[t];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-    {
-        const int n = rt * 16 + 4 * g + r;
-        if (n < p.N)
-        {
-            const int acc = a0[r] + a3[r] + (a1[r] >> 2) + (a2[r] >> 4) - rs2;
-            float y = __fmul_rn(__fmul_rn(p.tau[n], sv), (float)acc);
-            if (p.bias) y = __fadd_rn(y, p.bias[n]);
-            p.y[(size_t)n * p.M + t] = y;
-        }
-    }
-}
-
-__global__ __launch_bounds__(kGemvBlock) void k_gemv(GemvProblem p, int n_items)
-{
-    const int lane = threadIdx.x & 63;
-    const int waves = gridDim.x * (kGemvBlock / kWave);
-    for (int item = blockIdx.x * (kGemvBlock / kWave) + (threadIdx.x >> 6); item < n_items;
-         item += waves)
-        gemv_row_tile(p, item, lane);
-}
-
-// items[i] = (problem << 20) | row_tile
-__global__ __launch_bounds__(kGemvBlock) void k_gemv_grouped(const GemvProblem* __restrict__ probs,
-                                                             const uint32_t* __restrict__ items,
-                                                             int n_items)
-{
-    const int lane = threadIdx.x & 63;
-    const int waves = gridDim.x * (kGemvBlock / kWave);
-    for (int i = blockIdx.x * (kGemvBlock / kWave) + (threadIdx.x >> 6); i < n_items; i += waves)
-    {
-        const uint32_t it = items[i];
-        const GemvProblem p = probs[it >> 20];
-        gemv_row_tile(p, (int)(it & 0xFFFFFu), lane);
     }
 }
 
@@ -354,36 +251,6 @@ hipError_t launch_unrepack(hipStream_t st, const uint32_t* rp, size_t N, size_t 
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(k_unrepack, dim3(grid_cap(ceil_div(total, 256))), dim3(256), 0, st, rp, N, K, KT,
                        wq);
-    return hipGetLastError();
-}
-
-size_t gemv_grid_waves(size_t n_items, int num_cus)
-{
-    // enough resident waves to keep HBM busy (8 blocks of 4 waves per CU), never more
-    // waves than work items
-    size_t blocks = ceil_div(n_items, (size_t)(kGemvBlock / kWave));
-    const size_t cap = (size_t)(num_cus > 0 ? num_cus : 256) * 8;
-    if (blocks > cap) blocks = cap;
-    if (blocks < 1) blocks = 1;
-    return blocks * (kGemvBlock / kWave);
-}
-
-hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus)
-{
-    const size_t items = ceil_div((size_t)p.N, 16);
-    if (items == 0 || p.M == 0) return hipSuccess;
-    const unsigned blocks = (unsigned)(gemv_grid_waves(items, num_cus) / (kGemvBlock / kWave));
-    hipLaunchKernelGGL(k_gemv, dim3(blocks), dim3(kGemvBlock), 0, st, p, (int)items);
-    return hipGetLastError();
-}
-
-hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const uint32_t* d_items,
-                               size_t n_items, int num_cus)
-{
-    if (n_items == 0) return hipSuccess;
-    const unsigned blocks = (unsigned)(gemv_grid_waves(n_items, num_cus) / (kGemvBlock / kWave));
-    hipLaunchKernelGGL(k_gemv_grouped, dim3(blocks), dim3(kGemvBlock), 0, st, d_probs, d_items,
-                       (int)n_items);
     return hipGetLastError();
 }
 

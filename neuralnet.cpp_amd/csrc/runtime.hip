@@ -6,8 +6,10 @@
 
 #include "common.hpp"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <queue>
 #include <string>
 #include <vector>
 
@@ -26,8 +28,12 @@ struct nnhip_ctx
 struct nnhip_group
 {
     GemvProblem* d_probs = nullptr;
-    uint32_t* d_items = nullptr;
-    size_t n_items = 0;
+    uint32_t* d_wave_start = nullptr;  // n_waves + 1 offsets into d_wave_items
+    uint32_t* d_wave_items = nullptr;  // problem << 20 | row tile, grouped by wave
+    XStage* d_xstage = nullptr;        // activation blocks staged in LDS (if they fit)
+    int n_xstage = 0;
+    uint32_t lds_bytes = 0;
+    size_t n_waves = 0;
 };
 
 namespace
@@ -123,6 +129,7 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     p.K = (int32_t)K;
     p.M = (int32_t)M;
     p.KT = (int32_t)ceil_div(K, kTileK);
+    p.xlds = -1;
     if (M <= (size_t)kGemvMaxM)
         NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
     else
@@ -545,7 +552,6 @@ nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, si
     NNHIP_REQUIRE(descs != nullptr || count == 0, fn, "null descriptors");
     NNHIP_REQUIRE(count < (1u << 12), fn, "at most 4095 problems per group");
     std::vector<GemvProblem> probs(count);
-    std::vector<uint32_t> items;
     for (size_t i = 0; i < count; ++i)
     {
         const nnhip_gemv_desc& d = descs[i];
@@ -566,27 +572,115 @@ nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, si
         p.K = (int32_t)d.K;
         p.M = (int32_t)d.M;
         p.KT = (int32_t)ceil_div(d.K, kTileK);
-        const size_t rts = ceil_div(d.N, 16);
-        for (size_t rt = 0; rt < rts; ++rt) items.push_back((uint32_t)((i << 20) | rt));
+        p.xlds = -1;
+    }
+
+    // Distinct activation blocks: if they fit the LDS budget together, every block of the
+    // kernel stages them once and the problems read their B operands from LDS (LDS variant);
+    // otherwise the register variant loads them with the weights.
+    std::vector<XStage> xstage;
+    {
+        uint32_t lds = 0;
+        bool fits = true;
+        for (GemvProblem& p : probs)
+        {
+            const uint32_t bytes = (uint32_t)p.M * (uint32_t)p.KT * kTileK;
+            int found = -1;
+            for (size_t e = 0; e < xstage.size(); ++e)
+                if (xstage[e].src == p.xi && xstage[e].bytes == bytes) found = (int)e;
+            if (found < 0)
+            {
+                if (lds + bytes > kGemvLdsBudget)
+                {
+                    fits = false;
+                    break;
+                }
+                xstage.push_back(XStage{p.xi, bytes, lds});
+                found = (int)xstage.size() - 1;
+                lds += bytes;
+            }
+            p.xlds = (int32_t)xstage[found].lds_off;
+        }
+        if (!fits)
+        {
+            xstage.clear();
+            for (GemvProblem& p : probs) p.xlds = -1;
+        }
+    }
+    const bool use_lds = !xstage.empty();
+    const GemvVariant var = gemv_variant(use_lds);
+
+    std::vector<uint32_t> items;
+    for (size_t i = 0; i < count; ++i)
+    {
+        const size_t rts = ceil_div((size_t)probs[i].N, 16);
+        for (size_t rt = 0; rt < rts; rt += (size_t)var.row_tiles) items.push_back((uint32_t)((i << 20) | rt));
     }
     NNHIP_REQUIRE(items.size() < 0x7FFFFFFFull, fn, "too many row tiles");
+
+    // Longest-processing-time schedule: items (var.row_tiles row tiles of one problem) by
+    // decreasing cost (weight tiles + 1 for the epilogue), each to the currently
+    // least-loaded wave. Waves = the variant's resident wave slots.
+    const size_t n_waves = items.empty() ? 0 : gemv_grid_waves(items.size(), ctx->num_cus, use_lds);
+    std::vector<uint32_t> wave_start(n_waves + 1, 0), wave_items(items.size());
+    if (n_waves > 0)
+    {
+        auto cost = [&](uint32_t it) {
+            const GemvProblem& p = probs[it >> 20];
+            const uint64_t rts = std::min<uint64_t>((uint64_t)var.row_tiles, ceil_div(p.N, 16) - (it & 0xFFFFFu));
+            return (uint64_t)p.KT * rts + 1;
+        };
+        std::stable_sort(items.begin(), items.end(), [&](uint32_t a, uint32_t b) { return cost(a) > cost(b); });
+        using Slot = std::pair<uint64_t, uint32_t>;  // (load, wave)
+        std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> heap;
+        for (uint32_t w = 0; w < n_waves; ++w) heap.push({0, w});
+        std::vector<std::vector<uint32_t>> lists(n_waves);
+        for (const uint32_t it : items)
+        {
+            Slot sl = heap.top();
+            heap.pop();
+            lists[sl.second].push_back(it);
+            sl.first += cost(it);
+            heap.push(sl);
+        }
+        size_t pos = 0;
+        for (size_t w = 0; w < n_waves; ++w)
+        {
+            wave_start[w] = (uint32_t)pos;
+            for (const uint32_t it : lists[w]) wave_items[pos++] = it;
+        }
+        wave_start[n_waves] = (uint32_t)pos;
+    }
+
     auto* grp = new nnhip_group;
-    grp->n_items = items.size();
-    if (count > 0)
+    grp->n_waves = n_waves;
+    grp->n_xstage = (int)xstage.size();
+    for (const XStage& x : xstage) grp->lds_bytes += x.bytes;
+    if (n_waves > 0)
     {
         hipError_t e = hipMalloc(&grp->d_probs, sizeof(GemvProblem) * count);
-        if (e == hipSuccess && !items.empty()) e = hipMalloc(&grp->d_items, sizeof(uint32_t) * items.size());
+        if (e == hipSuccess && !xstage.empty()) e = hipMalloc(&grp->d_xstage, sizeof(XStage) * xstage.size());
+        if (e == hipSuccess && !xstage.empty())
+            e = hipMemcpyAsync(grp->d_xstage, xstage.data(), sizeof(XStage) * xstage.size(),
+                               hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipMalloc(&grp->d_wave_start, sizeof(uint32_t) * wave_start.size());
+        if (e == hipSuccess) e = hipMalloc(&grp->d_wave_items, sizeof(uint32_t) * wave_items.size());
         if (e == hipSuccess)
             e = hipMemcpyAsync(grp->d_probs, probs.data(), sizeof(GemvProblem) * count,
                                hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess && !items.empty())
-            e = hipMemcpyAsync(grp->d_items, items.data(), sizeof(uint32_t) * items.size(),
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(grp->d_wave_start, wave_start.data(), sizeof(uint32_t) * wave_start.size(),
+                               hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(grp->d_wave_items, wave_items.data(), sizeof(uint32_t) * wave_items.size(),
                                hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess)
         {
-            if (grp->d_probs) (void)hipFree(grp->d_probs);
-            if (grp->d_items) (void)hipFree(grp->d_items);
+            (void)hipFree(grp->d_probs);
+            (void)hipFree(grp->d_wave_start);
+            (void)hipFree(grp->d_wave_items);
+            (void)hipFree(grp->d_xstage);
             delete grp;
             return hip_fail(fn, "descriptor upload", e);
         }
@@ -600,8 +694,9 @@ nnhip_status nnhip_group_run(nnhip_ctx* ctx, nnhip_group* group)
     const char* fn = "nnhip_group_run";
     NNHIP_CHECK_CTX(fn);
     NNHIP_REQUIRE(group != nullptr, fn, "null group");
-    NNHIP_LAUNCH(fn, launch_gemv_grouped(ctx->stream, group->d_probs, group->d_items, group->n_items,
-                                         ctx->num_cus));
+    NNHIP_LAUNCH(fn, launch_gemv_grouped(ctx->stream, group->d_probs, group->d_wave_start,
+                                         group->d_wave_items, group->n_waves, group->d_xstage,
+                                         group->n_xstage, group->lds_bytes));
     return NNHIP_OK;
 }
 
@@ -611,8 +706,10 @@ nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group)
     NNHIP_CHECK_CTX(fn);
     if (!group) return NNHIP_OK;
     const hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (group->d_probs) (void)hipFree(group->d_probs);
-    if (group->d_items) (void)hipFree(group->d_items);
+    (void)hipFree(group->d_probs);
+    (void)hipFree(group->d_wave_start);
+    (void)hipFree(group->d_wave_items);
+    (void)hipFree(group->d_xstage);
     delete group;
     if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
     return NNHIP_OK;
@@ -620,7 +717,7 @@ nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group)
 
 size_t nnhip_gemv_grid_waves(nnhip_ctx* ctx, size_t items)
 {
-    return gemv_grid_waves(items, ctx ? ctx->num_cus : 256);
+    return gemv_grid_waves(items, ctx ? ctx->num_cus : 256, true);
 }
 
 }  // extern "C"
