@@ -1,0 +1,251 @@
+// compute_engine.cpp — the NVI layer of nn::ComputeEngine: domain, shape and precision
+// checks, output allocation and write-epoch bookkeeping around the engine's *_impl calls.
+// Shape contracts follow the reference call sites (see compute_engine.hpp).
+#include "neuralnet.cpp/compute_engine.hpp"
+
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "neuralnet.cpp/int8_pack.hpp"
+#include "neuralnet.cpp/ternary_pack.hpp"
+
+namespace nn
+{
+
+namespace
+{
+std::string shape(const Tensor& t) { return std::to_string(t.rows()) + "x" + std::to_string(t.cols()); }
+
+Result<void> require_f32(const Tensor& t, const char* fn, const char* what)
+{
+    if (!t.valid()) return Error{std::string(fn) + ": " + what + " is an empty tensor"};
+    if (t.precision() != Precision::F32)
+        return Error{std::string(fn) + ": " + what + " has precision " + precision_name(t.precision()) +
+                     "; this engine runs the W1.58A8 path in f32 containers only"};
+    return {};
+}
+
+// Write-epoch guard: the destination's epoch advances when the entry returns, success or not.
+struct EpochGuard
+{
+    const Tensor& t;
+    ~EpochGuard() { TensorAccess::mark_written(t); }
+};
+}  // namespace
+
+Result<void> ComputeEngine::check_owned(const Tensor& t, const char* what) const
+{
+    const detail::Storage* st = TensorAccess::storage(t);
+    if (!st) return Error{std::string(what) + ": empty tensor"};
+    if (st->owner != this) return Error{std::string(what) + ": tensor belongs to another engine"};
+    return {};
+}
+
+Tensor ComputeEngine::create_tensor(std::size_t rows, std::size_t cols, Precision p, InitSpec init)
+{
+    if (p != Precision::F32) return Tensor{};
+    auto t = alloc_impl(rows, cols, p);
+    if (!t) return Tensor{};
+    std::vector<float> host(rows * cols, 0.0f);
+    if (init.kind == InitSpec::Kind::Constant)
+        for (float& v : host) v = init.a;
+    else if (init.kind == InitSpec::Kind::Uniform)
+    {
+        std::mt19937 rng(static_cast<std::uint32_t>(init.seed));
+        std::uniform_real_distribution<float> d(init.a, init.b);
+        for (float& v : host) v = d(rng);
+    }
+    if (!host.empty() && !upload_impl(*t, host.data(), host.size() * sizeof(float))) return Tensor{};
+    return *t;
+}
+
+Result<Tensor> ComputeEngine::from_matrix(const Matrix& m, Precision p)
+{
+    if (p != Precision::F32)
+        return Error{std::string("from_matrix: precision ") + precision_name(p) + " is not supported by this engine"};
+    EX_TRY(t, alloc_impl(m.rows(), m.cols(), p));
+    if (m.size() > 0) EX_TRY_CHECK(upload_impl(*t, m.data(), m.size() * sizeof(float)));
+    return *t;
+}
+
+Result<Matrix> ComputeEngine::to_matrix(const Tensor& t, Precision p)
+{
+    EX_TRY_CHECK(check_owned(t, "to_matrix"));
+    if (p != Precision::F32) return Error{"to_matrix: only f32 output is supported"};
+    Matrix m(t.rows(), t.cols());
+    if (m.size() > 0) EX_TRY_CHECK(download_impl(t, m.data(), m.size() * sizeof(float)));
+    return m;
+}
+
+Result<void> ComputeEngine::copy_from(Tensor& dst, const Matrix& src)
+{
+    EX_TRY_CHECK(check_owned(dst, "copy_from"));
+    EpochGuard g{dst};
+    if (dst.rows() != src.rows() || dst.cols() != src.cols())
+        return Error{"copy_from: shape mismatch (tensor " + shape(dst) + ", matrix " + std::to_string(src.rows()) +
+                     "x" + std::to_string(src.cols()) + ")"};
+    if (src.size() == 0) return {};
+    return upload_impl(dst, src.data(), src.size() * sizeof(float));
+}
+
+Result<Tensor> ComputeEngine::trit_pack(const Tensor& W, const Tensor& tau)
+{
+    EX_TRY_CHECK(check_owned(W, "trit_pack"));
+    EX_TRY(out, alloc_impl(W.rows(), trit_pack::words_per_row(W.cols()), Precision::F32));
+    EX_TRY_CHECK(trit_pack_into(W, tau, *out));
+    return *out;
+}
+
+Result<void> ComputeEngine::trit_pack_into(const Tensor& W, const Tensor& tau, Tensor& out)
+{
+    EX_TRY_CHECK(check_owned(W, "trit_pack_into: W"));
+    EX_TRY_CHECK(check_owned(tau, "trit_pack_into: tau"));
+    EX_TRY_CHECK(check_owned(out, "trit_pack_into: out"));
+    EpochGuard g{out};
+    EX_TRY_CHECK(require_f32(W, "trit_pack_into", "W"));
+    EX_TRY_CHECK(require_f32(tau, "trit_pack_into", "tau"));
+    if (tau.rows() != W.rows() || tau.cols() != 1)
+        return Error{"trit_pack_into: tau must be (" + std::to_string(W.rows()) + ",1), got " + shape(tau)};
+    if (out.rows() != W.rows() || out.cols() != trit_pack::words_per_row(W.cols()))
+        return Error{"trit_pack_into: out must be (rows, ceil(K/16)), got " + shape(out)};
+    return trit_pack_impl(W, tau, out);
+}
+
+Result<void> ComputeEngine::row_absmean_into(const Tensor& W, Tensor& tau)
+{
+    EX_TRY_CHECK(check_owned(W, "row_absmean_into: W"));
+    EX_TRY_CHECK(check_owned(tau, "row_absmean_into: tau"));
+    EpochGuard g{tau};
+    EX_TRY_CHECK(require_f32(W, "row_absmean_into", "W"));
+    if (tau.rows() != W.rows() || tau.cols() != 1)
+        return Error{"row_absmean_into: tau must be (" + std::to_string(W.rows()) + ",1), got " + shape(tau)};
+    if (W.cols() == 0) return Error{"row_absmean_into: W has no columns"};
+    return row_absmean_impl(W, tau);
+}
+
+Result<Tensor> ComputeEngine::abs(const Tensor& x)
+{
+    EX_TRY_CHECK(check_owned(x, "abs"));
+    EX_TRY_CHECK(require_f32(x, "abs", "x"));
+    EX_TRY(out, alloc_impl(x.rows(), x.cols(), Precision::F32));
+    EX_TRY_CHECK(abs_impl(x, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::col_reduce_max(const Tensor& x, Precision p)
+{
+    EX_TRY_CHECK(check_owned(x, "col_reduce_max"));
+    EX_TRY_CHECK(require_f32(x, "col_reduce_max", "x"));
+    if (p != Precision::F32) return Error{"col_reduce_max: only f32 output is supported"};
+    EX_TRY(out, alloc_impl(1, x.cols(), Precision::F32));
+    EX_TRY_CHECK(col_reduce_max_impl(x, *out));
+    return *out;
+}
+
+Result<void> ComputeEngine::scale_inplace(Tensor& x, Scalar s)
+{
+    EX_TRY_CHECK(check_owned(x, "scale_inplace"));
+    EpochGuard g{x};
+    EX_TRY_CHECK(require_f32(x, "scale_inplace", "x"));
+    return scale_impl(x, s);
+}
+
+Result<Tensor> ComputeEngine::quantize_i8(const Tensor& x, const Tensor& scale, bool col_scale)
+{
+    EX_TRY_CHECK(check_owned(x, "quantize_i8: x"));
+    EX_TRY_CHECK(check_owned(scale, "quantize_i8: scale"));
+    EX_TRY_CHECK(require_f32(x, "quantize_i8", "x"));
+    EX_TRY_CHECK(require_f32(scale, "quantize_i8", "scale"));
+    if (col_scale ? (scale.rows() != 1 || scale.cols() != x.cols()) : (scale.rows() != x.rows() || scale.cols() != 1))
+        return Error{"quantize_i8: scale must be " +
+                     std::string(col_scale ? "(1, cols)" : "(rows, 1)") + ", got " + shape(scale)};
+    EX_TRY(out, alloc_impl(x.rows(), i8_pack::words_per_row(x.cols()), Precision::F32));
+    EX_TRY_CHECK(quantize_i8_impl(x, scale, col_scale, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::unpack_i8(const Tensor& packed, std::size_t cols)
+{
+    EX_TRY_CHECK(check_owned(packed, "unpack_i8"));
+    if (packed.cols() != i8_pack::words_per_row(cols))
+        return Error{"unpack_i8: container " + shape(packed) + " does not hold " + std::to_string(cols) + " columns"};
+    EX_TRY(out, alloc_impl(packed.rows(), cols, Precision::F32));
+    EX_TRY_CHECK(unpack_i8_impl(packed, cols, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::matmul_q_i8(const Tensor& wq, const Tensor& tau, const Tensor& xq, const Tensor& s,
+                                          Precision p)
+{
+    EX_TRY_CHECK(check_owned(wq, "matmul_q_i8: wq"));
+    EX_TRY_CHECK(check_owned(tau, "matmul_q_i8: tau"));
+    EX_TRY_CHECK(check_owned(xq, "matmul_q_i8: xq"));
+    EX_TRY_CHECK(check_owned(s, "matmul_q_i8: s"));
+    if (p != Precision::F32) return Error{"matmul_q_i8: only f32 output is supported by this engine"};
+    const std::size_t N = wq.rows(), K = xq.rows(), M = s.cols();
+    if (s.rows() != 1) return Error{"matmul_q_i8: s must be (1, M), got " + shape(s)};
+    if (wq.cols() != trit_pack::words_per_row(K))
+        return Error{"matmul_q_i8: wq " + shape(wq) + " does not match K=" + std::to_string(K)};
+    if (xq.cols() != i8_pack::words_per_row(M))
+        return Error{"matmul_q_i8: xq " + shape(xq) + " does not match M=" + std::to_string(M)};
+    if (tau.rows() != N || tau.cols() != 1) return Error{"matmul_q_i8: tau must be (N,1), got " + shape(tau)};
+    EX_TRY(y, alloc_impl(N, M, Precision::F32));
+    EX_TRY_CHECK(matmul_q_i8_impl(wq, tau, xq, s, *y));
+    return *y;
+}
+
+Result<Tensor> ComputeEngine::add_row_broadcast(const Tensor& y, const Tensor& b)
+{
+    EX_TRY_CHECK(check_owned(y, "add_row_broadcast: y"));
+    EX_TRY_CHECK(check_owned(b, "add_row_broadcast: b"));
+    if (b.rows() != y.rows() || b.cols() != 1)
+        return Error{"add_row_broadcast: b must be (" + std::to_string(y.rows()) + ",1), got " + shape(b)};
+    EX_TRY(out, alloc_impl(y.rows(), y.cols(), Precision::F32));
+    EX_TRY_CHECK(add_row_broadcast_impl(y, b, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::rmsnorm(const Tensor& x, const Tensor& gamma, Scalar eps)
+{
+    EX_TRY_CHECK(check_owned(x, "rmsnorm: x"));
+    EX_TRY_CHECK(check_owned(gamma, "rmsnorm: gamma"));
+    if (gamma.rows() != x.rows() || gamma.cols() != 1)
+        return Error{"rmsnorm: gamma must be (" + std::to_string(x.rows()) + ",1), got " + shape(gamma)};
+    EX_TRY(out, alloc_impl(x.rows(), x.cols(), Precision::F32));
+    EX_TRY_CHECK(rmsnorm_impl(x, gamma, eps, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::bitlinear_i8_forward(const Tensor& x, const Tensor& wq, const Tensor& tau,
+                                                   const Tensor& b, Precision p, Tensor* xq_out, Tensor* s_out)
+{
+    EX_TRY_CHECK(check_owned(x, "bitlinear_i8_forward: x"));
+    EX_TRY_CHECK(check_owned(wq, "bitlinear_i8_forward: wq"));
+    EX_TRY_CHECK(check_owned(tau, "bitlinear_i8_forward: tau"));
+    EX_TRY_CHECK(check_owned(b, "bitlinear_i8_forward: b"));
+    if (p != Precision::F32) return Error{"bitlinear_i8_forward: only f32 output is supported by this engine"};
+    if (wq.cols() != trit_pack::words_per_row(x.rows()))
+        return Error{"bitlinear_i8_forward: wq " + shape(wq) + " does not match input rows " + std::to_string(x.rows())};
+    if (tau.rows() != wq.rows() || b.rows() != wq.rows())
+        return Error{"bitlinear_i8_forward: tau / bias rows do not match wq"};
+    return bitlinear_i8_impl(x, wq, tau, b, xq_out, s_out);
+}
+
+// Default composition, exactly the reference layer's call sequence
+// (include/neuralnet.cpp/compute_layer_bitlinear.hpp:443-456).
+Result<Tensor> ComputeEngine::bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor& b,
+                                                Tensor* xq_out, Tensor* s_out)
+{
+    EX_TRY(xabs, abs(x));
+    EX_TRY(sraw, col_reduce_max(*xabs));
+    EX_TRY_CHECK(scale_inplace(*sraw, 1.0f / 127.0f));
+    EX_TRY(xq, quantize_i8(x, *sraw, true));
+    EX_TRY(y, matmul_q_i8(wq, tau, *xq, *sraw));
+    if (xq_out) *xq_out = *xq;
+    if (s_out) *s_out = *sraw;
+    return add_row_broadcast(*y, b);
+}
+
+}  // namespace nn

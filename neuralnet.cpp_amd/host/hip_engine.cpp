@@ -1,0 +1,280 @@
+// hip_engine.cpp — nn::HipEngine: the nn::ComputeEngine of libnn-hip.so. Plain C++ over the
+// C ABI (include/nnhip.h); no HIP header is included here.
+//
+// Engine-private layouts stay behind the interface: matmul_q_i8 repacks the reference
+// ternary container into the T16K256 tile layout once per (storage, write epoch) and caches
+// it on the weight tensor's storage; activations are converted to the token-major int8
+// layout in engine scratch. bitlinear_i8_forward runs the fused path: one quantization
+// kernel (abs-max, scale, int8, row sums) and one GEMV/GEMM launch with the bias add in
+// its epilogue, producing the same bits as the reference call sequence.
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "neuralnet.cpp/hip_engine.hpp"
+#include "neuralnet.cpp/int8_pack.hpp"
+#include "neuralnet.cpp/ternary_pack.hpp"
+#include "nnhip.h"
+
+namespace nn
+{
+
+namespace
+{
+
+thread_local std::string g_factory_error;
+
+Error hip_error(const char* what)
+{
+    return Error{std::string("HipEngine: ") + what + ": " + nnhip_last_error()};
+}
+
+#define NNHIP_TRY(call, what)                         \
+    do                                                \
+    {                                                 \
+        if ((call) != NNHIP_OK) return hip_error(what); \
+    } while (0)
+
+const float* fp(const Tensor& t) { return static_cast<const float*>(TensorAccess::ptr(t)); }
+float* fpw(const Tensor& t) { return static_cast<float*>(TensorAccess::ptr(t)); }
+const uint32_t* up(const Tensor& t) { return static_cast<const uint32_t*>(TensorAccess::ptr(t)); }
+uint32_t* upw(const Tensor& t) { return static_cast<uint32_t*>(TensorAccess::ptr(t)); }
+
+// Context shared with every allocation's deleter, so buffers can be freed after the engine.
+struct Ctx
+{
+    nnhip_ctx* h = nullptr;
+    ~Ctx()
+    {
+        if (h) (void)nnhip_ctx_destroy(h);
+    }
+};
+
+class HipEngine final : public ComputeEngine
+{
+public:
+    explicit HipEngine(std::shared_ptr<Ctx> ctx, int device) : ctx_(std::move(ctx)), device_(device) {}
+    ~HipEngine() override { (void)nnhip_sync(ctx_->h); }
+
+protected:
+    Result<std::shared_ptr<void>> device_alloc(std::size_t bytes)
+    {
+        void* p = nullptr;
+        NNHIP_TRY(nnhip_malloc(ctx_->h, bytes < 16 ? 16 : bytes, &p), "allocation");
+        std::shared_ptr<Ctx> keep = ctx_;
+        return std::shared_ptr<void>(p, [keep](void* q) { (void)nnhip_free(keep->h, q); });
+    }
+
+    Result<Tensor> alloc_impl(std::size_t rows, std::size_t cols, Precision p) override
+    {
+        auto st = std::make_shared<detail::Storage>();
+        st->bytes = rows * cols * sizeof(float);
+        EX_TRY(mem, device_alloc(st->bytes));
+        st->mem = *mem;
+        st->owner = this;
+        return TensorAccess::make(std::move(st), rows, cols, p);
+    }
+
+    Result<void> upload_impl(const Tensor& dst, const void* src, std::size_t bytes) override
+    {
+        NNHIP_TRY(nnhip_memcpy_h2d(ctx_->h, TensorAccess::ptr(dst), src, bytes), "upload");
+        return {};
+    }
+
+    Result<void> download_impl(const Tensor& src, void* dst, std::size_t bytes) override
+    {
+        NNHIP_TRY(nnhip_memcpy_d2h(ctx_->h, dst, TensorAccess::ptr(src), bytes), "download");
+        return {};
+    }
+
+    Result<void> trit_pack_impl(const Tensor& W, const Tensor& tau, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_trit_pack(ctx_->h, fp(W), fp(tau), W.rows(), W.cols(), upw(out)), "trit_pack");
+        return {};
+    }
+
+    Result<void> row_absmean_impl(const Tensor& W, const Tensor& tau) override
+    {
+        NNHIP_TRY(nnhip_row_absmean(ctx_->h, fp(W), W.rows(), W.cols(), fpw(tau)), "row_absmean");
+        return {};
+    }
+
+    Result<void> abs_impl(const Tensor& x, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_abs(ctx_->h, fp(x), x.size(), fpw(out)), "abs");
+        return {};
+    }
+
+    Result<void> col_reduce_max_impl(const Tensor& x, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_col_reduce_max(ctx_->h, fp(x), x.rows(), x.cols(), fpw(out)), "col_reduce_max");
+        return {};
+    }
+
+    Result<void> scale_impl(const Tensor& x, Scalar s) override
+    {
+        NNHIP_TRY(nnhip_scale_inplace(ctx_->h, fpw(x), x.size(), s), "scale_inplace");
+        return {};
+    }
+
+    Result<void> quantize_i8_impl(const Tensor& x, const Tensor& scale, bool col_scale, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_quantize_i8(ctx_->h, fp(x), fp(scale), x.rows(), x.cols(), col_scale ? 1 : 0, upw(out)),
+                  "quantize_i8");
+        return {};
+    }
+
+    Result<void> unpack_i8_impl(const Tensor& packed, std::size_t cols, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_unpack_i8(ctx_->h, up(packed), packed.rows(), cols, fpw(out)), "unpack_i8");
+        return {};
+    }
+
+    // T16K256 copy of a weight container, cached on its storage for the current write epoch.
+    Result<const void*> repacked(const Tensor& wq, std::size_t K)
+    {
+        detail::Storage* st = TensorAccess::storage(wq);
+        if (st->derived && st->derived_epoch == st->write_epoch) return static_cast<const void*>(st->derived.get());
+        EX_TRY(mem, device_alloc(nnhip_repacked_bytes(wq.rows(), K)));
+        NNHIP_TRY(nnhip_repack_ternary(ctx_->h, up(wq), wq.rows(), K, mem->get()), "repack");
+        st->derived = *mem;
+        st->derived_epoch = st->write_epoch;
+        return static_cast<const void*>(st->derived.get());
+    }
+
+    // Token-major int8 activations + row sums, reused across calls (all work of one engine
+    // is ordered on its stream); grown on demand after a sync.
+    struct ActScratch
+    {
+        int8_t* xi;
+        int32_t* rowsum;
+    };
+
+    Result<ActScratch> act_scratch(std::size_t K, std::size_t M)
+    {
+        const std::size_t xi_bytes = nnhip_act_i8_bytes(K, M), rs_bytes = M * sizeof(int32_t);
+        if (xi_bytes > xi_cap_ || rs_bytes > rs_cap_)
+        {
+            NNHIP_TRY(nnhip_sync(ctx_->h), "scratch sync");
+            xi_buf_.reset();
+            rs_buf_.reset();
+            EX_TRY(xi, device_alloc(xi_bytes > xi_cap_ ? xi_bytes : xi_cap_));
+            EX_TRY(rs, device_alloc(rs_bytes > rs_cap_ ? rs_bytes : rs_cap_));
+            xi_cap_ = xi_bytes > xi_cap_ ? xi_bytes : xi_cap_;
+            rs_cap_ = rs_bytes > rs_cap_ ? rs_bytes : rs_cap_;
+            xi_buf_ = *xi;
+            rs_buf_ = *rs;
+        }
+        return ActScratch{static_cast<int8_t*>(xi_buf_.get()), static_cast<int32_t*>(rs_buf_.get())};
+    }
+
+    Result<void> matmul_q_i8_impl(const Tensor& wq, const Tensor& tau, const Tensor& xq, const Tensor& s,
+                                  const Tensor& y) override
+    {
+        const std::size_t N = wq.rows(), K = xq.rows(), M = s.cols();
+        if (N == 0 || M == 0) return {};
+        EX_TRY(rp, repacked(wq, K));
+        EX_TRY(a, act_scratch(K, M));
+        int8_t* xi = a->xi;
+        int32_t* rs = a->rowsum;
+        NNHIP_TRY(nnhip_act_i8_from_container(ctx_->h, up(xq), K, M, xi, rs), "matmul_q_i8 (activations)");
+        NNHIP_TRY(nnhip_ternary_matmul(ctx_->h, *rp, fp(tau), xi, fp(s), rs, nullptr, N, K, M, fpw(y)),
+                  "matmul_q_i8");
+        return {};
+    }
+
+    Result<void> add_row_broadcast_impl(const Tensor& y, const Tensor& b, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_memcpy_d2d(ctx_->h, TensorAccess::ptr(out), TensorAccess::ptr(y), y.size() * sizeof(float)),
+                  "add_row_broadcast (copy)");
+        NNHIP_TRY(nnhip_add_row_broadcast(ctx_->h, fpw(out), fp(b), y.rows(), y.cols()), "add_row_broadcast");
+        return {};
+    }
+
+    Result<void> rmsnorm_impl(const Tensor& x, const Tensor& gamma, Scalar eps, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_rmsnorm(ctx_->h, fp(x), fp(gamma), eps, x.rows(), x.cols(), fpw(out)), "rmsnorm");
+        return {};
+    }
+
+    Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor& b,
+                                     Tensor* xq_out, Tensor* s_out) override
+    {
+        const std::size_t K = x.rows(), M = x.cols(), N = wq.rows();
+        EX_TRY(s, alloc_impl(1, M, Precision::F32));
+        EX_TRY(y, alloc_impl(N, M, Precision::F32));
+        Tensor xq;
+        if (xq_out)
+        {
+            EX_TRY(t, alloc_impl(K, i8_pack::words_per_row(M), Precision::F32));
+            xq = *t;
+        }
+        if (M == 0 || N == 0) return *y;
+        EX_TRY(rp, repacked(wq, K));
+        EX_TRY(a, act_scratch(K, M));
+        int8_t* xi = a->xi;
+        int32_t* rs = a->rowsum;
+        NNHIP_TRY(nnhip_act_quant_i8(ctx_->h, fp(x), K, M, xi, fpw(*s), rs, xq_out ? upw(xq) : nullptr),
+                  "bitlinear_i8_forward (activation quantization)");
+        NNHIP_TRY(nnhip_ternary_matmul(ctx_->h, *rp, fp(tau), xi, fp(*s), rs, fp(b), N, K, M, fpw(*y)),
+                  "bitlinear_i8_forward (ternary product)");
+        if (xq_out) *xq_out = xq;
+        if (s_out) *s_out = *s;
+        return *y;
+    }
+
+    EngineInfo describe_impl() const override
+    {
+        EngineInfo i;
+        i.engine = "hip";
+        i.device = "MI355X (gfx950) #" + std::to_string(device_);
+        i.ternary_gemm = true;
+        i.int8_dot = true;
+        i.int8_dot_accelerated = true;
+        return i;
+    }
+
+    void sync_impl() override { (void)nnhip_sync(ctx_->h); }
+
+private:
+    std::shared_ptr<Ctx> ctx_;
+    int device_;
+    std::shared_ptr<void> xi_buf_, rs_buf_;
+    std::size_t xi_cap_ = 0, rs_cap_ = 0;
+};
+
+int parse_device(const char* device)
+{
+    if (!device || !*device) return 0;
+    const char* p = device;
+    if (std::strncmp(p, "hip:", 4) == 0) p += 4;
+    char* end = nullptr;
+    const long v = std::strtol(p, &end, 10);
+    if (end == p || *end != '\0' || v < 0) return -1;
+    return static_cast<int>(v);
+}
+
+}  // namespace
+
+std::unique_ptr<ComputeEngine> create_hip_engine(const char* device)
+{
+    const int dev = parse_device(device);
+    if (dev < 0)
+    {
+        g_factory_error = std::string("create_hip_engine: bad device string '") + device + "'";
+        return nullptr;
+    }
+    auto ctx = std::make_shared<Ctx>();
+    if (nnhip_ctx_create(dev, &ctx->h) != NNHIP_OK)
+    {
+        g_factory_error = std::string("create_hip_engine: ") + nnhip_last_error();
+        ctx->h = nullptr;
+        return nullptr;
+    }
+    return std::make_unique<HipEngine>(std::move(ctx), dev);
+}
+
+const char* last_error() noexcept { return g_factory_error.c_str(); }
+
+}  // namespace nn

@@ -1,0 +1,193 @@
+#pragma once
+// compute_engine.hpp — nn::Tensor and the nn::ComputeEngine interface, the subset of the
+// reference engine API that the BitLinear W1.58A8 path calls.
+//
+// Reference shape (compute_engine.hpp lives in the un-vendored engine submodule; the
+// signatures below are reconstructed from its call sites, e.g.
+// include/neuralnet.cpp/compute_layer_bitlinear.hpp:305, :443-456, :650,
+// src/int8_act_test.cpp:106-204, src/ternary_gemm_test.cpp:224-320):
+//   * public non-virtual entries (NVI) check the device domain, shapes and precision, then
+//     call protected *_impl (docs/development/04-compute-engine-development.md:110-114);
+//   * every result is a Result<T>; errors never throw (-fno-exceptions convention);
+//   * Tensor is a value type with shared storage: a copy aliases the same device buffer;
+//   * packed containers (ternary words, int8 words) are Precision::F32 tensors holding raw
+//     32-bit words, transferred bitwise (docs/internal/21-quantized-weights.md:649-652);
+//   * every write entry advances the destination storage's write epoch, which BitLinear
+//     uses to know when its quantized weights are stale (AGENTS.md:160-164).
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <string>
+
+#include "matrix.hpp"
+#include "precision.hpp"
+#include "result.hpp"
+
+namespace nn
+{
+
+inline constexpr std::uint64_t kInitSeed = 0x5EEDB17Aull;
+
+struct InitSpec
+{
+    enum class Kind : std::uint8_t { Zero, Constant, Uniform };
+    Kind kind = Kind::Zero;
+    float a = 0.0f, b = 0.0f;
+    std::uint64_t seed = 0;
+    [[nodiscard]] static InitSpec zero() noexcept { return {}; }
+    [[nodiscard]] static InitSpec constant(float v) noexcept { return {Kind::Constant, v, 0.0f, 0}; }
+    [[nodiscard]] static InitSpec uniform(double lo, double hi, std::uint64_t seed) noexcept
+    {
+        return {Kind::Uniform, static_cast<float>(lo), static_cast<float>(hi), seed};
+    }
+};
+
+struct EngineInfo
+{
+    std::string engine;
+    std::string device;
+    bool ternary_gemm = false;          // trit_pack / matmul_q_i8 available
+    bool int8_dot = false;              // int8 dot products available
+    bool int8_dot_accelerated = false;  // ... on matrix hardware
+    [[nodiscard]] std::string text() const
+    {
+        return engine + " on " + device + " | ternary_gemm=" + (ternary_gemm ? "yes" : "no") +
+               " int8_dot=" + (int8_dot ? "yes" : "no") +
+               " int8_dot_accelerated=" + (int8_dot_accelerated ? "yes" : "no");
+    }
+};
+
+class ComputeEngine;
+
+namespace detail
+{
+// Device storage shared by tensor copies. `mem` frees itself through the owning engine.
+struct Storage
+{
+    std::shared_ptr<void> mem;
+    std::size_t bytes = 0;
+    const ComputeEngine* owner = nullptr;
+    std::uint64_t write_epoch = 0;
+    // Engine-private data derived from the contents (e.g. repacked weights), valid while
+    // write_epoch == derived_epoch.
+    std::shared_ptr<void> derived;
+    std::uint64_t derived_epoch = ~std::uint64_t{0};
+};
+}  // namespace detail
+
+class Tensor
+{
+public:
+    Tensor() = default;
+    [[nodiscard]] bool valid() const noexcept { return static_cast<bool>(st_); }
+    [[nodiscard]] std::size_t rows() const noexcept { return rows_; }
+    [[nodiscard]] std::size_t cols() const noexcept { return cols_; }
+    [[nodiscard]] std::size_t size() const noexcept { return rows_ * cols_; }
+    [[nodiscard]] Precision precision() const noexcept { return p_; }
+    [[nodiscard]] std::uint64_t write_epoch() const noexcept { return st_ ? st_->write_epoch : 0; }
+    [[nodiscard]] bool same_storage(const Tensor& o) const noexcept { return st_ == o.st_; }
+
+private:
+    friend class TensorAccess;
+    std::shared_ptr<detail::Storage> st_;
+    std::size_t rows_ = 0, cols_ = 0;
+    Precision p_ = Precision::F32;
+};
+
+// Reference to a tensor member (layers hand these to optimizers / serializers).
+using TensorRef = std::reference_wrapper<Tensor>;
+
+// Engine-side access to tensor internals. Layers and user code never need it.
+class TensorAccess
+{
+public:
+    [[nodiscard]] static Tensor make(std::shared_ptr<detail::Storage> st, std::size_t rows, std::size_t cols,
+                                     Precision p)
+    {
+        Tensor t;
+        t.st_ = std::move(st);
+        t.rows_ = rows;
+        t.cols_ = cols;
+        t.p_ = p;
+        return t;
+    }
+    [[nodiscard]] static detail::Storage* storage(const Tensor& t) noexcept { return t.st_.get(); }
+    [[nodiscard]] static void* ptr(const Tensor& t) noexcept { return t.st_ ? t.st_->mem.get() : nullptr; }
+    static void mark_written(const Tensor& t) noexcept
+    {
+        if (t.st_) ++t.st_->write_epoch;
+    }
+};
+
+class ComputeEngine
+{
+public:
+    virtual ~ComputeEngine() = default;
+    ComputeEngine() = default;
+    ComputeEngine(const ComputeEngine&) = delete;
+    ComputeEngine& operator=(const ComputeEngine&) = delete;
+
+    // ---- tensors and transfers
+    [[nodiscard]] Tensor create_tensor(std::size_t rows, std::size_t cols, Precision p = Precision::F32,
+                                       InitSpec init = InitSpec::zero());
+    [[nodiscard]] Result<Tensor> from_matrix(const Matrix& m, Precision p = Precision::F32);
+    [[nodiscard]] Result<Matrix> to_matrix(const Tensor& t, Precision p = Precision::F32);
+    [[nodiscard]] Result<void> copy_from(Tensor& dst, const Matrix& src);
+
+    // ---- the BitLinear W1.58A8 primitives (reference names and semantics)
+    [[nodiscard]] Result<Tensor> trit_pack(const Tensor& W, const Tensor& tau);
+    [[nodiscard]] Result<void> trit_pack_into(const Tensor& W, const Tensor& tau, Tensor& out);
+    // tau = per-row absmean of W (the reduction BitLinear runs through its DSL)
+    [[nodiscard]] Result<void> row_absmean_into(const Tensor& W, Tensor& tau);
+    [[nodiscard]] Result<Tensor> abs(const Tensor& x);
+    [[nodiscard]] Result<Tensor> col_reduce_max(const Tensor& x, Precision p = Precision::F32);
+    [[nodiscard]] Result<void> scale_inplace(Tensor& x, Scalar s);
+    [[nodiscard]] Result<Tensor> quantize_i8(const Tensor& x, const Tensor& scale, bool col_scale);
+    [[nodiscard]] Result<Tensor> unpack_i8(const Tensor& packed, std::size_t cols);
+    [[nodiscard]] Result<Tensor> matmul_q_i8(const Tensor& wq, const Tensor& tau, const Tensor& xq, const Tensor& s,
+                                             Precision p = Precision::F32);
+    // y + row_broadcast(b)
+    [[nodiscard]] Result<Tensor> add_row_broadcast(const Tensor& y, const Tensor& b);
+    // RMSNorm forward: (x * rsqrt(mean_f x^2 + eps)) * gamma, per column (token)
+    [[nodiscard]] Result<Tensor> rmsnorm(const Tensor& x, const Tensor& gamma, Scalar eps);
+
+    // Fused BitLinear int8 forward, the sequence of compute_layer_bitlinear.hpp:443-456:
+    // s = col_reduce_max(|x|) * fl(1/127); xq = quantize_i8(x, s); y = matmul_q_i8(wq, tau, xq, s) + b.
+    // xq_out / s_out (nullable) receive the activation cache of the reference layer.
+    // The default implementation composes the primitives; an engine may fuse them.
+    [[nodiscard]] Result<Tensor> bitlinear_i8_forward(const Tensor& x, const Tensor& wq, const Tensor& tau,
+                                                      const Tensor& b, Precision p, Tensor* xq_out, Tensor* s_out);
+
+    [[nodiscard]] EngineInfo describe() const { return describe_impl(); }
+    void begin_batch() {}
+    void end_batch() { sync_impl(); }
+    void flush_batch() { sync_impl(); }
+
+protected:
+    [[nodiscard]] virtual Result<Tensor> alloc_impl(std::size_t rows, std::size_t cols, Precision p) = 0;
+    [[nodiscard]] virtual Result<void> upload_impl(const Tensor& dst, const void* src, std::size_t bytes) = 0;
+    [[nodiscard]] virtual Result<void> download_impl(const Tensor& src, void* dst, std::size_t bytes) = 0;
+    [[nodiscard]] virtual Result<void> trit_pack_impl(const Tensor& W, const Tensor& tau, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> row_absmean_impl(const Tensor& W, const Tensor& tau) = 0;
+    [[nodiscard]] virtual Result<void> abs_impl(const Tensor& x, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> col_reduce_max_impl(const Tensor& x, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> scale_impl(const Tensor& x, Scalar s) = 0;
+    [[nodiscard]] virtual Result<void> quantize_i8_impl(const Tensor& x, const Tensor& scale, bool col_scale,
+                                                        const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> unpack_i8_impl(const Tensor& packed, std::size_t cols, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> matmul_q_i8_impl(const Tensor& wq, const Tensor& tau, const Tensor& xq,
+                                                        const Tensor& s, const Tensor& y) = 0;
+    [[nodiscard]] virtual Result<void> add_row_broadcast_impl(const Tensor& y, const Tensor& b, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> rmsnorm_impl(const Tensor& x, const Tensor& gamma, Scalar eps,
+                                                    const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau,
+                                                           const Tensor& b, Tensor* xq_out, Tensor* s_out);
+    [[nodiscard]] virtual EngineInfo describe_impl() const = 0;
+    virtual void sync_impl() = 0;
+
+    // helpers for implementations
+    [[nodiscard]] Result<void> check_owned(const Tensor& t, const char* what) const;
+};
+
+}  // namespace nn

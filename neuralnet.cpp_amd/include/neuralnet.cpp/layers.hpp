@@ -1,0 +1,242 @@
+#pragma once
+// layers.hpp — nn::Layer, nn::BitLinear and nn::RMSNorm: the layer side of the W1.58A8 path.
+//
+// Mirrors the reference classes' public surface and semantics for the inference path:
+//   Layer      include/neuralnet.cpp/compute_layer_base.hpp:261-363 (init -> init_impl NVI,
+//              precision profile fixed at init, forward)
+//   BitLinear  include/neuralnet.cpp/compute_layer_bitlinear.hpp:46-675
+//   RMSNorm    include/neuralnet.cpp/compute_layer_mlp.hpp:627-707
+// BitLinear keeps the reference's weight-side state machine: f32 latent weights, per-row
+// absmean tau and the packed ternary container recomputed only when the latent storage's
+// write epoch changed (:100-111, :607-674), and the packed-only deploy state loaded with
+// load_packed_weights (:359-380). forward() runs the int8 branch (set_activation_quant(true),
+// :441-457) through ComputeEngine::bitlinear_i8_forward. Training (backward, STE gradients)
+// and the f32/f16-activation matmul_q branch are outside this engine's scope and fail fast
+// with a Result error, never silently.
+
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "compute_engine.hpp"
+#include "ternary_pack.hpp"
+
+namespace nn
+{
+
+class Layer
+{
+public:
+    virtual ~Layer() = default;
+    [[nodiscard]] virtual const char* layer_name() const noexcept = 0;
+    [[nodiscard]] virtual PrecisionSupport precision_support() const { return PrecisionSupport::rounding_all_slots(); }
+
+    // The profile is fixed before init (setting it afterwards aborts, compute_layer_base.hpp:193-259).
+    void set_precision_profile(const PrecisionProfile& p)
+    {
+        EX_UNWRAP(engine_ == nullptr, std::string(layer_name()) + ": set_precision_profile after init");
+        p_ = p;
+    }
+    [[nodiscard]] const PrecisionProfile& precision_profile() const noexcept { return p_; }
+
+    [[nodiscard]] Result<void> init(ComputeEngine& engine)
+    {
+        const PrecisionSupport sup = precision_support();
+        if (!sup.param.has(p_.param))
+            return Error{std::string(layer_name()) + ": param precision " + precision_name(p_.param) +
+                         " not supported (supported: " + sup.param.to_string() + ")"};
+        engine_ = &engine;
+        return init_impl(engine);
+    }
+
+    [[nodiscard]] virtual Result<Tensor> forward(const Tensor& input) = 0;
+    [[nodiscard]] virtual Result<Tensor> backward(const Tensor&)
+    {
+        return Error{std::string(layer_name()) + ": backward is not provided by this inference engine"};
+    }
+    [[nodiscard]] virtual std::vector<TensorRef> parameters() { return {}; }
+    virtual void clear_cache() {}
+
+protected:
+    [[nodiscard]] virtual Result<void> init_impl(ComputeEngine& engine) = 0;
+    [[nodiscard]] ComputeEngine& engine_ref() const noexcept { return *engine_; }
+    PrecisionProfile p_{};
+
+private:
+    ComputeEngine* engine_ = nullptr;
+};
+
+class BitLinear final : public Layer
+{
+public:
+    BitLinear(std::size_t in_features, std::size_t out_features, bool inference_only = false)
+        : in_features_(in_features), out_features_(out_features), inference_only_(inference_only)
+    {
+    }
+
+    [[nodiscard]] const char* layer_name() const noexcept override { return "BitLinear"; }
+
+    [[nodiscard]] PrecisionSupport precision_support() const override
+    {
+        PrecisionSupport sup = PrecisionSupport::rounding_all_slots();
+        sup.param = PrecisionSet::of({Precision::T1_58});
+        return sup;
+    }
+
+    // int8 activation quantization (W1.58A8): s = per-token absmax/127 (:181-189)
+    void set_activation_quant(bool enabled) noexcept { act_quant_ = enabled; }
+    [[nodiscard]] bool activation_quant() const noexcept { return act_quant_; }
+
+    [[nodiscard]] std::vector<TensorRef> parameters() override
+    {
+        std::vector<TensorRef> r;
+        if (latent_w_.valid()) r.emplace_back(latent_w_);
+        r.emplace_back(b_);
+        return r;
+    }
+
+    [[nodiscard]] const Tensor& latent_weights() const noexcept { return latent_w_; }
+    [[nodiscard]] const Tensor& row_scales() const noexcept { return tau_; }
+    [[nodiscard]] const Tensor& bias() const noexcept { return b_; }
+    [[nodiscard]] bool uses_packed_weights() const noexcept { return true; }
+    [[nodiscard]] const Tensor& quantized_weights_packed() const noexcept { return wq_packed_; }
+    [[nodiscard]] std::uint64_t quantize_calls() const noexcept { return quantize_calls_; }
+    [[nodiscard]] bool packed_only() const noexcept { return packed_only_; }
+    [[nodiscard]] std::size_t in_features() const noexcept { return in_features_; }
+    [[nodiscard]] std::size_t out_features() const noexcept { return out_features_; }
+    // activation cache of the int8 branch: packed int8 input (K, ceil(M/4)) and scales (1, M)
+    [[nodiscard]] const Tensor& input_cache() const noexcept { return input_cache_; }
+    [[nodiscard]] const Tensor& activation_scales() const noexcept { return act_scale_; }
+
+    // Deploy state: packed words + tau replace the latent weights (read-only inference).
+    [[nodiscard]] Result<void> load_packed_weights(Tensor packed_words, Tensor tau)
+    {
+        if (!packed_words.valid() || !tau.valid()) return Error{"BitLinear: empty deploy tensors"};
+        if (packed_words.rows() != out_features_ || packed_words.cols() != trit_pack::words_per_row(in_features_))
+            return Error{"BitLinear: packed word shape mismatch (expected " + std::to_string(out_features_) + "x" +
+                         std::to_string(trit_pack::words_per_row(in_features_)) + ")"};
+        if (tau.rows() != out_features_ || tau.cols() != 1)
+            return Error{"BitLinear: tau shape mismatch (expected " + std::to_string(out_features_) + "x1)"};
+        wq_packed_ = std::move(packed_words);
+        tau_ = std::move(tau);
+        quant_valid_ = true;
+        packed_only_ = true;
+        latent_w_ = Tensor{};
+        return {};
+    }
+
+    [[nodiscard]] Result<void> ensure_quantized()
+    {
+        if (needs_quantize_()) return quantize_weights_();
+        return {};
+    }
+
+    void clear_cache() override
+    {
+        input_cache_ = Tensor{};
+        act_scale_ = Tensor{};
+    }
+
+    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
+    {
+        ComputeEngine& engine = engine_ref();
+        if (input.rows() != in_features_) return Error{"bitlinear forward: input shape mismatch"};
+        if (packed_only_ && !(wq_packed_.valid() && tau_.valid()))
+            return Error{"BitLinear(packed-only): deploy weights / tau missing"};
+        if (needs_quantize_()) EX_TRY_CHECK(quantize_weights_());
+        if (!act_quant_)
+            return Error{"BitLinear: the f32/f16-activation branch (matmul_q) is not provided by this "
+                         "engine; enable set_activation_quant(true) for the W1.58A8 path"};
+        Tensor xq, s;
+        EX_TRY(y, engine.bitlinear_i8_forward(input, wq_packed_, tau_, b_, Precision::F32, &xq, &s));
+        input_cache_ = xq;
+        act_scale_ = s;
+        return *y;
+    }
+
+protected:
+    [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
+    {
+        if (inference_only_) packed_only_ = true;
+        if (!packed_only_)
+        {
+            const double limit = std::sqrt(6.0 / static_cast<double>(in_features_ + out_features_));
+            latent_w_ = engine.create_tensor(out_features_, in_features_, Precision::F32,
+                                             InitSpec::uniform(-limit, limit, kInitSeed));
+            if (!latent_w_.valid()) return Error{"BitLinear: latent weight init failed"};
+            wq_packed_ = engine.create_tensor(out_features_, trit_pack::words_per_row(in_features_),
+                                              Precision::F32, InitSpec::zero());
+            tau_ = engine.create_tensor(out_features_, 1, Precision::F32, InitSpec::zero());
+            if (!wq_packed_.valid() || !tau_.valid()) return Error{"BitLinear: quantization buffer init failed"};
+        }
+        b_ = engine.create_tensor(out_features_, 1, Precision::F32, InitSpec::zero());
+        if (!b_.valid()) return Error{"BitLinear: bias init failed"};
+        return {};
+    }
+
+private:
+    [[nodiscard]] bool needs_quantize_() const noexcept
+    {
+        if (packed_only_) return !(wq_packed_.valid() && tau_.valid());
+        if (!quant_valid_) return true;
+        return quant_epoch_ != latent_w_.write_epoch();
+    }
+
+    // tau = per-row absmean(latent); wq = trit_pack(latent, tau)   (:627-674)
+    [[nodiscard]] Result<void> quantize_weights_()
+    {
+        if (packed_only_) return Error{"BitLinear(packed-only): no latent weights to quantize"};
+        ComputeEngine& engine = engine_ref();
+        EX_TRY_CHECK(engine.row_absmean_into(latent_w_, tau_));
+        EX_TRY_CHECK(engine.trit_pack_into(latent_w_, tau_, wq_packed_));
+        quant_epoch_ = latent_w_.write_epoch();
+        quant_valid_ = true;
+        ++quantize_calls_;
+        return {};
+    }
+
+    std::size_t in_features_, out_features_;
+    bool inference_only_ = false;
+    bool packed_only_ = false;
+    bool act_quant_ = false;
+    Tensor latent_w_, b_, wq_packed_, tau_;
+    Tensor input_cache_, act_scale_;
+    std::uint64_t quant_epoch_ = 0;
+    bool quant_valid_ = false;
+    std::uint64_t quantize_calls_ = 0;
+};
+
+class RMSNorm final : public Layer
+{
+public:
+    explicit RMSNorm(std::size_t normalized_shape, Scalar epsilon = 1e-5f)
+        : normalized_shape_(normalized_shape), epsilon_(epsilon)
+    {
+    }
+    [[nodiscard]] const char* layer_name() const noexcept override { return "RMSNorm"; }
+    [[nodiscard]] std::vector<TensorRef> parameters() override { return {gamma_}; }
+    [[nodiscard]] Tensor& gamma() noexcept { return gamma_; }
+
+    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
+    {
+        if (input.rows() != normalized_shape_) return Error{"rmsnorm forward: input shape mismatch"};
+        return engine_ref().rmsnorm(input, gamma_, epsilon_);
+    }
+
+protected:
+    [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
+    {
+        gamma_ = engine.create_tensor(normalized_shape_, 1, Precision::F32, InitSpec::constant(1.0f));
+        if (!gamma_.valid()) return Error{"RMSNorm: parameter init failed"};
+        return {};
+    }
+
+private:
+    std::size_t normalized_shape_;
+    Scalar epsilon_;
+    Tensor gamma_;
+};
+
+}  // namespace nn

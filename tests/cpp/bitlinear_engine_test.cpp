@@ -1,0 +1,492 @@
+// bitlinear_engine_test — the reference's W1.58A8 acceptance checks, run through the nn::
+// C++ API of libnn-hip.so on the HIP engine. Each section names the reference test it
+// ports; host references are computed inline (int32 / double), never by the engine.
+//   [1] ternary layout and codec           src/ternary_gemm_test.cpp [1] (:70-137)
+//   [2] engine trit_pack == host pack_row  src/ternary_gemm_test.cpp [2] (:224-251)
+//   [3] quantize_i8 values/NaN/s==0/layout src/int8_act_test.cpp [1] (:86-137)
+//   [4] unpack_i8 round trip               src/int8_act_test.cpp [2] (:140-168)
+//   [5] matmul_q_i8 bit-exact vs int32     src/int8_act_test.cpp [3] (:171-238)
+//   [6] BitLinear tau / trits / forward    src/t1_58_test.cpp [5] (:207-345), int8 branch
+//   [7] BitLinear int8 forward bound       src/int8_act_test.cpp [4] (:241-290), vs double
+//   [8] write-epoch quant cache            AGENTS.md:160-164 / compute_layer_bitlinear.hpp:100-111
+//   [9] deploy state + Model::add          compute_layer_bitlinear.hpp:359-380, model_container.hpp:91-125
+//  [10] engine factory never falls back    cli/cli_engine_factory.hpp:11-13, :60-66
+// Exit: 0 pass, 1 fail, 77 skip (no gfx950 device).
+#include <algorithm>
+#include <bit>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <limits>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "neuralnet.cpp/nn.hpp"
+
+namespace
+{
+
+int g_failures = 0;
+
+#define CHECK(cond, msg)                                              \
+    do                                                                \
+    {                                                                 \
+        if (cond) std::printf("  [ OK ] %s\n", msg);                  \
+        else                                                          \
+        {                                                             \
+            std::printf("  [FAIL] %s  (%s:%d)\n", msg, __FILE__, __LINE__); \
+            ++g_failures;                                             \
+        }                                                             \
+    } while (0)
+
+nn::Matrix random_matrix(std::size_t rows, std::size_t cols, unsigned seed)
+{
+    nn::Matrix m(rows, cols);
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> d(-1.0f, 1.0f);
+    for (auto& v : m.span()) v = d(rng);
+    return m;
+}
+
+nn::Tensor upload(nn::ComputeEngine& e, const nn::Matrix& m)
+{
+    auto r = e.from_matrix(m);
+    EX_UNWRAP(r.has_value(), "upload failed: " + r.error().message);
+    return *r;
+}
+
+nn::Matrix download(nn::ComputeEngine& e, const nn::Tensor& t)
+{
+    auto r = e.to_matrix(t);
+    EX_UNWRAP(r.has_value(), "download failed: " + r.error().message);
+    return *r;
+}
+
+bool bitwise_equal(const nn::Matrix& a, const nn::Matrix& b)
+{
+    if (a.rows() != b.rows() || a.cols() != b.cols()) return false;
+    for (std::size_t i = 0; i < a.size(); ++i)
+        if (std::bit_cast<std::uint32_t>(a.span()[i]) != std::bit_cast<std::uint32_t>(b.span()[i])) return false;
+    return true;
+}
+
+std::uint32_t word_of(const nn::Matrix& m, std::size_t r, std::size_t c)
+{
+    return std::bit_cast<std::uint32_t>(m.at(r, c));
+}
+
+// ---------------------------------------------------------------- [1]
+void test_layout()
+{
+    std::puts("[1] ternary layout: 2 bit / weight, code = trit + 2, LSB first, tail code 2");
+    using namespace nn::trit_pack;
+    CHECK(kBits == 2 && kPerByte == 4 && kPerWord == 16, "size constants");
+    CHECK(words_per_row(16) == 1 && words_per_row(17) == 2 && words_per_row(1) == 1, "words_per_row rounds up");
+    CHECK(bytes_per_row(512) == 128, "K=512 -> 128 B per row");
+    const float w[16] = {1.0f, -1.0f, 0.0f, 0.4f, -0.4f, 1.0f, -1.0f, 0.0f,
+                         0.9f, -0.9f, 0.1f, -0.1f, 0.6f, -0.6f, 0.0f, 0.0f};
+    const std::uint32_t expect[16] = {3, 1, 2, 2, 2, 3, 1, 2, 3, 1, 2, 2, 3, 1, 2, 2};
+    std::uint32_t word[1] = {0};
+    pack_row(w, 16, 1.0f, word);
+    bool ok = true;
+    for (std::uint32_t j = 0; j < 16; ++j)
+        if (((word[0] >> (2 * j)) & 3u) != expect[j]) ok = false;
+    CHECK(ok, "codes and bit order");
+    std::uint32_t w2[1] = {0};
+    pack_row(w, 5, 1.0f, w2);
+    bool tail = true;
+    for (std::size_t i = 0; i < 5; ++i)
+        if (at(w2, i) != value_of(expect[i])) tail = false;
+    for (std::size_t i = 5; i < 16; ++i)
+        if (at(w2, i) != 0.0f) tail = false;
+    CHECK(tail, "decode round trip, tail positions are trit 0 (code 2)");
+}
+
+// ---------------------------------------------------------------- [2]
+void test_trit_pack(nn::ComputeEngine& e)
+{
+    std::puts("[2] engine trit_pack == host pack_row (K not a multiple of 16)");
+    constexpr std::size_t ROWS = 7, K = 40;
+    nn::Matrix W(ROWS, K);
+    for (std::size_t r = 0; r < ROWS; ++r)
+        for (std::size_t c = 0; c < K; ++c) W.set_value(r, c, 0.13f * static_cast<float>((r * 7 + c * 3) % 11) - 0.6f);
+    nn::Matrix tau(ROWS, 1);
+    for (std::size_t r = 0; r < ROWS; ++r)
+    {
+        double s = 0.0;
+        for (std::size_t c = 0; c < K; ++c) s += std::fabs(static_cast<double>(W.at(r, c)));
+        tau.set_value(r, 0, static_cast<float>(s / K));
+    }
+    auto packed = e.trit_pack(upload(e, W), upload(e, tau));
+    CHECK(packed.has_value(), "trit_pack succeeds");
+    if (!packed) return;
+    CHECK(packed->rows() == ROWS && packed->cols() == nn::trit_pack::words_per_row(K), "container shape (rows, ceil(K/16))");
+    const nn::Matrix pm = download(e, *packed);
+    bool same = true;
+    std::vector<std::uint32_t> ref(nn::trit_pack::words_per_row(K));
+    for (std::size_t r = 0; r < ROWS; ++r)
+    {
+        nn::trit_pack::pack_row(W.span().data() + r * K, K, tau.at(r, 0), ref.data());
+        for (std::size_t i = 0; i < ref.size(); ++i)
+            if (word_of(pm, r, i) != ref[i]) same = false;
+    }
+    CHECK(same, "words bit-identical to pack_row");
+    // tau on the engine = per-row absmean to 1e-6 of the double reference
+    auto tau_e = e.create_tensor(ROWS, 1);
+    auto ok = e.row_absmean_into(upload(e, W), tau_e);
+    CHECK(ok.has_value(), "row_absmean_into succeeds");
+    const nn::Matrix tm = download(e, tau_e);
+    double worst = 0.0;
+    for (std::size_t r = 0; r < ROWS; ++r)
+        worst = std::max(worst, std::fabs(static_cast<double>(tm.at(r, 0)) - tau.at(r, 0)) / tau.at(r, 0));
+    CHECK(worst < 1e-6, "engine tau = absmean (1e-6 relative)");
+}
+
+// ---------------------------------------------------------------- [3]
+void test_quantize(nn::ComputeEngine& e)
+{
+    std::puts("[3] quantize_i8: round-half-away, clamp, s==0 -> 0, NaN -> 0, little-endian layout");
+    constexpr std::size_t M = 5, N = 7;
+    nn::Matrix xm = random_matrix(M, N, 11);
+    nn::Matrix sm(1, N);
+    for (std::size_t c = 0; c < N; ++c)
+    {
+        float mx = 0.0f;
+        for (std::size_t r = 0; r < M; ++r) mx = std::max(mx, std::fabs(xm.span()[r * N + c]));
+        sm.span()[c] = mx;
+    }
+    for (std::size_t r = 0; r < M; ++r) xm.span()[r * N + 0] = 0.0f;
+    xm.span()[1 * N + 1] = std::numeric_limits<float>::quiet_NaN();
+    auto q = e.quantize_i8(upload(e, xm), upload(e, sm), true);
+    CHECK(q.has_value(), "quantize_i8 succeeds");
+    if (!q) return;
+    const nn::Matrix qm = download(e, *q);
+    const std::size_t wpr = nn::i8_pack::words_per_row(N);
+    CHECK(qm.rows() == M && qm.cols() == wpr, "container shape (M, ceil(N/4))");
+    bool value_ok = true, layout_ok = true;
+    for (std::size_t r = 0; r < M; ++r)
+    {
+        std::vector<std::uint32_t> words(wpr);
+        for (std::size_t wi = 0; wi < wpr; ++wi) words[wi] = word_of(qm, r, wi);
+        for (std::size_t c = 0; c < N; ++c)
+        {
+            const std::int8_t want = nn::i8_pack::quantize(xm.span()[r * N + c], sm.span()[c]);
+            const std::int8_t got = nn::i8_pack::at(words.data(), c);
+            if (got != want) value_ok = false;
+            if ((words[c / 4] >> (8 * (c % 4)) & 0xFFu) != static_cast<std::uint8_t>(got)) layout_ok = false;
+        }
+        if ((words[wpr - 1] >> 24) != 0u) layout_ok = false;  // tail byte
+    }
+    CHECK(value_ok, "values equal the host quantize (incl. s==0 column and NaN)");
+    CHECK(layout_ok, "little-endian bytes, tail byte 0");
+}
+
+// ---------------------------------------------------------------- [4]
+void test_unpack(nn::ComputeEngine& e)
+{
+    std::puts("[4] unpack_i8: container -> f32 integers");
+    constexpr std::size_t M = 3, N = 6;
+    const nn::Matrix xm = random_matrix(M, N, 23);
+    nn::Matrix sm(1, N);
+    for (std::size_t c = 0; c < N; ++c) sm.span()[c] = std::max(0.3f, std::fabs(xm.span()[c]) + 0.1f);
+    auto q = e.quantize_i8(upload(e, xm), upload(e, sm), true);
+    CHECK(q.has_value(), "quantize_i8 succeeds");
+    if (!q) return;
+    auto u = e.unpack_i8(*q, N);
+    CHECK(u.has_value(), "unpack_i8 succeeds");
+    if (!u) return;
+    const nn::Matrix um = download(e, *u);
+    bool ok = um.rows() == M && um.cols() == N;
+    for (std::size_t r = 0; r < M && ok; ++r)
+        for (std::size_t c = 0; c < N; ++c)
+            if (um.at(r, c) != static_cast<float>(nn::i8_pack::quantize(xm.at(r, c), sm.at(0, c)))) ok = false;
+    CHECK(ok, "values are the quantized integers, exactly");
+}
+
+// ---------------------------------------------------------------- [5]
+bool test_matmul_q_i8_shape(nn::ComputeEngine& e, std::size_t OUT, std::size_t K, std::size_t N, unsigned seed,
+                            const char* label)
+{
+    std::printf("[5] matmul_q_i8 (%s): bit-identical to the host int32 loop\n", label);
+    const nn::Matrix wm = random_matrix(OUT, K, seed);
+    nn::Matrix tm(OUT, 1);
+    for (std::size_t r = 0; r < OUT; ++r)
+    {
+        double acc = 0.0;
+        for (std::size_t k = 0; k < K; ++k) acc += std::fabs(static_cast<double>(wm.span()[r * K + k]));
+        tm.span()[r] = static_cast<float>(acc / static_cast<double>(K));
+    }
+    const nn::Matrix xm = random_matrix(K, N, seed + 1);
+    nn::Matrix sm(1, N);
+    for (std::size_t c = 0; c < N; ++c)
+    {
+        float mx = 0.0f;
+        for (std::size_t k = 0; k < K; ++k) mx = std::max(mx, std::fabs(xm.span()[k * N + c]));
+        sm.span()[c] = mx;
+    }
+    const nn::Tensor wt = upload(e, wm), tt = upload(e, tm), xt = upload(e, xm), st = upload(e, sm);
+    auto pw = e.trit_pack(wt, tt);
+    auto px = e.quantize_i8(xt, st, true);
+    CHECK(pw.has_value() && px.has_value(), "trit_pack / quantize_i8 succeed");
+    if (!pw || !px) return false;
+    auto y = e.matmul_q_i8(*pw, tt, *px, st);
+    CHECK(y.has_value(), "matmul_q_i8 succeeds");
+    if (!y) return false;
+    const nn::Matrix ym = download(e, *y), qm = download(e, *px);
+    const std::size_t wpr_w = nn::trit_pack::words_per_row(K), wpr_q = nn::i8_pack::words_per_row(N);
+    std::vector<std::uint32_t> tw(wpr_w), qw(wpr_q);
+    nn::Matrix ref(OUT, N);
+    for (std::size_t m = 0; m < OUT; ++m)
+    {
+        nn::trit_pack::pack_row(wm.span().data() + m * K, K, tm.span()[m], tw.data());
+        for (std::size_t n = 0; n < N; ++n)
+        {
+            std::int32_t acc = 0;
+            for (std::size_t k = 0; k < K; ++k)
+            {
+                const std::uint32_t code = (tw[k / 16] >> (2 * (k % 16))) & 3u;
+                for (std::size_t wi = 0; wi < wpr_q; ++wi) qw[wi] = word_of(qm, k, wi);
+                acc += static_cast<std::int32_t>(nn::trit_pack::value_of(code)) *
+                       static_cast<std::int32_t>(nn::i8_pack::at(qw.data(), n));
+            }
+            ref.span()[m * N + n] = tm.span()[m] * sm.span()[n] * static_cast<float>(acc);
+        }
+    }
+    CHECK(bitwise_equal(ym, ref), "bitwise equal ((tau*s)*float(acc) epilogue order)");
+    return true;
+}
+
+// ---------------------------------------------------------------- [6]
+void test_bitlinear_rules(nn::ComputeEngine& e)
+{
+    std::puts("[6] BitLinear: tau = per-row absmean, trits = RoundClip(W/tau,-1,1), forward");
+    constexpr std::size_t IN = 4, OUT = 3, B = 2;
+    const float kRawW[OUT][IN] = {{1.0f, 0.3f, -0.3f, 0.3f}, {0.4f, -0.4f, 0.1f, -0.1f}, {0.7f, 0.6f, 0.5f, 0.1f}};
+    const float kX[IN][B] = {{1.f, -2.f}, {0.5f, 1.f}, {-1.f, 0.25f}, {2.f, -0.5f}};
+    nn::BitLinear bl(IN, OUT);
+    nn::PrecisionProfile prof;
+    prof.param = nn::Precision::T1_58;
+    bl.set_precision_profile(prof);
+    auto ir = bl.init(e);
+    CHECK(ir.has_value(), "BitLinear + param=T1_58 init");
+    if (!ir) return;
+    nn::Matrix W(OUT, IN), X(IN, B);
+    for (std::size_t o = 0; o < OUT; ++o)
+        for (std::size_t k = 0; k < IN; ++k) W.set_value(o, k, kRawW[o][k]);
+    for (std::size_t k = 0; k < IN; ++k)
+        for (std::size_t b = 0; b < B; ++b) X.set_value(k, b, kX[k][b]);
+    CHECK(e.copy_from(bl.parameters()[0].get(), W).has_value(), "write known latent weights");
+    bl.set_activation_quant(true);
+    auto y = bl.forward(upload(e, X));
+    CHECK(y.has_value(), "forward (int8 branch)");
+    if (!y) return;
+    double tau_ref[OUT], wq_ref[OUT][IN];
+    for (std::size_t o = 0; o < OUT; ++o)
+    {
+        double s = 0.0;
+        for (std::size_t k = 0; k < IN; ++k) s += std::fabs(static_cast<double>(kRawW[o][k]));
+        tau_ref[o] = s / IN;
+        for (std::size_t k = 0; k < IN; ++k)
+        {
+            const double w = kRawW[o][k];
+            wq_ref[o][k] = (w > 0.5 * tau_ref[o]) ? 1.0 : (w < -0.5 * tau_ref[o]) ? -1.0 : 0.0;
+        }
+    }
+    const nn::Matrix tau = download(e, bl.row_scales());
+    bool tau_ok = tau.rows() == OUT && tau.cols() == 1;
+    for (std::size_t o = 0; o < OUT && tau_ok; ++o)
+        if (std::fabs(static_cast<double>(tau.at(o, 0)) - tau_ref[o]) >= 1e-6) tau_ok = false;
+    CHECK(tau_ok, "tau = {0.475, 0.25, 0.475} (1e-6)");
+    const nn::Matrix packed = download(e, bl.quantized_weights_packed());
+    bool exact = true;
+    for (std::size_t o = 0; o < OUT; ++o)
+    {
+        const std::uint32_t wd = word_of(packed, o, 0);
+        for (std::size_t k = 0; k < IN; ++k)
+            if (static_cast<double>(nn::trit_pack::at(&wd, k)) != wq_ref[o][k]) exact = false;
+    }
+    CHECK(exact, "packed trits equal RoundClip(W/tau,-1,1); 0.3 survives absmean scaling");
+    // forward = (tau * s) * sum(trit * q) with s = absmax/127 (q = int8 activations)
+    const nn::Matrix Y = download(e, *y);
+    bool fwd = true;
+    for (std::size_t b = 0; b < B; ++b)
+    {
+        float mx = 0.0f;
+        for (std::size_t k = 0; k < IN; ++k) mx = std::max(mx, std::fabs(kX[k][b]));
+        const float s = mx * (1.0f / 127.0f);
+        for (std::size_t o = 0; o < OUT; ++o)
+        {
+            std::int32_t acc = 0;
+            for (std::size_t k = 0; k < IN; ++k)
+                acc += static_cast<std::int32_t>(wq_ref[o][k]) * nn::i8_pack::quantize(kX[k][b], s);
+            const float ref = (tau.at(o, 0) * s) * static_cast<float>(acc) + 0.0f;
+            if (std::bit_cast<std::uint32_t>(Y.at(o, b)) != std::bit_cast<std::uint32_t>(ref)) fwd = false;
+        }
+    }
+    CHECK(fwd, "forward bit-identical to the host W1.58A8 reference (bias 0)");
+}
+
+// ---------------------------------------------------------------- [7]
+void test_bitlinear_bound(nn::ComputeEngine& e)
+{
+    std::puts("[7] BitLinear int8 forward vs float64 dequantized product: |dY| <= tau*s*K/2");
+    constexpr std::size_t IN = 64, OUT = 32, B = 8;
+    nn::BitLinear layer(IN, OUT);
+    nn::PrecisionProfile t1;
+    t1.param = nn::Precision::T1_58;
+    layer.set_precision_profile(t1);
+    EX_UNWRAP(layer.init(e).has_value(), "init");
+    layer.set_activation_quant(true);
+    const nn::Matrix xm = random_matrix(IN, B, 5);
+    auto y = layer.forward(upload(e, xm));
+    CHECK(y.has_value(), "forward");
+    if (!y) return;
+    const nn::Matrix ym = download(e, *y), lm = download(e, layer.latent_weights());
+    const nn::Matrix tm = download(e, layer.row_scales());
+    double worst = 0.0;
+    for (std::size_t n = 0; n < B; ++n)
+    {
+        float mx = 0.0f;
+        for (std::size_t r = 0; r < IN; ++r) mx = std::max(mx, std::fabs(xm.at(r, n)));
+        const double s = mx / 127.0;
+        for (std::size_t m = 0; m < OUT; ++m)
+        {
+            const double tau = tm.at(m, 0);
+            double ref = 0.0;
+            for (std::size_t k = 0; k < IN; ++k)
+            {
+                const double w = lm.at(m, k);
+                const double t = (w > 0.5 * tau) ? 1.0 : (w < -0.5 * tau) ? -1.0 : 0.0;
+                ref += tau * t * static_cast<double>(xm.at(k, n));
+            }
+            const double bound = tau * s * IN * 0.5;
+            if (bound > 0.0) worst = std::max(worst, std::fabs(ym.at(m, n) - ref) / bound);
+        }
+    }
+    std::printf("    diff / bound worst = %.4f\n", worst);
+    CHECK(worst <= 1.0, "within the 8-bit quantization bound");
+}
+
+// ---------------------------------------------------------------- [8]
+void test_quant_cache(nn::ComputeEngine& e)
+{
+    std::puts("[8] quantized weights are recomputed only when the latent weights change");
+    nn::BitLinear layer(48, 20);
+    nn::PrecisionProfile t1;
+    t1.param = nn::Precision::T1_58;
+    layer.set_precision_profile(t1);
+    EX_UNWRAP(layer.init(e).has_value(), "init");
+    layer.set_activation_quant(true);
+    const nn::Tensor x = upload(e, random_matrix(48, 3, 9));
+    auto y1 = layer.forward(x);
+    auto y2 = layer.forward(x);
+    CHECK(y1.has_value() && y2.has_value() && layer.quantize_calls() == 1, "two forwards, one quantization");
+    CHECK(bitwise_equal(download(e, *y1), download(e, *y2)), "repeat forward is bit-identical");
+    CHECK(e.copy_from(layer.parameters()[0].get(), random_matrix(20, 48, 10)).has_value(), "write new latent");
+    auto y3 = layer.forward(x);
+    CHECK(y3.has_value() && layer.quantize_calls() == 2, "write epoch advanced -> requantized");
+    CHECK(!bitwise_equal(download(e, *y1), download(e, *y3)), "new weights change the output");
+}
+
+// ---------------------------------------------------------------- [9]
+void test_deploy_and_model(nn::ComputeEngine& e)
+{
+    std::puts("[9] packed-only deploy state and Model::add<BitLinear>");
+    constexpr std::size_t IN = 80, HID = 40, OUT = 24, B = 5;
+    nn::PrecisionProfile t1;
+    t1.param = nn::Precision::T1_58;
+    nn::BitLinear trained(IN, HID);
+    trained.set_precision_profile(t1);
+    EX_UNWRAP(trained.init(e).has_value(), "init");
+    trained.set_activation_quant(true);
+    const nn::Tensor x = upload(e, random_matrix(IN, B, 77));
+    auto y_ref = trained.forward(x);
+    CHECK(y_ref.has_value(), "trained-layer forward");
+    // deploy: a layer built without latent weights, fed the packed words + tau
+    nn::BitLinear deployed(IN, HID, /*inference_only=*/true);
+    deployed.set_precision_profile(t1);
+    EX_UNWRAP(deployed.init(e).has_value(), "init deploy");
+    deployed.set_activation_quant(true);
+    auto words = e.from_matrix(download(e, trained.quantized_weights_packed()));
+    auto tau = e.from_matrix(download(e, trained.row_scales()));
+    CHECK(deployed.load_packed_weights(*words, *tau).has_value() && deployed.packed_only(), "load_packed_weights");
+    auto y_dep = deployed.forward(x);
+    CHECK(y_dep.has_value() && bitwise_equal(download(e, *y_ref), download(e, *y_dep)),
+          "deployed forward bit-identical to the trained layer");
+    CHECK(!deployed.backward(x).has_value(), "deploy state refuses backward (fail fast)");
+
+    nn::Model model(e);
+    model.set_default_precision_profile(t1);
+    CHECK(model.add<nn::BitLinear>(IN, HID).has_value(), "Model::add<BitLinear>");
+    nn::PrecisionProfile f32;
+    nn::Model norm_model(e);
+    norm_model.set_default_precision_profile(f32);
+    CHECK(!norm_model.add<nn::BitLinear>(IN, HID).has_value(), "param=f32 rejected by BitLinear (precision_support)");
+    CHECK(model.add<nn::BitLinear>(HID, OUT).has_value(), "second BitLinear");
+    for (std::size_t i = 0; i < model.num_layers(); ++i)
+        static_cast<nn::BitLinear&>(model.layer_at(i)).set_activation_quant(true);
+    auto my = model.forward(x);
+    CHECK(my.has_value() && my->rows() == OUT && my->cols() == B, "Model::forward through two BitLinears");
+    // RMSNorm -> BitLinear: the norm's output quantized by the layer
+    nn::RMSNorm norm(IN, 1e-6f);
+    EX_UNWRAP(norm.init(e).has_value(), "rmsnorm init");
+    auto nx = norm.forward(x);
+    CHECK(nx.has_value(), "RMSNorm forward");
+    if (nx)
+    {
+        const nn::Matrix xm = download(e, x), nm = download(e, *nx);
+        double worst = 0.0;
+        for (std::size_t b = 0; b < B; ++b)
+        {
+            double ss = 0.0;
+            for (std::size_t f = 0; f < IN; ++f) ss += static_cast<double>(xm.at(f, b)) * xm.at(f, b);
+            const double ri = 1.0 / std::sqrt(ss / IN + 1e-6);
+            for (std::size_t f = 0; f < IN; ++f)
+                worst = std::max(worst, std::fabs(nm.at(f, b) - xm.at(f, b) * ri) / std::max(1e-3, std::fabs(xm.at(f, b) * ri)));
+        }
+        CHECK(worst < 2e-6, "RMSNorm matches the float64 formula");
+    }
+}
+
+// ---------------------------------------------------------------- [10]
+void test_factory()
+{
+    std::puts("[10] engine factory: explicit backends, no silent fallback");
+    nn::cli::EngineConfig none;
+    CHECK(!nn::cli::create_engine(none).has_value(), "no backend requested -> error, not a CPU fallback");
+    CHECK(nn::create_hip_engine("hip:x") == nullptr && std::string(nn::last_error()).find("bad device") != std::string::npos,
+          "malformed device string -> error");
+}
+
+}  // namespace
+
+int main()
+{
+    test_layout();
+    test_factory();
+    nn::cli::EngineConfig ec;
+    ec.use_hip = true;
+    auto eng = nn::cli::create_engine(ec);
+    if (!eng.has_value())
+    {
+        std::printf("HIP engine unavailable, skipping device sections: %s\n", eng.error().message.c_str());
+        return g_failures == 0 ? 77 : 1;
+    }
+    nn::ComputeEngine& e = **eng;
+    std::printf("engine: %s\n", e.describe().text().c_str());
+    test_trit_pack(e);
+    test_quantize(e);
+    test_unpack(e);
+    test_matmul_q_i8_shape(e, 130, 17, 6, 31, "K/N not multiples, crosses row blocks");
+    test_matmul_q_i8_shape(e, 512, 256, 8, 41, "2B4T order");
+    test_matmul_q_i8_shape(e, 300, 2560, 1, 43, "decode M=1");
+    test_matmul_q_i8_shape(e, 257, 700, 40, 44, "GEMM path, tails");
+    test_bitlinear_rules(e);
+    test_bitlinear_bound(e);
+    test_quant_cache(e);
+    test_deploy_and_model(e);
+    if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
+    else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
+    return g_failures == 0 ? 0 : 1;
+}
