@@ -189,6 +189,24 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
         s.voff_x = t < p.M ? (uint32_t)t * Kp + 16u * g : kOOB;
     }
 
+    // Epilogue operands: unconditional buffer loads issued before the weight stream (rows
+    // past N and tokens past M read 0), so they have landed by the end of the item.
+    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
+    const uint32_t tok = t < p.M ? (uint32_t)t : 0x40000000u;
+    const int rs2 = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.rowsum, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
+    const float sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.s, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
+    float tv[kRTW][4], bv[kRTW][4];
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const uint32_t n = (uint32_t)((rt0 + r) * 16 + 4 * g + i);
+            tv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, n * 4u, 0, 0));
+            bv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, n * 4u, 0, 0));
+        }
+
     Acc acc[kRTW];
 #pragma unroll
     for (int r = 0; r < kRTW; ++r) acc[r].a0 = acc[r].a1 = acc[r].a2 = acc[r].a3 = v4i{0, 0, 0, 0};
@@ -201,9 +219,8 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     default: gemv_stream<LDS, kRTW, kDepth, 0>(p.KT, s, acc); break;
     }
 
-    if (t >= p.M) return;
-    const int rs2 = 2 * p.rowsum[t];
-    const float sv = p.s[t];
+    // masked lanes (token >= M, row >= N) store out of range: dropped by the buffer unit
+    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
 #pragma unroll
     for (int r = 0; r < kRTW; ++r)
     {
@@ -211,13 +228,11 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
         for (int i = 0; i < 4; ++i)
         {
             const int n = (rt0 + r) * 16 + 4 * g + i;
-            if (n < p.N)
-            {
-                const int a = acc[r].a0[i] + acc[r].a3[i] + (acc[r].a1[i] >> 2) + (acc[r].a2[i] >> 4) - rs2;
-                float y = (p.tau[n] * sv) * (float)a;
-                if (p.bias) y = y + p.bias[n];
-                p.y[(size_t)n * p.M + t] = y;
-            }
+            const int a = acc[r].a0[i] + acc[r].a3[i] + (acc[r].a1[i] >> 2) + (acc[r].a2[i] >> 4) - rs2;
+            float y = (tv[r][i] * sv) * (float)a;
+            if (p.bias) y = y + bv[r][i];
+            const uint32_t off = (n < p.N && t < p.M) ? ((uint32_t)n * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
         }
     }
 }

@@ -110,6 +110,11 @@ nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
     NNHIP_REQUIRE(K >= 1 && K <= kMaxK, fn, "K must be in [1, 262144]");
     NNHIP_REQUIRE(ceil_div(N, 16) < (1u << 20), fn, "N must be below 2^24");
     NNHIP_REQUIRE(mul_ok(round_up(K, kTileK), M) && mul_ok(N, M), fn, "size overflow");
+    // the kernels address rp, xi and Y through 32-bit buffer ranges
+    NNHIP_REQUIRE(round_up(N, kTileRows) * round_up(K, kTileK) / 4 < 0x7FFFFFFFull, fn,
+                  "repacked weights must be below 2 GiB");
+    NNHIP_REQUIRE(round_up(K, kTileK) * M < 0x7FFFFFFFull, fn, "activations must be below 2 GiB");
+    NNHIP_REQUIRE(N * M * 4 < 0x7FFFFFFFull, fn, "output must be below 2 GiB");
     return NNHIP_OK;
 }
 
