@@ -149,7 +149,8 @@ nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* 
 nnhip_status nnhip_add_row_broadcast(nnhip_ctx* ctx, float* Y, const float* b, size_t N, size_t M);
 
 /* out (F, M) = RMSNorm(X (F, M)) with gain gamma (F): rms_inv = 1/sqrt(sum_f x^2 * fl(1/F) + eps)
- * (sum in the fixed 64-part butterfly order), out = (x * rms_inv) * gamma[f].
+ * (sum in a fixed order: 512 strided parts f % 512, each ascending, then a xor butterfly over
+ * offsets 256..1), out = (x * rms_inv) * gamma[f].
  * Replaces RMSNorm::forward (include/neuralnet.cpp/compute_layer_mlp.hpp:686-707). */
 nnhip_status nnhip_rmsnorm(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t F,
                            size_t M, float* out);

@@ -2,10 +2,19 @@
 // quantization into the token-major layout the ternary GEMV/GEMM read, RMSNorm alone,
 // and conversions between that layout and the reference int8 container.
 //
-// Both fused kernels evaluate the per-token sum of squares in one fixed order, the same
-// as the oracle: 64 strided parts (feature f in part f % 64), each summed in ascending f,
-// then the xor butterfly over 32,16,8,4,2,1. So the normalized values, the scale and the
-// int8 codes are bit-identical to the unfused reference sequence.
+// Every kernel here evaluates the per-token sum of squares in one fixed order, the same as
+// the oracle: 512 strided parts (feature f in part f % 512), each summed in ascending f, then
+// the xor butterfly over 256,128,...,1. So the normalized values, the scale and the int8 codes
+// are bit-identical to the unfused reference sequence whichever kernel runs.
+//
+// Kernels by shape:
+//   k_token_wave   M <= 32: one wave per token, lane l owns parts l + 64q (q = 0..7).
+//   k_token_regs   M > 32, K up to 512 * 22: 4 tokens per block (the layout also supports 8),
+//                  512 threads. Each thread loads its rows (16 B = 4 tokens per row) once and
+//                  keeps them in registers through the three passes (sum of squares, absmax,
+//                  quantize), so X is read from HBM exactly once; parts are whole per thread.
+//                  Codes leave through a 4x4 byte transpose in lane quads as dword stores.
+//   k_token_lanes  fallback for larger K: 64 tokens per block, re-reads X per pass.
 #include "common.hpp"
 
 #include <cmath>
@@ -16,6 +25,7 @@ namespace
 {
 
 constexpr int kBlock = 256;
+constexpr int kParts = 512;  // sum-of-squares parts
 
 __device__ __forceinline__ int quantize_one(float x, float s)
 {
@@ -24,6 +34,44 @@ __device__ __forceinline__ int quantize_one(float x, float s)
     if (isnan(v)) return 0;
     v = fminf(fmaxf(v, -127.0f), 127.0f);
     return (int)roundf(v);
+}
+
+// Per-token reciprocal for quantize_fast: fl(1/s), 0 when s == 0 (every code is then 0, as
+// quantize_one gives), +inf when 1/s overflows (the caller then takes the exact path).
+__device__ __forceinline__ float quant_rcp(float s)
+{
+    return s == 0.0f ? 0.0f : __fdiv_rn(1.0f, s);
+}
+
+// quantize_one(x, s) without a division in the common case. With r = fl(1/s) and
+// y = fl(x * r), |y - x/s| <= |x/s| * 2^-23 (two roundings), so |y - fl(x/s)| < 2^-15 for
+// |x/s| <= 128. Unless y lies within 2^-14 of a half-integer, round-to-nearest-even of y then
+// equals round-half-away-from-zero of fl(x/s) (no tie and no integer boundary in between), and
+// clamping after rounding equals clamping before (127 is an integer, and values past 127.5
+// round to 127 or more either way). Near a half-integer, for NaN inputs and when 1/s
+// overflowed, the exact quantize_one decides; the result is the same code bit for bit.
+__device__ __forceinline__ int quantize_fast(float x, float s, float r)
+{
+    const float y = __fmul_rn(x, r);
+    const float t = __builtin_rintf(y);
+    if (!(fabsf(y - t) < 0.5f - 0x1p-14f) || isinf(r)) return quantize_one(x, s);
+    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+}
+
+// The fast-path code alone; `amb` is set when the exact path must decide (see quantize_fast).
+__device__ __forceinline__ int quantize_guess(float x, float r, bool& amb)
+{
+    const float y = __fmul_rn(x, r);
+    const float t = __builtin_rintf(y);
+    amb |= !(fabsf(y - t) < 0.5f - 0x1p-14f);
+    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+}
+
+__device__ __forceinline__ uint32_t pack4(int q0, int q1, int q2, int q3)
+{
+    // low bytes of q0..q3 -> bytes 0..3
+    return __builtin_amdgcn_perm(__builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u),
+                                 __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u), 0x05040100u);
 }
 
 // Correctly rounded fp32 square root. v_sqrt_f32 alone is accurate to 1 ulp; the two
@@ -43,6 +91,11 @@ __device__ __forceinline__ float sqrt_rn(float v)
     return s;
 }
 
+__device__ __forceinline__ float rms_inv_of(float sum_sq, float inv_f, float eps)
+{
+    return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(sum_sq, inv_f), eps)));
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
 #pragma unroll
@@ -59,6 +112,94 @@ __device__ __forceinline__ int wave_sum_i(int v)
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
+}
+
+// In-register butterfly levels: v[k] holds part p + stride*k (k < N); after the levels for
+// offsets stride*N/2 .. stride, v[0] holds part p of the tree at level `stride`.
+template <int N>
+__device__ __forceinline__ float tree_levels(float (&v)[N])
+{
+#pragma unroll
+    for (int d = N / 2; d >= 1; d >>= 1)
+#pragma unroll
+        for (int k = 0; k < d; ++k) v[k] = __fadd_rn(v[k], v[k + d]);
+    return v[0];
+}
+
+// Value of lane l ^ OFF as seen after the butterfly levels above OFF (descending offsets):
+// by then a lane's value depends only on its lane bits below 2*OFF, so any partner with those
+// bits equal to (l mod 2*OFF) ^ OFF carries the same value. OFF = 1, 2: quad_perm [1,0,3,2] /
+// [2,3,0,1]; OFF = 4, 8: row_ror (l - OFF mod 16 agrees with l ^ OFF below 2*OFF); larger OFF:
+// ds_bpermute.
+template <int OFF>
+__device__ __forceinline__ int lane_xor(int v)
+{
+    if constexpr (OFF == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (OFF == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (OFF == 4) return __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false);
+    else if constexpr (OFF == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);
+    else return __shfl_xor(v, OFF, kWave);
+}
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    return __builtin_bit_cast(float, lane_xor<OFF>(__builtin_bit_cast(int, v)));
+}
+
+// Butterfly over lane bits below 2*OFF (offsets OFF, OFF/2, ..., 1), four values at a time so
+// the lane exchanges of one level overlap. Sum: fl(own + partner), the fixed order of the
+// oracle's tree; max ignores NaN as `a > b ? a : b` does; integer sum is exact.
+template <int OFF>
+__device__ __forceinline__ void bfly_fsum(float (&v)[4])
+{
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = lane_xor<OFF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], o[i]);
+    if constexpr (OFF > 1) bfly_fsum<OFF / 2>(v);
+}
+template <int OFF>
+__device__ __forceinline__ void bfly_fmax(float (&v)[4])
+{
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = lane_xor<OFF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = o[i] > v[i] ? o[i] : v[i];
+    if constexpr (OFF > 1) bfly_fmax<OFF / 2>(v);
+}
+template <int OFF>
+__device__ __forceinline__ void bfly_isum(int (&v)[4])
+{
+    int o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = lane_xor<OFF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] += o[i];
+    if constexpr (OFF > 1) bfly_isum<OFF / 2>(v);
+}
+
+__device__ __forceinline__ int lane_j(int fl) { return fl & 3; }
+
+// Integer sum over lane bits LO..log2(2*OFF)-1 (offsets OFF down to LO).
+template <int OFF, int LO>
+__device__ __forceinline__ int bfly_isum1(int v)
+{
+    v += lane_xor<OFF>(v);
+    if constexpr (OFF > LO) return bfly_isum1<OFF / 2, LO>(v);
+    else return v;
+}
+
+// 4x4 byte transpose inside each quad of lanes: lane j (= lane & 3) holds bytes B_j[0..3] and
+// ends with B_0[j], B_1[j], B_2[j], B_3[j]. Two exchanges, 16-bit halves with lane j^2, then
+// bytes with lane j^1 (v_perm: bytes 0..3 are the second operand, 4..7 the first).
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t v, int j)
+{
+    const uint32_t p2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+    const uint32_t a = __builtin_amdgcn_perm(p2, v, (j & 2) ? 0x03020706u : 0x05040100u);
+    const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0xB1, 0xF, 0xF, false);
+    return __builtin_amdgcn_perm(p1, a, (j & 1) ? 0x03070105u : 0x06020400u);
 }
 
 // out = (x * ri) * gamma  (two roundings, as RMSNorm's normed * gamma)
@@ -86,15 +227,25 @@ __global__ __launch_bounds__(kBlock) void k_token_wave(const float* __restrict__
     float ri = 1.0f;
     if (norm)
     {
-        float part = 0.0f;
-        for (size_t f = (size_t)lane; f < K; f += kWave)
-        {
-            const float x = X[f * M + m];
-            part = __fadd_rn(part, __fmul_rn(x, x));
-        }
+        // parts lane + 64q; the butterfly levels 256, 128, 64 stay in the lane
+        float pq[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pq[q] = 0.0f;
+        for (size_t f0 = 0; f0 < K; f0 += kParts)
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+            {
+                const size_t f = f0 + 64 * q + (size_t)lane;
+                if (f < K)
+                {
+                    const float x = X[f * M + m];
+                    pq[q] = __fadd_rn(pq[q], __fmul_rn(x, x));
+                }
+            }
+        float part = tree_levels(pq);
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_xor(part, off, kWave));
-        ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(part, inv_f), eps)));
+        ri = rms_inv_of(part, inv_f, eps);
     }
 
     if (mode == 1)
@@ -133,8 +284,8 @@ __global__ __launch_bounds__(kBlock) void k_token_wave(const float* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------
-// Large M: 64 tokens per block (lane = token, coalesced rows of the (K, M) layout),
-// 8 waves; wave w owns features f = 64*b + 8*w + j (j = 0..7), i.e. parts p = 8w + j.
+// Large K fallback: 64 tokens per block (lane = token, coalesced rows of the (K, M) layout),
+// 8 waves; wave w owns features f = 64*b + 8*w + j (j = 0..7), i.e. parts 64(b%8) + 8w + j.
 constexpr int kTW = 8;  // waves per block
 
 __global__ __launch_bounds__(kTW * kWave) void k_token_lanes(
@@ -154,35 +305,42 @@ __global__ __launch_bounds__(kTW * kWave) void k_token_lanes(
     float ri = 1.0f;
     if (norm)
     {
-        float acc[8];
+        // parts 64q + 8w + j (q = b % 8); the butterfly levels 256, 128, 64 combine q in the lane
+        float acc[8][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[q][j] = 0.0f;
         if (active)
-            for (size_t b = 0; b < nb; ++b)
+            for (size_t b = 0; b < nb; b += 8)
             {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                {
-                    const size_t f = 64 * b + 8 * w + j;
-                    if (f < K)
+                for (int q = 0; q < 8; ++q)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
                     {
-                        const float x = X[f * M + m];
-                        acc[j] = __fadd_rn(acc[j], __fmul_rn(x, x));
+                        const size_t f = 64 * (b + q) + 8 * w + j;
+                        if (f < K)
+                        {
+                            const float x = X[f * M + m];
+                            acc[q][j] = __fadd_rn(acc[q][j], __fmul_rn(x, x));
+                        }
                     }
-                }
             }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) part[8 * w + j][lane] = acc[j];
+        for (int j = 0; j < 8; ++j)
+        {
+            float v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = acc[q][j];
+            part[8 * w + j][lane] = tree_levels(v);
+        }
         __syncthreads();
-        // butterfly tree on the lower halves: v[p] = v[p] + v[p + off] for p < off
+        // the levels 32..1 on the lower halves: v[p] = v[p] + v[p + off] for p < off
         float v[64];
 #pragma unroll
         for (int p = 0; p < 64; ++p) v[p] = part[p][lane];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-            for (int p = 0; p < off; ++p) v[p] = __fadd_rn(v[p], v[p + off]);
-        ri = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(v[0], inv_f), eps)));
+        ri = rms_inv_of(tree_levels(v), inv_f, eps);
     }
 
     if (mode == 1)
@@ -250,6 +408,265 @@ __global__ __launch_bounds__(kTW * kWave) void k_token_lanes(
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Large M: TPB tokens per block (4 or 8), 512 threads, X read from HBM exactly once.
+// A thread holds 4 tokens of one row per round (16 B, a float4 when M % 4 == 0); LPR = TPB/4
+// lanes share a row, so a wave covers RPW = 64/LPR rows and a round RR = 8*RPW rows. Thread
+// (wave w, lane RPW*h + fl) loads rows f = RR*r + RPW*w + fl (r < R), tokens 4h..4h+3, keeps
+// them in registers, and owns sum-of-squares part f % 512 of its four tokens (one part when
+// RR = 512, two alternating parts when RR = 256). The butterfly levels down to offset RPW go
+// through LDS, the rest are lane shuffles.
+constexpr int kRegWaves = 8;  // 512 threads
+
+// Everything a block needs to load and finish token groups (uniform across the block).
+struct TokArgs
+{
+    const float* X;
+    bool norm;
+    float eps, inv_f;
+    int K, M, Kp, mode;
+    int8_t* xi;
+    float* s;
+    int32_t* rowsum;
+    uint32_t* xq_ref;
+    float* fout;
+};
+
+template <int TPB>
+struct TokShared
+{
+    float red[kParts][TPB];  // sum-of-squares parts
+    float wred[kRegWaves][TPB];
+    int wsum[kRegWaves][TPB];
+    float tok_ri[TPB];
+};
+
+// Issue the loads of group g into x (vector path: one buffer resource over X, K*M*4 < 2^31
+// checked at launch, so rows past K and tokens past M read 0 without a branch).
+template <int R, bool kVec, int TPB>
+__device__ __forceinline__ void load_group(float (&x)[R][4], const TokArgs& a, int g, int ro, int h)
+{
+    constexpr int RR = kRegWaves * kWave / (TPB / 4);
+    const int mt = g * TPB + 4 * h;
+    if (kVec)
+    {
+        typedef float v4f __attribute__((ext_vector_type(4)));
+        const __amdgpu_buffer_rsrc_t rx =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.X), (short)0, a.K * a.M * 4, 0x00020000);
+        const uint32_t moff = mt < a.M ? (uint32_t)mt * 4u : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const v4f v = __builtin_bit_cast(
+                v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, moff + (uint32_t)(RR * r + ro) * (uint32_t)a.M * 4u, 0, 0));
+            x[r][0] = v[0];
+            x[r][1] = v[1];
+            x[r][2] = v[2];
+            x[r][3] = v[3];
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = RR * r + ro;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                x[r][i] = (f < a.K && mt + i < a.M) ? a.X[(size_t)f * a.M + mt + i] : 0.0f;
+        }
+    }
+}
+
+// The three passes over one group held in registers: sum of squares -> rms_inv (RMSNorm),
+// per-token absmax -> scale, quantize -> xi / s / rowsum (and the reference container).
+template <int R, bool kVec, int TPB>
+__device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)[R], const TokArgs& a,
+                                             TokShared<TPB>& sh, int g, int w, int fl, int h, int ro)
+{
+    constexpr int LPR = TPB / 4;          // lanes per row
+    constexpr int RPW = kWave / LPR;      // rows per wave per round
+    constexpr int RR = kRegWaves * RPW;   // rows per round
+    constexpr int NP = kParts / RR;       // parts per thread (1 or 2)
+    const int mt = g * TPB + 4 * h;       // first of this thread's four tokens
+
+    // ---- pass 1: sum of squares -> rms_inv, then normalize in place
+    if (a.norm)
+    {
+        float acc[NP][4];
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[q][i] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[r % NP][i] = __fadd_rn(acc[r % NP][i], __fmul_rn(x[r][i], x[r][i]));
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sh.red[ro + RR * q][4 * h + i] = acc[q][i];
+        __syncthreads();
+        if (w == 0)
+        {
+            float sum[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                float v[kParts / RPW];
+#pragma unroll
+                for (int k = 0; k < kParts / RPW; ++k) v[k] = sh.red[fl + RPW * k][4 * h + i];
+                sum[i] = tree_levels(v);
+            }
+            bfly_fsum<RPW / 2>(sum);
+            if (fl == 0)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sh.tok_ri[4 * h + i] = rms_inv_of(sum[i], a.inv_f, a.eps);
+        }
+        __syncthreads();
+        float ri[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ri[i] = sh.tok_ri[4 * h + i];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[r][i] = __fmul_rn(__fmul_rn(x[r][i], ri[i]), gm[r]);
+    }
+
+    if (a.mode == 1)
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = RR * r + ro;
+            if (f >= a.K) continue;
+            if (kVec)
+            {
+                if (mt < a.M)
+                    *reinterpret_cast<float4*>(a.fout + (size_t)f * a.M + mt) = make_float4(x[r][0], x[r][1], x[r][2], x[r][3]);
+            }
+            else
+            {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (mt + i < a.M) a.fout[(size_t)f * a.M + mt + i] = x[r][i];
+            }
+        }
+        return;
+    }
+
+    // ---- pass 2: per-token absmax -> scale (fmaxf ignores NaN, as `a > m ? a : m` from 0 does)
+    float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], fabsf(x[r][i]));
+    bfly_fmax<RPW / 2>(mx);
+    if (fl == 0)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sh.wred[w][4 * h + i] = mx[i];
+    __syncthreads();
+    float sc[4], rc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        float t = sh.wred[0][4 * h + i];
+#pragma unroll
+        for (int v = 1; v < kRegWaves; ++v) t = fmaxf(t, sh.wred[v][4 * h + i]);
+        sc[i] = __fmul_rn(t, 1.0f / 127.0f);
+        rc[i] = quant_rcp(sc[i]);
+    }
+
+    // ---- pass 3: quantize; codes on the fast path with one flag for the thread. Rows past K
+    // hold x = 0 (or NaN when rms_inv is infinite), which both paths turn into code 0.
+    uint32_t pk[R];
+    bool amb = isinf(rc[0]) || isinf(rc[1]) || isinf(rc[2]) || isinf(rc[3]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+    {
+        int qv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] = quantize_guess(x[r][i], rc[i], amb);
+        pk[r] = pack4(qv[0], qv[1], qv[2], qv[3]);
+    }
+    if (amb)
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            int qv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qv[i] = quantize_fast(x[r][i], sc[i], rc[i]);
+            pk[r] = pack4(qv[0], qv[1], qv[2], qv[3]);
+        }
+    }
+    // xi: after a quad transpose lane (quad q, position j) holds token 4h+j for the four rows
+    // 4q..4q+3 of its wave's slice, one dword store each; dot4 against 1s sums those codes.
+    const int wpr = (a.M + 3) / 4;
+    const int j = lane_j(fl);
+    int tsum = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+    {
+        const int f = RR * r + ro;
+        if (a.xq_ref && f < a.K && g * LPR + h < wpr) a.xq_ref[(size_t)f * wpr + g * LPR + h] = pk[r];
+        const uint32_t col = quad_transpose(pk[r], j);
+        tsum = __builtin_amdgcn_sdot4((int)col, 0x01010101, tsum, false);
+        const int f0 = RR * r + RPW * w + (fl & ~3);  // first of the four rows (Kp % 256 == 0)
+        if (f0 < a.Kp && mt + j < a.M) *reinterpret_cast<uint32_t*>(a.xi + (size_t)(mt + j) * a.Kp + f0) = col;
+    }
+    tsum = bfly_isum1<RPW / 2, 4>(tsum);  // over the quads of the wave's slice
+    if (fl < 4) sh.wsum[w][4 * h + j] = tsum;
+    __syncthreads();
+    if (w == 0 && fl == 0)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            int t = 0;
+#pragma unroll
+            for (int v = 0; v < kRegWaves; ++v) t += sh.wsum[v][4 * h + i];
+            if (mt + i < a.M)
+            {
+                a.s[mt + i] = sc[i];
+                a.rowsum[mt + i] = t;
+            }
+        }
+    }
+}
+
+// One block per token group; block b takes group slot(b), XCD-aware when the group count is a
+// multiple of 8, so the blocks of one XCD take consecutive groups and the groups sharing a
+// 128-byte row segment of X meet in one L2.
+template <int R, bool kVec, int TPB>
+__global__ __launch_bounds__(kRegWaves * kWave) void k_token_regs(TokArgs a, const float* __restrict__ gamma,
+                                                                  int n_groups)
+{
+    constexpr int RPW = kWave / (TPB / 4);
+    constexpr int RR = kRegWaves * RPW;
+    static_assert(TPB == 4 || TPB == 8, "tokens per block");
+    __shared__ TokShared<TPB> sh;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int fl = lane % RPW, h = lane / RPW;  // row within the wave's slice, token quad
+    const int ro = RPW * w + fl;
+    const int b = blockIdx.x;
+    const int g = n_groups % 8 == 0 ? (b & 7) * (n_groups >> 3) + (b >> 3) : b;
+
+    float x[R][4];
+    load_group<R, kVec, TPB>(x, a, g, ro, h);
+    float gm[R];
+    if (a.norm)
+    {
+        const __amdgpu_buffer_rsrc_t rg =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(gamma), (short)0, a.K * 4, 0x00020000);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            gm[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, (uint32_t)(RR * r + ro) * 4u, 0, 0));
+    }
+    finish_group<R, kVec, TPB>(x, gm, a, sh, g, w, fl, h, ro);
+}
+
 // Reference container (K, ceil(M/4)) -> token-major xi + rowsum. One block per token.
 __global__ __launch_bounds__(kBlock) void k_from_container(const uint32_t* __restrict__ xq, size_t K,
                                                            size_t M, size_t Kp,
@@ -303,6 +720,23 @@ __global__ __launch_bounds__(kBlock) void k_to_container(const int8_t* __restric
 
 constexpr size_t kSmallM = 32;
 
+template <int TPB, int R>
+void launch_regs_r(bool vec, hipStream_t st, int n_groups, const TokArgs& a, const float* gamma)
+{
+    auto kern = vec ? k_token_regs<R, true, TPB> : k_token_regs<R, false, TPB>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)n_groups), dim3(kRegWaves * kWave), 0, st, a, gamma, n_groups);
+}
+
+// Launch the instantiation with the smallest R >= rounds from the ascending list Rs; false if
+// none is large enough.
+template <int TPB, int... Rs>
+bool launch_regs_pick(int rounds, bool vec, hipStream_t st, int n_groups, const TokArgs& a, const float* gamma)
+{
+    bool done = false;
+    ((done = done || (Rs >= rounds && (launch_regs_r<TPB, Rs>(vec, st, n_groups, a, gamma), true))), ...);
+    return done;
+}
+
 }  // namespace
 
 static hipError_t launch_token_kernel(hipStream_t st, const float* X, const float* gamma, bool norm,
@@ -317,13 +751,27 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
         const unsigned grid = (unsigned)ceil_div(M, kBlock / kWave);
         hipLaunchKernelGGL(k_token_wave, dim3(grid), dim3(kBlock), 0, st, X, gamma, norm, eps, inv_f,
                            K, M, Kp, mode, xi, s, rowsum, xq_ref, fout);
+        return hipGetLastError();
     }
-    else
+    // the register kernel addresses X through one 31-bit buffer range, including the padding
+    // rows of its last round (at most 4096 rows past K)
+    if ((K + 4096) * M * 4 < 0x7FFFFFFFull)
     {
-        const unsigned grid = (unsigned)ceil_div(M, kWave);
-        hipLaunchKernelGGL(k_token_lanes, dim3(grid), dim3(kTW * kWave), 0, st, X, gamma, norm, eps,
-                           inv_f, K, M, Kp, mode, xi, s, rowsum, xq_ref, fout);
+        // rows are read as float4 when every row start is 16-byte aligned
+        const bool vec = M % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
+                         (fout == nullptr || reinterpret_cast<uintptr_t>(fout) % 16 == 0);
+        // 4 tokens per block: an 8-token layout (32-byte row segments) loads faster in isolation
+        // but measured no faster end to end, and halves the block count
+        const int rounds = (int)ceil_div(K, (size_t)512);
+        const int n_groups = (int)ceil_div(M, (size_t)4);
+        TokArgs a{X, norm, eps, inv_f, (int)K, (int)M, (int)Kp, mode, xi, s, rowsum, xq_ref, fout};
+        const bool launched = launch_regs_pick<4, 1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(
+            rounds, vec, st, n_groups, a, gamma);
+        if (launched) return hipGetLastError();
     }
+    const unsigned grid = (unsigned)ceil_div(M, kWave);
+    hipLaunchKernelGGL(k_token_lanes, dim3(grid), dim3(kTW * kWave), 0, st, X, gamma, norm, eps,
+                       inv_f, K, M, Kp, mode, xi, s, rowsum, xq_ref, fout);
     return hipGetLastError();
 }
 

@@ -7,20 +7,30 @@
 // token-major int8 activations xi (M, Kp). MFMAs accumulate sum(code * x); the epilogue
 // subtracts 2 * rowsum[m] (codes are trit + 2).
 //
-// MFMA: v_mfma_i32_32x32x32_i8. On MI355X it sustains ~3.7 POP/s in a pure-MFMA loop against
-// ~2.6 for the 16x16x64 shape, so the GEMM uses 32x32 tiles. Lane l of a 32x32x32 MFMA holds
-// row l%32 (A) / token l%32 (B) and the 16 k of half l/32; for k0 = 64j + 32m it reads the
+// MFMA: v_mfma_i32_32x32x32_i8 (32 cycles, 64 Ki ops). Lane l of a 32x32x32 MFMA holds row
+// l%32 (A) / token l%32 (B) and the 16 k of half l/32; for k0 = 64j + 32m it reads the
 // T16K256 lane 16*(2m + l/32) + (row%16) of the row's tile and shifts by 2j, so the same tile
 // layout feeds both the 16x16 GEMV and this GEMM.
-// Tiling: one block per CU, kWavesN x kWavesM waves (default 2 x 4 = 8, two per SIMD so one
-// wave's LDS reads and unpacking overlap the other's MFMAs). Block tile 256 rows (16 row
-// tiles) x 128 tokens; default wave tile 128 rows x 32 tokens = 4 x 1 MFMA tiles of 32x32.
-// Per 256-wide k tile ("stage") the block stages A (16 KiB, copied as is) and B (128 token
-// rows of 256 B, 16-byte chunk c of token t stored at chunk c ^ (t & 15) so the 16 lanes of
-// a ds_read_b128 hit 16 distinct bank groups) with buffer->LDS DMA loads (no register
-// staging; out-of-range rows and tokens read as zeros). Three LDS slots form a ring: stage
-// s+2 is issued at the top of stage s, so two k tiles of loads are in flight while one is
-// multiplied; one barrier per stage. Waits on the DMA are explicit s_waitcnt vmcnt.
+//
+// Tiling: one block per CU, block tile 256 rows (16 row tiles) x 128 tokens, kWavesN x
+// kWavesM output tiles, each shared by kKSplit waves. The default 4 x 1 x 2 gives each pair
+// of waves 64 rows x 128 tokens (2 x 4 MFMA tiles); the two waves of a pair take the two k
+// halves of every 64-k group and add their partial sums through LDS at the end. So every
+// unpacked weight fragment (the only VALU work of the loop) feeds four MFMAs, LDS reads are
+// 0.75 KiB per MFMA, and two waves share each SIMD. Per 256-wide k tile ("stage") the block
+// stages A (16 KiB, copied as is) and B (128 token rows of 256 B, 16-byte chunk c of token t
+// stored at chunk c ^ (t & 15) so the 16 lanes of a ds_read_b128 hit 16 distinct bank
+// groups) with buffer->LDS DMA loads (no register staging; out-of-range rows and tokens read
+// as zeros).
+//
+// Pipeline: a ring of kSlots LDS slots (default 2: measured faster than 3, more DMA in flight
+// only added contention); the DMA of stage s+kSlots is issued as soon as every wave has
+// finished reading stage s. Within a stage the wave's 32-k steps are software-pipelined: the B
+// fragments of step i+1 are read from LDS while the MFMAs of step i run (two register sets),
+// and the A words plus the first B fragments of stage s+1 are read before the last MFMAs of
+// stage s. The one barrier per stage sits in the last step, after the wave's own reads of the
+// stage have landed and its own part of the next stage's DMA is complete (explicit vmcnt /
+// lgkmcnt waits, no memory fence, so the DMA of later stages is not drained).
 //
 // Block order is XCD-aware: blocks are dealt round-robin to the 8 XCDs, and each XCD gets
 // whole token blocks (all N for them), so a token block's activations stay in that XCD's L2.
@@ -32,6 +42,7 @@ namespace
 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr uint32_t kM3 = 0x03030303u;
@@ -39,34 +50,49 @@ constexpr uint32_t kM3 = 0x03030303u;
 #define NNHIP_GEMM_WAVES_N 4
 #endif
 #ifndef NNHIP_GEMM_WAVES_M
-#define NNHIP_GEMM_WAVES_M 2
+#define NNHIP_GEMM_WAVES_M 1
+#endif
+#ifndef NNHIP_GEMM_KSPLIT
+#define NNHIP_GEMM_KSPLIT 2
 #endif
 constexpr int kWavesN = NNHIP_GEMM_WAVES_N, kWavesM = NNHIP_GEMM_WAVES_M;
-constexpr int kWaves = kWavesN * kWavesM;
+constexpr int kKSplit = NNHIP_GEMM_KSPLIT;   // waves sharing one output tile, splitting its k steps
+constexpr int kWaves = kWavesN * kWavesM * kKSplit;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kWavesPerSimd = kWaves / 4;
 constexpr int kBN = 256, kBM = 128;          // block tile (rows, tokens)
 constexpr int kRowTiles = kBN / 16;          // 16
 constexpr int kWaveRows = kBN / kWavesN, kWaveToks = kBM / kWavesM;
-constexpr int kWaveRowBlocks = kWaveRows / 32, kWaveTokBlocks = kWaveToks / 32;  // 32x32 MFMA tiles
-constexpr int kSlots = 3;
+constexpr int kRB = kWaveRows / 32, kTB = kWaveToks / 32;  // 32x32 MFMA tiles per wave
+constexpr int kSteps = kTileK / 32;          // 8 MFMA k steps per stage
+constexpr int kWaveSteps = kSteps / kKSplit; // steps one wave runs per stage
+constexpr int kMs = 2 / kKSplit;             // k halves (of each 64-k group) one wave multiplies
+#ifndef NNHIP_GEMM_SLOTS
+#define NNHIP_GEMM_SLOTS 2  // measured: 2 slots beat 3 (more DMA in flight only adds contention)
+#endif
+constexpr int kSlots = NNHIP_GEMM_SLOTS;      // LDS ring depth (stages in flight)
 constexpr int kABytes = kRowTiles * 1024;    // 16 KiB
 constexpr int kBBytes = kBM * kTileK;        // 32 KiB
 constexpr int kSlotBytes = kABytes + kBBytes;
-constexpr int kLdsBytes = kSlots * kSlotBytes;  // 144 KiB
+// k split: one 32x32 partial sum is 16 ints x 64 lanes = 4 KiB; each wave hands over half its row blocks
+constexpr int kPartBytes = kRB / 2 * kTB * 4096;
+constexpr int kRingBytes = kSlots * kSlotBytes;  // 144 KiB for three slots
+constexpr int kLdsBytes = kKSplit == 2 && kWaves * kPartBytes > kRingBytes ? kWaves * kPartBytes : kRingBytes;
 // DMA instructions per wave per stage: A one row tile (1 KiB) each, B four token rows each
 constexpr int kADma = kRowTiles / kWaves, kBDma = kBM / 4 / kWaves;
-static_assert(kADma * kWaves == kRowTiles && kBDma * kWaves * 4 == kBM, "DMA split");
-constexpr int kDmaPerStage = kADma + kBDma;  // 12
+constexpr int kDmaPerStage = kADma + kBDma;
 constexpr int kRsrcFlags = 0x00020000;
 
-static_assert(kDmaPerStage < 63, "vmcnt range");
+static_assert(kWaves % 4 == 0 && kRB >= 1 && kTB >= 1, "wave layout");
+static_assert(kKSplit == 1 || (kKSplit == 2 && kRB % 2 == 0), "k split pairs finish one half of the row blocks each");
+static_assert(kADma * kWaves == kRowTiles && kBDma * kWaves * 4 == kBM, "DMA split");
+static_assert(kSlots >= 2 && kSlots <= 5 && 4 * kDmaPerStage < 63, "vmcnt range");
+static_assert(kTB * 32 * kTileK <= 65536, "B fragment offsets fit the ds_read immediate");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
 }
-
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c)
 {
@@ -80,13 +106,29 @@ __device__ __forceinline__ void wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
+// s_waitcnt lgkmcnt(0) with vmcnt / expcnt left open
+__device__ __forceinline__ void wait_lgkm0()
+{
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+}
+
+// Wait until this wave's DMA of a stage has landed when `later` stages have been issued after
+// it (loads complete in order, kDmaPerStage per stage).
+__device__ __forceinline__ void wait_stage_landed(int later)
+{
+    if (later <= 0) wait_vmcnt<0>();
+    else if (later == 1) wait_vmcnt<kDmaPerStage>();
+    else if (later == 2) wait_vmcnt<2 * kDmaPerStage>();
+    else if (later == 3) wait_vmcnt<3 * kDmaPerStage>();
+    else wait_vmcnt<4 * kDmaPerStage>();
+}
+
 // Workgroup barrier without a memory fence. __syncthreads() (and any workgroup fence, even
 // one limited to LDS) makes the compiler wait for every outstanding buffer->LDS load
-// (vmcnt(0)), which drains the DMA ring each stage. Here the caller's explicit vmcnt wait
-// covers the one stage that must have landed, and every LDS read of a slot is consumed
-// (lgkmcnt waited) before its wave reaches the barrier that lets the slot be refilled. The
-// empty asm statements are compiler-only memory clobbers (no wait instructions): no load or
-// store moves across the barrier.
+// (vmcnt(0)), which drains the DMA ring each stage. Here the caller's explicit waits cover
+// what must have landed (its own DMA part of the next stage, its own LDS reads of this
+// stage). The empty asm statements are compiler-only memory clobbers (no wait instructions):
+// no load or store moves across the barrier.
 __device__ __forceinline__ void lds_barrier()
 {
     asm volatile("" ::: "memory");
@@ -99,7 +141,7 @@ struct Dma
     __amdgpu_buffer_rsrc_t ra, rb;
     uint32_t a_voff;    // lane * 16 within a row tile
     uint32_t b_voff[kBDma];
-    uint32_t a_row0;    // first row tile (global) this wave copies
+    uint32_t a_row0;    // first row tile (global) of the block
 };
 
 // Issue the DMA of k tile kt into LDS slot `slot`.
@@ -123,12 +165,219 @@ __device__ __forceinline__ void issue_stage(uint8_t* lds, const Dma& d, int slot
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_gemm(GemvProblem p, int n_mblocks, int n_nblocks, int xcd_mode)
+// A words of one stage: row block rb, the wave's k half (T16K256 lane 16*(2m + h) + row%16;
+// the k half offset is part of p)
+__device__ __forceinline__ void read_a(v4i (&dst)[kRB][kMs], const uint8_t* p)
+{
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+        for (int m = 0; m < kMs; ++m) dst[rb][m] = *reinterpret_cast<const v4i*>(p + rb * 2048 + m * 512);
+}
+
+// B fragments of one step for the wave's kTB token blocks (32 token rows = 8 KiB apart)
+__device__ __forceinline__ void read_b(v4i (&dst)[kTB], const uint8_t* p)
+{
+#pragma unroll
+    for (int n = 0; n < kTB; ++n) dst[n] = *reinterpret_cast<const v4i*>(p + n * 32 * kTileK);
+}
+
+struct Lane
+{
+    uint32_t a_off;              // A read offset within a slot
+    uint32_t b_off;              // B read offset within a slot (token row of block 0)
+    uint32_t b_step[kWaveSteps]; // swizzled chunk offset of the wave's step i
+};
+
+// One stage: the wave's 32-k steps (all eight, or the four of its k half). P selects the
+// register set holding this stage's A words; the next stage's go to the other set.
+template <int P>
+__device__ __forceinline__ void run_stage(int s, int KT, uint8_t* lds, const Dma& d, const Lane& ln,
+                                          v4i (&wa)[2][kRB][kMs], v4i (&bf)[2][kTB], v16i (&acc)[kRB][kTB])
+{
+    const uint8_t* slot = lds + (s % kSlots) * kSlotBytes;
+#pragma unroll
+    for (int i = 0; i < kWaveSteps; ++i)
+    {
+        const int j = i / kMs, m = i % kMs;  // 64-k group, and the k half within the wave's set
+        const int cur = i & 1, nxt = cur ^ 1;
+        if (i + 1 < kWaveSteps)
+        {
+            read_b(bf[nxt], slot + ln.b_off + ln.b_step[i + 1]);
+        }
+        else if (s + 1 < KT)
+        {
+            wait_lgkm0();  // this wave's reads of stage s have landed
+            wait_stage_landed(min(KT - 2 - s, kSlots - 2));  // its part of stage s+1 has landed
+            lds_barrier();  // all of stage s+1 is in LDS; nobody reads stage s's slot any more
+            if (s + kSlots < KT) issue_stage(lds, d, s % kSlots, s + kSlots, KT);
+            const uint8_t* nslot = lds + ((s + 1) % kSlots) * kSlotBytes;
+            read_a(wa[P ^ 1], nslot + ln.a_off);
+            read_b(bf[nxt], nslot + ln.b_off + ln.b_step[0]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb)
+        {
+            const v4i a = (v4i)((__builtin_bit_cast(u32x4, wa[P][rb][m]) >> (2 * j)) & kM3);
+#pragma unroll
+            for (int n = 0; n < kTB; ++n) acc[rb][n] = mfma32(a, bf[cur][n], acc[rb][n]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Epilogue of a block that lies wholly inside Y: no masks. The 32x32 accumulator layout puts
+// element i of lane l at row 8*(i/4) + 4*(l/32) + i%4, token l%32; row offsets are scalar.
+template <bool kBias>
+__device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&acc)[kRB][kTB], int rb0, int nrb,
+                                           int row_w, int tok_w, int h, int l32)
+{
+    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rbias = rsrc(kBias ? p.bias : p.tau, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
+    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
+    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+    const uint32_t M4 = (uint32_t)p.M * 4u;
+    int rs2[kTB];
+    float sv[kTB];
+#pragma unroll
+    for (int n = 0; n < kTB; ++n)
+    {
+        const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
+        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
+        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+    }
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+    {
+        if (rb < rb0 || rb >= rb0 + nrb) continue;
+        const uint32_t row0 = (uint32_t)(row_w + rb * 32 + 4 * h);
+        float tv[16], bv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+        {
+            const uint32_t row = row0 + (uint32_t)(8 * (i >> 2) + (i & 3));
+            tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
+            if (kBias) bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
+        }
+        const uint32_t vbase = (row0 * (uint32_t)p.M + (uint32_t)(tok_w + l32)) * 4u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+        {
+            const int soff = (8 * (i >> 2) + (i & 3)) * (int)M4;
+#pragma unroll
+            for (int n = 0; n < kTB; ++n)
+            {
+                const int a = acc[rb][n][i] - rs2[n];
+                float y = (tv[i] * sv[n]) * (float)a;
+                if (kBias) y = y + bv[i];
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, vbase + (uint32_t)(n * 128),
+                                                      soff, 0);
+            }
+        }
+    }
+}
+
+// Epilogue of an edge block: rows past N and tokens past M are masked (their lanes store to
+// an out-of-range offset, which the buffer unit drops).
+__device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&acc)[kRB][kTB], int rb0, int nrb,
+                                           int row_w, int tok_w, int h, int l32)
+{
+    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
+    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
+    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+    int rs2[kTB];
+    float sv[kTB];
+#pragma unroll
+    for (int n = 0; n < kTB; ++n)
+    {
+        const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
+        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
+        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+    }
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+    {
+        if (rb < rb0 || rb >= rb0 + nrb) continue;
+        const int row0 = row_w + rb * 32 + 4 * h;
+        float tv[16], bv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+        {
+            const uint32_t row = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3));
+            tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
+            bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
+        }
+#pragma unroll
+        for (int n = 0; n < kTB; ++n)
+        {
+            const int m = tok_w + n * 32 + l32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+            {
+                const int row = row0 + 8 * (i >> 2) + (i & 3);
+                const int a = acc[rb][n][i] - rs2[n];
+                float y = (tv[i] * sv[n]) * (float)a;
+                if (p.bias) y = y + bv[i];
+                const uint32_t off = (row < p.N && m < p.M) ? ((uint32_t)row * (uint32_t)p.M + (uint32_t)m) * 4u
+                                                             : 0xFFFFFFF0u;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
+            }
+        }
+    }
+}
+
+// k split: wave KS of a pair hands the partial sums of the row blocks its partner finishes to
+// the partner through LDS (put_partials), and after a barrier adds the partner's partials of
+// its own row blocks (add_partials).
+
+template <int KS>
+__device__ __forceinline__ void put_partials(const v16i (&acc)[kRB][kTB], uint8_t* lds, int wave, int lane)
+{
+    constexpr int kHalf = kRB / 2;
+    v4i* mine = reinterpret_cast<v4i*>(lds + wave * kPartBytes);
+#pragma unroll
+    for (int r = 0; r < kHalf; ++r)
+#pragma unroll
+        for (int n = 0; n < kTB; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const v16i& a = acc[(1 - KS) * kHalf + r][n];
+                mine[((r * kTB + n) * 4 + q) * 64 + lane] = v4i{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            }
+}
+
+template <int KS>
+__device__ __forceinline__ void add_partials(v16i (&acc)[kRB][kTB], const uint8_t* lds, int wave, int lane)
+{
+    constexpr int kHalf = kRB / 2;
+    const v4i* theirs = reinterpret_cast<const v4i*>(lds + (wave ^ (kWavesN * kWavesM)) * kPartBytes);
+#pragma unroll
+    for (int r = 0; r < kHalf; ++r)
+#pragma unroll
+        for (int n = 0; n < kTB; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const v4i o = theirs[((r * kTB + n) * 4 + q) * 64 + lane];
+                v16i& a = acc[KS * kHalf + r][n];
+                a[4 * q] += o[0];
+                a[4 * q + 1] += o[1];
+                a[4 * q + 2] += o[2];
+                a[4 * q + 3] += o[3];
+            }
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd))) void
+k_gemm(GemvProblem p, int n_mblocks, int n_nblocks, int xcd_mode)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave % kWavesN, wm = wave / kWavesN;
-    const int g = lane >> 4, t = lane & 15;
+    const int wn = wave % kWavesN, wm = (wave / kWavesN) % kWavesM, ks = wave / (kWavesN * kWavesM);
     const int KT = p.KT;
     const uint32_t Kp = (uint32_t)KT * kTileK;
     const int RT = (p.N + 15) / 16;
@@ -167,110 +416,77 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemvProblem p, int n_mblocks,
         d.b_voff[i] = m < p.M ? (uint32_t)m * Kp + (uint32_t)c * 16u : 0x80000000u;
     }
 
-    v16i acc[kWaveRowBlocks][kWaveTokBlocks];
-#pragma unroll
-    for (int i = 0; i < kWaveRowBlocks; ++i)
-#pragma unroll
-        for (int n = 0; n < kWaveTokBlocks; ++n) acc[i][n] = v16i{};
-
+    // ---- per-lane LDS read offsets
     const int h = lane >> 5, l32 = lane & 31;
+    Lane ln;
+    ln.a_off = (uint32_t)((wn * (kWaveRows / 16) + (l32 >> 4)) * 1024 + (16 * h + (l32 & 15)) * 16 +
+                          (kKSplit == 2 ? ks * 512 : 0));
+    ln.b_off = (uint32_t)(kABytes + (wm * kWaveToks + l32) * kTileK);
+    const int rsw = h ^ (l32 & 15);  // token row % 16 is l32 % 16 for every token block
+#pragma unroll
+    for (int i = 0; i < kWaveSteps; ++i)
+    {
+        const int j = i / kMs, m = kKSplit == 2 ? ks : i % kMs;
+        const int c0 = 4 * j + 2 * m;  // chunk of lane half 0 for step (j, m)
+        ln.b_step[i] = (uint32_t)((c0 ^ rsw) << 4);
+    }
+
+    v16i acc[kRB][kTB];
+#pragma unroll
+    for (int i = 0; i < kRB; ++i)
+#pragma unroll
+        for (int n = 0; n < kTB; ++n) acc[i][n] = v16i{};
+
+    // ---- prologue: three stages in flight, then stage 0's first reads
     issue_stage(lds, d, 0, 0, KT);
-    if (KT > 1) issue_stage(lds, d, 1, 1, KT);
+#pragma unroll
+    for (int i = 1; i < kSlots; ++i)
+        if (i < KT) issue_stage(lds, d, i, i, KT);
+    wait_stage_landed(min(KT - 1, kSlots - 1));
+    lds_barrier();
+    v4i wa[2][kRB][kMs];
+    v4i bf[2][kTB];
+    read_a(wa[0], lds + ln.a_off);
+    read_b(bf[0], lds + ln.b_off + ln.b_step[0]);
 
-    for (int s = 0; s < KT; ++s)
+    int s = 0;
+    for (; s + 1 < KT; s += 2)
     {
-        // stage s has landed once at most the next stage's DMAs are outstanding
-        if (s + 1 < KT) wait_vmcnt<kDmaPerStage>();
-        else wait_vmcnt<0>();
-        lds_barrier();  // every wave's part of stage s is in LDS; stage s-1's slot is free
-        if (s + 2 < KT) issue_stage(lds, d, (s + 2) % kSlots, s + 2, KT);
+        run_stage<0>(s, KT, lds, d, ln, wa, bf, acc);
+        run_stage<1>(s + 1, KT, lds, d, ln, wa, bf, acc);
+    }
+    if (s < KT) run_stage<0>(s, KT, lds, d, ln, wa, bf, acc);
 
-        const uint8_t* sa = lds + (s % kSlots) * kSlotBytes;
-        const uint8_t* sb = sa + kABytes;
-        // A words: row block rb covers row tiles wn*8 + 2rb + (l32 / 16); half m of the 64-k
-        // group is T16K256 lane 16 * (2m + h) + l32 % 16
-        v4i wa[kWaveRowBlocks][2];
-#pragma unroll
-        for (int rb = 0; rb < kWaveRowBlocks; ++rb)
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-            {
-                const int rt_local = wn * (kWaveRows / 16) + 2 * rb + (l32 >> 4);
-                wa[rb][m] = *reinterpret_cast<const v4i*>(sa + rt_local * 1024 + (16 * (2 * m + h) + (l32 & 15)) * 16);
-            }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-        {
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-            {
-                const int c = 4 * j + 2 * m + h;  // 16-byte chunk of this lane's k half
-                v4i bf[kWaveTokBlocks];
-#pragma unroll
-                for (int n = 0; n < kWaveTokBlocks; ++n)
-                {
-                    const int row = wm * kWaveToks + n * 32 + l32;
-                    bf[n] = *reinterpret_cast<const v4i*>(sb + row * kTileK + ((c ^ (row & 15)) << 4));
-                }
-#pragma unroll
-                for (int rb = 0; rb < kWaveRowBlocks; ++rb)
-                {
-                    const v4i a = (v4i)((__builtin_bit_cast(u32x4, wa[rb][m]) >> (2 * j)) & kM3);
-#pragma unroll
-                    for (int n = 0; n < kWaveTokBlocks; ++n) acc[rb][n] = mfma32(a, bf[n], acc[rb][n]);
-                }
-            }
-        }
+    // ---- k split: the two waves of a pair swap partial sums through LDS; wave ks finishes row
+    // blocks [ks * kRB / 2, (ks + 1) * kRB / 2).
+    int rb0 = 0, nrb = kRB;
+    if (kKSplit == 2)
+    {
+        constexpr int kHalf = kRB / 2;
+        rb0 = ks * kHalf;
+        nrb = kHalf;
+        wait_lgkm0();
+        wait_vmcnt<0>();
+        lds_barrier();  // every wave is done with the ring
+        if (ks == 0) put_partials<0>(acc, lds, wave, lane);
+        else put_partials<1>(acc, lds, wave, lane);
+        lds_barrier();
+        if (ks == 0) add_partials<0>(acc, lds, wave, lane);
+        else add_partials<1>(acc, lds, wave, lane);
     }
 
-    // ---- epilogue. Operands come in with unconditional buffer loads (rows past N, tokens past M read 0),
-    // issued together so the waits do not serialize; masked lanes store to an out-of-range
-    // offset, which the buffer unit drops.
-    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
-    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
-    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
-    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)((size_t)p.N * p.M * 4u <= 0xFFFFFFFFull
-                                                               ? (size_t)p.N * p.M * 4u : 0xFFFFFFFFull));
-    int rs2[kWaveTokBlocks];
-    float sv[kWaveTokBlocks];
-#pragma unroll
-    for (int n = 0; n < kWaveTokBlocks; ++n)
+    // ---- epilogue
+    const int row_w = (rt0 + wn * (kWaveRows / 16)) * 16;
+    const int tok_w = m0 + wm * kWaveToks;
+    const bool full = rt0 * 16 + kBN <= p.N && m0 + kBM <= p.M;
+    if (full)
     {
-        const uint32_t m = (uint32_t)(m0 + wm * kWaveToks + n * 32 + l32);
-        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
-        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+        if (p.bias) store_full<true>(p, acc, rb0, nrb, row_w, tok_w, h, l32);
+        else store_full<false>(p, acc, rb0, nrb, row_w, tok_w, h, l32);
     }
-    // 32x32 accumulator layout: element i of lane l is row 8*(i/4) + 4*(l/32) + i%4, token l%32.
-    // One row block at a time: its 16 tau / bias values are loaded together, then stored.
-#pragma unroll
-    for (int rb = 0; rb < kWaveRowBlocks; ++rb)
+    else
     {
-        const int row0 = (rt0 + wn * (kWaveRows / 16) + 2 * rb) * 16 + 4 * h;
-        float tv[16], bv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-        {
-            const uint32_t row = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3));
-            tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
-            bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
-        }
-#pragma unroll
-        for (int n = 0; n < kWaveTokBlocks; ++n)
-        {
-            const int m = m0 + wm * kWaveToks + n * 32 + l32;
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-            {
-                const int row = row0 + 8 * (i >> 2) + (i & 3);
-                const int a = acc[rb][n][i] - rs2[n];
-                float y = (tv[i] * sv[n]) * (float)a;
-                if (p.bias) y = y + bv[i];
-                const uint32_t off = (row < p.N && m < p.M) ? ((uint32_t)row * (uint32_t)p.M + (uint32_t)m) * 4u
-                                                             : 0xFFFFFFF0u;
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
-            }
-        }
+        store_edge(p, acc, rb0, nrb, row_w, tok_w, h, l32);
     }
 }
 

@@ -334,17 +334,18 @@ void orc_add_row_broadcast(float* Y, const float* b, size_t N, size_t M)
 
 /* -------------------------------------------------------------- RMSNorm */
 
-/* The per-token sum of squares uses the same fixed order as the absmean above: 64 strided
- * parts (feature f goes to part f % 64), each summed in ascending f, then the xor butterfly
- * over offsets 32,16,8,4,2,1. Both GPU kernels (one wave per token, or 64 tokens per block
- * with 8 parts per lane) evaluate exactly this tree. */
+/* The per-token sum of squares uses a fixed order shared with every GPU kernel: 512 strided
+ * parts (feature f goes to part f % 512), each summed in ascending f, then the xor butterfly
+ * over offsets 256,128,...,1. (The reference evaluates this reduction inside its JIT engine,
+ * whose order is not available; any fixed order is as faithful, and this one lets a GPU
+ * thread own whole parts whether it holds one token per wave or 4-8 tokens per block.) */
 static float orc_rms_inv(const float* X, float eps, size_t F, size_t M, size_t m)
 {
-    float p[64];
-    for (int l = 0; l < 64; ++l)
+    float p[512];
+    for (int l = 0; l < 512; ++l)
     {
         float part = 0.0f;
-        for (size_t f = (size_t)l; f < F; f += 64)
+        for (size_t f = (size_t)l; f < F; f += 512)
         {
             const float x = X[f * M + m];
             const float sq = x * x;
@@ -352,10 +353,10 @@ static float orc_rms_inv(const float* X, float eps, size_t F, size_t M, size_t m
         }
         p[l] = part;
     }
-    for (int off = 32; off >= 1; off >>= 1)
+    for (int off = 256; off >= 1; off >>= 1)
     {
-        float q[64];
-        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ off];
+        float q[512];
+        for (int l = 0; l < 512; ++l) q[l] = p[l] + p[l ^ off];
         memcpy(p, q, sizeof p);
     }
     const float inv_f = 1.0f / (float)F;

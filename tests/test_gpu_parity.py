@@ -207,6 +207,55 @@ def test_rmsnorm_quant(ctx, orc, F, M, eps):
     assert np.array_equal(host(xi)[:, :F], orc.container_to_int8(xq_o, M).T)
 
 
+def check_quant(ctx, orc, X, g=None, eps=1e-6):
+    """act_quant_i8 (g None) or rmsnorm_quant_i8 on X (K, M) against the oracle, all outputs."""
+    K, M = X.shape
+    if g is None:
+        xi, s, rs, xq = ctx.act_quant_i8(dev(X), want_container=True)
+        s_o = orc.act_scale(X)
+        xq_o = orc.quantize_i8(X, s_o, True)
+    else:
+        xi, s, rs, xq = ctx.rmsnorm_quant_i8(dev(X), dev(g), eps, want_container=True)
+        xq_o, s_o = orc.rmsnorm_quant_i8(X, g, eps)
+    assert np.array_equal(host(s), s_o)
+    assert np.array_equal(host(xq, np.uint32), xq_o)
+    q = orc.container_to_int8(xq_o, M).T
+    xi_h = host(xi)
+    assert np.array_equal(xi_h[:, :K], q)
+    assert np.all(xi_h[:, K:] == 0)
+    assert np.array_equal(host(rs), q.astype(np.int64).sum(axis=1))
+
+
+# M > 32 runs the register-resident kernel (rounds of 512 rows, 4 tokens per block; M % 4 != 0
+# takes the scalar-load path); K = 11264 is its largest instantiation, K = 11265 the fallback.
+@pytest.mark.parametrize("K,M", [(1, 36), (255, 37), (512, 40), (513, 128), (1000, 66), (2560, 2048),
+                                 (4096, 2048), (6912, 132), (11264, 40), (11265, 36)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_token_kernel_shapes(ctx, orc, K, M, norm):
+    say(f"token kernel K={K} M={M} norm={norm}")
+    X = normal((K, M), K * 31 + M, 0.0, 1.0)
+    X.flat[::977] *= 20.0
+    g = normal((K,), K + 5, 1.0, 0.2) if norm else None
+    check_quant(ctx, orc, X, g)
+
+
+def test_quant_near_ties(ctx, orc):
+    """x / s on and within a few ulps of half-integers: the division-free path must hand these
+    to the exact division. Each token holds one 127 (s = fl(127 * fl(1/127))) and values
+    (n + 1/2) * (1 + d) with d in {0, +-2^-23, +-2^-20, +-2^-14}."""
+    say("act_quant near ties")
+    rng = np.random.default_rng(7)
+    K, M = 1024, 64
+    n = rng.integers(-126, 126, size=(K, M)).astype(np.float64)
+    d = rng.choice([0.0, 2.0 ** -23, -2.0 ** -23, 2.0 ** -20, -2.0 ** -20, 2.0 ** -14, -2.0 ** -14], size=(K, M))
+    X = ((n + 0.5) * (1.0 + d)).astype(np.float32)
+    X[0, :] = 127.0
+    X[1, ::3] = -127.0
+    check_quant(ctx, orc, X)
+    # and scaled so that s is far from 1
+    check_quant(ctx, orc, (X * np.float32(0.0371)).astype(np.float32))
+
+
 # ------------------------------------------------------------------ fast-path GEMV / GEMM
 
 def fast_case(ctx, orc, N, K, M, seed, outliers=False):
