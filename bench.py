@@ -7,9 +7,15 @@ ternary weights (more than twice the 256 MB MALL) — run as ONE grouped launch 
 value = algorithmic bytes of the whole sweep / average launch time, in GB/s.
 
 Reported beside it: the same sweep at M=16, per-shape grouped sweeps, single-GEMV launches,
-and the prefill GEMM (config 2: M=2048, K=4096, N in {4096, 11008}) in TOPS against the
-dense int8 MFMA peak. The CPU baseline is the oracle's CpuEngine restatement (row-block
-decode + dense f32 microkernel) on a bounded sample of the same workload, timed on this host.
+the prefill GEMM (config 2: M in {256, 1024, 2048, 4096}, K=4096, N in {4096, 11008}) in TOPS
+against the dense int8 MFMA peak, and the fused activation quantizers at prefill sizes
+(absmax -> int8 at K=4096, RMSNorm -> absmax -> int8 at the fused block's 2560 x 2048) in GB/s.
+The CPU baseline is the oracle's CpuEngine restatement (row-block decode + dense f32
+microkernel) on a bounded sample of the same workload, timed on this host.
+
+roofline.traffic (HBM bytes per headline launch) is read from the committed PMC summary
+profiles/k_gemv_grouped_m1_layerstack_pmc.md, which records the two rocprofv3 --pmc runs
+(FETCH_SIZE, WRITE_SIZE) and the copy-kernel calibration (`bench.py --copy-probe`).
 
 Inputs are synthetic (seeded): W ~ N(0, 0.02) ternarized by per-tensor absmean, activations
 ~ N(0, 1) quantized per token by absmax. All inputs are resident in HBM before timing.
@@ -150,8 +156,10 @@ def extra_gemv_lines(ctx, torch, stream, weights, acts1, out):
 
 
 def gemm_lines(ctx, torch, stream, steps, out):
-    M, K = 2048, 4096
-    _, xi, s, rs = make_acts(ctx, torch, K, M, 0xB17A0004, outliers=True)
+    """Config 2: the prefill GEMM at M in {256, 1024, 2048, 4096}, K=4096, N in {4096, 11008}
+    (activations with 0.1% outliers at 20x before the per-token absmax)."""
+    K = 4096
+    acts = {M: make_acts(ctx, torch, K, M, 0xB17A0004 + M, outliers=True) for M in (256, 1024, 2048, 4096)}
     gemm = {}
     for N in (4096, 11008):
         gen = torch.Generator(device="cuda")
@@ -160,16 +168,67 @@ def gemm_lines(ctx, torch, stream, steps, out):
         tau = W.abs().double().mean().float().expand(N).contiguous()
         rp = ctx.repack(ctx.trit_pack(W, tau), K)
         del W
-        y = torch.empty((N, M), dtype=torch.float32, device="cuda")
-        t, _ = time_launches(torch, stream,
-                             lambda: ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, out=y),
-                             max(10, steps // 2), 5)
-        tops = 2.0 * M * N * K / t / 1e12
-        gemm[f"M={M} K={K} N={N}"] = {"TOPS": round(tops, 1), "us": round(t * 1e6, 1),
-                                      "frac_int8_mfma": round(tops / INT8_PEAK_TOPS, 4)}
-        log(f"GEMM M={M} K={K} N={N}: {t * 1e6:.1f} us, {tops:.1f} TOPS "
-            f"({tops / INT8_PEAK_TOPS:.3f} of int8 MFMA peak)")
+        for M, (_, xi, s, rs) in acts.items():
+            y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+            t, _ = time_launches(torch, stream,
+                                 lambda: ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, out=y),
+                                 max(10, steps // 2), 5)
+            tops = 2.0 * M * N * K / t / 1e12
+            gemm[f"M={M} K={K} N={N}"] = {"TOPS": round(tops, 1), "us": round(t * 1e6, 1),
+                                          "frac_int8_mfma": round(tops / INT8_PEAK_TOPS, 4)}
+            log(f"GEMM M={M} K={K} N={N}: {t * 1e6:.1f} us, {tops:.1f} TOPS "
+                f"({tops / INT8_PEAK_TOPS:.3f} of int8 MFMA peak)")
+            del y
     out["prefill_gemm"] = gemm
+
+
+def act_quant_lines(ctx, torch, stream, steps, out):
+    """The fused activation quantizers at prefill sizes, in GB/s of algorithmic bytes
+    (4KM fp32 read + M*Kp int8 + 8M written)."""
+    res = {}
+    for K, M, norm in ((4096, 2048, False), (2560, 2048, True), (6912, 2048, False)):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0xB17A0006 + K)
+        X = torch.randn((K, M), generator=gen, device="cuda")
+        g = torch.ones(K, device="cuda")
+        outs = ctx._act_out(K, M)
+        if norm:
+            fn = lambda: ctx.rmsnorm_quant_i8(X, g, 1e-6, outs=outs)
+            name = f"rmsnorm_quant K={K} M={M}"
+        else:
+            fn = lambda: ctx.act_quant_i8(X, outs=outs)
+            name = f"act_quant K={K} M={M}"
+        t, _ = time_launches(torch, stream, fn, max(10, steps // 2), 5)
+        nb = 4 * K * M + M * ((K + 255) // 256 * 256) + 8 * M
+        res[name] = {"GB/s": round(nb / t / 1e9, 1), "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4),
+                     "us": round(t * 1e6, 2)}
+        log(f"{name}: {t * 1e6:.2f} us, {nb / t / 1e9:.1f} GB/s")
+    out["act_quant"] = res
+
+
+def profiled_traffic():
+    """Calibrated HBM bytes per headline launch from the committed PMC summary, or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", "k_gemv_grouped_m1_layerstack_pmc.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def copy_probe(mib):
+    """A plain device copy of known size (mib MiB read + mib MiB written), ten times: the PMC
+    FETCH_SIZE / WRITE_SIZE calibration kernel."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n * 4}), flush=True)
 
 
 def cpu_baseline(weights, acts1, budget_s=12.0):
@@ -209,12 +268,18 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM lines")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the M=16 / per-shape / single-launch GEMV lines")
+                    help="skip the M=16 / per-shape / single-launch GEMV and the quantizer lines")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB ten times (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     import torch
     nn = load_pkg()
@@ -246,6 +311,7 @@ def main():
     extra = {}
     if not args.no_extra:
         extra_gemv_lines(ctx, torch, stream, weights, acts1, extra)
+        act_quant_lines(ctx, torch, stream, args.steps, extra)
     if not args.no_gemm:
         gemm_lines(ctx, torch, stream, args.steps, extra)
     cpu = None
@@ -274,7 +340,7 @@ def main():
                    "packed_weight_bytes": wbytes, "algorithmic_bytes": nbytes,
                    "grid_waves": ctx.gemv_grid_waves(n_items)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                      "kernel": "k_gemv_grouped", "avg_launch_us": round(t_launch * 1e6, 2)},
         "cpu_baseline": cpu,
     }

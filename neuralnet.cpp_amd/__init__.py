@@ -308,10 +308,11 @@ class Context:
         rs = self._empty((M,), torch.int32)
         return xi, s, rs
 
-    def act_quant_i8(self, X, want_container: bool = False):
+    def act_quant_i8(self, X, want_container: bool = False, outs=None):
+        """outs: optional preallocated (xi, s, rowsum) to write into."""
         torch = self._torch
         K, M = X.shape
-        xi, s, rs = self._act_out(K, M)
+        xi, s, rs = self._act_out(K, M) if outs is None else outs
         xq = self._empty((K, (M + 3) // 4), torch.int32) if want_container else None
         self._bind_stream()
         _check(lib().nnhip_act_quant_i8(self.h, self._dev(X, torch.float32, "X"), K, M,
@@ -320,10 +321,11 @@ class Context:
                "nnhip_act_quant_i8")
         return (xi, s, rs, xq) if want_container else (xi, s, rs)
 
-    def rmsnorm_quant_i8(self, X, gamma, eps: float, want_container: bool = False):
+    def rmsnorm_quant_i8(self, X, gamma, eps: float, want_container: bool = False, outs=None):
+        """outs: optional preallocated (xi, s, rowsum) to write into."""
         torch = self._torch
         F, M = X.shape
-        xi, s, rs = self._act_out(F, M)
+        xi, s, rs = self._act_out(F, M) if outs is None else outs
         xq = self._empty((F, (M + 3) // 4), torch.int32) if want_container else None
         self._bind_stream()
         _check(lib().nnhip_rmsnorm_quant_i8(self.h, self._dev(X, torch.float32, "X"),
