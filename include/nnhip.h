@@ -144,6 +144,22 @@ nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* 
                                const uint32_t* xq, const float* s, size_t N, size_t K, size_t M,
                                float* Y);
 
+/* Y (N, M) = (tau o trit(wq)) . B: ternary weights times float activations with f32
+ * accumulation; B (K, M) and Y (N, M) are f32, or f16 when b_f16 / y_f16 != 0 (16-bit IEEE
+ * halves, round to nearest even on output). Accumulation order is not pinned by the reference;
+ * results match a float64 evaluation within 1e-4 x max(1, max|Y|) (f32) or 4e-3 (f16 output).
+ * Replaces ComputeEngine::matmul_q (include/neuralnet.cpp/compute_layer_bitlinear.hpp:464;
+ * src/ternary_gemm_test.cpp:253-289, :435-526). */
+nnhip_status nnhip_matmul_q(nnhip_ctx* ctx, const uint32_t* wq, const float* tau, const void* B, int b_f16,
+                            size_t N, size_t K, size_t M, void* Y, int y_f16);
+
+/* Y (M, N) = (tau o trit(A))^T . B, with A (K, ceil(M/16)) packed like wq (one stored row per
+ * k, tau (K, 1) per stored row) and B (K, N); precisions and tolerance as nnhip_matmul_q.
+ * Replaces ComputeEngine::matmul_q_t (include/neuralnet.cpp/compute_layer_bitlinear.hpp:494, the
+ * dX = (tau o W)^T . dY of BitLinear::backward; src/ternary_gemm_test.cpp:291-334, :435-526). */
+nnhip_status nnhip_matmul_q_t(nnhip_ctx* ctx, const uint32_t* A, const float* tau, const void* B, int b_f16,
+                              size_t K, size_t M, size_t N, void* Y, int y_f16);
+
 /* Y[n, m] = Y[n, m] + b[n]. Replaces dsl::compute(leaf(y) + row_broadcast(b))
  * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:455-456). */
 nnhip_status nnhip_add_row_broadcast(nnhip_ctx* ctx, float* Y, const float* b, size_t N, size_t M);

@@ -79,6 +79,8 @@ SIGNATURES = {
     "nnhip_unpack_i8": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_matmul_q_i8": (_st, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_add_row_broadcast": (_st, [_vp, _vp, _vp, _sz, _sz]),
+    "nnhip_matmul_q": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
+    "nnhip_matmul_q_t": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_rmsnorm": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _vp]),
     "nnhip_repacked_bytes": (_sz, [_sz, _sz]),
     "nnhip_repack_ternary": (_st, [_vp, _vp, _sz, _sz, _vp]),
@@ -262,6 +264,34 @@ class Context:
                                        self._dev(xq, torch.int32, "xq"),
                                        self._dev(s, torch.float32, "s"), N, K, M, self._dev(Y)),
                "nnhip_matmul_q_i8")
+        return Y
+
+    def matmul_q(self, wq, tau, B, K: int, out_f16: bool = False):
+        """Y (N, M) = (tau o trit(wq)) . B; B f32 or f16 (K, M); Y f32, or f16 if out_f16."""
+        torch = self._torch
+        N, M = wq.shape[0], B.shape[1]
+        if B.shape[0] != K:
+            raise NNHipError(1, f"B has {B.shape[0]} rows, expected K={K}")
+        Y = self._empty((N, M), torch.float16 if out_f16 else torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_matmul_q(self.h, self._dev(wq, torch.int32, "wq"), self._dev(tau, torch.float32, "tau"),
+                                    self._dev(B, (torch.float32, torch.float16), "B"),
+                                    1 if B.dtype == torch.float16 else 0, N, K, M, self._dev(Y),
+                                    1 if out_f16 else 0), "nnhip_matmul_q")
+        return Y
+
+    def matmul_q_t(self, A, tau, B, M: int, out_f16: bool = False):
+        """Y (M, N) = (tau o trit(A))^T . B, A (K, ceil(M/16)) packed with tau per stored row."""
+        torch = self._torch
+        K, N = A.shape[0], B.shape[1]
+        if B.shape[0] != K:
+            raise NNHipError(1, f"B has {B.shape[0]} rows, expected K={K}")
+        Y = self._empty((M, N), torch.float16 if out_f16 else torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_matmul_q_t(self.h, self._dev(A, torch.int32, "A"), self._dev(tau, torch.float32, "tau"),
+                                      self._dev(B, (torch.float32, torch.float16), "B"),
+                                      1 if B.dtype == torch.float16 else 0, K, M, N, self._dev(Y),
+                                      1 if out_f16 else 0), "nnhip_matmul_q_t")
         return Y
 
     def add_row_broadcast(self, Y, b):

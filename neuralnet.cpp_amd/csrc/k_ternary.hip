@@ -18,15 +18,6 @@ namespace nnhip
 namespace
 {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-constexpr uint32_t kM3 = 0x03030303u;
-
-__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c)
-{
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
 // ------------------------------------------------------------------ repack / unrepack
 
 // One thread per output word (rt, kt, lane l = 16g + r, q).

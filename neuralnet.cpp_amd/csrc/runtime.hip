@@ -425,6 +425,32 @@ nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* 
     return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, nullptr, N, K, M, Y);
 }
 
+nnhip_status nnhip_matmul_q(nnhip_ctx* ctx, const uint32_t* wq, const float* tau, const void* B, int b_f16,
+                            size_t N, size_t K, size_t M, void* Y, int y_f16)
+{
+    const char* fn = "nnhip_matmul_q";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(wq && tau && B && Y, fn, "null pointer");
+    NNHIP_REQUIRE(K >= 1 && N <= kMaxDim && M <= kMaxDim && K <= kMaxDim, fn, "bad shape");
+    NNHIP_REQUIRE(mul_ok(N, ceil_div(K, 16)) && mul_ok(K, M) && mul_ok(N, M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_matmul_q(ctx->stream, wq, tau, B, b_f16 != 0, N, K, M, Y, y_f16 != 0));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_matmul_q_t(nnhip_ctx* ctx, const uint32_t* A, const float* tau, const void* B, int b_f16,
+                              size_t K, size_t M, size_t N, void* Y, int y_f16)
+{
+    const char* fn = "nnhip_matmul_q_t";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(A && tau && B && Y, fn, "null pointer");
+    NNHIP_REQUIRE(K >= 1 && N <= kMaxDim && M <= kMaxDim && K <= kMaxDim, fn, "bad shape");
+    NNHIP_REQUIRE(mul_ok(K, ceil_div(M, 16)) && mul_ok(K, N) && mul_ok(M, N), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_matmul_q_t(ctx->stream, A, tau, B, b_f16 != 0, K, M, N, Y, y_f16 != 0));
+    return NNHIP_OK;
+}
+
 nnhip_status nnhip_add_row_broadcast(nnhip_ctx* ctx, float* Y, const float* b, size_t N, size_t M)
 {
     const char* fn = "nnhip_add_row_broadcast";

@@ -196,6 +196,40 @@ Result<Tensor> ComputeEngine::matmul_q_i8(const Tensor& wq, const Tensor& tau, c
     return *y;
 }
 
+Result<Tensor> ComputeEngine::matmul_q(const Tensor& wq, const Tensor& tau, const Tensor& B, Precision p)
+{
+    EX_TRY_CHECK(check_owned(wq, "matmul_q: wq"));
+    EX_TRY_CHECK(check_owned(tau, "matmul_q: tau"));
+    EX_TRY_CHECK(check_owned(B, "matmul_q: B"));
+    EX_TRY_CHECK(require_f32(B, "matmul_q", "B"));
+    if (p != Precision::F32) return Error{"matmul_q: only f32 output is supported by this engine"};
+    const std::size_t N = wq.rows(), K = B.rows(), M = B.cols();
+    if (wq.cols() != trit_pack::words_per_row(K))
+        return Error{"matmul_q: wq " + shape(wq) + " does not match K=" + std::to_string(K)};
+    if (tau.rows() != N || tau.cols() != 1) return Error{"matmul_q: tau must be (N,1), got " + shape(tau)};
+    EX_TRY(y, alloc_impl(N, M, Precision::F32));
+    EX_TRY_CHECK(matmul_q_impl(wq, tau, B, *y));
+    return *y;
+}
+
+Result<Tensor> ComputeEngine::matmul_q_t(const Tensor& A, const Tensor& tau, const Tensor& B, std::size_t M,
+                                         Precision p)
+{
+    EX_TRY_CHECK(check_owned(A, "matmul_q_t: A"));
+    EX_TRY_CHECK(check_owned(tau, "matmul_q_t: tau"));
+    EX_TRY_CHECK(check_owned(B, "matmul_q_t: B"));
+    EX_TRY_CHECK(require_f32(B, "matmul_q_t", "B"));
+    if (p != Precision::F32) return Error{"matmul_q_t: only f32 output is supported by this engine"};
+    const std::size_t K = A.rows(), N = B.cols();
+    if (A.cols() != trit_pack::words_per_row(M))
+        return Error{"matmul_q_t: A " + shape(A) + " does not hold M=" + std::to_string(M) + " columns"};
+    if (B.rows() != K) return Error{"matmul_q_t: B " + shape(B) + " does not match K=" + std::to_string(K)};
+    if (tau.rows() != K || tau.cols() != 1) return Error{"matmul_q_t: tau must be (K,1), got " + shape(tau)};
+    EX_TRY(y, alloc_impl(M, N, Precision::F32));
+    EX_TRY_CHECK(matmul_q_t_impl(A, tau, B, M, *y));
+    return *y;
+}
+
 Result<Tensor> ComputeEngine::add_row_broadcast(const Tensor& y, const Tensor& b)
 {
     EX_TRY_CHECK(check_owned(y, "add_row_broadcast: y"));

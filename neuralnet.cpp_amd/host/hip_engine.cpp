@@ -184,6 +184,21 @@ protected:
         return {};
     }
 
+    Result<void> matmul_q_impl(const Tensor& wq, const Tensor& tau, const Tensor& B, const Tensor& y) override
+    {
+        NNHIP_TRY(nnhip_matmul_q(ctx_->h, up(wq), fp(tau), fp(B), 0, wq.rows(), B.rows(), B.cols(), fpw(y), 0),
+                  "matmul_q");
+        return {};
+    }
+
+    Result<void> matmul_q_t_impl(const Tensor& A, const Tensor& tau, const Tensor& B, std::size_t M,
+                                 const Tensor& y) override
+    {
+        NNHIP_TRY(nnhip_matmul_q_t(ctx_->h, up(A), fp(tau), fp(B), 0, A.rows(), M, B.cols(), fpw(y), 0),
+                  "matmul_q_t");
+        return {};
+    }
+
     Result<void> add_row_broadcast_impl(const Tensor& y, const Tensor& b, const Tensor& out) override
     {
         NNHIP_TRY(nnhip_memcpy_d2d(ctx_->h, TensorAccess::ptr(out), TensorAccess::ptr(y), y.size() * sizeof(float)),

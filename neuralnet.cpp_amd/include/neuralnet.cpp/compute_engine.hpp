@@ -147,6 +147,13 @@ public:
     [[nodiscard]] Result<Tensor> unpack_i8(const Tensor& packed, std::size_t cols);
     [[nodiscard]] Result<Tensor> matmul_q_i8(const Tensor& wq, const Tensor& tau, const Tensor& xq, const Tensor& s,
                                              Precision p = Precision::F32);
+    // Float-activation ternary products (compute_layer_bitlinear.hpp:464 forward, :494 dX):
+    //   matmul_q   Y (N, M) = (tau o trit(wq)) . B,   wq (N, ceil(K/16)), B (K, M), tau (N, 1)
+    //   matmul_q_t Y (M, N) = (tau o trit(A))^T . B,  A (K, ceil(M/16)),  B (K, N), tau (K, 1)
+    [[nodiscard]] Result<Tensor> matmul_q(const Tensor& wq, const Tensor& tau, const Tensor& B,
+                                          Precision p = Precision::F32);
+    [[nodiscard]] Result<Tensor> matmul_q_t(const Tensor& A, const Tensor& tau, const Tensor& B, std::size_t M,
+                                            Precision p = Precision::F32);
     // y + row_broadcast(b)
     [[nodiscard]] Result<Tensor> add_row_broadcast(const Tensor& y, const Tensor& b);
     // RMSNorm forward: (x * rsqrt(mean_f x^2 + eps)) * gamma, per column (token)
@@ -178,6 +185,10 @@ protected:
     [[nodiscard]] virtual Result<void> unpack_i8_impl(const Tensor& packed, std::size_t cols, const Tensor& out) = 0;
     [[nodiscard]] virtual Result<void> matmul_q_i8_impl(const Tensor& wq, const Tensor& tau, const Tensor& xq,
                                                         const Tensor& s, const Tensor& y) = 0;
+    [[nodiscard]] virtual Result<void> matmul_q_impl(const Tensor& wq, const Tensor& tau, const Tensor& B,
+                                                     const Tensor& y) = 0;
+    [[nodiscard]] virtual Result<void> matmul_q_t_impl(const Tensor& A, const Tensor& tau, const Tensor& B,
+                                                       std::size_t M, const Tensor& y) = 0;
     [[nodiscard]] virtual Result<void> add_row_broadcast_impl(const Tensor& y, const Tensor& b, const Tensor& out) = 0;
     [[nodiscard]] virtual Result<void> rmsnorm_impl(const Tensor& x, const Tensor& gamma, Scalar eps,
                                                     const Tensor& out) = 0;

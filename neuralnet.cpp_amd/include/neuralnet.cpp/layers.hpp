@@ -10,9 +10,9 @@
 // absmean tau and the packed ternary container recomputed only when the latent storage's
 // write epoch changed (:100-111, :607-674), and the packed-only deploy state loaded with
 // load_packed_weights (:359-380). forward() runs the int8 branch (set_activation_quant(true),
-// :441-457) through ComputeEngine::bitlinear_i8_forward. Training (backward, STE gradients)
-// and the f32/f16-activation matmul_q branch are outside this engine's scope and fail fast
-// with a Result error, never silently.
+// :441-457) through ComputeEngine::bitlinear_i8_forward; with activation quantization off it
+// runs the f32-activation branch (:459-466) through ComputeEngine::matmul_q. Training
+// (backward, STE gradients) is outside this engine's scope.
 
 #include <cmath>
 #include <cstddef>
@@ -106,7 +106,8 @@ public:
     [[nodiscard]] bool packed_only() const noexcept { return packed_only_; }
     [[nodiscard]] std::size_t in_features() const noexcept { return in_features_; }
     [[nodiscard]] std::size_t out_features() const noexcept { return out_features_; }
-    // activation cache of the int8 branch: packed int8 input (K, ceil(M/4)) and scales (1, M)
+    // activation cache: the int8 branch keeps the packed int8 input (K, ceil(M/4)) and its scales
+    // (1, M); the f32 branch keeps the input itself and no scales
     [[nodiscard]] const Tensor& input_cache() const noexcept { return input_cache_; }
     [[nodiscard]] const Tensor& activation_scales() const noexcept { return act_scale_; }
 
@@ -147,8 +148,13 @@ public:
             return Error{"BitLinear(packed-only): deploy weights / tau missing"};
         if (needs_quantize_()) EX_TRY_CHECK(quantize_weights_());
         if (!act_quant_)
-            return Error{"BitLinear: the f32/f16-activation branch (matmul_q) is not provided by this "
-                         "engine; enable set_activation_quant(true) for the W1.58A8 path"};
+        {
+            // f32-activation branch (:459-466): one ternary x float product, then the bias.
+            input_cache_ = input;
+            act_scale_ = Tensor{};
+            EX_TRY(y, engine.matmul_q(wq_packed_, tau_, input, Precision::F32));
+            return engine.add_row_broadcast(*y, b_);
+        }
         Tensor xq, s;
         EX_TRY(y, engine.bitlinear_i8_forward(input, wq_packed_, tau_, b_, Precision::F32, &xq, &s));
         input_cache_ = xq;

@@ -332,6 +332,49 @@ void orc_add_row_broadcast(float* Y, const float* b, size_t N, size_t M)
         for (size_t m = 0; m < M; ++m) Y[n * M + m] = Y[n * M + m] + b[n];
 }
 
+/* ------------------------------------------------- float-activation GEMM */
+
+/* matmul_q: Y (N, M) = (tau o trit(wq)) . B, accumulated in double and rounded once to float,
+ * the host reference of src/ternary_gemm_test.cpp:141-154 (ref_gemm, transA = 0):
+ * acc += (double)(tau[m] * trit) * (double)B[k][n]. tau * trit is exact (trit in {-1,0,1}). */
+void orc_matmul_q(const uint32_t* wq, const float* tau, const float* B, size_t N, size_t K, size_t M,
+                  float* Y)
+{
+    const size_t wpr = (K + 15) / 16;
+    for (size_t n = 0; n < N; ++n)
+        for (size_t m = 0; m < M; ++m)
+        {
+            double acc = 0.0;
+            for (size_t k = 0; k < K; ++k)
+            {
+                const int code = (int)((wq[n * wpr + k / 16] >> (2 * (k % 16))) & 3u);
+                const float tw = tau[n] * (float)(code - 2);
+                acc += (double)tw * (double)B[k * M + m];
+            }
+            Y[n * M + m] = (float)acc;
+        }
+}
+
+/* matmul_q_t: Y (M, N) = (tau o trit(A))^T . B with A (K, ceil(M/16)) one stored row per k and
+ * tau per stored row, src/ternary_gemm_test.cpp:155-169 (ref_gemm, transA = 1). */
+void orc_matmul_q_t(const uint32_t* A, const float* tau, const float* B, size_t K, size_t M, size_t N,
+                    float* Y)
+{
+    const size_t wpa = (M + 15) / 16;
+    for (size_t m = 0; m < M; ++m)
+        for (size_t n = 0; n < N; ++n)
+        {
+            double acc = 0.0;
+            for (size_t k = 0; k < K; ++k)
+            {
+                const int code = (int)((A[k * wpa + m / 16] >> (2 * (m % 16))) & 3u);
+                const float tw = tau[k] * (float)(code - 2);
+                acc += (double)tw * (double)B[k * N + n];
+            }
+            Y[m * N + n] = (float)acc;
+        }
+}
+
 /* -------------------------------------------------------------- RMSNorm */
 
 /* The per-token sum of squares uses a fixed order shared with every GPU kernel: 512 strided

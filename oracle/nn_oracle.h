@@ -20,6 +20,9 @@
  *                       tie arithmetic (x/s vs x*(1/s)) is parity unpinned
  *   orc_matmul_q_i8*  : brute force in the tests (int64 numpy) + epilogue order
  *                       src/int8_act_test.cpp:210-236
+ *   orc_matmul_q(_t)  : ref_gemm of src/ternary_gemm_test.cpp:141-170 (float64 accumulation);
+ *                       checked against numpy float64 products of the decoded trits and the
+ *                       reference test's own patterns (:253-334)
  *   orc_rmsnorm*      : textbook formula include/neuralnet.cpp/compute_layer_mlp.hpp:615-619,
  *                       checked against a float64 recomputation within tolerance
  *   orc_repack*       : the MI355X tile layout is this build's own format; pinned by
@@ -71,6 +74,10 @@ void orc_matmul_q_i8(const uint32_t* wq, const float* tau, const uint32_t* xq, c
 int orc_matmul_q_i8_rowblock(const uint32_t* wq, const float* tau, const uint32_t* xq,
                              const float* s, size_t N, size_t K, size_t M, float* Y, int threads);
 void orc_add_row_broadcast(float* Y, const float* b, size_t N, size_t M);
+void orc_matmul_q(const uint32_t* wq, const float* tau, const float* B, size_t N, size_t K, size_t M,
+                  float* Y);
+void orc_matmul_q_t(const uint32_t* A, const float* tau, const float* B, size_t K, size_t M, size_t N,
+                    float* Y);
 
 /* ---- RMSNorm and the fused RMSNorm -> absmax -> int8 path ---- */
 void orc_rmsnorm(const float* X, const float* gamma, float eps, size_t F, size_t M, float* out);

@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
             "orc_matmul_q_i8": (None, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p]),
             "orc_matmul_q_i8_rowblock": (ctypes.c_int, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]),
             "orc_add_row_broadcast": (None, [_f32p, _f32p, _sz, _sz]),
+            "orc_matmul_q": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
+            "orc_matmul_q_t": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
             "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
             "orc_rmsnorm_quant_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _u32p, _f32p]),
             "orc_repacked_words": (_sz, [_sz, _sz]),
@@ -183,6 +185,28 @@ def matmul_q_i8_rowblock(wq, tau, xq, s, K: int, M: int, threads: int = 0) -> np
                                         _p(Y, ctypes.c_float), threads)
     if rc != 0:
         raise ValueError("rowblock path is exact only for 127*K < 2^24")
+    return Y
+
+
+def matmul_q(wq: np.ndarray, tau: np.ndarray, B: np.ndarray, K: int) -> np.ndarray:
+    """Y (N, M) = (tau o trit(wq)) . B in float64, rounded once (ref_gemm, transA = 0)."""
+    wq, B = _u32(wq), _f32(B)
+    N, M = wq.shape[0], B.shape[1]
+    tau = _f32(tau).reshape(N)
+    Y = np.empty((N, M), np.float32)
+    lib().orc_matmul_q(_p(wq, ctypes.c_uint32), _p(tau, ctypes.c_float), _p(B, ctypes.c_float), N, K, M,
+                       _p(Y, ctypes.c_float))
+    return Y
+
+
+def matmul_q_t(A: np.ndarray, tau: np.ndarray, B: np.ndarray, M: int) -> np.ndarray:
+    """Y (M, N) = (tau o trit(A))^T . B, A (K, ceil(M/16)) (ref_gemm, transA = 1)."""
+    A, B = _u32(A), _f32(B)
+    K, N = A.shape[0], B.shape[1]
+    tau = _f32(tau).reshape(K)
+    Y = np.empty((M, N), np.float32)
+    lib().orc_matmul_q_t(_p(A, ctypes.c_uint32), _p(tau, ctypes.c_float), _p(B, ctypes.c_float), K, M, N,
+                         _p(Y, ctypes.c_float))
     return Y
 
 

@@ -11,6 +11,8 @@
 //   [8] write-epoch quant cache            AGENTS.md:160-164 / compute_layer_bitlinear.hpp:100-111
 //   [9] deploy state + Model::add          compute_layer_bitlinear.hpp:359-380, model_container.hpp:91-125
 //  [10] engine factory never falls back    cli/cli_engine_factory.hpp:11-13, :60-66
+//  [11] matmul_q / matmul_q_t vs double   src/ternary_gemm_test.cpp [3][4] (:252-333), plus the
+//       BitLinear f32-activation branch     compute_layer_bitlinear.hpp:459-466
 // Exit: 0 pass, 1 fail, 77 skip (no gfx950 device).
 #include <algorithm>
 #include <bit>
@@ -459,6 +461,153 @@ void test_factory()
           "malformed device string -> error");
 }
 
+
+// ---------------------------------------------------------------- [11]
+// Host (tau o trit) product in double; trans = false: W (rows, k) . B; trans = true: the
+// stored (rows = K, k = M) container transposed, tau per stored row.
+nn::Matrix host_float_product(const std::vector<double>& trit, const std::vector<float>& tau, std::size_t rows,
+                              std::size_t k, const nn::Matrix& B, bool trans)
+{
+    const std::size_t n_out = trans ? k : rows, red = trans ? rows : k;
+    nn::Matrix out(n_out, B.cols());
+    for (std::size_t o = 0; o < n_out; ++o)
+        for (std::size_t c = 0; c < B.cols(); ++c)
+        {
+            double acc = 0.0;
+            for (std::size_t r = 0; r < red; ++r)
+            {
+                const std::size_t row = trans ? r : o, col = trans ? o : r;
+                acc += static_cast<double>(tau[row] * static_cast<float>(trit[row * k + col])) *
+                       static_cast<double>(B.at(r, c));
+            }
+            out.set_value(o, c, static_cast<float>(acc));
+        }
+    return out;
+}
+
+double max_abs_diff(const nn::Matrix& a, const nn::Matrix& b)
+{
+    if (a.rows() != b.rows() || a.cols() != b.cols()) return std::numeric_limits<double>::infinity();
+    double mx = 0.0;
+    for (std::size_t i = 0; i < a.size(); ++i)
+        mx = std::max(mx, std::fabs(static_cast<double>(a.span()[i]) - static_cast<double>(b.span()[i])));
+    return mx;
+}
+
+// Packs `W` (rows, k) with per-row tau on the engine and returns the trits it encodes.
+bool pack_on_engine(nn::ComputeEngine& e, const nn::Matrix& W, const std::vector<float>& tau, nn::Tensor& packed,
+                    nn::Tensor& tau_t, std::vector<double>& trit)
+{
+    nn::Matrix tm(W.rows(), 1);
+    for (std::size_t r = 0; r < W.rows(); ++r) tm.set_value(r, 0, tau[r]);
+    tau_t = upload(e, tm);
+    auto pk = e.trit_pack(upload(e, W), tau_t);
+    if (!pk) return false;
+    packed = *pk;
+    trit.assign(W.size(), 0.0);
+    for (std::size_t r = 0; r < W.rows(); ++r)
+        for (std::size_t c = 0; c < W.cols(); ++c)
+            trit[r * W.cols() + c] = nn::trit_pack::value_of(nn::trit_pack::code_of(W.at(r, c), tau[r]));
+    return true;
+}
+
+void test_float_products(nn::ComputeEngine& e)
+{
+    std::puts("[11] matmul_q / matmul_q_t (float activations) vs the double host product");
+    {
+        // the reference's deterministic patterns, K = 40 not a multiple of 16
+        constexpr std::size_t ROWS = 7, K = 40, N = 3;
+        nn::Matrix W(ROWS, K), X(K, N);
+        for (std::size_t r = 0; r < ROWS; ++r)
+            for (std::size_t c = 0; c < K; ++c) W.set_value(r, c, 0.13f * static_cast<float>((r * 7 + c * 3) % 11) - 0.6f);
+        for (std::size_t k = 0; k < K; ++k)
+            for (std::size_t n = 0; n < N; ++n) X.set_value(k, n, 0.21f * static_cast<float>((k + 2 * n) % 9) - 0.8f);
+        std::vector<float> tau(ROWS);
+        for (std::size_t r = 0; r < ROWS; ++r)
+        {
+            double s = 0.0;
+            for (std::size_t c = 0; c < K; ++c) s += std::fabs(static_cast<double>(W.at(r, c)));
+            tau[r] = static_cast<float>(s / static_cast<double>(K));
+        }
+        nn::Tensor pk, tt;
+        std::vector<double> trit;
+        CHECK(pack_on_engine(e, W, tau, pk, tt, trit), "trit_pack (W)");
+        const nn::Tensor Xt = upload(e, X);
+        auto y = e.matmul_q(pk, tt, Xt);
+        CHECK(y.has_value() && max_abs_diff(download(e, *y), host_float_product(trit, tau, ROWS, K, X, false)) < 1e-5,
+              "matmul_q = (tau o trit) . X (1e-5)");
+        // A stored (K, M = ROWS), tau 0.5 per stored row
+        nn::Matrix A(K, ROWS);
+        for (std::size_t k = 0; k < K; ++k)
+            for (std::size_t m = 0; m < ROWS; ++m) A.set_value(k, m, 0.19f * static_cast<float>((k * 5 + m * 3) % 7) - 0.5f);
+        const std::vector<float> tau_k(K, 0.5f);
+        nn::Tensor pa, ta;
+        std::vector<double> trit_a;
+        CHECK(pack_on_engine(e, A, tau_k, pa, ta, trit_a), "trit_pack (A, transposed form)");
+        auto yt = e.matmul_q_t(pa, ta, Xt, ROWS);
+        CHECK(yt.has_value() && yt->rows() == ROWS && yt->cols() == N, "matmul_q_t output shape (M, N)");
+        CHECK(yt.has_value() &&
+                  max_abs_diff(download(e, *yt), host_float_product(trit_a, tau_k, K, ROWS, X, true)) < 1e-5,
+              "matmul_q_t = (tau o trit)^T . X (1e-5)");
+        CHECK(!e.matmul_q_t(pa, ta, Xt, ROWS + 16).has_value(), "matmul_q_t rejects an M the container cannot hold");
+        CHECK(!e.matmul_q(pk, ta, Xt).has_value(), "matmul_q rejects a tau of the wrong length");
+    }
+    {
+        // decode-sized random case, relative tolerance of the reference's cross-shape check
+        constexpr std::size_t ROWS = 300, K = 2560, N = 2;
+        const nn::Matrix W = random_matrix(ROWS, K, 71), X = random_matrix(K, N, 72);
+        std::vector<float> tau(ROWS);
+        for (std::size_t r = 0; r < ROWS; ++r)
+        {
+            double s = 0.0;
+            for (std::size_t c = 0; c < K; ++c) s += std::fabs(static_cast<double>(W.at(r, c)));
+            tau[r] = static_cast<float>(s / static_cast<double>(K));
+        }
+        nn::Tensor pk, tt;
+        std::vector<double> trit;
+        CHECK(pack_on_engine(e, W, tau, pk, tt, trit), "trit_pack (300 x 2560)");
+        auto y = e.matmul_q(pk, tt, upload(e, X));
+        bool ok = y.has_value();
+        if (ok)
+        {
+            const nn::Matrix g = download(e, *y), ref = host_float_product(trit, tau, ROWS, K, X, false);
+            for (std::size_t i = 0; i < ref.size() && ok; ++i)
+                ok = std::fabs(static_cast<double>(g.span()[i]) - static_cast<double>(ref.span()[i])) <=
+                     1e-4 * std::max(1.0, std::fabs(static_cast<double>(ref.span()[i])));
+        }
+        CHECK(ok, "matmul_q 300 x 2560, N=2 within 1e-4 x max(1, |ref|)");
+    }
+    {
+        std::puts("[11] BitLinear f32-activation branch (activation quantization off)");
+        constexpr std::size_t IN = 24, OUT = 9, B = 4;  // IN not a multiple of 16
+        nn::BitLinear bl(IN, OUT);
+        nn::PrecisionProfile prof;
+        prof.param = nn::Precision::T1_58;
+        bl.set_precision_profile(prof);
+        CHECK(bl.init(e).has_value(), "BitLinear init");
+        const nn::Matrix W = random_matrix(OUT, IN, 81), X = random_matrix(IN, B, 82);
+        nn::Matrix bias(OUT, 1);
+        for (std::size_t o = 0; o < OUT; ++o) bias.set_value(o, 0, 0.125f * static_cast<float>(o) - 0.5f);
+        CHECK(e.copy_from(bl.parameters()[0].get(), W).has_value(), "write latent weights");
+        CHECK(e.copy_from(bl.parameters()[1].get(), bias).has_value(), "write bias");
+        bl.set_activation_quant(false);
+        auto y = bl.forward(upload(e, X));
+        CHECK(y.has_value(), "forward (f32 branch)");
+        if (!y) return;
+        const nn::Matrix tau_m = download(e, bl.row_scales());
+        std::vector<float> tau(OUT);
+        for (std::size_t o = 0; o < OUT; ++o) tau[o] = tau_m.at(o, 0);
+        std::vector<double> trit(OUT * IN);
+        for (std::size_t o = 0; o < OUT; ++o)
+            for (std::size_t k = 0; k < IN; ++k)
+                trit[o * IN + k] = nn::trit_pack::value_of(nn::trit_pack::code_of(W.at(o, k), tau[o]));
+        nn::Matrix ref = host_float_product(trit, tau, OUT, IN, X, false);
+        for (std::size_t o = 0; o < OUT; ++o)
+            for (std::size_t b = 0; b < B; ++b) ref.set_value(o, b, ref.at(o, b) + bias.at(o, 0));
+        CHECK(max_abs_diff(download(e, *y), ref) < 1e-5, "forward = (tau o trit) . X + b (1e-5)");
+        CHECK(!bl.activation_scales().valid() && bl.input_cache().rows() == IN, "f32 branch caches the input");
+    }
+}
 }  // namespace
 
 int main()
@@ -486,6 +635,7 @@ int main()
     test_bitlinear_bound(e);
     test_quant_cache(e);
     test_deploy_and_model(e);
+    test_float_products(e);
     if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
     else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
     return g_failures == 0 ? 0 : 1;

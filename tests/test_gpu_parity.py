@@ -1,10 +1,12 @@
 """GPU parity: every libnn-hip.so entry point of the BitLinear W1.58A8 path against the CPU
 oracle on the same seeded inputs, bit for bit (integer containers, int32 accumulators and
 the fp32 epilogue, whose order the kernels keep). Large shapes are checked on sampled rows
-(the oracle runs on the same rows) plus size-independent properties.
+(the oracle runs on the same rows) plus size-independent properties. The float-activation
+GEMM (matmul_q / matmul_q_t), whose accumulation order the reference leaves open, is checked
+against the oracle's float64 evaluation within the reference's own tolerances.
 
-Reference tests mirrored: src/int8_act_test.cpp [1]-[3], src/ternary_gemm_test.cpp [1]-[2],
-src/t1_58_test.cpp [5].
+Reference tests mirrored: src/int8_act_test.cpp [1]-[3], src/ternary_gemm_test.cpp [1]-[4]
+and [6], src/t1_58_test.cpp [5].
 """
 import numpy as np
 import pytest
@@ -326,3 +328,70 @@ def test_invalid_arguments_raise(ctx, nnhip):
     with pytest.raises(nnhip.NNHipError):   # misaligned xi
         bad = torch.zeros(300, dtype=torch.int8, device="cuda")[1:257].view(1, 256)
         ctx.ternary_matmul(rp, f, bad, f, i, 16, 256, 1)
+
+
+# ------------------------------------------------------------------ float-activation GEMM (a10)
+
+GEMM_SHAPES = [(64, 16, 64), (128, 32, 64), (64, 32, 128), (192, 48, 320), (65, 17, 65),
+               (129, 33, 7), (256, 40, 1), (9, 100, 3), (130, 16, 130)]
+
+
+def check_gemm_shape(ctx, orc, M, K, N, trans_a, f16):
+    """src/ternary_gemm_test.cpp:435-526: A latent 0.17*((r*7 + c*3) % 13) - 0.9 stored (M, K)
+    (or (K, M) for transA), tau per stored row absmean, B 0.21*((k + 2n) % 9) - 0.8; the
+    f16 mode rounds B and the reference to f16. Tolerance 1e-4 / 4e-3 x max(1, max|ref|)."""
+    import torch
+    sr, al = (K, M) if trans_a else (M, K)
+    r = np.arange(sr)[:, None]
+    c = np.arange(al)[None, :]
+    A = (np.float32(0.17) * ((r * 7 + c * 3) % 13).astype(np.float32) - np.float32(0.9)).astype(np.float32)
+    tau = np.abs(A.astype(np.float64)).mean(axis=1).astype(np.float32)
+    k = np.arange(K)[:, None]
+    n = np.arange(N)[None, :]
+    B = (np.float32(0.21) * ((k + 2 * n) % 9).astype(np.float32) - np.float32(0.8)).astype(np.float32)
+    if f16:
+        B = B.astype(np.float16).astype(np.float32)
+    packed = ctx.trit_pack(dev(A), dev(tau))
+    assert np.array_equal(host(packed, np.uint32), orc.trit_pack(A, tau))
+    Bd = dev(B).to(torch.float16) if f16 else dev(B)
+    if trans_a:
+        got = ctx.matmul_q_t(packed, dev(tau), Bd, M, out_f16=f16)
+        ref = orc.matmul_q_t(host(packed, np.uint32), tau, B, M)
+    else:
+        got = ctx.matmul_q(packed, dev(tau), Bd, K, out_f16=f16)
+        ref = orc.matmul_q(host(packed, np.uint32), tau, B, K)
+    if f16:
+        ref = ref.astype(np.float16).astype(np.float32)
+    g = got.float().cpu().numpy()
+    assert g.shape == (M, N)
+    scale = max(1.0, float(np.max(np.abs(ref))))
+    err = float(np.max(np.abs(g.astype(np.float64) - ref.astype(np.float64))))
+    assert err <= (4e-3 if f16 else 1e-4) * scale, (M, K, N, trans_a, f16, err)
+
+
+@pytest.mark.parametrize("M,K,N", GEMM_SHAPES)
+@pytest.mark.parametrize("trans_a", [False, True])
+@pytest.mark.parametrize("f16", [False, True])
+def test_matmul_q_shapes(ctx, orc, M, K, N, trans_a, f16):
+    say(f"matmul_q M={M} K={K} N={N} transA={trans_a} f16={f16}")
+    check_gemm_shape(ctx, orc, M, K, N, trans_a, f16)
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 2560, 64), (2560, 2048, 64)])
+@pytest.mark.parametrize("trans_a", [False, True])
+def test_matmul_q_large(ctx, orc, M, K, N, trans_a):
+    say(f"matmul_q large M={M} K={K} N={N} transA={trans_a}")
+    check_gemm_shape(ctx, orc, M, K, N, trans_a, False)
+
+
+def test_matmul_q_decode_gaussian(ctx, orc):
+    """The decode shape of the default BitLinear branch: N(0, 0.02) weights with per-tensor
+    absmean, one f32 token."""
+    N, K = 2560, 6912
+    W = normal((N, K), 21, 0.0, 0.02)
+    tau = np.full(N, np.abs(W.astype(np.float64)).mean(), np.float32)
+    X = normal((K, 1), 22, 0.0, 1.0)
+    wq = ctx.trit_pack(dev(W), dev(tau))
+    got = host(ctx.matmul_q(wq, dev(tau), dev(X), K))
+    ref = orc.matmul_q(host(wq, np.uint32), tau, X, K)
+    assert np.max(np.abs(got - ref)) <= 1e-4 * max(1.0, np.max(np.abs(ref)))

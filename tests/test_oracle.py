@@ -266,3 +266,54 @@ def test_golden_fixtures(orc):
             assert np.array_equal(orc.quantize_i8(g["X"], g["s"], True), g["xq"]), name
             assert np.array_equal(orc.matmul_q_i8_acc(g["wq"], g["xq"], K, M), g["acc"]), name
             assert np.array_equal(orc.matmul_q_i8(g["wq"], g["tau"], g["xq"], g["s"], K, M), g["Y"]), name
+
+
+# ------------------------------------------------------------------ float-activation GEMM (a10)
+
+def _ref_patterns(rows, K, N):
+    """The reference test's generators: W = 0.13*((r*7 + c*3) % 11) - 0.6,
+    X = 0.21*((k + 2n) % 9) - 0.8, tau = per-row absmean (src/ternary_gemm_test.cpp:187-210)."""
+    r = np.arange(rows)[:, None]
+    c = np.arange(K)[None, :]
+    W = (np.float32(0.13) * ((r * 7 + c * 3) % 11).astype(np.float32) - np.float32(0.6)).astype(np.float32)
+    k = np.arange(K)[:, None]
+    n = np.arange(N)[None, :]
+    X = (np.float32(0.21) * ((k + 2 * n) % 9).astype(np.float32) - np.float32(0.8)).astype(np.float32)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    return W, X, tau
+
+
+@pytest.mark.parametrize("rows,K,N", [(7, 40, 3), (65, 17, 65), (9, 100, 3), (256, 40, 1)])
+def test_matmul_q_against_float64(orc, rows, K, N):
+    W, X, tau = _ref_patterns(rows, K, N)
+    wq = orc.trit_pack(W, tau)
+    trits = orc.trits_of(wq, K).astype(np.float64)
+    ref = (tau.astype(np.float64)[:, None] * trits) @ X.astype(np.float64)
+    got = orc.matmul_q(wq, tau, X, K)
+    assert np.max(np.abs(got - ref)) <= 1e-6 * max(1.0, np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("K,M,N", [(40, 7, 3), (17, 65, 65), (33, 129, 7), (100, 9, 1)])
+def test_matmul_q_t_against_float64(orc, K, M, N):
+    # A stored (K, M): tau per stored row k, as the reference's transA form
+    A, _, tau = _ref_patterns(K, M, 1)
+    B = normal((K, N), K * 3 + N, 0.0, 1.0)
+    Aq = orc.trit_pack(A, tau)
+    trits = orc.trits_of(Aq, M).astype(np.float64)          # (K, M)
+    ref = (tau.astype(np.float64)[:, None] * trits).T @ B.astype(np.float64)
+    got = orc.matmul_q_t(Aq, tau, B, M)
+    assert got.shape == (M, N)
+    assert np.max(np.abs(got - ref)) <= 1e-6 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_matmul_q_identity_gives_scaled_trits(orc):
+    """Closed form: B = I makes Y the dequantized weights tau[n] * trit(n, k) exactly."""
+    N, K = 19, 37
+    W = normal((N, K), 11, 0.0, 0.02)
+    tau = orc.row_absmean(W)
+    wq = orc.trit_pack(W, tau)
+    got = orc.matmul_q(wq, tau, np.eye(K, dtype=np.float32), K)
+    assert np.array_equal(got, (tau[:, None] * orc.trits_of(wq, K)).astype(np.float32))
+    # and the transposed form on the same container reads it column-wise
+    got_t = orc.matmul_q_t(wq, tau, np.eye(N, dtype=np.float32), K)
+    assert np.array_equal(got_t, (tau[:, None] * orc.trits_of(wq, K)).astype(np.float32).T)
