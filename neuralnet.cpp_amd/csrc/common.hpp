@@ -36,8 +36,20 @@ constexpr int kGemvMaxM = 16;
 #ifndef NNHIP_GEMV_LDS_DEPTH
 #define NNHIP_GEMV_LDS_DEPTH 3
 #endif
-constexpr int kLdsRTW = 1, kLdsDepth = NNHIP_GEMV_LDS_DEPTH, kLdsWavesPerCu = 16;
-constexpr int kRegRTW = 4, kRegDepth = 4, kRegWavesPerCu = 8;
+#ifndef NNHIP_GEMV_LDS_WAVES
+#define NNHIP_GEMV_LDS_WAVES 16
+#endif
+#ifndef NNHIP_GEMV_REG_RTW
+#define NNHIP_GEMV_REG_RTW 4
+#endif
+#ifndef NNHIP_GEMV_REG_DEPTH
+#define NNHIP_GEMV_REG_DEPTH 4
+#endif
+#ifndef NNHIP_GEMV_REG_WAVES
+#define NNHIP_GEMV_REG_WAVES 8
+#endif
+constexpr int kLdsRTW = 1, kLdsDepth = NNHIP_GEMV_LDS_DEPTH, kLdsWavesPerCu = NNHIP_GEMV_LDS_WAVES;
+constexpr int kRegRTW = NNHIP_GEMV_REG_RTW, kRegDepth = NNHIP_GEMV_REG_DEPTH, kRegWavesPerCu = NNHIP_GEMV_REG_WAVES;
 
 struct GemvVariant
 {
