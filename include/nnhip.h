@@ -243,6 +243,51 @@ nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group);
 /* Number of waves the decode GEMV launches for `items` row tiles (for roofline accounting). */
 size_t nnhip_gemv_grid_waves(nnhip_ctx* ctx, size_t items);
 
+/* ---- gated feed-forward block (the reference FeedForward with a SwiGLU or ReLU2GLU
+ *      activation and BitLinear fc1/fc2, include/neuralnet.cpp/compute_layer_feedforward.hpp:182-204;
+ *      config C4 adds the block's RMSNorm in front) ---- */
+#define NNHIP_ACT_SWIGLU 0   /* (g * (1 / (1 + exp(-g)))) * u   compute_layer_mlp.hpp:317-328 */
+#define NNHIP_ACT_RELU2GLU 1 /* (r * r) * u, r = max(g, 0)      compute_layer_mlp.hpp:405-414 */
+
+/* Gated activation on fc1's output: Y1 (2F, M) with gate rows [0, F) and up rows [F, 2F)
+ * -> h (F, M). exp is this library's fp32 exp (IEEE operations in a fixed order, within 2 ulp).
+ * Replaces SwiGLU::forward / ReLU2GLU::forward (compute_layer_mlp.hpp:317-328, :405-414). */
+nnhip_status nnhip_glu(nnhip_ctx* ctx, const float* Y1, size_t F, size_t M, int act, float* h);
+
+/* Rows of the interleaved gate/up layout: 2 * roundup(F, 8). */
+size_t nnhip_glu_rows(size_t F);
+
+/* Load-time interleave of fc1's fused gate/up container wq (2F, ceil(K/16)) (the reference
+ * fc1 is one BitLinear of 2F rows, compute_layer_feedforward.hpp:54-60) and of its tau / bias
+ * (2F) into the engine-private order: 16-row group t = gate rows 8t..8t+7, then up rows
+ * 8t..8t+7; padding rows (features >= F) get code 2, tau 0, bias 0. Outputs: wq_out
+ * (nnhip_glu_rows(F), ceil(K/16)), tau_out / bias_out (nnhip_glu_rows(F)); bias may be NULL
+ * (then bias_out may be NULL too). Repack wq_out with nnhip_repack_ternary for the kernels. */
+nnhip_status nnhip_glu_interleave(nnhip_ctx* ctx, const uint32_t* wq, const float* tau, const float* bias,
+                                  size_t F, size_t K, uint32_t* wq_out, float* tau_out, float* bias_out);
+
+/* fc1 with the gated activation fused: h (F, M) = act(Y1), Y1 = the interleaved rows of
+ * (tau*s)*float(acc) [+ bias] exactly as nnhip_ternary_matmul computes them (rp, tau, bias in
+ * the interleaved order, N = nnhip_glu_rows(F)). M > 16 applies the activation in the GEMM
+ * epilogue; M <= 16 runs the decode GEMV into context scratch, then the activation. */
+nnhip_status nnhip_ternary_matmul_glu(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                      const float* s, const int32_t* rowsum, const float* bias, size_t F,
+                                      size_t K, size_t M, int act, float* h);
+
+/* Context scratch the block below uses (grown on demand, kept by the context). */
+size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M);
+
+/* The whole W1.58A8 gated block on X (d, M) f32:
+ *   [RMSNorm(gamma, eps) if gamma != NULL] -> absmax int8 -> fc1 (interleaved rp1, tau1, b1)
+ *   -> act -> absmax int8 -> fc2 (rp2 = repack of the (d, ceil(F/16)) container, tau2, b2)
+ *   -> Y (d, M) f32.
+ * Same bits as the reference sequence RMSNorm::forward, BitLinear::forward (int8 branch),
+ * SwiGLU/ReLU2GLU::forward, BitLinear::forward (compute_layer_mlp.hpp:686-707,
+ * compute_layer_bitlinear.hpp:441-457, compute_layer_feedforward.hpp:182-204). b1/b2 may be NULL. */
+nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d,
+                              size_t F, size_t M, int act, const void* rp1, const float* tau1, const float* b1,
+                              const void* rp2, const float* tau2, const float* b2, float* Y);
+
 #ifdef __cplusplus
 }
 #endif

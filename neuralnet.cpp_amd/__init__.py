@@ -95,7 +95,16 @@ SIGNATURES = {
     "nnhip_group_run": (_st, [_vp, _vp]),
     "nnhip_group_destroy": (_st, [_vp, _vp]),
     "nnhip_gemv_grid_waves": (_sz, [_vp, _sz]),
+    "nnhip_glu": (_st, [_vp, _vp, _sz, _sz, ctypes.c_int, _vp]),
+    "nnhip_glu_rows": (_sz, [_sz]),
+    "nnhip_glu_interleave": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
+    "nnhip_ternary_matmul_glu": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_int, _vp]),
+    "nnhip_ffn_glu_workspace_bytes": (_sz, [_sz, _sz, _sz]),
+    "nnhip_ffn_glu_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                               _vp]),
 }
+
+ACT_SWIGLU, ACT_RELU2GLU = 0, 1
 
 _lib = None
 
@@ -128,6 +137,10 @@ def repacked_bytes(N: int, K: int) -> int:
 
 def act_i8_bytes(K: int, M: int) -> int:
     return int(lib().nnhip_act_i8_bytes(K, M))
+
+
+def glu_rows(F: int) -> int:
+    return int(lib().nnhip_glu_rows(F))
 
 
 def kp(K: int) -> int:
@@ -394,6 +407,57 @@ class Context:
                                           self._dev(bias, torch.float32, "bias"), N, K, M,
                                           self._dev(Y, torch.float32, "Y")),
                "nnhip_ternary_matmul")
+        return Y
+
+    # -- gated feed-forward block
+    def glu(self, Y1, act: int = ACT_SWIGLU):
+        """Y1 (2F, M): gate rows then up rows -> h (F, M)."""
+        torch = self._torch
+        F, M = Y1.shape[0] // 2, Y1.shape[1]
+        h = self._empty((F, M), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_glu(self.h, self._dev(Y1, torch.float32, "Y1"), F, M, act, self._dev(h)), "nnhip_glu")
+        return h
+
+    def glu_interleave(self, wq, tau, bias, F: int, K: int):
+        """fc1 container (2F, ceil(K/16)) + tau/bias (2F) -> interleaved (wq, tau, bias)."""
+        torch = self._torch
+        rows = glu_rows(F)
+        wo = self._empty((rows, (K + 15) // 16), torch.int32)
+        to = self._empty((rows,), torch.float32)
+        bo = self._empty((rows,), torch.float32) if bias is not None else None
+        self._bind_stream()
+        _check(lib().nnhip_glu_interleave(self.h, self._dev(wq, torch.int32, "wq"), self._dev(tau, torch.float32, "tau"),
+                                          self._dev(bias, torch.float32, "bias"), F, K, self._dev(wo), self._dev(to),
+                                          self._dev(bo) if bo is not None else None), "nnhip_glu_interleave")
+        return wo, to, bo
+
+    def ternary_matmul_glu(self, rp, tau, xi, s, rowsum, F: int, K: int, M: int, act: int = ACT_SWIGLU,
+                           bias=None, out=None):
+        torch = self._torch
+        h = self._empty((F, M), torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_glu(self.h, self._dev(rp, torch.int32, "rp"),
+                                              self._dev(tau, torch.float32, "tau"), self._dev(xi, torch.int8, "xi"),
+                                              self._dev(s, torch.float32, "s"),
+                                              self._dev(rowsum, torch.int32, "rowsum"),
+                                              self._dev(bias, torch.float32, "bias"), F, K, M, act,
+                                              self._dev(h, torch.float32, "h")), "nnhip_ternary_matmul_glu")
+        return h
+
+    def ffn_glu_i8(self, X, gamma, eps: float, F: int, rp1, tau1, b1, rp2, tau2, b2, act: int = ACT_SWIGLU,
+                   out=None):
+        """Gated FFN block on X (d, M): [RMSNorm] -> int8 -> fc1 (interleaved) -> act -> int8 -> fc2."""
+        torch = self._torch
+        d, M = X.shape
+        Y = self._empty((d, M), torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ffn_glu_i8(self.h, self._dev(X, torch.float32, "X"), self._dev(gamma, torch.float32, "gamma"),
+                                      eps, d, F, M, act, self._dev(rp1, torch.int32, "rp1"),
+                                      self._dev(tau1, torch.float32, "tau1"), self._dev(b1, torch.float32, "b1"),
+                                      self._dev(rp2, torch.int32, "rp2"), self._dev(tau2, torch.float32, "tau2"),
+                                      self._dev(b2, torch.float32, "b2"), self._dev(Y, torch.float32, "Y")),
+               "nnhip_ffn_glu_i8")
         return Y
 
     def group_create(self, problems):

@@ -72,8 +72,47 @@ struct GemvProblem
     float* y;
     int32_t N, K, M, KT;  // KT = Kp / 256
     int32_t xlds;         // byte offset of this problem's activations in LDS, or -1
+    int32_t glu;          // prefill GEMM epilogue: 0 plain Y, else gated activation act = glu - 1
+                          // (0 SwiGLU, 1 ReLU^2-GLU) of interleaved gate/up rows into y (glu_F, M)
+    int32_t glu_F;        // features of the gated output (rows of y when glu != 0)
     int32_t pad_;
 };
+
+// ---- gated activations (shared by k_glu.hip and the GEMM epilogue)
+// exp(x) from IEEE-rounded operations in a fixed order (no fused multiply-add): Cody-Waite
+// reduction x = k ln2 + r with ln2 split as 22713/32768 + fl(ln2 - 22713/32768) (the first
+// product is exact for |k| < 256, the first difference exact by Sterbenz), then the Taylor
+// series of e^r to r^7 (|r| <= 0.347: truncation < 6e-9 relative) and ldexp. x > 100 -> inf,
+// x < -87 -> 0 (no subnormal results), NaN propagates. Within 2 ulp of exp.
+__device__ __forceinline__ float glu_exp(float x)
+{
+    if (x != x) return x;
+    if (x > 100.0f) return __builtin_inff();
+    if (x < -87.0f) return 0.0f;
+    const float k = __builtin_rintf(x * 0x1.715476p+0f);
+    const float r = (x - k * 0x1.62e4p-1f) - k * 0x1.7f7d1cp-20f;
+    float p = 0x1.a01a02p-13f;
+    p = p * r + 0x1.6c16c2p-10f;
+    p = p * r + 0x1.111112p-7f;
+    p = p * r + 0x1.555556p-5f;
+    p = p * r + 0x1.555556p-3f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return __builtin_ldexpf(p, (int)k);
+}
+
+// act 1: ReLU^2-GLU (r * r) * u with r = g > 0 ? g : 0; otherwise SwiGLU (g * (1/(1+exp(-g)))) * u
+__device__ __forceinline__ float glu_one(float g, float u, int act)
+{
+    if (act == 1)
+    {
+        const float r = g > 0.0f ? g : 0.0f;
+        return (r * r) * u;
+    }
+    const float sig = 1.0f / (1.0f + glu_exp(-g));
+    return (g * sig) * u;
+}
 
 // One activation block the decode GEMV stages in LDS at block start (M * Kp bytes).
 struct XStage
@@ -129,5 +168,10 @@ hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const
                                int n_xstage, uint32_t lds_bytes);
 size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds);
 hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus);
+
+// ---- gated activations (k_glu.hip)
+hipError_t launch_glu(hipStream_t st, const float* Y1, size_t F, size_t M, int act, bool interleaved, float* h);
+hipError_t launch_glu_interleave(hipStream_t st, const uint32_t* wq, const float* tau, const float* bias, size_t F,
+                                 size_t K, uint32_t* wq_out, float* tau_out, float* bias_out);
 
 }  // namespace nnhip

@@ -330,6 +330,64 @@ __device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&ac
     }
 }
 
+// Epilogue of the fused gated activation (p.glu != 0). Rows are in the interleaved GLU order
+// (16-row group t = gate rows of features 8t..8t+7, then their up rows), so accumulator element
+// i (row 8*(i/4) + 4h + i%4 of the 32-row block) and element i + 4 (8 rows below) are gate and
+// up of one feature when i/4 is even. Each is rescaled exactly as the plain epilogue does
+// ((tau * s) * float(acc) [+ bias]), then combined by glu_one; h (glu_F, M) gets the result.
+__device__ __forceinline__ void store_glu(const GemvProblem& p, const v16i (&acc)[kRB][kTB], int rb0, int nrb,
+                                          int row_w, int tok_w, int h, int l32)
+{
+    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
+    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
+    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.glu_F * (uint32_t)p.M * 4u);
+    const int act = p.glu - 1;
+    int rs2[kTB];
+    float sv[kTB];
+#pragma unroll
+    for (int n = 0; n < kTB; ++n)
+    {
+        const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
+        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
+        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+    }
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+    {
+        if (rb < rb0 || rb >= rb0 + nrb) continue;
+        const int row0 = row_w + rb * 32 + 4 * h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+        {
+            const int i = (e / 4) * 8 + (e % 4);  // gate element: i / 4 in {0, 2}
+            const uint32_t rg = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3)), ru = rg + 8u;
+            const float tg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, rg * 4u, 0, 0));
+            const float tu = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, ru * 4u, 0, 0));
+            const float bg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, rg * 4u, 0, 0));
+            const float bu = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, ru * 4u, 0, 0));
+            const int f = 8 * (int)(rg / 16u) + (int)(rg % 16u);
+#pragma unroll
+            for (int n = 0; n < kTB; ++n)
+            {
+                const int m = tok_w + n * 32 + l32;
+                float yg = (tg * sv[n]) * (float)(acc[rb][n][i] - rs2[n]);
+                float yu = (tu * sv[n]) * (float)(acc[rb][n][i + 4] - rs2[n]);
+                if (p.bias)
+                {
+                    yg = yg + bg;
+                    yu = yu + bu;
+                }
+                const float y = glu_one(yg, yu, act);
+                const uint32_t off = (f < p.glu_F && m < p.M) ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)m) * 4u
+                                                                : 0xFFFFFFF0u;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
+            }
+        }
+    }
+}
+
 // k split: wave KS of a pair hands the partial sums of the row blocks its partner finishes to
 // the partner through LDS (put_partials), and after a barrier adds the partner's partials of
 // its own row blocks (add_partials).
@@ -479,7 +537,11 @@ k_gemm(GemvProblem p, int n_mblocks, int n_nblocks, int xcd_mode)
     const int row_w = (rt0 + wn * (kWaveRows / 16)) * 16;
     const int tok_w = m0 + wm * kWaveToks;
     const bool full = rt0 * 16 + kBN <= p.N && m0 + kBM <= p.M;
-    if (full)
+    if (p.glu)
+    {
+        store_glu(p, acc, rb0, nrb, row_w, tok_w, h, l32);
+    }
+    else if (full)
     {
         if (p.bias) store_full<true>(p, acc, rb0, nrb, row_w, tok_w, h, l32);
         else store_full<false>(p, acc, rb0, nrb, row_w, tok_w, h, l32);

@@ -120,9 +120,9 @@ nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
 
 nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
                         const int8_t* xi, const float* s, const int32_t* rowsum, const float* bias,
-                        size_t N, size_t K, size_t M, float* Y)
+                        size_t N, size_t K, size_t M, float* Y, int glu = 0, size_t glu_F = 0)
 {
-    GemvProblem p;
+    GemvProblem p{};
     p.rp = static_cast<const u32x4*>(rp);
     p.tau = tau;
     p.xi = xi;
@@ -135,6 +135,8 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     p.M = (int32_t)M;
     p.KT = (int32_t)ceil_div(K, kTileK);
     p.xlds = -1;
+    p.glu = glu;
+    p.glu_F = (int32_t)glu_F;
     if (M <= (size_t)kGemvMaxM)
         NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
     else
@@ -749,6 +751,135 @@ nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group)
 size_t nnhip_gemv_grid_waves(nnhip_ctx* ctx, size_t items)
 {
     return gemv_grid_waves(items, ctx ? ctx->num_cus : 256, true);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------- gated feed-forward block
+
+namespace
+{
+
+// fc1 + gated activation into h (F, M); y1 is scratch of glu_rows(F) x M floats, used only by
+// the decode (GEMV) path, whose epilogue writes the plain interleaved rows first.
+nnhip_status run_matmul_glu(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau, const int8_t* xi,
+                            const float* s, const int32_t* rowsum, const float* bias, size_t F, size_t K, size_t M,
+                            int act, float* y1, float* h)
+{
+    const size_t N = nnhip_glu_rows(F);
+    if (M <= (size_t)kGemvMaxM)
+    {
+        const nnhip_status st = run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, y1);
+        if (st != NNHIP_OK) return st;
+        NNHIP_LAUNCH(fn, launch_glu(ctx->stream, y1, F, M, act, true, h));
+        return NNHIP_OK;
+    }
+    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, h, act + 1, F);
+}
+
+nnhip_status check_glu_args(const char* fn, size_t F, size_t K, size_t M, int act)
+{
+    NNHIP_REQUIRE(act == NNHIP_ACT_SWIGLU || act == NNHIP_ACT_RELU2GLU, fn, "act must be NNHIP_ACT_SWIGLU or NNHIP_ACT_RELU2GLU");
+    NNHIP_REQUIRE(F >= 1 && F <= kMaxDim / 4, fn, "F must be in [1, 2^29)");
+    NNHIP_REQUIRE(mul_ok(F, M) && F * M * 4 < 0x7FFFFFFFull, fn, "gated output must be below 2 GiB");
+    return check_matmul_shape(fn, nnhip_glu_rows(F), K, M);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nnhip_glu_rows(size_t F) { return 2 * round_up(F, 8); }
+
+nnhip_status nnhip_glu(nnhip_ctx* ctx, const float* Y1, size_t F, size_t M, int act, float* h)
+{
+    const char* fn = "nnhip_glu";
+    NNHIP_CHECK_CTX(fn);
+    if (F == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(Y1 && h, fn, "null pointer");
+    NNHIP_REQUIRE(act == NNHIP_ACT_SWIGLU || act == NNHIP_ACT_RELU2GLU, fn, "act must be NNHIP_ACT_SWIGLU or NNHIP_ACT_RELU2GLU");
+    NNHIP_REQUIRE(mul_ok(2 * F, M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_glu(ctx->stream, Y1, F, M, act, false, h));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_glu_interleave(nnhip_ctx* ctx, const uint32_t* wq, const float* tau, const float* bias, size_t F,
+                                  size_t K, uint32_t* wq_out, float* tau_out, float* bias_out)
+{
+    const char* fn = "nnhip_glu_interleave";
+    NNHIP_CHECK_CTX(fn);
+    if (F == 0 || K == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(wq && tau && wq_out && tau_out, fn, "null pointer");
+    NNHIP_REQUIRE(!bias || bias_out, fn, "bias_out is required when bias is given");
+    NNHIP_REQUIRE(F <= kMaxDim / 4 && mul_ok(nnhip_glu_rows(F), ceil_div(K, 16)), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_glu_interleave(ctx->stream, wq, tau, bias, F, K, wq_out, tau_out, bias_out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ternary_matmul_glu(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                      const float* s, const int32_t* rowsum, const float* bias, size_t F, size_t K,
+                                      size_t M, int act, float* h)
+{
+    const char* fn = "nnhip_ternary_matmul_glu";
+    NNHIP_CHECK_CTX(fn);
+    if (F == 0 || M == 0) return NNHIP_OK;
+    nnhip_status st = check_glu_args(fn, F, K, M, act);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && tau && xi && s && rowsum && h, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
+    float* y1 = nullptr;
+    if (M <= (size_t)kGemvMaxM)
+    {
+        st = ensure_ws(ctx, nnhip_glu_rows(F) * M * sizeof(float), fn);
+        if (st != NNHIP_OK) return st;
+        y1 = static_cast<float*>(ctx->ws);
+    }
+    return run_matmul_glu(ctx, fn, rp, tau, xi, s, rowsum, bias, F, K, M, act, y1, h);
+}
+
+size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M)
+{
+    size_t b = round_up(nnhip_act_i8_bytes(d, M), 256) + round_up(nnhip_act_i8_bytes(F, M), 256);
+    b += 4 * round_up(M * 4, 256);                 // s1, rowsum1, s2, rowsum2
+    b += round_up(F * M * 4, 256);                 // h
+    if (M <= (size_t)kGemvMaxM) b += round_up(nnhip_glu_rows(F) * M * 4, 256);  // y1 (decode)
+    return b;
+}
+
+nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
+                              size_t M, int act, const void* rp1, const float* tau1, const float* b1, const void* rp2,
+                              const float* tau2, const float* b2, float* Y)
+{
+    const char* fn = "nnhip_ffn_glu_i8";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0 || d == 0) return NNHIP_OK;
+    nnhip_status st = check_glu_args(fn, F, d, M, act);
+    if (st != NNHIP_OK) return st;
+    st = check_matmul_shape(fn, d, F, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(X && rp1 && tau1 && rp2 && tau2 && Y, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp1) && aligned16(rp2), fn, "rp1 and rp2 must be 16-byte aligned");
+    st = ensure_ws(ctx, nnhip_ffn_glu_workspace_bytes(d, F, M), fn);
+    if (st != NNHIP_OK) return st;
+    uint8_t* p = static_cast<uint8_t*>(ctx->ws);
+    auto take = [&p](size_t bytes) {
+        uint8_t* q = p;
+        p += round_up(bytes, 256);
+        return q;
+    };
+    int8_t* xi1 = reinterpret_cast<int8_t*>(take(nnhip_act_i8_bytes(d, M)));
+    int8_t* xi2 = reinterpret_cast<int8_t*>(take(nnhip_act_i8_bytes(F, M)));
+    float* s1 = reinterpret_cast<float*>(take(M * 4));
+    int32_t* rs1 = reinterpret_cast<int32_t*>(take(M * 4));
+    float* s2 = reinterpret_cast<float*>(take(M * 4));
+    int32_t* rs2 = reinterpret_cast<int32_t*>(take(M * 4));
+    float* h = reinterpret_cast<float*>(take(F * M * 4));
+    float* y1 = M <= (size_t)kGemvMaxM ? reinterpret_cast<float*>(take(nnhip_glu_rows(F) * M * 4)) : nullptr;
+    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, gamma != nullptr, eps, d, M, xi1, s1, rs1, nullptr));
+    st = run_matmul_glu(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, F, d, M, act, y1, h);
+    if (st != NNHIP_OK) return st;
+    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, nullptr, false, 0.0f, F, M, xi2, s2, rs2, nullptr));
+    return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y);
 }
 
 }  // extern "C"

@@ -504,3 +504,130 @@ void orc_unrepack(const uint32_t* rp, size_t N, size_t K, uint32_t* wq)
             wq[n * wpr + wi] = word;
         }
 }
+
+/* ------------------------------------------ gated activations and the FFN block */
+
+/* exp(x) in fp32 built from IEEE-rounded operations only (no fused multiply-add), so a GPU
+ * kernel that performs the same operations in the same order reproduces every bit:
+ *   k = rint(x * fl(1/ln2));  r = (x - k*L1) - k*L2   (L1 = 22713/32768 has 15 significant
+ *   bits, so k*L1 is exact for |k| < 256 and x - k*L1 is exact by Sterbenz; L2 = fl(ln2 - L1));
+ *   e^r by its Taylor series to r^7 in Horner form (|r| <= 0.3466: truncation below 6e-9
+ *   relative, under half an ulp);  result = ldexp(p, k).
+ * x > 100 gives +inf (k would overflow int), x < -87 gives 0 (results below FLT_MIN are
+ * flushed: the gated activations only use exp(-g) inside 1 + exp(-g), where such values
+ * vanish anyway). NaN propagates. Checked against float64 exp to within 2 ulp in the tests. */
+float orc_exp(float x)
+{
+    if (x != x) return x;
+    if (x > 100.0f) return INFINITY;
+    if (x < -87.0f) return 0.0f;
+    const float inv_ln2 = 0x1.715476p+0f;
+    const float ln2_hi = 0x1.62e4p-1f;
+    const float ln2_lo = 0x1.7f7d1cp-20f;
+    const float k = rintf(x * inv_ln2);
+    const float r = (x - k * ln2_hi) - k * ln2_lo;
+    float p = 0x1.a01a02p-13f;  /* 1/7! */
+    p = p * r + 0x1.6c16c2p-10f; /* 1/6! */
+    p = p * r + 0x1.111112p-7f;  /* 1/5! */
+    p = p * r + 0x1.555556p-5f;  /* 1/4! */
+    p = p * r + 0x1.555556p-3f;  /* 1/3! */
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, (int)k);
+}
+
+void orc_exp_array(const float* x, size_t n, float* out)
+{
+    for (size_t i = 0; i < n; ++i) out[i] = orc_exp(x[i]);
+}
+
+/* One gated activation (act 0 = SwiGLU, 1 = ReLU^2-GLU), in the reference's evaluation order:
+ *   SwiGLU   (g * (1 / (1 + exp(-g)))) * u   include/neuralnet.cpp/compute_layer_mlp.hpp:317-328
+ *   ReLU2GLU (r * r) * u, r = g > 0 ? g : 0  include/neuralnet.cpp/compute_layer_mlp.hpp:405-414 */
+float orc_glu_one(float g, float u, int act)
+{
+    if (act == 1)
+    {
+        const float r = g > 0.0f ? g : 0.0f;
+        return (r * r) * u;
+    }
+    const float sig = 1.0f / (1.0f + orc_exp(-g));
+    return (g * sig) * u;
+}
+
+/* in (2F, M): gate = rows [0, F), up = rows [F, 2F) (the SwiGLU/ReLU2GLU row split of the
+ * fused fc1 output, compute_layer_mlp.hpp:323-325); out (F, M). */
+void orc_glu(const float* in, size_t F, size_t M, int act, float* out)
+{
+    for (size_t f = 0; f < F; ++f)
+        for (size_t m = 0; m < M; ++m) out[f * M + m] = orc_glu_one(in[f * M + m], in[(F + f) * M + m], act);
+}
+
+/* Row order of the interleaved ("GLU") layout of a fused gate/up weight (this build's own
+ * format): 16-row group t holds gate rows 8t .. 8t+7, then up rows 8t .. 8t+7, so one
+ * 16-row tile carries both inputs of 8 features. Returns the reference row (in [0, 2F)) of
+ * interleaved row r, or -1 for padding rows (features >= F). Interleaved rows: 2*roundup(F, 8). */
+long orc_glu_src_row(size_t r, size_t F)
+{
+    const size_t t = r / 16, i = r % 16;
+    const size_t f = 8 * t + (i % 8);
+    if (f >= F) return -1;
+    return (long)(i < 8 ? f : F + f);
+}
+
+/* Reference container wq (2F, ceil(K/16)) + tau/bias (2F) -> interleaved container rows
+ * (2*roundup(F,8), ceil(K/16)) and tau/bias in the same order (padding: code 2, tau 0, bias 0). */
+void orc_glu_interleave(const uint32_t* wq, const float* tau, const float* bias, size_t F, size_t K,
+                        uint32_t* wq_out, float* tau_out, float* bias_out)
+{
+    const size_t wpr = orc_trit_words_per_row(K), rows = 2 * ((F + 7) / 8 * 8);
+    for (size_t r = 0; r < rows; ++r)
+    {
+        const long src = orc_glu_src_row(r, F);
+        for (size_t w = 0; w < wpr; ++w) wq_out[r * wpr + w] = src < 0 ? 0xAAAAAAAAu : wq[(size_t)src * wpr + w];
+        tau_out[r] = src < 0 ? 0.0f : tau[src];
+        if (bias_out) bias_out[r] = (src < 0 || !bias) ? 0.0f : bias[src];
+    }
+}
+
+/* BitLinear int8 forward (include/neuralnet.cpp/compute_layer_bitlinear.hpp:441-457) on an
+ * already computed per-token scale: y = (tau * s) * float(acc) [+ b as a separate rounding]. */
+static void orc_bitlinear_i8(const float* x, size_t K, size_t M, const uint32_t* wq, const float* tau,
+                             const float* b, size_t N, int threads, float* y)
+{
+    float* s = (float*)malloc(sizeof(float) * (M ? M : 1));
+    uint32_t* xq = (uint32_t*)malloc(sizeof(uint32_t) * (K * orc_i8_words_per_row(M) + 1));
+    orc_act_scale(x, K, M, s);
+    orc_quantize_i8(x, s, K, M, 1, xq);
+    if (orc_matmul_q_i8_rowblock(wq, tau, xq, s, N, K, M, y, threads) != 0) orc_matmul_q_i8(wq, tau, xq, s, N, K, M, y);
+    if (b) orc_add_row_broadcast(y, b, N, M);
+    free(xq);
+    free(s);
+}
+
+/* The W1.58A8 gated feed-forward block of config C4, as the reference composes it
+ * (FeedForward::forward, include/neuralnet.cpp/compute_layer_feedforward.hpp:182-204, with the
+ * int8 BitLinear forward for fc1 and fc2), preceded by the block's RMSNorm
+ * (compute_layer_mlp.hpp:686-707) when gamma is not NULL:
+ *   x1 = rmsnorm(X, gamma, eps) (d, M);  y1 = fc1(x1) (2F, M);  h = glu(y1) (F, M);
+ *   Y  = fc2(h) (d, M).
+ * wq1 (2F, ceil(d/16)) and wq2 (d, ceil(F/16)) are reference containers; b1/b2 may be NULL.
+ * h_out (F, M) receives the gated activation if not NULL. */
+void orc_ffn_glu_i8(const float* X, const float* gamma, float eps, size_t d, size_t F, size_t M, int act,
+                    const uint32_t* wq1, const float* tau1, const float* b1, const uint32_t* wq2,
+                    const float* tau2, const float* b2, int threads, float* h_out, float* Y)
+{
+    float* x1 = (float*)malloc(sizeof(float) * (d * M + 1));
+    float* y1 = (float*)malloc(sizeof(float) * (2 * F * M + 1));
+    float* h = (float*)malloc(sizeof(float) * (F * M + 1));
+    if (gamma) orc_rmsnorm(X, gamma, eps, d, M, x1);
+    else memcpy(x1, X, sizeof(float) * d * M);
+    orc_bitlinear_i8(x1, d, M, wq1, tau1, b1, 2 * F, threads, y1);
+    orc_glu(y1, F, M, act, h);
+    if (h_out) memcpy(h_out, h, sizeof(float) * F * M);
+    orc_bitlinear_i8(h, F, M, wq2, tau2, b2, d, threads, Y);
+    free(h);
+    free(y1);
+    free(x1);
+}

@@ -27,6 +27,15 @@
  *                       checked against a float64 recomputation within tolerance
  *   orc_repack*       : the MI355X tile layout is this build's own format; pinned by
  *                       the round trip repack -> unrepack == identity
+ *   orc_exp           : this build's own fp32 exp (the reference's exp lives in the absent
+ *                       engine: ulp-level parity with it is unpinned); checked against float64
+ *                       exp to within 2 ulp over a dense sweep and at the range edges
+ *   orc_glu*          : the reference's SwiGLU / ReLU2GLU expressions
+ *                       (compute_layer_mlp.hpp:317-328, :405-414), checked against float64
+ *                       evaluations within tolerance and exact special cases
+ *   orc_ffn_glu_i8    : composition of the pinned pieces above in the order of
+ *                       FeedForward::forward (compute_layer_feedforward.hpp:182-204); checked
+ *                       against a numpy composition (int64 products) in the tests
  */
 #ifndef NN_ORACLE_H
 #define NN_ORACLE_H
@@ -83,6 +92,18 @@ void orc_matmul_q_t(const uint32_t* A, const float* tau, const float* B, size_t 
 void orc_rmsnorm(const float* X, const float* gamma, float eps, size_t F, size_t M, float* out);
 void orc_rmsnorm_quant_i8(const float* X, const float* gamma, float eps, size_t F, size_t M,
                           uint32_t* xq, float* s);
+
+/* ---- gated activations (SwiGLU / ReLU^2-GLU) and the gated FFN block (config C4) ---- */
+float orc_exp(float x);
+void orc_exp_array(const float* x, size_t n, float* out);
+float orc_glu_one(float g, float u, int act);
+void orc_glu(const float* in, size_t F, size_t M, int act, float* out);
+long orc_glu_src_row(size_t r, size_t F);
+void orc_glu_interleave(const uint32_t* wq, const float* tau, const float* bias, size_t F, size_t K,
+                        uint32_t* wq_out, float* tau_out, float* bias_out);
+void orc_ffn_glu_i8(const float* X, const float* gamma, float eps, size_t d, size_t F, size_t M, int act,
+                    const uint32_t* wq1, const float* tau1, const float* b1, const uint32_t* wq2,
+                    const float* tau2, const float* b2, int threads, float* h_out, float* Y);
 
 /* ---- MI355X tile layout of packed ternary weights (checker for the repacker) ---- */
 size_t orc_repacked_words(size_t N, size_t K);

@@ -56,6 +56,14 @@ def lib() -> ctypes.CDLL:
             "orc_matmul_q_t": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
             "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
             "orc_rmsnorm_quant_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _u32p, _f32p]),
+            "orc_exp": (ctypes.c_float, [ctypes.c_float]),
+            "orc_exp_array": (None, [_f32p, _sz, _f32p]),
+            "orc_glu_one": (ctypes.c_float, [ctypes.c_float, ctypes.c_float, ctypes.c_int]),
+            "orc_glu": (None, [_f32p, _sz, _sz, ctypes.c_int, _f32p]),
+            "orc_glu_src_row": (ctypes.c_long, [_sz, _sz]),
+            "orc_glu_interleave": (None, [_u32p, _f32p, _f32p, _sz, _sz, _u32p, _f32p, _f32p]),
+            "orc_ffn_glu_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _sz, ctypes.c_int,
+                                      _u32p, _f32p, _f32p, _u32p, _f32p, _f32p, ctypes.c_int, _f32p, _f32p]),
             "orc_repacked_words": (_sz, [_sz, _sz]),
             "orc_repack": (None, [_u32p, _sz, _sz, _u32p]),
             "orc_unrepack": (None, [_u32p, _sz, _sz, _u32p]),
@@ -236,6 +244,63 @@ def rmsnorm_quant_i8(X: np.ndarray, gamma: np.ndarray, eps: float):
     lib().orc_rmsnorm_quant_i8(_p(X, ctypes.c_float), _p(gamma, ctypes.c_float), eps, F, M,
                                _p(xq, ctypes.c_uint32), _p(s, ctypes.c_float))
     return xq, s
+
+
+ACT_SWIGLU, ACT_RELU2 = 0, 1
+
+
+def exp(x) -> np.ndarray:
+    """Element-wise orc_exp (this build's fp32 exp, identical to the GPU kernels')."""
+    x = _f32(x)
+    out = np.empty(x.shape, np.float32)
+    lib().orc_exp_array(_p(x, ctypes.c_float), x.size, _p(out, ctypes.c_float))
+    return out
+
+
+def glu(Y1: np.ndarray, act: int = ACT_SWIGLU) -> np.ndarray:
+    """(2F, M) fused fc1 output -> (F, M) gated activation (gate rows first, then up)."""
+    Y1 = _f32(Y1)
+    F, M = Y1.shape[0] // 2, Y1.shape[1]
+    out = np.empty((F, M), np.float32)
+    lib().orc_glu(_p(Y1, ctypes.c_float), F, M, act, _p(out, ctypes.c_float))
+    return out
+
+
+def glu_src_rows(F: int) -> np.ndarray:
+    """Reference row of every interleaved row (-1 for padding), length 2*roundup(F, 8)."""
+    rows = 2 * ((F + 7) // 8 * 8)
+    return np.array([lib().orc_glu_src_row(r, F) for r in range(rows)], np.int64)
+
+
+def glu_interleave(wq: np.ndarray, tau: np.ndarray, bias, F: int, K: int):
+    """Fused gate/up container (2F, ceil(K/16)) -> interleaved container, tau and bias."""
+    wq = _u32(wq)
+    tau = _f32(tau).reshape(-1)
+    rows = 2 * ((F + 7) // 8 * 8)
+    wo = np.empty((rows, trit_words_per_row(K)), np.uint32)
+    to = np.empty(rows, np.float32)
+    bo = np.empty(rows, np.float32)
+    bp = _p(_f32(bias).reshape(-1), ctypes.c_float) if bias is not None else None
+    lib().orc_glu_interleave(_p(wq, ctypes.c_uint32), _p(tau, ctypes.c_float), bp, F, K,
+                             _p(wo, ctypes.c_uint32), _p(to, ctypes.c_float), _p(bo, ctypes.c_float))
+    return wo, to, bo
+
+
+def ffn_glu_i8(X, gamma, eps, F, wq1, tau1, b1, wq2, tau2, b2, act: int = ACT_SWIGLU, threads: int = 0):
+    """Config C4 block: [RMSNorm] -> int8 -> fc1 (2F) -> gated activation -> int8 -> fc2.
+    Returns (Y (d, M), h (F, M))."""
+    X = _f32(X)
+    d, M = X.shape
+    Y = np.empty((d, M), np.float32)
+    h = np.empty((F, M), np.float32)
+    fp = lambda a: None if a is None else _p(_f32(a).reshape(-1), ctypes.c_float)
+    keep = [None if a is None else _f32(a).reshape(-1) for a in (gamma, tau1, b1, tau2, b2)]
+    g_, t1, b1_, t2, b2_ = keep
+    wq1, wq2 = _u32(wq1), _u32(wq2)
+    lib().orc_ffn_glu_i8(_p(X, ctypes.c_float), fp(g_), eps, d, F, M, act, _p(wq1, ctypes.c_uint32), fp(t1), fp(b1_),
+                         _p(wq2, ctypes.c_uint32), fp(t2), fp(b2_), threads, _p(h, ctypes.c_float),
+                         _p(Y, ctypes.c_float))
+    return Y, h
 
 
 def repacked_words(N: int, K: int) -> int:

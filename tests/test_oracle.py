@@ -317,3 +317,109 @@ def test_matmul_q_identity_gives_scaled_trits(orc):
     # and the transposed form on the same container reads it column-wise
     got_t = orc.matmul_q_t(wq, tau, np.eye(N, dtype=np.float32), K)
     assert np.array_equal(got_t, (tau[:, None] * orc.trits_of(wq, K)).astype(np.float32).T)
+
+
+# ---------------------------------------------------------------- gated activations, FFN block
+
+def _ulp_dist(a32: np.ndarray, ref64: np.ndarray) -> np.ndarray:
+    """Distance in fp32 ulps between a32 and the float32 rounding of ref64 (finite values)."""
+    r32 = ref64.astype(np.float32)
+    ia = a32.view(np.int32).astype(np.int64)
+    ib = r32.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, np.int64(-2**31) - ia, ia)
+    ib = np.where(ib < 0, np.int64(-2**31) - ib, ib)
+    return np.abs(ia - ib)
+
+
+def test_exp_within_2ulp_of_float64(orc):
+    x = np.linspace(-87.0, 88.72, 2_000_003, dtype=np.float32)
+    x = np.concatenate([x, uniform((200_000,), 5, -1.0, 1.0), uniform((50_000,), 6, -1e-4, 1e-4)])
+    e = orc.exp(x)
+    ref = np.exp(x.astype(np.float64))
+    assert _ulp_dist(e, ref).max() <= 2
+    # exact points and the documented edges
+    assert orc.exp(np.float32([0.0]))[0] == 1.0
+    assert orc.exp(np.float32([-0.0]))[0] == 1.0
+    assert np.isinf(orc.exp(np.float32([88.73, 100.0, 1e30, np.inf]))).all()
+    assert (orc.exp(np.float32([-87.01, -100.0, -1e30, -np.inf])) == 0.0).all()
+    assert np.isnan(orc.exp(np.float32([np.nan])))[0]
+    # e^88.72 is still finite (FLT_MAX = e^88.7228...)
+    assert np.isfinite(orc.exp(np.float32([88.72])))[0]
+
+
+def test_swiglu_close_to_float64(orc):
+    F, M = 300, 7
+    Y1 = normal((2 * F, M), 21, 0.0, 4.0)
+    h = orc.glu(Y1, orc.ACT_SWIGLU)
+    g = Y1[:F].astype(np.float64)
+    u = Y1[F:].astype(np.float64)
+    ref = g / (1.0 + np.exp(-g)) * u
+    assert np.max(np.abs(h - ref) / np.maximum(np.abs(ref), 1e-30)) < 4e-7
+
+
+def test_glu_special_cases(orc):
+    one = lambda g, u, a: orc.lib().orc_glu_one(g, u, a)
+    # SwiGLU: silu(0) = 0, silu(g) -> g for large g, -> -0 for very negative g
+    assert one(0.0, 5.0, 0) == 0.0
+    assert one(200.0, 1.5, 0) == 300.0
+    assert one(-200.0, 1.0, 0) == 0.0
+    assert math.isnan(one(float("nan"), 1.0, 0))
+    assert math.isnan(one(float("-inf"), 1.0, 0))  # -inf * sigma(-inf) = -inf * 0
+    # ReLU^2-GLU: (max(g,0))^2 * u, NaN gate -> 0 (the select), exact on representable values
+    assert one(3.0, 2.0, 1) == 18.0
+    assert one(-3.0, 2.0, 1) == 0.0
+    assert one(float("nan"), 2.0, 1) == 0.0
+    g = normal((1000,), 22, 0.0, 3.0)
+    u = normal((1000,), 23, 0.0, 3.0)
+    Y1 = np.concatenate([g[None, :], u[None, :]])
+    r = np.maximum(g.astype(np.float64), 0.0)
+    ref = r * r * u.astype(np.float64)
+    out = orc.glu(Y1, orc.ACT_RELU2)[0]
+    assert np.max(np.abs(out - ref) / np.maximum(np.abs(ref), 1e-30)) < 2.5e-7
+
+
+def test_glu_interleave_rows(orc):
+    F = 12
+    src = orc.glu_src_rows(F)
+    assert len(src) == 32
+    assert list(src[:16]) == list(range(0, 8)) + list(range(12, 20))
+    assert list(src[16:]) == [8, 9, 10, 11, -1, -1, -1, -1, 20, 21, 22, 23, -1, -1, -1, -1]
+    K = 40
+    W = normal((2 * F, K), 24)
+    tau = orc.row_absmean(W)
+    wq = orc.trit_pack(W, tau)
+    b = normal((2 * F,), 25)
+    wo, to, bo = orc.glu_interleave(wq, tau, b, F, K)
+    for r, s in enumerate(src):
+        if s < 0:
+            assert (orc.trits_of(wo[r:r + 1], K) == 0).all() and to[r] == 0 and bo[r] == 0
+        else:
+            assert np.array_equal(wo[r], wq[s]) and to[r] == tau[s] and bo[r] == b[s]
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_ffn_block_is_the_composition(orc, act):
+    d, F, M = 96, 40, 5
+    X = normal((d, M), 31)
+    gamma = normal((d,), 32, 1.0, 0.1)
+    W1 = normal((2 * F, d), 33, 0.0, 0.02)
+    W2 = normal((d, F), 34, 0.0, 0.02)
+    t1, t2 = orc.row_absmean(W1), orc.row_absmean(W2)
+    wq1, wq2 = orc.trit_pack(W1, t1), orc.trit_pack(W2, t2)
+    b1, b2 = normal((2 * F,), 35, 0.0, 0.1), normal((d,), 36, 0.0, 0.1)
+    Y, h = orc.ffn_glu_i8(X, gamma, 1e-6, F, wq1, t1, b1, wq2, t2, b2, act)
+
+    def bitlinear(x, wq, tau, b, K):
+        s = orc.act_scale(x)
+        q = orc.container_to_int8(orc.quantize_i8(x, s, True), x.shape[1]).astype(np.int64)
+        acc = orc.trits_of(wq, K).astype(np.int64) @ q
+        return (tau[:, None] * s[None, :]) * acc.astype(np.float32) + b[:, None]
+
+    x1 = orc.rmsnorm(X, gamma, 1e-6)
+    y1 = bitlinear(x1, wq1, t1, b1, d)
+    h_ref = orc.glu(y1, act)
+    assert np.array_equal(h, h_ref)
+    assert np.array_equal(Y, bitlinear(h_ref, wq2, t2, b2, F))
+    # no norm: gamma None feeds X straight to fc1's quantizer
+    Y0, _ = orc.ffn_glu_i8(X, None, 0.0, F, wq1, t1, b1, wq2, t2, b2, act)
+    assert np.array_equal(Y0, bitlinear(orc.glu(bitlinear(X, wq1, t1, b1, d), act), wq2, t2, b2, F))
