@@ -206,6 +206,85 @@ def act_quant_lines(ctx, torch, stream, steps, out):
     out["act_quant"] = res
 
 
+def ffn_block_line(ctx, torch, stream, steps, out):
+    """Config C4: RMSNorm(eps=1e-6, gamma=1) -> absmax int8 -> fc1 (d -> 2F, gate/up) ->
+    SwiGLU -> absmax int8 -> fc2 (F -> d) on 2048 tokens, d=2560, F=6912, one
+    nnhip_ffn_glu_i8 call per step; also each step timed alone. Ops = 2*M*(2F*d + d*F)."""
+    d, F, M = D, FFN, 2048
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xB17A0007)
+    W1 = torch.randn((2 * F, d), generator=gen, device="cuda") * 0.02
+    W2 = torch.randn((d, F), generator=gen, device="cuda") * 0.02
+    t1, t2 = ctx.row_absmean(W1), ctx.row_absmean(W2)
+    wq1, wq2 = ctx.trit_pack(W1, t1), ctx.trit_pack(W2, t2)
+    del W1, W2
+    wo, to, _ = ctx.glu_interleave(wq1, t1, None, F, d)
+    rp1, rp2 = ctx.repack(wo, d), ctx.repack(wq2, F)
+    X = torch.randn((d, M), generator=gen, device="cuda")
+    g = torch.ones(d, device="cuda")
+    Y = torch.empty((d, M), device="cuda")
+    ops = 2.0 * M * (2 * F * d + d * F)
+    n = max(10, steps // 2)
+    t, _ = time_launches(torch, stream, lambda: ctx.ffn_glu_i8(X, g, 1e-6, F, rp1, to, None, rp2, t2, None, out=Y), n, 5)
+    # the steps alone (same kernels the block runs)
+    a1 = ctx._act_out(d, M)
+    a2 = ctx._act_out(F, M)
+    h = torch.empty((F, M), device="cuda")
+    ctx.rmsnorm_quant_i8(X, g, 1e-6, outs=a1)
+    ctx.ternary_matmul_glu(rp1, to, *a1, F, d, M, out=h)
+    ctx.act_quant_i8(h, outs=a2)
+    parts = {
+        "rmsnorm_quant 2560x2048": (lambda: ctx.rmsnorm_quant_i8(X, g, 1e-6, outs=a1), None),
+        "fc1+SwiGLU 13824x2560x2048": (lambda: ctx.ternary_matmul_glu(rp1, to, *a1, F, d, M, out=h),
+                                       2.0 * M * 2 * F * d),
+        "act_quant 6912x2048": (lambda: ctx.act_quant_i8(h, outs=a2), None),
+        "fc2 2560x6912x2048": (lambda: ctx.ternary_matmul(rp2, t2, *a2, d, F, M, out=Y), 2.0 * M * d * F),
+    }
+    res_parts = {}
+    for name, (fn, pops) in parts.items():
+        tp, _ = time_launches(torch, stream, fn, n, 5)
+        res_parts[name] = {"us": round(tp * 1e6, 2)}
+        if pops:
+            res_parts[name]["TOPS"] = round(pops / tp / 1e12, 1)
+    out["ffn_block_c4"] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
+                           "frac_int8_mfma": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4), "ops": ops,
+                           "parts": res_parts}
+    log(f"C4 block: {t * 1e6:.1f} us, {ops / t / 1e12:.1f} TOPS; parts {res_parts}")
+
+
+def matmul_q_lines(ctx, torch, stream, steps, out):
+    """Float-activation ternary products on the reference container (the reference's default
+    BitLinear branch and its dX product), per BitNet-2B shape at M (tokens) in {1, 16}, f32 in
+    and out. GB/s of algorithmic bytes: packed weights N*ceil(K/16)*4 + 4*K*M (B) + 4*N (tau)
+    + 4*N*M (Y); matmul_q_t reads the same container for the transposed product."""
+    res = {}
+    n = max(10, steps // 2)
+    for name, K, N in (("q 2560->2560", D, D), ("gate 2560->6912", D, FFN), ("down 6912->2560", FFN, D)):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0xB17A0008 + K + N)
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        tau = ctx.row_absmean(W)
+        wq = ctx.trit_pack(W, tau)
+        del W
+        wbytes = N * ((K + 15) // 16) * 4
+        for M in (1, 16):
+            B = torch.randn((K, M), generator=gen, device="cuda")
+            Y = torch.empty((N, M), device="cuda")
+            t, _ = time_launches(torch, stream, lambda: ctx.matmul_q(wq, tau, B, K, out=Y), n, 5)
+            nb = wbytes + 4 * K * M + 4 * N + 4 * N * M
+            res[f"matmul_q {name} M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                              "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+            # dX: (tau o A)^T . dY with A = the same (N, ceil(K/16)) container read transposed
+            dY = torch.randn((N, M), generator=gen, device="cuda")
+            dX = torch.empty((K, M), device="cuda")
+            t, _ = time_launches(torch, stream, lambda: ctx.matmul_q_t(wq, tau, dY, K, out=dX), n, 5)
+            nb = wbytes + 4 * N * M + 4 * N + 4 * K * M
+            res[f"matmul_q_t {name} M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                                "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+    out["matmul_q"] = res
+    log(f"matmul_q: {res}")
+
+
 def profiled_traffic():
     """Calibrated HBM bytes per headline launch from the committed PMC summary, or None."""
     import re
@@ -312,8 +391,10 @@ def main():
     if not args.no_extra:
         extra_gemv_lines(ctx, torch, stream, weights, acts1, extra)
         act_quant_lines(ctx, torch, stream, args.steps, extra)
+        matmul_q_lines(ctx, torch, stream, args.steps, extra)
     if not args.no_gemm:
         gemm_lines(ctx, torch, stream, args.steps, extra)
+        ffn_block_line(ctx, torch, stream, args.steps, extra)
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline (about 12 s)")

@@ -279,13 +279,17 @@ class Context:
                "nnhip_matmul_q_i8")
         return Y
 
-    def matmul_q(self, wq, tau, B, K: int, out_f16: bool = False):
+    def matmul_q(self, wq, tau, B, K: int, out_f16: bool = False, out=None):
         """Y (N, M) = (tau o trit(wq)) . B; B f32 or f16 (K, M); Y f32, or f16 if out_f16."""
         torch = self._torch
         N, M = wq.shape[0], B.shape[1]
         if B.shape[0] != K:
             raise NNHipError(1, f"B has {B.shape[0]} rows, expected K={K}")
-        Y = self._empty((N, M), torch.float16 if out_f16 else torch.float32)
+        ydt = torch.float16 if out_f16 else torch.float32
+        Y = self._empty((N, M), ydt) if out is None else out
+        self._dev(Y, ydt, "out")
+        if tuple(Y.shape) != (N, M):
+            raise NNHipError(1, f"out has shape {tuple(Y.shape)}, expected {(N, M)}")
         self._bind_stream()
         _check(lib().nnhip_matmul_q(self.h, self._dev(wq, torch.int32, "wq"), self._dev(tau, torch.float32, "tau"),
                                     self._dev(B, (torch.float32, torch.float16), "B"),
@@ -293,13 +297,17 @@ class Context:
                                     1 if out_f16 else 0), "nnhip_matmul_q")
         return Y
 
-    def matmul_q_t(self, A, tau, B, M: int, out_f16: bool = False):
+    def matmul_q_t(self, A, tau, B, M: int, out_f16: bool = False, out=None):
         """Y (M, N) = (tau o trit(A))^T . B, A (K, ceil(M/16)) packed with tau per stored row."""
         torch = self._torch
         K, N = A.shape[0], B.shape[1]
         if B.shape[0] != K:
             raise NNHipError(1, f"B has {B.shape[0]} rows, expected K={K}")
-        Y = self._empty((M, N), torch.float16 if out_f16 else torch.float32)
+        ydt = torch.float16 if out_f16 else torch.float32
+        Y = self._empty((M, N), ydt) if out is None else out
+        self._dev(Y, ydt, "out")
+        if tuple(Y.shape) != (M, N):
+            raise NNHipError(1, f"out has shape {tuple(Y.shape)}, expected {(M, N)}")
         self._bind_stream()
         _check(lib().nnhip_matmul_q_t(self.h, self._dev(A, torch.int32, "A"), self._dev(tau, torch.float32, "tau"),
                                       self._dev(B, (torch.float32, torch.float16), "B"),

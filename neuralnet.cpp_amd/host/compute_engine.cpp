@@ -282,4 +282,52 @@ Result<Tensor> ComputeEngine::bitlinear_i8_impl(const Tensor& x, const Tensor& w
     return add_row_broadcast(*y, b);
 }
 
+Result<Tensor> ComputeEngine::glu(const Tensor& y1, int act)
+{
+    EX_TRY_CHECK(check_owned(y1, "glu"));
+    EX_TRY_CHECK(require_f32(y1, "glu", "y1"));
+    if (act != 0 && act != 1) return Error{"glu: act must be 0 (SwiGLU) or 1 (ReLU2GLU)"};
+    if (y1.rows() % 2 != 0) return Error{"glu: input rows must be 2*d_ff, got " + shape(y1)};
+    EX_TRY(out, alloc_impl(y1.rows() / 2, y1.cols(), Precision::F32));
+    EX_TRY_CHECK(glu_impl(y1, act, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::ffn_glu_i8_forward(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
+                                                 const Tensor& tau1, const Tensor& b1, const Tensor& wq2,
+                                                 const Tensor& tau2, const Tensor& b2, int act)
+{
+    const char* fn = "ffn_glu_i8_forward";
+    for (const Tensor* t : {&x, &wq1, &tau1, &b1, &wq2, &tau2, &b2}) EX_TRY_CHECK(check_owned(*t, fn));
+    if (gamma) EX_TRY_CHECK(check_owned(*gamma, fn));
+    if (act != 0 && act != 1) return Error{"ffn_glu_i8_forward: act must be 0 (SwiGLU) or 1 (ReLU2GLU)"};
+    const std::size_t d = x.rows(), F2 = wq1.rows();
+    if (F2 % 2 != 0 || F2 == 0) return Error{"ffn_glu_i8_forward: fc1 must have 2*d_ff rows, got " + shape(wq1)};
+    const std::size_t F = F2 / 2;
+    if (wq1.cols() != trit_pack::words_per_row(d))
+        return Error{"ffn_glu_i8_forward: fc1 " + shape(wq1) + " does not match d_model " + std::to_string(d)};
+    if (wq2.rows() != d || wq2.cols() != trit_pack::words_per_row(F))
+        return Error{"ffn_glu_i8_forward: fc2 " + shape(wq2) + " does not match (d_model, ceil(d_ff/16))"};
+    if (tau1.rows() != F2 || b1.rows() != F2 || tau2.rows() != d || b2.rows() != d)
+        return Error{"ffn_glu_i8_forward: tau / bias rows do not match the weights"};
+    if (gamma && gamma->rows() != d) return Error{"ffn_glu_i8_forward: gamma must be (d_model, 1)"};
+    return ffn_glu_i8_impl(x, gamma, eps, wq1, tau1, b1, wq2, tau2, b2, act);
+}
+
+// Default composition in the reference layer order (compute_layer_feedforward.hpp:182-204).
+Result<Tensor> ComputeEngine::ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
+                                              const Tensor& tau1, const Tensor& b1, const Tensor& wq2,
+                                              const Tensor& tau2, const Tensor& b2, int act)
+{
+    Tensor in = x;
+    if (gamma)
+    {
+        EX_TRY(n, rmsnorm(x, *gamma, eps));
+        in = *n;
+    }
+    EX_TRY(y1, bitlinear_i8_forward(in, wq1, tau1, b1, Precision::F32, nullptr, nullptr));
+    EX_TRY(h, glu(*y1, act));
+    return bitlinear_i8_forward(*h, wq2, tau2, b2, Precision::F32, nullptr, nullptr);
+}
+
 }  // namespace nn

@@ -131,16 +131,77 @@ protected:
         return {};
     }
 
+    // Engine-private copies derived from a weight container, kept on its storage: the T16K256
+    // repack (valid for the storage's write epoch) and, for a fused gate/up container, the
+    // interleaved repack with tau / bias in the same row order (valid for the epochs of the
+    // container, tau and bias it was made from).
+    struct WeightCache
+    {
+        std::shared_ptr<void> rp;
+        std::uint64_t rp_epoch = ~std::uint64_t{0};
+        std::shared_ptr<void> glu_rp, glu_tau, glu_bias;
+        std::uint64_t glu_epoch = ~std::uint64_t{0}, glu_tau_epoch = 0, glu_bias_epoch = 0;
+        const detail::Storage* glu_tau_st = nullptr;
+        const detail::Storage* glu_bias_st = nullptr;
+    };
+
+    static WeightCache& cache_of(const Tensor& wq)
+    {
+        detail::Storage* st = TensorAccess::storage(wq);
+        if (!st->derived) st->derived = std::make_shared<WeightCache>();
+        return *static_cast<WeightCache*>(st->derived.get());
+    }
+
     // T16K256 copy of a weight container, cached on its storage for the current write epoch.
     Result<const void*> repacked(const Tensor& wq, std::size_t K)
     {
-        detail::Storage* st = TensorAccess::storage(wq);
-        if (st->derived && st->derived_epoch == st->write_epoch) return static_cast<const void*>(st->derived.get());
+        WeightCache& c = cache_of(wq);
+        if (c.rp && c.rp_epoch == wq.write_epoch()) return static_cast<const void*>(c.rp.get());
         EX_TRY(mem, device_alloc(nnhip_repacked_bytes(wq.rows(), K)));
         NNHIP_TRY(nnhip_repack_ternary(ctx_->h, up(wq), wq.rows(), K, mem->get()), "repack");
-        st->derived = *mem;
-        st->derived_epoch = st->write_epoch;
-        return static_cast<const void*>(st->derived.get());
+        c.rp = *mem;
+        c.rp_epoch = wq.write_epoch();
+        return static_cast<const void*>(c.rp.get());
+    }
+
+    struct GluWeights
+    {
+        const void* rp;
+        const float* tau;
+        const float* bias;
+    };
+
+    // Interleaved gate/up repack of fc1 (2F rows) plus tau / bias in that order.
+    Result<GluWeights> glu_weights(const Tensor& wq1, const Tensor& tau1, const Tensor& b1, std::size_t F,
+                                   std::size_t K)
+    {
+        WeightCache& c = cache_of(wq1);
+        const detail::Storage* ts = TensorAccess::storage(tau1);
+        const detail::Storage* bs = TensorAccess::storage(b1);
+        if (!(c.glu_rp && c.glu_epoch == wq1.write_epoch() && c.glu_tau_st == ts &&
+              c.glu_tau_epoch == tau1.write_epoch() && c.glu_bias_st == bs && c.glu_bias_epoch == b1.write_epoch()))
+        {
+            const std::size_t rows = nnhip_glu_rows(F);
+            EX_TRY(words, device_alloc(rows * trit_pack::words_per_row(K) * sizeof(uint32_t)));
+            EX_TRY(rp, device_alloc(nnhip_repacked_bytes(rows, K)));
+            EX_TRY(t, device_alloc(rows * sizeof(float)));
+            EX_TRY(b, device_alloc(rows * sizeof(float)));
+            NNHIP_TRY(nnhip_glu_interleave(ctx_->h, up(wq1), fp(tau1), fp(b1), F, K, static_cast<uint32_t*>(words->get()),
+                                           static_cast<float*>(t->get()), static_cast<float*>(b->get())),
+                      "ffn (gate/up interleave)");
+            NNHIP_TRY(nnhip_repack_ternary(ctx_->h, static_cast<const uint32_t*>(words->get()), rows, K, rp->get()),
+                      "ffn (repack)");
+            c.glu_rp = *rp;
+            c.glu_tau = *t;
+            c.glu_bias = *b;
+            c.glu_epoch = wq1.write_epoch();
+            c.glu_tau_st = ts;
+            c.glu_tau_epoch = tau1.write_epoch();
+            c.glu_bias_st = bs;
+            c.glu_bias_epoch = b1.write_epoch();
+        }
+        return GluWeights{c.glu_rp.get(), static_cast<const float*>(c.glu_tau.get()),
+                          static_cast<const float*>(c.glu_bias.get())};
     }
 
     // Token-major int8 activations + row sums, reused across calls (all work of one engine
@@ -236,6 +297,29 @@ protected:
                   "bitlinear_i8_forward (ternary product)");
         if (xq_out) *xq_out = xq;
         if (s_out) *s_out = *s;
+        return *y;
+    }
+
+    Result<void> glu_impl(const Tensor& y1, int act, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_glu(ctx_->h, fp(y1), y1.rows() / 2, y1.cols(), act, fpw(out)), "glu");
+        return {};
+    }
+
+    // The whole block in one library call: [RMSNorm ->] int8 -> fc1 with the gated activation in
+    // its epilogue -> int8 -> fc2 (nnhip_ffn_glu_i8), on cached interleaved / repacked weights.
+    Result<Tensor> ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
+                                   const Tensor& tau1, const Tensor& b1, const Tensor& wq2, const Tensor& tau2,
+                                   const Tensor& b2, int act) override
+    {
+        const std::size_t d = x.rows(), M = x.cols(), F = wq1.rows() / 2;
+        EX_TRY(y, alloc_impl(d, M, Precision::F32));
+        if (M == 0) return *y;
+        EX_TRY(g1, glu_weights(wq1, tau1, b1, F, d));
+        EX_TRY(rp2, repacked(wq2, F));
+        NNHIP_TRY(nnhip_ffn_glu_i8(ctx_->h, fp(x), gamma ? fp(*gamma) : nullptr, eps, d, F, M, act, g1->rp, g1->tau,
+                                   g1->bias, *rp2, fp(tau2), fp(b2), fpw(*y)),
+                  "ffn_glu_i8_forward");
         return *y;
     }
 

@@ -69,10 +69,9 @@ struct Storage
     std::size_t bytes = 0;
     const ComputeEngine* owner = nullptr;
     std::uint64_t write_epoch = 0;
-    // Engine-private data derived from the contents (e.g. repacked weights), valid while
-    // write_epoch == derived_epoch.
+    // Engine-private data derived from the contents (e.g. repacked weights); the engine records
+    // the write epoch each derived piece was made from and remakes it when the epoch moved on.
     std::shared_ptr<void> derived;
-    std::uint64_t derived_epoch = ~std::uint64_t{0};
 };
 }  // namespace detail
 
@@ -166,6 +165,19 @@ public:
     [[nodiscard]] Result<Tensor> bitlinear_i8_forward(const Tensor& x, const Tensor& wq, const Tensor& tau,
                                                       const Tensor& b, Precision p, Tensor* xq_out, Tensor* s_out);
 
+    // Gated activation on a fused fc1 output y1 (2F, M): gate rows [0, F), up rows [F, 2F) ->
+    // (F, M). act 0: SwiGLU (g * (1 / (1 + exp(-g)))) * u (compute_layer_mlp.hpp:317-328);
+    // act 1: ReLU^2-GLU (r * r) * u, r = max(g, 0) (:405-414).
+    [[nodiscard]] Result<Tensor> glu(const Tensor& y1, int act);
+
+    // Gated feed-forward block in the int8 branch (FeedForward::forward,
+    // compute_layer_feedforward.hpp:182-204): [RMSNorm(gamma, eps) if gamma] -> fc1 (BitLinear
+    // int8, 2F rows: gate then up) -> glu -> fc2 (BitLinear int8). The default implementation
+    // composes rmsnorm / bitlinear_i8_forward / glu; an engine may fuse them (same bits).
+    [[nodiscard]] Result<Tensor> ffn_glu_i8_forward(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
+                                                    const Tensor& tau1, const Tensor& b1, const Tensor& wq2,
+                                                    const Tensor& tau2, const Tensor& b2, int act);
+
     [[nodiscard]] EngineInfo describe() const { return describe_impl(); }
     void begin_batch() {}
     void end_batch() { sync_impl(); }
@@ -194,6 +206,11 @@ protected:
                                                     const Tensor& out) = 0;
     [[nodiscard]] virtual Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau,
                                                            const Tensor& b, Tensor* xq_out, Tensor* s_out);
+    [[nodiscard]] virtual Result<void> glu_impl(const Tensor& y1, int act, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<Tensor> ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps,
+                                                         const Tensor& wq1, const Tensor& tau1, const Tensor& b1,
+                                                         const Tensor& wq2, const Tensor& tau2, const Tensor& b2,
+                                                         int act);
     [[nodiscard]] virtual EngineInfo describe_impl() const = 0;
     virtual void sync_impl() = 0;
 

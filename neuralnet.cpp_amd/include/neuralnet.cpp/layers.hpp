@@ -1,10 +1,12 @@
 #pragma once
-// layers.hpp — nn::Layer, nn::BitLinear and nn::RMSNorm: the layer side of the W1.58A8 path.
+// layers.hpp — nn::Layer, nn::BitLinear, nn::FeedForward and nn::RMSNorm: the layer side of
+// the W1.58A8 path.
 //
 // Mirrors the reference classes' public surface and semantics for the inference path:
 //   Layer      include/neuralnet.cpp/compute_layer_base.hpp:261-363 (init -> init_impl NVI,
 //              precision profile fixed at init, forward)
 //   BitLinear  include/neuralnet.cpp/compute_layer_bitlinear.hpp:46-675
+//   FeedForward include/neuralnet.cpp/compute_layer_feedforward.hpp:22-204 (gated activations)
 //   RMSNorm    include/neuralnet.cpp/compute_layer_mlp.hpp:627-707
 // BitLinear keeps the reference's weight-side state machine: f32 latent weights, per-row
 // absmean tau and the packed ternary container recomputed only when the latent storage's
@@ -212,6 +214,104 @@ private:
     std::uint64_t quant_epoch_ = 0;
     bool quant_valid_ = false;
     std::uint64_t quantize_calls_ = 0;
+};
+
+// Activation of the feed-forward block (include/neuralnet.cpp/model_spec.hpp:47-54).
+enum class ActivationType : std::uint32_t
+{
+    GeLU = 0,
+    SwiGLU = 1,
+    ReLU2 = 2,
+};
+
+// Gated feed-forward block with ternary BitLinear projections
+// (include/neuralnet.cpp/compute_layer_feedforward.hpp:22-204, WeightQuant::T1_58):
+// fc1 = BitLinear(d_model -> 2*d_ff) whose rows [0, d_ff) are the gate and [d_ff, 2*d_ff) the
+// up projection, the gated activation (SwiGLU or ReLU^2-GLU), fc2 = BitLinear(d_ff -> d_model).
+// With int8 activation quantization on both projections, forward() is one
+// ComputeEngine::ffn_glu_i8_forward (the HIP engine fuses the block); otherwise it chains the
+// layers. Only the gated activations are provided (GeLU and SubLN are outside this path).
+class FeedForward final : public Layer
+{
+public:
+    FeedForward(std::size_t d_model, std::size_t d_ff, ActivationType activation = ActivationType::SwiGLU,
+                bool inference_only = false)
+        : d_model_(d_model), d_ff_(d_ff), activation_(activation), fc1_(d_model, 2 * d_ff, inference_only),
+          fc2_(d_ff, d_model, inference_only)
+    {
+    }
+
+    [[nodiscard]] const char* layer_name() const noexcept override { return "FeedForward"; }
+
+    // A ternary composite takes any profile and splits it (split_ternary_profile,
+    // include/neuralnet.cpp/compute_layer_base.hpp:151-164): the projections get param T1_58.
+    [[nodiscard]] PrecisionSupport precision_support() const override
+    {
+        PrecisionSupport sup = PrecisionSupport::rounding_all_slots();
+        sup.param.mask |= PrecisionSet::of({Precision::T1_58}).mask;
+        return sup;
+    }
+
+    void set_activation_quant(bool enabled) noexcept
+    {
+        fc1_.set_activation_quant(enabled);
+        fc2_.set_activation_quant(enabled);
+    }
+
+    [[nodiscard]] BitLinear& fc1() noexcept { return fc1_; }
+    [[nodiscard]] BitLinear& fc2() noexcept { return fc2_; }
+    [[nodiscard]] std::size_t d_model() const noexcept { return d_model_; }
+    [[nodiscard]] std::size_t d_ff() const noexcept { return d_ff_; }
+
+    [[nodiscard]] std::vector<TensorRef> parameters() override
+    {
+        auto r = fc1_.parameters();
+        auto r2 = fc2_.parameters();
+        r.insert(r.end(), r2.begin(), r2.end());
+        return r;
+    }
+
+    void clear_cache() override
+    {
+        fc1_.clear_cache();
+        fc2_.clear_cache();
+    }
+
+    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
+    {
+        if (input.rows() != d_model_) return Error{"feedforward forward: input shape mismatch"};
+        ComputeEngine& engine = engine_ref();
+        const int act = activation_ == ActivationType::ReLU2 ? 1 : 0;
+        if (fc1_.activation_quant() && fc2_.activation_quant())
+        {
+            EX_TRY_CHECK(fc1_.ensure_quantized());
+            EX_TRY_CHECK(fc2_.ensure_quantized());
+            return engine.ffn_glu_i8_forward(input, nullptr, 0.0f, fc1_.quantized_weights_packed(), fc1_.row_scales(),
+                                             fc1_.bias(), fc2_.quantized_weights_packed(), fc2_.row_scales(),
+                                             fc2_.bias(), act);
+        }
+        EX_TRY(h1, fc1_.forward(input));
+        EX_TRY(h2, engine.glu(*h1, act));
+        return fc2_.forward(*h2);
+    }
+
+protected:
+    [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
+    {
+        if (activation_ == ActivationType::GeLU)
+            return Error{"FeedForward: only the gated activations (SwiGLU, ReLU2) are provided by this engine"};
+        PrecisionProfile linear = p_;
+        linear.param = Precision::T1_58;
+        fc1_.set_precision_profile(linear);
+        fc2_.set_precision_profile(linear);
+        EX_TRY_CHECK(fc1_.init(engine));
+        return fc2_.init(engine);
+    }
+
+private:
+    std::size_t d_model_, d_ff_;
+    ActivationType activation_;
+    BitLinear fc1_, fc2_;
 };
 
 class RMSNorm final : public Layer

@@ -13,6 +13,9 @@
 //  [10] engine factory never falls back    cli/cli_engine_factory.hpp:11-13, :60-66
 //  [11] matmul_q / matmul_q_t vs double   src/ternary_gemm_test.cpp [3][4] (:252-333), plus the
 //       BitLinear f32-activation branch     compute_layer_bitlinear.hpp:459-466
+//  [12] FeedForward (SwiGLU / ReLU2, int8)  compute_layer_feedforward.hpp:182-204: the fused
+//       engine block equals the layer-by-layer composition bit for bit; RMSNorm + FeedForward
+//       through Model::add equals the fused block with the norm folded in
 // Exit: 0 pass, 1 fail, 77 skip (no gfx950 device).
 #include <algorithm>
 #include <bit>
@@ -608,10 +611,77 @@ void test_float_products(nn::ComputeEngine& e)
         CHECK(!bl.activation_scales().valid() && bl.input_cache().rows() == IN, "f32 branch caches the input");
     }
 }
+
+// ---------------------------------------------------------------- [12]
+void test_feedforward(nn::ComputeEngine& e)
+{
+    std::puts("[12] FeedForward: fused gated block == layer-by-layer composition");
+    constexpr std::size_t D = 48, F = 40, B = 5;  // F not a multiple of 8 or 16
+    for (const auto act : {nn::ActivationType::SwiGLU, nn::ActivationType::ReLU2})
+    {
+        const int a = act == nn::ActivationType::ReLU2 ? 1 : 0;
+        nn::FeedForward ff(D, F, act);
+        nn::PrecisionProfile prof;
+        prof.param = nn::Precision::T1_58;
+        ff.set_precision_profile(prof);
+        CHECK(ff.init(e).has_value(), a ? "FeedForward(ReLU2) init" : "FeedForward(SwiGLU) init");
+        if (!ff.fc1().latent_weights().valid()) return;
+        auto params = ff.parameters();  // fc1 latent, fc1 bias, fc2 latent, fc2 bias
+        CHECK(params.size() == 4, "parameters: two latents and two biases");
+        if (params.size() != 4) return;
+        CHECK(e.copy_from(params[0].get(), random_matrix(2 * F, D, 91)).has_value() &&
+                  e.copy_from(params[1].get(), random_matrix(2 * F, 1, 92)).has_value() &&
+                  e.copy_from(params[2].get(), random_matrix(D, F, 93)).has_value() &&
+                  e.copy_from(params[3].get(), random_matrix(D, 1, 94)).has_value(),
+              "write latent weights and biases");
+        ff.set_activation_quant(true);
+        const nn::Tensor x = upload(e, random_matrix(D, B, 95));
+        auto y = ff.forward(x);
+        CHECK(y.has_value() && y->rows() == D && y->cols() == B, "fused forward");
+        if (!y) return;
+        auto h1 = ff.fc1().forward(x);
+        auto h2 = h1 ? e.glu(*h1, a) : nn::Result<nn::Tensor>(nn::Error{"fc1 failed"});
+        auto y2 = h2 ? ff.fc2().forward(*h2) : nn::Result<nn::Tensor>(nn::Error{"glu failed"});
+        CHECK(y2.has_value() && bitwise_equal(download(e, *y), download(e, *y2)),
+              "fused block bit-identical to fc1 -> glu -> fc2");
+        // with RMSNorm in front (config C4's block): Model of two layers vs the fused call
+        nn::Model model(e);  // default f32 profile: the FeedForward gives its projections T1_58
+        CHECK(model.add<nn::RMSNorm>(D, 1e-6f).has_value(), "Model::add<RMSNorm>");
+        CHECK(model.add<nn::FeedForward>(D, F, act).has_value(), "Model::add<FeedForward>");
+        if (model.num_layers() != 2) return;
+        auto& mff = static_cast<nn::FeedForward&>(model.layer_at(1));
+        auto mp = mff.parameters();
+        (void)e.copy_from(mp[0].get(), random_matrix(2 * F, D, 91));
+        (void)e.copy_from(mp[1].get(), random_matrix(2 * F, 1, 92));
+        (void)e.copy_from(mp[2].get(), random_matrix(D, F, 93));
+        (void)e.copy_from(mp[3].get(), random_matrix(D, 1, 94));
+        mff.set_activation_quant(true);
+        auto ym = model.forward(x);
+        CHECK(ym.has_value(), "Model forward (RMSNorm, FeedForward)");
+        auto& norm = static_cast<nn::RMSNorm&>(model.layer_at(0));
+        auto yf = e.ffn_glu_i8_forward(x, &norm.gamma(), 1e-6f, mff.fc1().quantized_weights_packed(),
+                                       mff.fc1().row_scales(), mff.fc1().bias(), mff.fc2().quantized_weights_packed(),
+                                       mff.fc2().row_scales(), mff.fc2().bias(), a);
+        CHECK(ym.has_value() && yf.has_value() && bitwise_equal(download(e, *ym), download(e, *yf)),
+              "RMSNorm + FeedForward == one fused block with the norm folded in");
+        ff.set_activation_quant(false);
+        auto yf32 = ff.forward(x);
+        bool finite = yf32.has_value();
+        if (finite)
+            for (float v : download(e, *yf32).span()) finite = finite && std::isfinite(v);
+        CHECK(finite, "f32-activation branch (matmul_q) runs");
+    }
+    nn::FeedForward gelu(8, 8, nn::ActivationType::GeLU);
+    nn::PrecisionProfile prof;
+    prof.param = nn::Precision::T1_58;
+    gelu.set_precision_profile(prof);
+    CHECK(!gelu.init(e).has_value(), "GeLU FeedForward is refused (only gated activations)");
+}
 }  // namespace
 
 int main()
 {
+    std::setvbuf(stdout, nullptr, _IOLBF, 0);  // a crash still shows the last section reached
     test_layout();
     test_factory();
     nn::cli::EngineConfig ec;
@@ -636,6 +706,7 @@ int main()
     test_quant_cache(e);
     test_deploy_and_model(e);
     test_float_products(e);
+    test_feedforward(e);
     if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
     else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
     return g_failures == 0 ? 0 : 1;
