@@ -254,12 +254,15 @@ def ffn_block_line(ctx, torch, stream, steps, out):
 
 def matmul_q_lines(ctx, torch, stream, steps, out):
     """Float-activation ternary products on the reference container (the reference's default
-    BitLinear branch and its dX product), per BitNet-2B shape at M (tokens) in {1, 16}, f32 in
-    and out. GB/s of algorithmic bytes: packed weights N*ceil(K/16)*4 + 4*K*M (B) + 4*N (tau)
-    + 4*N*M (Y); matmul_q_t reads the same container for the transposed product."""
+    BitLinear branch and its dX product), per BitNet-2B shape at M (tokens) in {1, 16} and on a
+    64 MiB container (32768 x 8192) at M=1, f32 in and out. GB/s of algorithmic bytes: packed
+    weights N*ceil(K/16)*4 + 4*K*M (B) + 4*N (tau) + 4*N*M (Y); matmul_q_t reads the same
+    container for the transposed product. Times are per Python-issued call (events), so the
+    decode shapes include the launch path; kernel-only times are in the rocprof summary."""
     res = {}
     n = max(10, steps // 2)
-    for name, K, N in (("q 2560->2560", D, D), ("gate 2560->6912", D, FFN), ("down 6912->2560", FFN, D)):
+    for name, K, N in (("q 2560->2560", D, D), ("gate 2560->6912", D, FFN), ("down 6912->2560", FFN, D),
+                       ("big 8192->32768", 8192, 32768)):
         gen = torch.Generator(device="cuda")
         gen.manual_seed(0xB17A0008 + K + N)
         W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
@@ -267,7 +270,7 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
         wq = ctx.trit_pack(W, tau)
         del W
         wbytes = N * ((K + 15) // 16) * 4
-        for M in (1, 16):
+        for M in ((1,) if K == 8192 else (1, 16)):
             B = torch.randn((K, M), generator=gen, device="cuda")
             Y = torch.empty((N, M), device="cuda")
             t, _ = time_launches(torch, stream, lambda: ctx.matmul_q(wq, tau, B, K, out=Y), n, 5)

@@ -139,10 +139,21 @@ hipError_t launch_quantize_i8(hipStream_t st, const float* x, const float* scale
 hipError_t launch_unpack_i8(hipStream_t st, const uint32_t* packed, size_t rows, size_t cols,
                             float* out);
 hipError_t launch_add_row_broadcast(hipStream_t st, float* Y, const float* b, size_t N, size_t M);
+// Float-activation products (k_matq.hip): the plan splits the reduction into chunks whose
+// partial sums (part_bytes of scratch, 0 for one chunk) a second kernel adds in fixed order.
+struct MatqPlan
+{
+    int n_chunks;
+    int chunk;          // packed words of the reduction per chunk
+    size_t part_bytes;  // scratch: [transposed container (at_bytes)] + partial sums
+    size_t at_bytes;    // matmul_q_t only
+};
+MatqPlan plan_matmul_q(size_t N, size_t K, size_t M);
+MatqPlan plan_matmul_q_t(size_t K, size_t M, size_t N);
 hipError_t launch_matmul_q(hipStream_t st, const uint32_t* wq, const float* tau, const void* B, bool b16, size_t N,
-                           size_t K, size_t M, void* Y, bool y16);
+                           size_t K, size_t M, void* Y, bool y16, const MatqPlan& plan, float* part);
 hipError_t launch_matmul_q_t(hipStream_t st, const uint32_t* A, const float* tau, const void* B, bool b16, size_t K,
-                             size_t M, size_t N, void* Y, bool y16);
+                             size_t M, size_t N, void* Y, bool y16, const MatqPlan& plan, float* scratch);
 
 // ---- activation kernels (k_act.hip)
 hipError_t launch_rmsnorm(hipStream_t st, const float* X, const float* gamma, float eps, size_t F,

@@ -436,7 +436,14 @@ nnhip_status nnhip_matmul_q(nnhip_ctx* ctx, const uint32_t* wq, const float* tau
     NNHIP_REQUIRE(wq && tau && B && Y, fn, "null pointer");
     NNHIP_REQUIRE(K >= 1 && N <= kMaxDim && M <= kMaxDim && K <= kMaxDim, fn, "bad shape");
     NNHIP_REQUIRE(mul_ok(N, ceil_div(K, 16)) && mul_ok(K, M) && mul_ok(N, M), fn, "size overflow");
-    NNHIP_LAUNCH(fn, launch_matmul_q(ctx->stream, wq, tau, B, b_f16 != 0, N, K, M, Y, y_f16 != 0));
+    const MatqPlan plan = plan_matmul_q(N, K, M);
+    if (plan.part_bytes)
+    {
+        const nnhip_status st = ensure_ws(ctx, plan.part_bytes, fn);
+        if (st != NNHIP_OK) return st;
+    }
+    NNHIP_LAUNCH(fn, launch_matmul_q(ctx->stream, wq, tau, B, b_f16 != 0, N, K, M, Y, y_f16 != 0, plan,
+                                     static_cast<float*>(ctx->ws)));
     return NNHIP_OK;
 }
 
@@ -449,7 +456,14 @@ nnhip_status nnhip_matmul_q_t(nnhip_ctx* ctx, const uint32_t* A, const float* ta
     NNHIP_REQUIRE(A && tau && B && Y, fn, "null pointer");
     NNHIP_REQUIRE(K >= 1 && N <= kMaxDim && M <= kMaxDim && K <= kMaxDim, fn, "bad shape");
     NNHIP_REQUIRE(mul_ok(K, ceil_div(M, 16)) && mul_ok(K, N) && mul_ok(M, N), fn, "size overflow");
-    NNHIP_LAUNCH(fn, launch_matmul_q_t(ctx->stream, A, tau, B, b_f16 != 0, K, M, N, Y, y_f16 != 0));
+    const MatqPlan plan = plan_matmul_q_t(K, M, N);
+    if (plan.part_bytes)
+    {
+        const nnhip_status st = ensure_ws(ctx, plan.part_bytes, fn);
+        if (st != NNHIP_OK) return st;
+    }
+    NNHIP_LAUNCH(fn, launch_matmul_q_t(ctx->stream, A, tau, B, b_f16 != 0, K, M, N, Y, y_f16 != 0, plan,
+                                       static_cast<float*>(ctx->ws)));
     return NNHIP_OK;
 }
 
