@@ -90,6 +90,17 @@ Result<void> ComputeEngine::copy_from(Tensor& dst, const Matrix& src)
     return upload_impl(dst, src.data(), src.size() * sizeof(float));
 }
 
+Result<void> ComputeEngine::copy_into(Tensor& dst, const Tensor& src)
+{
+    EX_TRY_CHECK(check_owned(dst, "copy_into: dst"));
+    EX_TRY_CHECK(check_owned(src, "copy_into: src"));
+    EpochGuard g{dst};
+    if (dst.rows() != src.rows() || dst.cols() != src.cols() || dst.precision() != src.precision())
+        return Error{"copy_into: shape or precision mismatch (" + shape(dst) + " vs " + shape(src) + ")"};
+    if (dst.same_storage(src) || dst.size() == 0) return {};
+    return copy_impl(dst, src, dst.size() * sizeof(float));
+}
+
 Result<Tensor> ComputeEngine::trit_pack(const Tensor& W, const Tensor& tau)
 {
     EX_TRY_CHECK(check_owned(W, "trit_pack"));

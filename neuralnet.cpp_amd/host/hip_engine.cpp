@@ -88,6 +88,12 @@ protected:
         return {};
     }
 
+    Result<void> copy_impl(const Tensor& dst, const Tensor& src, std::size_t bytes) override
+    {
+        NNHIP_TRY(nnhip_memcpy_d2d(ctx_->h, TensorAccess::ptr(dst), TensorAccess::ptr(src), bytes), "copy");
+        return {};
+    }
+
     Result<void> trit_pack_impl(const Tensor& W, const Tensor& tau, const Tensor& out) override
     {
         NNHIP_TRY(nnhip_trit_pack(ctx_->h, fp(W), fp(tau), W.rows(), W.cols(), upw(out)), "trit_pack");

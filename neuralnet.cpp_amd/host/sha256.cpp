@@ -1,0 +1,112 @@
+// sha256.cpp — SHA-256 as specified in FIPS 180-4 (section 6.2): 64-byte blocks, big-endian
+// words, the message schedule W[0..63], 64 rounds with the constants K (the fractional parts
+// of the cube roots of the first 64 primes) and the initial hash H(0) (the fractional parts
+// of the square roots of the first 8 primes); padding 0x80, zeros, 64-bit big-endian bit length.
+#include "neuralnet.cpp/sha256.hpp"
+
+#include <cstring>
+
+namespace nn
+{
+
+namespace
+{
+
+constexpr std::uint32_t kRound[64] = {
+    0x428a2f98u, 0x71374491u, 0xb5c0fbcfu, 0xe9b5dba5u, 0x3956c25bu, 0x59f111f1u, 0x923f82a4u, 0xab1c5ed5u,
+    0xd807aa98u, 0x12835b01u, 0x243185beu, 0x550c7dc3u, 0x72be5d74u, 0x80deb1feu, 0x9bdc06a7u, 0xc19bf174u,
+    0xe49b69c1u, 0xefbe4786u, 0x0fc19dc6u, 0x240ca1ccu, 0x2de92c6fu, 0x4a7484aau, 0x5cb0a9dcu, 0x76f988dau,
+    0x983e5152u, 0xa831c66du, 0xb00327c8u, 0xbf597fc7u, 0xc6e00bf3u, 0xd5a79147u, 0x06ca6351u, 0x14292967u,
+    0x27b70a85u, 0x2e1b2138u, 0x4d2c6dfcu, 0x53380d13u, 0x650a7354u, 0x766a0abbu, 0x81c2c92eu, 0x92722c85u,
+    0xa2bfe8a1u, 0xa81a664bu, 0xc24b8b70u, 0xc76c51a3u, 0xd192e819u, 0xd6990624u, 0xf40e3585u, 0x106aa070u,
+    0x19a4c116u, 0x1e376c08u, 0x2748774cu, 0x34b0bcb5u, 0x391c0cb3u, 0x4ed8aa4au, 0x5b9cca4fu, 0x682e6ff3u,
+    0x748f82eeu, 0x78a5636fu, 0x84c87814u, 0x8cc70208u, 0x90befffau, 0xa4506cebu, 0xbef9a3f7u, 0xc67178f2u};
+
+inline std::uint32_t rotr(std::uint32_t x, unsigned n) noexcept { return (x >> n) | (x << (32 - n)); }
+
+}  // namespace
+
+Sha256::Sha256() noexcept
+    : h_{0x6a09e667u, 0xbb67ae85u, 0x3c6ef372u, 0xa54ff53au, 0x510e527fu, 0x9b05688cu, 0x1f83d9abu, 0x5be0cd19u},
+      buf_{}
+{
+}
+
+void Sha256::block(const std::uint8_t* p) noexcept
+{
+    std::uint32_t w[64];
+    for (int t = 0; t < 16; ++t)
+        w[t] = (std::uint32_t(p[4 * t]) << 24) | (std::uint32_t(p[4 * t + 1]) << 16) |
+               (std::uint32_t(p[4 * t + 2]) << 8) | std::uint32_t(p[4 * t + 3]);
+    for (int t = 16; t < 64; ++t)
+    {
+        const std::uint32_t s0 = rotr(w[t - 15], 7) ^ rotr(w[t - 15], 18) ^ (w[t - 15] >> 3);
+        const std::uint32_t s1 = rotr(w[t - 2], 17) ^ rotr(w[t - 2], 19) ^ (w[t - 2] >> 10);
+        w[t] = w[t - 16] + s0 + w[t - 7] + s1;
+    }
+    std::uint32_t a = h_[0], b = h_[1], c = h_[2], d = h_[3], e = h_[4], f = h_[5], g = h_[6], h = h_[7];
+    for (int t = 0; t < 64; ++t)
+    {
+        const std::uint32_t S1 = rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25);
+        const std::uint32_t ch = (e & f) ^ (~e & g);
+        const std::uint32_t t1 = h + S1 + ch + kRound[t] + w[t];
+        const std::uint32_t S0 = rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22);
+        const std::uint32_t maj = (a & b) ^ (a & c) ^ (b & c);
+        const std::uint32_t t2 = S0 + maj;
+        h = g;
+        g = f;
+        f = e;
+        e = d + t1;
+        d = c;
+        c = b;
+        b = a;
+        a = t1 + t2;
+    }
+    h_[0] += a;
+    h_[1] += b;
+    h_[2] += c;
+    h_[3] += d;
+    h_[4] += e;
+    h_[5] += f;
+    h_[6] += g;
+    h_[7] += h;
+}
+
+void Sha256::update(const void* data, std::size_t n) noexcept
+{
+    const auto* p = static_cast<const std::uint8_t*>(data);
+    total_ += n;
+    if (buf_len_ > 0)
+    {
+        const std::size_t take = n < 64 - buf_len_ ? n : 64 - buf_len_;
+        std::memcpy(buf_ + buf_len_, p, take);
+        buf_len_ += take;
+        p += take;
+        n -= take;
+        if (buf_len_ < 64) return;
+        block(buf_);
+        buf_len_ = 0;
+    }
+    for (; n >= 64; p += 64, n -= 64) block(p);
+    std::memcpy(buf_, p, n);
+    buf_len_ = n;
+}
+
+std::array<std::uint8_t, 32> Sha256::digest() noexcept
+{
+    const std::uint64_t bits = total_ * 8;
+    const std::uint8_t pad = 0x80;
+    update(&pad, 1);
+    const std::uint8_t zero[64] = {};
+    const std::size_t fill = buf_len_ <= 56 ? 56 - buf_len_ : 120 - buf_len_;
+    update(zero, fill);
+    std::uint8_t len[8];
+    for (int i = 0; i < 8; ++i) len[i] = static_cast<std::uint8_t>(bits >> (56 - 8 * i));
+    update(len, 8);
+    std::array<std::uint8_t, 32> out{};
+    for (int i = 0; i < 8; ++i)
+        for (int j = 0; j < 4; ++j) out[4 * i + j] = static_cast<std::uint8_t>(h_[i] >> (24 - 8 * j));
+    return out;
+}
+
+}  // namespace nn

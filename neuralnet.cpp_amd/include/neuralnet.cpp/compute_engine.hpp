@@ -133,6 +133,8 @@ public:
     [[nodiscard]] Result<Tensor> from_matrix(const Matrix& m, Precision p = Precision::F32);
     [[nodiscard]] Result<Matrix> to_matrix(const Tensor& t, Precision p = Precision::F32);
     [[nodiscard]] Result<void> copy_from(Tensor& dst, const Matrix& src);
+    // device-to-device copy of equal shapes (the layers' import_param uses it)
+    [[nodiscard]] Result<void> copy_into(Tensor& dst, const Tensor& src);
 
     // ---- the BitLinear W1.58A8 primitives (reference names and semantics)
     [[nodiscard]] Result<Tensor> trit_pack(const Tensor& W, const Tensor& tau);
@@ -187,6 +189,7 @@ protected:
     [[nodiscard]] virtual Result<Tensor> alloc_impl(std::size_t rows, std::size_t cols, Precision p) = 0;
     [[nodiscard]] virtual Result<void> upload_impl(const Tensor& dst, const void* src, std::size_t bytes) = 0;
     [[nodiscard]] virtual Result<void> download_impl(const Tensor& src, void* dst, std::size_t bytes) = 0;
+    [[nodiscard]] virtual Result<void> copy_impl(const Tensor& dst, const Tensor& src, std::size_t bytes) = 0;
     [[nodiscard]] virtual Result<void> trit_pack_impl(const Tensor& W, const Tensor& tau, const Tensor& out) = 0;
     [[nodiscard]] virtual Result<void> row_absmean_impl(const Tensor& W, const Tensor& tau) = 0;
     [[nodiscard]] virtual Result<void> abs_impl(const Tensor& x, const Tensor& out) = 0;

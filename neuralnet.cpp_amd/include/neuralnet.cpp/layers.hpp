@@ -28,6 +28,47 @@
 namespace nn
 {
 
+// Parameter entry protocol of the v7+ model files (include/neuralnet.cpp/compute_layer_base.hpp:193-208,
+// :425-533): every layer exposes its parameters by index as entries of one kind.
+enum class ParamKind : std::uint8_t
+{
+    Dense = 0,           // plain float parameter (bias, norm gain, ...)
+    TernaryLatent = 1,   // BitLinear f32 latent weights (checkpoint files)
+    TernaryPacked2 = 2,  // BitLinear 2-bit container + tau (the run-time form)
+    TernaryPacked3 = 3,  // base-3 on-disk form of the same (1.6 bpw)
+    I8Packed4 = 4,       // reserved
+};
+
+[[nodiscard]] inline const char* param_kind_name(ParamKind k) noexcept
+{
+    switch (k)
+    {
+    case ParamKind::Dense: return "Dense";
+    case ParamKind::TernaryLatent: return "TernaryLatent";
+    case ParamKind::TernaryPacked2: return "TernaryPacked2";
+    case ParamKind::TernaryPacked3: return "TernaryPacked3";
+    case ParamKind::I8Packed4: return "I8Packed4";
+    }
+    return "?";
+}
+
+// File role byte: Model = inference file (.nnmodel, ternary layers packed), Checkpoint =
+// training file (.nnckpt, ternary layers as f32 latents).
+enum class ModelRole : std::uint8_t
+{
+    Model = 0,
+    Checkpoint = 1,
+};
+
+struct ParamEntry
+{
+    ParamKind kind = ParamKind::Dense;
+    Precision precision = Precision::F32;
+    std::size_t rows = 0, cols = 0;  // logical shape (for packed kinds: out x in features)
+    Tensor payload;                  // values, latent, or packed words (raw u32 in an f32 tensor)
+    Tensor aux;                      // tau (rows, 1) for the ternary kinds
+};
+
 class Layer
 {
 public:
@@ -61,9 +102,46 @@ public:
     [[nodiscard]] virtual std::vector<TensorRef> parameters() { return {}; }
     virtual void clear_cache() {}
 
+    // Parameter entries by index (the model file's order). Default: every parameter is Dense.
+    [[nodiscard]] virtual std::size_t param_count() { return parameters().size(); }
+    [[nodiscard]] virtual Result<ParamEntry> export_param(std::size_t index, ModelRole /*role*/)
+    {
+        auto ps = parameters();
+        if (index >= ps.size()) return Error{std::string("export_param: index out of range (layer ") + layer_name() + ")"};
+        return dense_entry_(ps[index].get());
+    }
+    [[nodiscard]] virtual Result<void> import_param(std::size_t index, const ParamEntry& e)
+    {
+        if (e.kind != ParamKind::Dense)
+            return Error{std::string("import_param: layer ") + layer_name() + " takes Dense entries, got " +
+                         param_kind_name(e.kind)};
+        auto ps = parameters();
+        if (index >= ps.size()) return Error{std::string("import_param: index out of range (layer ") + layer_name() + ")"};
+        return import_into_(ps[index].get(), e);
+    }
+
 protected:
     [[nodiscard]] virtual Result<void> init_impl(ComputeEngine& engine) = 0;
     [[nodiscard]] ComputeEngine& engine_ref() const noexcept { return *engine_; }
+
+    [[nodiscard]] static ParamEntry dense_entry_(const Tensor& t)
+    {
+        ParamEntry e;
+        e.kind = ParamKind::Dense;
+        e.precision = t.precision();
+        e.rows = t.rows();
+        e.cols = t.cols();
+        e.payload = t;
+        return e;
+    }
+    [[nodiscard]] Result<void> import_into_(Tensor& dst, const ParamEntry& e)
+    {
+        if (e.rows != dst.rows() || e.cols != dst.cols() || !e.payload.valid())
+            return Error{std::string("import_param: shape mismatch (layer ") + layer_name() + ", expected " +
+                         std::to_string(dst.rows()) + "x" + std::to_string(dst.cols()) + ", got " +
+                         std::to_string(e.rows) + "x" + std::to_string(e.cols) + ")"};
+        return engine_ref().copy_into(dst, e.payload);
+    }
     PrecisionProfile p_{};
 
 private:
@@ -112,6 +190,72 @@ public:
     // (1, M); the f32 branch keeps the input itself and no scales
     [[nodiscard]] const Tensor& input_cache() const noexcept { return input_cache_; }
     [[nodiscard]] const Tensor& activation_scales() const noexcept { return act_scale_; }
+
+    // Entries (compute_layer_bitlinear.hpp:221-339): 0 = weights, 1 = bias (Dense). Weights go
+    // out as TernaryPacked2 (words + tau) in an inference file and as TernaryLatent in a
+    // checkpoint; they come in as either.
+    [[nodiscard]] std::size_t param_count() override { return 2; }
+
+    [[nodiscard]] Result<ParamEntry> export_param(std::size_t index, ModelRole role) override
+    {
+        if (index == 1) return dense_entry_(b_);
+        if (index != 0) return Error{"BitLinear::export_param: index must be 0 or 1"};
+        ParamEntry e;
+        e.rows = out_features_;
+        e.cols = in_features_;
+        e.precision = Precision::F32;
+        if (role == ModelRole::Checkpoint)
+        {
+            if (!latent_w_.valid())
+                return Error{"BitLinear::export_param: a deploy-state layer has no latent weights for a checkpoint"};
+            e.kind = ParamKind::TernaryLatent;
+            e.payload = latent_w_;
+            return e;
+        }
+        EX_TRY_CHECK(ensure_quantized());
+        e.kind = ParamKind::TernaryPacked2;
+        e.payload = wq_packed_;
+        e.aux = tau_;
+        return e;
+    }
+
+    [[nodiscard]] Result<void> import_param(std::size_t index, const ParamEntry& e) override
+    {
+        if (index == 1)
+        {
+            if (e.kind != ParamKind::Dense)
+                return Error{std::string("BitLinear::import_param: the bias must be Dense, got ") + param_kind_name(e.kind)};
+            return import_into_(b_, e);
+        }
+        if (index != 0) return Error{"BitLinear::import_param: index must be 0 or 1"};
+        if (e.rows != out_features_ || e.cols != in_features_)
+            return Error{"BitLinear::import_param: entry is " + std::to_string(e.rows) + "x" + std::to_string(e.cols) +
+                         ", layer is " + std::to_string(out_features_) + "x" + std::to_string(in_features_)};
+        switch (e.kind)
+        {
+        case ParamKind::TernaryPacked2:
+            return load_packed_weights(e.payload, e.aux);
+        case ParamKind::TernaryLatent:
+        {
+            if (!latent_w_.valid())
+            {
+                // back from the deploy state: a fresh latent and quantization buffers
+                latent_w_ = engine_ref().create_tensor(out_features_, in_features_, Precision::F32, InitSpec::zero());
+                wq_packed_ = engine_ref().create_tensor(out_features_, trit_pack::words_per_row(in_features_),
+                                                        Precision::F32, InitSpec::zero());
+                tau_ = engine_ref().create_tensor(out_features_, 1, Precision::F32, InitSpec::zero());
+                if (!latent_w_.valid() || !wq_packed_.valid() || !tau_.valid())
+                    return Error{"BitLinear::import_param: latent allocation failed"};
+                packed_only_ = false;
+            }
+            quant_valid_ = false;
+            return import_into_(latent_w_, e);
+        }
+        default:
+            return Error{std::string("BitLinear::import_param: entry kind ") + param_kind_name(e.kind) +
+                         " is not accepted (TernaryLatent, TernaryPacked2)"};
+        }
+    }
 
     // Deploy state: packed words + tau replace the latent weights (read-only inference).
     [[nodiscard]] Result<void> load_packed_weights(Tensor packed_words, Tensor tau)
@@ -269,6 +413,19 @@ public:
         auto r2 = fc2_.parameters();
         r.insert(r.end(), r2.begin(), r2.end());
         return r;
+    }
+
+    // entries: fc1 (weights, bias), then fc2 (compute_layer_feedforward.hpp:100-107)
+    [[nodiscard]] std::size_t param_count() override { return fc1_.param_count() + fc2_.param_count(); }
+    [[nodiscard]] Result<ParamEntry> export_param(std::size_t index, ModelRole role) override
+    {
+        const std::size_t n1 = fc1_.param_count();
+        return index < n1 ? fc1_.export_param(index, role) : fc2_.export_param(index - n1, role);
+    }
+    [[nodiscard]] Result<void> import_param(std::size_t index, const ParamEntry& e) override
+    {
+        const std::size_t n1 = fc1_.param_count();
+        return index < n1 ? fc1_.import_param(index, e) : fc2_.import_param(index - n1, e);
     }
 
     void clear_cache() override

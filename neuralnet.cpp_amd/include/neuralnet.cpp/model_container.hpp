@@ -31,6 +31,21 @@ public:
         return {};
     }
 
+    // An already built layer, with the model's default profile or an explicit one
+    // (include/neuralnet.cpp/model_container.hpp:103-124: e.g. BitLinear at param=T1_58 next
+    // to norm layers at the f32 default).
+    [[nodiscard]] Result<void> add_layer(std::unique_ptr<Layer> layer)
+    {
+        return add_layer(std::move(layer), profile_);
+    }
+    [[nodiscard]] Result<void> add_layer(std::unique_ptr<Layer> layer, const PrecisionProfile& profile)
+    {
+        layer->set_precision_profile(profile);
+        EX_TRY_CHECK(layer->init(*engine_));
+        layers_.push_back(std::move(layer));
+        return {};
+    }
+
     [[nodiscard]] Result<Tensor> forward(const Tensor& input)
     {
         if (layers_.empty()) return Error{"Model::forward: no layers"};

@@ -8,6 +8,8 @@
 #include "layers.hpp"
 #include "matrix.hpp"
 #include "model_container.hpp"
+#include "model_serialization.hpp"
 #include "precision.hpp"
 #include "result.hpp"
+#include "sha256.hpp"
 #include "ternary_pack.hpp"

@@ -16,9 +16,17 @@
 //  [12] FeedForward (SwiGLU / ReLU2, int8)  compute_layer_feedforward.hpp:182-204: the fused
 //       engine block equals the layer-by-layer composition bit for bit; RMSNorm + FeedForward
 //       through Model::add equals the fused block with the norm folded in
+//  [13] model files (v7 / v8)               model_serialization.hpp:38-82, :579-700, :1175-1311:
+//       SHA-256 vectors (FIPS 180-2), header / entry parsing of the tests/golden fixtures
+//       (host only), then load -> deploy state: packed words equal the file's bytes, repack ->
+//       unpack on the GPU gives them back, forward matches the host W1.58A8 reference, and
+//       save -> load reproduces the model
 // Exit: 0 pass, 1 fail, 77 skip (no gfx950 device).
 #include <algorithm>
+#include <array>
 #include <bit>
+#include <cstring>
+#include <memory>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -28,6 +36,7 @@
 #include <vector>
 
 #include "neuralnet.cpp/nn.hpp"
+#include "nnhip.h"
 
 namespace
 {
@@ -677,13 +686,235 @@ void test_feedforward(nn::ComputeEngine& e)
     gelu.set_precision_profile(prof);
     CHECK(!gelu.init(e).has_value(), "GeLU FeedForward is refused (only gated activations)");
 }
+
+// ---------------------------------------------------------------- [13]
+std::string g_golden = "tests/golden";
+
+std::string hex(const std::array<std::uint8_t, 32>& d)
+{
+    static const char* x = "0123456789abcdef";
+    std::string s;
+    for (std::uint8_t b : d)
+    {
+        s += x[b >> 4];
+        s += x[b & 15];
+    }
+    return s;
+}
+
+std::string sha_of(const std::string& msg)
+{
+    nn::Sha256 h;
+    h.update(msg.data(), msg.size());
+    return hex(h.digest());
+}
+
+bool same_bytes(const void* a, const void* b, std::size_t n) { return n == 0 || std::memcmp(a, b, n) == 0; }
+
+void test_model_files_host()
+{
+    std::puts("[13] model files: SHA-256 vectors and host-side parsing");
+    CHECK(sha_of("abc") == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad", "sha256(\"abc\")");
+    CHECK(sha_of("") == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855", "sha256(\"\")");
+    CHECK(sha_of("abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq") ==
+              "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1",
+          "sha256 two-block message");
+    {
+        nn::Sha256 h;  // the same message fed in odd-sized pieces
+        const std::string m = "abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq";
+        for (std::size_t i = 0; i < m.size(); i += 7) h.update(m.data() + i, std::min<std::size_t>(7, m.size() - i));
+        CHECK(hex(h.digest()) == "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1", "sha256 incremental");
+    }
+    const nn::ParamKind kinds[5] = {nn::ParamKind::Dense, nn::ParamKind::TernaryPacked2, nn::ParamKind::Dense,
+                                    nn::ParamKind::TernaryPacked2, nn::ParamKind::Dense};
+    const std::size_t shapes[5][2] = {{48, 1}, {20, 48}, {20, 1}, {12, 20}, {12, 1}};
+    for (const char* name : {"nnmodel_v8.nnmodel", "nnmodel_v7.nnmodel"})
+    {
+        auto f = nn::read_model_file(g_golden + "/" + name, 5);
+        CHECK(f.has_value(), name);
+        if (!f)
+        {
+            std::printf("    %s\n", f.error().message.c_str());
+            continue;
+        }
+        bool ok = f->params.size() == 5 && f->role == nn::ModelRole::Model &&
+                  f->version == (std::string(name).find("v8") != std::string::npos ? 8u : 7u) &&
+                  f->spec == "spec-bytes: opaque to the loader" && f->tokenizer == "NNVC-tokenizer-bytes";
+        for (std::size_t i = 0; ok && i < 5; ++i)
+            ok = f->params[i].kind == kinds[i] && f->params[i].rows == shapes[i][0] && f->params[i].cols == shapes[i][1];
+        ok = ok && f->params[1].payload.size() == 20 * 3 * 4 && f->params[1].aux.size() == 20 * 4 &&
+             f->params[3].payload.size() == 12 * 2 * 4;
+        CHECK(ok, "header, spec, entry kinds / shapes / sizes, tokenizer");
+    }
+    auto c = nn::read_model_file(g_golden + "/nnmodel_corrupt.nnmodel", 5);
+    CHECK(!c.has_value() && c.error().message.find("checksum") != std::string::npos, "a flipped byte fails the sha256 check");
+    auto w = nn::read_model_file(g_golden + "/nnmodel_v8.nnmodel", 4);
+    CHECK(!w.has_value(), "an entry count that does not match the file is an error");
+    auto t = nn::read_model_file(g_golden + "/nnmodel_trim_f16.nnmodel", 5);
+    CHECK(t.has_value() && t->params[0].precision_tag == nn::kTagF16 && t->params[3].payload.size() == 12 * 5,
+          "f16 Dense entry and byte-trimmed TernaryPacked2 rows parse");
+    auto k = nn::read_model_file(g_golden + "/nnmodel_ckpt.nnmodel", 5);
+    CHECK(k.has_value() && k->role == nn::ModelRole::Checkpoint && k->params[1].kind == nn::ParamKind::TernaryLatent,
+          "checkpoint role with TernaryLatent entries parses");
+    CHECK(!nn::read_model_file(g_golden + "/does_not_exist.nnmodel", 5).has_value(), "a missing file is an error");
+}
+
+// RMSNorm(48) -> BitLinear(48, 20) -> BitLinear(20, 12), the fixtures' layout
+bool build_file_model(nn::ComputeEngine& e, nn::Model& m)
+{
+    nn::PrecisionProfile t158;
+    t158.param = nn::Precision::T1_58;
+    return m.add<nn::RMSNorm>(48, 1e-6f).has_value() &&
+           m.add_layer(std::make_unique<nn::BitLinear>(48, 20), t158).has_value() &&
+           m.add_layer(std::make_unique<nn::BitLinear>(20, 12), t158).has_value() && (void(e), true);
+}
+
+// host W1.58A8 forward of one BitLinear from decoded words / tau / bias (x: K x B)
+nn::Matrix host_bitlinear(const nn::Matrix& x, const nn::Matrix& words, const nn::Matrix& tau, const nn::Matrix& b)
+{
+    const std::size_t K = x.rows(), B = x.cols(), N = words.rows(), wpr = words.cols();
+    nn::Matrix y(N, B);
+    for (std::size_t c = 0; c < B; ++c)
+    {
+        float mx = 0.0f;
+        for (std::size_t k = 0; k < K; ++k) mx = std::max(mx, std::fabs(x.at(k, c)));
+        const float s = mx * (1.0f / 127.0f);
+        for (std::size_t n = 0; n < N; ++n)
+        {
+            std::vector<std::uint32_t> w(wpr);
+            for (std::size_t i = 0; i < wpr; ++i) w[i] = word_of(words, n, i);
+            std::int32_t acc = 0;
+            for (std::size_t k = 0; k < K; ++k)
+                acc += static_cast<std::int32_t>(nn::trit_pack::at(w.data(), k)) * nn::i8_pack::quantize(x.at(k, c), s);
+            y.set_value(n, c, (tau.at(n, 0) * s) * static_cast<float>(acc) + b.at(n, 0));
+        }
+    }
+    return y;
+}
+
+void test_model_files_device(nn::ComputeEngine& e)
+{
+    std::puts("[13] model files: load -> deploy state -> repack round trip -> forward; save -> load");
+    auto file = nn::read_model_file(g_golden + "/nnmodel_v8.nnmodel", 5);
+    if (!file) return;
+    for (const char* name : {"nnmodel_v8.nnmodel", "nnmodel_v7.nnmodel", "nnmodel_trim_f16.nnmodel"})
+    {
+        nn::Model m(e);
+        CHECK(build_file_model(e, m), "RMSNorm + 2 x BitLinear built");
+        std::uint32_t ver = 0;
+        auto tok = nn::load_model(g_golden + "/" + name, m, &ver);
+        CHECK(tok.has_value() && *tok == "NNVC-tokenizer-bytes", name);
+        if (!tok)
+        {
+            std::printf("    %s\n", tok.error().message.c_str());
+            continue;
+        }
+        auto& l1 = static_cast<nn::BitLinear&>(m.layer_at(1));
+        auto& l2 = static_cast<nn::BitLinear&>(m.layer_at(2));
+        CHECK(l1.packed_only() && l2.packed_only(), "BitLinear layers are in the packed deploy state");
+        const nn::Matrix w1 = download(e, l1.quantized_weights_packed()), t1 = download(e, l1.row_scales());
+        const nn::Matrix w2 = download(e, l2.quantized_weights_packed());
+        const bool trimmed = std::string(name).find("trim") != std::string::npos;
+        bool words_ok = same_bytes(w1.data(), file->params[1].payload.data(), 20 * 3 * 4) &&
+                        same_bytes(t1.data(), file->params[1].aux.data(), 20 * 4);
+        for (std::size_t r = 0; r < 12 && words_ok; ++r)
+        {
+            // rows of 20 trits: 2 words; the file's bytes 0..4 (trimmed) or 0..7, the rest code 2
+            const auto* fw = file->params[3].payload.data() + r * 8;
+            std::uint8_t want[8];
+            std::memcpy(want, fw, 8);
+            if (trimmed) std::memset(want + 5, 0xAA, 3);
+            words_ok = same_bytes(w2.data() + r * 2, want, 8);
+        }
+        CHECK(words_ok, "packed words and tau equal the file bytes (tail bytes of trimmed rows = code 2)");
+        // repack -> unrepack on the GPU gives the container back bit for bit
+        const nn::Tensor& wq = l1.quantized_weights_packed();
+        auto rp = e.create_tensor(nnhip_repacked_bytes(20, 48) / 4, 1);
+        auto back = e.create_tensor(20, 3);
+        nnhip_ctx* ctx = nullptr;
+        bool rt = nnhip_ctx_create(0, &ctx) == NNHIP_OK && rp.valid() && back.valid();
+        if (rt)
+        {
+            rt = nnhip_repack_ternary(ctx, static_cast<const uint32_t*>(nn::TensorAccess::ptr(wq)), 20, 48,
+                                      nn::TensorAccess::ptr(rp)) == NNHIP_OK &&
+                 nnhip_unrepack_ternary(ctx, nn::TensorAccess::ptr(rp), 20, 48,
+                                        static_cast<uint32_t*>(nn::TensorAccess::ptr(back))) == NNHIP_OK &&
+                 nnhip_sync(ctx) == NNHIP_OK;
+            (void)nnhip_ctx_destroy(ctx);
+        }
+        CHECK(rt && bitwise_equal(download(e, back), w1), "file words -> repack -> unrepack on the GPU == file words");
+        // forward: RMSNorm (engine) then the two BitLinears against the host reference on the file's values
+        l1.set_activation_quant(true);
+        l2.set_activation_quant(true);
+        const nn::Matrix x = random_matrix(48, 3, 131);
+        auto y = m.forward(upload(e, x));
+        auto n0 = e.rmsnorm(upload(e, x), static_cast<nn::RMSNorm&>(m.layer_at(0)).gamma(), 1e-6f);
+        bool fwd = y.has_value() && n0.has_value();
+        if (fwd)
+        {
+            const nn::Matrix h1 = host_bitlinear(download(e, *n0), w1, t1, download(e, l1.bias()));
+            const nn::Matrix y2 = host_bitlinear(h1, w2, download(e, l2.row_scales()), download(e, l2.bias()));
+            fwd = bitwise_equal(download(e, *y), y2);
+        }
+        CHECK(fwd, "forward of the loaded model == host W1.58A8 reference on the file's values");
+        // save -> load round trip
+        const std::string tmp = "/tmp/nnhip_roundtrip_" + std::to_string(ver) + (trimmed ? "t" : "") + ".nnmodel";
+        auto sv = nn::save_model(tmp, m, nn::ModelRole::Model, "spec", "tok");
+        nn::Model m2(e);
+        bool rt2 = sv.has_value() && build_file_model(e, m2) && nn::load_model(tmp, m2).has_value();
+        if (rt2)
+        {
+            auto& k1 = static_cast<nn::BitLinear&>(m2.layer_at(1));
+            auto& k2 = static_cast<nn::BitLinear&>(m2.layer_at(2));
+            k1.set_activation_quant(true);
+            k2.set_activation_quant(true);
+            auto y2 = m2.forward(upload(e, x));
+            rt2 = bitwise_equal(download(e, k1.quantized_weights_packed()), w1) &&
+                  bitwise_equal(download(e, k2.quantized_weights_packed()), w2) && y2.has_value() && y.has_value() &&
+                  bitwise_equal(download(e, *y2), download(e, *y));
+        }
+        CHECK(rt2, "save_model -> load_model reproduces words, tau and outputs");
+        std::remove(tmp.c_str());
+    }
+    {
+        nn::Model m(e);
+        (void)build_file_model(e, m);
+        auto r = nn::load_model(g_golden + "/nnmodel_packed3.nnmodel", m);
+        CHECK(!r.has_value() && r.error().message.find("TernaryPacked3") != std::string::npos,
+              "base-3 entries are refused with a clear error");
+    }
+    {
+        nn::Model m(e);
+        (void)build_file_model(e, m);
+        nn::ModelRole role = nn::ModelRole::Model;
+        auto r = nn::load_model(g_golden + "/nnmodel_ckpt.nnmodel", m, nullptr, &role);
+        auto ck = nn::read_model_file(g_golden + "/nnmodel_ckpt.nnmodel", 5);
+        auto& l1 = static_cast<nn::BitLinear&>(m.layer_at(1));
+        bool ok = r.has_value() && ck.has_value() && role == nn::ModelRole::Checkpoint && l1.latent_weights().valid() &&
+                  !l1.packed_only();
+        if (ok)
+        {
+            const nn::Matrix lat = download(e, l1.latent_weights());
+            ok = lat.rows() == 20 && lat.cols() == 48 && same_bytes(lat.data(), ck->params[1].payload.data(), 20 * 48 * 4);
+        }
+        CHECK(ok, "checkpoint file: TernaryLatent entries land in the latent weights");
+        // the layer quantizes them on first use; its packed words equal the oracle's fixture words
+        l1.set_activation_quant(true);
+        auto q = l1.ensure_quantized();
+        CHECK(q.has_value() && same_bytes(download(e, l1.quantized_weights_packed()).data(), file->params[1].payload.data(),
+                                          20 * 3 * 4),
+              "latent -> absmean tau -> trit_pack reproduces the inference file's words");
+    }
+}
 }  // namespace
 
-int main()
+int main(int argc, char** argv)
 {
     std::setvbuf(stdout, nullptr, _IOLBF, 0);  // a crash still shows the last section reached
+    if (argc > 1) g_golden = argv[1];
     test_layout();
     test_factory();
+    test_model_files_host();
     nn::cli::EngineConfig ec;
     ec.use_hip = true;
     auto eng = nn::cli::create_engine(ec);
@@ -707,6 +938,7 @@ int main()
     test_deploy_and_model(e);
     test_float_products(e);
     test_feedforward(e);
+    test_model_files_device(e);
     if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
     else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
     return g_failures == 0 ? 0 : 1;

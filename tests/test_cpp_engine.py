@@ -14,7 +14,7 @@ BIN = os.path.join(ROOT, "tests", "cpp", "bin", "bitlinear_engine_test")
 
 def run():
     assert os.path.exists(BIN), "build it with __graft_entry__.build() (make -C neuralnet.cpp_amd)"
-    p = subprocess.run([BIN], capture_output=True, text=True, timeout=240)
+    p = subprocess.run([BIN, os.path.join(ROOT, "tests", "golden")], capture_output=True, text=True, timeout=240)
     print(p.stdout[-6000:], p.stderr[-2000:], flush=True)
     return p
 

@@ -423,3 +423,24 @@ def test_ffn_block_is_the_composition(orc, act):
     # no norm: gamma None feeds X straight to fc1's quantizer
     Y0, _ = orc.ffn_glu_i8(X, None, 0.0, F, wq1, t1, b1, wq2, t2, b2, act)
     assert np.array_equal(Y0, bitlinear(orc.glu(bitlinear(X, wq1, t1, b1, d), act), wq2, t2, b2, F))
+
+
+def test_model_file_fixtures_reproducible(tmp_path):
+    """The committed .nnmodel fixtures are exactly what tests/golden/make_nnmodel.py writes,
+    and their v8 tails verify with hashlib's sha256."""
+    import hashlib
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    subprocess.run([sys.executable, os.path.join(GOLDEN, "make_nnmodel.py"), str(tmp_path)], check=True,
+                   cwd=os.path.dirname(here), capture_output=True)
+    names = sorted(p.name for p in tmp_path.iterdir())
+    assert len(names) == 6
+    for n in names:
+        with open(os.path.join(GOLDEN, n), "rb") as f:
+            committed = f.read()
+        assert (tmp_path / n).read_bytes() == committed, n
+        if n != "nnmodel_v7.nnmodel":
+            body, digest, tail = committed[:-37], committed[-37:-5], committed[-5:]
+            assert tail == b"NNEND"
+            assert (hashlib.sha256(body).digest() == digest) == (n != "nnmodel_corrupt.nnmodel"), n
