@@ -24,13 +24,19 @@
 // as zeros).
 //
 // Pipeline: a ring of kSlots LDS slots (default 2: measured faster than 3, more DMA in flight
-// only added contention); the DMA of stage s+kSlots is issued as soon as every wave has
-// finished reading stage s. Within a stage the wave's 32-k steps are software-pipelined: the B
-// fragments of step i+1 are read from LDS while the MFMAs of step i run (two register sets),
-// and the A words plus the first B fragments of stage s+1 are read before the last MFMAs of
-// stage s. The one barrier per stage sits in the last step, after the wave's own reads of the
-// stage have landed and its own part of the next stage's DMA is complete (explicit vmcnt /
-// lgkmcnt waits, no memory fence, so the DMA of later stages is not drained).
+// only added contention); the DMA of stage s+kSlots may start as soon as every wave has
+// finished reading stage s. It is issued by the first wave of each k-split pair only, in
+// kDmaParts pieces: one right after that barrier, the rest between the MFMAs of the next
+// stage's first steps (issued all at once, 48 DMA instructions per block stalled every wave on
+// the full address FIFO of the texture unit). Within a stage the wave's 32-k steps are
+// software-pipelined: the B fragments of step i+1 are read from LDS while the MFMAs of step i
+// run (two register sets), and the A words plus the first B fragments of stage s+1 are read
+// before the last MFMAs of stage s. The one barrier per stage sits in the last step, after
+// the wave's own reads of the stage have landed and its own part of the next stage's DMA is
+// complete (explicit vmcnt / lgkmcnt waits, no memory fence, so the DMA of later stages is not
+// drained). Wave priorities fall step by step between barriers (s_setprio), so the two waves
+// of a SIMD stay level instead of the older one finishing first and idling at the barrier.
+// The epilogue operands (tau, s, rowsum, bias) are loaded before the k-split exchange.
 //
 // Block order is XCD-aware: blocks are dealt round-robin to the 8 XCDs, and each XCD gets
 // whole token blocks (all N for them), so a token block's activations stay in that XCD's L2.
@@ -79,14 +85,29 @@ constexpr int kPartBytes = kRB / 2 * kTB * 4096;
 constexpr int kRingBytes = kSlots * kSlotBytes;  // 144 KiB for three slots
 constexpr int kLdsBytes = kKSplit == 2 && kWaves * kPartBytes > kRingBytes ? kWaves * kPartBytes : kRingBytes;
 // DMA instructions per wave per stage: A one row tile (1 KiB) each, B four token rows each
-constexpr int kADma = kRowTiles / kWaves, kBDma = kBM / 4 / kWaves;
+// Waves 0 .. kDmaWaves-1 issue the DMA (with the default k split, the first wave of each pair:
+// the older wave of its SIMD, which the issue arbiter favours and which reaches the stage
+// barrier first)
+#ifndef NNHIP_GEMM_DMA_WAVES
+#define NNHIP_GEMM_DMA_WAVES (kWavesN * kWavesM)
+#endif
+constexpr int kDmaWaves = NNHIP_GEMM_DMA_WAVES;
+constexpr int kADma = kRowTiles / kDmaWaves, kBDma = kBM / 4 / kDmaWaves;
 constexpr int kDmaPerStage = kADma + kBDma;
+// The DMA of one stage is issued in kDmaParts pieces: the first right after the barrier that
+// frees its slot, the others at the start of the next stage's first kDmaParts - 1 steps.
+#ifndef NNHIP_GEMM_DMA_PARTS
+#define NNHIP_GEMM_DMA_PARTS 2
+#endif
+constexpr int kDmaParts = NNHIP_GEMM_DMA_PARTS;
+constexpr int kPartLoads = kDmaPerStage / kDmaParts;
 constexpr int kRsrcFlags = 0x00020000;
 
 static_assert(kWaves % 4 == 0 && kRB >= 1 && kTB >= 1, "wave layout");
 static_assert(kKSplit == 1 || (kKSplit == 2 && kRB % 2 == 0), "k split pairs finish one half of the row blocks each");
-static_assert(kADma * kWaves == kRowTiles && kBDma * kWaves * 4 == kBM, "DMA split");
+static_assert(kDmaWaves <= kWaves && kADma * kDmaWaves == kRowTiles && kBDma * kDmaWaves * 4 == kBM, "DMA split");
 static_assert(kSlots >= 2 && kSlots <= 5 && 4 * kDmaPerStage < 63, "vmcnt range");
+static_assert(kDmaParts >= 1 && kDmaPerStage % kDmaParts == 0 && kDmaParts <= kWaveSteps, "DMA parts");
 static_assert(kTB * 32 * kTileK <= 65536, "B fragment offsets fit the ds_read immediate");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -123,6 +144,24 @@ __device__ __forceinline__ void wait_stage_landed(int later)
     else wait_vmcnt<4 * kDmaPerStage>();
 }
 
+// Issue priority of a wave at step position `pos` of a barrier interval (0 = the step right
+// after the barrier, kWaveSteps - 1 = the step before it). The issue arbiter serves the
+// higher priority first and the older wave on a tie, so without this the older wave of a SIMD
+// runs ahead and idles at the barrier while the younger one finishes alone. Falling priority
+// keeps the two waves of a SIMD at the same step.
+#ifndef NNHIP_GEMM_PRIO
+#define NNHIP_GEMM_PRIO 1
+#endif
+__device__ __forceinline__ void step_prio(int pos)
+{
+    if (!NNHIP_GEMM_PRIO) return;
+    const int v = 3 - (pos * 4) / kWaveSteps;
+    if (v >= 3) __builtin_amdgcn_s_setprio(3);
+    else if (v == 2) __builtin_amdgcn_s_setprio(2);
+    else if (v == 1) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // Workgroup barrier without a memory fence. __syncthreads() (and any workgroup fence, even
 // one limited to LDS) makes the compiler wait for every outstanding buffer->LDS load
 // (vmcnt(0)), which drains the DMA ring each stage. Here the caller's explicit waits cover
@@ -144,25 +183,40 @@ struct Dma
     uint32_t a_row0;    // first row tile (global) of the block
 };
 
-// Issue the DMA of k tile kt into LDS slot `slot`.
-__device__ __forceinline__ void issue_stage(uint8_t* lds, const Dma& d, int slot, int kt, int KT)
+// Issue loads [lo, hi) of this wave's share of k tile kt's DMA into LDS slot `slot`: the
+// wave's kADma A row tiles come first, then its kBDma groups of four B token rows. lo and hi
+// are constants at every (unrolled) call site.
+__device__ __forceinline__ void issue_loads(uint8_t* lds, const Dma& d, int slot, int kt, int KT, int lo, int hi)
 {
     uint8_t* base = lds + slot * kSlotBytes;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (kDmaWaves < kWaves && wave >= kDmaWaves) return;
 #pragma unroll
-    for (int i = 0; i < kADma; ++i)
+    for (int q = 0; q < kDmaPerStage; ++q)
     {
-        const int rt_local = wave * kADma + i;
-        const uint32_t soff = ((d.a_row0 + rt_local) * (uint32_t)KT + (uint32_t)kt) * 1024u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, (lds_void*)(base + rt_local * 1024), 16, d.a_voff, soff, 0, 0);
+        if (q < lo || q >= hi) continue;
+        if (q < kADma)
+        {
+            const int rt_local = wave * kADma + q;
+            const uint32_t soff = ((d.a_row0 + rt_local) * (uint32_t)KT + (uint32_t)kt) * 1024u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, (lds_void*)(base + rt_local * 1024), 16, d.a_voff, soff, 0,
+                                                     0);
+        }
+        else
+        {
+            // this instruction fills token rows 4*(wave*kBDma + i) .. +3 (1 KiB)
+            const int i = q - kADma;
+            uint8_t* dst = base + kABytes + (wave * kBDma + i) * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rb, (lds_void*)dst, 16, d.b_voff[i], (uint32_t)kt * kTileK, 0,
+                                                     0);
+        }
     }
-#pragma unroll
-    for (int i = 0; i < kBDma; ++i)
-    {
-        // this instruction fills token rows 4*(wave*kBDma + i) .. +3 (1 KiB)
-        uint8_t* dst = base + kABytes + (wave * kBDma + i) * 1024;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rb, (lds_void*)dst, 16, d.b_voff[i], (uint32_t)kt * kTileK, 0, 0);
-    }
+}
+
+// The whole DMA of k tile kt (prologue stages).
+__device__ __forceinline__ void issue_stage(uint8_t* lds, const Dma& d, int slot, int kt, int KT)
+{
+    issue_loads(lds, d, slot, kt, KT, 0, kDmaPerStage);
 }
 
 // A words of one stage: row block rb, the wave's k half (T16K256 lane 16*(2m + h) + row%16;
@@ -210,57 +264,111 @@ __device__ __forceinline__ void run_stage(int s, int KT, uint8_t* lds, const Dma
             wait_lgkm0();  // this wave's reads of stage s have landed
             wait_stage_landed(min(KT - 2 - s, kSlots - 2));  // its part of stage s+1 has landed
             lds_barrier();  // all of stage s+1 is in LDS; nobody reads stage s's slot any more
-            if (s + kSlots < KT) issue_stage(lds, d, s % kSlots, s + kSlots, KT);
+            if (s + kSlots < KT) issue_loads(lds, d, s % kSlots, s + kSlots, KT, 0, kPartLoads);
             const uint8_t* nslot = lds + ((s + 1) % kSlots) * kSlotBytes;
             read_a(wa[P ^ 1], nslot + ln.a_off);
             read_b(bf[nxt], nslot + ln.b_off + ln.b_step[0]);
         }
         __builtin_amdgcn_sched_barrier(0);
+        step_prio(i == kWaveSteps - 1 ? 0 : i + 1);
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
         {
             const v4i a = (v4i)((__builtin_bit_cast(u32x4, wa[P][rb][m]) >> (2 * j)) & kM3);
 #pragma unroll
             for (int n = 0; n < kTB; ++n) acc[rb][n] = mfma32(a, bf[cur][n], acc[rb][n]);
+            if (rb == 0 && i + 1 < kDmaParts)
+            {
+                // piece i+1 of the DMA of stage s+kSlots-1, whose first piece went out at the
+                // barrier of stage s-1 (stages below kSlots were issued whole in the prologue)
+                const int t = s + kSlots - 1;
+                __builtin_amdgcn_sched_barrier(0);
+                if (s >= 1 && t < KT)
+                    issue_loads(lds, d, (s - 1) % kSlots, t, KT, (i + 1) * kPartLoads, (i + 2) * kPartLoads);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// Epilogue of a block that lies wholly inside Y: no masks. The 32x32 accumulator layout puts
-// element i of lane l at row 8*(i/4) + 4*(l/32) + i%4, token l%32; row offsets are scalar.
-template <bool kBias>
-__device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&acc)[kRB][kTB], int rb0, int nrb,
-                                           int row_w, int tok_w, int h, int l32)
+// Epilogue operands of the row blocks a wave finishes (kRBf of them, from rb0 on), loaded
+// before the k-split exchange so that their latency hides behind it. The 32x32 accumulator
+// layout puts element i of lane l at row 8*(i/4) + 4*(l/32) + i%4, token l%32. Buffer loads:
+// rows past N and tokens past M read zero; without a bias the bias values are zero.
+constexpr int kRBf = kRB / kKSplit;
+struct EpiOps
+{
+    int rs2[kTB];        // 2 * rowsum of the lane's tokens
+    float sv[kTB];       // activation scale of the lane's tokens
+    float tv[kRBf][16];  // tau of the lane's accumulator rows
+    float bv[kRBf][16];  // bias of the lane's accumulator rows
+};
+
+__device__ __forceinline__ void load_epilogue(const GemvProblem& p, EpiOps& e, int rb0, int row_w, int tok_w, int h,
+                                              int l32)
 {
     const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
-    const __amdgpu_buffer_rsrc_t rbias = rsrc(kBias ? p.bias : p.tau, (uint32_t)p.N * 4u);
     const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
     const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
-    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
-    const uint32_t M4 = (uint32_t)p.M * 4u;
-    int rs2[kTB];
-    float sv[kTB];
 #pragma unroll
     for (int n = 0; n < kTB; ++n)
     {
         const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
-        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
-        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+        e.rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
+        e.sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
     }
 #pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
+    for (int r = 0; r < kRBf; ++r)
     {
-        if (rb < rb0 || rb >= rb0 + nrb) continue;
-        const uint32_t row0 = (uint32_t)(row_w + rb * 32 + 4 * h);
-        float tv[16], bv[16];
+        const uint32_t row0 = (uint32_t)(row_w + (rb0 + r) * 32 + 4 * h);
 #pragma unroll
         for (int i = 0; i < 16; ++i)
         {
             const uint32_t row = row0 + (uint32_t)(8 * (i >> 2) + (i & 3));
-            tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
-            if (kBias) bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
+            e.tv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
         }
+    }
+    if (p.bias)
+    {
+        const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias, (uint32_t)p.N * 4u);
+#pragma unroll
+        for (int r = 0; r < kRBf; ++r)
+        {
+            const uint32_t row0 = (uint32_t)(row_w + (rb0 + r) * 32 + 4 * h);
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+            {
+                const uint32_t row = row0 + (uint32_t)(8 * (i >> 2) + (i & 3));
+                e.bv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
+            }
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int r = 0; r < kRBf; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) e.bv[r][i] = 0.0f;
+    }
+}
+
+// Index of row block rb (a compile-time loop index in [rb0, rb0 + nrb)) within EpiOps.
+__device__ __forceinline__ int epi_slot(int rb) { return kRBf == 1 ? 0 : rb; }
+
+// Epilogue of a block that lies wholly inside Y: no masks; row offsets are scalar.
+template <bool kBias>
+__device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
+                                           int nrb, int row_w, int tok_w, int h, int l32)
+{
+    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+    const uint32_t M4 = (uint32_t)p.M * 4u;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+    {
+        if (rb < rb0 || rb >= rb0 + nrb) continue;
+        const int r = epi_slot(rb);
+        const uint32_t row0 = (uint32_t)(row_w + rb * 32 + 4 * h);
         const uint32_t vbase = (row0 * (uint32_t)p.M + (uint32_t)(tok_w + l32)) * 4u;
 #pragma unroll
         for (int i = 0; i < 16; ++i)
@@ -269,9 +377,9 @@ __device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&ac
 #pragma unroll
             for (int n = 0; n < kTB; ++n)
             {
-                const int a = acc[rb][n][i] - rs2[n];
-                float y = (tv[i] * sv[n]) * (float)a;
-                if (kBias) y = y + bv[i];
+                const int a = acc[rb][n][i] - e.rs2[n];
+                float y = (e.tv[r][i] * e.sv[n]) * (float)a;
+                if (kBias) y = y + e.bv[r][i];
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, vbase + (uint32_t)(n * 128),
                                                       soff, 0);
             }
@@ -281,36 +389,16 @@ __device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&ac
 
 // Epilogue of an edge block: rows past N and tokens past M are masked (their lanes store to
 // an out-of-range offset, which the buffer unit drops).
-__device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&acc)[kRB][kTB], int rb0, int nrb,
-                                           int row_w, int tok_w, int h, int l32)
+__device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
+                                           int nrb, int row_w, int tok_w, int h, int l32)
 {
-    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
-    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
-    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
     const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
-    int rs2[kTB];
-    float sv[kTB];
-#pragma unroll
-    for (int n = 0; n < kTB; ++n)
-    {
-        const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
-        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
-        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
-    }
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb)
     {
         if (rb < rb0 || rb >= rb0 + nrb) continue;
+        const int r = epi_slot(rb);
         const int row0 = row_w + rb * 32 + 4 * h;
-        float tv[16], bv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-        {
-            const uint32_t row = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3));
-            tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
-            bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
-        }
 #pragma unroll
         for (int n = 0; n < kTB; ++n)
         {
@@ -319,9 +407,9 @@ __device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&ac
             for (int i = 0; i < 16; ++i)
             {
                 const int row = row0 + 8 * (i >> 2) + (i & 3);
-                const int a = acc[rb][n][i] - rs2[n];
-                float y = (tv[i] * sv[n]) * (float)a;
-                if (p.bias) y = y + bv[i];
+                const int a = acc[rb][n][i] - e.rs2[n];
+                float y = (e.tv[r][i] * e.sv[n]) * (float)a;
+                if (p.bias) y = y + e.bv[r][i];
                 const uint32_t off = (row < p.N && m < p.M) ? ((uint32_t)row * (uint32_t)p.M + (uint32_t)m) * 4u
                                                              : 0xFFFFFFF0u;
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
@@ -335,49 +423,33 @@ __device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&ac
 // i (row 8*(i/4) + 4h + i%4 of the 32-row block) and element i + 4 (8 rows below) are gate and
 // up of one feature when i/4 is even. Each is rescaled exactly as the plain epilogue does
 // ((tau * s) * float(acc) [+ bias]), then combined by glu_one; h (glu_F, M) gets the result.
-__device__ __forceinline__ void store_glu(const GemvProblem& p, const v16i (&acc)[kRB][kTB], int rb0, int nrb,
-                                          int row_w, int tok_w, int h, int l32)
+__device__ __forceinline__ void store_glu(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
+                                          int nrb, int row_w, int tok_w, int h, int l32)
 {
-    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
-    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
-    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
     const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.glu_F * (uint32_t)p.M * 4u);
     const int act = p.glu - 1;
-    int rs2[kTB];
-    float sv[kTB];
-#pragma unroll
-    for (int n = 0; n < kTB; ++n)
-    {
-        const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
-        rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
-        sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
-    }
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb)
     {
         if (rb < rb0 || rb >= rb0 + nrb) continue;
+        const int r = epi_slot(rb);
         const int row0 = row_w + rb * 32 + 4 * h;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
+        for (int q = 0; q < 8; ++q)
         {
-            const int i = (e / 4) * 8 + (e % 4);  // gate element: i / 4 in {0, 2}
-            const uint32_t rg = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3)), ru = rg + 8u;
-            const float tg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, rg * 4u, 0, 0));
-            const float tu = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, ru * 4u, 0, 0));
-            const float bg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, rg * 4u, 0, 0));
-            const float bu = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, ru * 4u, 0, 0));
+            const int i = (q / 4) * 8 + (q % 4);  // gate element: i / 4 in {0, 2}
+            const uint32_t rg = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3));
             const int f = 8 * (int)(rg / 16u) + (int)(rg % 16u);
 #pragma unroll
             for (int n = 0; n < kTB; ++n)
             {
                 const int m = tok_w + n * 32 + l32;
-                float yg = (tg * sv[n]) * (float)(acc[rb][n][i] - rs2[n]);
-                float yu = (tu * sv[n]) * (float)(acc[rb][n][i + 4] - rs2[n]);
+                float yg = (e.tv[r][i] * e.sv[n]) * (float)(acc[rb][n][i] - e.rs2[n]);
+                float yu = (e.tv[r][i + 4] * e.sv[n]) * (float)(acc[rb][n][i + 4] - e.rs2[n]);
                 if (p.bias)
                 {
-                    yg = yg + bg;
-                    yu = yu + bu;
+                    yg = yg + e.bv[r][i];
+                    yu = yu + e.bv[r][i + 4];
                 }
                 const float y = glu_one(yg, yu, act);
                 const uint32_t off = (f < p.glu_F && m < p.M) ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)m) * 4u
@@ -416,18 +488,25 @@ __device__ __forceinline__ void add_partials(v16i (&acc)[kRB][kTB], const uint8_
     const v4i* theirs = reinterpret_cast<const v4i*>(lds + (wave ^ (kWavesN * kWavesM)) * kPartBytes);
 #pragma unroll
     for (int r = 0; r < kHalf; ++r)
+    {
+        // all reads of the row block first (one LDS round trip), then the adds
+        v4i o[kTB][4];
+#pragma unroll
+        for (int n = 0; n < kTB; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[n][q] = theirs[((r * kTB + n) * 4 + q) * 64 + lane];
 #pragma unroll
         for (int n = 0; n < kTB; ++n)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
             {
-                const v4i o = theirs[((r * kTB + n) * 4 + q) * 64 + lane];
                 v16i& a = acc[KS * kHalf + r][n];
-                a[4 * q] += o[0];
-                a[4 * q + 1] += o[1];
-                a[4 * q + 2] += o[2];
-                a[4 * q + 3] += o[3];
+                a[4 * q] += o[n][q][0];
+                a[4 * q + 1] += o[n][q][1];
+                a[4 * q + 2] += o[n][q][2];
+                a[4 * q + 3] += o[n][q][3];
             }
+    }
 }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd))) void
@@ -517,14 +596,23 @@ k_gemm(GemvProblem p, int n_mblocks, int n_nblocks, int xcd_mode)
 
     // ---- k split: the two waves of a pair swap partial sums through LDS; wave ks finishes row
     // blocks [ks * kRB / 2, (ks + 1) * kRB / 2).
+    // ---- epilogue operands (issued before the k-split exchange, whose LDS round trip hides
+    // their latency), then the exchange: the two waves of a pair swap partial sums through LDS;
+    // wave ks finishes row blocks [ks * kRB / 2, (ks + 1) * kRB / 2).
+    const int row_w = (rt0 + wn * (kWaveRows / 16)) * 16;
+    const int tok_w = m0 + wm * kWaveToks;
     int rb0 = 0, nrb = kRB;
     if (kKSplit == 2)
     {
-        constexpr int kHalf = kRB / 2;
-        rb0 = ks * kHalf;
-        nrb = kHalf;
-        wait_lgkm0();
-        wait_vmcnt<0>();
+        rb0 = ks * (kRB / 2);
+        nrb = kRB / 2;
+    }
+    wait_lgkm0();
+    wait_vmcnt<0>();
+    EpiOps e;
+    load_epilogue(p, e, rb0, row_w, tok_w, h, l32);
+    if (kKSplit == 2)
+    {
         lds_barrier();  // every wave is done with the ring
         if (ks == 0) put_partials<0>(acc, lds, wave, lane);
         else put_partials<1>(acc, lds, wave, lane);
@@ -534,21 +622,19 @@ k_gemm(GemvProblem p, int n_mblocks, int n_nblocks, int xcd_mode)
     }
 
     // ---- epilogue
-    const int row_w = (rt0 + wn * (kWaveRows / 16)) * 16;
-    const int tok_w = m0 + wm * kWaveToks;
     const bool full = rt0 * 16 + kBN <= p.N && m0 + kBM <= p.M;
     if (p.glu)
     {
-        store_glu(p, acc, rb0, nrb, row_w, tok_w, h, l32);
+        store_glu(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
     }
     else if (full)
     {
-        if (p.bias) store_full<true>(p, acc, rb0, nrb, row_w, tok_w, h, l32);
-        else store_full<false>(p, acc, rb0, nrb, row_w, tok_w, h, l32);
+        if (p.bias) store_full<true>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
+        else store_full<false>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
     }
     else
     {
-        store_edge(p, acc, rb0, nrb, row_w, tok_w, h, l32);
+        store_edge(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
     }
 }
 
