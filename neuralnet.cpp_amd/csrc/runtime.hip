@@ -23,6 +23,10 @@ struct nnhip_ctx
     hipStream_t stream = nullptr;
     void* ws = nullptr;  // workspace of the reference-layout matmul_q_i8 path
     size_t ws_bytes = 0;
+    // per-token absmax between the gated GEMM epilogue and the next quantization of the fused
+    // FFN block: zero between calls (zero-filled when allocated, reset by its consumer)
+    uint32_t* amax = nullptr;
+    size_t amax_words = 0;
 };
 
 struct nnhip_group
@@ -104,6 +108,31 @@ nnhip_status ensure_ws(nnhip_ctx* ctx, size_t bytes, const char* fn)
     return NNHIP_OK;
 }
 
+nnhip_status ensure_amax(nnhip_ctx* ctx, size_t words, const char* fn)
+{
+    if (ctx->amax_words >= words) return NNHIP_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
+    if (ctx->amax)
+    {
+        e = hipFree(ctx->amax);
+        ctx->amax = nullptr;
+        ctx->amax_words = 0;
+        if (e != hipSuccess) return hip_fail(fn, "hipFree", e);
+    }
+    e = hipMalloc(reinterpret_cast<void**>(&ctx->amax), words * 4);
+    if (e != hipSuccess)
+    {
+        ctx->amax = nullptr;
+        (void)hipGetLastError();
+        return fail(NNHIP_ERR_OOM, fn, "absmax buffer allocation of " + std::to_string(words * 4) + " bytes failed");
+    }
+    e = launch_fill_u32(ctx->stream, ctx->amax, 0u, words);
+    if (e != hipSuccess) return hip_fail(fn, "launch_fill_u32", e);
+    ctx->amax_words = words;
+    return NNHIP_OK;
+}
+
 nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
 {
     NNHIP_REQUIRE(N <= kMaxDim && M <= kMaxDim, fn, "N and M must be below 2^31");
@@ -120,7 +149,8 @@ nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
 
 nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
                         const int8_t* xi, const float* s, const int32_t* rowsum, const float* bias,
-                        size_t N, size_t K, size_t M, float* Y, int glu = 0, size_t glu_F = 0)
+                        size_t N, size_t K, size_t M, float* Y, int glu = 0, size_t glu_F = 0,
+                        uint32_t* amax = nullptr)
 {
     GemvProblem p{};
     p.rp = static_cast<const u32x4*>(rp);
@@ -137,6 +167,7 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     p.xlds = -1;
     p.glu = glu;
     p.glu_F = (int32_t)glu_F;
+    p.amax = amax;
     if (M <= (size_t)kGemvMaxM)
         NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
     else
@@ -209,6 +240,7 @@ nnhip_status nnhip_ctx_destroy(nnhip_ctx* ctx)
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->amax) (void)hipFree(ctx->amax);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
     if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
@@ -889,10 +921,34 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
     int32_t* rs2 = reinterpret_cast<int32_t*>(take(M * 4));
     float* h = reinterpret_cast<float*>(take(F * M * 4));
     float* y1 = M <= (size_t)kGemvMaxM ? reinterpret_cast<float*>(take(nnhip_glu_rows(F) * M * 4)) : nullptr;
+    if (M > (size_t)kGemvMaxM)
+    {
+        // prefill: the gated GEMM epilogue leaves max |h| per token, so h is quantized in one
+        // streaming pass (the same scale and codes as the absmax kernel)
+        st = ensure_amax(ctx, M, fn);
+        if (st != NNHIP_OK) return st;
+    }
     NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, gamma != nullptr, eps, d, M, xi1, s1, rs1, nullptr));
-    st = run_matmul_glu(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, F, d, M, act, y1, h);
-    if (st != NNHIP_OK) return st;
-    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, nullptr, false, 0.0f, F, M, xi2, s2, rs2, nullptr));
+    if (M > (size_t)kGemvMaxM)
+    {
+        st = run_matmul(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, nnhip_glu_rows(F), d, M, h, act + 1, F, ctx->amax);
+        if (st == NNHIP_OK)
+        {
+            const hipError_t e = launch_quant_amax(ctx->stream, h, F, M, ctx->amax, xi2, s2, rs2);
+            if (e != hipSuccess) st = hip_fail(fn, "kernel launch", e);
+        }
+        if (st != NNHIP_OK)
+        {
+            ctx->amax_words = 0;  // contents unknown: re-allocated and zero-filled by the next call
+            return st;
+        }
+    }
+    else
+    {
+        st = run_matmul_glu(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, F, d, M, act, y1, h);
+        if (st != NNHIP_OK) return st;
+        NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, nullptr, false, 0.0f, F, M, xi2, s2, rs2, nullptr));
+    }
     return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y);
 }
 

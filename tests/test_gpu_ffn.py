@@ -153,3 +153,31 @@ def test_ffn_block_c4_sampled_tokens(ctx, orc):
                               host(wq2, np.uint32), host(t2), None, 0)
     assert same_bits(Y[:, cols], Y_ref)
     assert np.isfinite(Y).all()
+
+
+def test_ffn_block_repeat_and_special_h(ctx, orc):
+    """The prefill block carries max |h| per token from the fc1 epilogue to the second
+    quantization in a buffer of the context that each call must leave at zero: consecutive
+    calls on one context (a smaller M after a larger one, inputs of other magnitudes) each
+    match the oracle. The last call has a fc1 bias with NaN and inf entries, so h holds NaN
+    (ignored by the absmax, quantized to 0) and inf (scale inf, codes 0)."""
+    d, F = 256, 136
+    wq1, t1, b1, wq2, t2, b2 = block_case(orc, d, F, 900)
+    rp1, to, bo = prepare_fc1(ctx, wq1, t1, b1, F, d)
+    rp2 = ctx.repack(dev(wq2), F)
+    cases = [(300, 1.0, b1), (64, 30.0, b1), (300, 0.01, b1)]
+    b_special = b1.copy()
+    b_special[[3, 70]] = np.nan
+    b_special[[5]] = np.inf
+    cases.append((200, 1.0, b_special))
+    for i, (M, scale, bias) in enumerate(cases):
+        say(f"ffn_glu_i8 repeat call {i}: M={M} scale={scale}")
+        X = (normal((d, M), 910 + i, 0.0, 1.0) * np.float32(scale)).astype(np.float32)
+        gamma = normal((d,), 920 + i, 1.0, 0.1)
+        Y_ref, _ = orc.ffn_glu_i8(X, gamma, 1e-6, F, wq1, t1, bias, wq2, t2, b2, 0)
+        if bias is b1:
+            b_dev = bo
+        else:
+            _, _, b_dev = prepare_fc1(ctx, wq1, t1, bias, F, d)
+        Y = host(ctx.ffn_glu_i8(dev(X), dev(gamma), 1e-6, F, rp1, to, b_dev, rp2, dev(t2), dev(b2), 0))
+        assert same_bits(Y, Y_ref), f"call {i}"
