@@ -74,6 +74,16 @@ nnhip_status nnhip_ctx_set_stream(nnhip_ctx* ctx, void* stream);
 nnhip_status nnhip_ctx_reset_stream(nnhip_ctx* ctx);
 nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream);
 
+/* Block tile of the prefill GEMM (M > 16 tokens): automatic (the default) picks, per call, the
+ * tile with the fewest estimated block rounds over the CUs; the others force one tile. A tuning
+ * control of this library (the reference's GEMM shader has a single 64 x 64 tile); results are
+ * bit-identical whichever tile runs. */
+#define NNHIP_GEMM_TILE_AUTO 0
+#define NNHIP_GEMM_TILE_256x128 1
+#define NNHIP_GEMM_TILE_128x128 2
+#define NNHIP_GEMM_TILE_64x64 3
+nnhip_status nnhip_ctx_set_gemm_tile(nnhip_ctx* ctx, int tile);
+
 /* Block the host until all work queued on the context's stream has finished.
  * Replaces ComputeEngine::end_batch()/flush_batch() waits (compute_layer_gpt.hpp:715-719). */
 nnhip_status nnhip_sync(nnhip_ctx* ctx);

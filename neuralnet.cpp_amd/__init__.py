@@ -63,6 +63,7 @@ SIGNATURES = {
     "nnhip_ctx_reset_stream": (_st, [_vp]),
     "nnhip_ctx_get_stream": (_st, [_vp, ctypes.POINTER(_vp)]),
     "nnhip_sync": (_st, [_vp]),
+    "nnhip_ctx_set_gemm_tile": (_st, [_vp, _st]),
     "nnhip_malloc": (_st, [_vp, _sz, ctypes.POINTER(_vp)]),
     "nnhip_free": (_st, [_vp, _vp]),
     "nnhip_memcpy_h2d": (_st, [_vp, _vp, _vp, _sz]),
@@ -105,6 +106,8 @@ SIGNATURES = {
 }
 
 ACT_SWIGLU, ACT_RELU2GLU = 0, 1
+# prefill GEMM block tiles (nnhip_ctx_set_gemm_tile)
+GEMM_TILE_AUTO, GEMM_TILE_256x128, GEMM_TILE_128x128, GEMM_TILE_64x64 = 0, 1, 2, 3
 
 _lib = None
 
@@ -195,6 +198,10 @@ class Context:
     def sync(self) -> None:
         self._bind_stream()
         _check(lib().nnhip_sync(self.h), "nnhip_sync")
+
+    def set_gemm_tile(self, tile: int) -> None:
+        """Force the prefill GEMM block tile (GEMM_TILE_*); GEMM_TILE_AUTO picks per call."""
+        _check(lib().nnhip_ctx_set_gemm_tile(self.h, tile), "nnhip_ctx_set_gemm_tile")
 
     # -- reference-layout primitives
     def row_absmean(self, W):

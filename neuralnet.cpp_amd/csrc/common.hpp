@@ -9,6 +9,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "nnhip.h"
+
 namespace nnhip
 {
 
@@ -183,7 +185,13 @@ hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const
                                const uint32_t* d_wave_items, size_t n_waves, const XStage* d_xstage,
                                int n_xstage, uint32_t lds_bytes);
 size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds);
-hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus);
+// Prefill GEMM; tile is one of NNHIP_GEMM_TILE_* (AUTO: gemm_tile_choice).
+hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus, int tile);
+int gemm_tile_choice(const GemvProblem& p, int num_cus);
+// Time of one round of 128 x 128 / 64 x 64 blocks relative to one round of 256 x 128 blocks,
+// measured over M = 128..4096, K = 2560..6912, N = 2560..13824 (with these the automatic choice
+// picked the fastest tile on every measured shape).
+constexpr double kGemmRelB = 0.6, kGemmRelC = 0.45;
 
 // ---- gated activations (k_glu.hip)
 hipError_t launch_glu(hipStream_t st, const float* Y1, size_t F, size_t M, int act, bool interleaved, float* h);

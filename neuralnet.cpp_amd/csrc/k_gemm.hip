@@ -12,12 +12,15 @@
 // T16K256 lane 16*(2m + l/32) + (row%16) of the row's tile and shifts by 2j, so the same tile
 // layout feeds both the 16x16 GEMV and this GEMM.
 //
-// Tiling: one block per CU, block tile 256 rows (16 row tiles) x 128 tokens, kWavesN x
-// kWavesM output tiles, each shared by kKSplit waves. The default 4 x 1 x 2 gives each pair
-// of waves 64 rows x 128 tokens (2 x 4 MFMA tiles); the two waves of a pair take the two k
-// halves of every 64-k group and add their partial sums through LDS at the end. So every
-// unpacked weight fragment (the only VALU work of the loop) feeds four MFMAs, LDS reads are
-// 0.75 KiB per MFMA, and two waves share each SIMD. Per 256-wide k tile ("stage") the block
+// Tiling: one block per CU, block tile kBN rows x kBM tokens, kWavesN x kWavesM output tiles,
+// each shared by kKSplit waves (struct Gemm; three configurations, chosen per call by the
+// estimated block rounds over the CUs). The large one, 256 x 128 with 4 x 1 x 2 waves, gives
+// each pair of waves 64 rows x 128 tokens (2 x 4 MFMA tiles); the two waves of a pair take
+// the two k halves of every 64-k group and add their partial sums through LDS at the end. So
+// every unpacked weight fragment (the only VALU work of the loop) feeds four MFMAs, LDS reads
+// are 0.75 KiB per MFMA, and two waves share each SIMD. 128 x 128 (2 x 2 x 2 waves) and
+// 64 x 64 (2 x 2 x 1: one wave per SIMD, no k split) spread problems with few 256 x 128
+// blocks over more CUs. Per 256-wide k tile ("stage") the block
 // stages A (16 KiB, copied as is) and B (128 token rows of 256 B, 16-byte chunk c of token t
 // stored at chunk c ^ (t & 15) so the 16 lanes of a ds_read_b128 hit 16 distinct bank
 // groups) with buffer->LDS DMA loads (no register staging; out-of-range rows and tokens read
@@ -52,66 +55,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr uint32_t kM3 = 0x03030303u;
-#ifndef NNHIP_GEMM_WAVES_N
-#define NNHIP_GEMM_WAVES_N 4
-#endif
-#ifndef NNHIP_GEMM_WAVES_M
-#define NNHIP_GEMM_WAVES_M 1
-#endif
-#ifndef NNHIP_GEMM_KSPLIT
-#define NNHIP_GEMM_KSPLIT 2
-#endif
-constexpr int kWavesN = NNHIP_GEMM_WAVES_N, kWavesM = NNHIP_GEMM_WAVES_M;
-constexpr int kKSplit = NNHIP_GEMM_KSPLIT;   // waves sharing one output tile, splitting its k steps
-constexpr int kWaves = kWavesN * kWavesM * kKSplit;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kWavesPerSimd = kWaves / 4;
-constexpr int kBN = 256, kBM = 128;          // block tile (rows, tokens)
-constexpr int kRowTiles = kBN / 16;          // 16
-constexpr int kWaveRows = kBN / kWavesN, kWaveToks = kBM / kWavesM;
-constexpr int kRB = kWaveRows / 32, kTB = kWaveToks / 32;  // 32x32 MFMA tiles per wave
-constexpr int kSteps = kTileK / 32;          // 8 MFMA k steps per stage
-constexpr int kWaveSteps = kSteps / kKSplit; // steps one wave runs per stage
-constexpr int kMs = 2 / kKSplit;             // k halves (of each 64-k group) one wave multiplies
-#ifndef NNHIP_GEMM_SLOTS
-#define NNHIP_GEMM_SLOTS 2  // measured: 2 slots beat 3 (more DMA in flight only adds contention)
-#endif
-constexpr int kSlots = NNHIP_GEMM_SLOTS;      // LDS ring depth (stages in flight)
-constexpr int kABytes = kRowTiles * 1024;    // 16 KiB
-constexpr int kBBytes = kBM * kTileK;        // 32 KiB
-constexpr int kSlotBytes = kABytes + kBBytes;
-// k split: one 32x32 partial sum is 16 ints x 64 lanes = 4 KiB; each wave hands over half its row blocks
-constexpr int kPartBytes = kRB / 2 * kTB * 4096;
-constexpr int kRingBytes = kSlots * kSlotBytes;  // 144 KiB for three slots
-constexpr int kLdsMain = kKSplit == 2 && kWaves * kPartBytes > kRingBytes ? kWaves * kPartBytes : kRingBytes;
-// gated epilogue: per-token max |h| of each (wn, ks) wave row, reduced across the block
-constexpr int kAmaxRows = kWavesN * kKSplit;
-constexpr int kLdsBytes = kLdsMain + kAmaxRows * kBM * 4;
-// DMA instructions per wave per stage: A one row tile (1 KiB) each, B four token rows each
-// Waves 0 .. kDmaWaves-1 issue the DMA (with the default k split, the first wave of each pair:
-// the older wave of its SIMD, which the issue arbiter favours and which reaches the stage
-// barrier first)
-#ifndef NNHIP_GEMM_DMA_WAVES
-#define NNHIP_GEMM_DMA_WAVES (kWavesN * kWavesM)
-#endif
-constexpr int kDmaWaves = NNHIP_GEMM_DMA_WAVES;
-constexpr int kADma = kRowTiles / kDmaWaves, kBDma = kBM / 4 / kDmaWaves;
-constexpr int kDmaPerStage = kADma + kBDma;
-// The DMA of one stage is issued in kDmaParts pieces: the first right after the barrier that
-// frees its slot, the others at the start of the next stage's first kDmaParts - 1 steps.
-#ifndef NNHIP_GEMM_DMA_PARTS
-#define NNHIP_GEMM_DMA_PARTS 2
-#endif
-constexpr int kDmaParts = NNHIP_GEMM_DMA_PARTS;
-constexpr int kPartLoads = kDmaPerStage / kDmaParts;
 constexpr int kRsrcFlags = 0x00020000;
-
-static_assert(kWaves % 4 == 0 && kRB >= 1 && kTB >= 1, "wave layout");
-static_assert(kKSplit == 1 || (kKSplit == 2 && kRB % 2 == 0), "k split pairs finish one half of the row blocks each");
-static_assert(kDmaWaves <= kWaves && kADma * kDmaWaves == kRowTiles && kBDma * kDmaWaves * 4 == kBM, "DMA split");
-static_assert(kSlots >= 2 && kSlots <= 5 && 4 * kDmaPerStage < 63, "vmcnt range");
-static_assert(kDmaParts >= 1 && kDmaPerStage % kDmaParts == 0 && kDmaParts <= kWaveSteps, "DMA parts");
-static_assert(kTB * 32 * kTileK <= 65536, "B fragment offsets fit the ds_read immediate");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
 {
@@ -136,35 +80,6 @@ __device__ __forceinline__ void wait_lgkm0()
     __builtin_amdgcn_s_waitcnt(0xC07F);
 }
 
-// Wait until this wave's DMA of a stage has landed when `later` stages have been issued after
-// it (loads complete in order, kDmaPerStage per stage).
-__device__ __forceinline__ void wait_stage_landed(int later)
-{
-    if (later <= 0) wait_vmcnt<0>();
-    else if (later == 1) wait_vmcnt<kDmaPerStage>();
-    else if (later == 2) wait_vmcnt<2 * kDmaPerStage>();
-    else if (later == 3) wait_vmcnt<3 * kDmaPerStage>();
-    else wait_vmcnt<4 * kDmaPerStage>();
-}
-
-// Issue priority of a wave at step position `pos` of a barrier interval (0 = the step right
-// after the barrier, kWaveSteps - 1 = the step before it). The issue arbiter serves the
-// higher priority first and the older wave on a tie, so without this the older wave of a SIMD
-// runs ahead and idles at the barrier while the younger one finishes alone. Falling priority
-// keeps the two waves of a SIMD at the same step.
-#ifndef NNHIP_GEMM_PRIO
-#define NNHIP_GEMM_PRIO 1
-#endif
-__device__ __forceinline__ void step_prio(int pos)
-{
-    if (!NNHIP_GEMM_PRIO) return;
-    const int v = 3 - (pos * 4) / kWaveSteps;
-    if (v >= 3) __builtin_amdgcn_s_setprio(3);
-    else if (v == 2) __builtin_amdgcn_s_setprio(2);
-    else if (v == 1) __builtin_amdgcn_s_setprio(1);
-    else __builtin_amdgcn_s_setprio(0);
-}
-
 // Workgroup barrier without a memory fence. __syncthreads() (and any workgroup fence, even
 // one limited to LDS) makes the compiler wait for every outstanding buffer->LDS load
 // (vmcnt(0)), which drains the DMA ring each stage. Here the caller's explicit waits cover
@@ -178,163 +93,244 @@ __device__ __forceinline__ void lds_barrier()
     asm volatile("" ::: "memory");
 }
 
-struct Dma
+#ifndef NNHIP_GEMM_WAVES_N
+#define NNHIP_GEMM_WAVES_N 4
+#endif
+#ifndef NNHIP_GEMM_WAVES_M
+#define NNHIP_GEMM_WAVES_M 1
+#endif
+#ifndef NNHIP_GEMM_KSPLIT
+#define NNHIP_GEMM_KSPLIT 2
+#endif
+#ifndef NNHIP_GEMM_SLOTS
+#define NNHIP_GEMM_SLOTS 2  // 256 x 128 tile: 2 slots measured faster than 3
+#endif
+// DMA issuing waves (default: the first wave of each k-split pair) and pieces per stage
+#ifndef NNHIP_GEMM_DMA_WAVES
+#define NNHIP_GEMM_DMA_WAVES (kWavesN * kWavesM)
+#endif
+#ifndef NNHIP_GEMM_DMA_PARTS
+#define NNHIP_GEMM_DMA_PARTS 2
+#endif
+#ifndef NNHIP_GEMM_PRIO
+#define NNHIP_GEMM_PRIO 1
+#endif
+// One configuration of the kernel: block tile kBN_ rows x kBM_ tokens, kWavesN_ x kWavesM_
+// output tiles per block, each shared by kKSplit_ waves, a ring of kSlots_ LDS stages.
+template <int kBN_, int kBM_, int kWavesN_, int kWavesM_, int kKSplit_, int kSlots_>
+struct Gemm
 {
-    __amdgpu_buffer_rsrc_t ra, rb;
-    uint32_t a_voff;    // lane * 16 within a row tile
-    uint32_t b_voff[kBDma];
-    uint32_t a_row0;    // first row tile (global) of the block
-};
+    static constexpr int kWavesN = kWavesN_, kWavesM = kWavesM_;
+    static constexpr int kKSplit = kKSplit_;   // waves sharing one output tile, splitting its k steps
+    static constexpr int kWaves = kWavesN * kWavesM * kKSplit;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kWavesPerSimd = kWaves / 4;
+    static constexpr int kBN = kBN_, kBM = kBM_;        // block tile (rows, tokens)
+    static constexpr int kRowTiles = kBN / 16;
+    static constexpr int kWaveRows = kBN / kWavesN, kWaveToks = kBM / kWavesM;
+    static constexpr int kRB = kWaveRows / 32, kTB = kWaveToks / 32;  // 32x32 MFMA tiles per wave
+    static constexpr int kSteps = kTileK / 32;          // 8 MFMA k steps per stage
+    static constexpr int kWaveSteps = kSteps / kKSplit; // steps one wave runs per stage
+    static constexpr int kMs = 2 / kKSplit;             // k halves (of each 64-k group) one wave multiplies
+    static constexpr int kSlots = kSlots_;               // LDS ring depth (stages in flight)
+    static constexpr int kABytes = kRowTiles * 1024;
+    static constexpr int kBBytes = kBM * kTileK;
+    static constexpr int kSlotBytes = kABytes + kBBytes;
+    // k split: one 32x32 partial sum is 16 ints x 64 lanes = 4 KiB; each wave hands over half its row blocks
+    static constexpr int kPartBytes = kRB / 2 * kTB * 4096;
+    static constexpr int kRingBytes = kSlots * kSlotBytes;
+    static constexpr int kLdsMain = kKSplit == 2 && kWaves * kPartBytes > kRingBytes ? kWaves * kPartBytes : kRingBytes;
+    // gated epilogue: per-token max |h| of each (wn, ks) wave row, reduced across the block
+    static constexpr int kAmaxRows = kWavesN * kKSplit;
+    static constexpr int kLdsBytes = kLdsMain + kAmaxRows * kBM * 4;
+    // DMA instructions per wave per stage: A one row tile (1 KiB) each, B four token rows each
+    // Waves 0 .. kDmaWaves-1 issue the DMA (with the default k split, the first wave of each pair:
+    // the older wave of its SIMD, which the issue arbiter favours and which reaches the stage
+    // barrier first)
+    static constexpr int kDmaWaves = NNHIP_GEMM_DMA_WAVES;
+    static constexpr int kADma = kRowTiles / kDmaWaves, kBDma = kBM / 4 / kDmaWaves;
+    static constexpr int kDmaPerStage = kADma + kBDma;
+    // The DMA of one stage is issued in kDmaParts pieces: the first right after the barrier that
+    // frees its slot, the others at the start of the next stage's first kDmaParts - 1 steps.
+    static constexpr int kDmaParts = kDmaPerStage % NNHIP_GEMM_DMA_PARTS == 0 ? NNHIP_GEMM_DMA_PARTS : 1;
+    static constexpr int kPartLoads = kDmaPerStage / kDmaParts;
 
-// Issue loads [lo, hi) of this wave's share of k tile kt's DMA into LDS slot `slot`: the
-// wave's kADma A row tiles come first, then its kBDma groups of four B token rows. lo and hi
-// are constants at every (unrolled) call site.
-__device__ __forceinline__ void issue_loads(uint8_t* lds, const Dma& d, int slot, int kt, int KT, int lo, int hi)
-{
-    uint8_t* base = lds + slot * kSlotBytes;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (kDmaWaves < kWaves && wave >= kDmaWaves) return;
-#pragma unroll
-    for (int q = 0; q < kDmaPerStage; ++q)
+    static_assert(kWaves % 4 == 0 && kRB >= 1 && kTB >= 1, "wave layout");
+    static_assert(kKSplit == 1 || (kKSplit == 2 && kRB % 2 == 0), "k split pairs finish one half of the row blocks each");
+    static_assert(kDmaWaves <= kWaves && kADma * kDmaWaves == kRowTiles && kBDma * kDmaWaves * 4 == kBM, "DMA split");
+    static_assert(kSlots >= 2 && kSlots <= 6 && 4 * kDmaPerStage < 63, "vmcnt range");
+    static_assert(kDmaParts >= 1 && kDmaPerStage % kDmaParts == 0 && kDmaParts <= kWaveSteps, "DMA parts");
+    static_assert(kTB * 32 * kTileK <= 65536, "B fragment offsets fit the ds_read immediate");
+
+    // Wait until this wave's DMA of a stage has landed when `later` stages have been issued after
+    // it (loads complete in order, kDmaPerStage per stage).
+    static __device__ __forceinline__ void wait_stage_landed(int later)
     {
-        if (q < lo || q >= hi) continue;
-        if (q < kADma)
-        {
-            const int rt_local = wave * kADma + q;
-            const uint32_t soff = ((d.a_row0 + rt_local) * (uint32_t)KT + (uint32_t)kt) * 1024u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, (lds_void*)(base + rt_local * 1024), 16, d.a_voff, soff, 0,
-                                                     0);
-        }
-        else
-        {
-            // this instruction fills token rows 4*(wave*kBDma + i) .. +3 (1 KiB)
-            const int i = q - kADma;
-            uint8_t* dst = base + kABytes + (wave * kBDma + i) * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rb, (lds_void*)dst, 16, d.b_voff[i], (uint32_t)kt * kTileK, 0,
-                                                     0);
-        }
+        if (later <= 0) wait_vmcnt<0>();
+        else if (later == 1) wait_vmcnt<kDmaPerStage>();
+        else if (later == 2) wait_vmcnt<2 * kDmaPerStage>();
+        else if (later == 3) wait_vmcnt<3 * kDmaPerStage>();
+        else wait_vmcnt<4 * kDmaPerStage>();
     }
-}
 
-// The whole DMA of k tile kt (prologue stages).
-__device__ __forceinline__ void issue_stage(uint8_t* lds, const Dma& d, int slot, int kt, int KT)
-{
-    issue_loads(lds, d, slot, kt, KT, 0, kDmaPerStage);
-}
-
-// A words of one stage: row block rb, the wave's k half (T16K256 lane 16*(2m + h) + row%16;
-// the k half offset is part of p)
-__device__ __forceinline__ void read_a(v4i (&dst)[kRB][kMs], const uint8_t* p)
-{
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-#pragma unroll
-        for (int m = 0; m < kMs; ++m) dst[rb][m] = *reinterpret_cast<const v4i*>(p + rb * 2048 + m * 512);
-}
-
-// B fragments of one step for the wave's kTB token blocks (32 token rows = 8 KiB apart)
-__device__ __forceinline__ void read_b(v4i (&dst)[kTB], const uint8_t* p)
-{
-#pragma unroll
-    for (int n = 0; n < kTB; ++n) dst[n] = *reinterpret_cast<const v4i*>(p + n * 32 * kTileK);
-}
-
-struct Lane
-{
-    uint32_t a_off;              // A read offset within a slot
-    uint32_t b_off;              // B read offset within a slot (token row of block 0)
-    uint32_t b_step[kWaveSteps]; // swizzled chunk offset of the wave's step i
-};
-
-// One stage: the wave's 32-k steps (all eight, or the four of its k half). P selects the
-// register set holding this stage's A words; the next stage's go to the other set.
-template <int P>
-__device__ __forceinline__ void run_stage(int s, int KT, uint8_t* lds, const Dma& d, const Lane& ln,
-                                          v4i (&wa)[2][kRB][kMs], v4i (&bf)[2][kTB], v16i (&acc)[kRB][kTB])
-{
-    const uint8_t* slot = lds + (s % kSlots) * kSlotBytes;
-#pragma unroll
-    for (int i = 0; i < kWaveSteps; ++i)
+    // Issue priority of a wave at step position `pos` of a barrier interval (0 = the step right
+    // after the barrier, kWaveSteps - 1 = the step before it). The issue arbiter serves the
+    // higher priority first and the older wave on a tie, so without this the older wave of a SIMD
+    // runs ahead and idles at the barrier while the younger one finishes alone. Falling priority
+    // keeps the two waves of a SIMD at the same step.
+    static __device__ __forceinline__ void step_prio(int pos)
     {
-        const int j = i / kMs, m = i % kMs;  // 64-k group, and the k half within the wave's set
-        const int cur = i & 1, nxt = cur ^ 1;
-        if (i + 1 < kWaveSteps)
-        {
-            read_b(bf[nxt], slot + ln.b_off + ln.b_step[i + 1]);
-        }
-        else if (s + 1 < KT)
-        {
-            wait_lgkm0();  // this wave's reads of stage s have landed
-            wait_stage_landed(min(KT - 2 - s, kSlots - 2));  // its part of stage s+1 has landed
-            lds_barrier();  // all of stage s+1 is in LDS; nobody reads stage s's slot any more
-            if (s + kSlots < KT) issue_loads(lds, d, s % kSlots, s + kSlots, KT, 0, kPartLoads);
-            const uint8_t* nslot = lds + ((s + 1) % kSlots) * kSlotBytes;
-            read_a(wa[P ^ 1], nslot + ln.a_off);
-            read_b(bf[nxt], nslot + ln.b_off + ln.b_step[0]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        step_prio(i == kWaveSteps - 1 ? 0 : i + 1);
+        if (!NNHIP_GEMM_PRIO) return;
+        const int v = 3 - (pos * 4) / kWaveSteps;
+        if (v >= 3) __builtin_amdgcn_s_setprio(3);
+        else if (v == 2) __builtin_amdgcn_s_setprio(2);
+        else if (v == 1) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+    }
+
+    struct Dma
+    {
+        __amdgpu_buffer_rsrc_t ra, rb;
+        uint32_t a_voff;    // lane * 16 within a row tile
+        uint32_t b_voff[kBDma];
+        uint32_t a_row0;    // first row tile (global) of the block
+    };
+
+    // Issue loads [lo, hi) of this wave's share of k tile kt's DMA into LDS slot `slot`: the
+    // wave's kADma A row tiles come first, then its kBDma groups of four B token rows. lo and hi
+    // are constants at every (unrolled) call site.
+    static __device__ __forceinline__ void issue_loads(uint8_t* lds, const Dma& d, int slot, int kt, int KT, int lo, int hi)
+    {
+        uint8_t* base = lds + slot * kSlotBytes;
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if (kDmaWaves < kWaves && wave >= kDmaWaves) return;
 #pragma unroll
-        for (int rb = 0; rb < kRB; ++rb)
+        for (int q = 0; q < kDmaPerStage; ++q)
         {
-            const v4i a = (v4i)((__builtin_bit_cast(u32x4, wa[P][rb][m]) >> (2 * j)) & kM3);
-#pragma unroll
-            for (int n = 0; n < kTB; ++n) acc[rb][n] = mfma32(a, bf[cur][n], acc[rb][n]);
-            if (rb == 0 && i + 1 < kDmaParts)
+            if (q < lo || q >= hi) continue;
+            if (q < kADma)
             {
-                // piece i+1 of the DMA of stage s+kSlots-1, whose first piece went out at the
-                // barrier of stage s-1 (stages below kSlots were issued whole in the prologue)
-                const int t = s + kSlots - 1;
-                __builtin_amdgcn_sched_barrier(0);
-                if (s >= 1 && t < KT)
-                    issue_loads(lds, d, (s - 1) % kSlots, t, KT, (i + 1) * kPartLoads, (i + 2) * kPartLoads);
-                __builtin_amdgcn_sched_barrier(0);
+                const int rt_local = wave * kADma + q;
+                const uint32_t soff = ((d.a_row0 + rt_local) * (uint32_t)KT + (uint32_t)kt) * 1024u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, (lds_void*)(base + rt_local * 1024), 16, d.a_voff, soff, 0,
+                                                         0);
+            }
+            else
+            {
+                // this instruction fills token rows 4*(wave*kBDma + i) .. +3 (1 KiB)
+                const int i = q - kADma;
+                uint8_t* dst = base + kABytes + (wave * kBDma + i) * 1024;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rb, (lds_void*)dst, 16, d.b_voff[i], (uint32_t)kt * kTileK, 0,
+                                                         0);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
-}
 
-// Epilogue operands of the row blocks a wave finishes (kRBf of them, from rb0 on), loaded
-// before the k-split exchange so that their latency hides behind it. The 32x32 accumulator
-// layout puts element i of lane l at row 8*(i/4) + 4*(l/32) + i%4, token l%32. Buffer loads:
-// rows past N and tokens past M read zero; without a bias the bias values are zero.
-constexpr int kRBf = kRB / kKSplit;
-struct EpiOps
-{
-    int rs2[kTB];        // 2 * rowsum of the lane's tokens
-    float sv[kTB];       // activation scale of the lane's tokens
-    float tv[kRBf][16];  // tau of the lane's accumulator rows
-    float bv[kRBf][16];  // bias of the lane's accumulator rows
-};
-
-__device__ __forceinline__ void load_epilogue(const GemvProblem& p, EpiOps& e, int rb0, int row_w, int tok_w, int h,
-                                              int l32)
-{
-    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
-    const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
-    const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
-#pragma unroll
-    for (int n = 0; n < kTB; ++n)
+    // The whole DMA of k tile kt (prologue stages).
+    static __device__ __forceinline__ void issue_stage(uint8_t* lds, const Dma& d, int slot, int kt, int KT)
     {
-        const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
-        e.rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
-        e.sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+        issue_loads(lds, d, slot, kt, KT, 0, kDmaPerStage);
     }
-#pragma unroll
-    for (int r = 0; r < kRBf; ++r)
+
+    // A words of one stage: row block rb, the wave's k half (T16K256 lane 16*(2m + h) + row%16;
+    // the k half offset is part of p)
+    static __device__ __forceinline__ void read_a(v4i (&dst)[kRB][kMs], const uint8_t* p)
     {
-        const uint32_t row0 = (uint32_t)(row_w + (rb0 + r) * 32 + 4 * h);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+            for (int m = 0; m < kMs; ++m) dst[rb][m] = *reinterpret_cast<const v4i*>(p + rb * 2048 + m * 512);
+    }
+
+    // B fragments of one step for the wave's kTB token blocks (32 token rows = 8 KiB apart)
+    static __device__ __forceinline__ void read_b(v4i (&dst)[kTB], const uint8_t* p)
+    {
+#pragma unroll
+        for (int n = 0; n < kTB; ++n) dst[n] = *reinterpret_cast<const v4i*>(p + n * 32 * kTileK);
+    }
+
+    struct Lane
+    {
+        uint32_t a_off;              // A read offset within a slot
+        uint32_t b_off;              // B read offset within a slot (token row of block 0)
+        uint32_t b_step[kWaveSteps]; // swizzled chunk offset of the wave's step i
+    };
+
+    // One stage: the wave's 32-k steps (all eight, or the four of its k half). P selects the
+    // register set holding this stage's A words; the next stage's go to the other set.
+    template <int P>
+    static __device__ __forceinline__ void run_stage(int s, int KT, uint8_t* lds, const Dma& d, const Lane& ln,
+                                              v4i (&wa)[2][kRB][kMs], v4i (&bf)[2][kTB], v16i (&acc)[kRB][kTB])
+    {
+        const uint8_t* slot = lds + (s % kSlots) * kSlotBytes;
+#pragma unroll
+        for (int i = 0; i < kWaveSteps; ++i)
         {
-            const uint32_t row = row0 + (uint32_t)(8 * (i >> 2) + (i & 3));
-            e.tv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
+            const int j = i / kMs, m = i % kMs;  // 64-k group, and the k half within the wave's set
+            const int cur = i & 1, nxt = cur ^ 1;
+            if (i + 1 < kWaveSteps)
+            {
+                read_b(bf[nxt], slot + ln.b_off + ln.b_step[i + 1]);
+            }
+            else if (s + 1 < KT)
+            {
+                wait_lgkm0();  // this wave's reads of stage s have landed
+                wait_stage_landed(min(KT - 2 - s, kSlots - 2));  // its part of stage s+1 has landed
+                lds_barrier();  // all of stage s+1 is in LDS; nobody reads stage s's slot any more
+                if (s + kSlots < KT) issue_loads(lds, d, s % kSlots, s + kSlots, KT, 0, kPartLoads);
+                const uint8_t* nslot = lds + ((s + 1) % kSlots) * kSlotBytes;
+                read_a(wa[P ^ 1], nslot + ln.a_off);
+                read_b(bf[nxt], nslot + ln.b_off + ln.b_step[0]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            step_prio(i == kWaveSteps - 1 ? 0 : i + 1);
+#pragma unroll
+            for (int rb = 0; rb < kRB; ++rb)
+            {
+                const v4i a = (v4i)((__builtin_bit_cast(u32x4, wa[P][rb][m]) >> (2 * j)) & kM3);
+#pragma unroll
+                for (int n = 0; n < kTB; ++n) acc[rb][n] = mfma32(a, bf[cur][n], acc[rb][n]);
+                if (rb == 0 && i + 1 < kDmaParts)
+                {
+                    // piece i+1 of the DMA of stage s+kSlots-1, whose first piece went out at the
+                    // barrier of stage s-1 (stages below kSlots were issued whole in the prologue)
+                    const int t = s + kSlots - 1;
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (s >= 1 && t < KT)
+                        issue_loads(lds, d, (s - 1) % kSlots, t, KT, (i + 1) * kPartLoads, (i + 2) * kPartLoads);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    if (p.bias)
+
+    // Epilogue operands of the row blocks a wave finishes (kRBf of them, from rb0 on), loaded
+    // before the k-split exchange so that their latency hides behind it. The 32x32 accumulator
+    // layout puts element i of lane l at row 8*(i/4) + 4*(l/32) + i%4, token l%32. Buffer loads:
+    // rows past N and tokens past M read zero; without a bias the bias values are zero.
+    static constexpr int kRBf = kRB / kKSplit;
+    struct EpiOps
     {
-        const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias, (uint32_t)p.N * 4u);
+        int rs2[kTB];        // 2 * rowsum of the lane's tokens
+        float sv[kTB];       // activation scale of the lane's tokens
+        float tv[kRBf][16];  // tau of the lane's accumulator rows
+        float bv[kRBf][16];  // bias of the lane's accumulator rows
+    };
+
+    static __device__ __forceinline__ void load_epilogue(const GemvProblem& p, EpiOps& e, int rb0, int row_w, int tok_w, int h,
+                                                  int l32)
+    {
+        const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
+        const __amdgpu_buffer_rsrc_t rs_r = rsrc(p.rowsum, (uint32_t)p.M * 4u);
+        const __amdgpu_buffer_rsrc_t rs_s = rsrc(p.s, (uint32_t)p.M * 4u);
+#pragma unroll
+        for (int n = 0; n < kTB; ++n)
+        {
+            const uint32_t m = (uint32_t)(tok_w + n * 32 + l32);
+            e.rs2[n] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rs_r, m * 4u, 0, 0));
+            e.sv[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s, m * 4u, 0, 0));
+        }
 #pragma unroll
         for (int r = 0; r < kRBf; ++r)
         {
@@ -343,352 +339,412 @@ __device__ __forceinline__ void load_epilogue(const GemvProblem& p, EpiOps& e, i
             for (int i = 0; i < 16; ++i)
             {
                 const uint32_t row = row0 + (uint32_t)(8 * (i >> 2) + (i & 3));
-                e.bv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
+                e.tv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, row * 4u, 0, 0));
             }
         }
-    }
-    else
-    {
-#pragma unroll
-        for (int r = 0; r < kRBf; ++r)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) e.bv[r][i] = 0.0f;
-    }
-}
-
-// Index of row block rb (a compile-time loop index in [rb0, rb0 + nrb)) within EpiOps.
-__device__ __forceinline__ int epi_slot(int rb) { return kRBf == 1 ? 0 : rb; }
-
-// Epilogue of a block that lies wholly inside Y: no masks; row offsets are scalar.
-template <bool kBias>
-__device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
-                                           int nrb, int row_w, int tok_w, int h, int l32)
-{
-    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
-    const uint32_t M4 = (uint32_t)p.M * 4u;
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-    {
-        if (rb < rb0 || rb >= rb0 + nrb) continue;
-        const int r = epi_slot(rb);
-        const uint32_t row0 = (uint32_t)(row_w + rb * 32 + 4 * h);
-        const uint32_t vbase = (row0 * (uint32_t)p.M + (uint32_t)(tok_w + l32)) * 4u;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
+        if (p.bias)
         {
-            const int soff = (8 * (i >> 2) + (i & 3)) * (int)M4;
+            const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias, (uint32_t)p.N * 4u);
 #pragma unroll
-            for (int n = 0; n < kTB; ++n)
+            for (int r = 0; r < kRBf; ++r)
             {
-                const int a = acc[rb][n][i] - e.rs2[n];
-                float y = (e.tv[r][i] * e.sv[n]) * (float)a;
-                if (kBias) y = y + e.bv[r][i];
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, vbase + (uint32_t)(n * 128),
-                                                      soff, 0);
+                const uint32_t row0 = (uint32_t)(row_w + (rb0 + r) * 32 + 4 * h);
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                {
+                    const uint32_t row = row0 + (uint32_t)(8 * (i >> 2) + (i & 3));
+                    e.bv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, row * 4u, 0, 0));
+                }
             }
         }
-    }
-}
-
-// Epilogue of an edge block: rows past N and tokens past M are masked (their lanes store to
-// an out-of-range offset, which the buffer unit drops).
-__device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
-                                           int nrb, int row_w, int tok_w, int h, int l32)
-{
-    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
-    {
-        if (rb < rb0 || rb >= rb0 + nrb) continue;
-        const int r = epi_slot(rb);
-        const int row0 = row_w + rb * 32 + 4 * h;
-#pragma unroll
-        for (int n = 0; n < kTB; ++n)
+        else
         {
-            const int m = tok_w + n * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < kRBf; ++r)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) e.bv[r][i] = 0.0f;
+        }
+    }
+
+    // Index of row block rb (a compile-time loop index in [rb0, rb0 + nrb)) within EpiOps.
+    static __device__ __forceinline__ int epi_slot(int rb) { return kRBf == 1 ? 0 : rb; }
+
+    // Epilogue of a block that lies wholly inside Y: no masks; row offsets are scalar.
+    template <bool kBias>
+    static __device__ __forceinline__ void store_full(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
+                                               int nrb, int row_w, int tok_w, int h, int l32)
+    {
+        const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+        const uint32_t M4 = (uint32_t)p.M * 4u;
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb)
+        {
+            if (rb < rb0 || rb >= rb0 + nrb) continue;
+            const int r = epi_slot(rb);
+            const uint32_t row0 = (uint32_t)(row_w + rb * 32 + 4 * h);
+            const uint32_t vbase = (row0 * (uint32_t)p.M + (uint32_t)(tok_w + l32)) * 4u;
 #pragma unroll
             for (int i = 0; i < 16; ++i)
             {
-                const int row = row0 + 8 * (i >> 2) + (i & 3);
-                const int a = acc[rb][n][i] - e.rs2[n];
-                float y = (e.tv[r][i] * e.sv[n]) * (float)a;
-                if (p.bias) y = y + e.bv[r][i];
-                const uint32_t off = (row < p.N && m < p.M) ? ((uint32_t)row * (uint32_t)p.M + (uint32_t)m) * 4u
-                                                             : 0xFFFFFFF0u;
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
+                const int soff = (8 * (i >> 2) + (i & 3)) * (int)M4;
+#pragma unroll
+                for (int n = 0; n < kTB; ++n)
+                {
+                    const int a = acc[rb][n][i] - e.rs2[n];
+                    float y = (e.tv[r][i] * e.sv[n]) * (float)a;
+                    if (kBias) y = y + e.bv[r][i];
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, vbase + (uint32_t)(n * 128),
+                                                          soff, 0);
+                }
             }
         }
     }
-}
 
-// Epilogue of the fused gated activation (p.glu != 0). Rows are in the interleaved GLU order
-// (16-row group t = gate rows of features 8t..8t+7, then their up rows), so accumulator element
-// i (row 8*(i/4) + 4h + i%4 of the 32-row block) and element i + 4 (8 rows below) are gate and
-// up of one feature when i/4 is even. Each is rescaled exactly as the plain epilogue does
-// ((tau * s) * float(acc) [+ bias]), then combined by glu_one; h (glu_F, M) gets the result.
-// With p.amax, the block also folds max |h| per token (NaN ignored, as `a > m ? a : m` from 0
-// does) into p.amax (float bits; non-negative floats order as unsigned integers) with one
-// atomic max per token: the absmax of the next activation quantization, order-independent.
-__device__ __forceinline__ void store_glu(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
-                                          int nrb, int row_w, int tok_w, int h, int l32, uint8_t* lds, int amax_row,
-                                          int tok_local, int m0)
-{
-    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.glu_F * (uint32_t)p.M * 4u);
-    const int act = p.glu - 1;
-    float mx[kTB];
-#pragma unroll
-    for (int n = 0; n < kTB; ++n) mx[n] = 0.0f;
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb)
+    // Epilogue of an edge block: rows past N and tokens past M are masked (their lanes store to
+    // an out-of-range offset, which the buffer unit drops).
+    static __device__ __forceinline__ void store_edge(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
+                                               int nrb, int row_w, int tok_w, int h, int l32)
     {
-        if (rb < rb0 || rb >= rb0 + nrb) continue;
-        const int r = epi_slot(rb);
-        const int row0 = row_w + rb * 32 + 4 * h;
+        const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
+        for (int rb = 0; rb < kRB; ++rb)
         {
-            const int i = (q / 4) * 8 + (q % 4);  // gate element: i / 4 in {0, 2}
-            const uint32_t rg = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3));
-            const int f = 8 * (int)(rg / 16u) + (int)(rg % 16u);
+            if (rb < rb0 || rb >= rb0 + nrb) continue;
+            const int r = epi_slot(rb);
+            const int row0 = row_w + rb * 32 + 4 * h;
 #pragma unroll
             for (int n = 0; n < kTB; ++n)
             {
                 const int m = tok_w + n * 32 + l32;
-                float yg = (e.tv[r][i] * e.sv[n]) * (float)(acc[rb][n][i] - e.rs2[n]);
-                float yu = (e.tv[r][i + 4] * e.sv[n]) * (float)(acc[rb][n][i + 4] - e.rs2[n]);
-                if (p.bias)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
                 {
-                    yg = yg + e.bv[r][i];
-                    yu = yu + e.bv[r][i + 4];
+                    const int row = row0 + 8 * (i >> 2) + (i & 3);
+                    const int a = acc[rb][n][i] - e.rs2[n];
+                    float y = (e.tv[r][i] * e.sv[n]) * (float)a;
+                    if (p.bias) y = y + e.bv[r][i];
+                    const uint32_t off = (row < p.N && m < p.M) ? ((uint32_t)row * (uint32_t)p.M + (uint32_t)m) * 4u
+                                                                 : 0xFFFFFFF0u;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
                 }
-                const float y = glu_one(yg, yu, act);
-                const bool in = f < p.glu_F && m < p.M;
-                const uint32_t off = in ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)m) * 4u : 0xFFFFFFF0u;
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
-                const float a = fabsf(y);
-                if (in && a > mx[n]) mx[n] = a;
             }
         }
     }
-    if (!p.amax) return;
-    // lanes l and l ^ 32 hold the same tokens (other rows); then one row of LDS per wave
-    float* red = reinterpret_cast<float*>(lds + kLdsMain);
-#pragma unroll
-    for (int n = 0; n < kTB; ++n)
-    {
-        mx[n] = fmaxf(mx[n], __shfl_xor(mx[n], 32));
-        if (h == 0) red[amax_row * kBM + tok_local + n * 32 + l32] = mx[n];
-    }
-    wait_lgkm0();   // this wave's LDS writes are done; the h stores stay in flight
-    lds_barrier();
-    const int t = threadIdx.x;
-    if (t < kBM && m0 + t < p.M)
-    {
-        float v = red[t];
-#pragma unroll
-        for (int w = 1; w < kAmaxRows; ++w) v = fmaxf(v, red[w * kBM + t]);
-        __hip_atomic_fetch_max(p.amax + m0 + t, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
 
-// k split: wave KS of a pair hands the partial sums of the row blocks its partner finishes to
-// the partner through LDS (put_partials), and after a barrier adds the partner's partials of
-// its own row blocks (add_partials).
-
-template <int KS>
-__device__ __forceinline__ void put_partials(const v16i (&acc)[kRB][kTB], uint8_t* lds, int wave, int lane)
-{
-    constexpr int kHalf = kRB / 2;
-    v4i* mine = reinterpret_cast<v4i*>(lds + wave * kPartBytes);
+    // Epilogue of the fused gated activation (p.glu != 0). Rows are in the interleaved GLU order
+    // (16-row group t = gate rows of features 8t..8t+7, then their up rows), so accumulator element
+    // i (row 8*(i/4) + 4h + i%4 of the 32-row block) and element i + 4 (8 rows below) are gate and
+    // up of one feature when i/4 is even. Each is rescaled exactly as the plain epilogue does
+    // ((tau * s) * float(acc) [+ bias]), then combined by glu_one; h (glu_F, M) gets the result.
+    // With p.amax, the block also folds max |h| per token (NaN ignored, as `a > m ? a : m` from 0
+    // does) into p.amax (float bits; non-negative floats order as unsigned integers) with one
+    // atomic max per token: the absmax of the next activation quantization, order-independent.
+    static __device__ __forceinline__ void store_glu(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
+                                              int nrb, int row_w, int tok_w, int h, int l32, uint8_t* lds, int amax_row,
+                                              int tok_local, int m0)
+    {
+        const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.glu_F * (uint32_t)p.M * 4u);
+        const int act = p.glu - 1;
+        float mx[kTB];
 #pragma unroll
-    for (int r = 0; r < kHalf; ++r)
+        for (int n = 0; n < kTB; ++n) mx[n] = 0.0f;
 #pragma unroll
-        for (int n = 0; n < kTB; ++n)
+        for (int rb = 0; rb < kRB; ++rb)
+        {
+            if (rb < rb0 || rb >= rb0 + nrb) continue;
+            const int r = epi_slot(rb);
+            const int row0 = row_w + rb * 32 + 4 * h;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < 8; ++q)
             {
-                const v16i& a = acc[(1 - KS) * kHalf + r][n];
-                mine[((r * kTB + n) * 4 + q) * 64 + lane] = v4i{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-            }
-}
-
-template <int KS>
-__device__ __forceinline__ void add_partials(v16i (&acc)[kRB][kTB], const uint8_t* lds, int wave, int lane)
-{
-    constexpr int kHalf = kRB / 2;
-    const v4i* theirs = reinterpret_cast<const v4i*>(lds + (wave ^ (kWavesN * kWavesM)) * kPartBytes);
+                const int i = (q / 4) * 8 + (q % 4);  // gate element: i / 4 in {0, 2}
+                const uint32_t rg = (uint32_t)(row0 + 8 * (i >> 2) + (i & 3));
+                const int f = 8 * (int)(rg / 16u) + (int)(rg % 16u);
 #pragma unroll
-    for (int r = 0; r < kHalf; ++r)
-    {
-        // all reads of the row block first (one LDS round trip), then the adds
-        v4i o[kTB][4];
+                for (int n = 0; n < kTB; ++n)
+                {
+                    const int m = tok_w + n * 32 + l32;
+                    float yg = (e.tv[r][i] * e.sv[n]) * (float)(acc[rb][n][i] - e.rs2[n]);
+                    float yu = (e.tv[r][i + 4] * e.sv[n]) * (float)(acc[rb][n][i + 4] - e.rs2[n]);
+                    if (p.bias)
+                    {
+                        yg = yg + e.bv[r][i];
+                        yu = yu + e.bv[r][i + 4];
+                    }
+                    const float y = glu_one(yg, yu, act);
+                    const bool in = f < p.glu_F && m < p.M;
+                    const uint32_t off = in ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)m) * 4u : 0xFFFFFFF0u;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
+                    const float a = fabsf(y);
+                    if (in && a > mx[n]) mx[n] = a;
+                }
+            }
+        }
+        if (!p.amax) return;
+        // lanes l and l ^ 32 hold the same tokens (other rows); then one row of LDS per wave
+        float* red = reinterpret_cast<float*>(lds + kLdsMain);
 #pragma unroll
         for (int n = 0; n < kTB; ++n)
+        {
+            mx[n] = fmaxf(mx[n], __shfl_xor(mx[n], 32));
+            if (h == 0) red[amax_row * kBM + tok_local + n * 32 + l32] = mx[n];
+        }
+        wait_lgkm0();   // this wave's LDS writes are done; the h stores stay in flight
+        lds_barrier();
+        const int t = threadIdx.x;
+        if (t < kBM && m0 + t < p.M)
+        {
+            float v = red[t];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) o[n][q] = theirs[((r * kTB + n) * 4 + q) * 64 + lane];
-#pragma unroll
-        for (int n = 0; n < kTB; ++n)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-            {
-                v16i& a = acc[KS * kHalf + r][n];
-                a[4 * q] += o[n][q][0];
-                a[4 * q + 1] += o[n][q][1];
-                a[4 * q + 2] += o[n][q][2];
-                a[4 * q + 3] += o[n][q][3];
-            }
+            for (int w = 1; w < kAmaxRows; ++w) v = fmaxf(v, red[w * kBM + t]);
+            __hip_atomic_fetch_max(p.amax + m0 + t, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-}
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd))) void
+    // k split: wave KS of a pair hands the partial sums of the row blocks its partner finishes to
+    // the partner through LDS (put_partials), and after a barrier adds the partner's partials of
+    // its own row blocks (add_partials).
+
+    template <int KS>
+    static __device__ __forceinline__ void put_partials(const v16i (&acc)[kRB][kTB], uint8_t* lds, int wave, int lane)
+    {
+        constexpr int kHalf = kRB / 2;
+        v4i* mine = reinterpret_cast<v4i*>(lds + wave * kPartBytes);
+#pragma unroll
+        for (int r = 0; r < kHalf; ++r)
+#pragma unroll
+            for (int n = 0; n < kTB; ++n)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    const v16i& a = acc[(1 - KS) * kHalf + r][n];
+                    mine[((r * kTB + n) * 4 + q) * 64 + lane] = v4i{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                }
+    }
+
+    template <int KS>
+    static __device__ __forceinline__ void add_partials(v16i (&acc)[kRB][kTB], const uint8_t* lds, int wave, int lane)
+    {
+        constexpr int kHalf = kRB / 2;
+        const v4i* theirs = reinterpret_cast<const v4i*>(lds + (wave ^ (kWavesN * kWavesM)) * kPartBytes);
+#pragma unroll
+        for (int r = 0; r < kHalf; ++r)
+        {
+            // all reads of the row block first (one LDS round trip), then the adds
+            v4i o[kTB][4];
+#pragma unroll
+            for (int n = 0; n < kTB; ++n)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[n][q] = theirs[((r * kTB + n) * 4 + q) * 64 + lane];
+#pragma unroll
+            for (int n = 0; n < kTB; ++n)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    v16i& a = acc[KS * kHalf + r][n];
+                    a[4 * q] += o[n][q][0];
+                    a[4 * q + 1] += o[n][q][1];
+                    a[4 * q + 2] += o[n][q][2];
+                    a[4 * q + 3] += o[n][q][3];
+                }
+        }
+    }
+
+    static __device__ __forceinline__ void body(const GemvProblem& p, int n_mblocks, int n_nblocks, int xcd_mode)
+    {
+        extern __shared__ __align__(16) uint8_t lds[];
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int wn = wave % kWavesN, wm = (wave / kWavesN) % kWavesM, ks = wave / (kWavesN * kWavesM);
+        const int KT = p.KT;
+        const uint32_t Kp = (uint32_t)KT * kTileK;
+        const int RT = (p.N + 15) / 16;
+
+        // ---- block -> (token block, row block)
+        int mb, nb;
+        const int b = blockIdx.x;
+        if (xcd_mode)
+        {
+            const int xcd = b & 7, l = b >> 3;
+            const int per_xcd = n_mblocks >> 3;  // token blocks per XCD
+            mb = xcd * per_xcd + l / n_nblocks;
+            nb = l % n_nblocks;
+        }
+        else
+        {
+            mb = b / n_nblocks;
+            nb = b % n_nblocks;
+        }
+        const int m0 = mb * kBM;
+        const int rt0 = nb * kRowTiles;
+
+        // ---- DMA descriptors
+        Dma d;
+        d.ra = rsrc(p.rp, (uint32_t)RT * (uint32_t)KT * 1024u);  // rows past N read zero (code 0)
+        d.rb = rsrc(p.xi, (uint32_t)p.M * Kp);                    // tokens past M read zero
+        d.a_voff = (uint32_t)lane * 16u;
+        d.a_row0 = (uint32_t)rt0;
+#pragma unroll
+        for (int i = 0; i < kBDma; ++i)
+        {
+            const int row = (wave * kBDma + i) * 4 + (lane >> 4);  // token row within the block
+            const int pos = lane & 15;                             // chunk position in the LDS row
+            const int c = pos ^ (row & 15);                        // global chunk stored there
+            const int m = m0 + row;
+            d.b_voff[i] = m < p.M ? (uint32_t)m * Kp + (uint32_t)c * 16u : 0x80000000u;
+        }
+
+        // ---- per-lane LDS read offsets
+        const int h = lane >> 5, l32 = lane & 31;
+        Lane ln;
+        ln.a_off = (uint32_t)((wn * (kWaveRows / 16) + (l32 >> 4)) * 1024 + (16 * h + (l32 & 15)) * 16 +
+                              (kKSplit == 2 ? ks * 512 : 0));
+        ln.b_off = (uint32_t)(kABytes + (wm * kWaveToks + l32) * kTileK);
+        const int rsw = h ^ (l32 & 15);  // token row % 16 is l32 % 16 for every token block
+#pragma unroll
+        for (int i = 0; i < kWaveSteps; ++i)
+        {
+            const int j = i / kMs, m = kKSplit == 2 ? ks : i % kMs;
+            const int c0 = 4 * j + 2 * m;  // chunk of lane half 0 for step (j, m)
+            ln.b_step[i] = (uint32_t)((c0 ^ rsw) << 4);
+        }
+
+        v16i acc[kRB][kTB];
+#pragma unroll
+        for (int i = 0; i < kRB; ++i)
+#pragma unroll
+            for (int n = 0; n < kTB; ++n) acc[i][n] = v16i{};
+
+        // ---- prologue: three stages in flight, then stage 0's first reads
+        issue_stage(lds, d, 0, 0, KT);
+#pragma unroll
+        for (int i = 1; i < kSlots; ++i)
+            if (i < KT) issue_stage(lds, d, i, i, KT);
+        wait_stage_landed(min(KT - 1, kSlots - 1));
+        lds_barrier();
+        v4i wa[2][kRB][kMs];
+        v4i bf[2][kTB];
+        read_a(wa[0], lds + ln.a_off);
+        read_b(bf[0], lds + ln.b_off + ln.b_step[0]);
+
+        int s = 0;
+        for (; s + 1 < KT; s += 2)
+        {
+            run_stage<0>(s, KT, lds, d, ln, wa, bf, acc);
+            run_stage<1>(s + 1, KT, lds, d, ln, wa, bf, acc);
+        }
+        if (s < KT) run_stage<0>(s, KT, lds, d, ln, wa, bf, acc);
+
+        // ---- epilogue operands (issued before the k-split exchange, whose LDS round trip hides
+        // their latency), then the exchange: the two waves of a pair swap partial sums through LDS;
+        // wave ks finishes row blocks [ks * kRB / 2, (ks + 1) * kRB / 2).
+        const int row_w = (rt0 + wn * (kWaveRows / 16)) * 16;
+        const int tok_w = m0 + wm * kWaveToks;
+        int rb0 = 0, nrb = kRB;
+        if (kKSplit == 2)
+        {
+            rb0 = ks * (kRB / 2);
+            nrb = kRB / 2;
+        }
+        wait_lgkm0();
+        wait_vmcnt<0>();
+        EpiOps e;
+        load_epilogue(p, e, rb0, row_w, tok_w, h, l32);
+        if (kKSplit == 2)
+        {
+            lds_barrier();  // every wave is done with the ring
+            if (ks == 0) put_partials<0>(acc, lds, wave, lane);
+            else put_partials<1>(acc, lds, wave, lane);
+            lds_barrier();
+            if (ks == 0) add_partials<0>(acc, lds, wave, lane);
+            else add_partials<1>(acc, lds, wave, lane);
+        }
+
+        // ---- epilogue
+        const bool full = rt0 * 16 + kBN <= p.N && m0 + kBM <= p.M;
+        if (p.glu)
+        {
+            store_glu(p, acc, e, rb0, nrb, row_w, tok_w, h, l32, lds, wn * kKSplit + ks, wm * kWaveToks, m0);
+        }
+        else if (full)
+        {
+            if (p.bias) store_full<true>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
+            else store_full<false>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
+        }
+        else
+        {
+            store_edge(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
+        }
+    }
+};
+
+template <class G>
+__global__ __launch_bounds__(G::kThreads) __attribute__((amdgpu_waves_per_eu(G::kWavesPerSimd, G::kWavesPerSimd))) void
 k_gemm(GemvProblem p, int n_mblocks, int n_nblocks, int xcd_mode)
 {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave % kWavesN, wm = (wave / kWavesN) % kWavesM, ks = wave / (kWavesN * kWavesM);
-    const int KT = p.KT;
-    const uint32_t Kp = (uint32_t)KT * kTileK;
-    const int RT = (p.N + 15) / 16;
-
-    // ---- block -> (token block, row block)
-    int mb, nb;
-    const int b = blockIdx.x;
-    if (xcd_mode)
-    {
-        const int xcd = b & 7, l = b >> 3;
-        const int per_xcd = n_mblocks >> 3;  // token blocks per XCD
-        mb = xcd * per_xcd + l / n_nblocks;
-        nb = l % n_nblocks;
-    }
-    else
-    {
-        mb = b / n_nblocks;
-        nb = b % n_nblocks;
-    }
-    const int m0 = mb * kBM;
-    const int rt0 = nb * kRowTiles;
-
-    // ---- DMA descriptors
-    Dma d;
-    d.ra = rsrc(p.rp, (uint32_t)RT * (uint32_t)KT * 1024u);  // rows past N read zero (code 0)
-    d.rb = rsrc(p.xi, (uint32_t)p.M * Kp);                    // tokens past M read zero
-    d.a_voff = (uint32_t)lane * 16u;
-    d.a_row0 = (uint32_t)rt0;
-#pragma unroll
-    for (int i = 0; i < kBDma; ++i)
-    {
-        const int row = (wave * kBDma + i) * 4 + (lane >> 4);  // token row within the block
-        const int pos = lane & 15;                             // chunk position in the LDS row
-        const int c = pos ^ (row & 15);                        // global chunk stored there
-        const int m = m0 + row;
-        d.b_voff[i] = m < p.M ? (uint32_t)m * Kp + (uint32_t)c * 16u : 0x80000000u;
-    }
-
-    // ---- per-lane LDS read offsets
-    const int h = lane >> 5, l32 = lane & 31;
-    Lane ln;
-    ln.a_off = (uint32_t)((wn * (kWaveRows / 16) + (l32 >> 4)) * 1024 + (16 * h + (l32 & 15)) * 16 +
-                          (kKSplit == 2 ? ks * 512 : 0));
-    ln.b_off = (uint32_t)(kABytes + (wm * kWaveToks + l32) * kTileK);
-    const int rsw = h ^ (l32 & 15);  // token row % 16 is l32 % 16 for every token block
-#pragma unroll
-    for (int i = 0; i < kWaveSteps; ++i)
-    {
-        const int j = i / kMs, m = kKSplit == 2 ? ks : i % kMs;
-        const int c0 = 4 * j + 2 * m;  // chunk of lane half 0 for step (j, m)
-        ln.b_step[i] = (uint32_t)((c0 ^ rsw) << 4);
-    }
-
-    v16i acc[kRB][kTB];
-#pragma unroll
-    for (int i = 0; i < kRB; ++i)
-#pragma unroll
-        for (int n = 0; n < kTB; ++n) acc[i][n] = v16i{};
-
-    // ---- prologue: three stages in flight, then stage 0's first reads
-    issue_stage(lds, d, 0, 0, KT);
-#pragma unroll
-    for (int i = 1; i < kSlots; ++i)
-        if (i < KT) issue_stage(lds, d, i, i, KT);
-    wait_stage_landed(min(KT - 1, kSlots - 1));
-    lds_barrier();
-    v4i wa[2][kRB][kMs];
-    v4i bf[2][kTB];
-    read_a(wa[0], lds + ln.a_off);
-    read_b(bf[0], lds + ln.b_off + ln.b_step[0]);
-
-    int s = 0;
-    for (; s + 1 < KT; s += 2)
-    {
-        run_stage<0>(s, KT, lds, d, ln, wa, bf, acc);
-        run_stage<1>(s + 1, KT, lds, d, ln, wa, bf, acc);
-    }
-    if (s < KT) run_stage<0>(s, KT, lds, d, ln, wa, bf, acc);
-
-    // ---- k split: the two waves of a pair swap partial sums through LDS; wave ks finishes row
-    // blocks [ks * kRB / 2, (ks + 1) * kRB / 2).
-    // ---- epilogue operands (issued before the k-split exchange, whose LDS round trip hides
-    // their latency), then the exchange: the two waves of a pair swap partial sums through LDS;
-    // wave ks finishes row blocks [ks * kRB / 2, (ks + 1) * kRB / 2).
-    const int row_w = (rt0 + wn * (kWaveRows / 16)) * 16;
-    const int tok_w = m0 + wm * kWaveToks;
-    int rb0 = 0, nrb = kRB;
-    if (kKSplit == 2)
-    {
-        rb0 = ks * (kRB / 2);
-        nrb = kRB / 2;
-    }
-    wait_lgkm0();
-    wait_vmcnt<0>();
-    EpiOps e;
-    load_epilogue(p, e, rb0, row_w, tok_w, h, l32);
-    if (kKSplit == 2)
-    {
-        lds_barrier();  // every wave is done with the ring
-        if (ks == 0) put_partials<0>(acc, lds, wave, lane);
-        else put_partials<1>(acc, lds, wave, lane);
-        lds_barrier();
-        if (ks == 0) add_partials<0>(acc, lds, wave, lane);
-        else add_partials<1>(acc, lds, wave, lane);
-    }
-
-    // ---- epilogue
-    const bool full = rt0 * 16 + kBN <= p.N && m0 + kBM <= p.M;
-    if (p.glu)
-    {
-        store_glu(p, acc, e, rb0, nrb, row_w, tok_w, h, l32, lds, wn * kKSplit + ks, wm * kWaveToks, m0);
-    }
-    else if (full)
-    {
-        if (p.bias) store_full<true>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
-        else store_full<false>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
-    }
-    else
-    {
-        store_edge(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
-    }
+    G::body(p, n_mblocks, n_nblocks, xcd_mode);
 }
 
 }  // namespace
 
-hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int /*num_cus*/)
+namespace
 {
-    if (p.N == 0 || p.M == 0) return hipSuccess;
+
+// The three block tiles: 256 x 128 (8 waves, k-split pairs, 2 slots) for large problems,
+// 128 x 128 (8 waves, 64 x 64 per pair, 3 slots) and 64 x 64 (4 waves, one per SIMD, 6 slots:
+// short stages need a deeper ring to cover memory latency) to spread small problems over the
+// chip. gemm_tile_choice weighs block rounds over the CUs by the measured relative round times.
+using GemmA = Gemm<256, 128, NNHIP_GEMM_WAVES_N, NNHIP_GEMM_WAVES_M, NNHIP_GEMM_KSPLIT, NNHIP_GEMM_SLOTS>;
+using GemmB = Gemm<128, 128, 2, 2, 2, 3>;
+using GemmC = Gemm<64, 64, 2, 2, 1, 6>;
+
+template <class G>
+hipError_t launch_cfg(hipStream_t st, const GemvProblem& p)
+{
     static bool attr_set = false;
     if (!attr_set)
     {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<G>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, G::kLdsBytes);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const int n_mblocks = (int)ceil_div((size_t)p.M, kBM);
-    const int n_nblocks = (int)ceil_div((size_t)p.N, kBN);
+    const int n_mblocks = (int)ceil_div((size_t)p.M, G::kBM);
+    const int n_nblocks = (int)ceil_div((size_t)p.N, G::kBN);
     const int xcd_mode = (n_mblocks % 8 == 0) ? 1 : 0;
     const unsigned blocks = (unsigned)(n_mblocks * n_nblocks);
-    hipLaunchKernelGGL(k_gemm, dim3(blocks), dim3(kThreads), kLdsBytes, st, p, n_mblocks, n_nblocks, xcd_mode);
+    hipLaunchKernelGGL(k_gemm<G>, dim3(blocks), dim3(G::kThreads), G::kLdsBytes, st, p, n_mblocks, n_nblocks,
+                       xcd_mode);
     return hipGetLastError();
+}
+
+// Estimated time of a configuration in units of one 256 x 128 block: rounds of blocks over the
+// CUs times the block time relative to the 256 x 128 one.
+double gemm_cost(const GemvProblem& p, int num_cus, int bn, int bm, double rel)
+{
+    const size_t blocks = ceil_div((size_t)p.N, (size_t)bn) * ceil_div((size_t)p.M, (size_t)bm);
+    return (double)ceil_div(blocks, (size_t)num_cus) * rel;
+}
+
+}  // namespace
+
+int gemm_tile_choice(const GemvProblem& p, int num_cus)
+{
+    const int cus = num_cus > 0 ? num_cus : 256;
+    const double a = gemm_cost(p, cus, GemmA::kBN, GemmA::kBM, 1.0);
+    const double b = gemm_cost(p, cus, GemmB::kBN, GemmB::kBM, kGemmRelB);
+    const double c = gemm_cost(p, cus, GemmC::kBN, GemmC::kBM, kGemmRelC);
+    if (a <= b && a <= c) return NNHIP_GEMM_TILE_256x128;
+    return b <= c ? NNHIP_GEMM_TILE_128x128 : NNHIP_GEMM_TILE_64x64;
+}
+
+hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus, int tile)
+{
+    if (p.N == 0 || p.M == 0) return hipSuccess;
+    if (tile == NNHIP_GEMM_TILE_AUTO) tile = gemm_tile_choice(p, num_cus);
+    if (tile == NNHIP_GEMM_TILE_128x128) return launch_cfg<GemmB>(st, p);
+    if (tile == NNHIP_GEMM_TILE_64x64) return launch_cfg<GemmC>(st, p);
+    return launch_cfg<GemmA>(st, p);
 }
 
 }  // namespace nnhip

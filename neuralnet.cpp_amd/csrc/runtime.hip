@@ -27,6 +27,7 @@ struct nnhip_ctx
     // FFN block: zero between calls (zero-filled when allocated, reset by its consumer)
     uint32_t* amax = nullptr;
     size_t amax_words = 0;
+    int gemm_tile = NNHIP_GEMM_TILE_AUTO;
 };
 
 struct nnhip_group
@@ -171,7 +172,7 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     if (M <= (size_t)kGemvMaxM)
         NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
     else
-        NNHIP_LAUNCH(fn, launch_gemm(ctx->stream, p, ctx->num_cus));
+        NNHIP_LAUNCH(fn, launch_gemm(ctx->stream, p, ctx->num_cus, ctx->gemm_tile));
     return NNHIP_OK;
 }
 
@@ -266,6 +267,15 @@ nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream)
     NNHIP_CHECK_CTX("nnhip_ctx_get_stream");
     NNHIP_REQUIRE(stream != nullptr, "nnhip_ctx_get_stream", "null output");
     *stream = ctx->stream;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_set_gemm_tile(nnhip_ctx* ctx, int tile)
+{
+    NNHIP_CHECK_CTX("nnhip_ctx_set_gemm_tile");
+    NNHIP_REQUIRE(tile >= NNHIP_GEMM_TILE_AUTO && tile <= NNHIP_GEMM_TILE_64x64, "nnhip_ctx_set_gemm_tile",
+                  "tile must be one of NNHIP_GEMM_TILE_*");
+    ctx->gemm_tile = tile;
     return NNHIP_OK;
 }
 

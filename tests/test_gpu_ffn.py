@@ -181,3 +181,22 @@ def test_ffn_block_repeat_and_special_h(ctx, orc):
             _, _, b_dev = prepare_fc1(ctx, wq1, t1, bias, F, d)
         Y = host(ctx.ffn_glu_i8(dev(X), dev(gamma), 1e-6, F, rp1, to, b_dev, rp2, dev(t2), dev(b2), 0))
         assert same_bits(Y, Y_ref), f"call {i}"
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3])
+def test_ffn_block_each_tile(ctx, orc, tile):
+    """The gated epilogue (h and its per-token absmax) under every prefill GEMM block tile."""
+    d, F, M = 320, 100, 150
+    say(f"ffn_glu_i8 tile={tile} d={d} F={F} M={M}")
+    wq1, t1, b1, wq2, t2, b2 = block_case(orc, d, F, 930)
+    X = normal((d, M), 931, 0.0, 1.0)
+    gamma = normal((d,), 932, 1.0, 0.1)
+    Y_ref, _ = orc.ffn_glu_i8(X, gamma, 1e-6, F, wq1, t1, b1, wq2, t2, b2, 1)
+    rp1, to, bo = prepare_fc1(ctx, wq1, t1, b1, F, d)
+    rp2 = ctx.repack(dev(wq2), F)
+    ctx.set_gemm_tile(tile)
+    try:
+        Y = host(ctx.ffn_glu_i8(dev(X), dev(gamma), 1e-6, F, rp1, to, bo, rp2, dev(t2), dev(b2), 1))
+    finally:
+        ctx.set_gemm_tile(0)
+    assert same_bits(Y, Y_ref)

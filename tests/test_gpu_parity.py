@@ -295,6 +295,33 @@ def test_prefill_gemm_shapes(ctx, orc, N, K, M):
     assert np.all(np.abs(acc - np.rint(acc)) < 1e-3 * np.maximum(1, np.abs(acc)))
 
 
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("N,K,M", [(300, 520, 200), (130, 300, 130), (64, 256, 17), (1000, 2560, 96),
+                                   (4096, 4096, 256)])
+def test_prefill_gemm_each_tile(ctx, orc, tile, N, K, M):
+    """Every block tile of the prefill GEMM (256x128, 128x128, 64x64) forced on shapes with
+    tails in N, M and K, with a bias: bit-exact against the oracle (sampled rows for the
+    largest shape)."""
+    say(f"gemm tile={tile} N={N} K={K} M={M}")
+    tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, 17 + N + M, outliers=True)
+    b = normal((N,), 98)
+    ctx.set_gemm_tile(tile)
+    try:
+        Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M, bias=dev(b)))
+    finally:
+        ctx.set_gemm_tile(0)
+    rows = np.arange(N) if N * M <= 300 * 300 else np.unique(np.concatenate([np.arange(0, N, 61), [N - 1]]))
+    ref = orc.add_row_broadcast(orc.matmul_q_i8_rowblock(wq[rows], tau[rows], xq, s, K, M), b[rows])
+    assert np.array_equal(Y[rows], ref)
+
+
+def test_gemm_tile_setter_rejects(ctx, nnhip):
+    with pytest.raises(nnhip.NNHipError):
+        ctx.set_gemm_tile(4)
+    with pytest.raises(nnhip.NNHipError):
+        ctx.set_gemm_tile(-1)
+
+
 def test_grouped_gemv_matches_single(ctx, orc):
     say("grouped gemv")
     import torch
