@@ -289,14 +289,16 @@ size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M);
 
 /* The whole W1.58A8 gated block on X (d, M) f32:
  *   [RMSNorm(gamma, eps) if gamma != NULL] -> absmax int8 -> fc1 (interleaved rp1, tau1, b1)
- *   -> act -> absmax int8 -> fc2 (rp2 = repack of the (d, ceil(F/16)) container, tau2, b2)
- *   -> Y (d, M) f32.
+ *   -> act -> [SubLN: RMSNorm(gamma_sub, eps_sub) over the F features if gamma_sub != NULL]
+ *   -> absmax int8 -> fc2 (rp2 = repack of the (d, ceil(F/16)) container, tau2, b2) -> Y (d, M) f32.
  * Same bits as the reference sequence RMSNorm::forward, BitLinear::forward (int8 branch),
- * SwiGLU/ReLU2GLU::forward, BitLinear::forward (compute_layer_mlp.hpp:686-707,
- * compute_layer_bitlinear.hpp:441-457, compute_layer_feedforward.hpp:182-204). b1/b2 may be NULL. */
+ * SwiGLU/ReLU2GLU::forward, [sub_norm_ RMSNorm::forward], BitLinear::forward
+ * (compute_layer_mlp.hpp:686-707, compute_layer_bitlinear.hpp:441-457,
+ * compute_layer_feedforward.hpp:182-206). b1/b2 may be NULL. */
 nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d,
                               size_t F, size_t M, int act, const void* rp1, const float* tau1, const float* b1,
-                              const void* rp2, const float* tau2, const float* b2, float* Y);
+                              const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
+                              const float* b2, float* Y);
 
 #ifdef __cplusplus
 }

@@ -101,8 +101,8 @@ SIGNATURES = {
     "nnhip_glu_interleave": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
     "nnhip_ternary_matmul_glu": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_int, _vp]),
     "nnhip_ffn_glu_workspace_bytes": (_sz, [_sz, _sz, _sz]),
-    "nnhip_ffn_glu_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
-                               _vp]),
+    "nnhip_ffn_glu_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
+                               _vp, _vp]),
 }
 
 ACT_SWIGLU, ACT_RELU2GLU = 0, 1
@@ -461,8 +461,9 @@ class Context:
         return h
 
     def ffn_glu_i8(self, X, gamma, eps: float, F: int, rp1, tau1, b1, rp2, tau2, b2, act: int = ACT_SWIGLU,
-                   out=None):
-        """Gated FFN block on X (d, M): [RMSNorm] -> int8 -> fc1 (interleaved) -> act -> int8 -> fc2."""
+                   out=None, gamma_sub=None, eps_sub: float = 1e-5):
+        """Gated FFN block on X (d, M): [RMSNorm] -> int8 -> fc1 (interleaved) -> act -> [SubLN RMSNorm
+        (gamma_sub, eps_sub)] -> int8 -> fc2."""
         torch = self._torch
         d, M = X.shape
         Y = self._empty((d, M), torch.float32) if out is None else out
@@ -470,6 +471,7 @@ class Context:
         _check(lib().nnhip_ffn_glu_i8(self.h, self._dev(X, torch.float32, "X"), self._dev(gamma, torch.float32, "gamma"),
                                       eps, d, F, M, act, self._dev(rp1, torch.int32, "rp1"),
                                       self._dev(tau1, torch.float32, "tau1"), self._dev(b1, torch.float32, "b1"),
+                                      self._dev(gamma_sub, torch.float32, "gamma_sub"), eps_sub,
                                       self._dev(rp2, torch.int32, "rp2"), self._dev(tau2, torch.float32, "tau2"),
                                       self._dev(b2, torch.float32, "b2"), self._dev(Y, torch.float32, "Y")),
                "nnhip_ffn_glu_i8")

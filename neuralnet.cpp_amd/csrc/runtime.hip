@@ -903,8 +903,9 @@ size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M)
 }
 
 nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
-                              size_t M, int act, const void* rp1, const float* tau1, const float* b1, const void* rp2,
-                              const float* tau2, const float* b2, float* Y)
+                              size_t M, int act, const void* rp1, const float* tau1, const float* b1,
+                              const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
+                              const float* b2, float* Y)
 {
     const char* fn = "nnhip_ffn_glu_i8";
     NNHIP_CHECK_CTX(fn);
@@ -931,15 +932,17 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
     int32_t* rs2 = reinterpret_cast<int32_t*>(take(M * 4));
     float* h = reinterpret_cast<float*>(take(F * M * 4));
     float* y1 = M <= (size_t)kGemvMaxM ? reinterpret_cast<float*>(take(nnhip_glu_rows(F) * M * 4)) : nullptr;
-    if (M > (size_t)kGemvMaxM)
+    // prefill without SubLN: the gated GEMM epilogue leaves max |h| per token, so h is quantized
+    // in one streaming pass (the same scale and codes as the absmax kernel); with SubLN the
+    // fused RMSNorm -> absmax -> int8 kernel quantizes h
+    const bool fold = M > (size_t)kGemvMaxM && gamma_sub == nullptr;
+    if (fold)
     {
-        // prefill: the gated GEMM epilogue leaves max |h| per token, so h is quantized in one
-        // streaming pass (the same scale and codes as the absmax kernel)
         st = ensure_amax(ctx, M, fn);
         if (st != NNHIP_OK) return st;
     }
     NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, gamma != nullptr, eps, d, M, xi1, s1, rs1, nullptr));
-    if (M > (size_t)kGemvMaxM)
+    if (fold)
     {
         st = run_matmul(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, nnhip_glu_rows(F), d, M, h, act + 1, F, ctx->amax);
         if (st == NNHIP_OK)
@@ -957,7 +960,8 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
     {
         st = run_matmul_glu(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, F, d, M, act, y1, h);
         if (st != NNHIP_OK) return st;
-        NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, nullptr, false, 0.0f, F, M, xi2, s2, rs2, nullptr));
+        NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, gamma_sub, gamma_sub != nullptr, eps_sub, F, M, xi2, s2, rs2,
+                                          nullptr));
     }
     return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y);
 }

@@ -306,11 +306,13 @@ Result<Tensor> ComputeEngine::glu(const Tensor& y1, int act)
 
 Result<Tensor> ComputeEngine::ffn_glu_i8_forward(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
                                                  const Tensor& tau1, const Tensor& b1, const Tensor& wq2,
-                                                 const Tensor& tau2, const Tensor& b2, int act)
+                                                 const Tensor& tau2, const Tensor& b2, int act, const Tensor* gamma_sub,
+                                                 Scalar eps_sub)
 {
     const char* fn = "ffn_glu_i8_forward";
     for (const Tensor* t : {&x, &wq1, &tau1, &b1, &wq2, &tau2, &b2}) EX_TRY_CHECK(check_owned(*t, fn));
     if (gamma) EX_TRY_CHECK(check_owned(*gamma, fn));
+    if (gamma_sub) EX_TRY_CHECK(check_owned(*gamma_sub, fn));
     if (act != 0 && act != 1) return Error{"ffn_glu_i8_forward: act must be 0 (SwiGLU) or 1 (ReLU2GLU)"};
     const std::size_t d = x.rows(), F2 = wq1.rows();
     if (F2 % 2 != 0 || F2 == 0) return Error{"ffn_glu_i8_forward: fc1 must have 2*d_ff rows, got " + shape(wq1)};
@@ -322,13 +324,15 @@ Result<Tensor> ComputeEngine::ffn_glu_i8_forward(const Tensor& x, const Tensor* 
     if (tau1.rows() != F2 || b1.rows() != F2 || tau2.rows() != d || b2.rows() != d)
         return Error{"ffn_glu_i8_forward: tau / bias rows do not match the weights"};
     if (gamma && gamma->rows() != d) return Error{"ffn_glu_i8_forward: gamma must be (d_model, 1)"};
-    return ffn_glu_i8_impl(x, gamma, eps, wq1, tau1, b1, wq2, tau2, b2, act);
+    if (gamma_sub && gamma_sub->rows() != F) return Error{"ffn_glu_i8_forward: gamma_sub must be (d_ff, 1)"};
+    return ffn_glu_i8_impl(x, gamma, eps, wq1, tau1, b1, wq2, tau2, b2, act, gamma_sub, eps_sub);
 }
 
-// Default composition in the reference layer order (compute_layer_feedforward.hpp:182-204).
+// Default composition in the reference layer order (compute_layer_feedforward.hpp:182-206).
 Result<Tensor> ComputeEngine::ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
                                               const Tensor& tau1, const Tensor& b1, const Tensor& wq2,
-                                              const Tensor& tau2, const Tensor& b2, int act)
+                                              const Tensor& tau2, const Tensor& b2, int act, const Tensor* gamma_sub,
+                                              Scalar eps_sub)
 {
     Tensor in = x;
     if (gamma)
@@ -338,7 +342,13 @@ Result<Tensor> ComputeEngine::ffn_glu_i8_impl(const Tensor& x, const Tensor* gam
     }
     EX_TRY(y1, bitlinear_i8_forward(in, wq1, tau1, b1, Precision::F32, nullptr, nullptr));
     EX_TRY(h, glu(*y1, act));
-    return bitlinear_i8_forward(*h, wq2, tau2, b2, Precision::F32, nullptr, nullptr);
+    Tensor h2 = *h;
+    if (gamma_sub)
+    {
+        EX_TRY(n, rmsnorm(*h, *gamma_sub, eps_sub));
+        h2 = *n;
+    }
+    return bitlinear_i8_forward(h2, wq2, tau2, b2, Precision::F32, nullptr, nullptr);
 }
 
 }  // namespace nn

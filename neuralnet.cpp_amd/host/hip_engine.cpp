@@ -313,10 +313,11 @@ protected:
     }
 
     // The whole block in one library call: [RMSNorm ->] int8 -> fc1 with the gated activation in
-    // its epilogue -> int8 -> fc2 (nnhip_ffn_glu_i8), on cached interleaved / repacked weights.
+    // its epilogue -> [SubLN ->] int8 -> fc2 (nnhip_ffn_glu_i8), on cached interleaved / repacked
+    // weights.
     Result<Tensor> ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
                                    const Tensor& tau1, const Tensor& b1, const Tensor& wq2, const Tensor& tau2,
-                                   const Tensor& b2, int act) override
+                                   const Tensor& b2, int act, const Tensor* gamma_sub, Scalar eps_sub) override
     {
         const std::size_t d = x.rows(), M = x.cols(), F = wq1.rows() / 2;
         EX_TRY(y, alloc_impl(d, M, Precision::F32));
@@ -324,7 +325,8 @@ protected:
         EX_TRY(g1, glu_weights(wq1, tau1, b1, F, d));
         EX_TRY(rp2, repacked(wq2, F));
         NNHIP_TRY(nnhip_ffn_glu_i8(ctx_->h, fp(x), gamma ? fp(*gamma) : nullptr, eps, d, F, M, act, g1->rp, g1->tau,
-                                   g1->bias, *rp2, fp(tau2), fp(b2), fpw(*y)),
+                                   g1->bias, gamma_sub ? fp(*gamma_sub) : nullptr, eps_sub, *rp2, fp(tau2), fp(b2),
+                                   fpw(*y)),
                   "ffn_glu_i8_forward");
         return *y;
     }

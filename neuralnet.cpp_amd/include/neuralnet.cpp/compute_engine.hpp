@@ -173,12 +173,14 @@ public:
     [[nodiscard]] Result<Tensor> glu(const Tensor& y1, int act);
 
     // Gated feed-forward block in the int8 branch (FeedForward::forward,
-    // compute_layer_feedforward.hpp:182-204): [RMSNorm(gamma, eps) if gamma] -> fc1 (BitLinear
-    // int8, 2F rows: gate then up) -> glu -> fc2 (BitLinear int8). The default implementation
-    // composes rmsnorm / bitlinear_i8_forward / glu; an engine may fuse them (same bits).
+    // compute_layer_feedforward.hpp:182-206): [RMSNorm(gamma, eps) if gamma] -> fc1 (BitLinear
+    // int8, 2F rows: gate then up) -> glu -> [SubLN: RMSNorm(gamma_sub, eps_sub) if gamma_sub]
+    // -> fc2 (BitLinear int8). The default implementation composes rmsnorm /
+    // bitlinear_i8_forward / glu; an engine may fuse them (same bits).
     [[nodiscard]] Result<Tensor> ffn_glu_i8_forward(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
                                                     const Tensor& tau1, const Tensor& b1, const Tensor& wq2,
-                                                    const Tensor& tau2, const Tensor& b2, int act);
+                                                    const Tensor& tau2, const Tensor& b2, int act,
+                                                    const Tensor* gamma_sub = nullptr, Scalar eps_sub = 1e-5f);
 
     [[nodiscard]] EngineInfo describe() const { return describe_impl(); }
     void begin_batch() {}
@@ -213,7 +215,7 @@ protected:
     [[nodiscard]] virtual Result<Tensor> ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps,
                                                          const Tensor& wq1, const Tensor& tau1, const Tensor& b1,
                                                          const Tensor& wq2, const Tensor& tau2, const Tensor& b2,
-                                                         int act);
+                                                         int act, const Tensor* gamma_sub, Scalar eps_sub);
     [[nodiscard]] virtual EngineInfo describe_impl() const = 0;
     virtual void sync_impl() = 0;
 

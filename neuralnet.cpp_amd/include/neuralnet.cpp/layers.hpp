@@ -16,6 +16,7 @@
 // runs the f32-activation branch (:459-466) through ComputeEngine::matmul_q. Training
 // (backward, STE gradients) is outside this engine's scope.
 
+#include <memory>
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
@@ -360,6 +361,38 @@ private:
     std::uint64_t quantize_calls_ = 0;
 };
 
+class RMSNorm final : public Layer
+{
+public:
+    explicit RMSNorm(std::size_t normalized_shape, Scalar epsilon = 1e-5f)
+        : normalized_shape_(normalized_shape), epsilon_(epsilon)
+    {
+    }
+    [[nodiscard]] const char* layer_name() const noexcept override { return "RMSNorm"; }
+    [[nodiscard]] std::vector<TensorRef> parameters() override { return {gamma_}; }
+    [[nodiscard]] Tensor& gamma() noexcept { return gamma_; }
+    [[nodiscard]] Scalar epsilon() const noexcept { return epsilon_; }
+
+    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
+    {
+        if (input.rows() != normalized_shape_) return Error{"rmsnorm forward: input shape mismatch"};
+        return engine_ref().rmsnorm(input, gamma_, epsilon_);
+    }
+
+protected:
+    [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
+    {
+        gamma_ = engine.create_tensor(normalized_shape_, 1, Precision::F32, InitSpec::constant(1.0f));
+        if (!gamma_.valid()) return Error{"RMSNorm: parameter init failed"};
+        return {};
+    }
+
+private:
+    std::size_t normalized_shape_;
+    Scalar epsilon_;
+    Tensor gamma_;
+};
+
 // Activation of the feed-forward block (include/neuralnet.cpp/model_spec.hpp:47-54).
 enum class ActivationType : std::uint32_t
 {
@@ -369,20 +402,23 @@ enum class ActivationType : std::uint32_t
 };
 
 // Gated feed-forward block with ternary BitLinear projections
-// (include/neuralnet.cpp/compute_layer_feedforward.hpp:22-204, WeightQuant::T1_58):
+// (include/neuralnet.cpp/compute_layer_feedforward.hpp:22-206, WeightQuant::T1_58):
 // fc1 = BitLinear(d_model -> 2*d_ff) whose rows [0, d_ff) are the gate and [d_ff, 2*d_ff) the
-// up projection, the gated activation (SwiGLU or ReLU^2-GLU), fc2 = BitLinear(d_ff -> d_model).
-// With int8 activation quantization on both projections, forward() is one
-// ComputeEngine::ffn_glu_i8_forward (the HIP engine fuses the block); otherwise it chains the
-// layers. Only the gated activations are provided (GeLU and SubLN are outside this path).
+// up projection, the gated activation (SwiGLU or ReLU^2-GLU), optionally SubLN (an RMSNorm of
+// width d_ff with the RMSNorm default eps, BitNet b1.58's norm type; :37-45, :65, :201-206),
+// fc2 = BitLinear(d_ff -> d_model). With int8 activation quantization on both projections,
+// forward() is one ComputeEngine::ffn_glu_i8_forward (the HIP engine fuses the block);
+// otherwise it chains the layers. Only the gated activations are provided (GeLU is outside
+// this path), and SubLN is an RMSNorm (the reference's LayerNorm variant is not provided).
 class FeedForward final : public Layer
 {
 public:
     FeedForward(std::size_t d_model, std::size_t d_ff, ActivationType activation = ActivationType::SwiGLU,
-                bool inference_only = false)
+                bool subln = false, bool inference_only = false)
         : d_model_(d_model), d_ff_(d_ff), activation_(activation), fc1_(d_model, 2 * d_ff, inference_only),
           fc2_(d_ff, d_model, inference_only)
     {
+        if (subln) sub_norm_ = std::make_unique<RMSNorm>(d_ff);
     }
 
     [[nodiscard]] const char* layer_name() const noexcept override { return "FeedForward"; }
@@ -404,28 +440,42 @@ public:
 
     [[nodiscard]] BitLinear& fc1() noexcept { return fc1_; }
     [[nodiscard]] BitLinear& fc2() noexcept { return fc2_; }
+    [[nodiscard]] RMSNorm* sub_norm() noexcept { return sub_norm_.get(); }
     [[nodiscard]] std::size_t d_model() const noexcept { return d_model_; }
     [[nodiscard]] std::size_t d_ff() const noexcept { return d_ff_; }
 
+    // fc1, fc2, then the SubLN gamma (compute_layer_feedforward.hpp:87-105)
     [[nodiscard]] std::vector<TensorRef> parameters() override
     {
         auto r = fc1_.parameters();
         auto r2 = fc2_.parameters();
         r.insert(r.end(), r2.begin(), r2.end());
+        if (sub_norm_)
+        {
+            auto r3 = sub_norm_->parameters();
+            r.insert(r.end(), r3.begin(), r3.end());
+        }
         return r;
     }
 
-    // entries: fc1 (weights, bias), then fc2 (compute_layer_feedforward.hpp:100-107)
-    [[nodiscard]] std::size_t param_count() override { return fc1_.param_count() + fc2_.param_count(); }
+    // entries: fc1 (weights, bias), fc2 (weights, bias), [SubLN gamma] (same order)
+    [[nodiscard]] std::size_t param_count() override
+    {
+        return fc1_.param_count() + fc2_.param_count() + (sub_norm_ ? sub_norm_->param_count() : 0);
+    }
     [[nodiscard]] Result<ParamEntry> export_param(std::size_t index, ModelRole role) override
     {
-        const std::size_t n1 = fc1_.param_count();
-        return index < n1 ? fc1_.export_param(index, role) : fc2_.export_param(index - n1, role);
+        const std::size_t n1 = fc1_.param_count(), n2 = n1 + fc2_.param_count();
+        if (index < n1) return fc1_.export_param(index, role);
+        if (index < n2 || !sub_norm_) return fc2_.export_param(index - n1, role);
+        return sub_norm_->export_param(index - n2, role);
     }
     [[nodiscard]] Result<void> import_param(std::size_t index, const ParamEntry& e) override
     {
-        const std::size_t n1 = fc1_.param_count();
-        return index < n1 ? fc1_.import_param(index, e) : fc2_.import_param(index - n1, e);
+        const std::size_t n1 = fc1_.param_count(), n2 = n1 + fc2_.param_count();
+        if (index < n1) return fc1_.import_param(index, e);
+        if (index < n2 || !sub_norm_) return fc2_.import_param(index - n1, e);
+        return sub_norm_->import_param(index - n2, e);
     }
 
     void clear_cache() override
@@ -445,10 +495,16 @@ public:
             EX_TRY_CHECK(fc2_.ensure_quantized());
             return engine.ffn_glu_i8_forward(input, nullptr, 0.0f, fc1_.quantized_weights_packed(), fc1_.row_scales(),
                                              fc1_.bias(), fc2_.quantized_weights_packed(), fc2_.row_scales(),
-                                             fc2_.bias(), act);
+                                             fc2_.bias(), act, sub_norm_ ? &sub_norm_->gamma() : nullptr,
+                                             sub_norm_ ? sub_norm_->epsilon() : 0.0f);
         }
         EX_TRY(h1, fc1_.forward(input));
         EX_TRY(h2, engine.glu(*h1, act));
+        if (sub_norm_)
+        {
+            EX_TRY(h3, sub_norm_->forward(*h2));
+            return fc2_.forward(*h3);
+        }
         return fc2_.forward(*h2);
     }
 
@@ -462,44 +518,22 @@ protected:
         fc1_.set_precision_profile(linear);
         fc2_.set_precision_profile(linear);
         EX_TRY_CHECK(fc1_.init(engine));
-        return fc2_.init(engine);
+        EX_TRY_CHECK(fc2_.init(engine));
+        if (sub_norm_)
+        {
+            PrecisionProfile norm = p_;
+            norm.param = Precision::F32;
+            sub_norm_->set_precision_profile(norm);
+            EX_TRY_CHECK(sub_norm_->init(engine));
+        }
+        return {};
     }
 
 private:
     std::size_t d_model_, d_ff_;
     ActivationType activation_;
     BitLinear fc1_, fc2_;
-};
-
-class RMSNorm final : public Layer
-{
-public:
-    explicit RMSNorm(std::size_t normalized_shape, Scalar epsilon = 1e-5f)
-        : normalized_shape_(normalized_shape), epsilon_(epsilon)
-    {
-    }
-    [[nodiscard]] const char* layer_name() const noexcept override { return "RMSNorm"; }
-    [[nodiscard]] std::vector<TensorRef> parameters() override { return {gamma_}; }
-    [[nodiscard]] Tensor& gamma() noexcept { return gamma_; }
-
-    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
-    {
-        if (input.rows() != normalized_shape_) return Error{"rmsnorm forward: input shape mismatch"};
-        return engine_ref().rmsnorm(input, gamma_, epsilon_);
-    }
-
-protected:
-    [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
-    {
-        gamma_ = engine.create_tensor(normalized_shape_, 1, Precision::F32, InitSpec::constant(1.0f));
-        if (!gamma_.valid()) return Error{"RMSNorm: parameter init failed"};
-        return {};
-    }
-
-private:
-    std::size_t normalized_shape_;
-    Scalar epsilon_;
-    Tensor gamma_;
+    std::unique_ptr<RMSNorm> sub_norm_;  // SubLN, or none
 };
 
 }  // namespace nn

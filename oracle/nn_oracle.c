@@ -615,18 +615,23 @@ static void orc_bitlinear_i8(const float* x, size_t K, size_t M, const uint32_t*
  * wq1 (2F, ceil(d/16)) and wq2 (d, ceil(F/16)) are reference containers; b1/b2 may be NULL.
  * h_out (F, M) receives the gated activation if not NULL. */
 void orc_ffn_glu_i8(const float* X, const float* gamma, float eps, size_t d, size_t F, size_t M, int act,
-                    const uint32_t* wq1, const float* tau1, const float* b1, const uint32_t* wq2,
-                    const float* tau2, const float* b2, int threads, float* h_out, float* Y)
+                    const uint32_t* wq1, const float* tau1, const float* b1, const float* gamma_sub,
+                    float eps_sub, const uint32_t* wq2, const float* tau2, const float* b2, int threads,
+                    float* h_out, float* Y)
 {
     float* x1 = (float*)malloc(sizeof(float) * (d * M + 1));
     float* y1 = (float*)malloc(sizeof(float) * (2 * F * M + 1));
     float* h = (float*)malloc(sizeof(float) * (F * M + 1));
+    float* hn = gamma_sub ? (float*)malloc(sizeof(float) * (F * M + 1)) : NULL;
     if (gamma) orc_rmsnorm(X, gamma, eps, d, M, x1);
     else memcpy(x1, X, sizeof(float) * d * M);
     orc_bitlinear_i8(x1, d, M, wq1, tau1, b1, 2 * F, threads, y1);
     orc_glu(y1, F, M, act, h);
     if (h_out) memcpy(h_out, h, sizeof(float) * F * M);
-    orc_bitlinear_i8(h, F, M, wq2, tau2, b2, d, threads, Y);
+    /* SubLN: RMSNorm of the gated output before fc2 (compute_layer_feedforward.hpp:201-206) */
+    if (gamma_sub) orc_rmsnorm(h, gamma_sub, eps_sub, F, M, hn);
+    orc_bitlinear_i8(gamma_sub ? hn : h, F, M, wq2, tau2, b2, d, threads, Y);
+    free(hn);
     free(h);
     free(y1);
     free(x1);

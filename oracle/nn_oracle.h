@@ -34,8 +34,9 @@
  *                       (compute_layer_mlp.hpp:317-328, :405-414), checked against float64
  *                       evaluations within tolerance and exact special cases
  *   orc_ffn_glu_i8    : composition of the pinned pieces above in the order of
- *                       FeedForward::forward (compute_layer_feedforward.hpp:182-204); checked
- *                       against a numpy composition (int64 products) in the tests
+ *                       FeedForward::forward (compute_layer_feedforward.hpp:182-206, with the
+ *                       optional SubLN RMSNorm before fc2); checked against a numpy composition
+ *                       (int64 products) in the tests
  */
 #ifndef NN_ORACLE_H
 #define NN_ORACLE_H
@@ -102,8 +103,9 @@ long orc_glu_src_row(size_t r, size_t F);
 void orc_glu_interleave(const uint32_t* wq, const float* tau, const float* bias, size_t F, size_t K,
                         uint32_t* wq_out, float* tau_out, float* bias_out);
 void orc_ffn_glu_i8(const float* X, const float* gamma, float eps, size_t d, size_t F, size_t M, int act,
-                    const uint32_t* wq1, const float* tau1, const float* b1, const uint32_t* wq2,
-                    const float* tau2, const float* b2, int threads, float* h_out, float* Y);
+                    const uint32_t* wq1, const float* tau1, const float* b1, const float* gamma_sub,
+                    float eps_sub, const uint32_t* wq2, const float* tau2, const float* b2, int threads,
+                    float* h_out, float* Y);
 
 /* ---- MI355X tile layout of packed ternary weights (checker for the repacker) ---- */
 size_t orc_repacked_words(size_t N, size_t K);

@@ -63,7 +63,8 @@ def lib() -> ctypes.CDLL:
             "orc_glu_src_row": (ctypes.c_long, [_sz, _sz]),
             "orc_glu_interleave": (None, [_u32p, _f32p, _f32p, _sz, _sz, _u32p, _f32p, _f32p]),
             "orc_ffn_glu_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _sz, ctypes.c_int,
-                                      _u32p, _f32p, _f32p, _u32p, _f32p, _f32p, ctypes.c_int, _f32p, _f32p]),
+                                      _u32p, _f32p, _f32p, _f32p, ctypes.c_float, _u32p, _f32p, _f32p, ctypes.c_int,
+                                      _f32p, _f32p]),
             "orc_repacked_words": (_sz, [_sz, _sz]),
             "orc_repack": (None, [_u32p, _sz, _sz, _u32p]),
             "orc_unrepack": (None, [_u32p, _sz, _sz, _u32p]),
@@ -286,19 +287,20 @@ def glu_interleave(wq: np.ndarray, tau: np.ndarray, bias, F: int, K: int):
     return wo, to, bo
 
 
-def ffn_glu_i8(X, gamma, eps, F, wq1, tau1, b1, wq2, tau2, b2, act: int = ACT_SWIGLU, threads: int = 0):
-    """Config C4 block: [RMSNorm] -> int8 -> fc1 (2F) -> gated activation -> int8 -> fc2.
-    Returns (Y (d, M), h (F, M))."""
+def ffn_glu_i8(X, gamma, eps, F, wq1, tau1, b1, wq2, tau2, b2, act: int = ACT_SWIGLU, threads: int = 0,
+               gamma_sub=None, eps_sub: float = 1e-5):
+    """Config C4 block: [RMSNorm] -> int8 -> fc1 (2F) -> gated activation -> [SubLN RMSNorm] ->
+    int8 -> fc2. Returns (Y (d, M), h (F, M)); h is the gated output before SubLN."""
     X = _f32(X)
     d, M = X.shape
     Y = np.empty((d, M), np.float32)
     h = np.empty((F, M), np.float32)
     fp = lambda a: None if a is None else _p(_f32(a).reshape(-1), ctypes.c_float)
-    keep = [None if a is None else _f32(a).reshape(-1) for a in (gamma, tau1, b1, tau2, b2)]
-    g_, t1, b1_, t2, b2_ = keep
+    keep = [None if a is None else _f32(a).reshape(-1) for a in (gamma, tau1, b1, tau2, b2, gamma_sub)]
+    g_, t1, b1_, t2, b2_, gs_ = keep
     wq1, wq2 = _u32(wq1), _u32(wq2)
     lib().orc_ffn_glu_i8(_p(X, ctypes.c_float), fp(g_), eps, d, F, M, act, _p(wq1, ctypes.c_uint32), fp(t1), fp(b1_),
-                         _p(wq2, ctypes.c_uint32), fp(t2), fp(b2_), threads, _p(h, ctypes.c_float),
+                         fp(gs_), eps_sub, _p(wq2, ctypes.c_uint32), fp(t2), fp(b2_), threads, _p(h, ctypes.c_float),
                          _p(Y, ctypes.c_float))
     return Y, h
 

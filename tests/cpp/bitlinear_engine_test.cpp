@@ -680,6 +680,33 @@ void test_feedforward(nn::ComputeEngine& e)
             for (float v : download(e, *yf32).span()) finite = finite && std::isfinite(v);
         CHECK(finite, "f32-activation branch (matmul_q) runs");
     }
+    // SubLN: RMSNorm(d_ff, eps 1e-5) of the gated output before fc2; its gamma is the fifth entry
+    {
+        nn::FeedForward sf(D, F, nn::ActivationType::SwiGLU, true);
+        CHECK(sf.init(e).has_value(), "FeedForward(SwiGLU, SubLN) init");
+        auto sp = sf.parameters();  // fc1 latent, fc1 bias, fc2 latent, fc2 bias, SubLN gamma
+        CHECK(sp.size() == 5 && sf.param_count() == 5 && sf.sub_norm() != nullptr, "SubLN adds one parameter");
+        if (sp.size() == 5 && sf.sub_norm())
+        {
+            CHECK(e.copy_from(sp[0].get(), random_matrix(2 * F, D, 191)).has_value() &&
+                      e.copy_from(sp[1].get(), random_matrix(2 * F, 1, 192)).has_value() &&
+                      e.copy_from(sp[2].get(), random_matrix(D, F, 193)).has_value() &&
+                      e.copy_from(sp[3].get(), random_matrix(D, 1, 194)).has_value() &&
+                      e.copy_from(sp[4].get(), random_matrix(F, 1, 195)).has_value(),
+                  "write SubLN block parameters");
+            sf.set_activation_quant(true);
+            const nn::Tensor x = upload(e, random_matrix(D, B, 196));
+            auto y = sf.forward(x);
+            auto h1 = sf.fc1().forward(x);
+            auto h2 = h1 ? e.glu(*h1, 0) : nn::Result<nn::Tensor>(nn::Error{"fc1 failed"});
+            auto h3 = h2 ? sf.sub_norm()->forward(*h2) : nn::Result<nn::Tensor>(nn::Error{"glu failed"});
+            auto y2 = h3 ? sf.fc2().forward(*h3) : nn::Result<nn::Tensor>(nn::Error{"sub_norm failed"});
+            CHECK(y.has_value() && y2.has_value() && bitwise_equal(download(e, *y), download(e, *y2)),
+                  "fused SubLN block bit-identical to fc1 -> glu -> RMSNorm -> fc2");
+            auto g = sf.export_param(4, nn::ModelRole::Model);
+            CHECK(g.has_value() && g->kind == nn::ParamKind::Dense && g->rows == F, "SubLN gamma exports Dense");
+        }
+    }
     nn::FeedForward gelu(8, 8, nn::ActivationType::GeLU);
     nn::PrecisionProfile prof;
     prof.param = nn::Precision::T1_58;

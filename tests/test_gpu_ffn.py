@@ -200,3 +200,22 @@ def test_ffn_block_each_tile(ctx, orc, tile):
     finally:
         ctx.set_gemm_tile(0)
     assert same_bits(Y, Y_ref)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64, 300])
+@pytest.mark.parametrize("act", [0, 1])
+def test_ffn_block_subln(ctx, orc, M, act):
+    """SubLN (BitNet b1.58): an RMSNorm of the gated output (eps 1e-5) before fc2's quantizer,
+    decode and prefill sizes, bit-exact against the oracle."""
+    d, F = 256, 136
+    say(f"ffn_glu_i8 SubLN d={d} F={F} M={M} act={act}")
+    wq1, t1, b1, wq2, t2, b2 = block_case(orc, d, F, 940 + M)
+    X = normal((d, M), 941 + M, 0.0, 1.0)
+    gamma = normal((d,), 942, 1.0, 0.1)
+    gsub = normal((F,), 943, 1.0, 0.1)
+    Y_ref, _ = orc.ffn_glu_i8(X, gamma, 1e-6, F, wq1, t1, b1, wq2, t2, b2, act, gamma_sub=gsub, eps_sub=1e-5)
+    rp1, to, bo = prepare_fc1(ctx, wq1, t1, b1, F, d)
+    rp2 = ctx.repack(dev(wq2), F)
+    Y = host(ctx.ffn_glu_i8(dev(X), dev(gamma), 1e-6, F, rp1, to, bo, rp2, dev(t2), dev(b2), act,
+                            gamma_sub=dev(gsub), eps_sub=1e-5))
+    assert same_bits(Y, Y_ref)

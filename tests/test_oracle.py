@@ -423,6 +423,12 @@ def test_ffn_block_is_the_composition(orc, act):
     # no norm: gamma None feeds X straight to fc1's quantizer
     Y0, _ = orc.ffn_glu_i8(X, None, 0.0, F, wq1, t1, b1, wq2, t2, b2, act)
     assert np.array_equal(Y0, bitlinear(orc.glu(bitlinear(X, wq1, t1, b1, d), act), wq2, t2, b2, F))
+    # SubLN: an RMSNorm of the gated output (eps 1e-5, the RMSNorm default) before fc2
+    gs = normal((F,), 37, 1.0, 0.1)
+    Ys, hs = orc.ffn_glu_i8(X, gamma, 1e-6, F, wq1, t1, b1, wq2, t2, b2, act, gamma_sub=gs, eps_sub=1e-5)
+    assert np.array_equal(hs, h_ref)
+    assert np.array_equal(Ys, bitlinear(orc.rmsnorm(h_ref, gs, 1e-5), wq2, t2, b2, F))
+    assert not np.array_equal(Ys, Y)
 
 
 def test_model_file_fixtures_reproducible(tmp_path):
