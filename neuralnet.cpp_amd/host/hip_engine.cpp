@@ -7,6 +7,7 @@
 // layout in engine scratch. bitlinear_i8_forward runs the fused path: one quantization
 // kernel (abs-max, scale, int8, row sums) and one GEMV/GEMM launch with the bias add in
 // its epilogue, producing the same bits as the reference call sequence.
+#include <optional>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -232,6 +233,7 @@ protected:
             rs_cap_ = rs_bytes > rs_cap_ ? rs_bytes : rs_cap_;
             xi_buf_ = *xi;
             rs_buf_ = *rs;
+            last_quant_.reset();
         }
         return ActScratch{static_cast<int8_t*>(xi_buf_.get()), static_cast<int32_t*>(rs_buf_.get())};
     }
@@ -243,6 +245,7 @@ protected:
         if (N == 0 || M == 0) return {};
         EX_TRY(rp, repacked(wq, K));
         EX_TRY(a, act_scratch(K, M));
+        last_quant_.reset();  // the scratch now holds another activation
         int8_t* xi = a->xi;
         int32_t* rs = a->rowsum;
         NNHIP_TRY(nnhip_act_i8_from_container(ctx_->h, up(xq), K, M, xi, rs), "matmul_q_i8 (activations)");
@@ -280,31 +283,76 @@ protected:
         return {};
     }
 
+    // The last input quantized into the activation scratch. Another BitLinear on the same input
+    // (same storage, same write epoch, same shape; e.g. the q / k / v projections of one
+    // attention input) reuses it instead of quantizing again. The storage is held weakly, so a
+    // freed input never matches a new one at the same address.
+    struct LastQuant
+    {
+        std::weak_ptr<detail::Storage> src;
+        std::uint64_t epoch = 0;
+        std::size_t K = 0, M = 0;
+        Tensor s;
+        Tensor xq;  // the reference int8 container, when that quantization wrote one
+    };
+
+    bool reuses_last_quant(const Tensor& x) const
+    {
+        if (!last_quant_ || last_quant_->K != x.rows() || last_quant_->M != x.cols()) return false;
+        const auto src = last_quant_->src.lock();
+        return src && src.get() == TensorAccess::storage(x) && last_quant_->epoch == x.write_epoch();
+    }
+
     Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor& b,
                                      Tensor* xq_out, Tensor* s_out) override
     {
         const std::size_t K = x.rows(), M = x.cols(), N = wq.rows();
-        EX_TRY(s, alloc_impl(1, M, Precision::F32));
         EX_TRY(y, alloc_impl(N, M, Precision::F32));
-        Tensor xq;
-        if (xq_out)
+        if (M == 0 || N == 0)
         {
-            EX_TRY(t, alloc_impl(K, i8_pack::words_per_row(M), Precision::F32));
-            xq = *t;
+            EX_TRY(s0, alloc_impl(1, M, Precision::F32));
+            if (xq_out)
+            {
+                EX_TRY(t, alloc_impl(K, i8_pack::words_per_row(M), Precision::F32));
+                *xq_out = *t;
+            }
+            if (s_out) *s_out = *s0;
+            return *y;
         }
-        if (M == 0 || N == 0) return *y;
         EX_TRY(rp, repacked(wq, K));
         EX_TRY(a, act_scratch(K, M));
         int8_t* xi = a->xi;
         int32_t* rs = a->rowsum;
-        NNHIP_TRY(nnhip_act_quant_i8(ctx_->h, fp(x), K, M, xi, fpw(*s), rs, xq_out ? upw(xq) : nullptr),
-                  "bitlinear_i8_forward (activation quantization)");
-        NNHIP_TRY(nnhip_ternary_matmul(ctx_->h, *rp, fp(tau), xi, fp(*s), rs, fp(b), N, K, M, fpw(*y)),
+        Tensor s;
+        if (reuses_last_quant(x) && (!xq_out || last_quant_->xq.valid()))
+        {
+            s = last_quant_->s;
+            if (xq_out) *xq_out = last_quant_->xq;
+        }
+        else
+        {
+            EX_TRY(s1, alloc_impl(1, M, Precision::F32));
+            s = *s1;
+            Tensor xq;
+            if (xq_out)
+            {
+                EX_TRY(t, alloc_impl(K, i8_pack::words_per_row(M), Precision::F32));
+                xq = *t;
+            }
+            last_quant_.reset();
+            NNHIP_TRY(nnhip_act_quant_i8(ctx_->h, fp(x), K, M, xi, fpw(s), rs, xq_out ? upw(xq) : nullptr),
+                      "bitlinear_i8_forward (activation quantization)");
+            ++act_quant_calls_;
+            last_quant_ = LastQuant{TensorAccess::storage_ref(x), x.write_epoch(), K, M, s, xq};
+            if (xq_out) *xq_out = xq;
+        }
+        NNHIP_TRY(nnhip_ternary_matmul(ctx_->h, *rp, fp(tau), xi, fp(s), rs, fp(b), N, K, M, fpw(*y)),
                   "bitlinear_i8_forward (ternary product)");
-        if (xq_out) *xq_out = xq;
-        if (s_out) *s_out = *s;
+        if (s_out) *s_out = s;
         return *y;
     }
+
+    std::uint64_t activation_quantizations() const noexcept override { return act_quant_calls_; }
 
     Result<void> glu_impl(const Tensor& y1, int act, const Tensor& out) override
     {
@@ -349,6 +397,8 @@ private:
     int device_;
     std::shared_ptr<void> xi_buf_, rs_buf_;
     std::size_t xi_cap_ = 0, rs_cap_ = 0;
+    std::optional<LastQuant> last_quant_;
+    std::uint64_t act_quant_calls_ = 0;
 };
 
 int parse_device(const char* device)

@@ -112,6 +112,7 @@ public:
         return t;
     }
     [[nodiscard]] static detail::Storage* storage(const Tensor& t) noexcept { return t.st_.get(); }
+    [[nodiscard]] static std::weak_ptr<detail::Storage> storage_ref(const Tensor& t) noexcept { return t.st_; }
     [[nodiscard]] static void* ptr(const Tensor& t) noexcept { return t.st_ ? t.st_->mem.get() : nullptr; }
     static void mark_written(const Tensor& t) noexcept
     {
@@ -183,6 +184,10 @@ public:
                                                     const Tensor* gamma_sub = nullptr, Scalar eps_sub = 1e-5f);
 
     [[nodiscard]] EngineInfo describe() const { return describe_impl(); }
+    // Activation quantizations bitlinear_i8_forward has run (an engine may reuse the last one
+    // for another BitLinear on the same input, e.g. the q / k / v projections). Diagnostic of
+    // this engine layer; the reference has no counterpart.
+    [[nodiscard]] virtual std::uint64_t activation_quantizations() const noexcept { return 0; }
     void begin_batch() {}
     void end_batch() { sync_impl(); }
     void flush_batch() { sync_impl(); }

@@ -714,6 +714,56 @@ void test_feedforward(nn::ComputeEngine& e)
     CHECK(!gelu.init(e).has_value(), "GeLU FeedForward is refused (only gated activations)");
 }
 
+// ---------------------------------------------------------------- [14]
+// The q / k / v projections of an attention input (three BitLinears on one tensor; GQA shapes:
+// kv narrower than d, compute_layer_attention.hpp) share one activation quantization in an engine
+// that reuses it; outputs equal what each projection gives on its own input copy.
+void test_shared_input_quantization(nn::ComputeEngine& e)
+{
+    std::puts("[14] q/k/v BitLinears on one input: one activation quantization, same bits");
+    constexpr std::size_t D = 64, KV = 16, B = 20;
+    nn::BitLinear q(D, D), k(D, KV), v(D, KV);
+    nn::PrecisionProfile prof;
+    prof.param = nn::Precision::T1_58;
+    bool ok = true;
+    unsigned seed = 301;
+    for (nn::BitLinear* l : {&q, &k, &v})
+    {
+        l->set_precision_profile(prof);
+        ok = ok && l->init(e).has_value();
+        auto ps = l->parameters();
+        ok = ok && ps.size() == 2 && e.copy_from(ps[0].get(), random_matrix(l == &q ? D : KV, D, seed++)).has_value() &&
+             e.copy_from(ps[1].get(), random_matrix(l == &q ? D : KV, 1, seed++)).has_value();
+        l->set_activation_quant(true);
+    }
+    CHECK(ok, "q/k/v init");
+    if (!ok) return;
+    nn::Tensor x = upload(e, random_matrix(D, B, 310));
+    const std::uint64_t n0 = e.activation_quantizations();
+    auto yq = q.forward(x), yk = k.forward(x), yv = v.forward(x);
+    CHECK(yq.has_value() && yk.has_value() && yv.has_value(), "q/k/v forward");
+    if (!(yq && yk && yv)) return;
+    const std::uint64_t n1 = e.activation_quantizations();
+    CHECK(n1 - n0 == 1, "one activation quantization for the three projections");
+    bool same = true;
+    for (auto [l, y] : {std::pair{&q, &*yq}, std::pair{&k, &*yk}, std::pair{&v, &*yv}})
+    {
+        const nn::Tensor xc = upload(e, random_matrix(D, B, 310));  // same values, own storage
+        auto yc = l->forward(xc);
+        same = same && yc.has_value() && bitwise_equal(download(e, *y), download(e, *yc));
+    }
+    CHECK(same, "each projection == the same projection on its own copy of the input");
+    CHECK(e.activation_quantizations() - n1 == 3, "copies in their own storage are quantized anew");
+    // a write to the input invalidates the shared quantization
+    CHECK(e.copy_from(x, random_matrix(D, B, 311)).has_value(), "overwrite the input");
+    auto yq2 = q.forward(x);
+    const nn::Tensor x2 = upload(e, random_matrix(D, B, 311));
+    auto yq3 = q.forward(x2);
+    CHECK(yq2.has_value() && yq3.has_value() && bitwise_equal(download(e, *yq2), download(e, *yq3)) &&
+              !bitwise_equal(download(e, *yq2), download(e, *yq)),
+          "after a write the input is quantized again");
+}
+
 // ---------------------------------------------------------------- [13]
 std::string g_golden = "tests/golden";
 
@@ -966,6 +1016,7 @@ int main(int argc, char** argv)
     test_float_products(e);
     test_feedforward(e);
     test_model_files_device(e);
+    test_shared_input_quantization(e);
     if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
     else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
     return g_failures == 0 ? 0 : 1;
