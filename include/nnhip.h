@@ -300,6 +300,60 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
                               const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
                               const float* b2, float* Y);
 
+/* ---- batched decode step (config C5): one new token for each of B sequences through the
+ *      GPT block's attention (AttentionBase::forward_step, include/neuralnet.cpp/
+ *      compute_layer_attention.hpp:1003-1091; GPTBlock::forward_step, compute_layer_gpt.hpp:
+ *      201-219; GPTModel::forward_step, compute_layer_gpt.hpp:693-724). The reference advances
+ *      one sequence per call; these entry points take B sequences, each at its own position. ---- */
+
+/* RoPE tables on the HOST: cos_out / sin_out (max_len, dk/2), entry (pos, j) = cos / sin of
+ * theta = float(pos) / powf(10000, float(2j) / float(dk)), evaluated in float as the reference's
+ * RotaryEmbedding::fill_pos_column_ does (include/neuralnet.cpp/compute_position_encoding.hpp:64-80;
+ * the reference stores each value twice, for j and j + dk/2). Upload them once per model. */
+nnhip_status nnhip_rope_table(size_t dk, size_t max_len, float* cos_out, float* sin_out);
+
+/* Context scratch nnhip_attention_decode uses for len_bound (0 when len_bound <= 128). */
+size_t nnhip_attention_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound);
+
+/* Attention of B new tokens over their sequences' KV caches (grouped-query heads, RoPE):
+ *   q (H*dk, B), k / v (Hkv*dk, B): the projections of the new tokens (column b = sequence b);
+ *   pos (B) int32, DEVICE: position of sequence b's new token (its cache length so far);
+ *   k_cache / v_cache (B, max_len, Hkv*dk), 16-byte aligned: row t of sequence b = the rotated
+ *   key (value) at position t; this call writes row pos[b] of each sequence;
+ *   rope_cos / rope_sin (max_len, dk/2) from nnhip_rope_table, or both NULL (no position encoding);
+ *   out (H*dk, B) = per head h: softmax((rot(q_h) . K^T) * scale) . V over positions [0, pos[b]],
+ *   with query head h reading KV head h / (H / Hkv).
+ * The new key is rotated at pos[b] ((q*cos + rotate_half(q)*sin), two rounded products and a
+ * rounded sum) and stored bit-exactly; the products and the softmax are f32 with an order the
+ * reference does not pin (results within 1e-5 relative of a float64 evaluation).
+ * len_bound bounds every pos[b] + 1 (it sizes the launch; len_bound <= max_len); a sequence
+ * whose pos[b] is outside [0, len_bound) gets NaN outputs and its cache is left unchanged.
+ * dk in {64, 128, 256}; H / Hkv <= 8.
+ * Replaces AttentionBase::forward_step steps 1.5-8 (compute_layer_attention.hpp:1022-1083: RoPE
+ * apply_qk_step, GQA gather_rows, insert_rows into the caches, batched scores, softmax,
+ * V^T . attn). */
+nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                    size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                    const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
+                                    size_t max_len, float scale, float* out);
+
+/* out[i] = x[i] + y[i] (one IEEE add; out may alias x or y). Replaces the residual adds
+ * dsl::compute(leaf(x) + leaf(a)) of GPTBlock::forward_step (compute_layer_gpt.hpp:208-218). */
+nnhip_status nnhip_add(nnhip_ctx* ctx, const float* x, const float* y, size_t n, float* out);
+
+/* out (d, B): column b = row ids[b] of the (V, d) embedding table (ids DEVICE int32; an id
+ * outside [0, V) gives a NaN column). Replaces gather_rows(token_emb, id) + transpose
+ * (compute_layer_gpt.hpp:700-704). */
+nnhip_status nnhip_embedding_gather(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
+                                    size_t B, float* out);
+
+/* ids[b] = greedy choice over column b of logits (V, B): the first index of the largest value,
+ * NaN never chosen except that a NaN at index 0 keeps index 0 (the reference's
+ * best = l[0]; if (l[v] > best) ... loop, compute_layer_base.hpp:1152-1160; the reference
+ * runs it on the softmax of the logits, which orders the same except where exp rounding
+ * merges two nearly equal logits). */
+nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids);
+
 #ifdef __cplusplus
 }
 #endif

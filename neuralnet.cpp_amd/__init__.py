@@ -103,6 +103,13 @@ SIGNATURES = {
     "nnhip_ffn_glu_workspace_bytes": (_sz, [_sz, _sz, _sz]),
     "nnhip_ffn_glu_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
                                _vp, _vp]),
+    "nnhip_rope_table": (_st, [_sz, _sz, _vp, _vp]),
+    "nnhip_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz, _sz]),
+    "nnhip_attention_decode": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _f,
+                                     _vp]),
+    "nnhip_add": (_st, [_vp, _vp, _vp, _sz, _vp]),
+    "nnhip_embedding_gather": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_argmax_cols": (_st, [_vp, _vp, _sz, _sz, _vp]),
 }
 
 ACT_SWIGLU, ACT_RELU2GLU = 0, 1
@@ -144,6 +151,19 @@ def act_i8_bytes(K: int, M: int) -> int:
 
 def glu_rows(F: int) -> int:
     return int(lib().nnhip_glu_rows(F))
+
+
+def rope_table(dk: int, max_len: int):
+    """Host RoPE tables (cos, sin), each (max_len, dk/2) float32 numpy (nnhip_rope_table)."""
+    import numpy as np
+    c = np.empty((max_len, dk // 2), np.float32)
+    s = np.empty((max_len, dk // 2), np.float32)
+    _check(lib().nnhip_rope_table(dk, max_len, _vp(c.ctypes.data), _vp(s.ctypes.data)), "nnhip_rope_table")
+    return c, s
+
+
+def attention_workspace_bytes(B: int, H: int, Hkv: int, dk: int, len_bound: int) -> int:
+    return int(lib().nnhip_attention_workspace_bytes(B, H, Hkv, dk, len_bound))
 
 
 def kp(K: int) -> int:
@@ -423,6 +443,58 @@ class Context:
                                           self._dev(Y, torch.float32, "Y")),
                "nnhip_ternary_matmul")
         return Y
+
+    # -- batched decode step
+    def attention_decode(self, q, k, v, H: int, Hkv: int, dk: int, pos, len_bound: int, k_cache, v_cache,
+                         scale: float, cos=None, sin=None, out=None):
+        """q (H*dk, B), k/v (Hkv*dk, B), pos (B) int32 device, caches (B, max_len, Hkv*dk) updated in
+        place (row pos[b]); cos/sin (max_len, dk/2) device tables or None. Returns out (H*dk, B)."""
+        torch = self._torch
+        B = q.shape[1]
+        max_len = k_cache.shape[1]
+        if out is None:
+            out = self._empty((H * dk, B), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_attention_decode(
+            self.h, self._dev(q, torch.float32, "q"), self._dev(k, torch.float32, "k"),
+            self._dev(v, torch.float32, "v"), B, H, Hkv, dk, self._dev(pos, torch.int32, "pos"), len_bound,
+            self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
+            self._dev(k_cache, torch.float32, "k_cache"), self._dev(v_cache, torch.float32, "v_cache"), max_len,
+            scale, self._dev(out, torch.float32, "out")), "nnhip_attention_decode")
+        return out
+
+    def add(self, x, y, out=None):
+        torch = self._torch
+        if out is None:
+            out = self._empty(tuple(x.shape), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_add(self.h, self._dev(x, torch.float32, "x"), self._dev(y, torch.float32, "y"),
+                               x.numel(), self._dev(out, torch.float32, "out")), "nnhip_add")
+        return out
+
+    def embedding_gather(self, table, ids, out=None):
+        """table (V, d), ids (B) int32 device -> (d, B)."""
+        torch = self._torch
+        V, d = table.shape
+        B = ids.shape[0]
+        if out is None:
+            out = self._empty((d, B), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_embedding_gather(self.h, self._dev(table, torch.float32, "table"),
+                                            self._dev(ids, torch.int32, "ids"), V, d, B,
+                                            self._dev(out, torch.float32, "out")), "nnhip_embedding_gather")
+        return out
+
+    def argmax_cols(self, logits, out=None):
+        """logits (V, B) -> (B) int32 greedy token ids."""
+        torch = self._torch
+        V, B = logits.shape
+        if out is None:
+            out = self._empty((B,), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_argmax_cols(self.h, self._dev(logits, torch.float32, "logits"), V, B,
+                                       self._dev(out, torch.int32, "out")), "nnhip_argmax_cols")
+        return out
 
     # -- gated feed-forward block
     def glu(self, Y1, act: int = ACT_SWIGLU):

@@ -198,4 +198,16 @@ hipError_t launch_glu(hipStream_t st, const float* Y1, size_t F, size_t M, int a
 hipError_t launch_glu_interleave(hipStream_t st, const uint32_t* wq, const float* tau, const float* bias, size_t F,
                                  size_t K, uint32_t* wq_out, float* tau_out, float* bias_out);
 
+// ---- batched decode step (k_decode.hip)
+size_t attn_chunks(size_t len_bound);
+size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound);
+hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
+                              size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
+                              const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
+                              float* out);
+hipError_t launch_add(hipStream_t st, const float* x, const float* y, size_t n, float* out);
+hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B,
+                        float* out);
+hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids);
+
 }  // namespace nnhip

@@ -1,0 +1,488 @@
+// k_decode.hip — the kernels of a batched decode step around the BitLinear path: attention of
+// one new token per sequence over its KV cache (grouped-query heads, RoPE, the cache append
+// fused in), the token-embedding gather, the residual add and the greedy argmax.
+//
+// Reference: AttentionBase::forward_step (include/neuralnet.cpp/compute_layer_attention.hpp:
+// 1003-1091) advances ONE sequence by one token: q/k/v projections, RoPE at position cur_len
+// (compute_position_encoding.hpp:150-166), append to the (max_len, H*dk) caches, scores =
+// (q . K^T) * scale per head, softmax, V^T . attn. Here B sequences advance one token each in
+// one launch, each at its own position, and the caches keep the Hkv KV heads un-expanded
+// (the reference's gather_rows expansion only duplicates rows: query head h reads KV head
+// h / (H / Hkv), compute_layer_attention.hpp:444-449).
+//
+// Layouts (device, f32):
+//   q      (H*dk, B)      feature-major, one column per sequence (the q projection's output)
+//   k, v   (Hkv*dk, B)    the new token's key / value
+//   caches (B, max_len, Hkv*dk)   row t of sequence b = the key (value) at position t
+//   out    (H*dk, B)
+//   pos    (B) int32      position of sequence b's new token (= its cache length before the call)
+//   cos/sin (max_len, dk/2) RoPE tables (the reference's cat(freqs, freqs) halves, stored once)
+//
+// Work split (flash-decoding): work-group (chunk c, KV head g, sequence b) covers cache
+// positions [128c, 128c + 128) for the R = H/Hkv query heads that share KV head g, so every
+// key/value row is read from HBM once for all of them. The scores of a chunk stay in LDS; the
+// chunk writes (acc[R][dk], max, sum) and a second kernel merges the chunks of each head. With
+// a single chunk (every sequence shorter than 129) the first kernel writes the output itself.
+// The work-group whose chunk holds position pos[b] writes the rotated key and the value into the
+// cache and uses them from LDS; no other work-group reads that row in the same launch.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace nnhip
+{
+namespace
+{
+
+constexpr int kAttnT = 128;        // cache positions per work-group
+constexpr int kAttnThreads = 256;  // 4 waves
+constexpr int kAttnMaxR = 8;       // query heads per KV head
+constexpr int kRecPad = 16;        // record tail: max[8], sum[8]
+
+struct AttnArgs
+{
+    const float* q;
+    const float* k;
+    const float* v;
+    const int32_t* pos;
+    const float* cosT;
+    const float* sinT;
+    float* kc;
+    float* vc;
+    float* part;
+    float* out;
+    int B, H, Hkv, R, max_len, len_bound, nchunk;
+    float scale;
+};
+
+__device__ __forceinline__ float sum8(float v)
+{
+    // sum over the 8 lanes {8i .. 8i+7}: quad permutes (xor 1, xor 2), then xor 4
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __shfl_xor(v, 4, kWave);
+    return v;
+}
+
+// RoPE on one (x0, x1) = (q[j], q[j + dk/2]) pair, as the reference's
+// q*cos + rotate_half(q)*sin with rotate_half(q)[j] = -q[j + dk/2], [j + dk/2] = q[j]:
+// two rounded products and a rounded sum per output (no fused multiply-add).
+__device__ __forceinline__ void rope_pair(float x0, float x1, float cs, float sn, float& y0, float& y1)
+{
+    y0 = __fadd_rn(__fmul_rn(x0, cs), __fmul_rn(-x1, sn));
+    y1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(x0, sn));
+}
+
+template <int DK, bool kFinal>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
+{
+    constexpr int HALF = DK / 2;
+    constexpr int Q4 = DK / 4;         // float4 per row
+    constexpr int F4 = DK / 32;        // float4 per lane in the score phase (8 lanes per position)
+    constexpr int PB = DK <= 128 ? 4 : 2;  // positions passes whose loads are issued together
+    constexpr int VL = DK / 4;         // lanes per row in the value phase
+    constexpr int NG = kAttnThreads / VL;  // rows per value step
+    __shared__ float4 q_s[kAttnMaxR * Q4];
+    __shared__ float4 kn_s[Q4], vn_s[Q4];
+    __shared__ float S[kAttnMaxR][kAttnT];
+    __shared__ float ml[2][kAttnMaxR];
+    __shared__ float4 red[4][kAttnMaxR * Q4];
+
+    const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int R = a.R;
+    const int p = a.pos[b];
+    const int t0 = c * kAttnT;
+    if (p < 0 || p >= a.len_bound)
+    {
+        // out-of-range position: NaN output for this sequence's heads, cache untouched
+        if (kFinal && c == 0)
+            for (int e = tid; e < R * DK; e += kAttnThreads)
+                a.out[(size_t)((g * R + e / DK) * DK + e % DK) * a.B + b] = __builtin_nanf("");
+        return;
+    }
+    const int len = p + 1;
+    if (t0 >= len) return;
+    const int n = min(kAttnT, len - t0);
+    const bool has_new = p < t0 + kAttnT;
+    const size_t rstride = (size_t)a.Hkv * DK;
+    const size_t seq_off = (size_t)b * a.max_len * rstride + (size_t)g * DK;
+
+    // ---- stage the rotated queries (R heads) and, in the chunk holding p, the new key/value
+    float* qf = reinterpret_cast<float*>(q_s);
+    for (int e = tid; e < R * HALF; e += kAttnThreads)
+    {
+        const int r = e / HALF, j = e - r * HALF;
+        const int h = g * R + r;
+        const float x0 = a.q[(size_t)(h * DK + j) * a.B + b];
+        const float x1 = a.q[(size_t)(h * DK + j + HALF) * a.B + b];
+        float y0 = x0, y1 = x1;
+        if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
+        qf[r * DK + j] = y0;
+        qf[r * DK + j + HALF] = y1;
+    }
+    if (has_new)
+    {
+        float* kf = reinterpret_cast<float*>(kn_s);
+        float* vf = reinterpret_cast<float*>(vn_s);
+        for (int j = tid; j < HALF; j += kAttnThreads)
+        {
+            const float x0 = a.k[(size_t)(g * DK + j) * a.B + b];
+            const float x1 = a.k[(size_t)(g * DK + j + HALF) * a.B + b];
+            float y0 = x0, y1 = x1;
+            if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
+            kf[j] = y0;
+            kf[j + HALF] = y1;
+        }
+        for (int i = tid; i < DK; i += kAttnThreads) vf[i] = a.v[(size_t)(g * DK + i) * a.B + b];
+    }
+    __syncthreads();
+    if (has_new)
+    {
+        float4* krow = reinterpret_cast<float4*>(a.kc + seq_off + (size_t)p * rstride);
+        float4* vrow = reinterpret_cast<float4*>(a.vc + seq_off + (size_t)p * rstride);
+        for (int i = tid; i < Q4; i += kAttnThreads)
+        {
+            krow[i] = kn_s[i];
+            vrow[i] = vn_s[i];
+        }
+    }
+
+    // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row
+    const int pg = tid >> 3, j8 = tid & 7;
+    const float* kbase = a.kc + seq_off;
+#pragma unroll
+    for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
+    {
+        float4 kv[PB][F4];
+#pragma unroll
+        for (int u = 0; u < PB; ++u)
+        {
+            const int tl = (pass0 + u) * 32 + pg;
+            const int t = t0 + tl;
+#pragma unroll
+            for (int i = 0; i < F4; ++i)
+            {
+                if (tl < n && t < p)
+                    kv[u][i] = *reinterpret_cast<const float4*>(kbase + (size_t)t * rstride + 4 * (j8 + 8 * i));
+                else if (tl < n)
+                    kv[u][i] = kn_s[j8 + 8 * i];
+                else
+                    kv[u][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < PB; ++u)
+        {
+            const int tl = (pass0 + u) * 32 + pg;
+            float d[kAttnMaxR];
+#pragma unroll
+            for (int r = 0; r < kAttnMaxR; ++r)
+            {
+                d[r] = 0.f;
+                if (r < R)
+                {
+#pragma unroll
+                    for (int i = 0; i < F4; ++i)
+                    {
+                        const float4 qq = q_s[r * Q4 + j8 + 8 * i];
+                        d[r] = __builtin_fmaf(kv[u][i].x, qq.x, d[r]);
+                        d[r] = __builtin_fmaf(kv[u][i].y, qq.y, d[r]);
+                        d[r] = __builtin_fmaf(kv[u][i].z, qq.z, d[r]);
+                        d[r] = __builtin_fmaf(kv[u][i].w, qq.w, d[r]);
+                    }
+                    d[r] = sum8(d[r]);
+                }
+            }
+            if (tl < n)
+            {
+#pragma unroll
+                for (int r = 0; r < kAttnMaxR; ++r)
+                    if (r < R && j8 == r) S[r][tl] = __fmul_rn(d[r], a.scale);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- chunk softmax statistics: one wave per head
+    const int w = tid >> 6, lane = tid & 63;
+    for (int r = w; r < R; r += 4)
+    {
+        float m = -__builtin_inff();
+        for (int i = lane; i < n; i += kWave) m = fmaxf(m, S[r][i]);
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+        float l = 0.f;
+        for (int i = lane; i < n; i += kWave)
+        {
+            const float e = expf(S[r][i] - m);
+            S[r][i] = e;
+            l += e;
+        }
+        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, kWave);
+        if (lane == 0)
+        {
+            ml[0][r] = m;
+            ml[1][r] = l;
+        }
+    }
+    __syncthreads();
+
+    // ---- values: VL lanes per row (one float4 each), NG rows per step, 8 steps of loads in flight
+    const int vg = tid / VL, vi = tid % VL;
+    const float* vbase = a.vc + seq_off;
+    float4 acc[kAttnMaxR];
+#pragma unroll
+    for (int r = 0; r < kAttnMaxR; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int base = vg; base < n; base += 8 * NG)
+    {
+        float4 vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            const int tl = base + u * NG;
+            const int t = t0 + tl;
+            if (tl < n && t < p)
+                vv[u] = *reinterpret_cast<const float4*>(vbase + (size_t)t * rstride + 4 * vi);
+            else if (tl < n)
+                vv[u] = vn_s[vi];
+            else
+                vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            const int tl = base + u * NG;
+            if (tl < n)
+            {
+#pragma unroll
+                for (int r = 0; r < kAttnMaxR; ++r)
+                    if (r < R)
+                    {
+                        const float pr = S[r][tl];
+                        acc[r].x = __builtin_fmaf(pr, vv[u].x, acc[r].x);
+                        acc[r].y = __builtin_fmaf(pr, vv[u].y, acc[r].y);
+                        acc[r].z = __builtin_fmaf(pr, vv[u].z, acc[r].z);
+                        acc[r].w = __builtin_fmaf(pr, vv[u].w, acc[r].w);
+                    }
+            }
+        }
+    }
+    // rows of one wave -> lanes [0, VL), then the 4 waves through LDS in a fixed order
+#pragma unroll
+    for (int r = 0; r < kAttnMaxR; ++r)
+        if (r < R)
+            for (int off = VL; off < kWave; off <<= 1)
+            {
+                acc[r].x += __shfl_xor(acc[r].x, off, kWave);
+                acc[r].y += __shfl_xor(acc[r].y, off, kWave);
+                acc[r].z += __shfl_xor(acc[r].z, off, kWave);
+                acc[r].w += __shfl_xor(acc[r].w, off, kWave);
+            }
+    if (lane < VL)
+    {
+#pragma unroll
+        for (int r = 0; r < kAttnMaxR; ++r)
+            if (r < R) red[w][r * Q4 + vi] = acc[r];
+    }
+    __syncthreads();
+    float* rec = a.part + ((size_t)(b * a.Hkv + g) * a.nchunk + c) * (size_t)(R * DK + kRecPad);
+    for (int e = tid; e < R * Q4; e += kAttnThreads)
+    {
+        float4 s4 = red[0][e];
+#pragma unroll
+        for (int ww = 1; ww < 4; ++ww)
+        {
+            s4.x += red[ww][e].x;
+            s4.y += red[ww][e].y;
+            s4.z += red[ww][e].z;
+            s4.w += red[ww][e].w;
+        }
+        if constexpr (kFinal)
+        {
+            const int r = e / Q4, i = 4 * (e - r * Q4);
+            const float l = ml[1][r];
+            float* o = a.out + (size_t)((g * R + r) * DK + i) * a.B + b;
+            o[0] = s4.x / l;
+            o[a.B] = s4.y / l;
+            o[2 * a.B] = s4.z / l;
+            o[3 * a.B] = s4.w / l;
+        }
+        else
+        {
+            reinterpret_cast<float4*>(rec)[e] = s4;
+        }
+    }
+    if constexpr (!kFinal)
+    {
+        if (tid < R)
+        {
+            rec[R * DK + tid] = ml[0][tid];
+            rec[R * DK + 8 + tid] = ml[1][tid];
+        }
+    }
+}
+
+// Merge the chunks of one (sequence, head): out = sum_c e_c acc_c / sum_c e_c l_c,
+// e_c = exp(max_c - max), chunks in ascending order.
+template <int DK>
+__global__ __launch_bounds__(DK) void k_attn_merge(AttnArgs a)
+{
+    const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int g = h / a.R, r = h % a.R;
+    const int i = threadIdx.x;
+    float* o = a.out + (size_t)(h * DK + i) * a.B + b;
+    const int p = a.pos[b];
+    if (p < 0 || p >= a.len_bound)
+    {
+        *o = __builtin_nanf("");
+        return;
+    }
+    const int nch = (p + kAttnT) / kAttnT;
+    const size_t stride = (size_t)(a.R * DK + kRecPad);
+    const float* rec0 = a.part + (size_t)(b * a.Hkv + g) * a.nchunk * stride;
+    float M = -__builtin_inff();
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, rec0[c * stride + a.R * DK + r]);
+    float num = 0.f, den = 0.f;
+    for (int c = 0; c < nch; ++c)
+    {
+        const float* rec = rec0 + c * stride;
+        const float e = expf(rec[a.R * DK + r] - M);
+        num = __builtin_fmaf(e, rec[r * DK + i], num);
+        den = __builtin_fmaf(e, rec[a.R * DK + 8 + r], den);
+    }
+    *o = num / den;
+}
+
+template <int DK>
+hipError_t launch_attn_dk(hipStream_t st, AttnArgs a)
+{
+    if (a.nchunk == 1)
+    {
+        k_attn_chunk<DK, true><<<dim3(1, a.Hkv, a.B), kAttnThreads, 0, st>>>(a);
+        return hipGetLastError();
+    }
+    k_attn_chunk<DK, false><<<dim3(a.nchunk, a.Hkv, a.B), kAttnThreads, 0, st>>>(a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_attn_merge<DK><<<dim3(a.B * a.H), DK, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+// ---- small kernels of the decode step
+
+constexpr int kSmallBlock = 256;
+
+__global__ __launch_bounds__(kSmallBlock) void k_add(const float* __restrict__ x, const float* __restrict__ y,
+                                                     size_t n, float* out)
+{
+    const size_t i = (size_t)blockIdx.x * kSmallBlock + threadIdx.x;
+    if (i < n) out[i] = __fadd_rn(x[i], y[i]);
+}
+
+// out (d, B): column b = row ids[b] of the (V, d) table (NaN column for an id outside [0, V))
+__global__ __launch_bounds__(kSmallBlock) void k_embed(const float* __restrict__ table, const int32_t* __restrict__ ids,
+                                                       int V, int d, int B, float* __restrict__ out)
+{
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * kSmallBlock + threadIdx.x;
+    if (i >= d) return;
+    const int id = ids[b];
+    out[(size_t)i * B + b] = (id >= 0 && id < V) ? table[(size_t)id * d + i] : __builtin_nanf("");
+}
+
+// ids[b] = the reference greedy rule over column b of logits (V, B): best = l[0], then every
+// l[v] > best replaces it (first index of the largest value; NaN entries never win, a NaN at
+// v = 0 keeps index 0).
+__global__ __launch_bounds__(kSmallBlock) void k_argmax(const float* __restrict__ L, int V, int B, int32_t* ids)
+{
+    __shared__ float sv[kSmallBlock / kWave];
+    __shared__ int si[kSmallBlock / kWave];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    float bv = -__builtin_inff();
+    int bi = -1;
+    for (int v = tid; v < V; v += kSmallBlock)
+    {
+        const float x = L[(size_t)v * B + b];
+        if (x == x && (bi < 0 || x > bv))
+        {
+            bv = x;
+            bi = v;
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1)
+    {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi)))
+        {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0)
+    {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0)
+    {
+        for (int w = 1; w < kSmallBlock / kWave; ++w)
+            if (si[w] >= 0 && (bi < 0 || sv[w] > bv || (sv[w] == bv && si[w] < bi)))
+            {
+                bv = sv[w];
+                bi = si[w];
+            }
+        const float l0 = L[b];
+        ids[b] = (l0 != l0 || bi < 0) ? 0 : bi;
+    }
+}
+
+}  // namespace
+
+size_t attn_chunks(size_t len_bound) { return ceil_div(len_bound, kAttnT); }
+
+size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound)
+{
+    const size_t nchunk = attn_chunks(len_bound);
+    if (nchunk <= 1) return 0;
+    return B * Hkv * nchunk * ((H / Hkv) * dk + kRecPad) * sizeof(float);
+}
+
+hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
+                              size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
+                              const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
+                              float* out)
+{
+    AttnArgs a{q, k, v, pos, cosT, sinT, kc, vc, part, out, (int)B, (int)H, (int)Hkv, (int)(H / Hkv),
+               (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale};
+    switch (dk)
+    {
+    case 64: return launch_attn_dk<64>(st, a);
+    case 128: return launch_attn_dk<128>(st, a);
+    case 256: return launch_attn_dk<256>(st, a);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_add(hipStream_t st, const float* x, const float* y, size_t n, float* out)
+{
+    k_add<<<dim3((unsigned)ceil_div(n, kSmallBlock)), kSmallBlock, 0, st>>>(x, y, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B,
+                        float* out)
+{
+    k_embed<<<dim3((unsigned)ceil_div(d, kSmallBlock), (unsigned)B), kSmallBlock, 0, st>>>(table, ids, (int)V, (int)d,
+                                                                                         (int)B, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids)
+{
+    k_argmax<<<dim3((unsigned)B), kSmallBlock, 0, st>>>(L, (int)V, (int)B, ids);
+    return hipGetLastError();
+}
+
+}  // namespace nnhip

@@ -7,6 +7,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <queue>
@@ -28,6 +29,8 @@ struct nnhip_ctx
     uint32_t* amax = nullptr;
     size_t amax_words = 0;
     int gemm_tile = NNHIP_GEMM_TILE_AUTO;
+    void* attn_ws = nullptr;  // per-chunk partial results of the decode attention
+    size_t attn_ws_bytes = 0;
 };
 
 struct nnhip_group
@@ -86,27 +89,34 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool mul_ok(size_t a, size_t b) { return a == 0 || b <= SIZE_MAX / a; }
 
-nnhip_status ensure_ws(nnhip_ctx* ctx, size_t bytes, const char* fn)
+// Grow a context-owned device buffer to at least `bytes` (waits for queued work first, because
+// a kernel in flight may still use the old buffer).
+nnhip_status ensure_buf(nnhip_ctx* ctx, void*& buf, size_t& have, size_t bytes, const char* fn, const char* what)
 {
-    if (ctx->ws_bytes >= bytes) return NNHIP_OK;
+    if (have >= bytes) return NNHIP_OK;
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
-    if (ctx->ws)
+    if (buf)
     {
-        e = hipFree(ctx->ws);
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
+        e = hipFree(buf);
+        buf = nullptr;
+        have = 0;
         if (e != hipSuccess) return hip_fail(fn, "hipFree", e);
     }
-    e = hipMalloc(&ctx->ws, bytes);
+    e = hipMalloc(&buf, bytes);
     if (e != hipSuccess)
     {
-        ctx->ws = nullptr;
+        buf = nullptr;
         (void)hipGetLastError();
-        return fail(NNHIP_ERR_OOM, fn, "workspace allocation of " + std::to_string(bytes) + " bytes failed");
+        return fail(NNHIP_ERR_OOM, fn, std::string(what) + " allocation of " + std::to_string(bytes) + " bytes failed");
     }
-    ctx->ws_bytes = bytes;
+    have = bytes;
     return NNHIP_OK;
+}
+
+nnhip_status ensure_ws(nnhip_ctx* ctx, size_t bytes, const char* fn)
+{
+    return ensure_buf(ctx, ctx->ws, ctx->ws_bytes, bytes, fn, "workspace");
 }
 
 nnhip_status ensure_amax(nnhip_ctx* ctx, size_t words, const char* fn)
@@ -242,6 +252,7 @@ nnhip_status nnhip_ctx_destroy(nnhip_ctx* ctx)
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->amax) (void)hipFree(ctx->amax);
+    if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
     if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
@@ -964,6 +975,98 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
                                           nullptr));
     }
     return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y);
+}
+
+/* ------------------------------------------------ batched decode step */
+
+nnhip_status nnhip_rope_table(size_t dk, size_t max_len, float* cos_out, float* sin_out)
+{
+    const char* fn = "nnhip_rope_table";
+    NNHIP_REQUIRE(dk >= 2 && dk % 2 == 0, fn, "dk must be positive and even");
+    NNHIP_REQUIRE(max_len == 0 || (cos_out && sin_out), fn, "null pointer");
+    NNHIP_REQUIRE(max_len <= kMaxDim && mul_ok(max_len, dk / 2), fn, "size overflow");
+    // RotaryEmbedding::fill_pos_column_ (include/neuralnet.cpp/compute_position_encoding.hpp:64-80),
+    // in float like the reference's Scalar: theta = pos / 10000^(2j/dk), cos/sin of it
+    const size_t half = dk / 2;
+    for (size_t pos = 0; pos < max_len; ++pos)
+    {
+        const float pd = static_cast<float>(pos);
+        for (size_t j = 0; j < half; ++j)
+        {
+            const float theta = pd / std::pow(10000.0f, static_cast<float>(2 * j) / static_cast<float>(dk));
+            cos_out[pos * half + j] = std::cos(theta);
+            sin_out[pos * half + j] = std::sin(theta);
+        }
+    }
+    return NNHIP_OK;
+}
+
+size_t nnhip_attention_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound)
+{
+    if (Hkv == 0 || H % Hkv != 0) return 0;
+    return attn_workspace_bytes(B, H, Hkv, dk, len_bound);
+}
+
+nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                    size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                    const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
+                                    size_t max_len, float scale, float* out)
+{
+    const char* fn = "nnhip_attention_decode";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(q && k && v && pos && k_cache && v_cache && out, fn, "null pointer");
+    NNHIP_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), fn, "rope_cos and rope_sin go together");
+    NNHIP_REQUIRE(dk == 64 || dk == 128 || dk == 256, fn, "dk must be 64, 128 or 256");
+    NNHIP_REQUIRE(Hkv >= 1 && H >= Hkv && H % Hkv == 0 && H / Hkv <= 8, fn,
+                  "H must be a multiple of Hkv with at most 8 query heads per KV head");
+    NNHIP_REQUIRE(B <= 65535 && Hkv <= 65535 && H * dk <= kMaxDim, fn, "B, Hkv or H*dk too large");
+    NNHIP_REQUIRE(max_len >= 1 && max_len <= (1u << 24), fn, "max_len must be in [1, 2^24]");
+    NNHIP_REQUIRE(len_bound >= 1 && len_bound <= max_len, fn, "len_bound must be in [1, max_len]");
+    NNHIP_REQUIRE(mul_ok(B, max_len) && mul_ok(B * max_len, Hkv * dk), fn, "cache size overflow");
+    NNHIP_REQUIRE(aligned16(k_cache) && aligned16(v_cache), fn, "caches must be 16-byte aligned");
+    const size_t wsb = attn_workspace_bytes(B, H, Hkv, dk, len_bound);
+    if (wsb > 0)
+    {
+        const nnhip_status st = ensure_buf(ctx, ctx->attn_ws, ctx->attn_ws_bytes, wsb, fn, "attention workspace");
+        if (st != NNHIP_OK) return st;
+    }
+    NNHIP_LAUNCH(fn, launch_attn_decode(ctx->stream, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin,
+                                        k_cache, v_cache, max_len, scale, static_cast<float*>(ctx->attn_ws), out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_add(nnhip_ctx* ctx, const float* x, const float* y, size_t n, float* out)
+{
+    const char* fn = "nnhip_add";
+    NNHIP_CHECK_CTX(fn);
+    if (n == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(x && y && out, fn, "null pointer");
+    NNHIP_LAUNCH(fn, launch_add(ctx->stream, x, y, n, out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_embedding_gather(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
+                                    size_t B, float* out)
+{
+    const char* fn = "nnhip_embedding_gather";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0 || d == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(table && ids && out, fn, "null pointer");
+    NNHIP_REQUIRE(V >= 1 && V <= kMaxDim && d <= kMaxDim && B <= 65535 && mul_ok(V, d), fn, "size out of range");
+    NNHIP_LAUNCH(fn, launch_embed(ctx->stream, table, ids, V, d, B, out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids)
+{
+    const char* fn = "nnhip_argmax_cols";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(logits && ids, fn, "null pointer");
+    NNHIP_REQUIRE(V >= 1 && V <= kMaxDim && B <= kMaxDim && mul_ok(V, B), fn, "size out of range");
+    NNHIP_LAUNCH(fn, launch_argmax(ctx->stream, logits, V, B, ids));
+    return NNHIP_OK;
 }
 
 }  // extern "C"

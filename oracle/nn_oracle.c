@@ -636,3 +636,142 @@ void orc_ffn_glu_i8(const float* X, const float* gamma, float eps, size_t d, siz
     free(y1);
     free(x1);
 }
+
+/* ================================================================ batched decode step */
+
+/* RotaryEmbedding::fill_pos_column_ (include/neuralnet.cpp/compute_position_encoding.hpp:64-80):
+ * theta = pos / 10000^(2j/dk) in float, then cos / sin of it; the reference writes each value
+ * for j and j + dk/2, this table keeps it once: (max_len, dk/2). */
+void orc_rope_table(size_t dk, size_t max_len, float* cos_out, float* sin_out)
+{
+    const size_t half = dk / 2;
+    for (size_t pos = 0; pos < max_len; ++pos)
+    {
+        const float pd = (float)pos;
+        for (size_t j = 0; j < half; ++j)
+        {
+            const float theta = pd / powf(10000.0f, (float)(2 * j) / (float)dk);
+            cos_out[pos * half + j] = cosf(theta);
+            sin_out[pos * half + j] = sinf(theta);
+        }
+    }
+}
+
+/* out = x*cos + rotate_half(x)*sin for one head vector (compute_position_encoding.hpp:150-166):
+ * rotate_half(x)[j] = -x[j + dk/2] (j < dk/2), x[j - dk/2] (j >= dk/2); every product and the
+ * sum are separately rounded. out may not alias x. */
+void orc_rope_apply(const float* x, size_t dk, const float* cos_row, const float* sin_row, float* out)
+{
+    const size_t half = dk / 2;
+    for (size_t j = 0; j < half; ++j)
+    {
+        const float c = cos_row[j], s = sin_row[j];
+        const float a = x[j] * c, b = (-x[j + half]) * s;
+        out[j] = a + b;
+        const float a2 = x[j + half] * c, b2 = x[j] * s;
+        out[j + half] = a2 + b2;
+    }
+}
+
+/* AttentionBase::forward_step steps 1.5-8 (compute_layer_attention.hpp:1022-1083) for B
+ * sequences: rotate q and the new key at pos[b] (apply_qk_step), store key and value at row
+ * pos[b] (insert_rows), then per query head h (KV head h / (H/Hkv), the gather_rows map of
+ * :444-449): scores_t = fl(q_h . K_t) * scale over t <= pos[b] (dot products accumulated in
+ * ascending i), softmax exp(s - max) / sum (compute_layer_softmax.hpp:56-66, sum ascending in t),
+ * out_i = sum_t attn_t * V_t[i] (ascending t). Layouts as nnhip_attention_decode. cosT == NULL:
+ * no rotation. */
+void orc_attention_decode(const float* q, const float* k, const float* v, size_t B, size_t H, size_t Hkv,
+                          size_t dk, const int32_t* pos, const float* cosT, const float* sinT, float* k_cache,
+                          float* v_cache, size_t max_len, float scale, float* out)
+{
+    const size_t R = H / Hkv, half = dk / 2, row = Hkv * dk;
+    float* xbuf = (float*)malloc(dk * sizeof(float));
+    float* qr = (float*)malloc(dk * sizeof(float));
+    float* sc = (float*)malloc(max_len * sizeof(float));
+    for (size_t b = 0; b < B; ++b)
+    {
+        const int32_t p = pos[b];
+        float* kc = k_cache + b * max_len * row;
+        float* vc = v_cache + b * max_len * row;
+        if (p < 0 || (size_t)p >= max_len)
+        {
+            for (size_t e = 0; e < H * dk; ++e) out[e * B + b] = NAN;
+            continue;
+        }
+        for (size_t g = 0; g < Hkv; ++g)
+        {
+            for (size_t i = 0; i < dk; ++i) xbuf[i] = k[(g * dk + i) * B + b];
+            if (cosT)
+                orc_rope_apply(xbuf, dk, cosT + (size_t)p * half, sinT + (size_t)p * half, kc + (size_t)p * row + g * dk);
+            else
+                memcpy(kc + (size_t)p * row + g * dk, xbuf, dk * sizeof(float));
+            for (size_t i = 0; i < dk; ++i) vc[(size_t)p * row + g * dk + i] = v[(g * dk + i) * B + b];
+        }
+        for (size_t h = 0; h < H; ++h)
+        {
+            const size_t g = h / R;
+            for (size_t i = 0; i < dk; ++i) xbuf[i] = q[(h * dk + i) * B + b];
+            if (cosT)
+                orc_rope_apply(xbuf, dk, cosT + (size_t)p * half, sinT + (size_t)p * half, qr);
+            else
+                memcpy(qr, xbuf, dk * sizeof(float));
+            float m = -INFINITY;
+            for (int32_t t = 0; t <= p; ++t)
+            {
+                const float* kt = kc + (size_t)t * row + g * dk;
+                float d = 0.0f;
+                for (size_t i = 0; i < dk; ++i)
+                {
+                    const float pr = qr[i] * kt[i];
+                    d = d + pr;
+                }
+                sc[t] = d * scale;
+                if (sc[t] > m) m = sc[t];
+            }
+            float l = 0.0f;
+            for (int32_t t = 0; t <= p; ++t)
+            {
+                sc[t] = expf(sc[t] - m);
+                l = l + sc[t];
+            }
+            for (int32_t t = 0; t <= p; ++t) sc[t] = sc[t] / l;
+            for (size_t i = 0; i < dk; ++i)
+            {
+                float o = 0.0f;
+                for (int32_t t = 0; t <= p; ++t)
+                {
+                    const float pr = sc[t] * vc[(size_t)t * row + g * dk + i];
+                    o = o + pr;
+                }
+                out[(h * dk + i) * B + b] = o;
+            }
+        }
+    }
+    free(xbuf);
+    free(qr);
+    free(sc);
+}
+
+/* gather_rows(token_emb, id) + transpose (compute_layer_gpt.hpp:700-704) for B ids:
+ * out (d, B), NaN column for an id outside [0, V). */
+void orc_embedding_gather(const float* table, const int32_t* ids, size_t V, size_t d, size_t B, float* out)
+{
+    for (size_t b = 0; b < B; ++b)
+        for (size_t i = 0; i < d; ++i)
+            out[i * B + b] = (ids[b] >= 0 && (size_t)ids[b] < V) ? table[(size_t)ids[b] * d + i] : NAN;
+}
+
+/* The greedy branch of sample_next_token_ (compute_layer_base.hpp:1152-1160) over
+ * logits[v * stride], v < V. */
+int32_t orc_argmax(const float* logits, size_t V, size_t stride)
+{
+    size_t next = 0;
+    float best = logits[0];
+    for (size_t v = 1; v < V; ++v)
+        if (logits[v * stride] > best)
+        {
+            best = logits[v * stride];
+            next = v;
+        }
+    return (int32_t)next;
+}

@@ -37,6 +37,18 @@
  *                       FeedForward::forward (compute_layer_feedforward.hpp:182-206, with the
  *                       optional SubLN RMSNorm before fc2); checked against a numpy composition
  *                       (int64 products) in the tests
+ *   orc_rope_table    : RotaryEmbedding::fill_pos_column_ (include/neuralnet.cpp/
+ *                       compute_position_encoding.hpp:64-80) in float; checked bit for bit
+ *                       against libnn-hip.so's host table and against float64 cos/sin
+ *   orc_rope_apply    : q*cos + rotate_half(q)*sin (compute_position_encoding.hpp:150-166);
+ *                       checked against a float64 complex rotation (z * e^{i theta}) of the
+ *                       (j, j + dk/2) pairs and unit-vector cases
+ *   orc_attention_decode : AttentionBase::forward_step steps 1.5-8 (compute_layer_attention.hpp:
+ *                       1022-1083) per sequence, softmax as Softmax::forward
+ *                       (compute_layer_softmax.hpp:56-66); checked against a float64 numpy
+ *                       attention, and exactly on the closed forms (one position -> v; equal keys
+ *                       -> mean of v) and on a GQA head map with distinct KV heads
+ *   orc_argmax        : the greedy loop of sample_next_token_ (compute_layer_base.hpp:1152-1160)
  */
 #ifndef NN_ORACLE_H
 #define NN_ORACLE_H
@@ -106,6 +118,15 @@ void orc_ffn_glu_i8(const float* X, const float* gamma, float eps, size_t d, siz
                     const uint32_t* wq1, const float* tau1, const float* b1, const float* gamma_sub,
                     float eps_sub, const uint32_t* wq2, const float* tau2, const float* b2, int threads,
                     float* h_out, float* Y);
+
+/* ---- batched decode step (config C5) ---- */
+void orc_rope_table(size_t dk, size_t max_len, float* cos_out, float* sin_out);
+void orc_rope_apply(const float* x, size_t dk, const float* cos_row, const float* sin_row, float* out);
+void orc_attention_decode(const float* q, const float* k, const float* v, size_t B, size_t H, size_t Hkv,
+                          size_t dk, const int32_t* pos, const float* cosT, const float* sinT, float* k_cache,
+                          float* v_cache, size_t max_len, float scale, float* out);
+void orc_embedding_gather(const float* table, const int32_t* ids, size_t V, size_t d, size_t B, float* out);
+int32_t orc_argmax(const float* logits, size_t V, size_t stride);
 
 /* ---- MI355X tile layout of packed ternary weights (checker for the repacker) ---- */
 size_t orc_repacked_words(size_t N, size_t K);

@@ -65,6 +65,12 @@ def lib() -> ctypes.CDLL:
             "orc_ffn_glu_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _sz, ctypes.c_int,
                                       _u32p, _f32p, _f32p, _f32p, ctypes.c_float, _u32p, _f32p, _f32p, ctypes.c_int,
                                       _f32p, _f32p]),
+            "orc_rope_table": (None, [_sz, _sz, _f32p, _f32p]),
+            "orc_rope_apply": (None, [_f32p, _sz, _f32p, _f32p, _f32p]),
+            "orc_attention_decode": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _i32p, _f32p, _f32p, _f32p,
+                                            _f32p, _sz, ctypes.c_float, _f32p]),
+            "orc_embedding_gather": (None, [_f32p, _i32p, _sz, _sz, _sz, _f32p]),
+            "orc_argmax": (ctypes.c_int32, [_f32p, _sz, _sz]),
             "orc_repacked_words": (_sz, [_sz, _sz]),
             "orc_repack": (None, [_u32p, _sz, _sz, _u32p]),
             "orc_unrepack": (None, [_u32p, _sz, _sz, _u32p]),
@@ -322,6 +328,63 @@ def unrepack(rp: np.ndarray, N: int, K: int) -> np.ndarray:
     out = np.empty((N, trit_words_per_row(K)), np.uint32)
     lib().orc_unrepack(_p(rp, ctypes.c_uint32), N, K, _p(out, ctypes.c_uint32))
     return out
+
+
+# ---- batched decode step (config C5)
+
+def rope_table(dk: int, max_len: int):
+    """(cos, sin), each (max_len, dk/2) float32, as RotaryEmbedding::fill_pos_column_."""
+    c = np.empty((max_len, dk // 2), np.float32)
+    s = np.empty((max_len, dk // 2), np.float32)
+    lib().orc_rope_table(dk, max_len, _p(c, ctypes.c_float), _p(s, ctypes.c_float))
+    return c, s
+
+
+def rope_apply(x: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndarray:
+    """x*cos + rotate_half(x)*sin for one head vector x (dk)."""
+    x, c, s = _f32(x), _f32(cos_row), _f32(sin_row)
+    out = np.empty_like(x)
+    lib().orc_rope_apply(_p(x, ctypes.c_float), x.shape[0], _p(c, ctypes.c_float), _p(s, ctypes.c_float),
+                         _p(out, ctypes.c_float))
+    return out
+
+
+def attention_decode(q, k, v, H: int, Hkv: int, dk: int, pos, k_cache, v_cache, scale: float,
+                     cos=None, sin=None):
+    """One decode step for B sequences; q (H*dk, B), k/v (Hkv*dk, B), caches (B, max_len, Hkv*dk)
+    are updated IN PLACE (row pos[b] written). Returns out (H*dk, B)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B = q.shape[1]
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    assert k_cache.dtype == np.float32 and k_cache.flags["C_CONTIGUOUS"]
+    assert v_cache.dtype == np.float32 and v_cache.flags["C_CONTIGUOUS"]
+    max_len = k_cache.shape[1]
+    out = np.empty((H * dk, B), np.float32)
+    keep = (None if cos is None else _f32(cos), None if sin is None else _f32(sin))
+    cp = None if keep[0] is None else _p(keep[0], ctypes.c_float)
+    sp = None if keep[1] is None else _p(keep[1], ctypes.c_float)
+    lib().orc_attention_decode(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(v, ctypes.c_float), B, H, Hkv, dk,
+                               _p(pos, ctypes.c_int32), cp, sp, _p(k_cache, ctypes.c_float),
+                               _p(v_cache, ctypes.c_float), max_len, scale, _p(out, ctypes.c_float))
+    return out
+
+
+def embedding_gather(table: np.ndarray, ids) -> np.ndarray:
+    table = _f32(table)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    V, d = table.shape
+    out = np.empty((d, ids.shape[0]), np.float32)
+    lib().orc_embedding_gather(_p(table, ctypes.c_float), _p(ids, ctypes.c_int32), V, d, ids.shape[0],
+                               _p(out, ctypes.c_float))
+    return out
+
+
+def argmax_cols(L: np.ndarray) -> np.ndarray:
+    """Greedy token per column of logits (V, B)."""
+    L = _f32(L)
+    V, B = L.shape
+    flat = L.reshape(-1)
+    return np.array([lib().orc_argmax(_p(flat[b:], ctypes.c_float), V, B) for b in range(B)], np.int32)
 
 
 # ---- helpers on the reference containers (pure numpy; used by tests to cross-check) ----

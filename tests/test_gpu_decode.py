@@ -1,0 +1,179 @@
+"""GPU parity of the batched decode step (config C5): decode attention over per-sequence KV
+caches (grouped-query heads, RoPE, cache append), residual add, embedding gather and greedy
+argmax, against the CPU oracle.
+
+The cache rows the kernel appends (rotated keys, values), the adds, the gathers and the greedy
+ids are compared bit for bit. The attention output is compared within 5e-6 x max(1, max|out|)
+of the oracle and of a float64 evaluation: its dot products and softmax sums are f32 in an
+order the reference leaves open (AttentionBase::forward_step runs them as engine matmuls,
+include/neuralnet.cpp/compute_layer_attention.hpp:1059-1083).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import normal, uniform
+from test_oracle_decode import _attn64
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 5e-6   # x max(1, max|out|)
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return a.shape == b.shape and np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+def run_case(ctx, orc, nnhip, B, H, Hkv, dk, max_len, pos, len_bound, rope, seed, check64=True):
+    say(f"attention B={B} H={H} Hkv={Hkv} dk={dk} max_len={max_len} pos={list(pos)[:8]} len_bound={len_bound} "
+        f"rope={rope}")
+    q = normal((H * dk, B), seed)
+    k = normal((Hkv * dk, B), seed + 1)
+    v = normal((Hkv * dk, B), seed + 2)
+    kc = normal((B, max_len, Hkv * dk), seed + 3)
+    vc = normal((B, max_len, Hkv * dk), seed + 4)
+    cos, sin = nnhip.rope_table(dk, max_len) if rope else (None, None)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(dk)))
+    kc_d, vc_d = dev(kc), dev(vc)
+    out_d = ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, dev(np.array(pos, np.int32)), len_bound,
+                                 kc_d, vc_d, scale, None if cos is None else dev(cos), None if sin is None else dev(sin))
+    out = host(out_d)
+    kc_o, vc_o = kc.copy(), vc.copy()
+    ref = orc.attention_decode(q, k, v, H, Hkv, dk, pos, kc_o, vc_o, scale, cos, sin)
+    assert same_bits(host(kc_d), kc_o), "key cache differs"
+    assert same_bits(host(vc_d), vc_o), "value cache differs"
+    tol = ATOL * max(1.0, float(np.max(np.abs(ref))))
+    assert np.max(np.abs(out - ref)) <= tol
+    if check64:
+        ref64 = _attn64(q, kc_o, vc_o, H, Hkv, dk, pos, cos, sin, scale)
+        assert np.max(np.abs(out - ref64)) <= tol
+    return out
+
+
+@pytest.mark.parametrize("B,H,Hkv,dk,pos,rope", [
+    (1, 4, 4, 64, [0], True),            # single position: out = v
+    (2, 8, 2, 128, [5, 130], True),      # second chunk
+    (3, 20, 5, 128, [127, 128, 300], True),  # chunk boundaries 128 / 129 positions
+    (2, 4, 1, 256, [40, 3], False),      # dk 256, no rotation
+    (2, 16, 2, 128, [200, 17], True),    # 8 query heads per KV head
+    (4, 4, 2, 64, [63, 64, 255, 256], True),
+])
+def test_attention_decode_parity(ctx, orc, nnhip, B, H, Hkv, dk, pos, rope):
+    max_len = 320
+    run_case(ctx, orc, nnhip, B, H, Hkv, dk, max_len, pos, max(pos) + 1, rope, 0xD0 + B * 7 + dk)
+    # the same with the launch sized for the whole cache
+    run_case(ctx, orc, nnhip, B, H, Hkv, dk, max_len, pos, max_len, rope, 0xD1 + B * 7 + dk)
+
+
+def test_attention_decode_ragged_batch16(ctx, orc, nnhip):
+    """Config C5's heads (20 query / 5 KV, dk = 128) at batch 16 with ragged positions."""
+    pos = [0, 1, 2, 127, 128, 129, 255, 256, 511, 700, 1000, 1023, 1024, 1500, 2047, 2100]
+    run_case(ctx, orc, nnhip, 16, 20, 5, 128, 2176, pos, 2176, True, 0xC5, check64=False)
+
+
+def test_attention_decode_incremental(ctx, orc, nnhip):
+    """Several steps in a row from empty caches (zeros), each sequence starting at its own
+    position: every step's output and both caches stay with the oracle."""
+    import torch
+    B, H, Hkv, dk, max_len = 3, 8, 2, 64, 300
+    cos, sin = nnhip.rope_table(dk, max_len)
+    cos_d, sin_d = dev(cos), dev(sin)
+    kc = np.zeros((B, max_len, Hkv * dk), np.float32)
+    vc = np.zeros_like(kc)
+    kc_d, vc_d = dev(kc), dev(vc)
+    start = np.array([0, 120, 250], np.int32)
+    for step in range(10):
+        say(f"incremental step {step}")
+        pos = start + step
+        q = normal((H * dk, B), 100 + step)
+        k = normal((Hkv * dk, B), 200 + step)
+        v = normal((Hkv * dk, B), 300 + step)
+        out = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, dev(pos), int(pos.max()) + 1,
+                                        kc_d, vc_d, 0.125, cos_d, sin_d))
+        ref = orc.attention_decode(q, k, v, H, Hkv, dk, pos, kc, vc, 0.125, cos, sin)
+        assert np.max(np.abs(out - ref)) <= ATOL * max(1.0, float(np.max(np.abs(ref))))
+    torch.cuda.synchronize()
+    assert same_bits(host(kc_d), kc) and same_bits(host(vc_d), vc)
+
+
+def test_attention_decode_bad_position(ctx, nnhip):
+    """A position outside [0, len_bound) gives NaN outputs for that sequence and leaves its
+    cache alone; the other sequences are unaffected."""
+    B, H, Hkv, dk, max_len = 3, 4, 2, 64, 200
+    q = normal((H * dk, B), 1)
+    k = normal((Hkv * dk, B), 2)
+    v = normal((Hkv * dk, B), 3)
+    kc = normal((B, max_len, Hkv * dk), 4)
+    vc = normal((B, max_len, Hkv * dk), 5)
+    for len_bound in (150, 10):     # two chunks / one chunk
+        pos = np.array([-1, 5, len_bound], np.int32)
+        kc_d, vc_d = dev(kc), dev(vc)
+        say(f"bad position len_bound={len_bound}")
+        out = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, dev(pos), len_bound, kc_d, vc_d, 0.125))
+        assert np.all(np.isnan(out[:, 0])) and np.all(np.isnan(out[:, 2]))
+        assert np.all(np.isfinite(out[:, 1]))
+        kg, vg = host(kc_d), host(vc_d)
+        assert same_bits(kg[0], kc[0]) and same_bits(kg[2], kc[2]) and same_bits(vg[2], vc[2])
+        assert not same_bits(kg[1], kc[1])
+    with pytest.raises(nnhip.NNHipError):    # len_bound above max_len is refused on the host
+        ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, dev(np.zeros(B, np.int32)), max_len + 1,
+                             dev(kc), dev(vc), 0.125)
+
+
+def test_attention_decode_c5_full_context(ctx, orc, nnhip):
+    """Config C5's decode step at full context: 16 sequences at position 2048 of a 2176-row
+    cache, sampled sequences checked against the oracle."""
+    B, H, Hkv, dk, max_len = 16, 20, 5, 128, 2176
+    say("attention C5 full context")
+    q = normal((H * dk, B), 11)
+    k = normal((Hkv * dk, B), 12)
+    v = normal((Hkv * dk, B), 13)
+    kc = normal((B, max_len, Hkv * dk), 14)
+    vc = normal((B, max_len, Hkv * dk), 15)
+    cos, sin = nnhip.rope_table(dk, max_len)
+    pos = np.full(B, 2048, np.int32)
+    kc_d, vc_d = dev(kc), dev(vc)
+    out = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, dev(pos), 2049, kc_d, vc_d,
+                                    float(np.float32(1) / np.float32(math.sqrt(dk))), dev(cos), dev(sin)))
+    for b in (0, 7, 15):
+        kcb, vcb = kc[b:b + 1].copy(), vc[b:b + 1].copy()
+        ref = orc.attention_decode(q[:, b:b + 1], k[:, b:b + 1], v[:, b:b + 1], H, Hkv, dk, pos[b:b + 1], kcb, vcb,
+                                   float(np.float32(1) / np.float32(math.sqrt(dk))), cos, sin)
+        assert np.max(np.abs(out[:, b:b + 1] - ref)) <= ATOL * max(1.0, float(np.max(np.abs(ref))))
+        assert same_bits(host(kc_d[b]), kcb[0])
+
+
+def test_add_gather_argmax_bitexact(ctx, orc):
+    say("add / gather / argmax")
+    x = normal((2560, 16), 21)
+    y = normal((2560, 16), 22)
+    assert same_bits(host(ctx.add(dev(x), dev(y))), x + y)
+    table = normal((1000, 2560), 23)
+    ids = np.array([0, 999, 5, 5, 17, -3, 1000, 42], np.int32)
+    assert same_bits(host(ctx.embedding_gather(dev(table), dev(ids))), orc.embedding_gather(table, ids))
+    L = uniform((10000, 16), 24)
+    L[:, 3] = 0.5          # all ties
+    L[0, 4] = np.nan       # NaN at index 0
+    L[7, 5] = np.nan
+    L[11, 6] = np.inf
+    L[12, 6] = np.inf
+    L[:, 7] = np.nan
+    L[9999, 8] = 2.0
+    assert host(ctx.argmax_cols(dev(L))).tolist() == orc.argmax_cols(L).tolist()
