@@ -288,6 +288,100 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
     log(f"matmul_q: {res}")
 
 
+def decode_c5_line(ctx, torch, stream, steps, out):
+    """Config C5's decode: a 30-layer BitNet-b1.58 GPT (d=2560, 20 heads / 5 KV heads of 128,
+    SwiGLU FFN 6912 with SubLN, vocab 10000, BitLinear LM head) generating 128 greedy tokens for
+    16 sequences after a 2048-token context. The context's KV cache is synthetic (random keys and
+    values at positions 0..2047, as if prefilled); every step runs the whole model on the GPU
+    (embedding, 30 blocks, final norm, head, greedy argmax) and feeds its ids and positions to the
+    next step. The step is captured once in a graph and replayed 128 times. Also timed: the same
+    step issued eagerly, and one layer's attention call alone against HBM bandwidth."""
+    nn = load_pkg()
+    from nnhip_py import decoder as dm
+    L, d, H, Hkv, F, V, B, ctx_len, new = 30, D, 20, 5, FFN, 10000, 16, 2048, 128
+    max_len = ctx_len + new
+    cfg = dm.Config(d=d, H=H, Hkv=Hkv, F=F, vocab=V, max_len=max_len, act=0, eps=1e-5)
+    dk = cfg.dk
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xB17AC500)
+
+    def lin(N, K):
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        tau = ctx.row_absmean(W)
+        wq = ctx.trit_pack(W, tau)
+        del W
+        return wq, tau
+
+    ones_d, ones_f = torch.ones(d, device="cuda"), torch.ones(F, device="cuda")
+    blocks, wbytes = [], 0
+    for _ in range(L):
+        mats = {}
+        for name, N, K in (("q", d, d), ("k", Hkv * dk, d), ("v", Hkv * dk, d), ("o", d, d), ("fc2", d, F)):
+            wq, tau = lin(N, K)
+            mats[name] = dm.Linear(ctx.repack(wq, K), tau, None, N, K)
+            wbytes += N * K // 4
+        wq1, t1 = lin(2 * F, d)
+        wo, to, _ = ctx.glu_interleave(wq1, t1, None, F, d)
+        del wq1
+        wbytes += 2 * F * d // 4
+        fc1 = dm.Linear(ctx.repack(wo, d), to, None, nn.glu_rows(F), d)
+        blocks.append(dm.Block(g1=ones_d, q=mats["q"], k=mats["k"], v=mats["v"], o=mats["o"], g2=ones_d, fc1=fc1,
+                               fc2=mats["fc2"], g_attn_sub=ones_d, g_ffn_sub=ones_f))
+    hq, ht = lin(V, d)
+    head = dm.Linear(ctx.repack(hq, d), ht, None, V, d)
+    wbytes += V * d // 4
+    emb = torch.randn((V, d), generator=gen, device="cuda")
+    caches = [(torch.randn((B, max_len, Hkv * dk), generator=gen, device="cuda"),
+               torch.randn((B, max_len, Hkv * dk), generator=gen, device="cuda")) for _ in range(L)]
+    dec = dm.Decoder(ctx, cfg, blocks, emb, ones_d, head, B, caches=caches)
+    ids = torch.randint(0, V, (B,), generator=gen, device="cuda", dtype=torch.int32)
+    pos = torch.full((B,), ctx_len, device="cuda", dtype=torch.int32)
+
+    def one_step():
+        dec.step(ids, pos, max_len)
+        ids.copy_(dec.ids)
+        pos.add_(1)
+
+    one_step()                           # warm-up: context scratch grows outside the capture
+    torch.cuda.synchronize()
+    t_eager, _ = time_launches(torch, stream, one_step, 5, 1)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        one_step()
+    pos.fill_(ctx_len)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(new):
+        g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    t_step = start.elapsed_time(end) / new / 1e3
+    assert int(pos[0].item()) == ctx_len + new
+    # one layer's attention alone at the mean context of the run
+    mid = ctx_len + new // 2
+    pos.fill_(mid)
+    kc, vc = caches[0]
+    fn = lambda: ctx.attention_decode(dec.q, dec.k, dec.v, H, Hkv, dk, pos, max_len, kc, vc, cfg.scale, dec.cos,
+                                      dec.sin, out=dec.a)
+    t_att, _ = time_launches(torch, stream, fn, max(10, steps // 2), 3)
+    att_bytes = dm.attention_bytes(B, [mid + 1] * B, Hkv, dk, H)
+    kv_bytes = L * att_bytes
+    res = {
+        "tokens_per_s": round(B / t_step, 1), "ms_per_step": round(t_step * 1e3, 4),
+        "eager_ms_per_step": round(t_eager * 1e3, 4), "batch": B, "context": ctx_len, "new_tokens": new,
+        "layers": L, "packed_weight_bytes": wbytes, "kv_bytes_per_step_at_mean_context": kv_bytes,
+        "step_GB/s_weights_plus_kv": round((wbytes + kv_bytes) / t_step / 1e9, 1),
+        "attention_one_layer": {"us": round(t_att * 1e6, 2), "bytes": att_bytes,
+                                "GB/s": round(att_bytes / t_att / 1e9, 1),
+                                "frac_hbm": round(att_bytes / t_att / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+    out["decode_c5"] = res
+    log(f"C5 decode: {res}")
+    del caches, dec
+    torch.cuda.empty_cache()
+
+
 def profiled_traffic():
     """Calibrated HBM bytes per headline launch from the committed PMC summary, or None."""
     import re
@@ -349,6 +443,7 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM lines")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config C5 decode line")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the M=16 / per-shape / single-launch GEMV and the quantizer lines")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -398,6 +493,8 @@ def main():
     if not args.no_gemm:
         gemm_lines(ctx, torch, stream, args.steps, extra)
         ffn_block_line(ctx, torch, stream, args.steps, extra)
+    if not args.no_decode:
+        decode_c5_line(ctx, torch, stream, args.steps, extra)
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline (about 12 s)")

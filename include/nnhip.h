@@ -312,7 +312,9 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
  * the reference stores each value twice, for j and j + dk/2). Upload them once per model. */
 nnhip_status nnhip_rope_table(size_t dk, size_t max_len, float* cos_out, float* sin_out);
 
-/* Context scratch nnhip_attention_decode uses for len_bound (0 when len_bound <= 128). */
+/* Context scratch nnhip_attention_decode uses for len_bound (0 when len_bound <= 128): the
+ * per-chunk partial results. It grows on demand, so a first call of a new size allocates and
+ * later ones do not (call once before capturing a graph). */
 size_t nnhip_attention_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound);
 
 /* Attention of B new tokens over their sequences' KV caches (grouped-query heads, RoPE):

@@ -177,6 +177,13 @@ hipError_t launch_act_to_container(hipStream_t st, const int8_t* xi, size_t K, s
 hipError_t launch_repack(hipStream_t st, const uint32_t* wq, size_t N, size_t K, uint32_t* rp);
 hipError_t launch_unrepack(hipStream_t st, const uint32_t* rp, size_t N, size_t K, uint32_t* wq);
 hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus);
+// Deep single-problem decode GEMV (all k stages in flight per wave, activations staged in LDS;
+// p.glu selects the gated epilogue into p.y = h). Applies when gemv_deep_ok: KT in {4, 10, 16, 27},
+// M * Kp <= kGemvDeepLds and at most kGemvDeepMaxTilesPerCu row tiles per CU.
+constexpr uint32_t kGemvDeepLds = 160 * 1024;
+constexpr int kGemvDeepMaxTilesPerCu = 4;
+bool gemv_deep_ok(const GemvProblem& p, int num_cus);  // also needs round_up(M * Kp, 1 KiB) <= kGemvDeepLds
+hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p);
 // Grouped GEMV over a precomputed per-wave schedule: wave w runs the items
 // d_wave_items[d_wave_start[w] .. d_wave_start[w+1]) (item = problem << 20 | row tile).
 // If n_xstage > 0, the listed activation blocks (lds_bytes in total) are staged in LDS at
@@ -204,7 +211,7 @@ size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t le
 hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
                               size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
                               const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
-                              float* out);
+                              float* out, int num_cus);
 hipError_t launch_add(hipStream_t st, const float* x, const float* y, size_t n, float* out);
 hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B,
                         float* out);

@@ -8,13 +8,13 @@
 // are bit-identical to the unfused reference sequence whichever kernel runs.
 //
 // Kernels by shape:
-//   k_token_wave   M <= 32: one wave per token, lane l owns parts l + 64q (q = 0..7).
-//   k_token_regs   M > 32, K up to 512 * 22: 4 tokens per block (the layout also supports 8),
+//   k_token_regs   any M, K up to 512 * 22: 4 tokens per block (the layout also supports 8),
 //                  512 threads. Each thread loads its rows (16 B = 4 tokens per row) once and
 //                  keeps them in registers through the three passes (sum of squares, absmax,
 //                  quantize), so X is read from HBM exactly once; parts are whole per thread.
 //                  Codes leave through a 4x4 byte transpose in lane quads as dword stores.
-//   k_token_lanes  fallback for larger K: 64 tokens per block, re-reads X per pass.
+//   k_token_wave   larger K, M <= 32: one wave per token, lane l owns parts l + 64q (q = 0..7).
+//   k_token_lanes  larger K, M > 32: 64 tokens per block, re-reads X per pass.
 #include "common.hpp"
 
 #include <cmath>
@@ -847,28 +847,30 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
     if (M == 0) return hipSuccess;
     const float inv_f = 1.0f / (float)K;
     const size_t Kp = round_up(K, kTileK);
-    if (M <= kSmallM)
-    {
-        const unsigned grid = (unsigned)ceil_div(M, kBlock / kWave);
-        hipLaunchKernelGGL(k_token_wave, dim3(grid), dim3(kBlock), 0, st, X, gamma, norm, eps, inv_f,
-                           K, M, Kp, mode, xi, s, rowsum, xq_ref, fout);
-        return hipGetLastError();
-    }
+    const int rounds = (int)ceil_div(K, (size_t)512);
     // the register kernel addresses X through one 31-bit buffer range, including the padding
-    // rows of its last round (at most 4096 rows past K)
-    if ((K + 4096) * M * 4 < 0x7FFFFFFFull)
+    // rows of its last round (at most 4096 rows past K). It serves every M up to 22 rounds
+    // (K <= 11264): at decode sizes (M = 16, K = 2560) it takes ~3 us where one wave per token
+    // with strided loads took ~49 us.
+    if (rounds <= 22 && (K + 4096) * M * 4 < 0x7FFFFFFFull)
     {
         // rows are read as float4 when every row start is 16-byte aligned
         const bool vec = M % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
                          (fout == nullptr || reinterpret_cast<uintptr_t>(fout) % 16 == 0);
         // 4 tokens per block: an 8-token layout (32-byte row segments) loads faster in isolation
         // but measured no faster end to end, and halves the block count
-        const int rounds = (int)ceil_div(K, (size_t)512);
         const int n_groups = (int)ceil_div(M, (size_t)4);
         TokArgs a{X, norm, eps, inv_f, (int)K, (int)M, (int)Kp, mode, xi, s, rowsum, xq_ref, fout};
         const bool launched = launch_regs_pick<4, 1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(
             rounds, vec, st, n_groups, a, gamma);
         if (launched) return hipGetLastError();
+    }
+    if (M <= kSmallM)
+    {
+        const unsigned grid = (unsigned)ceil_div(M, kBlock / kWave);
+        hipLaunchKernelGGL(k_token_wave, dim3(grid), dim3(kBlock), 0, st, X, gamma, norm, eps, inv_f,
+                           K, M, Kp, mode, xi, s, rowsum, xq_ref, fout);
+        return hipGetLastError();
     }
     const unsigned grid = (unsigned)ceil_div(M, kWave);
     hipLaunchKernelGGL(k_token_lanes, dim3(grid), dim3(kTW * kWave), 0, st, X, gamma, norm, eps,

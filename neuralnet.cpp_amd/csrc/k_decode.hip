@@ -20,9 +20,13 @@
 //
 // Work split (flash-decoding): work-group (chunk c, KV head g, sequence b) covers cache
 // positions [128c, 128c + 128) for the R = H/Hkv query heads that share KV head g, so every
-// key/value row is read from HBM once for all of them. The scores of a chunk stay in LDS; the
-// chunk writes (acc[R][dk], max, sum) and a second kernel merges the chunks of each head. With
-// a single chunk (every sequence shorter than 129) the first kernel writes the output itself.
+// key/value row is read from HBM once for all of them. The grid is persistent (as many
+// work-groups as are resident at once, looping over the items). The scores of a chunk stay in
+// LDS; the chunk writes (acc[R][dk], max, sum) to scratch and a second kernel merges the chunks
+// of each (sequence, KV head). (Merging in the last chunk to finish, found with a counter, needs
+// an agent-scope fence in every work-group; with one L2 per XCD that fence cost far more than the
+// second launch.) With a single chunk (every sequence shorter than 129) the work-group writes the
+// output itself.
 // The work-group whose chunk holds position pos[b] writes the rotated key and the value into the
 // cache and uses them from LDS; no other work-group reads that row in the same launch.
 #include "common.hpp"
@@ -88,281 +92,322 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
     __shared__ float ml[2][kAttnMaxR];
     __shared__ float4 red[4][kAttnMaxR * Q4];
 
-    const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int R = a.R;
-    const int p = a.pos[b];
-    const int t0 = c * kAttnT;
-    if (p < 0 || p >= a.len_bound)
+    const int w = tid >> 6, lane = tid & 63;
+    const int total = a.nchunk * a.Hkv * a.B;
+    // persistent: work-group items (chunk fastest, then KV head, then sequence)
+    for (int item = blockIdx.x; item < total; item += gridDim.x)
     {
-        // out-of-range position: NaN output for this sequence's heads, cache untouched
-        if (kFinal && c == 0)
-            for (int e = tid; e < R * DK; e += kAttnThreads)
-                a.out[(size_t)((g * R + e / DK) * DK + e % DK) * a.B + b] = __builtin_nanf("");
-        return;
-    }
-    const int len = p + 1;
-    if (t0 >= len) return;
-    const int n = min(kAttnT, len - t0);
-    const bool has_new = p < t0 + kAttnT;
-    const size_t rstride = (size_t)a.Hkv * DK;
-    const size_t seq_off = (size_t)b * a.max_len * rstride + (size_t)g * DK;
-
-    // ---- stage the rotated queries (R heads) and, in the chunk holding p, the new key/value
-    float* qf = reinterpret_cast<float*>(q_s);
-    for (int e = tid; e < R * HALF; e += kAttnThreads)
-    {
-        const int r = e / HALF, j = e - r * HALF;
-        const int h = g * R + r;
-        const float x0 = a.q[(size_t)(h * DK + j) * a.B + b];
-        const float x1 = a.q[(size_t)(h * DK + j + HALF) * a.B + b];
-        float y0 = x0, y1 = x1;
-        if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
-        qf[r * DK + j] = y0;
-        qf[r * DK + j + HALF] = y1;
-    }
-    if (has_new)
-    {
-        float* kf = reinterpret_cast<float*>(kn_s);
-        float* vf = reinterpret_cast<float*>(vn_s);
-        for (int j = tid; j < HALF; j += kAttnThreads)
+        const int c = item % a.nchunk;
+        const int g = (item / a.nchunk) % a.Hkv;
+        const int b = item / (a.nchunk * a.Hkv);
+        const int p = a.pos[b];
+        const int t0 = c * kAttnT;
+        if (p < 0 || p >= a.len_bound)
         {
-            const float x0 = a.k[(size_t)(g * DK + j) * a.B + b];
-            const float x1 = a.k[(size_t)(g * DK + j + HALF) * a.B + b];
+            // out-of-range position: NaN output for this sequence's heads, cache untouched
+            if (c == 0)
+                for (int e = tid; e < R * DK; e += kAttnThreads)
+                    a.out[(size_t)((g * R + e / DK) * DK + e % DK) * a.B + b] = __builtin_nanf("");
+            continue;
+        }
+        const int len = p + 1;
+        if (t0 >= len) continue;
+        const int n = min(kAttnT, len - t0);
+        const bool has_new = p < t0 + kAttnT;
+        const size_t rstride = (size_t)a.Hkv * DK;
+        const size_t seq_off = (size_t)b * a.max_len * rstride + (size_t)g * DK;
+
+        // ---- stage the rotated queries (R heads) and, in the chunk holding p, the new key/value
+        float* qf = reinterpret_cast<float*>(q_s);
+        for (int e = tid; e < R * HALF; e += kAttnThreads)
+        {
+            const int r = e / HALF, j = e - r * HALF;
+            const int h = g * R + r;
+            const float x0 = a.q[(size_t)(h * DK + j) * a.B + b];
+            const float x1 = a.q[(size_t)(h * DK + j + HALF) * a.B + b];
             float y0 = x0, y1 = x1;
             if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
-            kf[j] = y0;
-            kf[j + HALF] = y1;
+            qf[r * DK + j] = y0;
+            qf[r * DK + j + HALF] = y1;
         }
-        for (int i = tid; i < DK; i += kAttnThreads) vf[i] = a.v[(size_t)(g * DK + i) * a.B + b];
-    }
-    __syncthreads();
-    if (has_new)
-    {
-        float4* krow = reinterpret_cast<float4*>(a.kc + seq_off + (size_t)p * rstride);
-        float4* vrow = reinterpret_cast<float4*>(a.vc + seq_off + (size_t)p * rstride);
-        for (int i = tid; i < Q4; i += kAttnThreads)
+        if (has_new)
         {
-            krow[i] = kn_s[i];
-            vrow[i] = vn_s[i];
-        }
-    }
-
-    // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row
-    const int pg = tid >> 3, j8 = tid & 7;
-    const float* kbase = a.kc + seq_off;
-#pragma unroll
-    for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
-    {
-        float4 kv[PB][F4];
-#pragma unroll
-        for (int u = 0; u < PB; ++u)
-        {
-            const int tl = (pass0 + u) * 32 + pg;
-            const int t = t0 + tl;
-#pragma unroll
-            for (int i = 0; i < F4; ++i)
+            float* kf = reinterpret_cast<float*>(kn_s);
+            float* vf = reinterpret_cast<float*>(vn_s);
+            for (int j = tid; j < HALF; j += kAttnThreads)
             {
-                if (tl < n && t < p)
-                    kv[u][i] = *reinterpret_cast<const float4*>(kbase + (size_t)t * rstride + 4 * (j8 + 8 * i));
-                else if (tl < n)
-                    kv[u][i] = kn_s[j8 + 8 * i];
-                else
-                    kv[u][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                const float x0 = a.k[(size_t)(g * DK + j) * a.B + b];
+                const float x1 = a.k[(size_t)(g * DK + j + HALF) * a.B + b];
+                float y0 = x0, y1 = x1;
+                if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
+                kf[j] = y0;
+                kf[j + HALF] = y1;
+            }
+            for (int i = tid; i < DK; i += kAttnThreads) vf[i] = a.v[(size_t)(g * DK + i) * a.B + b];
+        }
+        __syncthreads();
+        if (has_new)
+        {
+            float4* krow = reinterpret_cast<float4*>(a.kc + seq_off + (size_t)p * rstride);
+            float4* vrow = reinterpret_cast<float4*>(a.vc + seq_off + (size_t)p * rstride);
+            for (int i = tid; i < Q4; i += kAttnThreads)
+            {
+                krow[i] = kn_s[i];
+                vrow[i] = vn_s[i];
             }
         }
+
+        // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row
+        const int pg = tid >> 3, j8 = tid & 7;
+        const float* kbase = a.kc + seq_off;
 #pragma unroll
-        for (int u = 0; u < PB; ++u)
+        for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
         {
-            const int tl = (pass0 + u) * 32 + pg;
-            float d[kAttnMaxR];
+            float4 kv[PB][F4];
 #pragma unroll
-            for (int r = 0; r < kAttnMaxR; ++r)
+            for (int u = 0; u < PB; ++u)
             {
-                d[r] = 0.f;
-                if (r < R)
-                {
+                const int tl = (pass0 + u) * 32 + pg;
+                const int t = t0 + tl;
 #pragma unroll
-                    for (int i = 0; i < F4; ++i)
-                    {
-                        const float4 qq = q_s[r * Q4 + j8 + 8 * i];
-                        d[r] = __builtin_fmaf(kv[u][i].x, qq.x, d[r]);
-                        d[r] = __builtin_fmaf(kv[u][i].y, qq.y, d[r]);
-                        d[r] = __builtin_fmaf(kv[u][i].z, qq.z, d[r]);
-                        d[r] = __builtin_fmaf(kv[u][i].w, qq.w, d[r]);
-                    }
-                    d[r] = sum8(d[r]);
+                for (int i = 0; i < F4; ++i)
+                {
+                    if (tl < n && t < p)
+                        kv[u][i] = *reinterpret_cast<const float4*>(kbase + (size_t)t * rstride + 4 * (j8 + 8 * i));
+                    else if (tl < n)
+                        kv[u][i] = kn_s[j8 + 8 * i];
+                    else
+                        kv[u][i] = make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
-            if (tl < n)
+#pragma unroll
+            for (int u = 0; u < PB; ++u)
             {
+                const int tl = (pass0 + u) * 32 + pg;
+                float d[kAttnMaxR];
 #pragma unroll
                 for (int r = 0; r < kAttnMaxR; ++r)
-                    if (r < R && j8 == r) S[r][tl] = __fmul_rn(d[r], a.scale);
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- chunk softmax statistics: one wave per head
-    const int w = tid >> 6, lane = tid & 63;
-    for (int r = w; r < R; r += 4)
-    {
-        float m = -__builtin_inff();
-        for (int i = lane; i < n; i += kWave) m = fmaxf(m, S[r][i]);
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-        float l = 0.f;
-        for (int i = lane; i < n; i += kWave)
-        {
-            const float e = expf(S[r][i] - m);
-            S[r][i] = e;
-            l += e;
-        }
-        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, kWave);
-        if (lane == 0)
-        {
-            ml[0][r] = m;
-            ml[1][r] = l;
-        }
-    }
-    __syncthreads();
-
-    // ---- values: VL lanes per row (one float4 each), NG rows per step, 8 steps of loads in flight
-    const int vg = tid / VL, vi = tid % VL;
-    const float* vbase = a.vc + seq_off;
-    float4 acc[kAttnMaxR];
-#pragma unroll
-    for (int r = 0; r < kAttnMaxR; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int base = vg; base < n; base += 8 * NG)
-    {
-        float4 vv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-        {
-            const int tl = base + u * NG;
-            const int t = t0 + tl;
-            if (tl < n && t < p)
-                vv[u] = *reinterpret_cast<const float4*>(vbase + (size_t)t * rstride + 4 * vi);
-            else if (tl < n)
-                vv[u] = vn_s[vi];
-            else
-                vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-        {
-            const int tl = base + u * NG;
-            if (tl < n)
-            {
-#pragma unroll
-                for (int r = 0; r < kAttnMaxR; ++r)
+                {
+                    d[r] = 0.f;
                     if (r < R)
                     {
-                        const float pr = S[r][tl];
-                        acc[r].x = __builtin_fmaf(pr, vv[u].x, acc[r].x);
-                        acc[r].y = __builtin_fmaf(pr, vv[u].y, acc[r].y);
-                        acc[r].z = __builtin_fmaf(pr, vv[u].z, acc[r].z);
-                        acc[r].w = __builtin_fmaf(pr, vv[u].w, acc[r].w);
+#pragma unroll
+                        for (int i = 0; i < F4; ++i)
+                        {
+                            const float4 qq = q_s[r * Q4 + j8 + 8 * i];
+                            d[r] = __builtin_fmaf(kv[u][i].x, qq.x, d[r]);
+                            d[r] = __builtin_fmaf(kv[u][i].y, qq.y, d[r]);
+                            d[r] = __builtin_fmaf(kv[u][i].z, qq.z, d[r]);
+                            d[r] = __builtin_fmaf(kv[u][i].w, qq.w, d[r]);
+                        }
+                        d[r] = sum8(d[r]);
                     }
+                }
+                if (tl < n)
+                {
+#pragma unroll
+                    for (int r = 0; r < kAttnMaxR; ++r)
+                        if (r < R && j8 == r) S[r][tl] = __fmul_rn(d[r], a.scale);
+                }
             }
         }
-    }
-    // rows of one wave -> lanes [0, VL), then the 4 waves through LDS in a fixed order
-#pragma unroll
-    for (int r = 0; r < kAttnMaxR; ++r)
-        if (r < R)
-            for (int off = VL; off < kWave; off <<= 1)
+        __syncthreads();
+
+        // ---- chunk softmax statistics: one wave per head
+        for (int r = w; r < R; r += 4)
+        {
+            float m = -__builtin_inff();
+            for (int i = lane; i < n; i += kWave) m = fmaxf(m, S[r][i]);
+            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+            float l = 0.f;
+            for (int i = lane; i < n; i += kWave)
             {
-                acc[r].x += __shfl_xor(acc[r].x, off, kWave);
-                acc[r].y += __shfl_xor(acc[r].y, off, kWave);
-                acc[r].z += __shfl_xor(acc[r].z, off, kWave);
-                acc[r].w += __shfl_xor(acc[r].w, off, kWave);
+                const float e = expf(S[r][i] - m);
+                S[r][i] = e;
+                l += e;
             }
-    if (lane < VL)
-    {
+            for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, kWave);
+            if (lane == 0)
+            {
+                ml[0][r] = m;
+                ml[1][r] = l;
+            }
+        }
+        __syncthreads();
+
+        // ---- values: VL lanes per row (one float4 each), NG rows per step, 8 steps of loads in flight
+        const int vg = tid / VL, vi = tid % VL;
+        const float* vbase = a.vc + seq_off;
+        float4 acc[kAttnMaxR];
+#pragma unroll
+        for (int r = 0; r < kAttnMaxR; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int base = vg; base < n; base += 8 * NG)
+        {
+            float4 vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+            {
+                const int tl = base + u * NG;
+                const int t = t0 + tl;
+                if (tl < n && t < p)
+                    vv[u] = *reinterpret_cast<const float4*>(vbase + (size_t)t * rstride + 4 * vi);
+                else if (tl < n)
+                    vv[u] = vn_s[vi];
+                else
+                    vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+            {
+                const int tl = base + u * NG;
+                if (tl < n)
+                {
+#pragma unroll
+                    for (int r = 0; r < kAttnMaxR; ++r)
+                        if (r < R)
+                        {
+                            const float pr = S[r][tl];
+                            acc[r].x = __builtin_fmaf(pr, vv[u].x, acc[r].x);
+                            acc[r].y = __builtin_fmaf(pr, vv[u].y, acc[r].y);
+                            acc[r].z = __builtin_fmaf(pr, vv[u].z, acc[r].z);
+                            acc[r].w = __builtin_fmaf(pr, vv[u].w, acc[r].w);
+                        }
+                }
+            }
+        }
+        // rows of one wave -> lanes [0, VL), then the 4 waves through LDS in a fixed order
 #pragma unroll
         for (int r = 0; r < kAttnMaxR; ++r)
-            if (r < R) red[w][r * Q4 + vi] = acc[r];
-    }
-    __syncthreads();
-    float* rec = a.part + ((size_t)(b * a.Hkv + g) * a.nchunk + c) * (size_t)(R * DK + kRecPad);
-    for (int e = tid; e < R * Q4; e += kAttnThreads)
-    {
-        float4 s4 = red[0][e];
+            if (r < R)
+                for (int off = VL; off < kWave; off <<= 1)
+                {
+                    acc[r].x += __shfl_xor(acc[r].x, off, kWave);
+                    acc[r].y += __shfl_xor(acc[r].y, off, kWave);
+                    acc[r].z += __shfl_xor(acc[r].z, off, kWave);
+                    acc[r].w += __shfl_xor(acc[r].w, off, kWave);
+                }
+        if (lane < VL)
+        {
 #pragma unroll
-        for (int ww = 1; ww < 4; ++ww)
-        {
-            s4.x += red[ww][e].x;
-            s4.y += red[ww][e].y;
-            s4.z += red[ww][e].z;
-            s4.w += red[ww][e].w;
+            for (int r = 0; r < kAttnMaxR; ++r)
+                if (r < R) red[w][r * Q4 + vi] = acc[r];
         }
-        if constexpr (kFinal)
+        __syncthreads();
+        const size_t stride = (size_t)(R * DK + kRecPad);
+        float* rec0 = a.part + (size_t)(b * a.Hkv + g) * a.nchunk * stride;
+        float* rec = rec0 + (size_t)c * stride;
+        for (int e = tid; e < R * Q4; e += kAttnThreads)
         {
-            const int r = e / Q4, i = 4 * (e - r * Q4);
-            const float l = ml[1][r];
-            float* o = a.out + (size_t)((g * R + r) * DK + i) * a.B + b;
-            o[0] = s4.x / l;
-            o[a.B] = s4.y / l;
-            o[2 * a.B] = s4.z / l;
-            o[3 * a.B] = s4.w / l;
+            float4 s4 = red[0][e];
+#pragma unroll
+            for (int ww = 1; ww < 4; ++ww)
+            {
+                s4.x += red[ww][e].x;
+                s4.y += red[ww][e].y;
+                s4.z += red[ww][e].z;
+                s4.w += red[ww][e].w;
+            }
+            if constexpr (kFinal)
+            {
+                const int r = e / Q4, i = 4 * (e - r * Q4);
+                const float l = ml[1][r];
+                float* o = a.out + (size_t)((g * R + r) * DK + i) * a.B + b;
+                o[0] = s4.x / l;
+                o[a.B] = s4.y / l;
+                o[2 * a.B] = s4.z / l;
+                o[3 * a.B] = s4.w / l;
+            }
+            else
+            {
+                reinterpret_cast<float4*>(rec)[e] = s4;
+            }
         }
-        else
+        if constexpr (!kFinal)
         {
-            reinterpret_cast<float4*>(rec)[e] = s4;
+            if (tid < R)
+            {
+                rec[R * DK + tid] = ml[0][tid];
+                rec[R * DK + 8 + tid] = ml[1][tid];
+            }
         }
-    }
-    if constexpr (!kFinal)
-    {
-        if (tid < R)
-        {
-            rec[R * DK + tid] = ml[0][tid];
-            rec[R * DK + 8 + tid] = ml[1][tid];
-        }
+        __syncthreads();  // LDS is reused by the next item
     }
 }
 
-// Merge the chunks of one (sequence, head): out = sum_c e_c acc_c / sum_c e_c l_c,
-// e_c = exp(max_c - max), chunks in ascending order.
+// Merge of the chunk records (acc[R][DK], then max[8], sum[8]) of one (sequence, head):
+// out = sum_c e_c acc_c / sum_c e_c l_c, e_c = exp(max_c - max), in ascending batches of 16
+// chunks whose loads are all issued before use (an online maximum rescales earlier batches).
+constexpr int kMergeBatch = 16;
+
 template <int DK>
 __global__ __launch_bounds__(DK) void k_attn_merge(AttnArgs a)
 {
     const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
     const int g = h / a.R, r = h % a.R;
     const int i = threadIdx.x;
-    float* o = a.out + (size_t)(h * DK + i) * a.B + b;
     const int p = a.pos[b];
-    if (p < 0 || p >= a.len_bound)
-    {
-        *o = __builtin_nanf("");
-        return;
-    }
+    if (p < 0 || p >= a.len_bound) return;  // the chunk kernel wrote NaN
     const int nch = (p + kAttnT) / kAttnT;
     const size_t stride = (size_t)(a.R * DK + kRecPad);
     const float* rec0 = a.part + (size_t)(b * a.Hkv + g) * a.nchunk * stride;
-    float M = -__builtin_inff();
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, rec0[c * stride + a.R * DK + r]);
-    float num = 0.f, den = 0.f;
-    for (int c = 0; c < nch; ++c)
+    float M = -__builtin_inff(), num = 0.f, den = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += kMergeBatch)
     {
-        const float* rec = rec0 + c * stride;
-        const float e = expf(rec[a.R * DK + r] - M);
-        num = __builtin_fmaf(e, rec[r * DK + i], num);
-        den = __builtin_fmaf(e, rec[a.R * DK + 8 + r], den);
+        float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j)
+        {
+            const bool ok = c0 + j < nch;
+            const float* rc = rec0 + (size_t)(ok ? c0 + j : c0) * stride;
+            mv[j] = ok ? rc[a.R * DK + r] : -__builtin_inff();
+            lv[j] = ok ? rc[a.R * DK + 8 + r] : 0.f;
+            av[j] = ok ? rc[r * DK + i] : 0.f;
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, mv[j]);
+        const float resc = expf(M - Mb);  // 0 on the first batch (M = -inf)
+        num = c0 == 0 ? 0.f : num * resc;
+        den = c0 == 0 ? 0.f : den * resc;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j)
+        {
+            const float e = c0 + j < nch ? expf(mv[j] - Mb) : 0.f;
+            num = __builtin_fmaf(e, av[j], num);
+            den = __builtin_fmaf(e, lv[j], den);
+        }
+        M = Mb;
     }
-    *o = num / den;
+    a.out[(size_t)(h * DK + i) * a.B + b] = num / den;
+}
+
+// Persistent grid: as many work-groups as fit the device at once (at most one per item).
+template <int DK, bool kFinal>
+hipError_t launch_attn_variant(hipStream_t st, const AttnArgs& a, int num_cus)
+{
+    static int per_cu = 0;
+    if (per_cu == 0)
+    {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_chunk<DK, kFinal>, kAttnThreads, 0) != hipSuccess ||
+            n < 1)
+            n = 1;
+        per_cu = n;
+    }
+    const long total = (long)a.nchunk * a.Hkv * a.B;
+    const long cap = (long)per_cu * (num_cus > 0 ? num_cus : 256);
+    const unsigned grid = (unsigned)(total < cap ? total : cap);
+    k_attn_chunk<DK, kFinal><<<dim3(grid), kAttnThreads, 0, st>>>(a);
+    return hipGetLastError();
 }
 
 template <int DK>
-hipError_t launch_attn_dk(hipStream_t st, AttnArgs a)
+hipError_t launch_attn_dk(hipStream_t st, const AttnArgs& a, int num_cus)
 {
-    if (a.nchunk == 1)
-    {
-        k_attn_chunk<DK, true><<<dim3(1, a.Hkv, a.B), kAttnThreads, 0, st>>>(a);
-        return hipGetLastError();
-    }
-    k_attn_chunk<DK, false><<<dim3(a.nchunk, a.Hkv, a.B), kAttnThreads, 0, st>>>(a);
-    hipError_t e = hipGetLastError();
+    if (a.nchunk == 1) return launch_attn_variant<DK, true>(st, a, num_cus);
+    const hipError_t e = launch_attn_variant<DK, false>(st, a, num_cus);
     if (e != hipSuccess) return e;
     k_attn_merge<DK><<<dim3(a.B * a.H), DK, 0, st>>>(a);
     return hipGetLastError();
@@ -444,23 +489,22 @@ size_t attn_chunks(size_t len_bound) { return ceil_div(len_bound, kAttnT); }
 
 size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound)
 {
-    const size_t nchunk = attn_chunks(len_bound);
-    if (nchunk <= 1) return 0;
-    return B * Hkv * nchunk * ((H / Hkv) * dk + kRecPad) * sizeof(float);
+    if (attn_chunks(len_bound) <= 1) return 0;
+    return B * Hkv * attn_chunks(len_bound) * ((H / Hkv) * dk + kRecPad) * sizeof(float);
 }
 
 hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
                               size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
                               const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
-                              float* out)
+                              float* out, int num_cus)
 {
     AttnArgs a{q, k, v, pos, cosT, sinT, kc, vc, part, out, (int)B, (int)H, (int)Hkv, (int)(H / Hkv),
                (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale};
     switch (dk)
     {
-    case 64: return launch_attn_dk<64>(st, a);
-    case 128: return launch_attn_dk<128>(st, a);
-    case 256: return launch_attn_dk<256>(st, a);
+    case 64: return launch_attn_dk<64>(st, a, num_cus);
+    case 128: return launch_attn_dk<128>(st, a, num_cus);
+    case 256: return launch_attn_dk<256>(st, a, num_cus);
     default: return hipErrorInvalidValue;
     }
 }

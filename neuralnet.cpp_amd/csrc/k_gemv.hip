@@ -290,6 +290,126 @@ __global__ __launch_bounds__(kBlock) void k_gemv_grouped(const GemvProblem* __re
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Deep single-problem GEMV for grids smaller than the device (a decode step's BitLinears:
+// 160 - 864 row tiles). One 16-row tile per wave; the wave issues the loads of ALL its KT
+// weight stages first (one memory latency instead of KT / depth of them), then the block stages
+// the whole problem's activations (M x Kp bytes, up to 160 KB) into LDS while they land.
+// glu != 0: the rows are the interleaved gate/up rows of a gated FFN (16-row tile = gate rows
+// 8t..8t+7, then up rows 8t..8t+7); lanes of the gate half take their up values from the lane
+// 32 apart and store act(gate, up) as features 8t..8t+7 of h (glu_F, M) instead of Y.
+template <int KT>
+__global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvProblem p, int n_tiles, uint32_t xbytes)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int rt = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6));
+    const int g = lane >> 4, t = lane & 15;
+    const uint32_t Kp = (uint32_t)KT * kTileK;
+    const bool live = rt < n_tiles;
+
+    // 1. all weight stages of the tile (a tile past the matrix reads zero words)
+    const __amdgpu_buffer_rsrc_t rw = rsrc(p.rp + (size_t)(live ? rt : 0) * KT * 64, live ? (uint32_t)KT * 1024u : 0u);
+    v4i w[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) w[kt] = ld16<kNT>(rw, (uint32_t)lane * 16u, (uint32_t)kt * 1024u);
+
+    // 2. epilogue operands (rows past N and tokens past M read 0)
+    const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
+    const uint32_t tok = t < p.M ? (uint32_t)t : 0x40000000u;
+    const int rs2 = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.rowsum, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
+    const float sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.s, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
+    float tv[4], bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const uint32_t n = (uint32_t)(rt * 16 + 4 * g + i);
+        tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, n * 4u, 0, 0));
+        bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, n * 4u, 0, 0));
+    }
+
+    // 3. activations into LDS by buffer->LDS DMA (1 KiB per instruction, no registers), issued
+    //    behind the weight loads; __syncthreads waits for both and joins the waves
+    {
+        typedef __attribute__((address_space(3))) void lds_void;
+        const __amdgpu_buffer_rsrc_t rx = rsrc(p.xi, xbytes);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int nq = (int)((xbytes + 1023u) / 1024u);
+        for (int q = wave; q < nq; q += kBlock / kWave)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + q * 1024), 16, (uint32_t)lane * 16u,
+                                                     (uint32_t)q * 1024u, 0, 0);
+        __syncthreads();
+    }
+
+    // 4. MFMAs over the k tiles; tokens t >= M read token 0's row (their columns are never stored)
+    Acc acc[1];
+    acc[0].a0 = acc[0].a1 = acc[0].a2 = acc[0].a3 = v4i{0, 0, 0, 0};
+    const uint8_t* xl = lds + (t < p.M ? t : 0) * Kp + 16 * g;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+    {
+        v4i x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(xl + kt * 256 + 64 * j);
+        const v4i w1[1] = {w[kt]};
+        compute_stage<1>(w1, x, acc);
+    }
+
+    // 5. epilogue, the reference order: y = (tau * s) * float(acc) [+ bias]
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int a = acc[0].a0[i] + acc[0].a3[i] + (acc[0].a1[i] >> 2) + (acc[0].a2[i] >> 4) - rs2;
+        y[i] = (tv[i] * sv) * (float)a;
+        if (p.bias) y[i] = y[i] + bv[i];
+    }
+    if (p.glu == 0)
+    {
+        const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int n = rt * 16 + 4 * g + i;
+            const uint32_t off = (live && n < p.N && t < p.M) ? ((uint32_t)n * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[i]), ry, off, 0, 0);
+        }
+    }
+    else
+    {
+        const __amdgpu_buffer_rsrc_t rh = rsrc(p.y, (uint32_t)p.glu_F * (uint32_t)p.M * 4u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const float up = __shfl_xor(y[i], 32, kWave);  // tile row 8 + 4g + i
+            const int f = rt * 8 + 4 * g + i;
+            const bool st = live && g < 2 && f < p.glu_F && t < p.M;
+            const float hv = glu_one(y[i], up, p.glu - 1);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hv), rh,
+                                                  st ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u, 0, 0);
+        }
+    }
+}
+
+template <int KT>
+hipError_t launch_deep_kt(hipStream_t st, const GemvProblem& p, int n_tiles, uint32_t xbytes)
+{
+    static bool attr = false;
+    if (!attr)
+    {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_deep<KT>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvDeepLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const unsigned blocks = (unsigned)ceil_div((size_t)n_tiles, (size_t)(kBlock / kWave));
+    // the last DMA instruction fills a whole KiB (lanes past xbytes read zeros)
+    const uint32_t lds_bytes = (uint32_t)round_up(xbytes, 1024);
+    hipLaunchKernelGGL(k_gemv_deep<KT>, dim3(blocks), dim3(kBlock), lds_bytes, st, p, n_tiles, xbytes);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds)
@@ -303,9 +423,32 @@ size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds)
     return blocks * (kBlock / kWave);
 }
 
+bool gemv_deep_ok(const GemvProblem& p, int num_cus)
+{
+    const size_t tiles = ceil_div((size_t)p.N, 16);
+    const size_t xbytes = (size_t)p.M * (size_t)p.KT * kTileK;
+    const bool kt_ok = p.KT == 4 || p.KT == 10 || p.KT == 16 || p.KT == 27;
+    return kt_ok && round_up(xbytes, 1024) <= kGemvDeepLds && tiles <= (size_t)kGemvDeepMaxTilesPerCu * (size_t)(num_cus > 0 ? num_cus : 256);
+}
+
+hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p)
+{
+    const int n_tiles = (int)ceil_div((size_t)p.N, 16);
+    const uint32_t xbytes = (uint32_t)p.M * (uint32_t)p.KT * kTileK;
+    switch (p.KT)
+    {
+    case 4: return launch_deep_kt<4>(st, p, n_tiles, xbytes);
+    case 10: return launch_deep_kt<10>(st, p, n_tiles, xbytes);
+    case 16: return launch_deep_kt<16>(st, p, n_tiles, xbytes);
+    case 27: return launch_deep_kt<27>(st, p, n_tiles, xbytes);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus)
 {
     if (p.N == 0 || p.M == 0) return hipSuccess;
+    if (p.glu == 0 && gemv_deep_ok(p, num_cus)) return launch_gemv_deep(st, p);
     const uint32_t xbytes = (uint32_t)p.M * (uint32_t)p.KT * kTileK;
     const bool lds = xbytes <= kGemvLdsBudget;
     const GemvVariant v = gemv_variant(lds);

@@ -836,6 +836,27 @@ nnhip_status run_matmul_glu(nnhip_ctx* ctx, const char* fn, const void* rp, cons
     const size_t N = nnhip_glu_rows(F);
     if (M <= (size_t)kGemvMaxM)
     {
+        GemvProblem p{};
+        p.rp = static_cast<const u32x4*>(rp);
+        p.tau = tau;
+        p.xi = xi;
+        p.s = s;
+        p.rowsum = rowsum;
+        p.bias = bias;
+        p.y = h;
+        p.N = (int32_t)N;
+        p.K = (int32_t)K;
+        p.M = (int32_t)M;
+        p.KT = (int32_t)ceil_div(K, kTileK);
+        p.xlds = -1;
+        p.glu = act + 1;
+        p.glu_F = (int32_t)F;
+        if (gemv_deep_ok(p, ctx->num_cus))
+        {
+            // the gated activation in the deep GEMV's epilogue: no y1 round trip
+            NNHIP_LAUNCH(fn, launch_gemv_deep(ctx->stream, p));
+            return NNHIP_OK;
+        }
         const nnhip_status st = run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, y1);
         if (st != NNHIP_OK) return st;
         NNHIP_LAUNCH(fn, launch_glu(ctx->stream, y1, F, M, act, true, h));
@@ -1026,13 +1047,14 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
     NNHIP_REQUIRE(mul_ok(B, max_len) && mul_ok(B * max_len, Hkv * dk), fn, "cache size overflow");
     NNHIP_REQUIRE(aligned16(k_cache) && aligned16(v_cache), fn, "caches must be 16-byte aligned");
     const size_t wsb = attn_workspace_bytes(B, H, Hkv, dk, len_bound);
-    if (wsb > 0)
+    if (wsb > ctx->attn_ws_bytes)
     {
         const nnhip_status st = ensure_buf(ctx, ctx->attn_ws, ctx->attn_ws_bytes, wsb, fn, "attention workspace");
         if (st != NNHIP_OK) return st;
     }
     NNHIP_LAUNCH(fn, launch_attn_decode(ctx->stream, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin,
-                                        k_cache, v_cache, max_len, scale, static_cast<float*>(ctx->attn_ws), out));
+                                        k_cache, v_cache, max_len, scale,
+                                        wsb ? static_cast<float*>(ctx->attn_ws) : nullptr, out, ctx->num_cus));
     return NNHIP_OK;
 }
 

@@ -1,0 +1,158 @@
+"""Batched decode step of a BitNet-b1.58 GPT model over libnn-hip.so's C ABI.
+
+The Python mirror of nn::GPTModel::forward_step (include/neuralnet.cpp/decoder.hpp), used by
+the tests and bench.py: the reference's GPTModel::forward_step (compute_layer_gpt.hpp:693-724)
+for B sequences, one token each, each at its own position. Every buffer is allocated once at
+construction, so one step makes no allocation and can be captured in a graph and replayed.
+
+Per block (GPTBlock::forward_step, compute_layer_gpt.hpp:201-219, all BitLinears in the int8
+branch):
+    xi = int8(RMSNorm1(x))                        nnhip_rmsnorm_quant_i8
+    q, k, v = BitLinear(xi)                       nnhip_ternary_matmul x 3 (decode GEMV)
+    a = attention(q, k, v, caches, pos)           nnhip_attention_decode (RoPE, GQA, append)
+    xi = int8([SubLN] a)                          nnhip_rmsnorm_quant_i8 / nnhip_act_quant_i8
+    r = x + BitLinear_o(xi)                       nnhip_ternary_matmul, nnhip_add
+    x = r + FFN(RMSNorm2(r))                      nnhip_ffn_glu_i8 (norm fused), nnhip_add
+then logits = BitLinear_head(int8(RMSNorm_f(x))) and the greedy ids (nnhip_argmax_cols).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+
+@dataclass
+class Linear:
+    """One BitLinear on the device in the fast layout: repacked words, tau, bias (or None)."""
+    rp: object
+    tau: object
+    bias: Optional[object]
+    N: int
+    K: int
+
+
+@dataclass
+class Block:
+    g1: object
+    q: Linear
+    k: Linear
+    v: Linear
+    o: Linear
+    g2: object
+    fc1: Linear            # interleaved gate/up rows (nnhip_glu_interleave), N = glu_rows(F)
+    fc2: Linear
+    g_attn_sub: Optional[object] = None
+    g_ffn_sub: Optional[object] = None
+
+
+@dataclass
+class Config:
+    d: int
+    H: int
+    Hkv: int
+    F: int
+    vocab: int
+    max_len: int
+    act: int = 0            # ACT_SWIGLU / ACT_RELU2GLU
+    eps: float = 1e-5
+    rope: bool = True
+
+    @property
+    def dk(self) -> int:
+        return self.d // self.H
+
+    @property
+    def scale(self) -> float:
+        import numpy as np
+        return float(np.float32(1.0) / np.float32(math.sqrt(self.dk)))
+
+
+class Decoder:
+    """Device state of one model for B sequences: weights, KV caches, RoPE tables and the
+    step's scratch buffers."""
+
+    def __init__(self, ctx, cfg: Config, blocks: List[Block], emb, g_final, head: Linear, B: int, caches=None):
+        import torch
+
+        self.ctx, self.cfg, self.blocks, self.emb, self.g_final, self.head, self.B = \
+            ctx, cfg, blocks, emb, g_final, head, B
+        dev = f"cuda:{ctx.device}"
+        f32 = dict(dtype=torch.float32, device=dev)
+        d, H, Hkv, dk = cfg.d, cfg.H, cfg.Hkv, cfg.dk
+        if caches is None:
+            caches = [(torch.zeros((B, cfg.max_len, Hkv * dk), **f32), torch.zeros((B, cfg.max_len, Hkv * dk), **f32))
+                      for _ in blocks]
+        self.caches = caches
+        if cfg.rope:
+            c, s = _pkg().rope_table(dk, cfg.max_len)
+            self.cos, self.sin = torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev)
+        else:
+            self.cos = self.sin = None
+        kpd = _pkg().kp
+        self.x = torch.empty((d, B), **f32)
+        self.r = torch.empty((d, B), **f32)
+        self.f = torch.empty((d, B), **f32)
+        self.q = torch.empty((H * dk, B), **f32)
+        self.k = torch.empty((Hkv * dk, B), **f32)
+        self.v = torch.empty((Hkv * dk, B), **f32)
+        self.a = torch.empty((H * dk, B), **f32)
+        self.o = torch.empty((d, B), **f32)
+        self.xi = torch.empty((B * kpd(max(d, H * dk)),), dtype=torch.int8, device=dev)
+        self.s = torch.empty((B,), **f32)
+        self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
+        self.logits = torch.empty((cfg.vocab, B), **f32)
+        self.ids = torch.empty((B,), dtype=torch.int32, device=dev)
+
+    def _mm(self, lin: Linear, out):
+        return self.ctx.ternary_matmul(lin.rp, lin.tau, self.xi, self.s, self.rs, lin.N, lin.K, self.B,
+                                       bias=lin.bias, out=out)
+
+    def _quant(self, x, gamma):
+        outs = (self.xi, self.s, self.rs)
+        if gamma is None:
+            self.ctx.act_quant_i8(x, outs=outs)
+        else:
+            self.ctx.rmsnorm_quant_i8(x, gamma, self.cfg.eps, outs=outs)
+
+    def block_step(self, i: int, pos, len_bound: int, attn_hook=None):
+        """Block i on self.x (d, B) in place. attn_hook(a) may replace the attention output (tests)."""
+        cfg, blk, ctx = self.cfg, self.blocks[i], self.ctx
+        self._quant(self.x, blk.g1)
+        self._mm(blk.q, self.q)
+        self._mm(blk.k, self.k)
+        self._mm(blk.v, self.v)
+        kc, vc = self.caches[i]
+        ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
+                             self.cos, self.sin, out=self.a)
+        if attn_hook is not None:
+            attn_hook(i, self.a)
+        self._quant(self.a, blk.g_attn_sub)
+        self._mm(blk.o, self.o)
+        ctx.add(self.x, self.o, out=self.r)
+        ctx.ffn_glu_i8(self.r, blk.g2, cfg.eps, cfg.F, blk.fc1.rp, blk.fc1.tau, blk.fc1.bias, blk.fc2.rp, blk.fc2.tau,
+                       blk.fc2.bias, cfg.act, out=self.f, gamma_sub=blk.g_ffn_sub, eps_sub=cfg.eps)
+        ctx.add(self.r, self.f, out=self.x)
+
+    def step(self, ids, pos, len_bound: int, attn_hook=None):
+        """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,))."""
+        ctx = self.ctx
+        ctx.embedding_gather(self.emb, ids, out=self.x)
+        for i in range(len(self.blocks)):
+            self.block_step(i, pos, len_bound, attn_hook)
+        self._quant(self.x, self.g_final)
+        self._mm(self.head, self.logits)
+        ctx.argmax_cols(self.logits, out=self.ids)
+        return self.logits, self.ids
+
+
+def _pkg():
+    import sys
+    return sys.modules[__name__.rsplit(".", 1)[0]]
+
+
+def attention_bytes(B: int, lens, Hkv: int, dk: int, H: int) -> int:
+    """Algorithmic HBM bytes of one decode attention call: the cached keys and values read
+    (lens[b] - 1 rows each, f32), the new key/value rows written, q read and the output written."""
+    rows = sum(int(L) - 1 for L in lens)
+    return 2 * rows * Hkv * dk * 4 + 2 * B * Hkv * dk * 4 + 2 * B * Hkv * dk * 4 + 2 * B * H * dk * 4

@@ -328,6 +328,70 @@ Result<Tensor> ComputeEngine::ffn_glu_i8_forward(const Tensor& x, const Tensor* 
     return ffn_glu_i8_impl(x, gamma, eps, wq1, tau1, b1, wq2, tau2, b2, act, gamma_sub, eps_sub);
 }
 
+Result<Tensor> ComputeEngine::attention_decode(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& k_cache,
+                                               Tensor& v_cache, std::size_t max_len, const Tensor& positions,
+                                               std::size_t len_bound, const Tensor* rope_cos, const Tensor* rope_sin,
+                                               std::size_t heads, std::size_t kv_heads, Scalar scale)
+{
+    const char* fn = "attention_decode";
+    for (const Tensor* t : {&q, &k, &v, static_cast<const Tensor*>(&k_cache), static_cast<const Tensor*>(&v_cache), &positions})
+        EX_TRY_CHECK(check_owned(*t, fn));
+    if (kv_heads == 0 || heads % kv_heads != 0) return Error{"attention_decode: heads must be a multiple of kv_heads"};
+    if (q.rows() % heads != 0) return Error{"attention_decode: q rows must be heads * d_k, got " + shape(q)};
+    const std::size_t dk = q.rows() / heads, B = q.cols();
+    if (k.rows() != kv_heads * dk || v.rows() != kv_heads * dk || k.cols() != B || v.cols() != B)
+        return Error{"attention_decode: k / v must be (kv_heads * d_k, B), got " + shape(k) + " / " + shape(v)};
+    if (max_len == 0 || k_cache.rows() != B * max_len || k_cache.cols() != kv_heads * dk ||
+        v_cache.rows() != k_cache.rows() || v_cache.cols() != k_cache.cols())
+        return Error{"attention_decode: caches must be (B * max_len, kv_heads * d_k), got " + shape(k_cache) + " / " +
+                     shape(v_cache)};
+    if (positions.rows() != B || positions.cols() != 1)
+        return Error{"attention_decode: positions must be (B, 1), got " + shape(positions)};
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return Error{"attention_decode: rope tables go together"};
+    if (rope_cos)
+    {
+        EX_TRY_CHECK(check_owned(*rope_cos, fn));
+        EX_TRY_CHECK(check_owned(*rope_sin, fn));
+        if (rope_cos->rows() < max_len || rope_cos->cols() != dk / 2 || rope_sin->rows() != rope_cos->rows() ||
+            rope_sin->cols() != dk / 2)
+            return Error{"attention_decode: rope tables must be (>= max_len, d_k / 2)"};
+    }
+    EX_TRY(out, alloc_impl(q.rows(), B, Precision::F32));
+    EpochGuard gk{k_cache}, gv{v_cache};
+    EX_TRY_CHECK(attention_decode_impl(q, k, v, k_cache, v_cache, max_len, positions, len_bound, rope_cos, rope_sin,
+                                       heads, kv_heads, scale, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::add(const Tensor& x, const Tensor& y)
+{
+    EX_TRY_CHECK(check_owned(x, "add: x"));
+    EX_TRY_CHECK(check_owned(y, "add: y"));
+    if (x.rows() != y.rows() || x.cols() != y.cols()) return Error{"add: shape mismatch " + shape(x) + " vs " + shape(y)};
+    EX_TRY(out, alloc_impl(x.rows(), x.cols(), Precision::F32));
+    EX_TRY_CHECK(add_impl(x, y, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::embedding_gather(const Tensor& table, const Tensor& ids)
+{
+    EX_TRY_CHECK(check_owned(table, "embedding_gather: table"));
+    EX_TRY_CHECK(check_owned(ids, "embedding_gather: ids"));
+    if (ids.cols() != 1) return Error{"embedding_gather: ids must be (B, 1), got " + shape(ids)};
+    EX_TRY(out, alloc_impl(table.cols(), ids.rows(), Precision::F32));
+    EX_TRY_CHECK(embedding_gather_impl(table, ids, *out));
+    return *out;
+}
+
+Result<Tensor> ComputeEngine::argmax_cols(const Tensor& logits)
+{
+    EX_TRY_CHECK(check_owned(logits, "argmax_cols"));
+    if (logits.rows() == 0) return Error{"argmax_cols: empty logits"};
+    EX_TRY(out, alloc_impl(logits.cols(), 1, Precision::F32));
+    EX_TRY_CHECK(argmax_cols_impl(logits, *out));
+    return *out;
+}
+
 // Default composition in the reference layer order (compute_layer_feedforward.hpp:182-206).
 Result<Tensor> ComputeEngine::ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps, const Tensor& wq1,
                                               const Tensor& tau1, const Tensor& b1, const Tensor& wq2,

@@ -7,6 +7,8 @@
 // layout in engine scratch. bitlinear_i8_forward runs the fused path: one quantization
 // kernel (abs-max, scale, int8, row sums) and one GEMV/GEMM launch with the bias add in
 // its epilogue, producing the same bits as the reference call sequence.
+#include <map>
+#include <mutex>
 #include <optional>
 #include <cstdlib>
 #include <cstring>
@@ -43,12 +45,62 @@ const uint32_t* up(const Tensor& t) { return static_cast<const uint32_t*>(Tensor
 uint32_t* upw(const Tensor& t) { return static_cast<uint32_t*>(TensorAccess::ptr(t)); }
 
 // Context shared with every allocation's deleter, so buffers can be freed after the engine.
+// It also keeps a caching pool of device blocks: a tensor's storage goes back to the pool when
+// its last copy dies and a later allocation of the same size class takes it, so a decode loop
+// (a few dozen short-lived tensors per layer and step) makes no hipMalloc / hipFree calls once
+// warm. Reuse is safe without events because every call of the engine is ordered on the one
+// stream of the context: the kernels that used a block are queued before any that reuse it,
+// and host copies into a block wait for the stream.
 struct Ctx
 {
     nnhip_ctx* h = nullptr;
+    std::mutex mu;
+    std::multimap<std::size_t, void*> pool;  // size class -> free blocks
+    std::size_t pooled = 0;
+    static constexpr std::size_t kPoolCap = std::size_t(8) << 30;  // bytes kept before freeing instead
+
+    static std::size_t size_class(std::size_t bytes)
+    {
+        if (bytes <= 4096) return (bytes + 255) & ~std::size_t(255);
+        if (bytes <= (std::size_t(1) << 20)) return (bytes + 4095) & ~std::size_t(4095);
+        return (bytes + (std::size_t(1) << 20) - 1) & ~((std::size_t(1) << 20) - 1);
+    }
+    void* take(std::size_t cls)
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = pool.find(cls);
+        if (it == pool.end()) return nullptr;
+        void* p = it->second;
+        pool.erase(it);
+        pooled -= cls;
+        return p;
+    }
+    void give(void* p, std::size_t cls)
+    {
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            if (pooled + cls <= kPoolCap)
+            {
+                pool.emplace(cls, p);
+                pooled += cls;
+                return;
+            }
+        }
+        (void)nnhip_free(h, p);
+    }
+    void release_all()
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        for (auto& kv : pool) (void)nnhip_free(h, kv.second);
+        pool.clear();
+        pooled = 0;
+    }
     ~Ctx()
     {
-        if (h) (void)nnhip_ctx_destroy(h);
+        if (!h) return;
+        (void)nnhip_sync(h);
+        release_all();
+        (void)nnhip_ctx_destroy(h);
     }
 };
 
@@ -61,10 +113,18 @@ public:
 protected:
     Result<std::shared_ptr<void>> device_alloc(std::size_t bytes)
     {
-        void* p = nullptr;
-        NNHIP_TRY(nnhip_malloc(ctx_->h, bytes < 16 ? 16 : bytes, &p), "allocation");
+        const std::size_t cls = Ctx::size_class(bytes < 16 ? 16 : bytes);
+        void* p = ctx_->take(cls);
+        if (!p && nnhip_malloc(ctx_->h, cls, &p) != NNHIP_OK)
+        {
+            // out of memory: give the pooled blocks back to the device and try once more
+            (void)nnhip_sync(ctx_->h);
+            ctx_->release_all();
+            p = nullptr;
+            NNHIP_TRY(nnhip_malloc(ctx_->h, cls, &p), "allocation");
+        }
         std::shared_ptr<Ctx> keep = ctx_;
-        return std::shared_ptr<void>(p, [keep](void* q) { (void)nnhip_free(keep->h, q); });
+        return std::shared_ptr<void>(p, [keep, cls](void* q) { keep->give(q, cls); });
     }
 
     Result<Tensor> alloc_impl(std::size_t rows, std::size_t cols, Precision p) override
@@ -377,6 +437,43 @@ protected:
                                    fpw(*y)),
                   "ffn_glu_i8_forward");
         return *y;
+    }
+
+    Result<void> attention_decode_impl(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& k_cache,
+                                       const Tensor& v_cache, std::size_t max_len, const Tensor& positions,
+                                       std::size_t len_bound, const Tensor* rope_cos, const Tensor* rope_sin,
+                                       std::size_t heads, std::size_t kv_heads, Scalar scale,
+                                       const Tensor& out) override
+    {
+        const std::size_t dk = q.rows() / heads;
+        NNHIP_TRY(nnhip_attention_decode(ctx_->h, fp(q), fp(k), fp(v), q.cols(), heads, kv_heads, dk,
+                                         static_cast<const int32_t*>(TensorAccess::ptr(positions)), len_bound,
+                                         rope_cos ? fp(*rope_cos) : nullptr, rope_sin ? fp(*rope_sin) : nullptr,
+                                         fpw(k_cache), fpw(v_cache), max_len, scale, fpw(out)),
+                  "attention_decode");
+        return {};
+    }
+
+    Result<void> add_impl(const Tensor& x, const Tensor& y, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_add(ctx_->h, fp(x), fp(y), x.size(), fpw(out)), "add");
+        return {};
+    }
+
+    Result<void> embedding_gather_impl(const Tensor& table, const Tensor& ids, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_embedding_gather(ctx_->h, fp(table), static_cast<const int32_t*>(TensorAccess::ptr(ids)),
+                                         table.rows(), table.cols(), ids.rows(), fpw(out)),
+                  "embedding_gather");
+        return {};
+    }
+
+    Result<void> argmax_cols_impl(const Tensor& logits, const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_argmax_cols(ctx_->h, fp(logits), logits.rows(), logits.cols(),
+                                    static_cast<int32_t*>(TensorAccess::ptr(out))),
+                  "argmax_cols");
+        return {};
     }
 
     EngineInfo describe_impl() const override

@@ -17,8 +17,10 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstring>
 #include <memory>
 #include <string>
+#include <vector>
 
 #include "matrix.hpp"
 #include "precision.hpp"
@@ -183,6 +185,25 @@ public:
                                                     const Tensor& tau2, const Tensor& b2, int act,
                                                     const Tensor* gamma_sub = nullptr, Scalar eps_sub = 1e-5f);
 
+    // ---- batched decode step (config C5): one new token for each of B sequences. Index tensors
+    // (positions, token ids) are (B, 1) Precision::F32 containers of raw int32 words, like the
+    // packed containers (upload_indices / download_indices below).
+    // Decode attention, AttentionBase::forward_step steps 1.5-8 (compute_layer_attention.hpp:
+    // 1022-1083) for B sequences: q (H*dk, B), k / v (Hkv*dk, B); the caches are
+    // (B*max_len, Hkv*dk), sequence b's rows [b*max_len, (b+1)*max_len), and row pos[b] of each
+    // sequence receives the rotated key / the value; rope tables (max_len, dk/2) or null;
+    // len_bound >= every pos[b] + 1. Returns (H*dk, B).
+    [[nodiscard]] Result<Tensor> attention_decode(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& k_cache,
+                                                  Tensor& v_cache, std::size_t max_len, const Tensor& positions,
+                                                  std::size_t len_bound, const Tensor* rope_cos, const Tensor* rope_sin,
+                                                  std::size_t heads, std::size_t kv_heads, Scalar scale);
+    // x + y (the residual adds of GPTBlock::forward_step, compute_layer_gpt.hpp:208-218)
+    [[nodiscard]] Result<Tensor> add(const Tensor& x, const Tensor& y);
+    // gather_rows(table, ids) + transpose (compute_layer_gpt.hpp:700-704): table (V, d) -> (d, B)
+    [[nodiscard]] Result<Tensor> embedding_gather(const Tensor& table, const Tensor& ids);
+    // greedy token per column of logits (V, B) (compute_layer_base.hpp:1152-1160) -> (B, 1) ids
+    [[nodiscard]] Result<Tensor> argmax_cols(const Tensor& logits);
+
     [[nodiscard]] EngineInfo describe() const { return describe_impl(); }
     // Activation quantizations bitlinear_i8_forward has run (an engine may reuse the last one
     // for another BitLinear on the same input, e.g. the q / k / v projections). Diagnostic of
@@ -221,11 +242,37 @@ protected:
                                                          const Tensor& wq1, const Tensor& tau1, const Tensor& b1,
                                                          const Tensor& wq2, const Tensor& tau2, const Tensor& b2,
                                                          int act, const Tensor* gamma_sub, Scalar eps_sub);
+    [[nodiscard]] virtual Result<void> attention_decode_impl(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                             const Tensor& k_cache, const Tensor& v_cache,
+                                                             std::size_t max_len, const Tensor& positions,
+                                                             std::size_t len_bound, const Tensor* rope_cos,
+                                                             const Tensor* rope_sin, std::size_t heads,
+                                                             std::size_t kv_heads, Scalar scale, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> add_impl(const Tensor& x, const Tensor& y, const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> embedding_gather_impl(const Tensor& table, const Tensor& ids,
+                                                             const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> argmax_cols_impl(const Tensor& logits, const Tensor& out) = 0;
     [[nodiscard]] virtual EngineInfo describe_impl() const = 0;
     virtual void sync_impl() = 0;
 
     // helpers for implementations
     [[nodiscard]] Result<void> check_owned(const Tensor& t, const char* what) const;
 };
+
+// int32 index vectors (positions, token ids) as (n, 1) containers of raw words, and back
+[[nodiscard]] inline Result<Tensor> upload_indices(ComputeEngine& engine, const std::int32_t* ids, std::size_t n)
+{
+    Matrix m(n, 1);
+    if (n) std::memcpy(m.data(), ids, n * sizeof(std::int32_t));
+    return engine.from_matrix(m, Precision::F32);
+}
+
+[[nodiscard]] inline Result<std::vector<std::int32_t>> download_indices(ComputeEngine& engine, const Tensor& t)
+{
+    EX_TRY(m, engine.to_matrix(t, Precision::F32));
+    std::vector<std::int32_t> out(m->size());
+    if (!out.empty()) std::memcpy(out.data(), m->data(), out.size() * sizeof(std::int32_t));
+    return out;
+}
 
 }  // namespace nn

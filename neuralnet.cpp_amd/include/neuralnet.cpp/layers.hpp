@@ -484,7 +484,18 @@ public:
         fc2_.clear_cache();
     }
 
-    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
+    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override { return forward_normed_(input, nullptr); }
+
+    // `norm` (an RMSNorm of width d_model) and then the block, as a pre-norm residual block calls
+    // them (GPTBlock's norm2_ -> ff_, compute_layer_gpt.hpp:212-214). With int8 activations the
+    // engine runs the norm inside the fused block; the bits are those of norm.forward + forward.
+    [[nodiscard]] Result<Tensor> forward_with_norm(const Tensor& input, RMSNorm& norm)
+    {
+        return forward_normed_(input, &norm);
+    }
+
+private:
+    [[nodiscard]] Result<Tensor> forward_normed_(const Tensor& input, RMSNorm* norm)
     {
         if (input.rows() != d_model_) return Error{"feedforward forward: input shape mismatch"};
         ComputeEngine& engine = engine_ref();
@@ -493,12 +504,19 @@ public:
         {
             EX_TRY_CHECK(fc1_.ensure_quantized());
             EX_TRY_CHECK(fc2_.ensure_quantized());
-            return engine.ffn_glu_i8_forward(input, nullptr, 0.0f, fc1_.quantized_weights_packed(), fc1_.row_scales(),
+            return engine.ffn_glu_i8_forward(input, norm ? &norm->gamma() : nullptr, norm ? norm->epsilon() : 0.0f,
+                                             fc1_.quantized_weights_packed(), fc1_.row_scales(),
                                              fc1_.bias(), fc2_.quantized_weights_packed(), fc2_.row_scales(),
                                              fc2_.bias(), act, sub_norm_ ? &sub_norm_->gamma() : nullptr,
                                              sub_norm_ ? sub_norm_->epsilon() : 0.0f);
         }
-        EX_TRY(h1, fc1_.forward(input));
+        Tensor in = input;
+        if (norm)
+        {
+            EX_TRY(n, norm->forward(input));
+            in = *n;
+        }
+        EX_TRY(h1, fc1_.forward(in));
         EX_TRY(h2, engine.glu(*h1, act));
         if (sub_norm_)
         {
@@ -508,6 +526,7 @@ public:
         return fc2_.forward(*h2);
     }
 
+public:
 protected:
     [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
     {

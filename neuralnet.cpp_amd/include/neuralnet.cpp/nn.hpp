@@ -3,6 +3,7 @@
 // names through its C++ modules nn.core / nn.engine / nn.layer / nn.model / nn.cli).
 #include "cli_engine_factory.hpp"
 #include "compute_engine.hpp"
+#include "decoder.hpp"
 #include "hip_engine.hpp"
 #include "int8_pack.hpp"
 #include "layers.hpp"

@@ -21,6 +21,13 @@
 //       (host only), then load -> deploy state: packed words equal the file's bytes, repack ->
 //       unpack on the GPU gives them back, forward matches the host W1.58A8 reference, and
 //       save -> load reproduces the model
+//  [14] decoder step (config C5)            compute_position_encoding.hpp:45-166,
+//       compute_layer_attention.hpp:1003-1091, compute_layer_gpt.hpp:201-219, :693-851: RoPE
+//       table == libnn-hip.so's host table; attention forward_step vs a host double evaluation
+//       (rotation, GQA map, softmax) and the appended cache rows; batched forward_step ==
+//       the reference single-sequence signature per sequence; GPTBlock::forward_step == its
+//       composition of engine calls bit for bit; GPTModel greedy generation == forward_step +
+//       the reference greedy loop on the host
 // Exit: 0 pass, 1 fail, 77 skip (no gfx950 device).
 #include <algorithm>
 #include <array>
@@ -983,6 +990,224 @@ void test_model_files_device(nn::ComputeEngine& e)
               "latent -> absmean tau -> trit_pack reproduces the inference file's words");
     }
 }
+
+// Host double evaluation of one sequence's decode attention: q (H*dk) of the new token,
+// caches (len rows of Hkv*dk, already holding the rotated new key), RoPE at position len-1.
+std::vector<double> host_attention(const std::vector<float>& q, const std::vector<float>& kc, const std::vector<float>& vc,
+                                   std::size_t len, std::size_t H, std::size_t Hkv, std::size_t dk, float scale,
+                                   const nn::Matrix& cosT, const nn::Matrix& sinT)
+{
+    const std::size_t R = H / Hkv, half = dk / 2, p = len - 1;
+    std::vector<double> out(H * dk, 0.0);
+    for (std::size_t h = 0; h < H; ++h)
+    {
+        const std::size_t g = h / R;
+        std::vector<double> qr(dk);
+        for (std::size_t j = 0; j < half; ++j)
+        {
+            const double c = cosT.at(p, j), s = sinT.at(p, j), a = q[h * dk + j], b = q[h * dk + j + half];
+            qr[j] = a * c - b * s;
+            qr[j + half] = b * c + a * s;
+        }
+        std::vector<double> w(len);
+        double m = -1e300;
+        for (std::size_t t = 0; t < len; ++t)
+        {
+            double d = 0;
+            for (std::size_t i = 0; i < dk; ++i) d += qr[i] * kc[t * Hkv * dk + g * dk + i];
+            w[t] = d * scale;
+            m = std::max(m, w[t]);
+        }
+        double l = 0;
+        for (auto& x : w) l += (x = std::exp(x - m));
+        for (std::size_t i = 0; i < dk; ++i)
+        {
+            double o = 0;
+            for (std::size_t t = 0; t < len; ++t) o += w[t] / l * vc[t * Hkv * dk + g * dk + i];
+            out[h * dk + i] = o;
+        }
+    }
+    return out;
+}
+
+void test_decoder(nn::ComputeEngine& e)
+{
+    std::puts("[14] decoder step: RoPE, attention forward_step, GPTBlock, GPTModel greedy");
+    const std::size_t d = 256, H = 4, Hkv = 2, dk = 64, F = 320, max_len = 100;
+    // RoPE table
+    {
+        nn::RotaryTable rt;
+        CHECK(rt.build(e, dk, max_len).has_value(), "RotaryTable built");
+        std::vector<float> c(max_len * dk / 2), s(max_len * dk / 2);
+        const bool ok = nnhip_rope_table(dk, max_len, c.data(), s.data()) == NNHIP_OK;
+        CHECK(ok && same_bytes(download(e, rt.cos()).data(), c.data(), c.size() * 4) &&
+                  same_bytes(download(e, rt.sin()).data(), s.data(), s.size() * 4),
+              "RotaryTable == nnhip_rope_table bit for bit");
+    }
+    nn::CausalSelfAttention attn(d, H, max_len, Hkv, true, true);
+    CHECK(attn.init(e).has_value(), "CausalSelfAttention(256, 4 heads, 2 KV heads, SubLN) initialized");
+    attn.set_activation_quant(true);
+    CHECK(!attn.forward(upload(e, random_matrix(d, 1, 1))).has_value(), "full-sequence forward is refused");
+    // three sequences at positions 0, 5, 63 (all below 128: one work-group chunk each)
+    const std::size_t B = 3;
+    const std::int32_t posv[B] = {0, 5, 63};
+    auto cache = attn.make_cache(B);
+    CHECK(cache.has_value(), "KV cache for 3 sequences");
+    if (!cache) return;
+    // fill the earlier rows with arbitrary keys / values
+    {
+        nn::Matrix kc = random_matrix(B * max_len, Hkv * dk, 301), vc = random_matrix(B * max_len, Hkv * dk, 302);
+        (void)e.copy_from(cache->k, kc);
+        (void)e.copy_from(cache->v, vc);
+    }
+    const nn::Matrix kc0 = download(e, cache->k), vc0 = download(e, cache->v);
+    const nn::Matrix x = random_matrix(d, B, 303);
+    auto pos = nn::upload_indices(e, posv, B);
+    auto xt = upload(e, x);
+    auto y = attn.forward_step(e, xt, *cache, *pos, 64);
+    CHECK(y.has_value() && y->rows() == d && y->cols() == B, "batched forward_step -> (d_model, B)");
+    if (!y) return;
+    // the attention output itself: rerun the pieces and compare with the host double evaluation
+    {
+        auto q = attn.w_q().forward(xt);
+        auto k = attn.w_k().forward(xt);
+        auto v = attn.w_v().forward(xt);
+        nn::KVCache c2{e.create_tensor(B * max_len, Hkv * dk), e.create_tensor(B * max_len, Hkv * dk), B, max_len};
+        (void)e.copy_from(c2.k, kc0);
+        (void)e.copy_from(c2.v, vc0);
+        auto a = e.attention_decode(*q, *k, *v, c2.k, c2.v, max_len, *pos, 64, &attn.rotary()->cos(),
+                                    &attn.rotary()->sin(), H, Hkv, attn.scale());
+        bool ok = a.has_value();
+        double err = 0;
+        bool rows_ok = ok;
+        if (ok)
+        {
+            const nn::Matrix A = download(e, *a), Q = download(e, *q), K = download(e, *k), V = download(e, *v);
+            const nn::Matrix KC = download(e, c2.k), VC = download(e, c2.v);
+            const nn::Matrix cosT = download(e, attn.rotary()->cos()), sinT = download(e, attn.rotary()->sin());
+            for (std::size_t b = 0; b < B; ++b)
+            {
+                const std::size_t p = posv[b];
+                std::vector<float> qb(H * dk), kcb((p + 1) * Hkv * dk), vcb((p + 1) * Hkv * dk);
+                for (std::size_t i = 0; i < H * dk; ++i) qb[i] = Q.at(i, b);
+                for (std::size_t t = 0; t <= p; ++t)
+                    for (std::size_t i = 0; i < Hkv * dk; ++i)
+                    {
+                        kcb[t * Hkv * dk + i] = KC.at(b * max_len + t, i);
+                        vcb[t * Hkv * dk + i] = VC.at(b * max_len + t, i);
+                    }
+                // appended row: value exact, key = rotation of the new key (double, to 1e-6)
+                for (std::size_t g = 0; g < Hkv; ++g)
+                    for (std::size_t j = 0; j < dk / 2; ++j)
+                    {
+                        const double c = cosT.at(p, j), s = sinT.at(p, j);
+                        const double k0 = K.at(g * dk + j, b), k1 = K.at(g * dk + j + dk / 2, b);
+                        rows_ok = rows_ok && std::abs(KC.at(b * max_len + p, g * dk + j) - (k0 * c - k1 * s)) < 1e-6 &&
+                                  std::abs(KC.at(b * max_len + p, g * dk + j + dk / 2) - (k1 * c + k0 * s)) < 1e-6;
+                    }
+                for (std::size_t i = 0; i < Hkv * dk; ++i)
+                    rows_ok = rows_ok && VC.at(b * max_len + p, i) == V.at(i, b);
+                const auto ref = host_attention(qb, kcb, vcb, p + 1, H, Hkv, dk, attn.scale(), cosT, sinT);
+                for (std::size_t i = 0; i < H * dk; ++i) err = std::max(err, std::abs(A.at(i, b) - ref[i]));
+            }
+        }
+        CHECK(rows_ok, "appended cache rows: rotated key (vs double) and the exact value");
+        CHECK(ok && err < 1e-5, "attention_decode within 1e-5 of a host double evaluation");
+    }
+    // batched == the reference single-sequence signature, per sequence (same kernels, same chunking)
+    {
+        bool same = true;
+        const nn::Matrix Y = download(e, *y);
+        for (std::size_t b = 0; b < B && same; ++b)
+        {
+            nn::Matrix kb(max_len, Hkv * dk), vb(max_len, Hkv * dk), xb(d, 1);
+            std::memcpy(kb.data(), kc0.data() + b * max_len * Hkv * dk, kb.size() * 4);
+            std::memcpy(vb.data(), vc0.data() + b * max_len * Hkv * dk, vb.size() * 4);
+            for (std::size_t i = 0; i < d; ++i) xb.set_value(i, 0, x.at(i, b));
+            nn::Tensor kt = upload(e, kb), vt = upload(e, vb);
+            auto yb = attn.forward_step(e, upload(e, xb), kt, vt, posv[b]);
+            same = yb.has_value();
+            if (!same) break;
+            const nn::Matrix Yb = download(e, *yb);
+            for (std::size_t i = 0; i < d; ++i) same = same && Yb.at(i, 0) == Y.at(i, b);
+        }
+        CHECK(same, "forward_step(x (d, B), cache, positions) == forward_step(x_b, k_cache, v_cache, cur_len) per sequence");
+    }
+    // GPTBlock::forward_step == its composition of engine calls
+    {
+        nn::GPTBlock blk(d, H, F, max_len, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
+        CHECK(blk.init(e).has_value(), "GPTBlock initialized");
+        blk.set_activation_quant(true);
+        auto c1 = blk.attention().make_cache(B);
+        auto c2 = blk.attention().make_cache(B);
+        bool ok = c1.has_value() && c2.has_value();
+        if (ok)
+        {
+            (void)e.copy_from(c1->k, kc0);
+            (void)e.copy_from(c1->v, vc0);
+            (void)e.copy_from(c2->k, kc0);
+            (void)e.copy_from(c2->v, vc0);
+            auto yb = blk.forward_step(e, xt, *c1, *pos, 64);
+            auto n1 = blk.norm1().forward(xt);
+            auto a = n1 ? blk.attention().forward_step(e, *n1, *c2, *pos, 64) : nn::Result<nn::Tensor>(nn::Error{"n1"});
+            auto r2 = a ? e.add(xt, *a) : nn::Result<nn::Tensor>(nn::Error{"a"});
+            auto n2 = r2 ? blk.norm2().forward(*r2) : nn::Result<nn::Tensor>(nn::Error{"r2"});
+            auto f = n2 ? blk.feed_forward().forward(*n2) : nn::Result<nn::Tensor>(nn::Error{"n2"});
+            auto out = f ? e.add(*r2, *f) : nn::Result<nn::Tensor>(nn::Error{"f"});
+            ok = yb.has_value() && out.has_value() && bitwise_equal(download(e, *yb), download(e, *out)) &&
+                 bitwise_equal(download(e, c1->k), download(e, c2->k));
+        }
+        CHECK(ok, "GPTBlock::forward_step == norm1 -> attention -> add -> norm2 -> FeedForward -> add, bit for bit");
+    }
+    // GPTModel: greedy generation == forward_step + the reference greedy loop on the host
+    {
+        const std::size_t V = 97;
+        nn::GPTModel gm(V, d, 32, H, F, 2, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
+        CHECK(gm.init(e).has_value(), "GPTModel (2 blocks, vocab 97) initialized");
+        gm.set_activation_quant(true);
+        const std::vector<std::vector<std::int32_t>> prompts = {{5, 9, 2}, {1}, {40, 41, 42, 43, 44}};
+        auto gen = gm.generate_greedy(e, prompts, 6);
+        auto gen2 = gm.generate_greedy(e, prompts, 6);
+        CHECK(gen.has_value() && gen2.has_value() && *gen == *gen2 && (*gen)[0].size() == 6 && (*gen)[1].size() == 6,
+              "generate_greedy: 6 tokens per sequence, deterministic");
+        // manual lockstep loop with host-side greedy choice
+        bool same = gen.has_value();
+        auto caches = gm.make_caches(prompts.size());
+        std::vector<std::vector<std::int32_t>> manual(prompts.size());
+        std::vector<std::int32_t> cur(prompts.size()), pv(prompts.size());
+        for (std::size_t s = 0; same && s < 5 + 6 - 1; ++s)
+        {
+            for (std::size_t b = 0; b < prompts.size(); ++b)
+            {
+                if (s < prompts[b].size()) cur[b] = prompts[b][s];
+                pv[b] = static_cast<std::int32_t>(s);
+            }
+            auto ids = nn::upload_indices(e, cur.data(), cur.size());
+            auto pt = nn::upload_indices(e, pv.data(), pv.size());
+            auto lg = gm.forward_step(e, *ids, *pt, s + 1, *caches);
+            same = lg.has_value();
+            if (!same) break;
+            const nn::Matrix L = download(e, *lg);
+            for (std::size_t b = 0; b < prompts.size(); ++b)
+            {
+                std::size_t next = 0;
+                float best = L.at(0, b);
+                for (std::size_t v = 1; v < V; ++v)
+                    if (L.at(v, b) > best)
+                    {
+                        best = L.at(v, b);
+                        next = v;
+                    }
+                if (s + 1 < prompts[b].size()) continue;
+                if (manual[b].size() < 6) manual[b].push_back(static_cast<std::int32_t>(next));
+                cur[b] = static_cast<std::int32_t>(next);
+            }
+        }
+        CHECK(same && manual == *gen, "generate_greedy == forward_step + the reference greedy loop on downloaded logits");
+        auto too_long = gm.generate_greedy(e, prompts, 40);
+        CHECK(!too_long.has_value(), "prompt + new tokens beyond max_len is refused");
+    }
+}
 }  // namespace
 
 int main(int argc, char** argv)
@@ -1017,6 +1242,7 @@ int main(int argc, char** argv)
     test_feedforward(e);
     test_model_files_device(e);
     test_shared_input_quantization(e);
+    test_decoder(e);
     if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
     else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
     return g_failures == 0 ? 0 : 1;

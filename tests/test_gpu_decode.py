@@ -177,3 +177,149 @@ def test_add_gather_argmax_bitexact(ctx, orc):
     L[:, 7] = np.nan
     L[9999, 8] = 2.0
     assert host(ctx.argmax_cols(dev(L))).tolist() == orc.argmax_cols(L).tolist()
+
+
+# ---------------------------------------------------------------- the whole decode step
+
+def _linear(ctx, orc, N, K, seed, bias=True):
+    W = normal((N, K), seed, 0.0, 0.02)
+    tau = orc.row_absmean(W)
+    wq = orc.trit_pack(W, tau)
+    b = normal((N,), seed + 1, 0.0, 0.1) if bias else None
+    return wq, tau, b
+
+
+def _build_model(ctx, orc, nnhip, cfg, L, B, seed, subln):
+    """Random weights as oracle containers (host) and as device Linear objects."""
+    from nnhip_py import decoder as dmod
+    torch = __import__("torch")
+    host_blocks, dev_blocks = [], []
+    d, F, dk = cfg.d, cfg.F, cfg.dk
+    for l in range(L):
+        s0 = seed + 100 * l
+        hb = {
+            "g1": normal((d,), s0, 1.0, 0.1), "g2": normal((d,), s0 + 1, 1.0, 0.1),
+            "q": _linear(ctx, orc, cfg.H * dk, d, s0 + 2), "k": _linear(ctx, orc, cfg.Hkv * dk, d, s0 + 4),
+            "v": _linear(ctx, orc, cfg.Hkv * dk, d, s0 + 6), "o": _linear(ctx, orc, d, cfg.H * dk, s0 + 8),
+            "fc1": _linear(ctx, orc, 2 * F, d, s0 + 10), "fc2": _linear(ctx, orc, d, F, s0 + 12),
+            "ga": normal((d,), s0 + 14, 1.0, 0.1) if subln else None,
+            "gf": normal((F,), s0 + 15, 1.0, 0.1) if subln else None,
+        }
+        host_blocks.append(hb)
+
+        def lin(t, N, K):
+            wq, tau, b = t
+            return dmod.Linear(ctx.repack(dev(wq.view(np.int32)), K), dev(tau), None if b is None else dev(b), N, K)
+
+        wo, to, bo = ctx.glu_interleave(dev(hb["fc1"][0].view(np.int32)), dev(hb["fc1"][1]), dev(hb["fc1"][2]), F, d)
+        fc1 = dmod.Linear(ctx.repack(wo, d), to, bo, nnhip.glu_rows(F), d)
+        dev_blocks.append(dmod.Block(
+            g1=dev(hb["g1"]), q=lin(hb["q"], cfg.H * dk, d), k=lin(hb["k"], cfg.Hkv * dk, d), v=lin(hb["v"], cfg.Hkv * dk, d),
+            o=lin(hb["o"], d, cfg.H * dk), g2=dev(hb["g2"]), fc1=fc1, fc2=lin(hb["fc2"], d, F),
+            g_attn_sub=None if hb["ga"] is None else dev(hb["ga"]),
+            g_ffn_sub=None if hb["gf"] is None else dev(hb["gf"])))
+    emb = normal((cfg.vocab, d), seed + 7, 0.0, 1.0)
+    gfin = normal((d,), seed + 8, 1.0, 0.1)
+    head = _linear(ctx, orc, cfg.vocab, d, seed + 9, bias=False)
+    head_d = dmod.Linear(ctx.repack(dev(head[0].view(np.int32)), d), dev(head[1]), None, cfg.vocab, d)
+    dec = dmod.Decoder(ctx, cfg, dev_blocks, dev(emb), dev(gfin), head_d, B)
+    return dec, host_blocks, emb, gfin, head
+
+
+def _orc_bitlinear(orc, x, lin, gamma, eps):
+    """int8 BitLinear of the oracle: [RMSNorm ->] absmax int8 -> matmul_q_i8 [+ b]."""
+    wq, tau, b = lin
+    if gamma is None:
+        s = orc.act_scale(x)
+        xq = orc.quantize_i8(x, s, True)
+    else:
+        xq, s = orc.rmsnorm_quant_i8(x, gamma, eps)
+    y = orc.matmul_q_i8(wq, tau, xq, s, x.shape[0], x.shape[1])
+    return y if b is None else orc.add_row_broadcast(y, b)
+
+
+@pytest.mark.parametrize("subln", [True, False])
+def test_decode_step_chain(ctx, orc, nnhip, subln):
+    """Three decode steps of a 2-block model for 3 sequences at ragged positions (one crossing a
+    128-position chunk): every piece of the GPU chain against the oracle chain (GPTBlock::
+    forward_step order), with the GPU's attention output fed to the oracle's next step so the
+    int8 stages stay bit-exact: q/k/v, o, FFN, residuals, final norm + head, greedy ids bit for
+    bit; attention within tolerance; the KV caches bit for bit."""
+    import torch
+    from nnhip_py import decoder as dmod
+    cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=200, act=0, eps=1e-5)
+    L, B = 2, 3
+    dec, hb, emb, gfin, head = _build_model(ctx, orc, nnhip, cfg, L, B, 0x5EC + subln, subln)
+    cos, sin = orc.rope_table(cfg.dk, cfg.max_len)
+    kc_o = [np.zeros((B, cfg.max_len, cfg.Hkv * cfg.dk), np.float32) for _ in range(L)]
+    vc_o = [np.zeros_like(kc_o[0]) for _ in range(L)]
+    start = np.array([0, 7, 126], np.int32)
+    ids = np.array([3, 50, 96], np.int32)
+    for step in range(3):
+        pos = start + step
+        say(f"decode chain subln={subln} step {step} pos={pos.tolist()}")
+        attn_gpu = {}
+        dec_ids = dev(ids)
+        logits_d, next_d = dec.step(dec_ids, dev(pos), int(pos.max()) + 1,
+                                    attn_hook=lambda i, a: attn_gpu.__setitem__(i, a.cpu().numpy()))
+        logits, nxt = host(logits_d), host(next_d)
+        # oracle chain
+        x = orc.embedding_gather(emb, ids)
+        for l in range(L):
+            b = hb[l]
+            q = _orc_bitlinear(orc, x, b["q"], b["g1"], cfg.eps)
+            k = _orc_bitlinear(orc, x, b["k"], b["g1"], cfg.eps)
+            v = _orc_bitlinear(orc, x, b["v"], b["g1"], cfg.eps)
+            a = orc.attention_decode(q, k, v, cfg.H, cfg.Hkv, cfg.dk, pos, kc_o[l], vc_o[l], cfg.scale, cos, sin)
+            ag = attn_gpu[l]
+            assert np.max(np.abs(ag - a)) <= ATOL * max(1.0, float(np.max(np.abs(a))))
+            o = _orc_bitlinear(orc, ag, b["o"], b["ga"], cfg.eps)
+            r = x + o
+            f, _ = orc.ffn_glu_i8(r, b["g2"], cfg.eps, cfg.F, *b["fc1"], *b["fc2"], 0, gamma_sub=b["gf"],
+                                  eps_sub=cfg.eps)
+            x = r + f
+        lg = _orc_bitlinear(orc, x, head, gfin, cfg.eps)
+        assert same_bits(logits, lg), "logits differ"
+        assert nxt.tolist() == orc.argmax_cols(lg).tolist()
+        torch.cuda.synchronize()
+        for l in range(L):
+            assert same_bits(host(dec.caches[l][0]), kc_o[l]) and same_bits(host(dec.caches[l][1]), vc_o[l])
+        ids = nxt.astype(np.int32)
+
+
+def test_decode_step_graph_replay(ctx, orc, nnhip):
+    """The step captured in a graph (no allocation inside) and replayed: every replay equals an
+    eager step from the same state, with eager work and synchronizations between replays."""
+    import torch
+    from nnhip_py import decoder as dmod
+    cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=300, act=1, eps=1e-5)
+    L, B = 2, 4
+    dec, *_ = _build_model(ctx, orc, nnhip, cfg, L, B, 0x6A, True)
+    ids = dev(np.array([1, 2, 3, 4], np.int32))
+    pos = dev(np.array([10, 140, 0, 255], np.int32))
+    # fill the caches with arbitrary history
+    for kc, vc in dec.caches:
+        kc.copy_(torch.from_numpy(normal(tuple(kc.shape), 7)).cuda())
+        vc.copy_(torch.from_numpy(normal(tuple(vc.shape), 8)).cuda())
+    snap = [(kc.clone(), vc.clone()) for kc, vc in dec.caches]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dec.step(ids, pos, 300)          # warm-up: grows the context scratch outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = host(dec.logits).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dec.step(ids, pos, 300)
+    for rep in range(3):
+        for (kc, vc), (k0, v0) in zip(dec.caches, snap):
+            kc.copy_(k0)
+            vc.copy_(v0)
+        torch.cuda.synchronize()
+        say(f"graph replay {rep}")
+        g.replay()
+        torch.cuda.synchronize()
+        assert same_bits(host(dec.logits), eager)
+        _ = ctx.add(dev(np.ones(64, np.float32)), dev(np.ones(64, np.float32)))   # eager work between replays
+        torch.cuda.synchronize()

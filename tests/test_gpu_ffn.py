@@ -106,6 +106,27 @@ def test_matmul_glu(ctx, orc, M, act):
     assert same_bits(h, ref)
 
 
+@pytest.mark.parametrize("d,F,M", [(2560, 6912, 16), (1024, 100, 5), (2560, 13, 1), (4096, 700, 3)])
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("bias", [True, False])
+def test_matmul_glu_deep_gemv(ctx, orc, d, F, M, act, bias):
+    """Decode fc1 through the deep GEMV with the gated activation in its epilogue (k-tile counts
+    4, 10, 16; feature counts not multiples of 8), bit for bit against fc1 + glu."""
+    say(f"deep ternary_matmul_glu d={d} F={F} M={M} act={act} bias={bias}")
+    wq1, t1, b1 = fc1_case(orc, d, F, 700 + F + M, bias=bias)
+    X = normal((d, M), 800 + M, 0.0, 1.0)
+    s = orc.act_scale(X)
+    xq = orc.quantize_i8(X, s, True)
+    y1 = orc.matmul_q_i8(wq1, t1, xq, s, d, M)
+    if bias:
+        y1 = orc.add_row_broadcast(y1, b1)
+    ref = orc.glu(y1, act)
+    rp, to, bo = prepare_fc1(ctx, wq1, t1, b1, F, d)
+    xi, sg, rs = ctx.act_quant_i8(dev(X))
+    h = host(ctx.ternary_matmul_glu(rp, to, xi, sg, rs, F, d, M, act, bias=bo))
+    assert same_bits(h, ref)
+
+
 def block_case(orc, d, F, seed):
     wq1, t1, b1 = fc1_case(orc, d, F, seed)
     W2 = normal((d, F), seed + 2, 0.0, 0.02)

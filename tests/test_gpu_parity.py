@@ -279,6 +279,25 @@ def test_decode_gemv_shapes(ctx, orc, N, K, M):
     assert np.array_equal(Y, ref)
 
 
+@pytest.mark.parametrize("N,K,M,bias", [
+    (100, 1024, 3, True), (2561, 2560, 5, False), (17, 4096, 16, True), (2560, 6912, 16, True),
+    (10000, 2560, 16, False), (1, 2560, 1, True), (33, 6900, 2, True), (640, 2560, 13, False),
+    (20000, 2560, 2, True),   # more row tiles than the deep variant takes: the streaming GEMV
+])
+def test_decode_gemv_deep(ctx, orc, N, K, M, bias):
+    """The deep single-problem GEMV (all k stages in flight, activations staged in LDS by DMA,
+    up to 110 KB at K = 6912, M = 16) on its k-tile counts 4, 10, 16, 27 with row / token / k
+    tails, bit for bit."""
+    say(f"deep gemv N={N} K={K} M={M} bias={bias}")
+    tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, 3 * N + K + M)
+    b = normal((N,), 98) if bias else None
+    Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M, bias=dev(b) if bias else None))
+    ref = orc.matmul_q_i8(wq, tau, xq, s, K, M)
+    if bias:
+        ref = orc.add_row_broadcast(ref, b)
+    assert np.array_equal(Y, ref)
+
+
 @pytest.mark.parametrize("N,K,M", [(4096, 4096, 256), (11008, 4096, 1024), (4096, 4096, 2048),
                                    (2560, 2560, 100)])
 def test_prefill_gemm_shapes(ctx, orc, N, K, M):
