@@ -230,6 +230,24 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
                                   const float* s, const int32_t* rowsum, const float* bias, size_t N,
                                   size_t K, size_t M, float* Y);
 
+/* Y = nnhip_ternary_matmul(...) + res: the decoder's residual add in the same launch on the decode
+ * path (res (N, M) f32, must not alias Y). Same bits as nnhip_ternary_matmul then nnhip_add(res, Y).
+ * Replaces w_o's BitLinear::forward followed by the residual add of GPTBlock::forward_step
+ * (include/neuralnet.cpp/compute_layer_attention.hpp:1089; compute_layer_gpt.hpp:208-209). */
+nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                      const float* s, const int32_t* rowsum, const float* bias, const float* res,
+                                      size_t N, size_t K, size_t M, float* Y);
+
+/* count (1..4) BitLinears on the same int8 input (xi, s, rowsum; shared K and M):
+ * Y[i] (N[i], M) = nnhip_ternary_matmul(rp[i], tau[i], xi, s, rowsum, bias[i], N[i], K, M), as one
+ * launch on the decode path. rp / tau / N / Y are HOST arrays of count entries; bias may be NULL
+ * (no bias anywhere) or an array holding NULLs. Same bits as count separate calls.
+ * Replaces the q / k / v BitLinear::forward calls on one input
+ * (include/neuralnet.cpp/compute_layer_attention.hpp:1009-1011). */
+nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* const* rp, const float* const* tau,
+                                    const float* const* bias, const size_t* N, float* const* Y, const int8_t* xi,
+                                    const float* s, const int32_t* rowsum, size_t K, size_t M);
+
 /* Grouped decode GEMV: many independent (weights, activations) problems with M <= 16 in one
  * launch, e.g. the q/k/v or gate/up projections of a layer, or a whole layer stack. The
  * descriptors are copied to the device once at creation; run() launches one kernel. */
@@ -355,6 +373,14 @@ nnhip_status nnhip_embedding_gather(nnhip_ctx* ctx, const float* table, const in
  * runs it on the softmax of the logits, which orders the same except where exp rounding
  * merges two nearly equal logits). */
 nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids);
+
+/* Y = res + the gated block of nnhip_ffn_glu_i8 on X (res (d, M) f32, must not alias Y): the second
+ * residual add of GPTBlock::forward_step in fc2's launch on the decode path. Same bits as
+ * nnhip_ffn_glu_i8 then nnhip_add(res, Y) (compute_layer_gpt.hpp:212-218). */
+nnhip_status nnhip_ffn_glu_i8_add(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
+                                  size_t M, int act, const void* rp1, const float* tau1, const float* b1,
+                                  const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
+                                  const float* b2, const float* res, float* Y);
 
 #ifdef __cplusplus
 }

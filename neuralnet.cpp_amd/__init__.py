@@ -92,6 +92,11 @@ SIGNATURES = {
     "nnhip_act_i8_from_container": (_st, [_vp, _vp, _sz, _sz, _vp, _vp]),
     "nnhip_act_i8_to_container": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_ternary_matmul": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_ternary_matmul_add": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                     ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
+    "nnhip_ffn_glu_i8_add": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
+                                   _vp, _vp, _vp]),
     "nnhip_group_create": (_st, [_vp, ctypes.POINTER(GemvDesc), _sz, ctypes.POINTER(_vp)]),
     "nnhip_group_run": (_st, [_vp, _vp]),
     "nnhip_group_destroy": (_st, [_vp, _vp]),
@@ -442,6 +447,53 @@ class Context:
                                           self._dev(bias, torch.float32, "bias"), N, K, M,
                                           self._dev(Y, torch.float32, "Y")),
                "nnhip_ternary_matmul")
+        return Y
+
+    def ternary_matmul_add(self, rp, tau, xi, s, rowsum, N: int, K: int, M: int, res, bias=None, out=None):
+        """Y = ternary_matmul(...) + res (res must not alias Y)."""
+        torch = self._torch
+        Y = self._empty((N, M), torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_add(self.h, self._dev(rp, torch.int32, "rp"),
+                                              self._dev(tau, torch.float32, "tau"), self._dev(xi, torch.int8, "xi"),
+                                              self._dev(s, torch.float32, "s"),
+                                              self._dev(rowsum, torch.int32, "rowsum"),
+                                              self._dev(bias, torch.float32, "bias"),
+                                              self._dev(res, torch.float32, "res"), N, K, M,
+                                              self._dev(Y, torch.float32, "Y")), "nnhip_ternary_matmul_add")
+        return Y
+
+    def ternary_matmul_n(self, problems, xi, s, rowsum, K: int, M: int):
+        """problems: list of (rp, tau, bias or None, N, out or None) sharing the input; returns the outputs."""
+        torch = self._torch
+        n = len(problems)
+        outs = [p[4] if p[4] is not None else self._empty((p[3], M), torch.float32) for p in problems]
+        rp = (_vp * n)(*[self._dev(p[0], torch.int32, "rp") for p in problems])
+        tau = (_vp * n)(*[self._dev(p[1], torch.float32, "tau") for p in problems])
+        bias = (_vp * n)(*[self._dev(p[2], torch.float32, "bias") for p in problems])
+        Ns = (_sz * n)(*[p[3] for p in problems])
+        Ys = (_vp * n)(*[self._dev(o, torch.float32, "Y") for o in outs])
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_n(self.h, n, rp, tau, bias, Ns, Ys, self._dev(xi, torch.int8, "xi"),
+                                            self._dev(s, torch.float32, "s"), self._dev(rowsum, torch.int32, "rowsum"),
+                                            K, M), "nnhip_ternary_matmul_n")
+        return outs
+
+    def ffn_glu_i8_add(self, X, gamma, eps: float, F: int, rp1, tau1, b1, rp2, tau2, b2, res, act: int = ACT_SWIGLU,
+                       out=None, gamma_sub=None, eps_sub: float = 1e-5):
+        """res + ffn_glu_i8(X, ...) (res must not alias the output)."""
+        torch = self._torch
+        d, M = X.shape
+        Y = self._empty((d, M), torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ffn_glu_i8_add(self.h, self._dev(X, torch.float32, "X"),
+                                          self._dev(gamma, torch.float32, "gamma"), eps, d, F, M, act,
+                                          self._dev(rp1, torch.int32, "rp1"), self._dev(tau1, torch.float32, "tau1"),
+                                          self._dev(b1, torch.float32, "b1"),
+                                          self._dev(gamma_sub, torch.float32, "gamma_sub"), eps_sub,
+                                          self._dev(rp2, torch.int32, "rp2"), self._dev(tau2, torch.float32, "tau2"),
+                                          self._dev(b2, torch.float32, "b2"), self._dev(res, torch.float32, "res"),
+                                          self._dev(Y, torch.float32, "Y")), "nnhip_ffn_glu_i8_add")
         return Y
 
     # -- batched decode step

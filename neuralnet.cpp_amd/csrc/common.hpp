@@ -79,6 +79,7 @@ struct GemvProblem
     int32_t glu_F;        // features of the gated output (rows of y when glu != 0)
     int32_t pad_;
     uint32_t* amax;       // prefill GEMM with glu: per-token max |h| (float bits, atomic max), or null
+    const float* res;     // deep decode GEMV: residual (N, M) added after the epilogue (may alias y), or null
 };
 
 // ---- gated activations (shared by k_glu.hip and the GEMM epilogue)
@@ -184,6 +185,11 @@ constexpr uint32_t kGemvDeepLds = 160 * 1024;
 constexpr int kGemvDeepMaxTilesPerCu = 4;
 bool gemv_deep_ok(const GemvProblem& p, int num_cus);  // also needs round_up(M * Kp, 1 KiB) <= kGemvDeepLds
 hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p);
+// Up to kGemvDeepMulti problems that share K, M and the activations (xi, s, rowsum) in one deep
+// launch; gemv_deep_multi_ok checks the shared shape and the total row tiles.
+constexpr int kGemvDeepMulti = 4;
+bool gemv_deep_multi_ok(const GemvProblem* ps, int count, int num_cus);
+hipError_t launch_gemv_deep_multi(hipStream_t st, const GemvProblem* ps, int count);
 // Grouped GEMV over a precomputed per-wave schedule: wave w runs the items
 // d_wave_items[d_wave_start[w] .. d_wave_start[w+1]) (item = problem << 20 | row tile).
 // If n_xstage > 0, the listed activation blocks (lds_bytes in total) are staged in LDS at

@@ -40,7 +40,12 @@ namespace
 
 constexpr int kAttnT = 128;        // cache positions per work-group
 constexpr int kAttnThreads = 256;  // 4 waves
-constexpr int kAttnMaxR = 8;       // query heads per KV head
+#ifndef NNHIP_ATTN_MINW
+#define NNHIP_ATTN_MINW 4          // waves per SIMD the chunk kernel is compiled for (<= 128 VGPRs)
+#endif
+#ifndef NNHIP_ATTN_PB
+#define NNHIP_ATTN_PB 4            // score passes (32 positions each) whose loads are in flight together
+#endif
 constexpr int kRecPad = 16;        // record tail: max[8], sum[8]
 
 struct AttnArgs
@@ -77,23 +82,39 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float cs, float sn
     y1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(x0, sn));
 }
 
-template <int DK, bool kFinal>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes at byte offset voff + soff of the resource (0 when out of range). The cached keys and
+// values are read once per call: non-temporal loads ("nt" on gfx950) keep them from displacing
+// the rest of L2.
+#ifndef NNHIP_ATTN_LOAD_AUX
+#define NNHIP_ATTN_LOAD_AUX 2
+#endif
+__device__ __forceinline__ float4 ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
+}
+
+template <int DK, int RT, bool kFinal>
+__global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_MINW : 1) void k_attn_chunk(AttnArgs a)
 {
     constexpr int HALF = DK / 2;
     constexpr int Q4 = DK / 4;         // float4 per row
     constexpr int F4 = DK / 32;        // float4 per lane in the score phase (8 lanes per position)
-    constexpr int PB = DK <= 128 ? 4 : 2;  // positions passes whose loads are issued together
+    constexpr int PB = DK <= 128 ? NNHIP_ATTN_PB : 2;  // position passes whose loads are issued together
     constexpr int VL = DK / 4;         // lanes per row in the value phase
     constexpr int NG = kAttnThreads / VL;  // rows per value step
-    __shared__ float4 q_s[kAttnMaxR * Q4];
+    __shared__ float4 q_s[RT * Q4];
     __shared__ float4 kn_s[Q4], vn_s[Q4];
-    __shared__ float S[kAttnMaxR][kAttnT];
-    __shared__ float ml[2][kAttnMaxR];
-    __shared__ float4 red[4][kAttnMaxR * Q4];
+    __shared__ float S[RT][kAttnT];
+    __shared__ float ml[2][RT];
+    __shared__ float4 red[4][RT * Q4];
 
     const int tid = threadIdx.x;
-    const int R = a.R;
+    const int R = a.R;  // query heads per KV head (<= RT, the register / LDS sizing)
     const int w = tid >> 6, lane = tid & 63;
     const int total = a.nchunk * a.Hkv * a.B;
     // persistent: work-group items (chunk fastest, then KV head, then sequence)
@@ -159,9 +180,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
             }
         }
 
-        // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row
+        // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row.
+        //      Cached rows come through one buffer resource per (sequence, KV head): lanes past the
+        //      chunk or on the new position read zeros without a branch, so every load of a pass
+        //      is in flight at once; the new position's key is selected from LDS afterwards.
         const int pg = tid >> 3, j8 = tid & 7;
-        const float* kbase = a.kc + seq_off;
+        const __amdgpu_buffer_rsrc_t rk = attn_rsrc(a.kc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
+        const __amdgpu_buffer_rsrc_t rv = attn_rsrc(a.vc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
 #pragma unroll
         for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
         {
@@ -171,24 +196,27 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
             {
                 const int tl = (pass0 + u) * 32 + pg;
                 const int t = t0 + tl;
+                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
 #pragma unroll
-                for (int i = 0; i < F4; ++i)
+                for (int i = 0; i < F4; ++i) kv[u][i] = ld_f4(rk, row, 16u * (j8 + 8 * i));
+            }
+#pragma unroll
+            for (int u = 0; u < PB; ++u)
+            {
+                const int tl = (pass0 + u) * 32 + pg;
+                if (t0 + tl == p)
                 {
-                    if (tl < n && t < p)
-                        kv[u][i] = *reinterpret_cast<const float4*>(kbase + (size_t)t * rstride + 4 * (j8 + 8 * i));
-                    else if (tl < n)
-                        kv[u][i] = kn_s[j8 + 8 * i];
-                    else
-                        kv[u][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int i = 0; i < F4; ++i) kv[u][i] = kn_s[j8 + 8 * i];
                 }
             }
 #pragma unroll
             for (int u = 0; u < PB; ++u)
             {
                 const int tl = (pass0 + u) * 32 + pg;
-                float d[kAttnMaxR];
+                float d[RT];
 #pragma unroll
-                for (int r = 0; r < kAttnMaxR; ++r)
+                for (int r = 0; r < RT; ++r)
                 {
                     d[r] = 0.f;
                     if (r < R)
@@ -208,12 +236,27 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
                 if (tl < n)
                 {
 #pragma unroll
-                    for (int r = 0; r < kAttnMaxR; ++r)
+                    for (int r = 0; r < RT; ++r)
                         if (r < R && j8 == r) S[r][tl] = __fmul_rn(d[r], a.scale);
                 }
             }
         }
         __syncthreads();
+
+        // ---- value rows: VL lanes per row (one float4 each), NG rows per step; the loads of the
+        //      whole chunk (VR rows per thread) are issued before the softmax so its latency
+        //      hides behind them
+        constexpr int VR = kAttnT / NG;
+        const int vg = tid / VL, vi = tid % VL;
+        float4 vv[VR];
+#pragma unroll
+        for (int u = 0; u < VR; ++u)
+        {
+            const int tl = vg + u * NG;
+            const int t = t0 + tl;
+            const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
+            vv[u] = ld_f4(rv, row, 16u * vi);
+        }
 
         // ---- chunk softmax statistics: one wave per head
         for (int r = w; r < R; r += 4)
@@ -237,49 +280,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
         }
         __syncthreads();
 
-        // ---- values: VL lanes per row (one float4 each), NG rows per step, 8 steps of loads in flight
-        const int vg = tid / VL, vi = tid % VL;
-        const float* vbase = a.vc + seq_off;
-        float4 acc[kAttnMaxR];
+        // ---- weighted values (the new position's value from LDS)
 #pragma unroll
-        for (int r = 0; r < kAttnMaxR; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int base = vg; base < n; base += 8 * NG)
+        for (int u = 0; u < VR; ++u)
+            if (t0 + vg + u * NG == p) vv[u] = vn_s[vi];
+        float4 acc[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < VR; ++u)
         {
-            float4 vv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
+            const int tl = vg + u * NG;
+            if (tl < n)
             {
-                const int tl = base + u * NG;
-                const int t = t0 + tl;
-                if (tl < n && t < p)
-                    vv[u] = *reinterpret_cast<const float4*>(vbase + (size_t)t * rstride + 4 * vi);
-                else if (tl < n)
-                    vv[u] = vn_s[vi];
-                else
-                    vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-            {
-                const int tl = base + u * NG;
-                if (tl < n)
-                {
-#pragma unroll
-                    for (int r = 0; r < kAttnMaxR; ++r)
-                        if (r < R)
-                        {
-                            const float pr = S[r][tl];
-                            acc[r].x = __builtin_fmaf(pr, vv[u].x, acc[r].x);
-                            acc[r].y = __builtin_fmaf(pr, vv[u].y, acc[r].y);
-                            acc[r].z = __builtin_fmaf(pr, vv[u].z, acc[r].z);
-                            acc[r].w = __builtin_fmaf(pr, vv[u].w, acc[r].w);
-                        }
-                }
+                for (int r = 0; r < RT; ++r)
+                    if (r < R)
+                    {
+                        const float pr = S[r][tl];
+                        acc[r].x = __builtin_fmaf(pr, vv[u].x, acc[r].x);
+                        acc[r].y = __builtin_fmaf(pr, vv[u].y, acc[r].y);
+                        acc[r].z = __builtin_fmaf(pr, vv[u].z, acc[r].z);
+                        acc[r].w = __builtin_fmaf(pr, vv[u].w, acc[r].w);
+                    }
             }
         }
         // rows of one wave -> lanes [0, VL), then the 4 waves through LDS in a fixed order
 #pragma unroll
-        for (int r = 0; r < kAttnMaxR; ++r)
+        for (int r = 0; r < RT; ++r)
             if (r < R)
                 for (int off = VL; off < kWave; off <<= 1)
                 {
@@ -291,7 +319,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_chunk(AttnArgs a)
         if (lane < VL)
         {
 #pragma unroll
-            for (int r = 0; r < kAttnMaxR; ++r)
+            for (int r = 0; r < RT; ++r)
                 if (r < R) red[w][r * Q4 + vi] = acc[r];
         }
         __syncthreads();
@@ -384,14 +412,15 @@ __global__ __launch_bounds__(DK) void k_attn_merge(AttnArgs a)
 }
 
 // Persistent grid: as many work-groups as fit the device at once (at most one per item).
-template <int DK, bool kFinal>
+template <int DK, int RT, bool kFinal>
 hipError_t launch_attn_variant(hipStream_t st, const AttnArgs& a, int num_cus)
 {
     static int per_cu = 0;
     if (per_cu == 0)
     {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_chunk<DK, kFinal>, kAttnThreads, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_chunk<DK, RT, kFinal>, kAttnThreads, 0) !=
+                hipSuccess ||
             n < 1)
             n = 1;
         per_cu = n;
@@ -399,15 +428,26 @@ hipError_t launch_attn_variant(hipStream_t st, const AttnArgs& a, int num_cus)
     const long total = (long)a.nchunk * a.Hkv * a.B;
     const long cap = (long)per_cu * (num_cus > 0 ? num_cus : 256);
     const unsigned grid = (unsigned)(total < cap ? total : cap);
-    k_attn_chunk<DK, kFinal><<<dim3(grid), kAttnThreads, 0, st>>>(a);
+    k_attn_chunk<DK, RT, kFinal><<<dim3(grid), kAttnThreads, 0, st>>>(a);
     return hipGetLastError();
+}
+
+// query heads per KV head: 1, 2, 4 or 8 at compile time (3, 5, 6, 7 run as the next power of two
+// with the extra heads masked)
+template <int DK, bool kFinal>
+hipError_t launch_attn_r(hipStream_t st, const AttnArgs& a, int num_cus)
+{
+    if (a.R == 1) return launch_attn_variant<DK, 1, kFinal>(st, a, num_cus);
+    if (a.R == 2) return launch_attn_variant<DK, 2, kFinal>(st, a, num_cus);
+    if (a.R <= 4) return launch_attn_variant<DK, 4, kFinal>(st, a, num_cus);
+    return launch_attn_variant<DK, 8, kFinal>(st, a, num_cus);
 }
 
 template <int DK>
 hipError_t launch_attn_dk(hipStream_t st, const AttnArgs& a, int num_cus)
 {
-    if (a.nchunk == 1) return launch_attn_variant<DK, true>(st, a, num_cus);
-    const hipError_t e = launch_attn_variant<DK, false>(st, a, num_cus);
+    if (a.nchunk == 1) return launch_attn_r<DK, true>(st, a, num_cus);
+    const hipError_t e = launch_attn_r<DK, false>(st, a, num_cus);
     if (e != hipSuccess) return e;
     k_attn_merge<DK><<<dim3(a.B * a.H), DK, 0, st>>>(a);
     return hipGetLastError();

@@ -291,22 +291,40 @@ __global__ __launch_bounds__(kBlock) void k_gemv_grouped(const GemvProblem* __re
 }
 
 // ---------------------------------------------------------------------------------------
-// Deep single-problem GEMV for grids smaller than the device (a decode step's BitLinears:
-// 160 - 864 row tiles). One 16-row tile per wave; the wave issues the loads of ALL its KT
-// weight stages first (one memory latency instead of KT / depth of them), then the block stages
-// the whole problem's activations (M x Kp bytes, up to 160 KB) into LDS while they land.
-// glu != 0: the rows are the interleaved gate/up rows of a gated FFN (16-row tile = gate rows
-// 8t..8t+7, then up rows 8t..8t+7); lanes of the gate half take their up values from the lane
-// 32 apart and store act(gate, up) as features 8t..8t+7 of h (glu_F, M) instead of Y.
+// Deep decode GEMV for grids smaller than the device (a decode step's BitLinears: 160 - 864
+// row tiles), over up to kGemvDeepMulti problems that share K, M and the activations (the
+// q / k / v projections of one input). One 16-row tile per wave; the wave issues the loads of
+// ALL its KT weight stages first (one memory latency instead of KT / depth of them), then the
+// block stages the shared activations (M x Kp bytes, up to 160 KB) into LDS by buffer->LDS DMA
+// while they land. res != 0: y = epilogue + res[n, m] (the decoder's residual add, the same
+// single rounding as a separate add). glu != 0: the rows are the interleaved gate/up rows of a
+// gated FFN (16-row tile = gate rows 8t..8t+7, then up rows 8t..8t+7); lanes of the gate half
+// take their up values from the lane 32 apart and store act(gate, up) as features 8t..8t+7 of
+// h (glu_F, M) instead of Y.
+struct GemvDeepArgs
+{
+    GemvProblem p[kGemvDeepMulti];
+    int tile0[kGemvDeepMulti + 1];  // first row tile of each problem in the launch (prefix sums)
+    int count;
+    uint32_t xbytes;
+};
+
 template <int KT>
-__global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvProblem p, int n_tiles, uint32_t xbytes)
+__global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvDeepArgs da)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
-    const int rt = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6));
+    const int gt = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6));
+    int pi = 0;
+#pragma unroll
+    for (int j = 1; j < kGemvDeepMulti; ++j)
+        if (j < da.count && gt >= da.tile0[j]) pi = j;
+    const GemvProblem& p = da.p[pi];
+    const int rt = gt - da.tile0[pi];
+    const int n_tiles = da.tile0[pi + 1] - da.tile0[pi];
     const int g = lane >> 4, t = lane & 15;
     const uint32_t Kp = (uint32_t)KT * kTileK;
-    const bool live = rt < n_tiles;
+    const bool live = gt < da.tile0[da.count];
 
     // 1. all weight stages of the tile (a tile past the matrix reads zero words)
     const __amdgpu_buffer_rsrc_t rw = rsrc(p.rp + (size_t)(live ? rt : 0) * KT * 64, live ? (uint32_t)KT * 1024u : 0u);
@@ -317,25 +335,28 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvProblem p, int n_tiles
     // 2. epilogue operands (rows past N and tokens past M read 0)
     const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
     const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rres = rsrc(p.res ? p.res : p.tau, p.res ? (uint32_t)p.N * (uint32_t)p.M * 4u : 0u);
     const uint32_t tok = t < p.M ? (uint32_t)t : 0x40000000u;
     const int rs2 = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.rowsum, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
     const float sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.s, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
-    float tv[4], bv[4];
+    float tv[4], bv[4], rv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
     {
         const uint32_t n = (uint32_t)(rt * 16 + 4 * g + i);
         tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, n * 4u, 0, 0));
         bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, n * 4u, 0, 0));
+        const uint32_t ro = (n < (uint32_t)p.N && t < p.M) ? (n * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u;
+        rv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, ro, 0, 0));
     }
 
     // 3. activations into LDS by buffer->LDS DMA (1 KiB per instruction, no registers), issued
     //    behind the weight loads; __syncthreads waits for both and joins the waves
     {
         typedef __attribute__((address_space(3))) void lds_void;
-        const __amdgpu_buffer_rsrc_t rx = rsrc(p.xi, xbytes);
+        const __amdgpu_buffer_rsrc_t rx = rsrc(p.xi, da.xbytes);
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        const int nq = (int)((xbytes + 1023u) / 1024u);
+        const int nq = (int)((da.xbytes + 1023u) / 1024u);
         for (int q = wave; q < nq; q += kBlock / kWave)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + q * 1024), 16, (uint32_t)lane * 16u,
                                                      (uint32_t)q * 1024u, 0, 0);
@@ -356,7 +377,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvProblem p, int n_tiles
         compute_stage<1>(w1, x, acc);
     }
 
-    // 5. epilogue, the reference order: y = (tau * s) * float(acc) [+ bias]
+    // 5. epilogue, the reference order: y = (tau * s) * float(acc) [+ bias] [+ residual]
     float y[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -364,6 +385,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvProblem p, int n_tiles
         const int a = acc[0].a0[i] + acc[0].a3[i] + (acc[0].a1[i] >> 2) + (acc[0].a2[i] >> 4) - rs2;
         y[i] = (tv[i] * sv) * (float)a;
         if (p.bias) y[i] = y[i] + bv[i];
+        if (p.res) y[i] = y[i] + rv[i];
     }
     if (p.glu == 0)
     {
@@ -390,10 +412,11 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvProblem p, int n_tiles
                                                   st ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u, 0, 0);
         }
     }
+    (void)n_tiles;
 }
 
 template <int KT>
-hipError_t launch_deep_kt(hipStream_t st, const GemvProblem& p, int n_tiles, uint32_t xbytes)
+hipError_t launch_deep_kt(hipStream_t st, const GemvDeepArgs& da)
 {
     static bool attr = false;
     if (!attr)
@@ -403,10 +426,10 @@ hipError_t launch_deep_kt(hipStream_t st, const GemvProblem& p, int n_tiles, uin
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const unsigned blocks = (unsigned)ceil_div((size_t)n_tiles, (size_t)(kBlock / kWave));
+    const unsigned blocks = (unsigned)ceil_div((size_t)da.tile0[da.count], (size_t)(kBlock / kWave));
     // the last DMA instruction fills a whole KiB (lanes past xbytes read zeros)
-    const uint32_t lds_bytes = (uint32_t)round_up(xbytes, 1024);
-    hipLaunchKernelGGL(k_gemv_deep<KT>, dim3(blocks), dim3(kBlock), lds_bytes, st, p, n_tiles, xbytes);
+    const uint32_t lds_bytes = (uint32_t)round_up(da.xbytes, 1024);
+    hipLaunchKernelGGL(k_gemv_deep<KT>, dim3(blocks), dim3(kBlock), lds_bytes, st, da);
     return hipGetLastError();
 }
 
@@ -423,27 +446,49 @@ size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds)
     return blocks * (kBlock / kWave);
 }
 
-bool gemv_deep_ok(const GemvProblem& p, int num_cus)
+bool gemv_deep_multi_ok(const GemvProblem* ps, int count, int num_cus)
 {
-    const size_t tiles = ceil_div((size_t)p.N, 16);
+    if (count < 1 || count > kGemvDeepMulti) return false;
+    const GemvProblem& p = ps[0];
+    size_t tiles = 0;
+    for (int i = 0; i < count; ++i)
+    {
+        if (ps[i].K != p.K || ps[i].M != p.M || ps[i].xi != p.xi || ps[i].s != p.s || ps[i].rowsum != p.rowsum ||
+            ps[i].N < 1)
+            return false;
+        tiles += ceil_div((size_t)ps[i].N, 16);
+    }
     const size_t xbytes = (size_t)p.M * (size_t)p.KT * kTileK;
     const bool kt_ok = p.KT == 4 || p.KT == 10 || p.KT == 16 || p.KT == 27;
-    return kt_ok && round_up(xbytes, 1024) <= kGemvDeepLds && tiles <= (size_t)kGemvDeepMaxTilesPerCu * (size_t)(num_cus > 0 ? num_cus : 256);
+    return kt_ok && round_up(xbytes, 1024) <= kGemvDeepLds &&
+           tiles <= (size_t)kGemvDeepMaxTilesPerCu * (size_t)(num_cus > 0 ? num_cus : 256);
 }
 
-hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p)
+bool gemv_deep_ok(const GemvProblem& p, int num_cus) { return gemv_deep_multi_ok(&p, 1, num_cus); }
+
+hipError_t launch_gemv_deep_multi(hipStream_t st, const GemvProblem* ps, int count)
 {
-    const int n_tiles = (int)ceil_div((size_t)p.N, 16);
-    const uint32_t xbytes = (uint32_t)p.M * (uint32_t)p.KT * kTileK;
-    switch (p.KT)
+    GemvDeepArgs da{};
+    da.count = count;
+    da.tile0[0] = 0;
+    for (int i = 0; i < count; ++i)
     {
-    case 4: return launch_deep_kt<4>(st, p, n_tiles, xbytes);
-    case 10: return launch_deep_kt<10>(st, p, n_tiles, xbytes);
-    case 16: return launch_deep_kt<16>(st, p, n_tiles, xbytes);
-    case 27: return launch_deep_kt<27>(st, p, n_tiles, xbytes);
+        da.p[i] = ps[i];
+        da.tile0[i + 1] = da.tile0[i] + (int)ceil_div((size_t)ps[i].N, 16);
+    }
+    for (int i = count; i < kGemvDeepMulti; ++i) da.tile0[i + 1] = da.tile0[count];
+    da.xbytes = (uint32_t)ps[0].M * (uint32_t)ps[0].KT * kTileK;
+    switch (ps[0].KT)
+    {
+    case 4: return launch_deep_kt<4>(st, da);
+    case 10: return launch_deep_kt<10>(st, da);
+    case 16: return launch_deep_kt<16>(st, da);
+    case 27: return launch_deep_kt<27>(st, da);
     default: return hipErrorInvalidValue;
     }
 }
+
+hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p) { return launch_gemv_deep_multi(st, &p, 1); }
 
 hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus)
 {

@@ -161,7 +161,7 @@ nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
 nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
                         const int8_t* xi, const float* s, const int32_t* rowsum, const float* bias,
                         size_t N, size_t K, size_t M, float* Y, int glu = 0, size_t glu_F = 0,
-                        uint32_t* amax = nullptr)
+                        uint32_t* amax = nullptr, const float* res = nullptr)
 {
     GemvProblem p{};
     p.rp = static_cast<const u32x4*>(rp);
@@ -179,10 +179,18 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     p.glu = glu;
     p.glu_F = (int32_t)glu_F;
     p.amax = amax;
+    if (res && glu == 0 && M <= (size_t)kGemvMaxM && gemv_deep_ok(p, ctx->num_cus))
+    {
+        // the residual in the deep GEMV's epilogue
+        p.res = res;
+        NNHIP_LAUNCH(fn, launch_gemv_deep(ctx->stream, p));
+        return NNHIP_OK;
+    }
     if (M <= (size_t)kGemvMaxM)
         NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
     else
         NNHIP_LAUNCH(fn, launch_gemm(ctx->stream, p, ctx->num_cus, ctx->gemm_tile));
+    if (res) NNHIP_LAUNCH(fn, launch_add(ctx->stream, res, Y, N * M, Y));
     return NNHIP_OK;
 }
 
@@ -642,6 +650,66 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
     return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y);
 }
 
+nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                      const float* s, const int32_t* rowsum, const float* bias, const float* res,
+                                      size_t N, size_t K, size_t M, float* Y)
+{
+    const char* fn = "nnhip_ternary_matmul_add";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    const nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && tau && xi && s && rowsum && res && Y, fn, "null pointer");
+    NNHIP_REQUIRE(res != Y, fn, "res must not alias Y");
+    NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
+    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y, 0, 0, nullptr, res);
+}
+
+nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* const* rp, const float* const* tau,
+                                    const float* const* bias, const size_t* N, float* const* Y, const int8_t* xi,
+                                    const float* s, const int32_t* rowsum, size_t K, size_t M)
+{
+    const char* fn = "nnhip_ternary_matmul_n";
+    NNHIP_CHECK_CTX(fn);
+    if (count == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(count <= (size_t)kGemvDeepMulti, fn, "count must be in [1, 4]");
+    NNHIP_REQUIRE(rp && tau && N && Y && xi && s && rowsum, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
+    GemvProblem ps[kGemvDeepMulti]{};
+    for (size_t i = 0; i < count; ++i)
+    {
+        const nnhip_status st = check_matmul_shape(fn, N[i], K, M);
+        if (st != NNHIP_OK) return st;
+        NNHIP_REQUIRE(N[i] >= 1 && rp[i] && tau[i] && Y[i], fn, "null pointer or empty problem");
+        NNHIP_REQUIRE(aligned16(rp[i]), fn, "rp must be 16-byte aligned");
+        GemvProblem& p = ps[i];
+        p.rp = static_cast<const u32x4*>(rp[i]);
+        p.tau = tau[i];
+        p.xi = xi;
+        p.s = s;
+        p.rowsum = rowsum;
+        p.bias = bias ? bias[i] : nullptr;
+        p.y = Y[i];
+        p.N = (int32_t)N[i];
+        p.K = (int32_t)K;
+        p.M = (int32_t)M;
+        p.KT = (int32_t)ceil_div(K, kTileK);
+        p.xlds = -1;
+    }
+    if (M <= (size_t)kGemvMaxM && gemv_deep_multi_ok(ps, (int)count, ctx->num_cus))
+    {
+        NNHIP_LAUNCH(fn, launch_gemv_deep_multi(ctx->stream, ps, (int)count));
+        return NNHIP_OK;
+    }
+    for (size_t i = 0; i < count; ++i)
+    {
+        const nnhip_status st = run_matmul(ctx, fn, rp[i], tau[i], xi, s, rowsum, bias ? bias[i] : nullptr, N[i], K, M,
+                                           Y[i]);
+        if (st != NNHIP_OK) return st;
+    }
+    return NNHIP_OK;
+}
+
 nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, size_t count,
                                 nnhip_group** out)
 {
@@ -934,12 +1002,11 @@ size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M)
     return b;
 }
 
-nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
-                              size_t M, int act, const void* rp1, const float* tau1, const float* b1,
-                              const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
-                              const float* b2, float* Y)
+static nnhip_status ffn_glu_i8(nnhip_ctx* ctx, const char* fn, const float* X, const float* gamma, float eps,
+                               size_t d, size_t F, size_t M, int act, const void* rp1, const float* tau1,
+                               const float* b1, const float* gamma_sub, float eps_sub, const void* rp2,
+                               const float* tau2, const float* b2, const float* res, float* Y)
 {
-    const char* fn = "nnhip_ffn_glu_i8";
     NNHIP_CHECK_CTX(fn);
     if (M == 0 || d == 0) return NNHIP_OK;
     nnhip_status st = check_glu_args(fn, F, d, M, act);
@@ -995,7 +1062,27 @@ nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma
         NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, gamma_sub, gamma_sub != nullptr, eps_sub, F, M, xi2, s2, rs2,
                                           nullptr));
     }
-    return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y);
+    return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y, 0, 0, nullptr, res);
+}
+
+nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
+                              size_t M, int act, const void* rp1, const float* tau1, const float* b1,
+                              const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
+                              const float* b2, float* Y)
+{
+    return ffn_glu_i8(ctx, "nnhip_ffn_glu_i8", X, gamma, eps, d, F, M, act, rp1, tau1, b1, gamma_sub, eps_sub, rp2,
+                      tau2, b2, nullptr, Y);
+}
+
+nnhip_status nnhip_ffn_glu_i8_add(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
+                                  size_t M, int act, const void* rp1, const float* tau1, const float* b1,
+                                  const float* gamma_sub, float eps_sub, const void* rp2, const float* tau2,
+                                  const float* b2, const float* res, float* Y)
+{
+    const char* fn = "nnhip_ffn_glu_i8_add";
+    NNHIP_REQUIRE(res != nullptr, fn, "null residual");
+    NNHIP_REQUIRE(res != Y, fn, "res must not alias Y");
+    return ffn_glu_i8(ctx, fn, X, gamma, eps, d, F, M, act, rp1, tau1, b1, gamma_sub, eps_sub, rp2, tau2, b2, res, Y);
 }
 
 /* ------------------------------------------------ batched decode step */
@@ -1045,6 +1132,8 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
     NNHIP_REQUIRE(max_len >= 1 && max_len <= (1u << 24), fn, "max_len must be in [1, 2^24]");
     NNHIP_REQUIRE(len_bound >= 1 && len_bound <= max_len, fn, "len_bound must be in [1, max_len]");
     NNHIP_REQUIRE(mul_ok(B, max_len) && mul_ok(B * max_len, Hkv * dk), fn, "cache size overflow");
+    // one sequence's cache is addressed through a 32-bit buffer range
+    NNHIP_REQUIRE(max_len * Hkv * dk * 4 < 0x7FFFFFFFull, fn, "max_len * Hkv * dk * 4 must stay below 2^31");
     NNHIP_REQUIRE(aligned16(k_cache) && aligned16(v_cache), fn, "caches must be 16-byte aligned");
     const size_t wsb = attn_workspace_bytes(B, H, Hkv, dk, len_bound);
     if (wsb > ctx->attn_ws_bytes)

@@ -8,11 +8,11 @@ construction, so one step makes no allocation and can be captured in a graph and
 Per block (GPTBlock::forward_step, compute_layer_gpt.hpp:201-219, all BitLinears in the int8
 branch):
     xi = int8(RMSNorm1(x))                        nnhip_rmsnorm_quant_i8
-    q, k, v = BitLinear(xi)                       nnhip_ternary_matmul x 3 (decode GEMV)
+    q, k, v = BitLinear(xi)                       nnhip_ternary_matmul_n (one launch)
     a = attention(q, k, v, caches, pos)           nnhip_attention_decode (RoPE, GQA, append)
     xi = int8([SubLN] a)                          nnhip_rmsnorm_quant_i8 / nnhip_act_quant_i8
-    r = x + BitLinear_o(xi)                       nnhip_ternary_matmul, nnhip_add
-    x = r + FFN(RMSNorm2(r))                      nnhip_ffn_glu_i8 (norm fused), nnhip_add
+    r = x + BitLinear_o(xi)                       nnhip_ternary_matmul_add (residual in the epilogue)
+    x = r + FFN(RMSNorm2(r))                      nnhip_ffn_glu_i8_add (norm and residual fused)
 then logits = BitLinear_head(int8(RMSNorm_f(x))) and the greedy ids (nnhip_argmax_cols).
 """
 from __future__ import annotations
@@ -92,12 +92,10 @@ class Decoder:
         kpd = _pkg().kp
         self.x = torch.empty((d, B), **f32)
         self.r = torch.empty((d, B), **f32)
-        self.f = torch.empty((d, B), **f32)
         self.q = torch.empty((H * dk, B), **f32)
         self.k = torch.empty((Hkv * dk, B), **f32)
         self.v = torch.empty((Hkv * dk, B), **f32)
         self.a = torch.empty((H * dk, B), **f32)
-        self.o = torch.empty((d, B), **f32)
         self.xi = torch.empty((B * kpd(max(d, H * dk)),), dtype=torch.int8, device=dev)
         self.s = torch.empty((B,), **f32)
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
@@ -116,23 +114,25 @@ class Decoder:
             self.ctx.rmsnorm_quant_i8(x, gamma, self.cfg.eps, outs=outs)
 
     def block_step(self, i: int, pos, len_bound: int, attn_hook=None):
-        """Block i on self.x (d, B) in place. attn_hook(a) may replace the attention output (tests)."""
+        """Block i on self.x (d, B) in place. attn_hook(i, a) sees the attention output (tests)."""
         cfg, blk, ctx = self.cfg, self.blocks[i], self.ctx
         self._quant(self.x, blk.g1)
-        self._mm(blk.q, self.q)
-        self._mm(blk.k, self.k)
-        self._mm(blk.v, self.v)
+        ctx.ternary_matmul_n([(blk.q.rp, blk.q.tau, blk.q.bias, blk.q.N, self.q),
+                              (blk.k.rp, blk.k.tau, blk.k.bias, blk.k.N, self.k),
+                              (blk.v.rp, blk.v.tau, blk.v.bias, blk.v.N, self.v)],
+                             self.xi, self.s, self.rs, blk.q.K, self.B)
         kc, vc = self.caches[i]
         ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
                              self.cos, self.sin, out=self.a)
         if attn_hook is not None:
             attn_hook(i, self.a)
         self._quant(self.a, blk.g_attn_sub)
-        self._mm(blk.o, self.o)
-        ctx.add(self.x, self.o, out=self.r)
-        ctx.ffn_glu_i8(self.r, blk.g2, cfg.eps, cfg.F, blk.fc1.rp, blk.fc1.tau, blk.fc1.bias, blk.fc2.rp, blk.fc2.tau,
-                       blk.fc2.bias, cfg.act, out=self.f, gamma_sub=blk.g_ffn_sub, eps_sub=cfg.eps)
-        ctx.add(self.r, self.f, out=self.x)
+        o = blk.o
+        ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, self.B, self.x, bias=o.bias,
+                               out=self.r)
+        ctx.ffn_glu_i8_add(self.r, blk.g2, cfg.eps, cfg.F, blk.fc1.rp, blk.fc1.tau, blk.fc1.bias, blk.fc2.rp,
+                           blk.fc2.tau, blk.fc2.bias, self.r, cfg.act, out=self.x, gamma_sub=blk.g_ffn_sub,
+                           eps_sub=cfg.eps)
 
     def step(self, ids, pos, len_bound: int, attn_hook=None):
         """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,))."""

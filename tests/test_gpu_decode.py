@@ -323,3 +323,66 @@ def test_decode_step_graph_replay(ctx, orc, nnhip):
         assert same_bits(host(dec.logits), eager)
         _ = ctx.add(dev(np.ones(64, np.float32)), dev(np.ones(64, np.float32)))   # eager work between replays
         torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- fused decode entry points
+
+def _fast_linear(ctx, orc, N, K, seed, bias):
+    W = normal((N, K), seed, 0.0, 0.02)
+    tau = orc.row_absmean(W)
+    wq = orc.trit_pack(W, tau)
+    rp = ctx.repack(dev(wq.view(np.int32)), K)
+    b = dev(normal((N,), seed + 1, 0.0, 0.1)) if bias else None
+    return rp, dev(tau), b
+
+
+@pytest.mark.parametrize("N,K,M", [(2560, 2560, 16), (2560, 6912, 3), (100, 520, 3), (300, 520, 40)])
+def test_ternary_matmul_add_equals_unfused(ctx, orc, N, K, M):
+    """Residual in the epilogue (deep GEMV) or a trailing add (other paths): the same bits as
+    ternary_matmul followed by add."""
+    say(f"ternary_matmul_add N={N} K={K} M={M}")
+    rp, tau, b = _fast_linear(ctx, orc, N, K, 10 + N + K, True)
+    xi, s, rs = ctx.act_quant_i8(dev(normal((K, M), 11)))
+    res = dev(normal((N, M), 12))
+    y = host(ctx.ternary_matmul_add(rp, tau, xi, s, rs, N, K, M, res, bias=b))
+    ref = host(ctx.add(res, ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, bias=b)))
+    assert same_bits(y, ref)
+    with pytest.raises(Exception):
+        out = ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M)
+        ctx.ternary_matmul_add(rp, tau, xi, s, rs, N, K, M, out, out=out)   # aliasing is refused
+
+
+@pytest.mark.parametrize("K,M,Ns", [(2560, 16, (2560, 640, 640)), (2560, 1, (2560, 2560, 2560, 17)),
+                                    (520, 5, (100, 30)), (1024, 40, (64, 64, 64))])
+def test_ternary_matmul_n_equals_separate(ctx, orc, K, M, Ns):
+    """Several BitLinears on one input in one launch (deep path) or in turn: the same bits as
+    separate ternary_matmul calls."""
+    say(f"ternary_matmul_n K={K} M={M} Ns={Ns}")
+    xi, s, rs = ctx.act_quant_i8(dev(normal((K, M), 21)))
+    probs = []
+    for j, N in enumerate(Ns):
+        rp, tau, b = _fast_linear(ctx, orc, N, K, 30 + 7 * j, j % 2 == 1)
+        probs.append((rp, tau, b, N, None))
+    outs = ctx.ternary_matmul_n(probs, xi, s, rs, K, M)
+    for (rp, tau, b, N, _), y in zip(probs, outs):
+        ref = ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, bias=b)
+        assert same_bits(host(y), host(ref))
+
+
+@pytest.mark.parametrize("d,F,M", [(2560, 6912, 16), (256, 136, 16), (320, 100, 40)])
+def test_ffn_glu_i8_add_equals_unfused(ctx, orc, nnhip, d, F, M):
+    """The FFN block with the residual in fc2's epilogue: the same bits as ffn_glu_i8 + add."""
+    say(f"ffn_glu_i8_add d={d} F={F} M={M}")
+    W1 = normal((2 * F, d), 41, 0.0, 0.02)
+    t1 = orc.row_absmean(W1)
+    wq1 = orc.trit_pack(W1, t1)
+    wo, to, _ = ctx.glu_interleave(dev(wq1.view(np.int32)), dev(t1), None, F, d)
+    rp1 = ctx.repack(wo, d)
+    rp2, t2, b2 = _fast_linear(ctx, orc, d, F, 43, True)
+    X = dev(normal((d, M), 44))
+    g = dev(normal((d,), 45, 1.0, 0.1))
+    gs = dev(normal((F,), 46, 1.0, 0.1))
+    res = dev(normal((d, M), 47))
+    y = host(ctx.ffn_glu_i8_add(X, g, 1e-5, F, rp1, to, None, rp2, t2, b2, res, gamma_sub=gs))
+    ref = host(ctx.add(res, ctx.ffn_glu_i8(X, g, 1e-5, F, rp1, to, None, rp2, t2, b2, gamma_sub=gs)))
+    assert same_bits(y, ref)
