@@ -258,7 +258,10 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
     64 MiB container (32768 x 8192) at M=1, f32 in and out. GB/s of algorithmic bytes: packed
     weights N*ceil(K/16)*4 + 4*K*M (B) + 4*N (tau) + 4*N*M (Y); matmul_q_t reads the same
     container for the transposed product. Times are per Python-issued call (events), so the
-    decode shapes include the launch path; kernel-only times are in the rocprof summary."""
+    decode shapes include the launch path; kernel-only times are in the rocprof summary.
+    matmul_q_mfma: the same product on the repacked weights (nnhip_ternary_matmul_f, the HIP
+    engine's f32 BitLinear branch): activations split into int8 digits, int8 MFMA, int64 combine;
+    same algorithmic bytes."""
     res = {}
     n = max(10, steps // 2)
     for name, K, N in (("q 2560->2560", D, D), ("gate 2560->6912", D, FFN), ("down 6912->2560", FFN, D),
@@ -277,6 +280,12 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
             nb = wbytes + 4 * K * M + 4 * N + 4 * N * M
             res[f"matmul_q {name} M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
                                               "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+            # the same product on the repacked weights through the int8 MFMA path (digit split)
+            rp = ctx.repack(wq, K)
+            t, _ = time_launches(torch, stream, lambda: ctx.ternary_matmul_f(rp, tau, B, N, K, out=Y), n, 5)
+            res[f"matmul_q_mfma {name} M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                                   "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+            del rp
             # dX: (tau o A)^T . dY with A = the same (N, ceil(K/16)) container read transposed
             dY = torch.randn((N, M), generator=gen, device="cuda")
             dX = torch.empty((K, M), device="cuda")

@@ -230,6 +230,20 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
                                   const float* s, const int32_t* rowsum, const float* bias, size_t N,
                                   size_t K, size_t M, float* Y);
 
+/* Float-activation product on the fast layout: Y (N, M) = (tau o trit(rp)) . B with B (K, M) f32, or
+ * f16 when b_f16 != 0, and Y f32 or f16 (y_f16). The activations of each token are split exactly
+ * into four int8 digits of a per-token 31-bit fixed point (x rounded to 2^(E-31) where
+ * max|x| < 2^E), the digit products run on the int8 MFMA GEMV / GEMM (exact int32) and are
+ * combined in int64; results match a float64 evaluation far inside the reference tolerance
+ * (1e-4 x max(1, max|Y|)). A token holding NaN or an infinity gets the IEEE result of its
+ * non-finite terms per row (NaN for NaN, 0 x inf or opposite infinities, else the infinity).
+ * K < 131072. Uses context scratch (grown on demand).
+ * Replaces ComputeEngine::matmul_q on the BitLinear f32 branch (include/neuralnet.cpp/
+ * compute_layer_bitlinear.hpp:459-466; src/ternary_gemm_test.cpp:253-289) when the weights are
+ * kept repacked; nnhip_matmul_q takes the reference container. */
+nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float* tau, const void* B, int b_f16,
+                                    size_t N, size_t K, size_t M, void* Y, int y_f16);
+
 /* Y = nnhip_ternary_matmul(...) + res: the decoder's residual add in the same launch on the decode
  * path (res (N, M) f32, must not alias Y). Same bits as nnhip_ternary_matmul then nnhip_add(res, Y).
  * Replaces w_o's BitLinear::forward followed by the residual add of GPTBlock::forward_step

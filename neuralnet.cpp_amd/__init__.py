@@ -92,6 +92,7 @@ SIGNATURES = {
     "nnhip_act_i8_from_container": (_st, [_vp, _vp, _sz, _sz, _vp, _vp]),
     "nnhip_act_i8_to_container": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_ternary_matmul": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_ternary_matmul_f": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_ternary_matmul_add": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                      ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
@@ -447,6 +448,19 @@ class Context:
                                           self._dev(bias, torch.float32, "bias"), N, K, M,
                                           self._dev(Y, torch.float32, "Y")),
                "nnhip_ternary_matmul")
+        return Y
+
+    def ternary_matmul_f(self, rp, tau, B, N: int, K: int, out_f16: bool = False, out=None):
+        """Float-activation product on repacked weights: (tau o trit) . B, B (K, M) f32 or f16."""
+        torch = self._torch
+        M = B.shape[1]
+        Y = self._empty((N, M), torch.float16 if out_f16 else torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_f(self.h, self._dev(rp, torch.int32, "rp"), self._dev(tau, torch.float32, "tau"),
+                                            self._dev(B, (torch.float32, torch.float16), "B"),
+                                            int(B.dtype == torch.float16), N, K, M,
+                                            self._dev(Y, (torch.float32, torch.float16), "Y"), int(out_f16)),
+               "nnhip_ternary_matmul_f")
         return Y
 
     def ternary_matmul_add(self, rp, tau, xi, s, rowsum, N: int, K: int, M: int, res, bias=None, out=None):

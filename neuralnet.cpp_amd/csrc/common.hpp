@@ -211,6 +211,14 @@ hipError_t launch_glu(hipStream_t st, const float* Y1, size_t F, size_t M, int a
 hipError_t launch_glu_interleave(hipStream_t st, const uint32_t* wq, const float* tau, const float* bias, size_t F,
                                  size_t K, uint32_t* wq_out, float* tau_out, float* bias_out);
 
+// ---- ternary x float products on the MFMA path (k_digits.hip): digit split of the activations
+// (4 int8 digit tokens per token, row sums, per-token exponents) and the int64 combine
+hipError_t launch_digits(hipStream_t st, const void* B, bool b16, size_t K, size_t M, int8_t* xi, int32_t* rowsum,
+                         int32_t* ex);
+hipError_t launch_digit_combine(hipStream_t st, const float* Yp, const float* tau, const int32_t* ex,
+                                const uint32_t* rp, const void* B, bool b16, size_t N, size_t K, size_t M, void* Y,
+                                bool y16);
+
 // ---- batched decode step (k_decode.hip)
 size_t attn_chunks(size_t len_bound);
 size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound);

@@ -31,6 +31,9 @@ struct nnhip_ctx
     int gemm_tile = NNHIP_GEMM_TILE_AUTO;
     void* attn_ws = nullptr;  // per-chunk partial results of the decode attention
     size_t attn_ws_bytes = 0;
+    float* ones = nullptr;  // 1.0f, the unit scales of the digit products
+    size_t ones_words = 0;
+    size_t ones_bytes_ = 0;
 };
 
 struct nnhip_group
@@ -261,6 +264,7 @@ nnhip_status nnhip_ctx_destroy(nnhip_ctx* ctx)
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->amax) (void)hipFree(ctx->amax);
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+    if (ctx->ones) (void)hipFree(ctx->ones);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
     if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
@@ -648,6 +652,45 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
     NNHIP_REQUIRE(rp && tau && xi && s && rowsum && Y, fn, "null pointer");
     NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
     return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y);
+}
+
+nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float* tau, const void* B, int b_f16,
+                                    size_t N, size_t K, size_t M, void* Y, int y_f16)
+{
+    const char* fn = "nnhip_ternary_matmul_f";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && tau && B && Y, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp), fn, "rp must be 16-byte aligned");
+    NNHIP_REQUIRE(M <= kMaxDim / 4 && mul_ok(N, 4 * M), fn, "size overflow");
+    // the digit products are exact integers in f32 while 128 K < 2^24
+    if (K >= 131072) return fail(NNHIP_ERR_UNSUPPORTED, fn, "K must be below 131072 (use nnhip_matmul_q)");
+    const size_t Kp = round_up(K, kTileK), M4 = 4 * M;
+    const size_t b_xi = round_up(M4 * Kp, 256), b_rs = round_up(M4 * 4, 256), b_ex = round_up(M * 4, 256);
+    const size_t b_yp = N * M4 * 4;
+    st = ensure_ws(ctx, b_xi + b_rs + b_ex + b_yp, fn);
+    if (st != NNHIP_OK) return st;
+    const size_t ones = N > M4 ? N : M4;
+    if (ctx->ones_words < ones)
+    {
+        st = ensure_buf(ctx, reinterpret_cast<void*&>(ctx->ones), ctx->ones_bytes_, ones * 4, fn, "unit scales");
+        if (st != NNHIP_OK) return st;
+        NNHIP_LAUNCH(fn, launch_fill_u32(ctx->stream, reinterpret_cast<uint32_t*>(ctx->ones), 0x3F800000u, ones));
+        ctx->ones_words = ones;
+    }
+    uint8_t* w = static_cast<uint8_t*>(ctx->ws);
+    int8_t* xi = reinterpret_cast<int8_t*>(w);
+    int32_t* rs = reinterpret_cast<int32_t*>(w + b_xi);
+    int32_t* ex = reinterpret_cast<int32_t*>(w + b_xi + b_rs);
+    float* yp = reinterpret_cast<float*>(w + b_xi + b_rs + b_ex);
+    NNHIP_LAUNCH(fn, launch_digits(ctx->stream, B, b_f16 != 0, K, M, xi, rs, ex));
+    st = run_matmul(ctx, fn, rp, ctx->ones, xi, ctx->ones, rs, nullptr, N, K, M4, yp);
+    if (st != NNHIP_OK) return st;
+    NNHIP_LAUNCH(fn, launch_digit_combine(ctx->stream, yp, tau, ex, static_cast<const uint32_t*>(rp), B, b_f16 != 0, N,
+                                          K, M, Y, y_f16 != 0));
+    return NNHIP_OK;
 }
 
 nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,

@@ -314,10 +314,19 @@ protected:
         return {};
     }
 
+    // f32 activations: the MFMA path on the cached repack (int8 digits of a per-token fixed point,
+    // nnhip_ternary_matmul_f) up to its K bound, else the reference-layout VALU kernel.
     Result<void> matmul_q_impl(const Tensor& wq, const Tensor& tau, const Tensor& B, const Tensor& y) override
     {
-        NNHIP_TRY(nnhip_matmul_q(ctx_->h, up(wq), fp(tau), fp(B), 0, wq.rows(), B.rows(), B.cols(), fpw(y), 0),
-                  "matmul_q");
+        const std::size_t N = wq.rows(), K = B.rows(), M = B.cols();
+        if (N == 0 || M == 0) return {};
+        if (K < 131072)
+        {
+            EX_TRY(rp, repacked(wq, K));
+            NNHIP_TRY(nnhip_ternary_matmul_f(ctx_->h, *rp, fp(tau), fp(B), 0, N, K, M, fpw(y), 0), "matmul_q");
+            return {};
+        }
+        NNHIP_TRY(nnhip_matmul_q(ctx_->h, up(wq), fp(tau), fp(B), 0, N, K, M, fpw(y), 0), "matmul_q");
         return {};
     }
 

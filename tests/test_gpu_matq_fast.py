@@ -1,0 +1,143 @@
+"""GPU parity of the float-activation product on the MFMA path (nnhip_ternary_matmul_f): f32 /
+f16 activations split into four int8 digits of a per-token 31-bit fixed point, ternary x int8
+products, int64 combine. Checked against the oracle's float64 evaluation of
+(tau o trit) . B (src/ternary_gemm_test.cpp:141-170): within 2e-6 x max(1, max|ref|) (f32 out;
+the reference itself allows 1e-4) and, for f16 outputs, within the reference's 4e-3; NaN and
+infinity patterns exactly.
+
+Reference: ComputeEngine::matmul_q on the BitLinear f32 branch
+(include/neuralnet.cpp/compute_layer_bitlinear.hpp:459-466).
+"""
+import numpy as np
+import pytest
+
+from conftest import normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-6
+
+
+def dev(a):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def case(ctx, orc, N, K, W=None, seed=0):
+    if W is None:
+        W = normal((N, K), seed, 0.0, 0.02)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    wq = orc.trit_pack(W, tau)
+    rp = ctx.repack(dev(wq), K)
+    return wq, tau, rp
+
+
+def check(got, ref, tol):
+    scale = max(1.0, float(np.nanmax(np.abs(np.where(np.isfinite(ref), ref, 0)))))
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN pattern differs"
+    inf = np.isinf(ref)
+    assert np.array_equal(np.isinf(got), inf) and np.array_equal(got[inf], ref[inf]), "infinities differ"
+    fin = np.isfinite(ref)
+    err = float(np.max(np.abs(got[fin].astype(np.float64) - ref[fin].astype(np.float64)))) if fin.any() else 0.0
+    assert err <= tol * scale, err
+
+
+@pytest.mark.parametrize("N,K,M", [(2560, 6912, 1), (2560, 2560, 4), (6912, 2560, 16), (640, 2560, 7),
+                                   (100, 520, 3), (65, 17, 65), (300, 1000, 40), (2560, 4096, 2)])
+def test_matmul_f_gaussian(ctx, orc, N, K, M):
+    say(f"ternary_matmul_f N={N} K={K} M={M}")
+    wq, tau, rp = case(ctx, orc, N, K, seed=N + K + M)
+    X = normal((K, M), 7 + M)
+    X[:, ::3] *= 37.0  # tokens of different magnitudes
+    got = host(ctx.ternary_matmul_f(rp, dev(tau), dev(X), N, K))
+    check(got, orc.matmul_q(wq, tau, X, K), TOL)
+
+
+def test_matmul_f_reference_pattern(ctx, orc):
+    """src/ternary_gemm_test.cpp:435-526 patterns (the int8 digits see exact 0.21 * j - 0.8 values)."""
+    M, K, N = 192, 48, 320    # rows, reduction, tokens
+    r = np.arange(M)[:, None]
+    c = np.arange(K)[None, :]
+    A = (np.float32(0.17) * ((r * 7 + c * 3) % 13).astype(np.float32) - np.float32(0.9)).astype(np.float32)
+    wq, tau, rp = case(ctx, orc, M, K, W=A)
+    k = np.arange(K)[:, None]
+    n = np.arange(N)[None, :]
+    B = (np.float32(0.21) * ((k + 2 * n) % 9).astype(np.float32) - np.float32(0.8)).astype(np.float32)
+    got = host(ctx.ternary_matmul_f(rp, dev(tau), dev(B), M, K))
+    check(got, orc.matmul_q(wq, tau, B, K), TOL)
+
+
+@pytest.mark.parametrize("b16,y16", [(True, False), (False, True), (True, True)])
+def test_matmul_f_half(ctx, orc, b16, y16):
+    import torch
+    N, K, M = 1000, 2560, 5
+    say(f"ternary_matmul_f f16 in={b16} out={y16}")
+    wq, tau, rp = case(ctx, orc, N, K, seed=3)
+    X = normal((K, M), 4)
+    if b16:
+        X = X.astype(np.float16).astype(np.float32)
+    Xd = dev(X).to(torch.float16) if b16 else dev(X)
+    got = host(ctx.ternary_matmul_f(rp, dev(tau), Xd, N, K, out_f16=y16))
+    ref = orc.matmul_q(wq, tau, X, K)
+    if y16:
+        ref = ref.astype(np.float16).astype(np.float32)
+    check(got, ref, 4e-3 if y16 else TOL)
+
+
+def test_matmul_f_special_values(ctx, orc):
+    """NaN and infinities give the IEEE result of the reference's per-term products; zero,
+    subnormal-only and very wide tokens stay within tolerance."""
+    N, K, M = 300, 1000, 8
+    say("ternary_matmul_f special values")
+    W = normal((N, K), 5, 0.0, 0.02)
+    W[:, 10] = 0.0          # trit 0 at k = 10 for every row
+    W[::2, 20] = 1.0        # +1 at k = 20 for even rows
+    W[1::2, 20] = -1.0      # -1 for odd rows
+    wq, tau, rp = case(ctx, orc, N, K, W=W)
+    X = normal((K, M), 6)
+    X[33, 0] = np.nan                       # token 0: NaN everywhere
+    X[20, 1] = np.inf                       # token 1: +inf on a +-1 column -> +inf / -inf rows
+    X[10, 2] = -np.inf                      # token 2: inf on a 0 column -> NaN
+    X[20, 3] = np.inf                       # token 3: +inf and -inf on the same column sign
+    X[21, 3] = -np.inf
+    X[:, 4] = 0.0                           # token 4: zeros
+    X[:, 5] = normal((K,), 7) * np.float32(1e-41)   # token 5: subnormals only
+    X[:, 6] = normal((K,), 8) * np.float32(1e-30)
+    X[5, 6] = np.float32(3e38)              # token 6: enormous range
+    X[:, 7] = normal((K,), 9) * np.float32(1e30)
+    got = host(ctx.ternary_matmul_f(rp, dev(tau), dev(X), N, K))
+    ref = orc.matmul_q(wq, tau, X, K)
+    for m in range(M):
+        check(got[:, m:m + 1], ref[:, m:m + 1], TOL)
+    assert np.all(np.isnan(got[:, 0])) and np.all(np.isnan(got[:, 2]))
+    assert np.all(got[::2, 1] == np.inf) and np.all(got[1::2, 1] == -np.inf)
+
+
+def test_matmul_f_agrees_with_valu_kernel(ctx, orc):
+    """The MFMA path and the reference-layout VALU kernel (nnhip_matmul_q) on the same inputs."""
+    N, K, M = 2560, 2560, 16
+    wq, tau, rp = case(ctx, orc, N, K, seed=11)
+    X = normal((K, M), 12)
+    a = host(ctx.ternary_matmul_f(rp, dev(tau), dev(X), N, K))
+    b = host(ctx.matmul_q(dev(wq), dev(tau), dev(X), K))
+    assert np.max(np.abs(a - b)) <= 1e-4 * max(1.0, float(np.max(np.abs(b))))
+
+
+def test_matmul_f_rejects_large_k(ctx, nnhip):
+    import torch
+    rp = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    tau = torch.ones(16, device="cuda")
+    B = torch.zeros((131072, 1), device="cuda")
+    with pytest.raises(nnhip.NNHipError):
+        ctx.ternary_matmul_f(rp, tau, B, 16, 131072)
