@@ -261,7 +261,8 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
     decode shapes include the launch path; kernel-only times are in the rocprof summary.
     matmul_q_mfma: the same product on the repacked weights (nnhip_ternary_matmul_f, the HIP
     engine's f32 BitLinear branch): activations split into int8 digits, int8 MFMA, int64 combine;
-    same algorithmic bytes."""
+    same algorithmic bytes. matmul_q_t_mfma: dX on the repack of the bit-transposed container
+    (nnhip_ternary_matmul_t_f), same bytes as matmul_q_t."""
     res = {}
     n = max(10, steps // 2)
     for name, K, N in (("q 2560->2560", D, D), ("gate 2560->6912", D, FFN), ("down 6912->2560", FFN, D),
@@ -293,6 +294,13 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
             nb = wbytes + 4 * N * M + 4 * N + 4 * K * M
             res[f"matmul_q_t {name} M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
                                                 "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+            # the same dX on the MFMA path: the transposed repack (made once per weight), tau folded
+            # into the digit split
+            rpT = ctx.repack(ctx.trit_transpose(wq, K), N)
+            t, _ = time_launches(torch, stream, lambda: ctx.ternary_matmul_t_f(rpT, tau, dY, K, out=dX), n, 5)
+            res[f"matmul_q_t_mfma {name} M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                                     "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+            del rpT
     out["matmul_q"] = res
     log(f"matmul_q: {res}")
 

@@ -244,6 +244,21 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
 nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float* tau, const void* B, int b_f16,
                                     size_t N, size_t K, size_t M, void* Y, int y_f16);
 
+/* Transposed float-activation product on the fast layout: Y (M, N) = (tau o trit(A))^T . B for a
+ * container A (K, ceil(M/16)) with tau (K) per stored row, B (K, N) f32 or f16, given rpT = the
+ * T16K256 repack of A's transpose (nnhip_trit_transpose, then nnhip_repack_ternary of the
+ * (M, ceil(K/16)) result with M rows and K columns). tau folds into the activations,
+ * fl(tau_k * b) * trit = fl(tau_k * trit) * b term by term; then as nnhip_ternary_matmul_f.
+ * Replaces ComputeEngine::matmul_q_t, the dX product of BitLinear::backward
+ * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:494; src/ternary_gemm_test.cpp:291-334). */
+nnhip_status nnhip_ternary_matmul_t_f(nnhip_ctx* ctx, const void* rpT, const float* tau, const void* B, int b_f16,
+                                      size_t K, size_t M, size_t N, void* Y, int y_f16);
+
+/* Bit transpose of a packed container: A (K, ceil(M/16)) -> At (M, ceil(K/16)), trit (m, k) of At =
+ * trit (k, m) of A, tail codes 2. The load-time step before nnhip_ternary_matmul_t_f (no
+ * reference counterpart: the reference reads the container transposed in place). */
+nnhip_status nnhip_trit_transpose(nnhip_ctx* ctx, const uint32_t* A, size_t K, size_t M, uint32_t* At);
+
 /* Y = nnhip_ternary_matmul(...) + res: the decoder's residual add in the same launch on the decode
  * path (res (N, M) f32, must not alias Y). Same bits as nnhip_ternary_matmul then nnhip_add(res, Y).
  * Replaces w_o's BitLinear::forward followed by the residual add of GPTBlock::forward_step

@@ -93,6 +93,8 @@ SIGNATURES = {
     "nnhip_act_i8_to_container": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_ternary_matmul": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_ternary_matmul_f": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
+    "nnhip_ternary_matmul_t_f": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
+    "nnhip_trit_transpose": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_ternary_matmul_add": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                      ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
@@ -461,6 +463,30 @@ class Context:
                                             int(B.dtype == torch.float16), N, K, M,
                                             self._dev(Y, (torch.float32, torch.float16), "Y"), int(out_f16)),
                "nnhip_ternary_matmul_f")
+        return Y
+
+    def trit_transpose(self, A, M: int):
+        """A (K, ceil(M/16)) packed -> At (M, ceil(K/16))."""
+        torch = self._torch
+        K = A.shape[0]
+        At = self._empty((M, (K + 15) // 16), torch.int32)
+        self._bind_stream()
+        _check(lib().nnhip_trit_transpose(self.h, self._dev(A, torch.int32, "A"), K, M, self._dev(At)),
+               "nnhip_trit_transpose")
+        return At
+
+    def ternary_matmul_t_f(self, rpT, tau, B, M: int, out_f16: bool = False, out=None):
+        """(tau o trit(A))^T . B on rpT = repack(transpose(A)); B (K, N); returns (M, N)."""
+        torch = self._torch
+        K, N = B.shape
+        Y = self._empty((M, N), torch.float16 if out_f16 else torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_t_f(self.h, self._dev(rpT, torch.int32, "rpT"),
+                                              self._dev(tau, torch.float32, "tau"),
+                                              self._dev(B, (torch.float32, torch.float16), "B"),
+                                              int(B.dtype == torch.float16), K, M, N,
+                                              self._dev(Y, (torch.float32, torch.float16), "Y"), int(out_f16)),
+               "nnhip_ternary_matmul_t_f")
         return Y
 
     def ternary_matmul_add(self, rp, tau, xi, s, rowsum, N: int, K: int, M: int, res, bias=None, out=None):

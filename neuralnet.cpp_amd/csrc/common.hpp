@@ -213,11 +213,15 @@ hipError_t launch_glu_interleave(hipStream_t st, const uint32_t* wq, const float
 
 // ---- ternary x float products on the MFMA path (k_digits.hip): digit split of the activations
 // (4 int8 digit tokens per token, row sums, per-token exponents) and the int64 combine
-hipError_t launch_digits(hipStream_t st, const void* B, bool b16, size_t K, size_t M, int8_t* xi, int32_t* rowsum,
-                         int32_t* ex);
+// kscale (nullable, per k) multiplies the activations first (the transposed product's tau);
+// tau (nullable) is the per-row output factor.
+hipError_t launch_digits(hipStream_t st, const void* B, bool b16, const float* kscale, size_t K, size_t M, int8_t* xi,
+                         int32_t* rowsum, int32_t* ex);
 hipError_t launch_digit_combine(hipStream_t st, const float* Yp, const float* tau, const int32_t* ex,
-                                const uint32_t* rp, const void* B, bool b16, size_t N, size_t K, size_t M, void* Y,
-                                bool y16);
+                                const uint32_t* rp, const void* B, bool b16, const float* kscale, size_t N, size_t K,
+                                size_t M, void* Y, bool y16);
+// Bit transpose of a packed container: A (K, ceil(M/16)) -> At (M, ceil(K/16)) (k_matq.hip)
+hipError_t launch_trit_transpose(hipStream_t st, const uint32_t* A, size_t K, size_t M, uint32_t* At);
 
 // ---- batched decode step (k_decode.hip)
 size_t attn_chunks(size_t len_bound);

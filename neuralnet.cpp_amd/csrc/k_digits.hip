@@ -31,12 +31,21 @@ __device__ __forceinline__ float load_b(const void* B, size_t idx, bool f16)
     return f16 ? (float)reinterpret_cast<const _Float16*>(B)[idx] : reinterpret_cast<const float*>(B)[idx];
 }
 
+// activation k of token m, times kscale[k] when given (one rounding: the transposed product's
+// fl(tau_k * b), equal to the reference's fl(tau_k * trit) * b term by term)
+__device__ __forceinline__ float load_bk(const void* B, const float* kscale, int k, int M, int m, bool f16)
+{
+    const float x = load_b(B, (size_t)k * M + m, f16);
+    return kscale ? __fmul_rn(kscale[k], x) : x;
+}
+
 // One block per token: absmax (and non-finite detection), then the four digit rows. Each thread
 // takes columns k = tid + kDigThreads * (8 i + u), eight independent loads in flight per step.
 constexpr int kDigThreads = 1024;
 constexpr int kDigUnroll = 8;
 
-__global__ __launch_bounds__(kDigThreads) void k_digits(const void* __restrict__ B, bool f16, int K, int M, int Kp,
+__global__ __launch_bounds__(kDigThreads) void k_digits(const void* __restrict__ B, bool f16,
+                                                        const float* __restrict__ kscale, int K, int M, int Kp,
                                                         int8_t* __restrict__ xi, int32_t* __restrict__ rowsum,
                                                         int32_t* __restrict__ ex)
 {
@@ -55,7 +64,7 @@ __global__ __launch_bounds__(kDigThreads) void k_digits(const void* __restrict__
         for (int u = 0; u < kDigUnroll; ++u)
         {
             const int k = k0 + u * kDigThreads;
-            v[u] = k < K ? load_b(B, (size_t)k * M + m, f16) : 0.0f;
+            v[u] = k < K ? load_bk(B, kscale, k, M, m, f16) : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kDigUnroll; ++u)
@@ -93,7 +102,7 @@ __global__ __launch_bounds__(kDigThreads) void k_digits(const void* __restrict__
         for (int u = 0; u < kDigUnroll; ++u)
         {
             const int k = k0 + u * kDigThreads;
-            v[u] = (k < K && !bad) ? load_b(B, (size_t)k * M + m, f16) : 0.0f;
+            v[u] = (k < K && !bad) ? load_bk(B, kscale, k, M, m, f16) : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kDigUnroll; ++u)
@@ -147,14 +156,15 @@ __device__ __forceinline__ int code_at(const uint32_t* rp, int KT, int n, int k)
 __global__ __launch_bounds__(kDigBlock) void k_digit_combine(const float* __restrict__ Yp, const float* __restrict__ tau,
                                                              const int32_t* __restrict__ ex,
                                                              const uint32_t* __restrict__ rp, int KT,
-                                                             const void* __restrict__ B, bool b16, int N, int K, int M,
+                                                             const void* __restrict__ B, bool b16,
+                                                             const float* __restrict__ kscale, int N, int K, int M,
                                                              void* __restrict__ Y, bool y16)
 {
     const size_t idx = (size_t)blockIdx.x * kDigBlock + threadIdx.x;
     if (idx >= (size_t)N * M) return;
     const int n = (int)(idx / M), m = (int)(idx % M);
     const int E = ex[m];
-    const float tn = tau[n];
+    const float tn = tau ? tau[n] : 1.0f;
     float y;
     if (E != kSpecialToken)
     {
@@ -168,7 +178,7 @@ __global__ __launch_bounds__(kDigBlock) void k_digit_combine(const float* __rest
         bool nan = false, pos = false, neg = false;
         for (int k = 0; k < K; ++k)
         {
-            const float x = load_b(B, (size_t)k * M + m, b16);
+            const float x = load_bk(B, kscale, k, M, m, b16);
             if (fabsf(x) <= 3.4028234663852886e38f) continue;
             const float tw = tn * (float)(code_at(rp, KT, n, k) - 2);
             if (x != x || tw != tw || tw == 0.0f)
@@ -188,21 +198,21 @@ __global__ __launch_bounds__(kDigBlock) void k_digit_combine(const float* __rest
 
 }  // namespace
 
-hipError_t launch_digits(hipStream_t st, const void* B, bool b16, size_t K, size_t M, int8_t* xi, int32_t* rowsum,
-                         int32_t* ex)
+hipError_t launch_digits(hipStream_t st, const void* B, bool b16, const float* kscale, size_t K, size_t M, int8_t* xi,
+                         int32_t* rowsum, int32_t* ex)
 {
     const size_t Kp = round_up(K, kTileK);
-    k_digits<<<dim3((unsigned)M), kDigThreads, 0, st>>>(B, b16, (int)K, (int)M, (int)Kp, xi, rowsum, ex);
+    k_digits<<<dim3((unsigned)M), kDigThreads, 0, st>>>(B, b16, kscale, (int)K, (int)M, (int)Kp, xi, rowsum, ex);
     return hipGetLastError();
 }
 
 hipError_t launch_digit_combine(hipStream_t st, const float* Yp, const float* tau, const int32_t* ex,
-                                const uint32_t* rp, const void* B, bool b16, size_t N, size_t K, size_t M, void* Y,
-                                bool y16)
+                                const uint32_t* rp, const void* B, bool b16, const float* kscale, size_t N, size_t K,
+                                size_t M, void* Y, bool y16)
 {
     const size_t n = N * M;
     k_digit_combine<<<dim3((unsigned)ceil_div(n, kDigBlock)), kDigBlock, 0, st>>>(
-        Yp, tau, ex, rp, (int)ceil_div(K, kTileK), B, b16, (int)N, (int)K, (int)M, Y, y16);
+        Yp, tau, ex, rp, (int)ceil_div(K, kTileK), B, b16, kscale, (int)N, (int)K, (int)M, Y, y16);
     return hipGetLastError();
 }
 

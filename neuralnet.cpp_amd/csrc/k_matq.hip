@@ -291,6 +291,14 @@ hipError_t launch_matmul_q(hipStream_t st, const uint32_t* wq, const float* tau,
     return run_mq(st, wq, tau, nullptr, B, b16, N, K, M, Y, y16, plan, part);
 }
 
+hipError_t launch_trit_transpose(hipStream_t st, const uint32_t* A, size_t K, size_t M, uint32_t* At)
+{
+    if (K == 0 || M == 0) return hipSuccess;
+    const dim3 tgrid((unsigned)ceil_div(ceil_div(M, 16), (size_t)kTpWords), (unsigned)ceil_div(K, (size_t)kTpRows));
+    hipLaunchKernelGGL(k_trit_transpose, tgrid, dim3(256), 0, st, A, (int)K, (int)M, At);
+    return hipGetLastError();
+}
+
 hipError_t launch_matmul_q_t(hipStream_t st, const uint32_t* A, const float* tau, const void* B, bool b16, size_t K,
                              size_t M, size_t N, void* Y, bool y16, const MatqPlan& plan, float* scratch)
 {

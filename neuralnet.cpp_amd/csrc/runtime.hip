@@ -654,15 +654,15 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
     return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y);
 }
 
-nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float* tau, const void* B, int b_f16,
-                                    size_t N, size_t K, size_t M, void* Y, int y_f16)
+static nnhip_status matmul_digits(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
+                                  const float* kscale, const void* B, int b_f16, size_t N, size_t K, size_t M, void* Y,
+                                  int y_f16)
 {
-    const char* fn = "nnhip_ternary_matmul_f";
     NNHIP_CHECK_CTX(fn);
     if (N == 0 || M == 0) return NNHIP_OK;
     nnhip_status st = check_matmul_shape(fn, N, K, M);
     if (st != NNHIP_OK) return st;
-    NNHIP_REQUIRE(rp && tau && B && Y, fn, "null pointer");
+    NNHIP_REQUIRE(rp && B && Y, fn, "null pointer");
     NNHIP_REQUIRE(aligned16(rp), fn, "rp must be 16-byte aligned");
     NNHIP_REQUIRE(M <= kMaxDim / 4 && mul_ok(N, 4 * M), fn, "size overflow");
     // the digit products are exact integers in f32 while 128 K < 2^24
@@ -685,11 +685,38 @@ nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float*
     int32_t* rs = reinterpret_cast<int32_t*>(w + b_xi);
     int32_t* ex = reinterpret_cast<int32_t*>(w + b_xi + b_rs);
     float* yp = reinterpret_cast<float*>(w + b_xi + b_rs + b_ex);
-    NNHIP_LAUNCH(fn, launch_digits(ctx->stream, B, b_f16 != 0, K, M, xi, rs, ex));
+    NNHIP_LAUNCH(fn, launch_digits(ctx->stream, B, b_f16 != 0, kscale, K, M, xi, rs, ex));
     st = run_matmul(ctx, fn, rp, ctx->ones, xi, ctx->ones, rs, nullptr, N, K, M4, yp);
     if (st != NNHIP_OK) return st;
-    NNHIP_LAUNCH(fn, launch_digit_combine(ctx->stream, yp, tau, ex, static_cast<const uint32_t*>(rp), B, b_f16 != 0, N,
-                                          K, M, Y, y_f16 != 0));
+    NNHIP_LAUNCH(fn, launch_digit_combine(ctx->stream, yp, tau, ex, static_cast<const uint32_t*>(rp), B, b_f16 != 0,
+                                          kscale, N, K, M, Y, y_f16 != 0));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float* tau, const void* B, int b_f16,
+                                    size_t N, size_t K, size_t M, void* Y, int y_f16)
+{
+    const char* fn = "nnhip_ternary_matmul_f";
+    NNHIP_REQUIRE(tau != nullptr || N == 0 || M == 0, fn, "null tau");
+    return matmul_digits(ctx, fn, rp, tau, nullptr, B, b_f16, N, K, M, Y, y_f16);
+}
+
+nnhip_status nnhip_ternary_matmul_t_f(nnhip_ctx* ctx, const void* rpT, const float* tau, const void* B, int b_f16,
+                                      size_t K, size_t M, size_t N, void* Y, int y_f16)
+{
+    const char* fn = "nnhip_ternary_matmul_t_f";
+    NNHIP_REQUIRE(tau != nullptr || M == 0 || N == 0, fn, "null tau");
+    return matmul_digits(ctx, fn, rpT, nullptr, tau, B, b_f16, M, K, N, Y, y_f16);
+}
+
+nnhip_status nnhip_trit_transpose(nnhip_ctx* ctx, const uint32_t* A, size_t K, size_t M, uint32_t* At)
+{
+    const char* fn = "nnhip_trit_transpose";
+    NNHIP_CHECK_CTX(fn);
+    if (K == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(A && At, fn, "null pointer");
+    NNHIP_REQUIRE(K <= kMaxDim && M <= kMaxDim, fn, "size out of range");
+    NNHIP_LAUNCH(fn, launch_trit_transpose(ctx->stream, A, K, M, At));
     return NNHIP_OK;
 }
 

@@ -206,6 +206,9 @@ protected:
     {
         std::shared_ptr<void> rp;
         std::uint64_t rp_epoch = ~std::uint64_t{0};
+        std::shared_ptr<void> rpt;  // repack of the transposed container (M rows, K columns)
+        std::uint64_t rpt_epoch = ~std::uint64_t{0};
+        std::size_t rpt_m = 0;
         std::shared_ptr<void> glu_rp, glu_tau, glu_bias;
         std::uint64_t glu_epoch = ~std::uint64_t{0}, glu_tau_epoch = 0, glu_bias_epoch = 0;
         const detail::Storage* glu_tau_st = nullptr;
@@ -229,6 +232,24 @@ protected:
         c.rp = *mem;
         c.rp_epoch = wq.write_epoch();
         return static_cast<const void*>(c.rp.get());
+    }
+
+    // T16K256 copy of the transposed container At (M, ceil(K/16)) of A (K, ceil(M/16)), cached
+    // like repacked(): the operand of the transposed product on the MFMA path.
+    Result<const void*> repacked_t(const Tensor& A, std::size_t M)
+    {
+        WeightCache& c = cache_of(A);
+        const std::size_t K = A.rows();
+        if (c.rpt && c.rpt_epoch == A.write_epoch() && c.rpt_m == M) return static_cast<const void*>(c.rpt.get());
+        EX_TRY(at, device_alloc(M * trit_pack::words_per_row(K) * sizeof(uint32_t)));
+        EX_TRY(mem, device_alloc(nnhip_repacked_bytes(M, K)));
+        NNHIP_TRY(nnhip_trit_transpose(ctx_->h, up(A), K, M, static_cast<uint32_t*>(at->get())), "transpose");
+        NNHIP_TRY(nnhip_repack_ternary(ctx_->h, static_cast<const uint32_t*>(at->get()), M, K, mem->get()),
+                  "repack (transposed)");
+        c.rpt = *mem;
+        c.rpt_epoch = A.write_epoch();
+        c.rpt_m = M;
+        return static_cast<const void*>(c.rpt.get());
     }
 
     struct GluWeights
@@ -330,9 +351,19 @@ protected:
         return {};
     }
 
+    // Transposed product (BitLinear's dX): the MFMA path on the cached transposed repack with tau
+    // folded into the activations, up to its K bound; else the reference-layout VALU kernel.
     Result<void> matmul_q_t_impl(const Tensor& A, const Tensor& tau, const Tensor& B, std::size_t M,
                                  const Tensor& y) override
     {
+        const std::size_t K = A.rows(), N = B.cols();
+        if (M == 0 || N == 0) return {};
+        if (K < 131072)
+        {
+            EX_TRY(rpt, repacked_t(A, M));
+            NNHIP_TRY(nnhip_ternary_matmul_t_f(ctx_->h, *rpt, fp(tau), fp(B), 0, K, M, N, fpw(y), 0), "matmul_q_t");
+            return {};
+        }
         NNHIP_TRY(nnhip_matmul_q_t(ctx_->h, up(A), fp(tau), fp(B), 0, A.rows(), M, B.cols(), fpw(y), 0),
                   "matmul_q_t");
         return {};

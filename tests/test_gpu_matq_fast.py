@@ -141,3 +141,96 @@ def test_matmul_f_rejects_large_k(ctx, nnhip):
     B = torch.zeros((131072, 1), device="cuda")
     with pytest.raises(nnhip.NNHipError):
         ctx.ternary_matmul_f(rp, tau, B, 16, 131072)
+
+
+def transposed_case(ctx, orc, K, M, seed):
+    """A container (K, ceil(M/16)) with tau per stored row (BitLinear's W with K = out features,
+    M = in features), its bit transpose and the repack of that."""
+    W = normal((K, M), seed, 0.0, 0.02)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    A = orc.trit_pack(W, tau)
+    At = ctx.trit_transpose(dev(A), M)
+    rpT = ctx.repack(At, K)
+    return A, tau, At, rpT
+
+
+@pytest.mark.parametrize("K,M", [(1, 1), (17, 65), (48, 192), (2560, 6912), (300, 33)])
+def test_trit_transpose_bits(ctx, orc, K, M):
+    """trit (m, k) of the transpose = trit (k, m) of the container; tail codes 2 (trit 0)."""
+    say(f"trit_transpose K={K} M={M}")
+    W = normal((K, M), K + M, 0.0, 0.02)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    A = orc.trit_pack(W, tau)
+    At = ctx.trit_transpose(dev(A), M).cpu().numpy().view(np.uint32)
+    assert At.shape == (M, (K + 15) // 16)
+    codes = lambda P: ((P[:, :, None] >> (2 * np.arange(16, dtype=np.uint32))) & 3).reshape(P.shape[0], -1)
+    ca = codes(A)[:, :M]
+    ct = codes(At)
+    assert np.array_equal(ct[:, :K], ca.T)
+    assert np.all(ct[:, K:] == 2)
+
+
+@pytest.mark.parametrize("K,M,N", [(2560, 6912, 16), (6912, 2560, 4), (2560, 2560, 1), (640, 2560, 7),
+                                   (520, 100, 3), (17, 65, 65), (1000, 300, 40)])
+def test_matmul_t_f_gaussian(ctx, orc, K, M, N):
+    """dX = (tau o trit(W))^T . dY on the transposed repack (src/ternary_gemm_test.cpp:291-334)."""
+    say(f"ternary_matmul_t_f K={K} M={M} N={N}")
+    A, tau, _, rpT = transposed_case(ctx, orc, K, M, seed=K + M + N)
+    B = normal((K, N), 3 + N)
+    B[:, ::3] *= 41.0
+    got = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(B), M))
+    check(got, orc.matmul_q_t(A, tau, B, M), TOL)
+
+
+def test_matmul_t_f_reference_pattern(ctx, orc):
+    """src/ternary_gemm_test.cpp:435-526 patterns with transA (A stored (K, M))."""
+    M, K, N = 192, 48, 320
+    r = np.arange(K)[:, None]
+    c = np.arange(M)[None, :]
+    W = (np.float32(0.17) * ((r * 7 + c * 3) % 13).astype(np.float32) - np.float32(0.9)).astype(np.float32)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    A = orc.trit_pack(W, tau)
+    rpT = ctx.repack(ctx.trit_transpose(dev(A), M), K)
+    k = np.arange(K)[:, None]
+    n = np.arange(N)[None, :]
+    B = (np.float32(0.21) * ((k + 2 * n) % 9).astype(np.float32) - np.float32(0.8)).astype(np.float32)
+    got = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(B), M))
+    check(got, orc.matmul_q_t(A, tau, B, M), TOL)
+
+
+def test_matmul_t_f_half_and_specials(ctx, orc):
+    """f16 activations / outputs, and the IEEE path for non-finite tokens with tau folded in."""
+    import torch
+    K, M, N = 700, 300, 6
+    say("ternary_matmul_t_f f16 and special values")
+    W = normal((K, M), 21, 0.0, 0.02)
+    W[20, ::2] = 1.0
+    W[20, 1::2] = -1.0
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    A = orc.trit_pack(W, tau)
+    tau[10] = 0.0                             # stored row 10 scaled by 0: 0 x inf -> NaN
+    rpT = ctx.repack(ctx.trit_transpose(dev(A), M), K)
+    B = normal((K, N), 22)
+    B[33, 0] = np.nan
+    B[20, 1] = np.inf                         # +-1 column -> +-inf per output row
+    B[10, 2] = -np.inf                        # tau 0 -> NaN for every output row
+    B[:, 3] = 0.0
+    B[:, 4] *= np.float32(1e30)
+    got = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(B), M))
+    ref = orc.matmul_q_t(A, tau, B, M)
+    for n in range(N):
+        check(got[:, n:n + 1], ref[:, n:n + 1], TOL)
+    Bh = B[:, [3, 5]].astype(np.float16).astype(np.float32)
+    got = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(Bh).to(torch.float16), M, out_f16=True))
+    ref = orc.matmul_q_t(A, tau, Bh, M).astype(np.float16).astype(np.float32)
+    check(got, ref, 4e-3)
+
+
+def test_matmul_t_f_agrees_with_valu_kernel(ctx, orc):
+    """MFMA transposed path vs the reference-layout VALU kernel (nnhip_matmul_q_t)."""
+    K, M, N = 2560, 2560, 16
+    A, tau, _, rpT = transposed_case(ctx, orc, K, M, seed=31)
+    B = normal((K, N), 32)
+    a = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(B), M))
+    b = host(ctx.matmul_q_t(dev(A), dev(tau), dev(B), M))
+    assert np.max(np.abs(a - b)) <= 1e-4 * max(1.0, float(np.max(np.abs(b))))
