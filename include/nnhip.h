@@ -62,6 +62,11 @@ const char* nnhip_version(void);
 /* Number of visible HIP devices. */
 nnhip_status nnhip_device_count(int* count);
 
+/* Compute units, peak engine clock (kHz), memory clock (kHz) and memory bus width (bits) of a
+ * device, as HIP reports them: the inputs of the roofline peaks (dense int8 MFMA = CUs x clock x
+ * 8192 ops per clock on gfx950). No reference counterpart (a measurement aid). */
+nnhip_status nnhip_device_info(int device, int* cus, int* clock_khz, int* mem_clock_khz, int* bus_bits);
+
 /* Create a context bound to `device` with its own stream (default priority).
  * Replaces nn::create_gpu_engine(const char* device) (cli/cli_engine_factory.hpp:51-76). */
 nnhip_status nnhip_ctx_create(int device, nnhip_ctx** out);
@@ -253,6 +258,12 @@ nnhip_status nnhip_ternary_matmul_f(nnhip_ctx* ctx, const void* rp, const float*
  * (include/neuralnet.cpp/compute_layer_bitlinear.hpp:494; src/ternary_gemm_test.cpp:291-334). */
 nnhip_status nnhip_ternary_matmul_t_f(nnhip_ctx* ctx, const void* rpT, const float* tau, const void* B, int b_f16,
                                       size_t K, size_t M, size_t N, void* Y, int y_f16);
+
+/* *out ^= the XOR of the bytes / 4 32-bit words at src (bytes a multiple of 4, src 16-byte
+ * aligned), in one streaming pass of non-temporal 16-byte loads; zero *out first for the plain
+ * checksum. A measurement aid with no reference counterpart: its rate is the achievable HBM read
+ * bandwidth that the HBM-bound kernels here are compared with. */
+nnhip_status nnhip_stream_xor(nnhip_ctx* ctx, const void* src, size_t bytes, uint32_t* out);
 
 /* Bit transpose of a packed container: A (K, ceil(M/16)) -> At (M, ceil(K/16)), trit (m, k) of At =
  * trit (k, m) of A, tail codes 2. The load-time step before nnhip_ternary_matmul_t_f (no

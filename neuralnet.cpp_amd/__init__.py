@@ -95,6 +95,8 @@ SIGNATURES = {
     "nnhip_ternary_matmul_f": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_ternary_matmul_t_f": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_trit_transpose": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_stream_xor": (_st, [_vp, _vp, _sz, _vp]),
+    "nnhip_device_info": (_st, [ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 4),
     "nnhip_ternary_matmul_add": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                      ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
@@ -172,6 +174,13 @@ def rope_table(dk: int, max_len: int):
 
 def attention_workspace_bytes(B: int, H: int, Hkv: int, dk: int, len_bound: int) -> int:
     return int(lib().nnhip_attention_workspace_bytes(B, H, Hkv, dk, len_bound))
+
+
+def device_info(device: int = 0) -> dict:
+    """HIP's compute-unit count, peak engine clock, memory clock (kHz) and bus width (bits)."""
+    v = [ctypes.c_int(0) for _ in range(4)]
+    _check(lib().nnhip_device_info(device, *[ctypes.byref(x) for x in v]), "nnhip_device_info")
+    return {"cus": v[0].value, "clock_khz": v[1].value, "mem_clock_khz": v[2].value, "bus_bits": v[3].value}
 
 
 def kp(K: int) -> int:
@@ -464,6 +473,14 @@ class Context:
                                             self._dev(Y, (torch.float32, torch.float16), "Y"), int(out_f16)),
                "nnhip_ternary_matmul_f")
         return Y
+
+    def stream_xor(self, src, out):
+        """out (1 int32 word on the device) ^= xor of src's 32-bit words."""
+        torch = self._torch
+        self._bind_stream()
+        _check(lib().nnhip_stream_xor(self.h, self._dev(src), src.numel() * src.element_size(),
+                                      self._dev(out, torch.int32, "out")), "nnhip_stream_xor")
+        return out
 
     def trit_transpose(self, A, M: int):
         """A (K, ceil(M/16)) packed -> At (M, ceil(K/16))."""

@@ -220,6 +220,11 @@ hipError_t launch_digits(hipStream_t st, const void* B, bool b16, const float* k
 hipError_t launch_digit_combine(hipStream_t st, const float* Yp, const float* tau, const int32_t* ex,
                                 const uint32_t* rp, const void* B, bool b16, const float* kscale, size_t N, size_t K,
                                 size_t M, void* Y, bool y16);
+// *out ^= xor of the bytes / 4 words at src, one streaming pass into stream_xor_blocks()
+// per-block partials, then a one-block fold (k_ref.hip)
+size_t stream_xor_blocks(size_t bytes, int num_cus);
+hipError_t launch_stream_xor(hipStream_t st, const void* src, size_t bytes, uint32_t* part, uint32_t* out,
+                             int num_cus);
 // Bit transpose of a packed container: A (K, ceil(M/16)) -> At (M, ceil(K/16)) (k_matq.hip)
 hipError_t launch_trit_transpose(hipStream_t st, const uint32_t* A, size_t K, size_t M, uint32_t* At);
 

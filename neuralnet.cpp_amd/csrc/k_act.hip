@@ -13,6 +13,9 @@
 //                  keeps them in registers through the three passes (sum of squares, absmax,
 //                  quantize), so X is read from HBM exactly once; parts are whole per thread.
 //                  Codes leave through a 4x4 byte transpose in lane quads as dword stores.
+//   k_token_one    M <= 32, K up to 512 * 22: one token per block, 512 threads, thread t owns
+//                  part t and holds one element per row (decode sizes: the per-token VALU work
+//                  of the 4-token kernel on one CU was its limit).
 //   k_token_wave   larger K, M <= 32: one wave per token, lane l owns parts l + 64q (q = 0..7).
 //   k_token_lanes  larger K, M > 32: 64 tokens per block, re-reads X per pass.
 #include "common.hpp"
@@ -26,6 +29,9 @@ namespace
 
 constexpr int kBlock = 256;
 constexpr int kParts = 512;  // sum-of-squares parts
+#ifndef NNHIP_ONE_TOK_MAX_M
+#define NNHIP_ONE_TOK_MAX_M 32  // largest M for k_token_one
+#endif
 
 __device__ __forceinline__ int quantize_one(float x, float s)
 {
@@ -667,6 +673,133 @@ __global__ __launch_bounds__(kRegWaves * kWave) void k_token_regs(TokArgs a, con
     finish_group<R, kVec, TPB>(x, gm, a, sh, g, w, fl, h, ro);
 }
 
+// Decode-sized M: one token per block, 512 threads. Thread t owns sum-of-squares part t (rows
+// f = t + 512 r, r < R) of token m = blockIdx.x and holds one element per row, so a token's
+// VALU work (the three passes) is spread over M CUs rather than M/4, which is what bounds the
+// 4-token kernel at these sizes (one CU per 4 tokens, ~20 VALU ops per element). Same passes,
+// orders and codes as finish_group: parts summed in ascending f, the tree over the 512 parts in
+// wave 0, fmaxf absmax, the fast / exact quantizer pair.
+constexpr int kOneThreads = 512;
+
+__device__ __forceinline__ float wave_bfly_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+template <int R>
+__global__ __launch_bounds__(kOneThreads) void k_token_one(TokArgs a, const float* __restrict__ gamma)
+{
+    constexpr int NW = kOneThreads / kWave;
+    static_assert(kOneThreads == kParts, "one part per thread");
+    __shared__ float red[kParts];
+    __shared__ float wred[NW];
+    __shared__ int wsum[NW];
+    __shared__ float tok_ri;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int m = blockIdx.x;
+    float x[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+    {
+        const int f = t + kParts * r;
+        x[r] = f < a.K ? a.X[(size_t)f * a.M + m] : 0.0f;
+    }
+    if (a.norm)
+    {
+        float gm[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = t + kParts * r;
+            gm[r] = f < a.K ? gamma[f] : 0.0f;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc = __fadd_rn(acc, __fmul_rn(x[r], x[r]));
+        red[t] = acc;
+        __syncthreads();
+        if (w == 0)
+        {
+            float v[kParts / kWave];
+#pragma unroll
+            for (int k = 0; k < kParts / kWave; ++k) v[k] = red[lane + kWave * k];
+            const float sum = wave_bfly_sum(tree_levels(v));
+            if (lane == 0) tok_ri = rms_inv_of(sum, a.inv_f, a.eps);
+        }
+        __syncthreads();
+        const float ri = tok_ri;
+#pragma unroll
+        for (int r = 0; r < R; ++r) x[r] = __fmul_rn(__fmul_rn(x[r], ri), gm[r]);
+    }
+    if (a.mode == 1)
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = t + kParts * r;
+            if (f < a.K) a.fout[(size_t)f * a.M + m] = x[r];
+        }
+        return;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) mx = fmaxf(mx, fabsf(x[r]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    if (lane == 0) wred[w] = mx;
+    __syncthreads();
+    float tm = wred[0];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) tm = fmaxf(tm, wred[v]);
+    const float sc = __fmul_rn(tm, 1.0f / 127.0f);
+    const float rc = quant_rcp(sc);
+    int q[R];
+    bool amb = isinf(rc);
+#pragma unroll
+    for (int r = 0; r < R; ++r) q[r] = quantize_guess(x[r], rc, amb);
+    if (amb)
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = quantize_fast(x[r], sc, rc);
+    int tsum = 0;
+    const int wpr = (a.M + 3) / 4;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+    {
+        const int f = t + kParts * r;
+        tsum += q[r];  // rows past K hold code 0
+        if (f < a.Kp) a.xi[(size_t)m * a.Kp + f] = (int8_t)q[r];
+        if (a.xq_ref && f < a.K)
+            reinterpret_cast<int8_t*>(a.xq_ref)[((size_t)f * wpr + m / 4) * 4 + m % 4] = (int8_t)q[r];
+    }
+    tsum = wave_sum_i(tsum);
+    if (lane == 0) wsum[w] = tsum;
+    __syncthreads();
+    if (t == 0)
+    {
+        int sum = 0;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) sum += wsum[v];
+        a.s[m] = sc;
+        a.rowsum[m] = sum;
+    }
+}
+
+template <int R>
+void launch_one_r(hipStream_t st, const TokArgs& a, const float* gamma)
+{
+    hipLaunchKernelGGL(k_token_one<R>, dim3((unsigned)a.M), dim3(kOneThreads), 0, st, a, gamma);
+}
+
+template <int... Rs>
+bool launch_one_pick(int rounds, hipStream_t st, const TokArgs& a, const float* gamma)
+{
+    bool done = false;
+    ((done = done || (Rs >= rounds && (launch_one_r<Rs>(st, a, gamma), true))), ...);
+    return done;
+}
+
 // Reference container (K, ceil(M/4)) -> token-major xi + rowsum. One block per token.
 __global__ __launch_bounds__(kBlock) void k_from_container(const uint32_t* __restrict__ xq, size_t K,
                                                            size_t M, size_t Kp,
@@ -820,6 +953,7 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_amax(const float* __res
 }
 
 constexpr size_t kSmallM = 32;
+constexpr size_t kOneTokMaxM = NNHIP_ONE_TOK_MAX_M;
 
 template <int TPB, int R>
 void launch_regs_r(bool vec, hipStream_t st, int n_groups, const TokArgs& a, const float* gamma)
@@ -849,9 +983,15 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
     const size_t Kp = round_up(K, kTileK);
     const int rounds = (int)ceil_div(K, (size_t)512);
     // the register kernel addresses X through one 31-bit buffer range, including the padding
-    // rows of its last round (at most 4096 rows past K). It serves every M up to 22 rounds
-    // (K <= 11264): at decode sizes (M = 16, K = 2560) it takes ~3 us where one wave per token
-    // with strided loads took ~49 us.
+    // rows of its last round (at most 4096 rows past K). It serves every larger M up to 22
+    // rounds (K <= 11264).
+    // decode sizes: one token per block (more CUs share each token group's VALU work)
+    if (M <= kOneTokMaxM && rounds <= 22)
+    {
+        TokArgs a{X, norm, eps, inv_f, (int)K, (int)M, (int)Kp, mode, xi, s, rowsum, xq_ref, fout};
+        if (launch_one_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, gamma))
+            return hipGetLastError();
+    }
     if (rounds <= 22 && (K + 4096) * M * 4 < 0x7FFFFFFFull)
     {
         // rows are read as float4 when every row start is 16-byte aligned

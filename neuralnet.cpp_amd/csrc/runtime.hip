@@ -367,6 +367,43 @@ nnhip_status nnhip_memcpy_d2d(nnhip_ctx* ctx, void* dst, const void* src, size_t
     return copy_sync(ctx, "nnhip_memcpy_d2d", dst, src, bytes, hipMemcpyDeviceToDevice);
 }
 
+nnhip_status nnhip_stream_xor(nnhip_ctx* ctx, const void* src, size_t bytes, uint32_t* out)
+{
+    const char* fn = "nnhip_stream_xor";
+    NNHIP_CHECK_CTX(fn);
+    if (bytes == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(src && out, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(src), fn, "src must be 16-byte aligned");
+    NNHIP_REQUIRE((reinterpret_cast<uintptr_t>(out) & 3u) == 0, fn, "out must be 4-byte aligned");
+    NNHIP_REQUIRE(bytes % 4 == 0, fn, "bytes must be a multiple of 4");
+    nnhip_status st = ensure_ws(ctx, stream_xor_blocks(bytes, ctx->num_cus) * 4, fn);
+    if (st != NNHIP_OK) return st;
+    NNHIP_LAUNCH(fn, launch_stream_xor(ctx->stream, src, bytes, static_cast<uint32_t*>(ctx->ws), out, ctx->num_cus));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_device_info(int device, int* cus, int* clock_khz, int* mem_clock_khz, int* bus_bits)
+{
+    const char* fn = "nnhip_device_info";
+    NNHIP_REQUIRE(cus && clock_khz && mem_clock_khz && bus_bits, fn, "null output");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+    {
+        (void)hipGetLastError();
+        return fail(NNHIP_ERR_NO_DEVICE, fn, "no HIP device visible");
+    }
+    NNHIP_REQUIRE(device >= 0 && device < n, fn, "device index out of range");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(fn, "hipGetDeviceProperties", e);
+    *cus = prop.multiProcessorCount;
+    *clock_khz = prop.clockRate;
+    *mem_clock_khz = prop.memoryClockRate;
+    *bus_bits = prop.memoryBusWidth;
+    return NNHIP_OK;
+}
+
 nnhip_status nnhip_fill_u32(nnhip_ctx* ctx, void* dst, uint32_t value, size_t words)
 {
     const char* fn = "nnhip_fill_u32";

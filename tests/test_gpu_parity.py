@@ -241,6 +241,37 @@ def test_token_kernel_shapes(ctx, orc, K, M, norm):
     check_quant(ctx, orc, X, g)
 
 
+# M <= 32 runs the one-token-per-block kernel (one sum-of-squares part per thread, R rows of
+# 512); K = 11265 is past its largest instantiation (the one-wave-per-token fallback).
+@pytest.mark.parametrize("K,M", [(1, 1), (255, 7), (512, 32), (513, 3), (2560, 16), (6912, 16), (11264, 5),
+                                 (11265, 2)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_token_one_shapes(ctx, orc, K, M, norm):
+    say(f"one-token kernel K={K} M={M} norm={norm}")
+    X = normal((K, M), K * 13 + M, 0.0, 1.0)
+    X.flat[::613] *= 20.0
+    g = normal((K,), K + 9, 1.0, 0.2) if norm else None
+    check_quant(ctx, orc, X, g)
+    if norm:
+        assert np.array_equal(host(ctx.rmsnorm(dev(X), dev(g), 1e-6)), orc.rmsnorm(X, g, 1e-6))
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_token_one_special_values(ctx, orc, norm):
+    """NaN, infinities and all-zero tokens at decode sizes (M = 8)."""
+    say(f"one-token kernel special values norm={norm}")
+    K, M = 2560, 8
+    X = normal((K, M), 99, 0.0, 1.0)
+    X[5, 0] = np.nan
+    X[7, 1] = np.inf
+    X[9, 2] = -np.inf
+    X[:, 3] = 0.0
+    X[:, 4] *= np.float32(1e-30)
+    X[:, 5] *= np.float32(1e30)
+    g = normal((K,), 4, 1.0, 0.2) if norm else None
+    check_quant(ctx, orc, X, g)
+
+
 def test_quant_near_ties(ctx, orc):
     """x / s on and within a few ulps of half-integers: the division-free path must hand these
     to the exact division. Each token holds one 127 (s = fl(127 * fl(1/127))) and values
@@ -256,6 +287,8 @@ def test_quant_near_ties(ctx, orc):
     check_quant(ctx, orc, X)
     # and scaled so that s is far from 1
     check_quant(ctx, orc, (X * np.float32(0.0371)).astype(np.float32))
+    # the same values at decode sizes (one-token kernel)
+    check_quant(ctx, orc, np.ascontiguousarray(X[:, :16]))
 
 
 # ------------------------------------------------------------------ fast-path GEMV / GEMM
@@ -441,3 +474,19 @@ def test_matmul_q_decode_gaussian(ctx, orc):
     got = host(ctx.matmul_q(wq, dev(tau), dev(X), K))
     ref = orc.matmul_q(host(wq, np.uint32), tau, X, K)
     assert np.max(np.abs(got - ref)) <= 1e-4 * max(1.0, np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("nbytes", [4, 12, 16, 20, 4096, 1000004, (64 << 20) + 12])
+def test_stream_xor(ctx, nbytes):
+    """nnhip_stream_xor: out ^= xor of all words (any word count, the 16-byte body and the
+    tail); a second call cancels the first."""
+    import torch
+    print(f"stream_xor bytes={nbytes}", flush=True)
+    words = np.random.default_rng(nbytes).integers(0, 2 ** 32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    src = dev(words)
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx.stream_xor(src, out)
+    got = int(out.cpu().numpy().view(np.uint32)[0])
+    assert got == int(np.bitwise_xor.reduce(words))
+    ctx.stream_xor(src, out)
+    assert int(out.cpu().numpy().view(np.uint32)[0]) == 0
