@@ -40,6 +40,9 @@ namespace
 
 constexpr int kAttnT = 128;        // cache positions per work-group
 constexpr int kAttnThreads = 256;  // 4 waves
+#ifndef NNHIP_ATTN_VEARLY
+#define NNHIP_ATTN_VEARLY 0  // value loads issued together with the key loads
+#endif
 #ifndef NNHIP_ATTN_MINW
 #define NNHIP_ATTN_MINW 4          // waves per SIMD the chunk kernel is compiled for (<= 128 VGPRs)
 #endif
@@ -180,13 +183,31 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             }
         }
 
+        // value-row geometry: VL lanes per row (one float4 each), NG rows per step, VR rows per thread
+        constexpr int VR = kAttnT / NG;
+        const int vg = tid / VL, vi = tid % VL;
+        float4 vv[VR];
+        const __amdgpu_buffer_rsrc_t rv = attn_rsrc(a.vc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
+        auto load_values = [&]() {
+#pragma unroll
+            for (int u = 0; u < VR; ++u)
+            {
+                const int tl = vg + u * NG;
+                const int t = t0 + tl;
+                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
+                vv[u] = ld_f4(rv, row, 16u * vi);
+            }
+        };
+#if NNHIP_ATTN_VEARLY
+        load_values();
+#endif
+
         // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row.
         //      Cached rows come through one buffer resource per (sequence, KV head): lanes past the
         //      chunk or on the new position read zeros without a branch, so every load of a pass
         //      is in flight at once; the new position's key is selected from LDS afterwards.
         const int pg = tid >> 3, j8 = tid & 7;
         const __amdgpu_buffer_rsrc_t rk = attn_rsrc(a.kc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
-        const __amdgpu_buffer_rsrc_t rv = attn_rsrc(a.vc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
 #pragma unroll
         for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
         {
@@ -243,20 +264,11 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         }
         __syncthreads();
 
-        // ---- value rows: VL lanes per row (one float4 each), NG rows per step; the loads of the
-        //      whole chunk (VR rows per thread) are issued before the softmax so its latency
-        //      hides behind them
-        constexpr int VR = kAttnT / NG;
-        const int vg = tid / VL, vi = tid % VL;
-        float4 vv[VR];
-#pragma unroll
-        for (int u = 0; u < VR; ++u)
-        {
-            const int tl = vg + u * NG;
-            const int t = t0 + tl;
-            const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
-            vv[u] = ld_f4(rv, row, 16u * vi);
-        }
+        // ---- value rows of the whole chunk: issued before the softmax so its latency hides
+        //      behind them (or with the keys, NNHIP_ATTN_VEARLY)
+#if !NNHIP_ATTN_VEARLY
+        load_values();
+#endif
 
         // ---- chunk softmax statistics: one wave per head
         for (int r = w; r < R; r += 4)
