@@ -195,6 +195,24 @@ def gemm_lines(ctx, torch, stream, steps, out):
             log(f"GEMM M={M} K={K} N={N}: {t * 1e6:.1f} us, {tops:.1f} TOPS "
                 f"({tops / INT8_PEAK_TOPS:.3f} of int8 MFMA peak)")
             del y
+    # context: the vendor library's dense int8 GEMM on the same shapes (torch._int_mm, int32
+    # out, no ternary unpacking, no epilogue); not part of this library
+    lib_lines = {}
+    for N in (4096, 11008):
+        Bm = torch.randint(-127, 128, (K, N), dtype=torch.int8, device="cuda")
+        for M in (2048, 4096):
+            Am = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
+            try:
+                t, _ = time_launches(torch, stream, lambda: torch._int_mm(Am, Bm), max(10, steps // 2), 5)
+            except RuntimeError as e:  # not every build ships an int8 GEMM
+                lib_lines[f"M={M} K={K} N={N}"] = {"error": str(e)[:80]}
+                continue
+            tops = 2.0 * M * N * K / t / 1e12
+            lib_lines[f"M={M} K={K} N={N}"] = {"TOPS": round(tops, 1), "us": round(t * 1e6, 1),
+                                              "frac_int8_mfma": round(tops / INT8_PEAK_TOPS, 4)}
+        del Bm
+    gemm["torch._int_mm (dense int8, library)"] = lib_lines
+    log(f"torch._int_mm: {lib_lines}")
     out["prefill_gemm"] = gemm
 
 
