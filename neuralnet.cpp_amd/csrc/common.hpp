@@ -32,8 +32,9 @@ constexpr int kGemvMaxM = 16;
 // Decode GEMV geometry shared by the kernels and the host schedule. Two variants:
 //  * LDS: the group's activations are staged in LDS (they fit kGemvLdsBudget), one 16-row
 //    tile per wave item, 3 k-tile stages in flight, 16 waves per CU (M = 1 decode);
-//  * register: activations are loaded with the weights, 4 row tiles per item share them,
-//    4 stages, 8 waves per CU (larger M).
+//  * register: activations are loaded with the weights, 8 row tiles per item share them,
+//    3 stages, 8 waves per CU (larger M). At M = 16 the sweep measured 4505 GB/s with 4 tiles
+//    and 4 stages, 5038 with 8 and 3 (16 tiles: 2038, register-starved).
 // Tuned on MI355X with the 30-layer BitNet-2B sweep (M = 1 and M = 16).
 #ifndef NNHIP_GEMV_LDS_DEPTH
 #define NNHIP_GEMV_LDS_DEPTH 3
@@ -42,10 +43,10 @@ constexpr int kGemvMaxM = 16;
 #define NNHIP_GEMV_LDS_WAVES 16
 #endif
 #ifndef NNHIP_GEMV_REG_RTW
-#define NNHIP_GEMV_REG_RTW 4
+#define NNHIP_GEMV_REG_RTW 8
 #endif
 #ifndef NNHIP_GEMV_REG_DEPTH
-#define NNHIP_GEMV_REG_DEPTH 4
+#define NNHIP_GEMV_REG_DEPTH 3
 #endif
 #ifndef NNHIP_GEMV_REG_WAVES
 #define NNHIP_GEMV_REG_WAVES 8
