@@ -47,7 +47,8 @@ constexpr int kAttnThreads = 256;  // 4 waves
 #define NNHIP_ATTN_MINW 4          // waves per SIMD the chunk kernel is compiled for (<= 128 VGPRs)
 #endif
 #ifndef NNHIP_ATTN_PB
-#define NNHIP_ATTN_PB 4            // score passes (32 positions each) whose loads are in flight together
+#define NNHIP_ATTN_PB 2            // score passes (32 positions each) whose loads are in flight together
+                                   // (2: 136.0 us at 16 x 8192 positions, 4: 141.6; equal at 2112)
 #endif
 constexpr int kRecPad = 16;        // record tail: max[8], sum[8]
 
