@@ -13,7 +13,7 @@
 //                  keeps them in registers through the three passes (sum of squares, absmax,
 //                  quantize), so X is read from HBM exactly once; parts are whole per thread.
 //                  Codes leave through a 4x4 byte transpose in lane quads as dword stores.
-//   k_token_one    M <= 32, K up to 512 * 22: one token per block, 512 threads, thread t owns
+//   k_token_one    M <= 64, K up to 512 * 22: one token per block, 512 threads, thread t owns
 //                  part t and holds one element per row (decode sizes: the per-token VALU work
 //                  of the 4-token kernel on one CU was its limit).
 //   k_token_wave   larger K, M <= 32: one wave per token, lane l owns parts l + 64q (q = 0..7).
@@ -30,7 +30,8 @@ namespace
 constexpr int kBlock = 256;
 constexpr int kParts = 512;  // sum-of-squares parts
 #ifndef NNHIP_ONE_TOK_MAX_M
-#define NNHIP_ONE_TOK_MAX_M 32  // largest M for k_token_one
+#define NNHIP_ONE_TOK_MAX_M 64  // largest M for k_token_one (K=6912, M=64: 6.8 us per call, the
+                                // 4-token kernel 11.0; equal at K=2560)
 #endif
 
 __device__ __forceinline__ int quantize_one(float x, float s)
@@ -673,7 +674,7 @@ __global__ __launch_bounds__(kRegWaves * kWave) void k_token_regs(TokArgs a, con
     finish_group<R, kVec, TPB>(x, gm, a, sh, g, w, fl, h, ro);
 }
 
-// Decode-sized M: one token per block, 512 threads. Thread t owns sum-of-squares part t (rows
+// Decode-sized M (up to 64 tokens): one token per block, 512 threads. Thread t owns sum-of-squares part t (rows
 // f = t + 512 r, r < R) of token m = blockIdx.x and holds one element per row, so a token's
 // VALU work (the three passes) is spread over M CUs rather than M/4, which is what bounds the
 // 4-token kernel at these sizes (one CU per 4 tokens, ~20 VALU ops per element). Same passes,

@@ -228,8 +228,9 @@ def check_quant(ctx, orc, X, g=None, eps=1e-6):
     assert np.array_equal(host(rs), q.astype(np.int64).sum(axis=1))
 
 
-# M > 32 runs the register-resident kernel (rounds of 512 rows, 4 tokens per block; M % 4 != 0
-# takes the scalar-load path); K = 11264 is its largest instantiation, K = 11265 the fallback.
+# M > 64 runs the register-resident kernel (rounds of 512 rows, 4 tokens per block; M % 4 != 0
+# takes the scalar-load path), M <= 64 the one-token kernel; K = 11264 is the largest
+# instantiation of both, K = 11265 the fallback.
 @pytest.mark.parametrize("K,M", [(1, 36), (255, 37), (512, 40), (513, 128), (1000, 66), (2560, 2048),
                                  (4096, 2048), (6912, 132), (11264, 40), (11265, 36)])
 @pytest.mark.parametrize("norm", [False, True])
@@ -241,7 +242,7 @@ def test_token_kernel_shapes(ctx, orc, K, M, norm):
     check_quant(ctx, orc, X, g)
 
 
-# M <= 32 runs the one-token-per-block kernel (one sum-of-squares part per thread, R rows of
+# M <= 64 runs the one-token-per-block kernel (one sum-of-squares part per thread, R rows of
 # 512); K = 11265 is past its largest instantiation (the one-wave-per-token fallback).
 @pytest.mark.parametrize("K,M", [(1, 1), (255, 7), (512, 32), (513, 3), (2560, 16), (6912, 16), (11264, 5),
                                  (11265, 2)])
