@@ -106,6 +106,7 @@ SIGNATURES = {
     "nnhip_group_run": (_st, [_vp, _vp]),
     "nnhip_group_destroy": (_st, [_vp, _vp]),
     "nnhip_gemv_grid_waves": (_sz, [_vp, _sz]),
+    "nnhip_group_info": (_st, [_vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "nnhip_glu": (_st, [_vp, _vp, _sz, _sz, ctypes.c_int, _vp]),
     "nnhip_glu_rows": (_sz, [_sz]),
     "nnhip_glu_interleave": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
@@ -679,6 +680,12 @@ class Context:
     def group_destroy(self, h) -> None:
         self._bind_stream()
         _check(lib().nnhip_group_destroy(self.h, h), "nnhip_group_destroy")
+
+    def group_info(self, h) -> dict:
+        """The variant nnhip_group_create chose: {"lds": bool, "waves": int, "lds_bytes": int}."""
+        v, w, b = ctypes.c_int(0), _sz(0), _sz(0)
+        _check(lib().nnhip_group_info(h, ctypes.byref(v), ctypes.byref(w), ctypes.byref(b)), "nnhip_group_info")
+        return {"lds": bool(v.value), "waves": int(w.value), "lds_bytes": int(b.value)}
 
     def gemv_grid_waves(self, items: int) -> int:
         return int(lib().nnhip_gemv_grid_waves(self.h, items))

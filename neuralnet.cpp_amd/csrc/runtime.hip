@@ -990,6 +990,16 @@ nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group)
     return NNHIP_OK;
 }
 
+nnhip_status nnhip_group_info(const nnhip_group* group, int* lds_variant, size_t* waves, size_t* lds_bytes)
+{
+    const char* fn = "nnhip_group_info";
+    NNHIP_REQUIRE(group != nullptr, fn, "null group");
+    if (lds_variant) *lds_variant = group->n_xstage > 0 ? 1 : 0;
+    if (waves) *waves = group->n_waves;
+    if (lds_bytes) *lds_bytes = group->lds_bytes;
+    return NNHIP_OK;
+}
+
 size_t nnhip_gemv_grid_waves(nnhip_ctx* ctx, size_t items)
 {
     return gemv_grid_waves(items, ctx ? ctx->num_cus : 256, true);

@@ -332,20 +332,64 @@ def test_decode_gemv_deep(ctx, orc, N, K, M, bias):
     assert np.array_equal(Y, ref)
 
 
+def c3_case(ctx, orc, N, K, M, seed):
+    """Config 2 inputs at full size: W ~ N(0, 0.02) ternarized by per-tensor absmean on the GPU
+    (trit_pack is checked bit for bit elsewhere; the oracle reads the same container), X ~ N(0, 1)
+    with 0.1% of the elements at 20x, quantized per token by the GPU and by the oracle."""
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    W = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+    tau_d = W.abs().double().mean().float().expand(N).contiguous()
+    wq_d = ctx.trit_pack(W, tau_d)
+    del W
+    rp = ctx.repack(wq_d, K)
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((K, M), dtype=np.float32)
+    idx = rng.choice(K * M, size=max(1, K * M // 1000), replace=False)
+    X.flat[idx] *= np.float32(20.0)
+    xi, s_d, rs = ctx.act_quant_i8(dev(X))
+    s = orc.act_scale(X)
+    assert np.array_equal(host(s_d), s)
+    xq = orc.quantize_i8(X, s, True)
+    return host(wq_d, np.uint32), host(tau_d), xq, s, rp, tau_d, xi, s_d, rs
+
+
 @pytest.mark.parametrize("N,K,M", [(4096, 4096, 256), (11008, 4096, 1024), (4096, 4096, 2048),
+                                   (11008, 4096, 2048), (4096, 4096, 4096), (11008, 4096, 4096),
                                    (2560, 2560, 100)])
 def test_prefill_gemm_shapes(ctx, orc, N, K, M):
-    """BASELINE config 2 shapes, 0.1% activation outliers at 20x; oracle on sampled rows."""
+    """BASELINE config 2 (K=4096, N in {4096, 11008}, M up to 4096; 0.1% activation outliers at 20x):
+    every row of Y bit for bit against the oracle's CpuEngine restatement (row-block decode + dense
+    f32 microkernel, exact because every partial sum is an integer below 2^24), the check of
+    src/int8_act_test.cpp:171-238."""
     say(f"gemm N={N} K={K} M={M}")
-    tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, 5 + M, outliers=True)
-    Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M))
-    rows = np.unique(np.concatenate([np.arange(0, N, max(1, N // 48)), [N - 1]]))
-    ref = orc.matmul_q_i8_rowblock(wq[rows], tau[rows], xq, s, K, M)
-    assert np.array_equal(Y[rows], ref)
-    # size-independent property on every row: Y / (tau*s) is an integer accumulator
-    ts = (tau[:, None] * s[None, :]).astype(np.float32)
-    acc = Y / ts
-    assert np.all(np.abs(acc - np.rint(acc)) < 1e-3 * np.maximum(1, np.abs(acc)))
+    wq, tau, xq, s, rp, tau_d, xi, s_d, rs = c3_case(ctx, orc, N, K, M, 5 + M + N)
+    Y = host(ctx.ternary_matmul(rp, tau_d, xi, s_d, rs, N, K, M))
+    ref = orc.matmul_q_i8_rowblock(wq, tau, xq, s, K, M)
+    bad = Y != ref
+    assert not bad.any(), f"{int(bad.sum())} of {Y.size} outputs differ, first at {np.argwhere(bad)[0]}"
+
+
+@pytest.mark.parametrize("N,K,M", [(11008, 4096, 4096), (4096, 4096, 2048)])
+def test_prefill_gemm_unit_scales_sums(ctx, orc, N, K, M):
+    """Size-independent exact identities with tau = 1 and s = 1 (then Y = float(acc) exactly, since
+    |acc| <= 127 K < 2^24): for every token m, sum_n Y[n, m] = sum_k (sum_n trit[n, k]) q[k, m], and for
+    every row n, sum_m Y[n, m] = sum_k trit[n, k] (sum_m q[k, m]), in int64 on the host. A dropped or
+    repeated k tile, row tile or token block changes one of the two."""
+    import torch
+    say(f"gemm unit-scale sums N={N} K={K} M={M}")
+    wq, _, xq, _, rp, _, xi, _, rs = c3_case(ctx, orc, N, K, M, 77 + M + N)
+    ones_n = torch.ones(N, dtype=torch.float32, device="cuda")
+    ones_m = torch.ones(M, dtype=torch.float32, device="cuda")
+    Y = host(ctx.ternary_matmul(rp, ones_n, xi, ones_m, rs, N, K, M)).astype(np.float64)
+    assert np.array_equal(Y, np.rint(Y))
+    t = orc.trits_of(wq, K).astype(np.int64)                                    # (N, K)
+    q = xq.view(np.int8).reshape(K, -1)[:, :M].astype(np.int64)                # (K, M)
+    col = t.sum(axis=0) @ q                                                     # (M,)
+    row = t @ q.sum(axis=1)                                                     # (N,)
+    assert np.array_equal(Y.sum(axis=0).astype(np.int64), col)
+    assert np.array_equal(Y.sum(axis=1).astype(np.int64), row)
 
 
 @pytest.mark.parametrize("tile", [1, 2, 3])
@@ -393,6 +437,78 @@ def test_grouped_gemv_matches_single(ctx, orc):
     for p, ref in zip(probs, singles):
         assert np.array_equal(host(p["y"]), ref)
     ctx.group_destroy(h)
+
+
+STACK_SHAPES = [("q", 2560, 2560), ("k", 2560, 640), ("v", 2560, 640), ("o", 2560, 2560),
+                ("gate", 2560, 6912), ("up", 2560, 6912), ("down", 6912, 2560)]   # (name, K, N)
+
+
+def stack_group(ctx, orc, layers, M, seed, bias_layer=-1):
+    """A reduced-depth copy of bench.py's headline group: `layers` x the seven BitNet-2B shapes,
+    weights N(0, 0.02) ternarized by per-tensor absmean on the GPU (trit_pack is checked bit for
+    bit elsewhere; the oracle below reads the same containers), one quantized activation block
+    per K shared by every problem of that K. Returns the problems and their host operands."""
+    import torch
+    gen = torch.Generator(device="cuda")
+    acts = {}
+    for K in (2560, 6912):
+        X = normal((K, M), seed + K)
+        xi, s_d, rs = ctx.act_quant_i8(dev(X))
+        s = orc.act_scale(X)
+        assert np.array_equal(host(s_d), s)
+        acts[K] = (xi, s_d, rs, orc.quantize_i8(X, s, True), s)
+    probs, hosts = [], []
+    for layer in range(layers):
+        for idx, (name, K, N) in enumerate(STACK_SHAPES):
+            gen.manual_seed(seed * 131 + layer * 16 + idx)
+            W = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+            tau = W.abs().double().mean().float().expand(N).contiguous()
+            wq = ctx.trit_pack(W, tau)
+            rp = ctx.repack(wq, K)
+            del W
+            xi, s_d, rs, xq, s = acts[K]
+            b = normal((N,), seed + 7 * layer + idx) if layer == bias_layer else None
+            y = torch.full((N, M), float("nan"), dtype=torch.float32, device="cuda")
+            probs.append(dict(rp=rp, tau=tau, xi=xi, s=s_d, rowsum=rs, bias=dev(b) if b is not None else None,
+                              y=y, N=N, K=K, M=M))
+            hosts.append((host(wq, np.uint32), host(tau), xq, s, b, name, layer))
+    return probs, hosts
+
+
+def check_stack_group(ctx, orc, probs, hosts, expect_lds):
+    h = ctx.group_create(probs)
+    try:
+        info = ctx.group_info(h)
+        assert info["lds"] == expect_lds, info
+        for _ in range(3):   # repeated runs rewrite the same bits
+            ctx.group_run(h)
+        ctx.sync()
+    finally:
+        ctx.group_destroy(h)
+    for p, (wq, tau, xq, s, b, name, layer) in zip(probs, hosts):
+        ref = orc.matmul_q_i8_rowblock(wq, tau, xq, s, p["K"], p["M"])
+        if b is not None:
+            ref = orc.add_row_broadcast(ref, b)
+        Y = host(p["y"])
+        assert np.array_equal(Y, ref), f"layer {layer} {name}: {int(np.sum(Y != ref))} of {Y.size} differ"
+
+
+def test_grouped_gemv_headline_group_lds(ctx, orc):
+    """The benchmarked launch: bench.py's M=1 layer-stack group (here 3 layers x q/k/v/o/gate/up/down,
+    activations shared per K, so they fit the LDS budget and the LDS variant runs), every output row
+    of every problem bit for bit against the oracle's CpuEngine restatement; layer 1 carries a bias.
+    Mirrors the int32 + epilogue check of src/int8_act_test.cpp:210-236."""
+    say("grouped gemv: headline group (LDS variant), 3 layers x 7 shapes, M=1")
+    probs, hosts = stack_group(ctx, orc, 3, 1, 0xA1, bias_layer=1)
+    check_stack_group(ctx, orc, probs, hosts, expect_lds=True)
+
+
+def test_grouped_gemv_m16_group_register(ctx, orc):
+    """bench.py's M=16 sweep group (2 layers x 7 shapes): its activations exceed the LDS budget, so
+    the register variant runs; every row of every problem bit for bit against the oracle."""
+    say("grouped gemv: M=16 group (register variant), 2 layers x 7 shapes")
+    probs, hosts = stack_group(ctx, orc, 2, 16, 0xA2, bias_layer=0)
+    check_stack_group(ctx, orc, probs, hosts, expect_lds=False)
 
 
 def test_invalid_arguments_raise(ctx, nnhip):
