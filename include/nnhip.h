@@ -159,6 +159,21 @@ nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* 
                                const uint32_t* xq, const float* s, size_t N, size_t K, size_t M,
                                float* Y);
 
+/* nnhip_matmul_q_i8 without any device allocation: the same operands, kernels and bits, with the
+ * repacked weights and transposed activations kept in a scratch array that the library holds on
+ * each GPU from the first context created on it until the process ends
+ * (NNHIP_NOALLOC_SCRATCH_BYTES). A call needs round_up(nnhip_repacked_bytes(N, K), 256) +
+ * round_up(nnhip_act_i8_bytes(K, M), 256) + round_up(4 M, 256) bytes of it (e.g. N = 11008,
+ * K = 4096, M = 4096 fits); larger calls fail with NNHIP_ERR_UNSUPPORTED before any work is queued.
+ * Calls no hipMalloc / hipFree. Every call on one GPU shares that GPU's scratch, whichever context
+ * it comes from: calls that overlap in time on one GPU (other streams, other threads) race.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation). */
+#define NNHIP_NOALLOC_SCRATCH_BYTES (32u << 20)
+nnhip_status nnhip_matmul_q_i8_noalloc(nnhip_ctx* ctx, const uint32_t* wq, const float* tau,
+                                       const uint32_t* xq, const float* s, size_t N, size_t K,
+                                       size_t M, float* Y);
+
 /* Y (N, M) = (tau o trit(wq)) . B: ternary weights times float activations with f32
  * accumulation; B (K, M) and Y (N, M) are f32, or f16 when b_f16 / y_f16 != 0 (16-bit IEEE
  * halves, round to nearest even on output). Accumulation order is not pinned by the reference;

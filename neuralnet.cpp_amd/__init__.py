@@ -79,6 +79,7 @@ SIGNATURES = {
     "nnhip_quantize_i8": (_st, [_vp, _vp, _vp, _sz, _sz, ctypes.c_int, _vp]),
     "nnhip_unpack_i8": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_matmul_q_i8": (_st, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_matmul_q_i8_noalloc": (_st, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_add_row_broadcast": (_st, [_vp, _vp, _vp, _sz, _sz]),
     "nnhip_matmul_q": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_matmul_q_t": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
@@ -323,6 +324,22 @@ class Context:
                                        self._dev(s, torch.float32, "s"), N, K, M, self._dev(Y)),
                "nnhip_matmul_q_i8")
         return Y
+
+    def matmul_q_i8_noalloc(self, wq, tau, xq, s, K: int, M: int, out):
+        """nnhip_matmul_q_i8 with the library's static per-GPU scratch (no device allocation);
+        `out` (N, M) float32 is required, so the call allocates nothing on the device."""
+        torch = self._torch
+        N = wq.shape[0]
+        if tuple(out.shape) != (N, M):
+            raise NNHipError(1, f"out has shape {tuple(out.shape)}, expected {(N, M)}")
+        self._bind_stream()
+        _check(lib().nnhip_matmul_q_i8_noalloc(self.h, self._dev(wq, torch.int32, "wq"),
+                                               self._dev(tau, torch.float32, "tau"),
+                                               self._dev(xq, torch.int32, "xq"),
+                                               self._dev(s, torch.float32, "s"), N, K, M,
+                                               self._dev(out, torch.float32, "out")),
+               "nnhip_matmul_q_i8_noalloc")
+        return out
 
     def matmul_q(self, wq, tau, B, K: int, out_f16: bool = False, out=None):
         """Y (N, M) = (tau o trit(wq)) . B; B f32 or f16 (K, M); Y f32, or f16 if out_f16."""

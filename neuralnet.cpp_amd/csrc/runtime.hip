@@ -10,15 +10,23 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <queue>
 #include <string>
 #include <vector>
 
 using namespace nnhip;
 
+// Scratch of nnhip_matmul_q_i8_noalloc (repacked weights, token-major activations, row sums):
+// one copy per GPU, loaded with the code object and held until the process ends. In host code
+// the name is only a stand-in for the symbol: its device address comes from
+// hipGetSymbolAddress (g_scratch_dev below), never from taking the array's address here.
+static __device__ __align__(256) uint8_t scratch[NNHIP_NOALLOC_SCRATCH_BYTES];
+
 struct nnhip_ctx
 {
     int device = 0;
+    void* scratch = nullptr;  // this device's copy of `scratch` (device address)
     int num_cus = 256;
     hipStream_t own = nullptr;
     hipStream_t stream = nullptr;
@@ -61,6 +69,31 @@ nnhip_status fail(nnhip_status st, const char* fn, const std::string& msg)
 nnhip_status hip_fail(const char* fn, const char* what, hipError_t e)
 {
     return fail(NNHIP_ERR_HIP, fn, std::string(what) + " failed: " + hipGetErrorString(e));
+}
+
+// Device address of `scratch` on each device, resolved once per device by the first context
+// created on it (with that device current).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+nnhip_status resolve_scratch(int device, void** out, const char* fn)
+{
+    if (device < 0 || device >= kMaxDevices) return fail(NNHIP_ERR_UNSUPPORTED, fn, "device index beyond 63");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[device])
+    {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+        {
+            (void)hipGetLastError();
+            return hip_fail(fn, "hipGetSymbolAddress(scratch)", e);
+        }
+        g_scratch_dev[device] = ptr;
+    }
+    *out = g_scratch_dev[device];
+    return NNHIP_OK;
 }
 
 #define NNHIP_CHECK_CTX(fn)                                                  \
@@ -241,8 +274,12 @@ nnhip_status nnhip_ctx_create(int device, nnhip_ctx** out)
                     std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950 only");
     e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(fn, "hipSetDevice", e);
+    void* scr = nullptr;
+    const nnhip_status sst = resolve_scratch(device, &scr, fn);
+    if (sst != NNHIP_OK) return sst;
     auto* ctx = new nnhip_ctx;
     ctx->device = device;
+    ctx->scratch = scr;
     ctx->num_cus = prop.multiProcessorCount;
     e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
     if (e != hipSuccess)
@@ -521,6 +558,37 @@ nnhip_status nnhip_matmul_q_i8(nnhip_ctx* ctx, const uint32_t* wq, const float* 
     st = ensure_ws(ctx, rp_bytes + xi_bytes + rs_bytes, fn);
     if (st != NNHIP_OK) return st;
     uint8_t* base = static_cast<uint8_t*>(ctx->ws);
+    uint32_t* rp = reinterpret_cast<uint32_t*>(base);
+    int8_t* xi = reinterpret_cast<int8_t*>(base + rp_bytes);
+    int32_t* rowsum = reinterpret_cast<int32_t*>(base + rp_bytes + xi_bytes);
+    NNHIP_LAUNCH(fn, launch_repack(ctx->stream, wq, N, K, rp));
+    NNHIP_LAUNCH(fn, launch_act_from_container(ctx->stream, xq, K, M, xi, rowsum));
+    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, nullptr, N, K, M, Y);
+}
+
+nnhip_status nnhip_matmul_q_i8_noalloc(nnhip_ctx* ctx, const uint32_t* wq, const float* tau, const uint32_t* xq,
+                                       const float* s, size_t N, size_t K, size_t M, float* Y)
+{
+    const char* fn = "nnhip_matmul_q_i8_noalloc";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(wq && tau && xq && s && Y, fn, "null pointer");
+    NNHIP_REQUIRE(ctx->scratch != nullptr, fn, "scratch address not resolved");
+    // the same split of the scratch as nnhip_matmul_q_i8's workspace
+    const size_t rp_bytes = round_up(nnhip_repacked_bytes(N, K), 256);
+    const size_t xi_bytes = round_up(nnhip_act_i8_bytes(K, M), 256);
+    const size_t rs_bytes = round_up(M * sizeof(int32_t), 256);
+    const size_t need = rp_bytes + xi_bytes + rs_bytes;
+    if (need > (size_t)NNHIP_NOALLOC_SCRATCH_BYTES)
+        return fail(NNHIP_ERR_UNSUPPORTED, fn,
+                    "needs " + std::to_string(need) + " bytes of scratch (repacked weights " + std::to_string(rp_bytes) +
+                        " + activations " + std::to_string(xi_bytes + rs_bytes) + "), more than the " +
+                        std::to_string((size_t)NNHIP_NOALLOC_SCRATCH_BYTES) + " bytes this entry point has");
+    // every byte used below is written by the repack / transpose before the product reads it
+    // (pad codes and zero pad included), so the previous call's contents need no clearing
+    uint8_t* base = static_cast<uint8_t*>(ctx->scratch);
     uint32_t* rp = reinterpret_cast<uint32_t*>(base);
     int8_t* xi = reinterpret_cast<int8_t*>(base + rp_bytes);
     int32_t* rowsum = reinterpret_cast<int32_t*>(base + rp_bytes + xi_bytes);
