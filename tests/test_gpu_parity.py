@@ -394,11 +394,14 @@ def test_prefill_gemm_unit_scales_sums(ctx, orc, N, K, M):
 
 @pytest.mark.parametrize("tile", [1, 2, 3])
 @pytest.mark.parametrize("N,K,M", [(300, 520, 200), (130, 300, 130), (64, 256, 17), (1000, 2560, 96),
-                                   (4096, 4096, 256)])
+                                   (4096, 4096, 256), (30000, 520, 300), (11008, 1024, 1024),
+                                   (4100, 768, 2056)])
 def test_prefill_gemm_each_tile(ctx, orc, tile, N, K, M):
     """Every block tile of the prefill GEMM (256x128, 128x128, 64x64) forced on shapes with
-    tails in N, M and K, with a bias: bit-exact against the oracle (sampled rows for the
-    largest shape)."""
+    tails in N, M and K, with a bias: bit-exact against the oracle (every row below 2e10
+    multiply-adds, sampled rows above). (30000, 520, 300), (11008, 1024, 1024) and (4100, 768, 2056)
+    run several block rounds, with and without the XCD-aware block order, odd k-tile counts and
+    edge blocks."""
     say(f"gemm tile={tile} N={N} K={K} M={M}")
     tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, 17 + N + M, outliers=True)
     b = normal((N,), 98)
@@ -407,7 +410,7 @@ def test_prefill_gemm_each_tile(ctx, orc, tile, N, K, M):
         Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M, bias=dev(b)))
     finally:
         ctx.set_gemm_tile(0)
-    rows = np.arange(N) if N * M <= 300 * 300 else np.unique(np.concatenate([np.arange(0, N, 61), [N - 1]]))
+    rows = np.arange(N) if N * M * K <= 2e10 else np.unique(np.concatenate([np.arange(0, N, 61), [N - 1]]))
     ref = orc.add_row_broadcast(orc.matmul_q_i8_rowblock(wq[rows], tau[rows], xq, s, K, M), b[rows])
     assert np.array_equal(Y[rows], ref)
 
