@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA (5.0 POP/s)
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 LAYERS = 30
 D, FFN, KV = 2560, 6912, 640
 SHAPES = [("q", D, D), ("k", D, KV), ("v", D, KV), ("o", D, D),
@@ -68,7 +69,6 @@ class Weights:
 
     def __init__(self, ctx, torch, layers):
         self.mats = []   # (layer, name, K, N, rp, tau)
-        self.ref0 = {}   # layer-0 reference containers, for the CPU baseline
         gen = torch.Generator(device="cuda")
         for layer in range(layers):
             for idx, (name, K, N) in enumerate(SHAPES):
@@ -77,8 +77,6 @@ class Weights:
                 tau = W.abs().double().mean().float().expand(N).contiguous()   # per-tensor absmean
                 wq = ctx.trit_pack(W, tau)
                 rp = ctx.repack(wq, K)
-                if layer == 0:
-                    self.ref0[name] = (wq.cpu().numpy().view(np.uint32), tau.cpu().numpy())
                 del W, wq
                 self.mats.append((layer, name, K, N, rp, tau))
         torch.cuda.synchronize()
@@ -192,6 +190,8 @@ def gemm_lines(ctx, torch, stream, steps, out):
             tops = 2.0 * M * N * K / t / 1e12
             gemm[f"M={M} K={K} N={N}"] = {"TOPS": round(tops, 1), "us": round(t * 1e6, 1),
                                           "frac_int8_mfma": round(tops / INT8_PEAK_TOPS, 4)}
+            if M == 2048:
+                gemm[f"M={M} K={K} N={N}"]["hash"] = load_pkg().fnv1a64(y)
             log(f"GEMM M={M} K={K} N={N}: {t * 1e6:.1f} us, {tops:.1f} TOPS "
                 f"({tops / INT8_PEAK_TOPS:.3f} of int8 MFMA peak)")
             del y
@@ -340,13 +340,16 @@ def matmul_q_lines(ctx, torch, stream, steps, out):
 
 
 def decode_c5_line(ctx, torch, stream, steps, out):
-    """Config C5's decode: a 30-layer BitNet-b1.58 GPT (d=2560, 20 heads / 5 KV heads of 128,
-    SwiGLU FFN 6912 with SubLN, vocab 10000, BitLinear LM head) generating 128 greedy tokens for
-    16 sequences after a 2048-token context. The context's KV cache is synthetic (random keys and
-    values at positions 0..2047, as if prefilled); every step runs the whole model on the GPU
-    (embedding, 30 blocks, final norm, head, greedy argmax) and feeds its ids and positions to the
-    next step. The step is captured once in a graph and replayed 128 times. Also timed: the same
-    step issued eagerly, and one layer's attention call alone against HBM bandwidth."""
+    """Config C5: a 30-layer BitNet-b1.58 GPT (d=2560, 20 heads / 5 KV heads of 128, SwiGLU FFN 6912
+    with SubLN, vocab 10000, BitLinear LM head), random init, 16 sequences: prefill 2048 random prompt
+    tokens per sequence, then 128 greedy decode steps. The prefill is one Decoder.prefill pass (the
+    32768 prompt tokens through every block on the prefill GEMM, nnhip_kv_cache_fill and the causal
+    nnhip_attention_prefill; the reference runs one forward_step per prompt token,
+    compute_layer_gpt.hpp:774-794); it fills the KV caches and picks each sequence's first new token.
+    The decode steps continue from those caches and tokens: the step is captured once in a graph and
+    replayed 128 times. Reported separately: prefill time and tokens/s, decode ms per step and
+    tokens/s, the end-to-end time, one layer's prefill attention against the fp32 MFMA peak, and one
+    layer's decode attention call against HBM bandwidth."""
     nn = load_pkg()
     from nnhip_py import decoder as dm
     L, d, H, Hkv, F, V, B, ctx_len, new = 30, D, 20, 5, FFN, 10000, 16, 2048, 128
@@ -382,10 +385,17 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     head = dm.Linear(ctx.repack(hq, d), ht, None, V, d)
     wbytes += V * d // 4
     emb = torch.randn((V, d), generator=gen, device="cuda")
-    caches = [(torch.randn((B, max_len, Hkv * dk), generator=gen, device="cuda"),
-               torch.randn((B, max_len, Hkv * dk), generator=gen, device="cuda")) for _ in range(L)]
-    dec = dm.Decoder(ctx, cfg, blocks, emb, ones_d, head, B, caches=caches)
-    ids = torch.randint(0, V, (B,), generator=gen, device="cuda", dtype=torch.int32)
+    dec = dm.Decoder(ctx, cfg, blocks, emb, ones_d, head, B)
+    prompt = torch.randint(0, V, (B * ctx_len,), generator=gen, device="cuda", dtype=torch.int32)
+
+    # ---- prefill: 2048 prompt tokens per sequence in one pass (repeatable: it rewrites rows 0..2047)
+    dec.prefill(prompt, ctx_len)                    # warm-up: the prefill scratch is allocated here
+    torch.cuda.synchronize()
+    n_pf = 3
+    t_prefill, _ = time_launches(torch, stream, lambda: dec.prefill(prompt, ctx_len), n_pf, 0)
+    first_ids = dec.ids.clone()
+    prefill_hash = nn.fnv1a64(dec.logits)
+    ids = first_ids.clone()
     pos = torch.full((B,), ctx_len, device="cuda", dtype=torch.int32)
 
     def one_step():
@@ -399,6 +409,8 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         one_step()
+    # decode from the prefilled state: the first new token and position 2048
+    ids.copy_(first_ids)
     pos.fill_(ctx_len)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -409,27 +421,42 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     torch.cuda.synchronize()
     t_step = start.elapsed_time(end) / new / 1e3
     assert int(pos[0].item()) == ctx_len + new
-    # one layer's attention alone at the mean context of the run
+    tokens_hash = nn.fnv1a64(ids)
+
+    # one layer's prefill attention at the C5 geometry (causal, 16 x 2048 tokens, 20 heads)
+    pf = dec._pf
+    kc, vc = dec.caches[0]
+    fn_pf = lambda: ctx.attention_prefill(pf["q"], kc, vc, B, ctx_len, H, Hkv, dk, 0, cfg.scale, dec.cos, dec.sin,
+                                          out=pf["a"])
+    t_pfa, _ = time_launches(torch, stream, fn_pf, 10, 2)
+    pfa_flops = 4.0 * B * H * dk * (ctx_len * (ctx_len + 1) / 2)   # QK^T and PV over the causal triangle
+    # one layer's decode attention alone at the mean context of the run
     mid = ctx_len + new // 2
     pos.fill_(mid)
-    kc, vc = caches[0]
     fn = lambda: ctx.attention_decode(dec.q, dec.k, dec.v, H, Hkv, dk, pos, max_len, kc, vc, cfg.scale, dec.cos,
                                       dec.sin, out=dec.a)
     t_att, _ = time_launches(torch, stream, fn, max(10, steps // 2), 3)
     att_bytes = dm.attention_bytes(B, [mid + 1] * B, Hkv, dk, H)
     kv_bytes = L * att_bytes
     res = {
+        "prefill_ms": round(t_prefill * 1e3, 3), "prefill_tokens_per_s": round(B * ctx_len / t_prefill, 1),
+        "prefill_attention_one_layer": {"us": round(t_pfa * 1e6, 1), "TFLOP/s": round(pfa_flops / t_pfa / 1e12, 1),
+                                        "frac_fp32_mfma": round(pfa_flops / t_pfa / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                                        "flops": pfa_flops},
         "tokens_per_s": round(B / t_step, 1), "ms_per_step": round(t_step * 1e3, 4),
-        "eager_ms_per_step": round(t_eager * 1e3, 4), "batch": B, "context": ctx_len, "new_tokens": new,
+        "eager_ms_per_step": round(t_eager * 1e3, 4),
+        "end_to_end_s": round(t_prefill + new * t_step, 4),
+        "batch": B, "context": ctx_len, "new_tokens": new,
         "layers": L, "packed_weight_bytes": wbytes, "kv_bytes_per_step_at_mean_context": kv_bytes,
         "step_GB/s_weights_plus_kv": round((wbytes + kv_bytes) / t_step / 1e9, 1),
         "attention_one_layer": {"us": round(t_att * 1e6, 2), "bytes": att_bytes,
                                 "GB/s": round(att_bytes / t_att / 1e9, 1),
                                 "frac_hbm": round(att_bytes / t_att / 1e9 / HBM_PEAK_GBS, 4)},
+        "hash": {"prefill_last_logits": prefill_hash, "last_ids": tokens_hash},
     }
     out["decode_c5"] = res
-    log(f"C5 decode: {res}")
-    del caches, dec
+    log(f"C5: {res}")
+    del dec
     torch.cuda.empty_cache()
 
 
@@ -458,32 +485,120 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes": n * 4}), flush=True)
 
 
-def cpu_baseline(weights, acts1, budget_s=12.0):
-    """Oracle CpuEngine restatement (row-block RB=64 decode + dense f32 microkernel) at M=1
-    on a bounded sample: layer 0's seven matrices, repeated for about budget_s seconds."""
+def _host_l3_bytes():
+    """Total L3 of the CPUs this process may run on (distinct L3 instances summed), or None."""
+    seen, total = set(), 0
+    try:
+        for cpu in sorted(os.sched_getaffinity(0)):
+            base = f"/sys/devices/system/cpu/cpu{cpu}/cache/index3"
+            with open(base + "/shared_cpu_list") as f:
+                key = f.read().strip()
+            if key in seen:
+                continue
+            seen.add(key)
+            with open(base + "/size") as f:
+                v = f.read().strip()
+            total += int(v[:-1]) * 1024 if v.endswith("K") else int(v)
+    except (OSError, ValueError):
+        return None
+    return total or None
+
+
+def cpu_baseline(ctx, torch, weights, acts1):
+    """The oracle's CpuEngine restatement (row-block RB=64 decode + dense f32 microkernel,
+    oracle/nn_oracle.c orc_matmul_q_i8_rowblock) built with the reference's Release flags
+    (oracle/Makefile), timed on this host:
+      * the headline workload, M=1 GEMVs over a DRAM-resident sample of the layer stack: enough
+        layers for at least 4x the host's L3 (all 30 if that is not enough), every pass streaming
+        the reference containers from memory, with all the cores this process may use and with one;
+      * the M=2048 prefill GEMM (N=K=4096) on a 1024-row block of the weights;
+      * config C4's gated FFN block on 64 of its 2048 tokens (every step is per token).
+    Best-of-passes wall clock, as src/layer_bench.cpp:693-715 times the reference."""
     from oracle import nn_oracle as orc   # the CPU restatement, timed as the baseline
-    threads = min(16, os.cpu_count() or 1)
+    L, level = orc.release_lib()
+    affinity = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, omp) if omp > 0 else affinity
+    l3 = _host_l3_bytes()
+    layer_bytes = sum(gemv_bytes(N, K, 1) for _, K, N in SHAPES)
+    n_layers = len(weights.mats) // len(SHAPES)
+    want = n_layers if l3 is None else min(n_layers, max(1, -(-4 * l3 // layer_bytes)))
+    # reference containers of the sample, from the GPU's repacked words
+    sample = []
+    for (layer, name, K, N, rp, tau) in weights.mats:
+        if layer >= want:
+            break
+        wq = ctx.unrepack(rp, N, K).cpu().numpy().view(np.uint32)
+        sample.append((wq, tau.cpu().numpy(), K, N))
     acts_host = {}
     for K in (D, FFN):
         X, _, s, _ = acts1[K]
         s_h = s.cpu().numpy()
         acts_host[K] = (orc.quantize_i8(X.cpu().numpy(), s_h, True), s_h)
-    nbytes, elapsed, reps = 0, 0.0, 0
-    while elapsed < budget_s and reps < 5000:
-        for name, K, N in SHAPES:
-            wq, tau = weights.ref0[name]
-            xq, s = acts_host[K]
+    sample_bytes = sum(gemv_bytes(N, K, 1) for (_, _, K, N) in sample)
+
+    def sweep(nthreads, budget_s):
+        best, t_all, passes = None, 0.0, 0
+        while passes < 1 or (t_all < budget_s and passes < 50):
             t0 = time.perf_counter()
-            orc.matmul_q_i8_rowblock(wq, tau, xq, s, K, 1, threads)
-            elapsed += time.perf_counter() - t0
-            nbytes += gemv_bytes(N, K, 1)
-        reps += 1
-    layer_bytes = sum(gemv_bytes(N, K, 1) for _, K, N in SHAPES)
-    return {"value": round(nbytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"layer 0 of the stack (7 GEMVs, {layer_bytes} B) x {reps} repetitions at "
-                      f"M=1 ({elapsed:.1f} s); oracle/nn_oracle.c orc_matmul_q_i8_rowblock, "
-                      f"{threads} OpenMP threads"}
+            for wq, tau, K, N in sample:
+                xq, s = acts_host[K]
+                orc.matmul_q_i8_rowblock(wq, tau, xq, s, K, 1, nthreads, L=L)
+            dt = time.perf_counter() - t0
+            t_all += dt
+            passes += 1
+            best = dt if best is None else min(best, dt)
+        return sample_bytes / best / 1e9, passes, t_all
+
+    v_all, p_all, t_all = sweep(threads, 8.0)
+    v_one, p_one, t_one = sweep(1, 6.0)
+    # prefill GEMM, N=K=4096, M=2048, one 256-row block
+    rng = np.random.default_rng(0xB17A)
+    Kg, Mg, rows = 4096, 2048, 1024
+    wq = rng.integers(0, 2 ** 32, (rows, Kg // 16), dtype=np.uint32)   # the timing does not depend on the codes
+    xq = rng.integers(0, 2 ** 32, (Kg, Mg // 4), dtype=np.uint32)
+    tg = np.ones(rows, np.float32)
+    sg = np.ones(Mg, np.float32)
+    best = None
+    t_g = 0.0
+    while best is None or t_g < 3.0:
+        t0 = time.perf_counter()
+        orc.matmul_q_i8_rowblock(wq, tg, xq, sg, Kg, Mg, threads, L=L)
+        dt = time.perf_counter() - t0
+        t_g += dt
+        best = dt if best is None else min(best, dt)
+    gemm_tops = 2.0 * rows * Kg * Mg / best / 1e12
+    # C4 block on 64 tokens
+    d, F, Mt = D, FFN, 64
+    X = rng.standard_normal((d, Mt), dtype=np.float32)
+    g = np.ones(d, np.float32)
+    W1 = (rng.standard_normal((2 * F, d), dtype=np.float32) * np.float32(0.02))
+    W2 = (rng.standard_normal((d, F), dtype=np.float32) * np.float32(0.02))
+    t1, t2 = orc.row_absmean(W1), orc.row_absmean(W2)
+    wq1, wq2 = orc.trit_pack(W1, t1), orc.trit_pack(W2, t2)
+    del W1, W2
+    best = None
+    t_c = 0.0
+    while best is None or t_c < 3.0:
+        t0 = time.perf_counter()
+        orc.ffn_glu_i8(X, g, 1e-6, F, wq1, t1, None, wq2, t2, None, 0, threads, L=L)
+        dt = time.perf_counter() - t0
+        t_c += dt
+        best = dt if best is None else min(best, dt)
+    c4_ops = 2.0 * Mt * (2 * F * d + d * F)
+    return {"value": round(v_all, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(sample)} GEMVs = layers 0-{want - 1} of the stack ({sample_bytes} B of reference "
+                      f"containers per pass; host L3 {l3} B) at M=1, best of {p_all} passes ({t_all:.1f} s); "
+                      f"oracle/nn_oracle.c orc_matmul_q_i8_rowblock built with the reference Release flags "
+                      f"(x86-64-{level}), {threads} OpenMP threads of {affinity} CPUs in the affinity mask",
+            "one_core": {"value": round(v_one, 3), "unit": "GB/s", "cores": 1,
+                         "sample": f"the same sample, best of {p_one} passes ({t_one:.1f} s)"},
+            "gemm_m2048": {"TOPS": round(gemm_tops, 4), "cores": threads,
+                           "sample": f"N=K=4096, M=2048 on a {rows}-row block: {2 * rows * Kg * Mg} ops per call"},
+            "ffn_block_c4": {"TOPS": round(c4_ops / best / 1e12, 4), "us_per_token": round(best / Mt * 1e6, 1),
+                             "cores": threads,
+                             "sample": f"RMSNorm -> int8 -> fc1 + SwiGLU -> int8 -> fc2 (d=2560, F=6912) on "
+                                       f"{Mt} tokens ({c4_ops:.3g} ops per call)"}}
 
 
 def main():
@@ -529,6 +644,8 @@ def main():
     log(f"M=1 sweep: {t_launch * 1e6:.1f} us/launch (events), {ms_per_step * 1e3:.1f} us/step wall, "
         f"{gbs:.1f} GB/s = {gbs / HBM_PEAK_GBS:.3f} of HBM peak")
 
+    # bit hash of the sweep's outputs (the 210 Y, concatenated in problem order), as layer_bench --hash
+    out_hash = nn.fnv1a64(torch.cat([p["y"].reshape(-1) for p in probs]))
     # the sweep's last output must equal the single-problem launch bit for bit
     p0 = probs[-1]
     y_single = ctx.ternary_matmul(p0["rp"], p0["tau"], p0["xi"], p0["s"], p0["rowsum"],
@@ -550,9 +667,9 @@ def main():
     log(f"achievable read: {ach}")
     cpu = None
     if not args.no_cpu:
-        log("timing the CPU baseline (about 12 s)")
-        cpu = cpu_baseline(weights, acts1)
-        log(f"CPU baseline: {cpu['value']} GB/s with {cpu['cores']} threads")
+        log("timing the CPU baseline (about 25 s)")
+        cpu = cpu_baseline(ctx, torch, weights, acts1)
+        log(f"CPU baseline: {cpu}")
 
     n_items = sum((p["N"] + 15) // 16 for p in probs)
     line = {
@@ -572,7 +689,8 @@ def main():
                                f"{args.layers} layers x q/k/v/o/gate/up/down of d=2560, ffn=6912, kv=640",
                    "M": 1, "layers": args.layers, "gemvs": len(probs), "row_tiles": n_items,
                    "packed_weight_bytes": wbytes, "algorithmic_bytes": nbytes,
-                   "grid_waves": ctx.gemv_grid_waves(n_items)},
+                   "grid_waves": ctx.gemv_grid_waves(n_items), "variant": ctx.group_info(grp),
+                   "output_hash": out_hash},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                      "kernel": "k_gemv_grouped", "avg_launch_us": round(t_launch * 1e6, 2),

@@ -59,6 +59,14 @@ const char* nnhip_last_error(void);
 /* Library version string, e.g. "nnhip 0.1.0 gfx950". */
 const char* nnhip_version(void);
 
+/* FNV-1a over `bytes` bytes of HOST memory in address order, with the constants of the reference's
+ * layer_bench --hash (src/layer_bench.cpp:732-741): start value 1469598103934665603 as the reference
+ * writes it (the published FNV-1a 64 offset basis is 14695981039346656037; the reference's value is
+ * kept so that hashes compare with its output), prime 1099511628211, each f32's four bytes low to
+ * high, i.e. the little-endian memory order. A measurement aid: two kernel versions that agree bit
+ * for bit give the same hash. */
+uint64_t nnhip_fnv1a64(const void* data, size_t bytes);
+
 /* Number of visible HIP devices. */
 nnhip_status nnhip_device_count(int* count);
 
@@ -418,6 +426,40 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
                                     size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
                                     const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
                                     size_t max_len, float scale, float* out);
+
+/* ---- batched prefill (config C5's 2048-token context): T new tokens of each of B sequences at
+ *      positions pos0 .. pos0 + T - 1 in one pass. The reference fills the cache by running
+ *      forward_step once per context token (GPTModel::generate, include/neuralnet.cpp/
+ *      compute_layer_gpt.hpp:774-794); these give every token the result of its own step. Token
+ *      column m = b * T + t of the (rows, B * T) feature-major tensors below. ---- */
+
+/* Append T tokens per sequence to the KV caches: k / v (Hkv*dk, B*T) are the k / v projections;
+ * cache row pos0 + t of sequence b gets the key of token t rotated at position pos0 + t (as
+ * nnhip_attention_decode stores it, bit for bit) and its value. Needs pos0 + T <= max_len;
+ * dk in {64, 128}; rope tables as nnhip_attention_decode (both NULL: no position encoding).
+ * Replaces the insert_rows steps of T AttentionBase::forward_step calls
+ * (include/neuralnet.cpp/compute_layer_attention.hpp:1040-1060). */
+nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,
+                                 size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin, float* k_cache,
+                                 float* v_cache, size_t max_len);
+
+/* Causal attention of the T tokens over caches already holding rows [0, pos0 + T) (after
+ * nnhip_kv_cache_fill): out (H*dk, B*T), column b*T + t = per query head h the softmax
+ * ((rot(q_h) . K^T) * scale) . V over cache rows [0, pos0 + t] of sequence b, KV head h / (H/Hkv),
+ * q rotated at pos0 + t. f32 on the fp32 MFMA with an online softmax: within 2e-6 relative of a
+ * float64 evaluation (the reference does not pin the order). dk in {64, 128}; H / Hkv in
+ * {1, 2, 4, 8}. Replaces the attention steps of T AttentionBase::forward_step calls
+ * (compute_layer_attention.hpp:1022-1083). */
+nnhip_status nnhip_attention_prefill(nnhip_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
+                                     size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0,
+                                     const float* rope_cos, const float* rope_sin, size_t max_len, float scale,
+                                     float* out);
+
+/* dst (rows, n): column j = column col0 + j * stride of src (rows, src_cols), e.g. the last token of
+ * each sequence after a prefill (col0 = T - 1, stride = T) for the LM head. Replaces the reference's
+ * use of the last step's output (last_logits_t, compute_layer_gpt.hpp:785-790). */
+nnhip_status nnhip_copy_columns(nnhip_ctx* ctx, const float* src, size_t rows, size_t src_cols, size_t col0,
+                                size_t stride, size_t n, float* dst);
 
 /* out[i] = x[i] + y[i] (one IEEE add; out may alias x or y). Replaces the residual adds
  * dsl::compute(leaf(x) + leaf(a)) of GPTBlock::forward_step (compute_layer_gpt.hpp:208-218). */

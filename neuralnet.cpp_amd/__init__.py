@@ -56,6 +56,7 @@ class GemvDesc(ctypes.Structure):
 SIGNATURES = {
     "nnhip_last_error": (ctypes.c_char_p, []),
     "nnhip_version": (ctypes.c_char_p, []),
+    "nnhip_fnv1a64": (ctypes.c_uint64, [_vp, _sz]),
     "nnhip_device_count": (_st, [ctypes.POINTER(ctypes.c_int)]),
     "nnhip_ctx_create": (_st, [ctypes.c_int, ctypes.POINTER(_vp)]),
     "nnhip_ctx_destroy": (_st, [_vp]),
@@ -120,6 +121,9 @@ SIGNATURES = {
     "nnhip_attention_decode": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _f,
                                      _vp]),
     "nnhip_add": (_st, [_vp, _vp, _vp, _sz, _vp]),
+    "nnhip_kv_cache_fill": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz]),
+    "nnhip_attention_prefill": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _f, _vp]),
+    "nnhip_copy_columns": (_st, [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp]),
     "nnhip_embedding_gather": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_argmax_cols": (_st, [_vp, _vp, _sz, _sz, _vp]),
 }
@@ -151,6 +155,14 @@ def _check(status: int, fn: str) -> None:
     if status != 0:
         msg = lib().nnhip_last_error().decode(errors="replace")
         raise NNHipError(status, msg or fn)
+
+
+def fnv1a64(t) -> str:
+    """FNV-1a 64 of a tensor's bytes (a device tensor is copied to the host first), as hex: the
+    reference layer_bench --hash of an output."""
+    import numpy as np
+    a = np.ascontiguousarray(t.detach().cpu().numpy() if hasattr(t, "detach") else t)
+    return "%016x" % lib().nnhip_fnv1a64(_vp(a.ctypes.data), a.nbytes)
 
 
 def repacked_bytes(N: int, K: int) -> int:
@@ -589,6 +601,41 @@ class Context:
             self._dev(k_cache, torch.float32, "k_cache"), self._dev(v_cache, torch.float32, "v_cache"), max_len,
             scale, self._dev(out, torch.float32, "out")), "nnhip_attention_decode")
         return out
+
+    def kv_cache_fill(self, k, v, B: int, T: int, Hkv: int, dk: int, pos0: int, k_cache, v_cache, cos=None, sin=None):
+        """Append T tokens of each of B sequences (k / v (Hkv*dk, B*T)) to the caches at rows pos0 + t."""
+        torch = self._torch
+        self._bind_stream()
+        _check(lib().nnhip_kv_cache_fill(self.h, self._dev(k, torch.float32, "k"), self._dev(v, torch.float32, "v"),
+                                         B, T, Hkv, dk, pos0, self._dev(cos, torch.float32, "cos"),
+                                         self._dev(sin, torch.float32, "sin"),
+                                         self._dev(k_cache, torch.float32, "k_cache"),
+                                         self._dev(v_cache, torch.float32, "v_cache"), k_cache.shape[1]),
+               "nnhip_kv_cache_fill")
+
+    def attention_prefill(self, q, k_cache, v_cache, B: int, T: int, H: int, Hkv: int, dk: int, pos0: int,
+                          scale: float, cos=None, sin=None, out=None):
+        """Causal attention of T tokens per sequence (q (H*dk, B*T)) over caches holding rows [0, pos0 + T)."""
+        torch = self._torch
+        Y = out if out is not None else self._empty((H * dk, B * T), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_attention_prefill(self.h, self._dev(q, torch.float32, "q"),
+                                             self._dev(k_cache, torch.float32, "k_cache"),
+                                             self._dev(v_cache, torch.float32, "v_cache"), B, T, H, Hkv, dk, pos0,
+                                             self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
+                                             k_cache.shape[1], scale, self._dev(Y, torch.float32, "out")),
+               "nnhip_attention_prefill")
+        return Y
+
+    def copy_columns(self, src, col0: int, stride: int, n: int, out=None):
+        """dst (rows, n): column j = src column col0 + j * stride."""
+        torch = self._torch
+        rows, cols = src.shape
+        Y = out if out is not None else self._empty((rows, n), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_copy_columns(self.h, self._dev(src, torch.float32, "src"), rows, cols, col0, stride, n,
+                                        self._dev(Y, torch.float32, "dst")), "nnhip_copy_columns")
+        return Y
 
     def add(self, x, y, out=None):
         torch = self._torch

@@ -477,6 +477,16 @@ __global__ __launch_bounds__(kSmallBlock) void k_add(const float* __restrict__ x
     if (i < n) out[i] = __fadd_rn(x[i], y[i]);
 }
 
+// dst (rows, n): column j = column col0 + j * stride of src (rows, src_cols)
+__global__ __launch_bounds__(kSmallBlock) void k_copy_cols(const float* __restrict__ src, size_t rows, size_t src_cols,
+                                                           size_t col0, size_t stride, size_t n, float* __restrict__ dst)
+{
+    const size_t i = (size_t)blockIdx.x * kSmallBlock + threadIdx.x;
+    if (i >= rows * n) return;
+    const size_t r = i / n, j = i % n;
+    dst[i] = src[r * src_cols + col0 + j * stride];
+}
+
 // out (d, B): column b = row ids[b] of the (V, d) table (NaN column for an id outside [0, V))
 __global__ __launch_bounds__(kSmallBlock) void k_embed(const float* __restrict__ table, const int32_t* __restrict__ ids,
                                                        int V, int d, int B, float* __restrict__ out)
@@ -565,6 +575,15 @@ hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, co
 hipError_t launch_add(hipStream_t st, const float* x, const float* y, size_t n, float* out)
 {
     k_add<<<dim3((unsigned)ceil_div(n, kSmallBlock)), kSmallBlock, 0, st>>>(x, y, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_cols(hipStream_t st, const float* src, size_t rows, size_t src_cols, size_t col0, size_t stride,
+                            size_t n, float* dst)
+{
+    if (rows * n == 0) return hipSuccess;
+    k_copy_cols<<<dim3((unsigned)ceil_div(rows * n, kSmallBlock)), kSmallBlock, 0, st>>>(src, rows, src_cols, col0,
+                                                                                       stride, n, dst);
     return hipGetLastError();
 }
 

@@ -238,6 +238,18 @@ const char* nnhip_last_error(void) { return g_err.c_str(); }
 
 const char* nnhip_version(void) { return "nnhip 0.1.0 gfx950"; }
 
+uint64_t nnhip_fnv1a64(const void* data, size_t bytes)
+{
+    const uint8_t* p = static_cast<const uint8_t*>(data);
+    uint64_t h = 1469598103934665603ull;
+    for (size_t i = 0; i < bytes && p; ++i)
+    {
+        h ^= p[i];
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
 nnhip_status nnhip_device_count(int* count)
 {
     if (!count) return fail(NNHIP_ERR_INVALID_ARG, "nnhip_device_count", "null output");
@@ -1329,6 +1341,61 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
     NNHIP_LAUNCH(fn, launch_attn_decode(ctx->stream, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin,
                                         k_cache, v_cache, max_len, scale,
                                         wsb ? static_cast<float*>(ctx->attn_ws) : nullptr, out, ctx->num_cus));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,
+                                 size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin, float* k_cache,
+                                 float* v_cache, size_t max_len)
+{
+    const char* fn = "nnhip_kv_cache_fill";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0 || T == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(k && v && k_cache && v_cache, fn, "null pointer");
+    NNHIP_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), fn, "rope_cos and rope_sin must both be given or both NULL");
+    if (!prefill_dk_supported(dk)) return fail(NNHIP_ERR_UNSUPPORTED, fn, "dk must be 64 or 128");
+    NNHIP_REQUIRE(Hkv >= 1 && pos0 + T <= max_len && mul_ok(B, T), fn, "need Hkv >= 1 and pos0 + T <= max_len");
+    NNHIP_REQUIRE(B * T <= kMaxDim && mul_ok(Hkv * dk, B * T) && Hkv * dk * B * T < 0x7FFFFFFFull, fn,
+                  "k / v must be below 2^31 elements");
+    NNHIP_LAUNCH(fn, launch_kv_fill(ctx->stream, k, v, B, T, Hkv, dk, pos0, rope_cos, rope_sin, k_cache, v_cache, max_len));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_attention_prefill(nnhip_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
+                                     size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0,
+                                     const float* rope_cos, const float* rope_sin, size_t max_len, float scale,
+                                     float* out)
+{
+    const char* fn = "nnhip_attention_prefill";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0 || T == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(q && k_cache && v_cache && out, fn, "null pointer");
+    NNHIP_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), fn, "rope_cos and rope_sin must both be given or both NULL");
+    if (!prefill_dk_supported(dk)) return fail(NNHIP_ERR_UNSUPPORTED, fn, "dk must be 64 or 128");
+    NNHIP_REQUIRE(Hkv >= 1 && H % Hkv == 0, fn, "H must be a multiple of Hkv");
+    const size_t R = H / Hkv;
+    if (R != 1 && R != 2 && R != 4 && R != 8)
+        return fail(NNHIP_ERR_UNSUPPORTED, fn, "H / Hkv must be 1, 2, 4 or 8");
+    NNHIP_REQUIRE(pos0 + T <= max_len && mul_ok(B, T), fn, "need pos0 + T <= max_len");
+    NNHIP_REQUIRE(aligned16(k_cache) && aligned16(v_cache), fn, "caches must be 16-byte aligned");
+    NNHIP_REQUIRE(B * T <= kMaxDim && mul_ok(H * dk, B * T) && H * dk * B * T < 0x3FFFFFFFull, fn,
+                  "q / out must be below 2^30 elements");
+    NNHIP_REQUIRE(max_len * Hkv * dk < 0x3FFFFFFFull, fn, "one sequence's cache must be below 2^30 elements");
+    NNHIP_LAUNCH(fn, launch_attn_prefill(ctx->stream, q, k_cache, v_cache, B, T, H, Hkv, dk, pos0, rope_cos, rope_sin,
+                                         max_len, scale, out));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_copy_columns(nnhip_ctx* ctx, const float* src, size_t rows, size_t src_cols, size_t col0,
+                                size_t stride, size_t n, float* dst)
+{
+    const char* fn = "nnhip_copy_columns";
+    NNHIP_CHECK_CTX(fn);
+    if (rows == 0 || n == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(src && dst, fn, "null pointer");
+    NNHIP_REQUIRE(mul_ok(rows, n) && mul_ok(n - 1, stride) && col0 + (n - 1) * stride < src_cols, fn,
+                  "columns col0 + j * stride must lie below src_cols");
+    NNHIP_LAUNCH(fn, launch_copy_cols(ctx->stream, src, rows, src_cols, col0, stride, n, dst));
     return NNHIP_OK;
 }
 

@@ -14,6 +14,12 @@ branch):
     r = x + BitLinear_o(xi)                       nnhip_ternary_matmul_add (residual in the epilogue)
     x = r + FFN(RMSNorm2(r))                      nnhip_ffn_glu_i8_add (norm and residual fused)
 then logits = BitLinear_head(int8(RMSNorm_f(x))) and the greedy ids (nnhip_argmax_cols).
+
+Decoder.prefill runs T tokens of every sequence through the same chain at once (M = B*T token
+columns: the GEMM path, nnhip_kv_cache_fill and the causal nnhip_attention_prefill), giving each
+token the result of its own step() (the reference fills the cache with one forward_step per
+context token, compute_layer_gpt.hpp:774-794), and the logits and greedy ids of each sequence's
+last token.
 """
 from __future__ import annotations
 
@@ -101,6 +107,73 @@ class Decoder:
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
         self.logits = torch.empty((cfg.vocab, B), **f32)
         self.ids = torch.empty((B,), dtype=torch.int32, device=dev)
+
+    def _prefill_buffers(self, M: int):
+        """Scratch of a prefill over M = B*T token columns (allocated once per M)."""
+        import torch
+        if getattr(self, "_pf_M", None) == M:
+            return self._pf
+        cfg = self.cfg
+        dev = f"cuda:{self.ctx.device}"
+        f32 = dict(dtype=torch.float32, device=dev)
+        d, H, Hkv, dk = cfg.d, cfg.H, cfg.Hkv, cfg.dk
+        kpd = _pkg().kp
+        self._pf = dict(
+            x=torch.empty((d, M), **f32), r=torch.empty((d, M), **f32), q=torch.empty((H * dk, M), **f32),
+            k=torch.empty((Hkv * dk, M), **f32), v=torch.empty((Hkv * dk, M), **f32),
+            a=torch.empty((H * dk, M), **f32),
+            xi=torch.empty((M * kpd(max(d, H * dk)),), dtype=torch.int8, device=dev),
+            s=torch.empty((M,), **f32), rs=torch.empty((M,), dtype=torch.int32, device=dev))
+        self._pf_M = M
+        return self._pf
+
+    def prefill(self, ids, T: int, pos0: int = 0, hook=None):
+        """T tokens of each of the B sequences, at positions pos0 .. pos0 + T - 1, through every block
+        in one pass: the caches get rows pos0 .. pos0 + T - 1 and every token the result of its own
+        step(). ids: (B*T,) int32 device tensor, token column b*T + t. hook(i, name, tensor) sees each
+        block's q / k / v / attention output / block output (tests). Returns (logits (vocab, B), greedy
+        ids (B,)) of each sequence's last token."""
+        cfg, ctx, B = self.cfg, self.ctx, self.B
+        M = B * T
+        pf = self._prefill_buffers(M)
+        outs = (pf["xi"], pf["s"], pf["rs"])
+        x, r = pf["x"], pf["r"]
+
+        def quant(t, gamma):
+            if gamma is None:
+                ctx.act_quant_i8(t, outs=outs)
+            else:
+                ctx.rmsnorm_quant_i8(t, gamma, cfg.eps, outs=outs)
+
+        def mm(lin, out):
+            return ctx.ternary_matmul(lin.rp, lin.tau, pf["xi"], pf["s"], pf["rs"], lin.N, lin.K, M, bias=lin.bias,
+                                      out=out)
+
+        ctx.embedding_gather(self.emb, ids, out=x)
+        for i, blk in enumerate(self.blocks):
+            quant(x, blk.g1)
+            mm(blk.q, pf["q"])
+            mm(blk.k, pf["k"])
+            mm(blk.v, pf["v"])
+            kc, vc = self.caches[i]
+            ctx.kv_cache_fill(pf["k"], pf["v"], B, T, cfg.Hkv, cfg.dk, pos0, kc, vc, self.cos, self.sin)
+            ctx.attention_prefill(pf["q"], kc, vc, B, T, cfg.H, cfg.Hkv, cfg.dk, pos0, cfg.scale, self.cos, self.sin,
+                                  out=pf["a"])
+            if hook is not None:
+                for name in ("q", "k", "v", "a"):
+                    hook(i, name, pf[name])
+            quant(pf["a"], blk.g_attn_sub)
+            o = blk.o
+            ctx.ternary_matmul_add(o.rp, o.tau, pf["xi"], pf["s"], pf["rs"], o.N, o.K, M, x, bias=o.bias, out=r)
+            ctx.ffn_glu_i8_add(r, blk.g2, cfg.eps, cfg.F, blk.fc1.rp, blk.fc1.tau, blk.fc1.bias, blk.fc2.rp,
+                               blk.fc2.tau, blk.fc2.bias, r, cfg.act, out=x, gamma_sub=blk.g_ffn_sub, eps_sub=cfg.eps)
+            if hook is not None:
+                hook(i, "x", x)
+        ctx.copy_columns(x, T - 1, T, B, out=self.x)
+        self._quant(self.x, self.g_final)
+        self._mm(self.head, self.logits)
+        ctx.argmax_cols(self.logits, out=self.ids)
+        return self.logits, self.ids
 
     def _mm(self, lin: Linear, out):
         return self.ctx.ternary_matmul(lin.rp, lin.tau, self.xi, self.s, self.rs, lin.N, lin.K, self.B,

@@ -28,59 +28,90 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
 
 
+def release_lib():
+    """The same oracle built with the reference's Release flags (oracle/Makefile), for the timed CPU
+    baseline: the x86-64-v4 (AVX-512) build when this host's CPU has the subsets v4 needs, else the
+    x86-64-v3 build. Returns (library, "v4" or "v3")."""
+    global _rel
+    if _rel is None:
+        flags = set()
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("flags"):
+                        flags = set(line.split(":", 1)[1].split())
+                        break
+        except OSError:
+            pass
+        level = "v4" if {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags else "v3"
+        path = os.path.join(_HERE, f"libnnoracle_rel_{level}.so")
+        if not os.path.exists(path):
+            build()
+        _rel = (_load(path), level)
+    return _rel
+
+
+_rel = None
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
-        sig = {
-            "orc_fill_uniform": (None, [_f32p, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
-            "orc_fill_normal": (None, [_f32p, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
-            "orc_trit_words_per_row": (_sz, [_sz]),
-            "orc_trit_code": (ctypes.c_uint32, [ctypes.c_float, ctypes.c_float]),
-            "orc_trit_pack": (None, [_f32p, _f32p, _sz, _sz, _u32p]),
-            "orc_trit_at": (ctypes.c_int, [_u32p, _sz]),
-            "orc_row_absmean": (None, [_f32p, _sz, _sz, _f32p]),
-            "orc_i8_words_per_row": (_sz, [_sz]),
-            "orc_quantize_one": (ctypes.c_int8, [ctypes.c_float, ctypes.c_float]),
-            "orc_col_absmax": (None, [_f32p, _sz, _sz, _f32p]),
-            "orc_act_scale": (None, [_f32p, _sz, _sz, _f32p]),
-            "orc_quantize_i8": (None, [_f32p, _f32p, _sz, _sz, ctypes.c_int, _u32p]),
-            "orc_unpack_i8": (None, [_u32p, _sz, _sz, _f32p]),
-            "orc_matmul_q_i8_acc": (None, [_u32p, _u32p, _sz, _sz, _sz, _i32p]),
-            "orc_matmul_q_i8": (None, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p]),
-            "orc_matmul_q_i8_rowblock": (ctypes.c_int, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]),
-            "orc_add_row_broadcast": (None, [_f32p, _f32p, _sz, _sz]),
-            "orc_matmul_q": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
-            "orc_matmul_q_t": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
-            "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
-            "orc_rmsnorm_quant_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _u32p, _f32p]),
-            "orc_exp": (ctypes.c_float, [ctypes.c_float]),
-            "orc_exp_array": (None, [_f32p, _sz, _f32p]),
-            "orc_glu_one": (ctypes.c_float, [ctypes.c_float, ctypes.c_float, ctypes.c_int]),
-            "orc_glu": (None, [_f32p, _sz, _sz, ctypes.c_int, _f32p]),
-            "orc_glu_src_row": (ctypes.c_long, [_sz, _sz]),
-            "orc_glu_interleave": (None, [_u32p, _f32p, _f32p, _sz, _sz, _u32p, _f32p, _f32p]),
-            "orc_ffn_glu_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _sz, ctypes.c_int,
-                                      _u32p, _f32p, _f32p, _f32p, ctypes.c_float, _u32p, _f32p, _f32p, ctypes.c_int,
-                                      _f32p, _f32p]),
-            "orc_rope_table": (None, [_sz, _sz, _f32p, _f32p]),
-            "orc_rope_apply": (None, [_f32p, _sz, _f32p, _f32p, _f32p]),
-            "orc_attention_decode": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _i32p, _f32p, _f32p, _f32p,
-                                            _f32p, _sz, ctypes.c_float, _f32p]),
-            "orc_embedding_gather": (None, [_f32p, _i32p, _sz, _sz, _sz, _f32p]),
-            "orc_argmax": (ctypes.c_int32, [_f32p, _sz, _sz]),
-            "orc_repacked_words": (_sz, [_sz, _sz]),
-            "orc_repack": (None, [_u32p, _sz, _sz, _u32p]),
-            "orc_unrepack": (None, [_u32p, _sz, _sz, _u32p]),
-        }
-        for name, (res, args) in sig.items():
-            f = getattr(L, name)
-            f.restype = res
-            f.argtypes = args
-        _lib = L
+        _lib = _load(LIB_PATH)
     return _lib
+
+
+def _load(path) -> ctypes.CDLL:
+    """Load one build of the oracle and declare every entry's signature."""
+    L = ctypes.CDLL(path)
+    sig = {
+        "orc_fill_uniform": (None, [_f32p, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+        "orc_fill_normal": (None, [_f32p, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+        "orc_trit_words_per_row": (_sz, [_sz]),
+        "orc_trit_code": (ctypes.c_uint32, [ctypes.c_float, ctypes.c_float]),
+        "orc_trit_pack": (None, [_f32p, _f32p, _sz, _sz, _u32p]),
+        "orc_trit_at": (ctypes.c_int, [_u32p, _sz]),
+        "orc_row_absmean": (None, [_f32p, _sz, _sz, _f32p]),
+        "orc_i8_words_per_row": (_sz, [_sz]),
+        "orc_quantize_one": (ctypes.c_int8, [ctypes.c_float, ctypes.c_float]),
+        "orc_col_absmax": (None, [_f32p, _sz, _sz, _f32p]),
+        "orc_act_scale": (None, [_f32p, _sz, _sz, _f32p]),
+        "orc_quantize_i8": (None, [_f32p, _f32p, _sz, _sz, ctypes.c_int, _u32p]),
+        "orc_unpack_i8": (None, [_u32p, _sz, _sz, _f32p]),
+        "orc_matmul_q_i8_acc": (None, [_u32p, _u32p, _sz, _sz, _sz, _i32p]),
+        "orc_matmul_q_i8": (None, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p]),
+        "orc_matmul_q_i8_rowblock": (ctypes.c_int, [_u32p, _f32p, _u32p, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]),
+        "orc_add_row_broadcast": (None, [_f32p, _f32p, _sz, _sz]),
+        "orc_matmul_q": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
+        "orc_matmul_q_t": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
+        "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
+        "orc_rmsnorm_quant_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _u32p, _f32p]),
+        "orc_exp": (ctypes.c_float, [ctypes.c_float]),
+        "orc_exp_array": (None, [_f32p, _sz, _f32p]),
+        "orc_glu_one": (ctypes.c_float, [ctypes.c_float, ctypes.c_float, ctypes.c_int]),
+        "orc_glu": (None, [_f32p, _sz, _sz, ctypes.c_int, _f32p]),
+        "orc_glu_src_row": (ctypes.c_long, [_sz, _sz]),
+        "orc_glu_interleave": (None, [_u32p, _f32p, _f32p, _sz, _sz, _u32p, _f32p, _f32p]),
+        "orc_ffn_glu_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _sz, ctypes.c_int,
+                                  _u32p, _f32p, _f32p, _f32p, ctypes.c_float, _u32p, _f32p, _f32p, ctypes.c_int,
+                                  _f32p, _f32p]),
+        "orc_rope_table": (None, [_sz, _sz, _f32p, _f32p]),
+        "orc_rope_apply": (None, [_f32p, _sz, _f32p, _f32p, _f32p]),
+        "orc_attention_decode": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _i32p, _f32p, _f32p, _f32p,
+                                        _f32p, _sz, ctypes.c_float, _f32p]),
+        "orc_embedding_gather": (None, [_f32p, _i32p, _sz, _sz, _sz, _f32p]),
+        "orc_argmax": (ctypes.c_int32, [_f32p, _sz, _sz]),
+        "orc_repacked_words": (_sz, [_sz, _sz]),
+        "orc_repack": (None, [_u32p, _sz, _sz, _u32p]),
+        "orc_unrepack": (None, [_u32p, _sz, _sz, _u32p]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    return L
 
 
 def _p(a: np.ndarray, ctype):
@@ -190,12 +221,14 @@ def matmul_q_i8(wq, tau, xq, s, K: int, M: int) -> np.ndarray:
     return Y
 
 
-def matmul_q_i8_rowblock(wq, tau, xq, s, K: int, M: int, threads: int = 0) -> np.ndarray:
+def matmul_q_i8_rowblock(wq, tau, xq, s, K: int, M: int, threads: int = 0, L=None) -> np.ndarray:
+    """CpuEngine restatement (row-block decode + dense f32 microkernel); L selects another build of
+    the oracle (release_lib()[0] for the timed baseline)."""
     wq, xq = _u32(wq), _u32(xq)
     N = wq.shape[0]
     tau, s = _f32(tau).reshape(N), _f32(s).reshape(M)
     Y = np.empty((N, M), np.float32)
-    rc = lib().orc_matmul_q_i8_rowblock(_p(wq, ctypes.c_uint32), _p(tau, ctypes.c_float),
+    rc = (L or lib()).orc_matmul_q_i8_rowblock(_p(wq, ctypes.c_uint32), _p(tau, ctypes.c_float),
                                         _p(xq, ctypes.c_uint32), _p(s, ctypes.c_float), N, K, M,
                                         _p(Y, ctypes.c_float), threads)
     if rc != 0:
@@ -294,7 +327,7 @@ def glu_interleave(wq: np.ndarray, tau: np.ndarray, bias, F: int, K: int):
 
 
 def ffn_glu_i8(X, gamma, eps, F, wq1, tau1, b1, wq2, tau2, b2, act: int = ACT_SWIGLU, threads: int = 0,
-               gamma_sub=None, eps_sub: float = 1e-5):
+               gamma_sub=None, eps_sub: float = 1e-5, L=None):
     """Config C4 block: [RMSNorm] -> int8 -> fc1 (2F) -> gated activation -> [SubLN RMSNorm] ->
     int8 -> fc2. Returns (Y (d, M), h (F, M)); h is the gated output before SubLN."""
     X = _f32(X)
@@ -305,7 +338,7 @@ def ffn_glu_i8(X, gamma, eps, F, wq1, tau1, b1, wq2, tau2, b2, act: int = ACT_SW
     keep = [None if a is None else _f32(a).reshape(-1) for a in (gamma, tau1, b1, tau2, b2, gamma_sub)]
     g_, t1, b1_, t2, b2_, gs_ = keep
     wq1, wq2 = _u32(wq1), _u32(wq2)
-    lib().orc_ffn_glu_i8(_p(X, ctypes.c_float), fp(g_), eps, d, F, M, act, _p(wq1, ctypes.c_uint32), fp(t1), fp(b1_),
+    (L or lib()).orc_ffn_glu_i8(_p(X, ctypes.c_float), fp(g_), eps, d, F, M, act, _p(wq1, ctypes.c_uint32), fp(t1), fp(b1_),
                          fp(gs_), eps_sub, _p(wq2, ctypes.c_uint32), fp(t2), fp(b2_), threads, _p(h, ctypes.c_float),
                          _p(Y, ctypes.c_float))
     return Y, h

@@ -68,3 +68,19 @@ def test_no_cpu_fallback_without_gpu(nnhip):
         pytest.skip("a GPU is visible")
     with pytest.raises(nnhip.NNHipError):
         nnhip.Context(0)
+
+
+def test_fnv1a64_output_hash(nnhip):
+    """The bench's output hash uses the reference layer_bench --hash constants
+    (src/layer_bench.cpp:732-741): the empty input gives its start value, and every byte is folded
+    as h = (h ^ byte) * 1099511628211 mod 2^64 (a host function, no GPU)."""
+    import numpy as np
+    assert nnhip.fnv1a64(np.zeros(0, np.uint8)) == "%016x" % 1469598103934665603
+    data = np.frombuffer(b"BitLinear W1.58A8", np.uint8)
+    h = 1469598103934665603
+    for byte in data.tolist():
+        h = ((h ^ byte) * 1099511628211) % (1 << 64)
+    assert nnhip.fnv1a64(data) == "%016x" % h
+    # f32 values hash their little-endian bytes
+    x = np.array([1.0, -2.5], np.float32)
+    assert nnhip.fnv1a64(x) == nnhip.fnv1a64(x.view(np.uint8))
