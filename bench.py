@@ -612,6 +612,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the config C5 decode line")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the M=16 / per-shape / single-launch GEMV and the quantizer lines")
+    ap.add_argument("--lines", default="all",
+                    help="comma-separated lines besides the headline: gemv_extra, act_quant, matmul_q, gemm, "
+                         "ffn, c5 (default all; the --no-* flags remove lines from it)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB ten times (PMC calibration)")
     args = ap.parse_args()
@@ -653,15 +656,26 @@ def main():
     torch.cuda.synchronize()
     assert torch.equal(y_single, p0["y"]), "grouped GEMV differs from the single launch"
 
+    lines = {"gemv_extra", "act_quant", "matmul_q", "gemm", "ffn", "c5"} if args.lines == "all" else \
+        set(args.lines.split(","))
+    if args.no_extra:
+        lines -= {"gemv_extra", "act_quant", "matmul_q"}
+    if args.no_gemm:
+        lines -= {"gemm", "ffn"}
+    if args.no_decode:
+        lines -= {"c5"}
     extra = {}
-    if not args.no_extra:
+    if "gemv_extra" in lines:
         extra_gemv_lines(ctx, torch, stream, weights, acts1, extra)
+    if "act_quant" in lines:
         act_quant_lines(ctx, torch, stream, args.steps, extra)
+    if "matmul_q" in lines:
         matmul_q_lines(ctx, torch, stream, args.steps, extra)
-    if not args.no_gemm:
+    if "gemm" in lines:
         gemm_lines(ctx, torch, stream, args.steps, extra)
+    if "ffn" in lines:
         ffn_block_line(ctx, torch, stream, args.steps, extra)
-    if not args.no_decode:
+    if "c5" in lines:
         decode_c5_line(ctx, torch, stream, args.steps, extra)
     ach = achievable_read(nn, ctx, torch, stream, args.steps)
     log(f"achievable read: {ach}")
