@@ -75,6 +75,11 @@ nnhip_status nnhip_device_count(int* count);
  * 8192 ops per clock on gfx950). No reference counterpart (a measurement aid). */
 nnhip_status nnhip_device_info(int device, int* cus, int* clock_khz, int* mem_clock_khz, int* bus_bits);
 
+/* The device's name and architecture as HIP reports them, e.g. "AMD Instinct MI355X (gfx950:...)",
+ * written NUL-terminated into buf (truncated to len - 1 characters). Fills EngineInfo::device of
+ * ComputeEngine::describe (docs/internal/23-library-design-cleanup-and-model-file-roles.md:240-246). */
+nnhip_status nnhip_device_name(int device, char* buf, size_t len);
+
 /* Create a context bound to `device` with its own stream (default priority).
  * Replaces nn::create_gpu_engine(const char* device) (cli/cli_engine_factory.hpp:51-76). */
 nnhip_status nnhip_ctx_create(int device, nnhip_ctx** out);
@@ -111,6 +116,13 @@ nnhip_status nnhip_free(nnhip_ctx* ctx, void* ptr);
 nnhip_status nnhip_memcpy_h2d(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes);
 nnhip_status nnhip_memcpy_d2h(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes);
 nnhip_status nnhip_memcpy_d2d(nnhip_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* Precision casts at the engine boundary: f32 -> IEEE binary16 (round to nearest even; overflow to
+ * infinity, NaN stays NaN) and binary16 -> f32 (exact). The reference's public engine entries cast
+ * F16 tensors to the f32 of their implementation and their results to the requested precision
+ * (docs/development/04-compute-engine-development.md:110-114); these are those casts. */
+nnhip_status nnhip_convert_f32_f16(nnhip_ctx* ctx, const float* src, size_t n, uint16_t* dst);
+nnhip_status nnhip_convert_f16_f32(nnhip_ctx* ctx, const uint16_t* src, size_t n, float* dst);
 
 /* Fill `words` u32 words with `value` using a kernel (safe inside a captured graph). */
 nnhip_status nnhip_fill_u32(nnhip_ctx* ctx, void* dst, uint32_t value, size_t words);

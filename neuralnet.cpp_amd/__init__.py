@@ -71,6 +71,9 @@ SIGNATURES = {
     "nnhip_memcpy_d2h": (_st, [_vp, _vp, _vp, _sz]),
     "nnhip_memcpy_d2d": (_st, [_vp, _vp, _vp, _sz]),
     "nnhip_fill_u32": (_st, [_vp, _vp, ctypes.c_uint32, _sz]),
+    "nnhip_device_name": (_st, [ctypes.c_int, ctypes.c_char_p, _sz]),
+    "nnhip_convert_f32_f16": (_st, [_vp, _vp, _sz, _vp]),
+    "nnhip_convert_f16_f32": (_st, [_vp, _vp, _sz, _vp]),
     "nnhip_row_absmean": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_trit_pack": (_st, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "nnhip_col_reduce_max": (_st, [_vp, _vp, _sz, _sz, _vp]),
@@ -195,6 +198,13 @@ def device_info(device: int = 0) -> dict:
     v = [ctypes.c_int(0) for _ in range(4)]
     _check(lib().nnhip_device_info(device, *[ctypes.byref(x) for x in v]), "nnhip_device_info")
     return {"cus": v[0].value, "clock_khz": v[1].value, "mem_clock_khz": v[2].value, "bus_bits": v[3].value}
+
+
+def device_name(device: int = 0) -> str:
+    """HIP's name and architecture of a device (nnhip_device_name)."""
+    buf = ctypes.create_string_buffer(256)
+    _check(lib().nnhip_device_name(device, buf, 256), "nnhip_device_name")
+    return buf.value.decode(errors="replace")
 
 
 def kp(K: int) -> int:
@@ -635,6 +645,24 @@ class Context:
         self._bind_stream()
         _check(lib().nnhip_copy_columns(self.h, self._dev(src, torch.float32, "src"), rows, cols, col0, stride, n,
                                         self._dev(Y, torch.float32, "dst")), "nnhip_copy_columns")
+        return Y
+
+    def to_f16(self, x, out=None):
+        """f32 -> binary16 (round to nearest even), as a torch.float16 tensor."""
+        torch = self._torch
+        Y = out if out is not None else self._empty(tuple(x.shape), torch.float16)
+        self._bind_stream()
+        _check(lib().nnhip_convert_f32_f16(self.h, self._dev(x, torch.float32, "x"), x.numel(),
+                                           self._dev(Y, torch.float16, "out")), "nnhip_convert_f32_f16")
+        return Y
+
+    def to_f32(self, x, out=None):
+        """binary16 -> f32 (exact)."""
+        torch = self._torch
+        Y = out if out is not None else self._empty(tuple(x.shape), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_convert_f16_f32(self.h, self._dev(x, torch.float16, "x"), x.numel(),
+                                           self._dev(Y, torch.float32, "out")), "nnhip_convert_f16_f32")
         return Y
 
     def add(self, x, y, out=None):

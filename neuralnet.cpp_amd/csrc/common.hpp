@@ -132,6 +132,8 @@ constexpr uint32_t kGemvLdsBudget = 48 * 1024;
 
 // ---- reference-layout kernels (k_ref.hip)
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* dst, uint32_t value, size_t words);
+hipError_t launch_f32_to_f16(hipStream_t st, const float* src, size_t n, uint16_t* dst);
+hipError_t launch_f16_to_f32(hipStream_t st, const uint16_t* src, size_t n, float* dst);
 // Quantize X (K, M) f32 with a known per-token absmax (float bits in amax[M], as the gated GEMM
 // epilogue leaves them) into token-major xi (M, Kp) + s + rowsum; resets amax to 0.
 hipError_t launch_quant_amax(hipStream_t st, const float* X, size_t K, size_t M, uint32_t* amax, int8_t* xi,

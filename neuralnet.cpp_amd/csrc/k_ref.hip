@@ -22,6 +22,19 @@ inline unsigned grid_for(size_t n, int per_block = kBlock)
     return (unsigned)g;
 }
 
+// f32 -> IEEE binary16, round to nearest even (overflow -> inf, NaN stays NaN), and back (exact)
+__global__ void k_f32_to_f16(const float* __restrict__ src, size_t n, uint16_t* __restrict__ dst)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = __builtin_bit_cast(uint16_t, (_Float16)src[i]);
+}
+
+__global__ void k_f16_to_f32(const uint16_t* __restrict__ src, size_t n, float* __restrict__ dst)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = (float)__builtin_bit_cast(_Float16, src[i]);
+}
+
 __global__ void k_fill_u32(uint32_t* __restrict__ dst, uint32_t value, size_t words)
 {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
@@ -281,6 +294,20 @@ hipError_t launch_stream_xor(hipStream_t st, const void* src, size_t bytes, uint
     hipLaunchKernelGGL(k_stream_xor, dim3((unsigned)g), dim3(kBlock), 0, st, static_cast<const u32x4*>(src), n16,
                        static_cast<const uint32_t*>(src) + n16 * 4, ntail, part);
     hipLaunchKernelGGL(k_xor_fold, dim3(1), dim3(kBlock), 0, st, part, (int)g, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_to_f16(hipStream_t st, const float* src, size_t n, uint16_t* dst)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_f32_to_f16, dim3(grid_for(n)), dim3(kBlock), 0, st, src, n, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_f16_to_f32(hipStream_t st, const uint16_t* src, size_t n, float* dst)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_f16_to_f32, dim3(grid_for(n)), dim3(kBlock), 0, st, src, n, dst);
     return hipGetLastError();
 }
 

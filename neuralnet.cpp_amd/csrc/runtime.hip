@@ -453,6 +453,46 @@ nnhip_status nnhip_device_info(int device, int* cus, int* clock_khz, int* mem_cl
     return NNHIP_OK;
 }
 
+nnhip_status nnhip_device_name(int device, char* buf, size_t len)
+{
+    const char* fn = "nnhip_device_name";
+    NNHIP_REQUIRE(buf && len > 0, fn, "null or empty output buffer");
+    buf[0] = '\0';
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+    {
+        (void)hipGetLastError();
+        return fail(NNHIP_ERR_NO_DEVICE, fn, "no HIP device visible");
+    }
+    NNHIP_REQUIRE(device >= 0 && device < n, fn, "device index out of range");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(fn, "hipGetDeviceProperties", e);
+    std::snprintf(buf, len, "%s (%s)", prop.name, prop.gcnArchName);
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_convert_f32_f16(nnhip_ctx* ctx, const float* src, size_t n, uint16_t* dst)
+{
+    const char* fn = "nnhip_convert_f32_f16";
+    NNHIP_CHECK_CTX(fn);
+    if (n == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(src && dst, fn, "null pointer");
+    NNHIP_LAUNCH(fn, launch_f32_to_f16(ctx->stream, src, n, dst));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_convert_f16_f32(nnhip_ctx* ctx, const uint16_t* src, size_t n, float* dst)
+{
+    const char* fn = "nnhip_convert_f16_f32";
+    NNHIP_CHECK_CTX(fn);
+    if (n == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(src && dst, fn, "null pointer");
+    NNHIP_LAUNCH(fn, launch_f16_to_f32(ctx->stream, src, n, dst));
+    return NNHIP_OK;
+}
+
 nnhip_status nnhip_fill_u32(nnhip_ctx* ctx, void* dst, uint32_t value, size_t words)
 {
     const char* fn = "nnhip_fill_u32";

@@ -43,9 +43,38 @@ Result<void> ComputeEngine::check_owned(const Tensor& t, const char* what) const
     return {};
 }
 
+namespace
+{
+bool is_float(Precision p) { return p == Precision::F32 || p == Precision::F16; }
+}  // namespace
+
+Result<Tensor> ComputeEngine::widen_f32(const Tensor& t)
+{
+    if (t.precision() != Precision::F16) return t;
+    EX_TRY(w, alloc_impl(t.rows(), t.cols(), Precision::F32));
+    if (t.size() > 0) EX_TRY_CHECK(convert_impl(t, *w));
+    return *w;
+}
+
+Result<Tensor> ComputeEngine::narrow_to(const Tensor& y32, Precision p)
+{
+    if (p != Precision::F16) return y32;
+    EX_TRY(n, alloc_impl(y32.rows(), y32.cols(), Precision::F16));
+    if (y32.size() > 0) EX_TRY_CHECK(convert_impl(y32, *n));
+    return *n;
+}
+
 Tensor ComputeEngine::create_tensor(std::size_t rows, std::size_t cols, Precision p, InitSpec init)
 {
-    if (p != Precision::F32) return Tensor{};
+    if (!is_float(p)) return Tensor{};
+    if (p == Precision::F16)
+    {
+        // the f32 values, rounded once
+        const Tensor f = create_tensor(rows, cols, Precision::F32, init);
+        if (!f.valid()) return Tensor{};
+        auto h = narrow_to(f, Precision::F16);
+        return h ? *h : Tensor{};
+    }
     auto t = alloc_impl(rows, cols, p);
     if (!t) return Tensor{};
     std::vector<float> host(rows * cols, 0.0f);
@@ -63,19 +92,28 @@ Tensor ComputeEngine::create_tensor(std::size_t rows, std::size_t cols, Precisio
 
 Result<Tensor> ComputeEngine::from_matrix(const Matrix& m, Precision p)
 {
-    if (p != Precision::F32)
+    if (!is_float(p))
         return Error{std::string("from_matrix: precision ") + precision_name(p) + " is not supported by this engine"};
-    EX_TRY(t, alloc_impl(m.rows(), m.cols(), p));
+    EX_TRY(t, alloc_impl(m.rows(), m.cols(), Precision::F32));
     if (m.size() > 0) EX_TRY_CHECK(upload_impl(*t, m.data(), m.size() * sizeof(float)));
-    return *t;
+    return narrow_to(*t, p);   // F16: each value rounded to nearest even
 }
 
+// P is the precision of the values handed back: F32 widens f16 storage exactly; F16 rounds f32
+// storage to binary16 first (the matrix itself holds floats).
 Result<Matrix> ComputeEngine::to_matrix(const Tensor& t, Precision p)
 {
     EX_TRY_CHECK(check_owned(t, "to_matrix"));
-    if (p != Precision::F32) return Error{"to_matrix: only f32 output is supported"};
+    if (!is_float(p)) return Error{std::string("to_matrix: precision ") + precision_name(p) + " is not supported"};
+    Tensor src = t;
+    if (p == Precision::F16 && t.precision() == Precision::F32)
+    {
+        EX_TRY(h, narrow_to(t, Precision::F16));
+        src = *h;
+    }
+    EX_TRY(w, widen_f32(src));
     Matrix m(t.rows(), t.cols());
-    if (m.size() > 0) EX_TRY_CHECK(download_impl(t, m.data(), m.size() * sizeof(float)));
+    if (m.size() > 0) EX_TRY_CHECK(download_impl(*w, m.data(), m.size() * sizeof(float)));
     return m;
 }
 
@@ -87,6 +125,12 @@ Result<void> ComputeEngine::copy_from(Tensor& dst, const Matrix& src)
         return Error{"copy_from: shape mismatch (tensor " + shape(dst) + ", matrix " + std::to_string(src.rows()) +
                      "x" + std::to_string(src.cols()) + ")"};
     if (src.size() == 0) return {};
+    if (dst.precision() == Precision::F16)
+    {
+        EX_TRY(f, alloc_impl(src.rows(), src.cols(), Precision::F32));
+        EX_TRY_CHECK(upload_impl(*f, src.data(), src.size() * sizeof(float)));
+        return convert_impl(*f, dst);
+    }
     return upload_impl(dst, src.data(), src.size() * sizeof(float));
 }
 
@@ -98,7 +142,7 @@ Result<void> ComputeEngine::copy_into(Tensor& dst, const Tensor& src)
     if (dst.rows() != src.rows() || dst.cols() != src.cols() || dst.precision() != src.precision())
         return Error{"copy_into: shape or precision mismatch (" + shape(dst) + " vs " + shape(src) + ")"};
     if (dst.same_storage(src) || dst.size() == 0) return {};
-    return copy_impl(dst, src, dst.size() * sizeof(float));
+    return copy_impl(dst, src, dst.size() * element_bytes(dst.precision()));
 }
 
 Result<Tensor> ComputeEngine::trit_pack(const Tensor& W, const Tensor& tau)
@@ -194,7 +238,8 @@ Result<Tensor> ComputeEngine::matmul_q_i8(const Tensor& wq, const Tensor& tau, c
     EX_TRY_CHECK(check_owned(tau, "matmul_q_i8: tau"));
     EX_TRY_CHECK(check_owned(xq, "matmul_q_i8: xq"));
     EX_TRY_CHECK(check_owned(s, "matmul_q_i8: s"));
-    if (p != Precision::F32) return Error{"matmul_q_i8: only f32 output is supported by this engine"};
+    if (!is_float(p)) return Error{"matmul_q_i8: output precision must be f32 or f16"};
+    EX_TRY_CHECK(require_f32(s, "matmul_q_i8", "s"));
     const std::size_t N = wq.rows(), K = xq.rows(), M = s.cols();
     if (s.rows() != 1) return Error{"matmul_q_i8: s must be (1, M), got " + shape(s)};
     if (wq.cols() != trit_pack::words_per_row(K))
@@ -204,7 +249,7 @@ Result<Tensor> ComputeEngine::matmul_q_i8(const Tensor& wq, const Tensor& tau, c
     if (tau.rows() != N || tau.cols() != 1) return Error{"matmul_q_i8: tau must be (N,1), got " + shape(tau)};
     EX_TRY(y, alloc_impl(N, M, Precision::F32));
     EX_TRY_CHECK(matmul_q_i8_impl(wq, tau, xq, s, *y));
-    return *y;
+    return narrow_to(*y, p);
 }
 
 Result<Tensor> ComputeEngine::matmul_q(const Tensor& wq, const Tensor& tau, const Tensor& B, Precision p)
@@ -212,15 +257,16 @@ Result<Tensor> ComputeEngine::matmul_q(const Tensor& wq, const Tensor& tau, cons
     EX_TRY_CHECK(check_owned(wq, "matmul_q: wq"));
     EX_TRY_CHECK(check_owned(tau, "matmul_q: tau"));
     EX_TRY_CHECK(check_owned(B, "matmul_q: B"));
-    EX_TRY_CHECK(require_f32(B, "matmul_q", "B"));
-    if (p != Precision::F32) return Error{"matmul_q: only f32 output is supported by this engine"};
+    if (!is_float(B.precision())) return Error{"matmul_q: B must be f32 or f16"};
+    if (!is_float(p)) return Error{"matmul_q: output precision must be f32 or f16"};
     const std::size_t N = wq.rows(), K = B.rows(), M = B.cols();
     if (wq.cols() != trit_pack::words_per_row(K))
         return Error{"matmul_q: wq " + shape(wq) + " does not match K=" + std::to_string(K)};
     if (tau.rows() != N || tau.cols() != 1) return Error{"matmul_q: tau must be (N,1), got " + shape(tau)};
+    EX_TRY(b32, widen_f32(B));
     EX_TRY(y, alloc_impl(N, M, Precision::F32));
-    EX_TRY_CHECK(matmul_q_impl(wq, tau, B, *y));
-    return *y;
+    EX_TRY_CHECK(matmul_q_impl(wq, tau, *b32, *y));
+    return narrow_to(*y, p);
 }
 
 Result<Tensor> ComputeEngine::matmul_q_t(const Tensor& A, const Tensor& tau, const Tensor& B, std::size_t M,
@@ -229,16 +275,17 @@ Result<Tensor> ComputeEngine::matmul_q_t(const Tensor& A, const Tensor& tau, con
     EX_TRY_CHECK(check_owned(A, "matmul_q_t: A"));
     EX_TRY_CHECK(check_owned(tau, "matmul_q_t: tau"));
     EX_TRY_CHECK(check_owned(B, "matmul_q_t: B"));
-    EX_TRY_CHECK(require_f32(B, "matmul_q_t", "B"));
-    if (p != Precision::F32) return Error{"matmul_q_t: only f32 output is supported by this engine"};
+    if (!is_float(B.precision())) return Error{"matmul_q_t: B must be f32 or f16"};
+    if (!is_float(p)) return Error{"matmul_q_t: output precision must be f32 or f16"};
     const std::size_t K = A.rows(), N = B.cols();
     if (A.cols() != trit_pack::words_per_row(M))
         return Error{"matmul_q_t: A " + shape(A) + " does not hold M=" + std::to_string(M) + " columns"};
     if (B.rows() != K) return Error{"matmul_q_t: B " + shape(B) + " does not match K=" + std::to_string(K)};
     if (tau.rows() != K || tau.cols() != 1) return Error{"matmul_q_t: tau must be (K,1), got " + shape(tau)};
+    EX_TRY(b32, widen_f32(B));
     EX_TRY(y, alloc_impl(M, N, Precision::F32));
-    EX_TRY_CHECK(matmul_q_t_impl(A, tau, B, M, *y));
-    return *y;
+    EX_TRY_CHECK(matmul_q_t_impl(A, tau, *b32, M, *y));
+    return narrow_to(*y, p);
 }
 
 Result<Tensor> ComputeEngine::add_row_broadcast(const Tensor& y, const Tensor& b)
@@ -247,9 +294,12 @@ Result<Tensor> ComputeEngine::add_row_broadcast(const Tensor& y, const Tensor& b
     EX_TRY_CHECK(check_owned(b, "add_row_broadcast: b"));
     if (b.rows() != y.rows() || b.cols() != 1)
         return Error{"add_row_broadcast: b must be (" + std::to_string(y.rows()) + ",1), got " + shape(b)};
+    if (!is_float(y.precision())) return Error{"add_row_broadcast: y must be f32 or f16"};
+    EX_TRY_CHECK(require_f32(b, "add_row_broadcast", "b"));
+    EX_TRY(y32, widen_f32(y));
     EX_TRY(out, alloc_impl(y.rows(), y.cols(), Precision::F32));
-    EX_TRY_CHECK(add_row_broadcast_impl(y, b, *out));
-    return *out;
+    EX_TRY_CHECK(add_row_broadcast_impl(*y32, b, *out));
+    return narrow_to(*out, y.precision());
 }
 
 Result<Tensor> ComputeEngine::rmsnorm(const Tensor& x, const Tensor& gamma, Scalar eps)
@@ -270,17 +320,23 @@ Result<Tensor> ComputeEngine::bitlinear_i8_forward(const Tensor& x, const Tensor
     EX_TRY_CHECK(check_owned(wq, "bitlinear_i8_forward: wq"));
     EX_TRY_CHECK(check_owned(tau, "bitlinear_i8_forward: tau"));
     EX_TRY_CHECK(check_owned(b, "bitlinear_i8_forward: b"));
-    if (p != Precision::F32) return Error{"bitlinear_i8_forward: only f32 output is supported by this engine"};
+    if (!is_float(p)) return Error{"bitlinear_i8_forward: output precision must be f32 or f16"};
+    if (!is_float(x.precision())) return Error{"bitlinear_i8_forward: x must be f32 or f16"};
     if (wq.cols() != trit_pack::words_per_row(x.rows()))
         return Error{"bitlinear_i8_forward: wq " + shape(wq) + " does not match input rows " + std::to_string(x.rows())};
     if (tau.rows() != wq.rows() || b.rows() != wq.rows())
         return Error{"bitlinear_i8_forward: tau / bias rows do not match wq"};
-    return bitlinear_i8_impl(x, wq, tau, b, xq_out, s_out);
+    EX_TRY(x32, widen_f32(x));
+    if (p == Precision::F32) return bitlinear_i8_impl(*x32, wq, tau, &b, xq_out, s_out);
+    // f16: y = matmul_q_i8(..., F16), then y + b in F16 (compute_layer_bitlinear.hpp:454-456)
+    EX_TRY(y, bitlinear_i8_impl(*x32, wq, tau, nullptr, xq_out, s_out));
+    EX_TRY(y16, narrow_to(*y, Precision::F16));
+    return add_row_broadcast(*y16, b);
 }
 
 // Default composition, exactly the reference layer's call sequence
 // (include/neuralnet.cpp/compute_layer_bitlinear.hpp:443-456).
-Result<Tensor> ComputeEngine::bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor& b,
+Result<Tensor> ComputeEngine::bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor* b,
                                                 Tensor* xq_out, Tensor* s_out)
 {
     EX_TRY(xabs, abs(x));
@@ -290,7 +346,8 @@ Result<Tensor> ComputeEngine::bitlinear_i8_impl(const Tensor& x, const Tensor& w
     EX_TRY(y, matmul_q_i8(wq, tau, *xq, *sraw));
     if (xq_out) *xq_out = *xq;
     if (s_out) *s_out = *sraw;
-    return add_row_broadcast(*y, b);
+    if (!b) return *y;
+    return add_row_broadcast(*y, *b);
 }
 
 Result<Tensor> ComputeEngine::glu(const Tensor& y1, int act)

@@ -130,7 +130,7 @@ protected:
     Result<Tensor> alloc_impl(std::size_t rows, std::size_t cols, Precision p) override
     {
         auto st = std::make_shared<detail::Storage>();
-        st->bytes = rows * cols * sizeof(float);
+        st->bytes = rows * cols * element_bytes(p);
         EX_TRY(mem, device_alloc(st->bytes));
         st->mem = *mem;
         st->owner = this;
@@ -153,6 +153,24 @@ protected:
     {
         NNHIP_TRY(nnhip_memcpy_d2d(ctx_->h, TensorAccess::ptr(dst), TensorAccess::ptr(src), bytes), "copy");
         return {};
+    }
+
+    Result<void> convert_impl(const Tensor& src, const Tensor& dst) override
+    {
+        if (src.precision() == Precision::F32 && dst.precision() == Precision::F16)
+        {
+            NNHIP_TRY(nnhip_convert_f32_f16(ctx_->h, fp(src), src.size(), static_cast<uint16_t*>(TensorAccess::ptr(dst))),
+                      "f32 -> f16");
+            return {};
+        }
+        if (src.precision() == Precision::F16 && dst.precision() == Precision::F32)
+        {
+            NNHIP_TRY(nnhip_convert_f16_f32(ctx_->h, static_cast<const uint16_t*>(TensorAccess::ptr(src)), src.size(),
+                                            fpw(dst)),
+                      "f16 -> f32");
+            return {};
+        }
+        return Error{"convert: only f32 <-> f16"};
     }
 
     Result<void> trit_pack_impl(const Tensor& W, const Tensor& tau, const Tensor& out) override
@@ -403,7 +421,7 @@ protected:
         return src && src.get() == TensorAccess::storage(x) && last_quant_->epoch == x.write_epoch();
     }
 
-    Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor& b,
+    Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau, const Tensor* b,
                                      Tensor* xq_out, Tensor* s_out) override
     {
         const std::size_t K = x.rows(), M = x.cols(), N = wq.rows();
@@ -446,7 +464,7 @@ protected:
             last_quant_ = LastQuant{TensorAccess::storage_ref(x), x.write_epoch(), K, M, s, xq};
             if (xq_out) *xq_out = xq;
         }
-        NNHIP_TRY(nnhip_ternary_matmul(ctx_->h, *rp, fp(tau), xi, fp(s), rs, fp(b), N, K, M, fpw(*y)),
+        NNHIP_TRY(nnhip_ternary_matmul(ctx_->h, *rp, fp(tau), xi, fp(s), rs, b ? fp(*b) : nullptr, N, K, M, fpw(*y)),
                   "bitlinear_i8_forward (ternary product)");
         if (s_out) *s_out = s;
         return *y;
@@ -520,7 +538,11 @@ protected:
     {
         EngineInfo i;
         i.engine = "hip";
-        i.device = "MI355X (gfx950) #" + std::to_string(device_);
+        char name[256] = {};
+        if (nnhip_device_name(device_, name, sizeof(name)) == NNHIP_OK)
+            i.device = std::string(name) + " #" + std::to_string(device_);
+        else
+            i.device = "HIP device #" + std::to_string(device_);
         i.ternary_gemm = true;
         i.int8_dot = true;
         i.int8_dot_accelerated = true;

@@ -12,6 +12,11 @@
 //   * Tensor is a value type with shared storage: a copy aliases the same device buffer;
 //   * packed containers (ternary words, int8 words) are Precision::F32 tensors holding raw
 //     32-bit words, transferred bitwise (docs/internal/21-quantized-weights.md:649-652);
+//   * F16 tensors hold IEEE binary16 values (2 bytes each). The public entries of the
+//     BitLinear products cast F16 operands to f32 and their f32 result to the requested
+//     precision P (round to nearest even), the reference NVI's boundary cast
+//     (docs/development/04-compute-engine-development.md:110-114); from_matrix / to_matrix
+//     convert at the host boundary (to_matrix widens f16 exactly, src/test_common.hpp:84-91);
 //   * every write entry advances the destination storage's write epoch, which BitLinear
 //     uses to know when its quantized weights are stale (AGENTS.md:160-164).
 
@@ -30,6 +35,12 @@ namespace nn
 {
 
 inline constexpr std::uint64_t kInitSeed = 0x5EEDB17Aull;
+
+// Bytes per element of a tensor's storage (packed containers are F32 tensors of raw words).
+[[nodiscard]] inline constexpr std::size_t element_bytes(Precision p) noexcept
+{
+    return p == Precision::F16 ? 2 : 4;
+}
 
 struct InitSpec
 {
@@ -158,15 +169,18 @@ public:
                                           Precision p = Precision::F32);
     [[nodiscard]] Result<Tensor> matmul_q_t(const Tensor& A, const Tensor& tau, const Tensor& B, std::size_t M,
                                             Precision p = Precision::F32);
-    // y + row_broadcast(b)
+    // y + row_broadcast(b), computed in f32 and returned in y's precision
     [[nodiscard]] Result<Tensor> add_row_broadcast(const Tensor& y, const Tensor& b);
     // RMSNorm forward: (x * rsqrt(mean_f x^2 + eps)) * gamma, per column (token)
     [[nodiscard]] Result<Tensor> rmsnorm(const Tensor& x, const Tensor& gamma, Scalar eps);
 
     // Fused BitLinear int8 forward, the sequence of compute_layer_bitlinear.hpp:443-456:
-    // s = col_reduce_max(|x|) * fl(1/127); xq = quantize_i8(x, s); y = matmul_q_i8(wq, tau, xq, s) + b.
-    // xq_out / s_out (nullable) receive the activation cache of the reference layer.
-    // The default implementation composes the primitives; an engine may fuse them.
+    // s = col_reduce_max(|x|) * fl(1/127); xq = quantize_i8(x, s); y = matmul_q_i8(wq, tau, xq, s, p);
+    // out = y + row_broadcast(b) in p. With p = F32 the bias rides in the product's epilogue (one
+    // launch); with p = F16, y is rounded to f16 and the bias added to it in f32 and rounded
+    // again, the reference's two steps. xq_out / s_out (nullable) receive the activation cache of
+    // the reference layer. The default implementation composes the primitives; an engine may
+    // fuse them.
     [[nodiscard]] Result<Tensor> bitlinear_i8_forward(const Tensor& x, const Tensor& wq, const Tensor& tau,
                                                       const Tensor& b, Precision p, Tensor* xq_out, Tensor* s_out);
 
@@ -235,8 +249,11 @@ protected:
     [[nodiscard]] virtual Result<void> add_row_broadcast_impl(const Tensor& y, const Tensor& b, const Tensor& out) = 0;
     [[nodiscard]] virtual Result<void> rmsnorm_impl(const Tensor& x, const Tensor& gamma, Scalar eps,
                                                     const Tensor& out) = 0;
+    // b may be null (no bias); x is f32 here (the public entry casts f16 inputs)
     [[nodiscard]] virtual Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau,
-                                                           const Tensor& b, Tensor* xq_out, Tensor* s_out);
+                                                           const Tensor* b, Tensor* xq_out, Tensor* s_out);
+    // elementwise precision cast between equal-shape tensors (F32 <-> F16)
+    [[nodiscard]] virtual Result<void> convert_impl(const Tensor& src, const Tensor& dst) = 0;
     [[nodiscard]] virtual Result<void> glu_impl(const Tensor& y1, int act, const Tensor& out) = 0;
     [[nodiscard]] virtual Result<Tensor> ffn_glu_i8_impl(const Tensor& x, const Tensor* gamma, Scalar eps,
                                                          const Tensor& wq1, const Tensor& tau1, const Tensor& b1,
@@ -257,6 +274,10 @@ protected:
 
     // helpers for implementations
     [[nodiscard]] Result<void> check_owned(const Tensor& t, const char* what) const;
+    // t as f32 (F16 tensors are widened into a new tensor; F32 tensors are returned as they are)
+    [[nodiscard]] Result<Tensor> widen_f32(const Tensor& t);
+    // an f32 result in precision p (rounded into a new F16 tensor when p is F16)
+    [[nodiscard]] Result<Tensor> narrow_to(const Tensor& y32, Precision p);
 };
 
 // int32 index vectors (positions, token ids) as (n, 1) containers of raw words, and back

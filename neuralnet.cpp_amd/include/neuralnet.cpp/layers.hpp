@@ -294,16 +294,18 @@ public:
         if (packed_only_ && !(wq_packed_.valid() && tau_.valid()))
             return Error{"BitLinear(packed-only): deploy weights / tau missing"};
         if (needs_quantize_()) EX_TRY_CHECK(quantize_weights_());
+        // the compute slot sets the precision of the product and of the bias add (:454-456, :464-466)
+        const Precision P = p_.compute == Precision::F16 ? Precision::F16 : Precision::F32;
         if (!act_quant_)
         {
-            // f32-activation branch (:459-466): one ternary x float product, then the bias.
+            // float-activation branch (:459-466): one ternary x float product, then the bias.
             input_cache_ = input;
             act_scale_ = Tensor{};
-            EX_TRY(y, engine.matmul_q(wq_packed_, tau_, input, Precision::F32));
+            EX_TRY(y, engine.matmul_q(wq_packed_, tau_, input, P));
             return engine.add_row_broadcast(*y, b_);
         }
         Tensor xq, s;
-        EX_TRY(y, engine.bitlinear_i8_forward(input, wq_packed_, tau_, b_, Precision::F32, &xq, &s));
+        EX_TRY(y, engine.bitlinear_i8_forward(input, wq_packed_, tau_, b_, P, &xq, &s));
         input_cache_ = xq;
         act_scale_ = s;
         return *y;

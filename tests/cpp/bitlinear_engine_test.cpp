@@ -28,6 +28,10 @@
 //       the reference single-sequence signature per sequence; GPTBlock::forward_step == its
 //       composition of engine calls bit for bit; GPTModel greedy generation == forward_step +
 //       the reference greedy loop on the host
+//  [15] compute = F16                      src/t1_58_test.cpp [7a] (:407-460), [9] (:668-690),
+//       compute_layer_bitlinear.hpp:454-456, :464-466: f16 tensors at the host boundary, BitLinear
+//       under profile_t1_58 in both branches = its f32 output rounded as the reference's f16
+//       product and f16 bias add, f16 inputs; cli::create_engine in the reference's shape
 // Exit: 0 pass, 1 fail, 77 skip (no gfx950 device).
 #include <algorithm>
 #include <array>
@@ -1208,6 +1212,91 @@ void test_decoder(nn::ComputeEngine& e)
         CHECK(!too_long.has_value(), "prompt + new tokens beyond max_len is refused");
     }
 }
+// ---------------------------------------------------------------- [15]
+// binary16 rounding on the host (round to nearest even), widened back: fl16(v)
+float fl16(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+
+// one BitLinear of the given profile with latent weights W, bias b and the branch chosen
+std::unique_ptr<nn::BitLinear> make_bitlinear(nn::ComputeEngine& e, const nn::PrecisionProfile& prof,
+                                              const nn::Matrix& W, const nn::Matrix& b, bool act_quant)
+{
+    auto bl = std::make_unique<nn::BitLinear>(W.cols(), W.rows());
+    bl->set_precision_profile(prof);
+    auto r = bl->init(e);
+    EX_UNWRAP(r.has_value(), "BitLinear init failed");
+    EX_UNWRAP(e.copy_from(bl->parameters()[0].get(), W).has_value(), "latent upload failed");
+    EX_UNWRAP(e.copy_from(bl->parameters()[1].get(), b).has_value(), "bias upload failed");
+    bl->set_activation_quant(act_quant);
+    return bl;
+}
+
+void test_f16_compute(nn::ComputeEngine& e)
+{
+    std::puts("[15] compute = F16 (profile_t1_58, src/t1_58_test.cpp:668-690): f16 tensors at the host boundary; "
+              "BitLinear's f16 output = the f32 path rounded as the reference's two f16 steps");
+    // host boundary: one rounding to binary16 (nearest even, overflow to inf), exact widening back
+    nn::Matrix m(3, 5);
+    const float vals[15] = {1.0f, 0.1f, -0.3333333f, 65504.0f, 65520.0f, -7e5f, 1e-8f, 6.1e-5f,
+                            3.0f + 0x1p-11f, 3.0f + 0x1p-10f, -0.0f, 2049.0f, 2051.0f, 1234.567f, -1e-3f};
+    for (std::size_t i = 0; i < 15; ++i) m.span()[i] = vals[i];
+    auto t16 = e.from_matrix(m, nn::Precision::F16);
+    CHECK(t16.has_value() && t16->precision() == nn::Precision::F16, "from_matrix(F16) gives an f16 tensor");
+    if (!t16) return;
+    nn::Matrix back = download(e, *t16), want(3, 5);
+    for (std::size_t i = 0; i < 15; ++i) want.span()[i] = fl16(vals[i]);
+    CHECK(bitwise_equal(back, want), "to_matrix of an f16 tensor = the values rounded once to binary16, widened exactly");
+    auto r16 = e.to_matrix(upload(e, m), nn::Precision::F16);
+    CHECK(r16.has_value() && bitwise_equal(*r16, want), "to_matrix(f32 tensor, F16) rounds the values to binary16");
+
+    const nn::PrecisionProfile t1 = nn::profile_t1_58();
+    nn::PrecisionProfile f32p;
+    f32p.param = nn::Precision::T1_58;
+    constexpr std::size_t IN = 300, OUT = 70, B = 9;
+    const nn::Matrix W = random_matrix(OUT, IN, 1501);
+    const nn::Matrix X = random_matrix(IN, B, 1502);
+    nn::Matrix zero(OUT, 1), bias = random_matrix(OUT, 1, 1503);
+    for (std::size_t o = 0; o < OUT; ++o) zero.set_value(o, 0, 0.0f);
+    for (const bool act : {true, false})
+    {
+        const char* br = act ? "int8 branch" : "float branch";
+        // bias 0: the f16 output is the f32 output rounded once
+        auto a32 = make_bitlinear(e, f32p, W, zero, act);
+        auto a16 = make_bitlinear(e, t1, W, zero, act);
+        auto y32 = a32->forward(upload(e, X));
+        auto y16 = a16->forward(upload(e, X));
+        CHECK(y32.has_value() && y16.has_value(), "f32 and f16 forwards succeed");
+        if (!y32 || !y16) return;
+        CHECK(y16->precision() == nn::Precision::F16 && y32->precision() == nn::Precision::F32,
+              "the compute slot sets the output precision");
+        const nn::Matrix Y32 = download(e, *y32), Y16 = download(e, *y16);
+        nn::Matrix r(OUT, B);
+        for (std::size_t i = 0; i < r.size(); ++i) r.span()[i] = fl16(Y32.span()[i]);
+        std::printf("    %s, bias 0:\n", br);
+        CHECK(bitwise_equal(Y16, r), "f16 output = fl16(f32 output) bit for bit");
+        // nonzero bias: y = product rounded to f16, then fl16(y + b) (compute_layer_bitlinear.hpp:454-456, :464-466)
+        auto b16 = make_bitlinear(e, t1, W, bias, act);
+        auto yb = b16->forward(upload(e, X));
+        CHECK(yb.has_value(), "f16 forward with a bias succeeds");
+        if (!yb) return;
+        const nn::Matrix YB = download(e, *yb);
+        const nn::Matrix bh = download(e, b16->bias());
+        nn::Matrix rb(OUT, B);
+        for (std::size_t o = 0; o < OUT; ++o)
+            for (std::size_t c = 0; c < B; ++c) rb.set_value(o, c, fl16(fl16(Y32.at(o, c)) + bh.at(o, 0)));
+        std::printf("    %s, bias:\n", br);
+        CHECK(bitwise_equal(YB, rb), "f16 output = fl16(fl16(product) + b) bit for bit");
+        // f16 input (the reference uploads activations in the compute precision): widened exactly first
+        auto x16 = e.from_matrix(X, nn::Precision::F16);
+        nn::Matrix Xr(IN, B);
+        for (std::size_t i = 0; i < Xr.size(); ++i) Xr.span()[i] = fl16(X.span()[i]);
+        auto y_in16 = a16->forward(*x16);
+        auto y_inr = a16->forward(upload(e, Xr));
+        CHECK(y_in16.has_value() && y_inr.has_value() &&
+                  bitwise_equal(download(e, *y_in16), download(e, *y_inr)),
+              "an f16 input equals its widened f32 values");
+    }
+    CHECK(e.describe().device.find("gfx950") != std::string::npos, "EngineInfo.device is HIP's device name (gfx950)");
+}
 }  // namespace
 
 int main(int argc, char** argv)
@@ -1217,9 +1306,9 @@ int main(int argc, char** argv)
     test_layout();
     test_factory();
     test_model_files_host();
-    nn::cli::EngineConfig ec;
-    ec.use_hip = true;
-    auto eng = nn::cli::create_engine(ec);
+    // the reference call site (cli/cli_engine_factory.hpp:32-77): aggregate config, shared_ptr result
+    const nn::cli::EngineConfig ec{true, "0"};
+    nn::Result<std::shared_ptr<nn::ComputeEngine>> eng = nn::cli::create_engine(ec, std::cout);
     if (!eng.has_value())
     {
         std::printf("HIP engine unavailable, skipping device sections: %s\n", eng.error().message.c_str());
@@ -1243,6 +1332,7 @@ int main(int argc, char** argv)
     test_model_files_device(e);
     test_shared_input_quantization(e);
     test_decoder(e);
+    test_f16_compute(e);
     if (g_failures == 0) std::puts("bitlinear_engine_test: all passed");
     else std::printf("bitlinear_engine_test: %d failure(s)\n", g_failures);
     return g_failures == 0 ? 0 : 1;
