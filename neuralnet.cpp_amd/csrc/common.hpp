@@ -183,10 +183,10 @@ hipError_t launch_unrepack(hipStream_t st, const uint32_t* rp, size_t N, size_t 
 hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus);
 // Deep single-problem decode GEMV (all k stages in flight per wave, activations staged in LDS;
 // p.glu selects the gated epilogue into p.y = h). Applies when gemv_deep_ok: KT in {4, 10, 16, 27},
-// M * Kp <= kGemvDeepLds and at most kGemvDeepMaxTilesPerCu row tiles per CU.
+// round_up(M * Kp, 1 KiB) <= kGemvDeepLds and at most kGemvDeepMaxTilesPerCu row tiles per CU.
 constexpr uint32_t kGemvDeepLds = 160 * 1024;
 constexpr int kGemvDeepMaxTilesPerCu = 4;
-bool gemv_deep_ok(const GemvProblem& p, int num_cus);  // also needs round_up(M * Kp, 1 KiB) <= kGemvDeepLds
+bool gemv_deep_ok(const GemvProblem& p, int num_cus);
 hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p);
 // Up to kGemvDeepMulti problems that share K, M and the activations (xi, s, rowsum) in one deep
 // launch; gemv_deep_multi_ok checks the shared shape and the total row tiles.

@@ -296,7 +296,14 @@ __global__ __launch_bounds__(kBlock) void k_gemv_grouped(const GemvProblem* __re
 // q / k / v projections of one input). One 16-row tile per wave; the wave issues the loads of
 // ALL its KT weight stages first (one memory latency instead of KT / depth of them), then the
 // block stages the shared activations (M x Kp bytes, up to 160 KB) into LDS by buffer->LDS DMA
-// while they land. res != 0: y = epilogue + res[n, m] (the decoder's residual add, the same
+// while they land.
+// LDS layout of the staged activations: token-major rows of Kp bytes with the 16-byte units of
+// each 128-byte group permuted per token, unit u of row t holding column u ^ (t & 7). An MFMA
+// operand read (lane = token t of 16-byte column c, 16 tokens) then touches 8 distinct bank
+// groups per 8 lanes; without the permutation all 16 tokens of a column share banks (Kp is a
+// multiple of 256 bytes) and the 16-way conflict made the MFMA loop 3-4x slower than its LDS
+// bandwidth. Each DMA instruction still fetches one contiguous KiB of the activations (lane l
+// takes the unit its LDS slot needs, a permutation within each 128-byte line). res != 0: y = epilogue + res[n, m] (the decoder's residual add, the same
 // single rounding as a separate add). glu != 0: the rows are the interleaved gate/up rows of a
 // gated FFN (16-row tile = gate rows 8t..8t+7, then up rows 8t..8t+7); lanes of the gate half
 // take their up values from the lane 32 apart and store act(gate, up) as features 8t..8t+7 of
@@ -306,8 +313,10 @@ struct GemvDeepArgs
     GemvProblem p[kGemvDeepMulti];
     int tile0[kGemvDeepMulti + 1];  // first row tile of each problem in the launch (prefix sums)
     int count;
-    uint32_t xbytes;
+    uint32_t xbytes;  // M * Kp: the activation bytes
 };
+
+inline size_t gemv_deep_lds_bytes(int M, int KT) { return round_up((size_t)M * KT * kTileK, 1024); }
 
 template <int KT>
 __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvDeepArgs da)
@@ -358,21 +367,32 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvDeepArgs da)
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int nq = (int)((da.xbytes + 1023u) / 1024u);
         for (int q = wave; q < nq; q += kBlock / kWave)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + q * 1024), 16, (uint32_t)lane * 16u,
-                                                     (uint32_t)q * 1024u, 0, 0);
+        {
+            // LDS unit L = (row t, unit u) takes column u ^ (t & 7) of row t (units past the
+            // activations read zeros)
+            const uint32_t L = (uint32_t)q * 64u + (uint32_t)lane;
+            const uint32_t tr = L / (uint32_t)(KT * 16), u = L - tr * (uint32_t)(KT * 16);
+            const uint32_t src = tr * Kp + ((u ^ (tr & 7u)) * 16u);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + q * 1024), 16, src, 0, 0, 0);
+        }
         __syncthreads();
     }
 
     // 4. MFMAs over the k tiles; tokens t >= M read token 0's row (their columns are never stored)
     Acc acc[1];
     acc[0].a0 = acc[0].a1 = acc[0].a2 = acc[0].a3 = v4i{0, 0, 0, 0};
-    const uint8_t* xl = lds + (t < p.M ? t : 0) * Kp + 16 * g;
+    // operand j of stage kt is column c = 16 kt + 4 j + g: unit (4 (j & 1) + g) ^ (t & 7) of the
+    // 128-byte group 2 kt + (j >> 1)
+    const int tr = t < p.M ? t : 0;
+    const uint8_t* xrow = lds + (size_t)tr * Kp;
+    const int sw0 = 16 * (g ^ (tr & 7)), sw1 = 16 * ((4 + g) ^ (tr & 7));
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
     {
         v4i x[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(xl + kt * 256 + 64 * j);
+        for (int j = 0; j < 4; ++j)
+            x[j] = *reinterpret_cast<const v4i*>(xrow + kt * 256 + (j >> 1) * 128 + ((j & 1) ? sw1 : sw0));
         const v4i w1[1] = {w[kt]};
         compute_stage<1>(w1, x, acc);
     }
@@ -427,8 +447,8 @@ hipError_t launch_deep_kt(hipStream_t st, const GemvDeepArgs& da)
         attr = true;
     }
     const unsigned blocks = (unsigned)ceil_div((size_t)da.tile0[da.count], (size_t)(kBlock / kWave));
-    // the last DMA instruction fills a whole KiB (lanes past xbytes read zeros)
-    const uint32_t lds_bytes = (uint32_t)round_up(da.xbytes, 1024);
+    // the last DMA instruction fills a whole KiB (lanes past the activations read zeros)
+    const uint32_t lds_bytes = (uint32_t)gemv_deep_lds_bytes(da.p[0].M, da.p[0].KT);
     hipLaunchKernelGGL(k_gemv_deep<KT>, dim3(blocks), dim3(kBlock), lds_bytes, st, da);
     return hipGetLastError();
 }
@@ -458,9 +478,8 @@ bool gemv_deep_multi_ok(const GemvProblem* ps, int count, int num_cus)
             return false;
         tiles += ceil_div((size_t)ps[i].N, 16);
     }
-    const size_t xbytes = (size_t)p.M * (size_t)p.KT * kTileK;
     const bool kt_ok = p.KT == 4 || p.KT == 10 || p.KT == 16 || p.KT == 27;
-    return kt_ok && round_up(xbytes, 1024) <= kGemvDeepLds &&
+    return kt_ok && p.M >= 1 && p.M <= kGemvMaxM && gemv_deep_lds_bytes(p.M, p.KT) <= kGemvDeepLds &&
            tiles <= (size_t)kGemvDeepMaxTilesPerCu * (size_t)(num_cus > 0 ? num_cus : 256);
 }
 
