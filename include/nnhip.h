@@ -313,6 +313,32 @@ nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const floa
                                       const float* s, const int32_t* rowsum, const float* bias, const float* res,
                                       size_t N, size_t K, size_t M, float* Y);
 
+/* Split-k partial sums of a decode ternary GEMV, without the epilogue: part[ks][m][n] (int32,
+ * slices x M x N, token-major) = sum over slice ks of the k tiles of trit-code(n, k) * xi(m, k), the
+ * integer dot products of nnhip_ternary_matmul's MFMAs, the K range cut into `slices` runs of
+ * ceil(K/256 / slices) k tiles (each non-empty; slices in [1, 8], M <= 16). The slices add up
+ * exactly to the whole-K sum; nnhip_partial_residual_quant_i8 applies the epilogue. For decode
+ * BitLinears whose row count alone leaves most CUs idle (N = 2560: 40 work-groups of the
+ * whole-K GEMV): the same weights stream from more CUs. The first half of
+ * BitLinear::forward's int8 product (include/neuralnet.cpp/compute_layer_bitlinear.hpp:449-466). */
+nnhip_status nnhip_ternary_matmul_partial(nnhip_ctx* ctx, const void* rp, const int8_t* xi, size_t N, size_t K,
+                                          size_t M, size_t slices, int32_t* part);
+
+/* The epilogue of nnhip_ternary_matmul_partial, the residual add and the next BitLinear's
+ * quantizer in one kernel per token:
+ *   x_out[n, m] = (tau[n] * s_in[m]) * float(sum_ks part[ks][m][n] - 2 rowsum_in[m]) [+ bias[n]]
+ *                 [+ res[n, m]]          (res may alias x_out; bias, res nullable)
+ *   then [RMSNorm(gamma, eps) when gamma is non-null ->] per-token absmax -> int8: xi, s, rowsum
+ *   as nnhip_rmsnorm_quant_i8 / nnhip_act_quant_i8 on x_out.
+ * Bit-identical to nnhip_ternary_matmul_add (or nnhip_ternary_matmul) followed by that quantizer.
+ * M <= 64, N <= 11264. Replaces w_o's (fc2's) BitLinear epilogue, the residual add of
+ * GPTBlock::forward_step and the following RMSNorm + int8 prologue (compute_layer_bitlinear.hpp:
+ * 459-466; compute_layer_gpt.hpp:208-216; compute_layer_mlp.hpp:686-707). */
+nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part, size_t slices, const float* tau,
+                                             const float* s_in, const int32_t* rowsum_in, const float* bias,
+                                             const float* res, size_t N, size_t M, float* x_out,
+                                             const float* gamma, float eps, int8_t* xi, float* s, int32_t* rowsum);
+
 /* count (1..4) BitLinears on the same int8 input (xi, s, rowsum; shared K and M):
  * Y[i] (N[i], M) = nnhip_ternary_matmul(rp[i], tau[i], xi, s, rowsum, bias[i], N[i], K, M), as one
  * launch on the decode path. rp / tau / N / Y are HOST arrays of count entries; bias may be NULL

@@ -103,6 +103,9 @@ SIGNATURES = {
     "nnhip_stream_xor": (_st, [_vp, _vp, _sz, _vp]),
     "nnhip_device_info": (_st, [ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 4),
     "nnhip_ternary_matmul_add": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_ternary_matmul_partial": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
+    "nnhip_partial_residual_quant_i8": (_st, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _f, _vp,
+                                              _vp, _vp]),
     "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                      ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
     "nnhip_ffn_glu_i8_add": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
@@ -559,6 +562,35 @@ class Context:
                                               self._dev(res, torch.float32, "res"), N, K, M,
                                               self._dev(Y, torch.float32, "Y")), "nnhip_ternary_matmul_add")
         return Y
+
+    def ternary_matmul_partial(self, rp, xi, N: int, K: int, M: int, slices: int, out=None):
+        """Split-k integer partial sums part (slices, M, N) int32 of the ternary GEMV (no epilogue)."""
+        torch = self._torch
+        part = self._empty((slices, M, N), torch.int32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_partial(self.h, self._dev(rp, torch.int32, "rp"),
+                                                  self._dev(xi, torch.int8, "xi"), N, K, M, slices,
+                                                  self._dev(part, torch.int32, "part")),
+               "nnhip_ternary_matmul_partial")
+        return part
+
+    def partial_residual_quant_i8(self, part, tau, s_in, rowsum_in, N: int, M: int, x_out, res=None, bias=None,
+                                  gamma=None, eps: float = 0.0, outs=None):
+        """x_out = epilogue(sum of part) [+ bias] [+ res], then [RMSNorm(gamma) ->] int8: returns (xi, s, rowsum)."""
+        torch = self._torch
+        xi, s, rs = self._act_out(N, M) if outs is None else outs
+        self._bind_stream()
+        _check(lib().nnhip_partial_residual_quant_i8(self.h, self._dev(part, torch.int32, "part"), part.shape[0],
+                                                     self._dev(tau, torch.float32, "tau"),
+                                                     self._dev(s_in, torch.float32, "s_in"),
+                                                     self._dev(rowsum_in, torch.int32, "rowsum_in"),
+                                                     self._dev(bias, torch.float32, "bias"),
+                                                     self._dev(res, torch.float32, "res"), N, M,
+                                                     self._dev(x_out, torch.float32, "x_out"),
+                                                     self._dev(gamma, torch.float32, "gamma"), eps,
+                                                     self._dev(xi), self._dev(s), self._dev(rs)),
+               "nnhip_partial_residual_quant_i8")
+        return xi, s, rs
 
     def ternary_matmul_n(self, problems, xi, s, rowsum, K: int, M: int):
         """problems: list of (rp, tau, bias or None, N, out or None) sharing the input; returns the outputs."""

@@ -169,6 +169,22 @@ hipError_t launch_matmul_q_t(hipStream_t st, const uint32_t* A, const float* tau
 // ---- activation kernels (k_act.hip)
 hipError_t launch_rmsnorm(hipStream_t st, const float* X, const float* gamma, float eps, size_t F,
                           size_t M, float* out);
+// Epilogue of a split-k GEMV (part[S][M][N] slice sums) + residual, then [RMSNorm ->] absmax
+// int8 quantization, one token per block (epilogue_quant_ok: M <= 64, N <= 11264).
+struct EpiArgs
+{
+    const int32_t* part;
+    int S;
+    const float* tau;          // (N)
+    const float* s_in;         // (M) scales of the GEMV's input tokens
+    const int32_t* rowsum_in;  // (M) code sums of the GEMV's input tokens
+    const float* bias;         // (N) or null
+    const float* res;          // (N, M) residual or null
+    float* xout;               // (N, M) epilogue + residual (may alias res)
+};
+bool epilogue_quant_ok(size_t N, size_t M);
+hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* gamma, bool norm, float eps, size_t N,
+                                 size_t M, int8_t* xi, float* s, int32_t* rowsum);
 hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, bool norm, float eps,
                             size_t K, size_t M, int8_t* xi, float* s, int32_t* rowsum,
                             uint32_t* xq_ref);
@@ -193,6 +209,10 @@ hipError_t launch_gemv_deep(hipStream_t st, const GemvProblem& p);
 constexpr int kGemvDeepMulti = 4;
 bool gemv_deep_multi_ok(const GemvProblem* ps, int count, int num_cus);
 hipError_t launch_gemv_deep_multi(hipStream_t st, const GemvProblem* ps, int count);
+// Split-k partial sums (no epilogue): part[ks][t][n] int32, S slices of ceil(KT / S) k tiles
+// (each slice non-empty, S <= 8, M <= 16); the epilogue runs in the per-token kernel that follows.
+bool gemv_part_ok(const GemvProblem& p, int S);
+hipError_t launch_gemv_part(hipStream_t st, const GemvProblem& p, int S, int32_t* part);
 // Grouped GEMV over a precomputed per-wave schedule: wave w runs the items
 // d_wave_items[d_wave_start[w] .. d_wave_start[w+1]) (item = problem << 20 | row tile).
 // If n_xstage > 0, the listed activation blocks (lds_bytes in total) are staged in LDS at

@@ -19,6 +19,7 @@
 //   k_token_wave   larger K, M <= 32: one wave per token, lane l owns parts l + 64q (q = 0..7).
 //   k_token_lanes  larger K, M > 32: 64 tokens per block, re-reads X per pass.
 #include "common.hpp"
+#include "token_quant.hpp"
 
 #include <cmath>
 
@@ -28,79 +29,16 @@ namespace
 {
 
 constexpr int kBlock = 256;
-constexpr int kParts = 512;  // sum-of-squares parts
 #ifndef NNHIP_ONE_TOK_MAX_M
 #define NNHIP_ONE_TOK_MAX_M 64  // largest M for k_token_one (K=6912, M=64: 6.8 us per call, the
                                 // 4-token kernel 11.0; equal at K=2560)
 #endif
-
-__device__ __forceinline__ int quantize_one(float x, float s)
-{
-    if (s == 0.0f || isnan(x)) return 0;
-    float v = __fdiv_rn(x, s);
-    if (isnan(v)) return 0;
-    v = fminf(fmaxf(v, -127.0f), 127.0f);
-    return (int)roundf(v);
-}
-
-// Per-token reciprocal for quantize_fast: fl(1/s), 0 when s == 0 (every code is then 0, as
-// quantize_one gives), +inf when 1/s overflows (the caller then takes the exact path).
-__device__ __forceinline__ float quant_rcp(float s)
-{
-    return s == 0.0f ? 0.0f : __fdiv_rn(1.0f, s);
-}
-
-// quantize_one(x, s) without a division in the common case. With r = fl(1/s) and
-// y = fl(x * r), |y - x/s| <= |x/s| * 2^-23 (two roundings), so |y - fl(x/s)| < 2^-15 for
-// |x/s| <= 128. Unless y lies within 2^-14 of a half-integer, round-to-nearest-even of y then
-// equals round-half-away-from-zero of fl(x/s) (no tie and no integer boundary in between), and
-// clamping after rounding equals clamping before (127 is an integer, and values past 127.5
-// round to 127 or more either way). Near a half-integer, for NaN inputs and when 1/s
-// overflowed, the exact quantize_one decides; the result is the same code bit for bit.
-__device__ __forceinline__ int quantize_fast(float x, float s, float r)
-{
-    const float y = __fmul_rn(x, r);
-    const float t = __builtin_rintf(y);
-    if (!(fabsf(y - t) < 0.5f - 0x1p-14f) || isinf(r)) return quantize_one(x, s);
-    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
-}
-
-// The fast-path code alone; `amb` is set when the exact path must decide (see quantize_fast).
-__device__ __forceinline__ int quantize_guess(float x, float r, bool& amb)
-{
-    const float y = __fmul_rn(x, r);
-    const float t = __builtin_rintf(y);
-    amb |= !(fabsf(y - t) < 0.5f - 0x1p-14f);
-    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
-}
 
 __device__ __forceinline__ uint32_t pack4(int q0, int q1, int q2, int q3)
 {
     // low bytes of q0..q3 -> bytes 0..3
     return __builtin_amdgcn_perm(__builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u),
                                  __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u), 0x05040100u);
-}
-
-// Correctly rounded fp32 square root. v_sqrt_f32 alone is accurate to 1 ulp; the two
-// fma residuals pick between its neighbours (the same correction LLVM's IEEE fsqrt
-// lowering applies), so the result matches a host sqrtf bit for bit. Inputs here are
-// ms + eps >= eps > 0 and far from the denormal range.
-__device__ __forceinline__ float sqrt_rn(float v)
-{
-    float s = __builtin_sqrtf(v);
-    if (!(v > 0.0f) || isinf(v)) return s;
-    const float s_dn = __int_as_float(__float_as_int(s) - 1);
-    const float s_up = __int_as_float(__float_as_int(s) + 1);
-    const float r_dn = __builtin_fmaf(-s_dn, s, v);
-    const float r_up = __builtin_fmaf(-s_up, s, v);
-    if (r_dn <= 0.0f) s = s_dn;
-    if (r_up > 0.0f) s = s_up;
-    return s;
-}
-
-__device__ __forceinline__ float rms_inv_of(float sum_sq, float inv_f, float eps)
-{
-    return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(sum_sq, inv_f), eps)));
 }
 
 __device__ __forceinline__ float wave_max(float v)
@@ -112,25 +50,6 @@ __device__ __forceinline__ float wave_max(float v)
         v = o > v ? o : v;
     }
     return v;
-}
-
-__device__ __forceinline__ int wave_sum_i(int v)
-{
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-// In-register butterfly levels: v[k] holds part p + stride*k (k < N); after the levels for
-// offsets stride*N/2 .. stride, v[0] holds part p of the tree at level `stride`.
-template <int N>
-__device__ __forceinline__ float tree_levels(float (&v)[N])
-{
-#pragma unroll
-    for (int d = N / 2; d >= 1; d >>= 1)
-#pragma unroll
-        for (int k = 0; k < d; ++k) v[k] = __fadd_rn(v[k], v[k + d]);
-    return v[0];
 }
 
 // Value of lane l ^ OFF as seen after the butterfly levels above OFF (descending offsets):
@@ -426,19 +345,6 @@ __global__ __launch_bounds__(kTW * kWave) void k_token_lanes(
 constexpr int kRegWaves = 8;  // 512 threads
 
 // Everything a block needs to load and finish token groups (uniform across the block).
-struct TokArgs
-{
-    const float* X;
-    bool norm;
-    float eps, inv_f;
-    int K, M, Kp, mode;
-    int8_t* xi;
-    float* s;
-    int32_t* rowsum;
-    uint32_t* xq_ref;
-    float* fout;
-};
-
 template <int TPB>
 struct TokShared
 {
@@ -674,32 +580,16 @@ __global__ __launch_bounds__(kRegWaves * kWave) void k_token_regs(TokArgs a, con
     finish_group<R, kVec, TPB>(x, gm, a, sh, g, w, fl, h, ro);
 }
 
-// Decode-sized M (up to 64 tokens): one token per block, 512 threads. Thread t owns sum-of-squares part t (rows
-// f = t + 512 r, r < R) of token m = blockIdx.x and holds one element per row, so a token's
-// VALU work (the three passes) is spread over M CUs rather than M/4, which is what bounds the
-// 4-token kernel at these sizes (one CU per 4 tokens, ~20 VALU ops per element). Same passes,
-// orders and codes as finish_group: parts summed in ascending f, the tree over the 512 parts in
-// wave 0, fmaxf absmax, the fast / exact quantizer pair.
-constexpr int kOneThreads = 512;
-
-__device__ __forceinline__ float wave_bfly_sum(float v)
-{
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, kWave));
-    return v;
-}
-
+// Decode-sized M (up to 64 tokens): one token per block, 512 threads. Thread t owns sum-of-squares
+// part t (rows f = t + 512 r, r < R) of token m = blockIdx.x and holds one element per row, so a
+// token's VALU work (the three passes) is spread over M CUs rather than M/4, which is what bounds
+// the 4-token kernel at these sizes (one CU per 4 tokens, ~20 VALU ops per element). Same passes,
+// orders and codes as finish_group (one_token_finish, token_quant.hpp).
 template <int R>
 __global__ __launch_bounds__(kOneThreads) void k_token_one(TokArgs a, const float* __restrict__ gamma)
 {
-    constexpr int NW = kOneThreads / kWave;
-    static_assert(kOneThreads == kParts, "one part per thread");
-    __shared__ float red[kParts];
-    __shared__ float wred[NW];
-    __shared__ int wsum[NW];
-    __shared__ float tok_ri;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int m = blockIdx.x;
+    __shared__ OneShared sh;
+    const int t = threadIdx.x, m = blockIdx.x;
     float x[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -707,84 +597,76 @@ __global__ __launch_bounds__(kOneThreads) void k_token_one(TokArgs a, const floa
         const int f = t + kParts * r;
         x[r] = f < a.K ? a.X[(size_t)f * a.M + m] : 0.0f;
     }
-    if (a.norm)
-    {
-        float gm[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-        {
-            const int f = t + kParts * r;
-            gm[r] = f < a.K ? gamma[f] : 0.0f;
-        }
-        float acc = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc = __fadd_rn(acc, __fmul_rn(x[r], x[r]));
-        red[t] = acc;
-        __syncthreads();
-        if (w == 0)
-        {
-            float v[kParts / kWave];
-#pragma unroll
-            for (int k = 0; k < kParts / kWave; ++k) v[k] = red[lane + kWave * k];
-            const float sum = wave_bfly_sum(tree_levels(v));
-            if (lane == 0) tok_ri = rms_inv_of(sum, a.inv_f, a.eps);
-        }
-        __syncthreads();
-        const float ri = tok_ri;
-#pragma unroll
-        for (int r = 0; r < R; ++r) x[r] = __fmul_rn(__fmul_rn(x[r], ri), gm[r]);
-    }
-    if (a.mode == 1)
-    {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-        {
-            const int f = t + kParts * r;
-            if (f < a.K) a.fout[(size_t)f * a.M + m] = x[r];
-        }
-        return;
-    }
-    float mx = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) mx = fmaxf(mx, fabsf(x[r]));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-    if (lane == 0) wred[w] = mx;
-    __syncthreads();
-    float tm = wred[0];
-#pragma unroll
-    for (int v = 1; v < NW; ++v) tm = fmaxf(tm, wred[v]);
-    const float sc = __fmul_rn(tm, 1.0f / 127.0f);
-    const float rc = quant_rcp(sc);
-    int q[R];
-    bool amb = isinf(rc);
-#pragma unroll
-    for (int r = 0; r < R; ++r) q[r] = quantize_guess(x[r], rc, amb);
-    if (amb)
-#pragma unroll
-        for (int r = 0; r < R; ++r) q[r] = quantize_fast(x[r], sc, rc);
-    int tsum = 0;
-    const int wpr = (a.M + 3) / 4;
+    one_token_finish<R>(x, a, gamma, sh);
+}
+
+// The same passes after the epilogue of a split-k GEMV (k_gemv_part) and the decoder's residual
+// add: x = (tau[f] * s_in[m]) * float(sum over slices of part[.][m][f] - 2 rowsum_in[m]) [+ bias[f]]
+// [+ res[f][m]], the deep GEMV's epilogue operation for operation (the slice sums add up exactly),
+// stored to xout (the residual stream, may alias res) and quantized for the next BitLinear.
+template <int R, int kEpiMaxSlices>
+__global__ __launch_bounds__(kOneThreads) void k_token_epi(TokArgs a, EpiArgs e, const float* __restrict__ gamma)
+{
+    __shared__ OneShared sh;
+    const int t = threadIdx.x, m = blockIdx.x, N = a.K, M = a.M;
+    const float sv = e.s_in[m];
+    const int rs2 = 2 * e.rowsum_in[m];
+    // every load of the thread is issued before the first use: the slice sums through one buffer
+    // resource over part (slices past S and features past N read 0), tau and the residual
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(e.part), (short)0, (int)((size_t)e.S * M * N * 4), 0x00020000);
+    int ps[R][kEpiMaxSlices];
+    float tv[R], rv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)
     {
         const int f = t + kParts * r;
-        tsum += q[r];  // rows past K hold code 0
-        if (f < a.Kp) a.xi[(size_t)m * a.Kp + f] = (int8_t)q[r];
-        if (a.xq_ref && f < a.K)
-            reinterpret_cast<int8_t*>(a.xq_ref)[((size_t)f * wpr + m / 4) * 4 + m % 4] = (int8_t)q[r];
-    }
-    tsum = wave_sum_i(tsum);
-    if (lane == 0) wsum[w] = tsum;
-    __syncthreads();
-    if (t == 0)
-    {
-        int sum = 0;
 #pragma unroll
-        for (int v = 0; v < NW; ++v) sum += wsum[v];
-        a.s[m] = sc;
-        a.rowsum[m] = sum;
+        for (int k = 0; k < kEpiMaxSlices; ++k)
+        {
+            const uint32_t off = (k < e.S && f < N) ? (uint32_t)(((size_t)k * M + m) * N + f) * 4u : 0x80000000u;
+            ps[r][k] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
+        }
+        tv[r] = f < N ? e.tau[f] : 0.0f;
+        rv[r] = (f < N && e.res) ? e.res[(size_t)f * M + m] : 0.0f;
     }
+    float x[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+    {
+        const int f = t + kParts * r;
+        x[r] = 0.0f;
+        if (f < N)
+        {
+            int acc = 0;
+#pragma unroll
+            for (int k = 0; k < kEpiMaxSlices; ++k) acc += ps[r][k];
+            float y = (tv[r] * sv) * (float)(acc - rs2);
+            if (e.bias) y = y + e.bias[f];
+            if (e.res) y = y + rv[r];
+            e.xout[(size_t)f * M + m] = y;
+            x[r] = y;
+        }
+    }
+    one_token_finish<R>(x, a, gamma, sh);
+}
+
+// slices are loaded up to a compiled maximum (4 or 8; those past S read 0)
+template <int R>
+void launch_epi_r(hipStream_t st, const TokArgs& a, const EpiArgs& e, const float* gamma)
+{
+    if (e.S <= 4)
+        hipLaunchKernelGGL((k_token_epi<R, 4>), dim3((unsigned)a.M), dim3(kOneThreads), 0, st, a, e, gamma);
+    else
+        hipLaunchKernelGGL((k_token_epi<R, 8>), dim3((unsigned)a.M), dim3(kOneThreads), 0, st, a, e, gamma);
+}
+
+template <int... Rs>
+bool launch_epi_pick(int rounds, hipStream_t st, const TokArgs& a, const EpiArgs& e, const float* gamma)
+{
+    bool done = false;
+    ((done = done || (Rs >= rounds && (launch_epi_r<Rs>(st, a, e, gamma), true))), ...);
+    return done;
 }
 
 template <int R>
@@ -1037,6 +919,24 @@ hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, 
         if (e != hipSuccess) return e;
     }
     return launch_token_kernel(st, X, gamma, norm, eps, K, M, 0, xi, s, rowsum, xq_ref, nullptr);
+}
+
+bool epilogue_quant_ok(size_t N, size_t M)
+{
+    return M >= 1 && M <= kOneTokMaxM && ceil_div(N, (size_t)kParts) <= 22;
+}
+
+hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* gamma, bool norm, float eps, size_t N,
+                                 size_t M, int8_t* xi, float* s, int32_t* rowsum)
+{
+    if (M == 0) return hipSuccess;
+    if (!epilogue_quant_ok(N, M)) return hipErrorInvalidValue;
+    const TokArgs a{nullptr, norm, eps, 1.0f / (float)N, (int)N, (int)M, (int)round_up(N, kTileK), 0, xi, s, rowsum,
+                    nullptr, nullptr};
+    const int rounds = (int)ceil_div(N, (size_t)kParts);
+    if (!launch_epi_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, e, gamma))
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 hipError_t launch_quant_amax(hipStream_t st, const float* X, size_t K, size_t M, uint32_t* amax, int8_t* xi,

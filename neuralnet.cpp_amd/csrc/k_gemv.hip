@@ -453,7 +453,143 @@ hipError_t launch_deep_kt(hipStream_t st, const GemvDeepArgs& da)
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------
+// Split-k decode GEMV without epilogue: the integer dot products of slice ks of the k tiles,
+// part[ks][t][n] = sum over the slice's k of code(n, k) * x(t, k) (the four MFMA sums combined,
+// a0 + a3 + (a1 >> 2) + (a2 >> 4), each an exact integer of the slice), token-major so that a
+// per-token epilogue kernel reads its row contiguously. The slice sums add up exactly to the
+// whole-K sum, so (tau * s) * float(sum_ks part - 2 rowsum) is the deep GEMV's epilogue bit for
+// bit. Block b takes slice b % S (the blocks of one XCD share one slice's activations in L2) and
+// row group b / S (4 row tiles, one per wave); the slice's KTS k tiles (KTS_MAX at compile time,
+// loads past the slice read zeros) and its activation columns (M x KTS x 256 bytes, the XOR-
+// swizzled rows of the deep GEMV) are staged as there. For grids that would leave most CUs idle
+// (N = 2560: 40 row groups of the deep GEMV).
+template <int KTS_MAX>
+__global__ __launch_bounds__(kBlock) void k_gemv_part(GemvProblem p, int S, int kts, int32_t* __restrict__ part)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int ks = (int)(blockIdx.x % (unsigned)S);
+    const int rg = (int)(blockIdx.x / (unsigned)S);
+    const int rt = rg * (kBlock / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int RT = (p.N + 15) / 16;
+    const int g = lane >> 4, t = lane & 15;
+    const uint32_t Kp = (uint32_t)p.KT * kTileK;
+    const int k0 = ks * kts;
+    const int nk = min(kts, p.KT - k0);  // this slice's k tiles (>= 1)
+    const bool live = rt < RT;
+
+    // 1. the slice's weight stages (tiles past the slice or the matrix read zero words)
+    const __amdgpu_buffer_rsrc_t rw =
+        rsrc(p.rp + ((size_t)(live ? rt : 0) * p.KT + k0) * 64, live ? (uint32_t)nk * 1024u : 0u);
+    v4i w[KTS_MAX];
+#pragma unroll
+    for (int kt = 0; kt < KTS_MAX; ++kt) w[kt] = ld16<kNT>(rw, (uint32_t)lane * 16u, (uint32_t)kt * 1024u);
+
+    // 2. the slice's activation columns into LDS (row tr: Kr = KTS_MAX * 256 bytes, units
+    //    permuted per token as in the deep GEMV); columns past the slice are multiplied by zeros
+    constexpr uint32_t Kr = (uint32_t)KTS_MAX * kTileK;
+    {
+        typedef __attribute__((address_space(3))) void lds_void;
+        const uint32_t xbytes = (uint32_t)p.M * Kp;
+        const __amdgpu_buffer_rsrc_t rx = rsrc(p.xi, xbytes);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int nq = (int)(((uint32_t)p.M * Kr + 1023u) / 1024u);
+        for (int q = wave; q < nq; q += kBlock / kWave)
+        {
+            const uint32_t L = (uint32_t)q * 64u + (uint32_t)lane;
+            const uint32_t tr = L / (uint32_t)(KTS_MAX * 16), u = L - tr * (uint32_t)(KTS_MAX * 16);
+            const uint32_t col = (uint32_t)k0 * kTileK + ((u ^ (tr & 7u)) * 16u);
+            const uint32_t src = tr < (uint32_t)p.M && col < Kp ? tr * Kp + col : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + q * 1024), 16, src, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    // 3. MFMAs over the slice's k tiles (tokens t >= M read token 0's row; never stored)
+    Acc acc[1];
+    acc[0].a0 = acc[0].a1 = acc[0].a2 = acc[0].a3 = v4i{0, 0, 0, 0};
+    const int tr = t < p.M ? t : 0;
+    const uint8_t* xrow = lds + (size_t)tr * Kr;
+    const int sw0 = 16 * (g ^ (tr & 7)), sw1 = 16 * ((4 + g) ^ (tr & 7));
+#pragma unroll
+    for (int kt = 0; kt < KTS_MAX; ++kt)
+    {
+        v4i x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            x[j] = *reinterpret_cast<const v4i*>(xrow + kt * 256 + (j >> 1) * 128 + ((j & 1) ? sw1 : sw0));
+        const v4i w1[1] = {w[kt]};
+        compute_stage<1>(w1, x, acc);
+    }
+
+    // 4. the slice's sums, part[ks][t][n] (rows past N and tokens past M are not stored)
+    const __amdgpu_buffer_rsrc_t rp = rsrc(part + (size_t)ks * p.M * p.N, (uint32_t)p.M * (uint32_t)p.N * 4u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int n = rt * 16 + 4 * g + i;
+        const int a = acc[0].a0[i] + acc[0].a3[i] + (acc[0].a1[i] >> 2) + (acc[0].a2[i] >> 4);
+        const uint32_t off = (live && n < p.N && t < p.M) ? ((uint32_t)t * (uint32_t)p.N + (uint32_t)n) * 4u : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)a, rp, off, 0, 0);
+    }
+}
+
+template <int KTS_MAX>
+hipError_t launch_part_kts(hipStream_t st, const GemvProblem& p, int S, int kts, int32_t* part)
+{
+    static bool attr = false;
+    const uint32_t lds_bytes = (uint32_t)round_up((size_t)p.M * KTS_MAX * kTileK, 1024);
+    if (!attr)
+    {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_part<KTS_MAX>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvDeepLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const unsigned row_groups = (unsigned)ceil_div(ceil_div((size_t)p.N, 16), (size_t)(kBlock / kWave));
+    hipLaunchKernelGGL(k_gemv_part<KTS_MAX>, dim3(row_groups * (unsigned)S), dim3(kBlock), lds_bytes, st, p, S, kts,
+                       part);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// k tiles per slice for S slices, rounded up to a compiled width (0 when none fits)
+static int gemv_part_width(int KT, int S)
+{
+    const int kts = (KT + S - 1) / S;
+    static const int widths[] = {1, 2, 3, 4, 5, 7, 10, 14};
+    for (int w : widths)
+        if (w >= kts) return w;
+    return 0;
+}
+
+bool gemv_part_ok(const GemvProblem& p, int S)
+{
+    if (S < 1 || S > 8 || p.M < 1 || p.M > kGemvMaxM || p.N < 1) return false;
+    const int kts = (p.KT + S - 1) / S;
+    if ((S - 1) * kts >= p.KT) return false;  // every slice holds at least one k tile
+    const int w = gemv_part_width(p.KT, S);
+    return w > 0 && round_up((size_t)p.M * w * kTileK, 1024) <= kGemvDeepLds;
+}
+
+hipError_t launch_gemv_part(hipStream_t st, const GemvProblem& p, int S, int32_t* part)
+{
+    const int kts = (p.KT + S - 1) / S;
+    switch (gemv_part_width(p.KT, S))
+    {
+    case 1: return launch_part_kts<1>(st, p, S, kts, part);
+    case 2: return launch_part_kts<2>(st, p, S, kts, part);
+    case 3: return launch_part_kts<3>(st, p, S, kts, part);
+    case 4: return launch_part_kts<4>(st, p, S, kts, part);
+    case 5: return launch_part_kts<5>(st, p, S, kts, part);
+    case 7: return launch_part_kts<7>(st, p, S, kts, part);
+    case 10: return launch_part_kts<10>(st, p, S, kts, part);
+    case 14: return launch_part_kts<14>(st, p, S, kts, part);
+    default: return hipErrorInvalidValue;
+    }
+}
 
 size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds)
 {

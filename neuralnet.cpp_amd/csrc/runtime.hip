@@ -892,6 +892,50 @@ nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const floa
     return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y, 0, 0, nullptr, res);
 }
 
+nnhip_status nnhip_ternary_matmul_partial(nnhip_ctx* ctx, const void* rp, const int8_t* xi, size_t N, size_t K,
+                                          size_t M, size_t slices, int32_t* part)
+{
+    const char* fn = "nnhip_ternary_matmul_partial";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    const nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && xi && part, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
+    NNHIP_REQUIRE(M <= (size_t)kGemvMaxM, fn, "M must be at most 16");
+    NNHIP_REQUIRE(slices >= 1 && slices <= 8, fn, "slices must be in [1, 8]");
+    NNHIP_REQUIRE(mul_ok(slices * M, N) && slices * M * N * 4 < 0x7FFFFFFFull, fn, "part must stay below 2^31 bytes");
+    GemvProblem p{};
+    p.rp = static_cast<const u32x4*>(rp);
+    p.xi = xi;
+    p.N = (int32_t)N;
+    p.K = (int32_t)K;
+    p.M = (int32_t)M;
+    p.KT = (int32_t)ceil_div(K, kTileK);
+    p.xlds = -1;
+    NNHIP_REQUIRE(gemv_part_ok(p, (int)slices), fn, "every slice must hold at least one k tile of at most 14");
+    NNHIP_LAUNCH(fn, launch_gemv_part(ctx->stream, p, (int)slices, part));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part, size_t slices, const float* tau,
+                                             const float* s_in, const int32_t* rowsum_in, const float* bias,
+                                             const float* res, size_t N, size_t M, float* x_out,
+                                             const float* gamma, float eps, int8_t* xi, float* s, int32_t* rowsum)
+{
+    const char* fn = "nnhip_partial_residual_quant_i8";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(part && tau && s_in && rowsum_in && x_out && xi && s && rowsum, fn, "null pointer");
+    NNHIP_REQUIRE(slices >= 1 && slices <= 8, fn, "slices must be in [1, 8]");
+    NNHIP_REQUIRE(epilogue_quant_ok(N, M), fn, "needs M <= 64 and N <= 11264");
+    NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
+    NNHIP_REQUIRE(!gamma || eps >= 0.0f, fn, "eps must be >= 0");
+    const EpiArgs e{part, (int)slices, tau, s_in, rowsum_in, bias, res, x_out};
+    NNHIP_LAUNCH(fn, launch_epilogue_quant(ctx->stream, e, gamma, gamma != nullptr, eps, N, M, xi, s, rowsum));
+    return NNHIP_OK;
+}
+
 nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* const* rp, const float* const* tau,
                                     const float* const* bias, const size_t* N, float* const* Y, const int8_t* xi,
                                     const float* s, const int32_t* rowsum, size_t K, size_t M)
@@ -1352,14 +1396,12 @@ size_t nnhip_attention_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk
     return attn_workspace_bytes(B, H, Hkv, dk, len_bound);
 }
 
-nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
-                                    size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
-                                    const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
-                                    size_t max_len, float scale, float* out)
+// Shared argument checks of the decode attention entry points; grows the chunk workspace.
+static nnhip_status attention_prep(nnhip_ctx* ctx, const char* fn, const float* q, const float* k, const float* v,
+                                   size_t B, size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                   const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
+                                   size_t max_len, float* out, size_t& wsb)
 {
-    const char* fn = "nnhip_attention_decode";
-    NNHIP_CHECK_CTX(fn);
-    if (B == 0) return NNHIP_OK;
     NNHIP_REQUIRE(q && k && v && pos && k_cache && v_cache && out, fn, "null pointer");
     NNHIP_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), fn, "rope_cos and rope_sin go together");
     NNHIP_REQUIRE(dk == 64 || dk == 128 || dk == 256, fn, "dk must be 64, 128 or 256");
@@ -1372,12 +1414,27 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
     // one sequence's cache is addressed through a 32-bit buffer range
     NNHIP_REQUIRE(max_len * Hkv * dk * 4 < 0x7FFFFFFFull, fn, "max_len * Hkv * dk * 4 must stay below 2^31");
     NNHIP_REQUIRE(aligned16(k_cache) && aligned16(v_cache), fn, "caches must be 16-byte aligned");
-    const size_t wsb = attn_workspace_bytes(B, H, Hkv, dk, len_bound);
+    wsb = attn_workspace_bytes(B, H, Hkv, dk, len_bound);
     if (wsb > ctx->attn_ws_bytes)
     {
         const nnhip_status st = ensure_buf(ctx, ctx->attn_ws, ctx->attn_ws_bytes, wsb, fn, "attention workspace");
         if (st != NNHIP_OK) return st;
     }
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                    size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                    const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
+                                    size_t max_len, float scale, float* out)
+{
+    const char* fn = "nnhip_attention_decode";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0) return NNHIP_OK;
+    size_t wsb = 0;
+    const nnhip_status st = attention_prep(ctx, fn, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin, k_cache,
+                                           v_cache, max_len, out, wsb);
+    if (st != NNHIP_OK) return st;
     NNHIP_LAUNCH(fn, launch_attn_decode(ctx->stream, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin,
                                         k_cache, v_cache, max_len, scale,
                                         wsb ? static_cast<float*>(ctx->attn_ws) : nullptr, out, ctx->num_cus));

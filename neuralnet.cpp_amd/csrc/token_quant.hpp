@@ -1,0 +1,274 @@
+// token_quant.hpp — the per-token [RMSNorm ->] absmax -> int8 quantizer passes of the
+// one-token-per-block kernels, shared by k_act.hip (activations from a (K, M) matrix), k_gemv.hip
+// (the split-k GEMV epilogue and residual add first) and k_decode.hip (the attention merge
+// first). Every kernel evaluates the per-token sum of squares in one fixed order, the same as the
+// oracle: 512 strided parts (feature f in part f % 512), each summed in ascending f, then the xor
+// butterfly over 256, 128, ..., 1. So the normalized values, the scale and the int8 codes are
+// bit-identical to the unfused reference sequence whichever kernel runs.
+#pragma once
+
+#include "common.hpp"
+
+#include <cmath>
+
+namespace nnhip
+{
+namespace
+{
+
+constexpr int kParts = 512;  // sum-of-squares parts
+constexpr int kOneThreads = 512;  // one-token kernels: thread t owns part t
+
+__device__ __forceinline__ int quantize_one(float x, float s)
+{
+    if (s == 0.0f || isnan(x)) return 0;
+    float v = __fdiv_rn(x, s);
+    if (isnan(v)) return 0;
+    v = fminf(fmaxf(v, -127.0f), 127.0f);
+    return (int)roundf(v);
+}
+
+// Per-token reciprocal for quantize_fast: fl(1/s), 0 when s == 0 (every code is then 0, as
+// quantize_one gives), +inf when 1/s overflows (the caller then takes the exact path).
+__device__ __forceinline__ float quant_rcp(float s)
+{
+    return s == 0.0f ? 0.0f : __fdiv_rn(1.0f, s);
+}
+
+// quantize_one(x, s) without a division in the common case. With r = fl(1/s) and
+// y = fl(x * r), |y - x/s| <= |x/s| * 2^-23 (two roundings), so |y - fl(x/s)| < 2^-15 for
+// |x/s| <= 128. Unless y lies within 2^-14 of a half-integer, round-to-nearest-even of y then
+// equals round-half-away-from-zero of fl(x/s) (no tie and no integer boundary in between), and
+// clamping after rounding equals clamping before (127 is an integer, and values past 127.5
+// round to 127 or more either way). Near a half-integer, for NaN inputs and when 1/s
+// overflowed, the exact quantize_one decides; the result is the same code bit for bit.
+__device__ __forceinline__ int quantize_fast(float x, float s, float r)
+{
+    const float y = __fmul_rn(x, r);
+    const float t = __builtin_rintf(y);
+    if (!(fabsf(y - t) < 0.5f - 0x1p-14f) || isinf(r)) return quantize_one(x, s);
+    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+}
+
+// The fast-path code alone; `amb` is set when the exact path must decide (see quantize_fast).
+__device__ __forceinline__ int quantize_guess(float x, float r, bool& amb)
+{
+    const float y = __fmul_rn(x, r);
+    const float t = __builtin_rintf(y);
+    amb |= !(fabsf(y - t) < 0.5f - 0x1p-14f);
+    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+}
+
+// Correctly rounded fp32 square root. v_sqrt_f32 alone is accurate to 1 ulp; the two
+// fma residuals pick between its neighbours (the same correction LLVM's IEEE fsqrt
+// lowering applies), so the result matches a host sqrtf bit for bit. Inputs here are
+// ms + eps >= eps > 0 and far from the denormal range.
+__device__ __forceinline__ float sqrt_rn(float v)
+{
+    float s = __builtin_sqrtf(v);
+    if (!(v > 0.0f) || isinf(v)) return s;
+    const float s_dn = __int_as_float(__float_as_int(s) - 1);
+    const float s_up = __int_as_float(__float_as_int(s) + 1);
+    const float r_dn = __builtin_fmaf(-s_dn, s, v);
+    const float r_up = __builtin_fmaf(-s_up, s, v);
+    if (r_dn <= 0.0f) s = s_dn;
+    if (r_up > 0.0f) s = s_up;
+    return s;
+}
+
+__device__ __forceinline__ float rms_inv_of(float sum_sq, float inv_f, float eps)
+{
+    return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fmul_rn(sum_sq, inv_f), eps)));
+}
+
+__device__ __forceinline__ int wave_sum_i(int v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// In-register butterfly levels: v[k] holds part p + stride*k (k < N); after the levels for
+// offsets stride*N/2 .. stride, v[0] holds part p of the tree at level `stride`.
+template <int N>
+__device__ __forceinline__ float tree_levels(float (&v)[N])
+{
+#pragma unroll
+    for (int d = N / 2; d >= 1; d >>= 1)
+#pragma unroll
+        for (int k = 0; k < d; ++k) v[k] = __fadd_rn(v[k], v[k + d]);
+    return v[0];
+}
+
+
+// Lane exchanges of a butterfly with descending offsets: the value of lane l ^ OFF as seen after
+// the levels above OFF (by then a lane's value depends only on its lane bits below 2*OFF, so any
+// partner with those bits equal to (l mod 2*OFF) ^ OFF carries the same value). OFF = 1, 2:
+// quad_perm; OFF = 4, 8: row_ror; OFF = 16, 32: v_permlane16_swap / v_permlane32_swap of two
+// copies (inline asm; the two-result builtin returned its first register for both with this
+// compiler), which leave the lower row's value in the first register and the upper row's in the
+// second in every lane of a pair. bfly() combines own and partner with op, which is commutative
+// here (fl(a + b), max, integer +), so both lanes of a pair get the same bits.
+template <int CTRL>
+__device__ __forceinline__ int tq_dpp(int v)
+{
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+template <int OFF, class T, class Op>
+__device__ __forceinline__ T bfly(T v, Op op)
+{
+    if constexpr (OFF >= 16)
+    {
+        int a = __builtin_bit_cast(int, v), b = a;
+        if constexpr (OFF == 32)
+            asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+        else
+            asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+        return op(__builtin_bit_cast(T, a), __builtin_bit_cast(T, b));
+    }
+    else
+    {
+        constexpr int ctrl = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x124 : 0x128;
+        return op(v, __builtin_bit_cast(T, tq_dpp<ctrl>(__builtin_bit_cast(int, v))));
+    }
+}
+// over all 64 lanes, offsets 32, 16, ..., 1 (every lane gets the result)
+template <class T, class Op>
+__device__ __forceinline__ T wave_bfly(T v, Op op)
+{
+    v = bfly<32>(v, op);
+    v = bfly<16>(v, op);
+    v = bfly<8>(v, op);
+    v = bfly<4>(v, op);
+    v = bfly<2>(v, op);
+    return bfly<1>(v, op);
+}
+struct TqAdd
+{
+    __device__ float operator()(float a, float b) const { return __fadd_rn(a, b); }
+};
+struct TqMax
+{
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct TqIAdd
+{
+    __device__ int operator()(int a, int b) const { return a + b; }
+};
+
+struct TokArgs
+{
+    const float* X;
+    bool norm;
+    float eps, inv_f;
+    int K, M, Kp, mode;
+    int8_t* xi;
+    float* s;
+    int32_t* rowsum;
+    uint32_t* xq_ref;
+    float* fout;
+};
+
+// LDS of the one-token kernels
+struct OneShared
+{
+    float red[kParts];
+    float wred[kOneThreads / kWave];
+    int wsum[kOneThreads / kWave];
+    float tok_ri;
+};
+
+// The passes of one token (m = blockIdx.x) once thread t holds x[r] = its value at feature
+// f = t + 512 r (0 past K): [RMSNorm with gamma: rms_inv from the 512 parts summed in ascending f
+// and the tree over them in wave 0, then (x * rms_inv) * gamma], then either the normalized values
+// to a.fout (mode 1) or the absmax scale, the codes (fast / exact quantizer pair) into the
+// token-major xi, the container a.xq_ref if given, s and the code row sum.
+template <int R>
+__device__ __forceinline__ void one_token_finish(float (&x)[R], const TokArgs& a, const float* __restrict__ gamma,
+                                                 OneShared& sh)
+{
+    constexpr int NW = kOneThreads / kWave;
+    static_assert(kOneThreads == kParts, "one part per thread");
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int m = blockIdx.x;
+    if (a.norm)
+    {
+        float gm[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = t + kParts * r;
+            gm[r] = f < a.K ? gamma[f] : 0.0f;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc = __fadd_rn(acc, __fmul_rn(x[r], x[r]));
+        sh.red[t] = acc;
+        __syncthreads();
+        if (w == 0)
+        {
+            float v[kParts / kWave];
+#pragma unroll
+            for (int k = 0; k < kParts / kWave; ++k) v[k] = sh.red[lane + kWave * k];
+            const float sum = wave_bfly(tree_levels(v), TqAdd{});
+            if (lane == 0) sh.tok_ri = rms_inv_of(sum, a.inv_f, a.eps);
+        }
+        __syncthreads();
+        const float ri = sh.tok_ri;
+#pragma unroll
+        for (int r = 0; r < R; ++r) x[r] = __fmul_rn(__fmul_rn(x[r], ri), gm[r]);
+    }
+    if (a.mode == 1)
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = t + kParts * r;
+            if (f < a.K) a.fout[(size_t)f * a.M + m] = x[r];
+        }
+        return;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) mx = fmaxf(mx, fabsf(x[r]));
+    mx = wave_bfly(mx, TqMax{});
+    if (lane == 0) sh.wred[w] = mx;
+    __syncthreads();
+    float tm = sh.wred[0];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) tm = fmaxf(tm, sh.wred[v]);
+    const float sc = __fmul_rn(tm, 1.0f / 127.0f);
+    const float rc = quant_rcp(sc);
+    int q[R];
+    bool amb = isinf(rc);
+#pragma unroll
+    for (int r = 0; r < R; ++r) q[r] = quantize_guess(x[r], rc, amb);
+    if (amb)
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = quantize_fast(x[r], sc, rc);
+    int tsum = 0;
+    const int wpr = (a.M + 3) / 4;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+    {
+        const int f = t + kParts * r;
+        tsum += q[r];  // rows past K hold code 0
+        if (f < a.Kp) a.xi[(size_t)m * a.Kp + f] = (int8_t)q[r];
+        if (a.xq_ref && f < a.K)
+            reinterpret_cast<int8_t*>(a.xq_ref)[((size_t)f * wpr + m / 4) * 4 + m % 4] = (int8_t)q[r];
+    }
+    tsum = wave_bfly(tsum, TqIAdd{});
+    if (lane == 0) sh.wsum[w] = tsum;
+    __syncthreads();
+    if (t == 0)
+    {
+        int sum = 0;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) sum += sh.wsum[v];
+        a.s[m] = sc;
+        a.rowsum[m] = sum;
+    }
+}
+
+}  // namespace
+}  // namespace nnhip

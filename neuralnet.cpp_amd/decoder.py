@@ -102,7 +102,7 @@ class Decoder:
         self.k = torch.empty((Hkv * dk, B), **f32)
         self.v = torch.empty((Hkv * dk, B), **f32)
         self.a = torch.empty((H * dk, B), **f32)
-        self.xi = torch.empty((B * kpd(max(d, H * dk)),), dtype=torch.int8, device=dev)
+        self.xi = torch.empty((B * kpd(max(d, H * dk, cfg.F)),), dtype=torch.int8, device=dev)
         self.s = torch.empty((B,), **f32)
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
         self.logits = torch.empty((cfg.vocab, B), **f32)
@@ -207,13 +207,77 @@ class Decoder:
                            blk.fc2.tau, blk.fc2.bias, self.r, cfg.act, out=self.x, gamma_sub=blk.g_ffn_sub,
                            eps_sub=cfg.eps)
 
+    # split-k slices of fc2 on the fused step path
+    slices_fc2 = 4
+
+    def fused_ok(self) -> bool:
+        """The fused step path (fc2 split-k, its epilogue, the residual add and the next block's
+        RMSNorm -> int8 as one per-token kernel) applies to batches of at most 16 sequences."""
+        return self.B <= 16
+
+    @staticmethod
+    def _slices(K: int, want: int) -> int:
+        """The largest slice count <= want whose slices of ceil(KT / S) k tiles (KT = ceil(K / 256))
+        are all non-empty and at most 14 tiles long."""
+        KT = (K + 255) // 256
+        for S in range(min(want, 8), 0, -1):
+            kts = (KT + S - 1) // S
+            if (S - 1) * kts < KT and kts <= 14:
+                return S
+        raise ValueError(f"no split-k slicing for K={K}")
+
+    def _scratch(self):
+        import torch
+        if getattr(self, "_part_buf", None) is None:
+            dev = f"cuda:{self.ctx.device}"
+            self._part_buf = torch.empty((self.slices_fc2, self.B, self.cfg.d), dtype=torch.int32, device=dev)
+            self._h_buf = torch.empty((self.cfg.F, self.B), dtype=torch.float32, device=dev)
+        return self._part_buf, self._h_buf
+
+    def block_step_fused(self, i: int, pos, len_bound: int, attn_hook=None):
+        """Block i with self.xi / s / rs holding int8(RMSNorm1(x)) on entry; on exit self.x holds the
+        block output and self.xi / s / rs its quantization for the next block (gamma = next block's
+        g1, or g_final after the last block). The same operations, in the same order, as
+        block_step followed by the next block's first quantizer."""
+        cfg, blk, ctx, B, d = self.cfg, self.blocks[i], self.ctx, self.B, self.cfg.d
+        outs = (self.xi, self.s, self.rs)
+        ctx.ternary_matmul_n([(blk.q.rp, blk.q.tau, blk.q.bias, blk.q.N, self.q),
+                              (blk.k.rp, blk.k.tau, blk.k.bias, blk.k.N, self.k),
+                              (blk.v.rp, blk.v.tau, blk.v.bias, blk.v.N, self.v)],
+                             self.xi, self.s, self.rs, blk.q.K, B)
+        kc, vc = self.caches[i]
+        ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
+                             self.cos, self.sin, out=self.a)
+        if attn_hook is not None:
+            attn_hook(i, self.a)
+        self._quant(self.a, blk.g_attn_sub)
+        o = blk.o
+        ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x, bias=o.bias,
+                               out=self.r)
+        self._quant(self.r, blk.g2)
+        part, h = self._scratch()
+        ctx.ternary_matmul_glu(blk.fc1.rp, blk.fc1.tau, self.xi, self.s, self.rs, cfg.F, d, B, act=cfg.act,
+                               bias=blk.fc1.bias, out=h)
+        self._quant(h, blk.g_ffn_sub)
+        f2 = blk.fc2
+        S = self._slices(f2.K, self.slices_fc2)
+        pf = ctx.ternary_matmul_partial(f2.rp, self.xi, f2.N, f2.K, B, S, out=part[:S])
+        g_next = self.blocks[i + 1].g1 if i + 1 < len(self.blocks) else self.g_final
+        ctx.partial_residual_quant_i8(pf, f2.tau, self.s, self.rs, d, B, self.x, res=self.r, bias=f2.bias,
+                                      gamma=g_next, eps=cfg.eps, outs=outs)
+
     def step(self, ids, pos, len_bound: int, attn_hook=None):
         """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,))."""
         ctx = self.ctx
         ctx.embedding_gather(self.emb, ids, out=self.x)
-        for i in range(len(self.blocks)):
-            self.block_step(i, pos, len_bound, attn_hook)
-        self._quant(self.x, self.g_final)
+        if self.fused_ok():
+            self._quant(self.x, self.blocks[0].g1 if self.blocks else self.g_final)
+            for i in range(len(self.blocks)):
+                self.block_step_fused(i, pos, len_bound, attn_hook)
+        else:
+            for i in range(len(self.blocks)):
+                self.block_step(i, pos, len_bound, attn_hook)
+            self._quant(self.x, self.g_final)
         self._mm(self.head, self.logits)
         ctx.argmax_cols(self.logits, out=self.ids)
         return self.logits, self.ids

@@ -1,0 +1,122 @@
+"""GPU parity of the fused decode-step entry points: the split-k partial GEMV
+(nnhip_ternary_matmul_partial) and its epilogue + residual + quantizer kernel
+(nnhip_partial_residual_quant_i8), bit for bit against the oracle's integer accumulators and
+against the unfused GPU sequence (nnhip_ternary_matmul_add, then nnhip_rmsnorm_quant_i8 /
+nnhip_act_quant_i8), whose own parity with the oracle the other GPU tests establish.
+"""
+import numpy as np
+import pytest
+
+from conftest import normal
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def case(ctx, orc, N, K, M, seed):
+    W = normal((N, K), seed, 0.0, 0.02)
+    tau = np.full(N, np.abs(W.astype(np.float64)).mean(), np.float32)
+    X = normal((K, M), seed + 1)
+    s = orc.act_scale(X)
+    wq = orc.trit_pack(W, tau)
+    xq = orc.quantize_i8(X, s, True)
+    rp = ctx.repack(dev(wq), K)
+    xi, s_d, rs = ctx.act_quant_i8(dev(X))
+    assert np.array_equal(host(s_d), s)
+    return tau, wq, xq, rp, xi, s_d, rs
+
+
+@pytest.mark.parametrize("N,K,M,slices", [
+    (2560, 2560, 16, 4), (2560, 6912, 16, 4), (2560, 6912, 16, 7), (2560, 2560, 16, 2),
+    (3840, 2560, 16, 1), (100, 1024, 3, 4), (2561, 6900, 5, 3), (17, 4096, 16, 8), (33, 256, 1, 1),
+    (640, 3584, 13, 7),
+])
+def test_matmul_partial_sums(ctx, orc, N, K, M, slices):
+    """sum over the slices of part - 2 rowsum = the oracle's integer accumulator trit . xq."""
+    say(f"partial N={N} K={K} M={M} slices={slices}")
+    tau, wq, xq, rp, xi, s_d, rs = case(ctx, orc, N, K, M, N + K + M + slices)
+    part = host(ctx.ternary_matmul_partial(rp, xi, N, K, M, slices)).astype(np.int64)
+    assert part.shape == (slices, M, N)
+    total = part.sum(axis=0) - 2 * host(rs).astype(np.int64)[:, None]       # (M, N)
+    ref = orc.matmul_q_i8_acc(wq, xq, K, M).astype(np.int64)                  # (N, M)
+    assert np.array_equal(total.T, ref)
+
+
+@pytest.mark.parametrize("N,K,M,slices,bias,res,norm", [
+    (2560, 2560, 16, 4, False, True, True),    # C5 w_o: + residual, RMSNorm2
+    (2560, 6912, 16, 4, False, True, True),    # C5 fc2: + residual, next block's RMSNorm1
+    (2560, 6912, 16, 4, True, True, False),    # bias, plain absmax
+    (1000, 2560, 7, 2, True, False, True),     # no residual
+    (2561, 6900, 5, 3, False, True, False),
+    (6912, 2560, 16, 4, False, False, True),   # K of the next BitLinear = 6912 (14 rounds)
+])
+def test_partial_residual_quant_equals_unfused(ctx, orc, N, K, M, slices, bias, res, norm):
+    say(f"epilogue N={N} K={K} M={M} slices={slices} bias={bias} res={res} norm={norm}")
+    import torch
+    tau, wq, xq, rp, xi, s_d, rs = case(ctx, orc, N, K, M, 3 * N + K + M)
+    b = dev(normal((N,), 7)) if bias else None
+    r = dev(normal((N, M), 8)) if res else None
+    gamma = dev(1.0 + 0.1 * normal((N,), 9)) if norm else None
+    eps = 1e-5
+    part = ctx.ternary_matmul_partial(rp, xi, N, K, M, slices)
+    x_out = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    xi2, s2, rs2 = ctx.partial_residual_quant_i8(part, dev(tau), s_d, rs, N, M, x_out, res=r, bias=b,
+                                                 gamma=gamma, eps=eps)
+    zero = torch.zeros((N, M), dtype=torch.float32, device="cuda")
+    Y = ctx.ternary_matmul_add(rp, dev(tau), xi, s_d, rs, N, K, M, r if res else zero, bias=b)
+    assert np.array_equal(host(x_out).view(np.uint32), host(Y).view(np.uint32))
+    ref = ctx.rmsnorm_quant_i8(Y, gamma, eps) if norm else ctx.act_quant_i8(Y)
+    assert np.array_equal(host(xi2), host(ref[0]))
+    assert np.array_equal(host(s2).view(np.uint32), host(ref[1]).view(np.uint32))
+    assert np.array_equal(host(rs2), host(ref[2]))
+
+
+def test_partial_residual_in_place(ctx, orc):
+    """x_out aliasing res: the decoder's residual stream updated in place."""
+    import torch
+    N, K, M, slices = 2560, 2560, 16, 4
+    tau, wq, xq, rp, xi, s_d, rs = case(ctx, orc, N, K, M, 77)
+    x0 = normal((N, M), 78)
+    x = dev(x0)
+    part = ctx.ternary_matmul_partial(rp, xi, N, K, M, slices)
+    ctx.partial_residual_quant_i8(part, dev(tau), s_d, rs, N, M, x, res=x, gamma=dev(np.ones(N, np.float32)), eps=1e-5)
+    Y = ctx.ternary_matmul_add(rp, dev(tau), xi, s_d, rs, N, K, M, dev(x0))
+    assert np.array_equal(host(x).view(np.uint32), host(Y).view(np.uint32))
+
+
+def test_partial_rejects(ctx, nnhip):
+    import torch
+    xi = torch.zeros((16, 512), dtype=torch.int8, device="cuda")
+    rp = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    with pytest.raises(nnhip.NNHipError):
+        ctx.ternary_matmul_partial(rp, xi, 64, 512, 16, 9)    # slices > 8
+    with pytest.raises(nnhip.NNHipError):
+        ctx.ternary_matmul_partial(rp, xi, 64, 512, 16, 3)    # 2 k tiles: a slice would be empty
+    with pytest.raises(nnhip.NNHipError):
+        ctx.ternary_matmul_partial(rp, xi, 64, 512, 17, 1)    # M > 16
+    xi27 = torch.zeros((16, 6912), dtype=torch.int8, device="cuda")
+    rp27 = torch.zeros(64 * 27 * 256, dtype=torch.int32, device="cuda")
+    with pytest.raises(nnhip.NNHipError):
+        ctx.ternary_matmul_partial(rp27, xi27, 64, 6912, 16, 8)  # 27 k tiles in 8 slices of 4: the last is empty
+    part = torch.zeros((1, 65, 8), dtype=torch.int32, device="cuda")
+    f = torch.zeros(8, dtype=torch.float32, device="cuda")
+    i = torch.zeros(65, dtype=torch.int32, device="cuda")
+    x = torch.zeros((8, 65), dtype=torch.float32, device="cuda")
+    with pytest.raises(nnhip.NNHipError):                       # M > 64
+        ctx.partial_residual_quant_i8(part, f, torch.zeros(65, device="cuda"), i, 8, 65, x)
+
