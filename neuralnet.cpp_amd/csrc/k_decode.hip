@@ -44,7 +44,7 @@ constexpr int kAttnThreads = 256;  // 4 waves
 #define NNHIP_ATTN_VEARLY 0  // value loads issued together with the key loads
 #endif
 #ifndef NNHIP_ATTN_MINW
-#define NNHIP_ATTN_MINW 4          // waves per SIMD the chunk kernel is compiled for (<= 128 VGPRs)
+#define NNHIP_ATTN_MINW 5          // waves per SIMD the chunk kernel is compiled for (<= 96 VGPRs)
 #endif
 #ifndef NNHIP_ATTN_PB
 #define NNHIP_ATTN_PB 2            // score passes (32 positions each) whose loads are in flight together
@@ -102,6 +102,24 @@ __device__ __forceinline__ float4 ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff,
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
 }
 
+// 4 bytes at byte offset off of the resource (0 when out of range), default cache policy
+__device__ __forceinline__ float ld_f1(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations (lgkmcnt(0); the
+// gfx950 s_barrier does not wait for them by itself), then s_barrier. There is no vmcnt wait, so
+// global loads in flight stay in flight. The empty asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_only_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt and expcnt at their maxima, lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <int DK, int RT, bool kFinal>
 __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_MINW : 1) void k_attn_chunk(AttnArgs a)
 {
@@ -111,22 +129,42 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
     constexpr int PB = DK <= 128 ? NNHIP_ATTN_PB : 2;  // position passes whose loads are issued together
     constexpr int VL = DK / 4;         // lanes per row in the value phase
     constexpr int NG = kAttnThreads / VL;  // rows per value step
+    constexpr int QI = (RT * HALF + kAttnThreads - 1) / kAttnThreads;  // query pairs per thread
+    static_assert(DK <= kAttnThreads, "one thread per element of the new key / value");
     __shared__ float4 q_s[RT * Q4];
     __shared__ float4 kn_s[Q4], vn_s[Q4];
     __shared__ float S[RT][kAttnT];
     __shared__ float ml[2][RT];
     __shared__ float4 red[4][RT * Q4];
 
-    const int tid = threadIdx.x;
+    const int tid0 = threadIdx.x;
     const int R = a.R;  // query heads per KV head (<= RT, the register / LDS sizing)
-    const int w = tid >> 6, lane = tid & 63;
     const int total = a.nchunk * a.Hkv * a.B;
-    // persistent: work-group items (chunk fastest, then KV head, then sequence)
+    // persistent: work-group items. The chunks before each (sequence, KV head)'s last come first
+    // (chunk fastest, then KV head, then sequence), then the last chunks: those are partial
+    // (positions past the last multiple of 128), so when the items outnumber the resident
+    // work-groups by a little, the second round is made of short items.
+    const int nfull = (a.nchunk - 1) * a.Hkv * a.B;
     for (int item = blockIdx.x; item < total; item += gridDim.x)
     {
-        const int c = item % a.nchunk;
-        const int g = (item / a.nchunk) % a.Hkv;
-        const int b = item / (a.nchunk * a.Hkv);
+        int tid = tid0;
+        // opaque per item: the compiler keeps no thread-index arithmetic live across items (hoisted
+        // out of the loop, those values took ~28 VGPRs and pushed the kernel into spills)
+        asm volatile("" : "+v"(tid));
+        const int w = tid >> 6, lane = tid & 63;
+        int c, pr;
+        if (item < nfull)
+        {
+            c = item % (a.nchunk - 1);
+            pr = item / (a.nchunk - 1);
+        }
+        else
+        {
+            c = a.nchunk - 1;
+            pr = item - nfull;
+        }
+        const int g = pr % a.Hkv;
+        const int b = pr / a.Hkv;
         const int p = a.pos[b];
         const int t0 = c * kAttnT;
         if (p < 0 || p >= a.len_bound)
@@ -144,35 +182,94 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         const size_t rstride = (size_t)a.Hkv * DK;
         const size_t seq_off = (size_t)b * a.max_len * rstride + (size_t)g * DK;
 
+        // ---- loads first, in this order: the query pairs (and, in the chunk holding p, the new
+        //      key/value), then the first PB passes of cached key rows. The queries' RoPE and
+        //      LDS staging wait only for the query loads, so the key rows stream in meanwhile.
+        // (buffer-resource loads: 32-bit offsets keep the address registers few)
+        const uint32_t qkv_rows = (uint32_t)a.B * 4u;  // bytes between features of one column
+        const __amdgpu_buffer_rsrc_t rq = attn_rsrc(a.q + b, (uint32_t)a.H * DK * qkv_rows);
+        const __amdgpu_buffer_rsrc_t rkn = attn_rsrc(a.k + b, (uint32_t)a.Hkv * DK * qkv_rows);
+        const __amdgpu_buffer_rsrc_t rvn = attn_rsrc(a.v + b, (uint32_t)a.Hkv * DK * qkv_rows);
+        // the RoPE table rows of position p (unused without tables)
+        const __amdgpu_buffer_rsrc_t rcs = attn_rsrc(a.cosT ? a.cosT + (size_t)p * HALF : a.q, HALF * 4u);
+        const __amdgpu_buffer_rsrc_t rsn = attn_rsrc(a.sinT ? a.sinT + (size_t)p * HALF : a.q, HALF * 4u);
+        float qx0[QI], qx1[QI], qcs[QI], qsn[QI];
+#pragma unroll
+        for (int u = 0; u < QI; ++u)
+        {
+            const int e = tid + u * kAttnThreads;
+            const int r = e / HALF, j = e - r * HALF;
+            // lanes past R heads read zeros (offset beyond the resource)
+            const uint32_t qo = e < R * HALF ? (uint32_t)((g * R + r) * DK + j) * qkv_rows : 0x80000000u;
+            qx0[u] = ld_f1(rq, qo);
+            qx1[u] = ld_f1(rq, qo + HALF * qkv_rows);
+            qcs[u] = a.cosT ? ld_f1(rcs, 4u * j) : 1.f;
+            qsn[u] = a.cosT ? ld_f1(rsn, 4u * j) : 0.f;
+        }
+        float kx0 = 0.f, kx1 = 0.f, kcs = 1.f, ksn = 0.f, vx = 0.f;
+        if (has_new)
+        {
+            const uint32_t ko = tid < HALF ? (uint32_t)(g * DK + tid) * qkv_rows : 0x80000000u;
+            kx0 = ld_f1(rkn, ko);
+            kx1 = ld_f1(rkn, ko + HALF * qkv_rows);
+            if (a.cosT)
+            {
+                kcs = ld_f1(rcs, 4u * (tid & (HALF - 1)));
+                ksn = ld_f1(rsn, 4u * (tid & (HALF - 1)));
+            }
+            vx = ld_f1(rvn, tid < DK ? (uint32_t)(g * DK + tid) * qkv_rows : 0x80000000u);
+        }
+
+        // key rows: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row.
+        // Cached rows come through one buffer resource per (sequence, KV head): lanes past the
+        // chunk or on the new position read zeros without a branch, so every load of a pass
+        // group is in flight at once; the new position's key is selected from LDS afterwards.
+        const int pg = tid >> 3, j8 = tid & 7;
+        const __amdgpu_buffer_rsrc_t rk = attn_rsrc(a.kc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
+        float4 kv[PB][F4];
+        auto load_keys = [&](int pass0) {
+#pragma unroll
+            for (int u = 0; u < PB; ++u)
+            {
+                const int tl = (pass0 + u) * 32 + pg;
+                const int t = t0 + tl;
+                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
+#pragma unroll
+                for (int i = 0; i < F4; ++i) kv[u][i] = ld_f4(rk, row, 16u * (j8 + 8 * i));
+            }
+        };
+        load_keys(0);
+
         // ---- stage the rotated queries (R heads) and, in the chunk holding p, the new key/value
         float* qf = reinterpret_cast<float*>(q_s);
-        for (int e = tid; e < R * HALF; e += kAttnThreads)
+#pragma unroll
+        for (int u = 0; u < QI; ++u)
         {
-            const int r = e / HALF, j = e - r * HALF;
-            const int h = g * R + r;
-            const float x0 = a.q[(size_t)(h * DK + j) * a.B + b];
-            const float x1 = a.q[(size_t)(h * DK + j + HALF) * a.B + b];
-            float y0 = x0, y1 = x1;
-            if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
-            qf[r * DK + j] = y0;
-            qf[r * DK + j + HALF] = y1;
+            const int e = tid + u * kAttnThreads;
+            if (e < R * HALF)
+            {
+                const int r = e / HALF, j = e - r * HALF;
+                float y0 = qx0[u], y1 = qx1[u];
+                if (a.cosT) rope_pair(qx0[u], qx1[u], qcs[u], qsn[u], y0, y1);
+                qf[r * DK + j] = y0;
+                qf[r * DK + j + HALF] = y1;
+            }
         }
         if (has_new)
         {
             float* kf = reinterpret_cast<float*>(kn_s);
             float* vf = reinterpret_cast<float*>(vn_s);
-            for (int j = tid; j < HALF; j += kAttnThreads)
+            if (tid < HALF)
             {
-                const float x0 = a.k[(size_t)(g * DK + j) * a.B + b];
-                const float x1 = a.k[(size_t)(g * DK + j + HALF) * a.B + b];
-                float y0 = x0, y1 = x1;
-                if (a.cosT) rope_pair(x0, x1, a.cosT[(size_t)p * HALF + j], a.sinT[(size_t)p * HALF + j], y0, y1);
-                kf[j] = y0;
-                kf[j + HALF] = y1;
+                float y0 = kx0, y1 = kx1;
+                if (a.cosT) rope_pair(kx0, kx1, kcs, ksn, y0, y1);
+                kf[tid] = y0;
+                kf[tid + HALF] = y1;
             }
-            for (int i = tid; i < DK; i += kAttnThreads) vf[i] = a.v[(size_t)(g * DK + i) * a.B + b];
+            if (tid < DK) vf[tid] = vx;
         }
-        __syncthreads();
+        // LDS-only barrier: a workgroup fence (__syncthreads) would also wait for the key loads
+        lds_only_barrier();
         if (has_new)
         {
             float4* krow = reinterpret_cast<float4*>(a.kc + seq_off + (size_t)p * rstride);
@@ -203,25 +300,11 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         load_values();
 #endif
 
-        // ---- scores: 8 lanes per position, lane j8 holds float4 columns j8 + 8i of the row.
-        //      Cached rows come through one buffer resource per (sequence, KV head): lanes past the
-        //      chunk or on the new position read zeros without a branch, so every load of a pass
-        //      is in flight at once; the new position's key is selected from LDS afterwards.
-        const int pg = tid >> 3, j8 = tid & 7;
-        const __amdgpu_buffer_rsrc_t rk = attn_rsrc(a.kc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
+        // ---- scores of the chunk, PB passes of 32 positions at a time
 #pragma unroll
         for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
         {
-            float4 kv[PB][F4];
-#pragma unroll
-            for (int u = 0; u < PB; ++u)
-            {
-                const int tl = (pass0 + u) * 32 + pg;
-                const int t = t0 + tl;
-                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
-#pragma unroll
-                for (int i = 0; i < F4; ++i) kv[u][i] = ld_f4(rk, row, 16u * (j8 + 8 * i));
-            }
+            if (pass0 > 0) load_keys(pass0);
 #pragma unroll
             for (int u = 0; u < PB; ++u)
             {
