@@ -243,6 +243,12 @@ hipError_t launch_digits(hipStream_t st, const void* B, bool b16, const float* k
 hipError_t launch_digit_combine(hipStream_t st, const float* Yp, const float* tau, const int32_t* ex,
                                 const uint32_t* rp, const void* B, bool b16, const float* kscale, size_t N, size_t K,
                                 size_t M, void* Y, bool y16);
+// the same product in one launch at decode sizes (f32 activations, M <= 4, K % 4 == 0, 16-byte
+// aligned B, the compiled k-tile counts): digits in LDS per block, int64 combine in the
+// epilogue; bit-identical to the three launches
+bool digit_gemv_ok(size_t N, size_t K, size_t M, bool b16, const void* B);
+hipError_t launch_digit_gemv(hipStream_t st, const void* rp, const float* tau, const float* kscale, const float* B,
+                             size_t N, size_t K, size_t M, void* Y, bool y16);
 // *out ^= xor of the bytes / 4 words at src, one streaming pass into stream_xor_blocks()
 // per-block partials, then a one-block fold (k_ref.hip)
 size_t stream_xor_blocks(size_t bytes, int num_cus);

@@ -20,6 +20,7 @@
 // Epilogue (reference order, src/int8_act_test.cpp:233): y = (tau[n] * s[t]) * float(acc),
 // then y + bias[n] as a separate rounding (compiled with -ffp-contract=off).
 #include "common.hpp"
+#include "gemv_tile.hpp"
 
 
 namespace nnhip
@@ -27,37 +28,7 @@ namespace nnhip
 namespace
 {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-constexpr uint32_t kM3 = 0x03030303u;
 constexpr int kBlock = 256;                 // 4 waves
-constexpr uint32_t kOOB = 0x80000000u;
-constexpr int kRsrcFlags = 0x00020000;      // gfx9-family buffer resource word 3 (raw, dword)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
-}
-
-// kAux is the cache-policy operand: 0 = default; kNT = non-temporal ("nt" on gfx950), for the
-// weight stream, which is read once per launch (measured on MI355X: a streaming read reaches
-// about 7.0 TB/s with nt loads and about 6.1 TB/s without).
-constexpr int kNT = 2;
-template <int kAux = 0>
-__device__ __forceinline__ v4i ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
-{
-    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kAux));
-}
-
-__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c)
-{
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
-struct Acc
-{
-    v4i a0, a1, a2, a3;
-};
 
 template <int kRTW>
 struct Stage
@@ -92,20 +63,6 @@ __device__ __forceinline__ void read_x_lds(v4i (&x)[4], const Src<kRTW>& s, int 
 {
 #pragma unroll
     for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(s.xl + kt * 256 + 64 * j);
-}
-
-template <int kRTW>
-__device__ __forceinline__ void compute_stage(const v4i (&w4)[kRTW], const v4i (&x)[4], Acc (&acc)[kRTW])
-{
-#pragma unroll
-    for (int r = 0; r < kRTW; ++r)
-    {
-        const v4i w = w4[r];
-        acc[r].a0 = mfma16(w & (int)kM3, x[0], acc[r].a0);
-        acc[r].a1 = mfma16(w & (int)(kM3 << 2), x[1], acc[r].a1);
-        acc[r].a2 = mfma16(w & (int)(kM3 << 4), x[2], acc[r].a2);
-        acc[r].a3 = mfma16((v4i)((__builtin_bit_cast(u32x4, w) >> 6) & kM3), x[3], acc[r].a3);
-    }
 }
 
 // Loads are unconditional: a stage past the last k tile reads beyond its resource

@@ -824,6 +824,12 @@ static nnhip_status matmul_digits(nnhip_ctx* ctx, const char* fn, const void* rp
     NNHIP_REQUIRE(M <= kMaxDim / 4 && mul_ok(N, 4 * M), fn, "size overflow");
     // the digit products are exact integers in f32 while 128 K < 2^24
     if (K >= 131072) return fail(NNHIP_ERR_UNSUPPORTED, fn, "K must be below 131072 (use nnhip_matmul_q)");
+    if (digit_gemv_ok(N, K, M, b_f16 != 0, B))
+    {
+        NNHIP_LAUNCH(fn, launch_digit_gemv(ctx->stream, rp, tau, kscale, static_cast<const float*>(B), N, K, M, Y,
+                                           y_f16 != 0));
+        return NNHIP_OK;
+    }
     const size_t Kp = round_up(K, kTileK), M4 = 4 * M;
     const size_t b_xi = round_up(M4 * Kp, 256), b_rs = round_up(M4 * 4, 256), b_ex = round_up(M * 4, 256);
     const size_t b_yp = N * M4 * 4;

@@ -234,3 +234,96 @@ def test_matmul_t_f_agrees_with_valu_kernel(ctx, orc):
     a = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(B), M))
     b = host(ctx.matmul_q_t(dev(A), dev(tau), dev(B), M))
     assert np.max(np.abs(a - b)) <= 1e-4 * max(1.0, float(np.max(np.abs(b))))
+
+
+def digit_model(trits, X, tau=None, kscale=None):
+    """The digit-split product bit for bit, for finite tokens: x (times kscale[k] in f32 when
+    given), E = the exponent of max|x| (max < 2^E), X = rint(x 2^(30 - E)) (exact in f32),
+    T = sum_k trit X in int64 (the four digit products recombined), y = tau_n * (f32(T) 2^(E - 30))
+    in f32. trits (N, K), X (K, M) f32 -> (N, M) f32."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    if kscale is not None:
+        X = (kscale.astype(np.float32)[:, None] * X).astype(np.float32)
+    t64 = trits.astype(np.int64)
+    Y = np.empty((trits.shape[0], X.shape[1]), np.float32)
+    for m in range(X.shape[1]):
+        col = X[:, m]
+        _, E = np.frexp(np.max(np.abs(col)))
+        Xi = np.rint(np.ldexp(col, 30 - int(E))).astype(np.int64)
+        y = np.ldexp((t64 @ Xi).astype(np.float32), int(E) - 30).astype(np.float32)
+        Y[:, m] = y if tau is None else (tau.astype(np.float32) * y).astype(np.float32)
+    return Y
+
+
+def misaligned(t):
+    """A copy of t whose data pointer is 4 bytes past a 16-byte boundary: the digit-split product
+    then runs as three launches (digits, int8 GEMV on the digit tokens, combine) instead of one."""
+    import torch
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = buf[1:].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+def same_bits(a, b):
+    return np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(
+        a[~np.isnan(a)].view(np.uint32) if a.dtype == np.float32 else a[~np.isnan(a)],
+        b[~np.isnan(b)].view(np.uint32) if b.dtype == np.float32 else b[~np.isnan(b)])
+
+
+@pytest.mark.parametrize("N,K,M", [(2560, 2560, 1), (6912, 2560, 1), (2560, 6912, 1), (2560, 6912, 2),
+                                   (2560, 2560, 3), (2560, 2560, 4), (1000, 4096, 4), (3000, 8192, 1),
+                                   (37, 1000, 2), (16, 1024, 1)])
+def test_matmul_f_one_launch_bits(ctx, orc, N, K, M):
+    """Decode sizes (M <= 4 tokens) run the digit split, the MFMAs and the int64 combine in one
+    launch: its outputs equal the three-launch path's and the exact digit model's bit for bit."""
+    say(f"ternary_matmul_f one launch N={N} K={K} M={M}")
+    wq, tau, rp = case(ctx, orc, N, K, seed=N + 3 * K + M)
+    X = normal((K, M), 40 + M)
+    X[:, ::2] *= 29.0
+    Xd = dev(X)
+    assert Xd.data_ptr() % 16 == 0
+    one = host(ctx.ternary_matmul_f(rp, dev(tau), Xd, N, K))
+    three = host(ctx.ternary_matmul_f(rp, dev(tau), misaligned(Xd), N, K))
+    assert same_bits(one, three)
+    assert same_bits(one, digit_model(orc.trits_of(wq, K), X, tau=tau))
+    one16 = ctx.ternary_matmul_f(rp, dev(tau), Xd, N, K, out_f16=True).cpu().numpy()
+    assert np.array_equal(one16.view(np.uint16), one.astype(np.float16).view(np.uint16))
+
+
+def test_matmul_f_one_launch_specials(ctx, orc):
+    """Non-finite and zero tokens in the one-launch kernel: the same IEEE results as the three
+    launches, and finite tokens beside them unaffected."""
+    N, K, M = 300, 2560, 4
+    W = normal((N, K), 51, 0.0, 0.02)
+    W[::2, 20] = 1.0
+    W[1::2, 20] = -1.0
+    W[:, 10] = 0.0
+    wq, tau, rp = case(ctx, orc, N, K, W=W)
+    X = normal((K, M), 52)
+    X[20, 0] = np.inf       # +-1 column -> +-inf rows
+    X[10, 1] = -np.inf      # 0 column -> NaN
+    X[:, 2] = 0.0
+    Xd = dev(X)
+    one = host(ctx.ternary_matmul_f(rp, dev(tau), Xd, N, K))
+    three = host(ctx.ternary_matmul_f(rp, dev(tau), misaligned(Xd), N, K))
+    assert same_bits(one, three)
+    assert np.all(one[::2, 0] == np.inf) and np.all(one[1::2, 0] == -np.inf) and np.all(np.isnan(one[:, 1]))
+    assert np.all(one[:, 2] == 0.0)
+    assert same_bits(one[:, 3:], digit_model(orc.trits_of(wq, K), X[:, 3:], tau=tau))
+
+
+@pytest.mark.parametrize("K,M,N", [(2560, 2560, 1), (2560, 6912, 2), (1000, 300, 4), (6912, 2560, 1)])
+def test_matmul_t_f_one_launch_bits(ctx, orc, K, M, N):
+    """The transposed product (tau folded into the digit split per k) in one launch, against the
+    three launches and the digit model on the transposed trits."""
+    say(f"ternary_matmul_t_f one launch K={K} M={M} N={N}")
+    A, tau, At, rpT = transposed_case(ctx, orc, K, M, seed=K + M + 5 * N)
+    B = normal((K, N), 60 + N)
+    Bd = dev(B)
+    one = host(ctx.ternary_matmul_t_f(rpT, dev(tau), Bd, M))
+    three = host(ctx.ternary_matmul_t_f(rpT, dev(tau), misaligned(Bd), M))
+    assert same_bits(one, three)
+    trT = orc.trits_of(At.cpu().numpy().view(np.uint32), K)
+    assert same_bits(one, digit_model(trT, B, kscale=tau))
