@@ -584,21 +584,34 @@ __global__ __launch_bounds__(kSmallBlock) void k_embed(const float* __restrict__
 // ids[b] = the reference greedy rule over column b of logits (V, B): best = l[0], then every
 // l[v] > best replaces it (first index of the largest value; NaN entries never win, a NaN at
 // v = 0 keeps index 0).
-__global__ __launch_bounds__(kSmallBlock) void k_argmax(const float* __restrict__ L, int V, int B, int32_t* ids)
+constexpr int kArgThreads = 1024;
+constexpr int kArgBatch = 16;  // loads in flight per thread (V <= 16384 in one batch)
+
+__global__ __launch_bounds__(kArgThreads) void k_argmax(const float* __restrict__ L, int V, int B, int32_t* ids)
 {
-    __shared__ float sv[kSmallBlock / kWave];
-    __shared__ int si[kSmallBlock / kWave];
+    __shared__ float sv[kArgThreads / kWave];
+    __shared__ int si[kArgThreads / kWave];
     const int b = blockIdx.x, tid = threadIdx.x;
     float bv = -__builtin_inff();
     int bi = -1;
-    for (int v = tid; v < V; v += kSmallBlock)
+    // each thread scans v = tid + kArgThreads j in ascending order (strict > keeps the first of
+    // equal values; NaN never wins), a batch of loads at a time
+    for (int v0 = tid; v0 < V; v0 += kArgThreads * kArgBatch)
     {
-        const float x = L[(size_t)v * B + b];
-        if (x == x && (bi < 0 || x > bv))
+        float x[kArgBatch];
+#pragma unroll
+        for (int u = 0; u < kArgBatch; ++u)
         {
-            bv = x;
-            bi = v;
+            const int v = v0 + u * kArgThreads;
+            x[u] = v < V ? L[(size_t)v * B + b] : __builtin_nanf("");
         }
+#pragma unroll
+        for (int u = 0; u < kArgBatch; ++u)
+            if (x[u] == x[u] && (bi < 0 || x[u] > bv))
+            {
+                bv = x[u];
+                bi = v0 + u * kArgThreads;
+            }
     }
     for (int off = 32; off >= 1; off >>= 1)
     {
@@ -618,12 +631,13 @@ __global__ __launch_bounds__(kSmallBlock) void k_argmax(const float* __restrict_
     __syncthreads();
     if (tid == 0)
     {
-        for (int w = 1; w < kSmallBlock / kWave; ++w)
+        for (int w = 1; w < kArgThreads / kWave; ++w)
             if (si[w] >= 0 && (bi < 0 || sv[w] > bv || (sv[w] == bv && si[w] < bi)))
             {
                 bv = sv[w];
                 bi = si[w];
             }
+        // the reference's loop starts from l[0]: a NaN there is never replaced
         const float l0 = L[b];
         ids[b] = (l0 != l0 || bi < 0) ? 0 : bi;
     }
@@ -680,7 +694,7 @@ hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, 
 
 hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids)
 {
-    k_argmax<<<dim3((unsigned)B), kSmallBlock, 0, st>>>(L, (int)V, (int)B, ids);
+    k_argmax<<<dim3((unsigned)B), kArgThreads, 0, st>>>(L, (int)V, (int)B, ids);
     return hipGetLastError();
 }
 

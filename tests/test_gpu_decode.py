@@ -177,6 +177,14 @@ def test_add_gather_argmax_bitexact(ctx, orc):
     L[:, 7] = np.nan
     L[9999, 8] = 2.0
     assert host(ctx.argmax_cols(dev(L))).tolist() == orc.argmax_cols(L).tolist()
+    # a vocabulary past one load batch per thread (16 x 1024): ties across batches, all -inf
+    L = uniform((40000, 4), 25)
+    L[5, 0] = L[20000, 0] = 3.0        # equal maxima in different batches: the first wins
+    L[39999, 1] = 3.0
+    L[:, 2] = -np.inf
+    L[16384, 3] = np.nan
+    L[16385, 3] = 2.0
+    assert host(ctx.argmax_cols(dev(L))).tolist() == orc.argmax_cols(L).tolist() == [5, 39999, 0, 16385]
 
 
 # ---------------------------------------------------------------- the whole decode step
