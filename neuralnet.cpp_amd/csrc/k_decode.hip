@@ -477,32 +477,43 @@ __global__ __launch_bounds__(DK) void k_attn_merge(AttnArgs a)
     const size_t stride = (size_t)(a.R * DK + kRecPad);
     const float* rec0 = a.part + (size_t)(b * a.Hkv + g) * a.nchunk * stride;
     float M = -__builtin_inff(), num = 0.f, den = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += kMergeBatch)
+    // the loads of two batches are issued together (one round trip for up to 32 chunks); the
+    // arithmetic stays per batch of kMergeBatch
+    for (int c00 = 0; c00 < nch; c00 += 2 * kMergeBatch)
     {
-        float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+        float mv[2][kMergeBatch], lv[2][kMergeBatch], av[2][kMergeBatch];
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j)
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j)
+            {
+                const int c = c00 + hb * kMergeBatch + j;
+                const bool ok = c < nch;
+                const float* rc = rec0 + (size_t)(ok ? c : c00) * stride;
+                mv[hb][j] = ok ? rc[a.R * DK + r] : -__builtin_inff();
+                lv[hb][j] = ok ? rc[a.R * DK + 8 + r] : 0.f;
+                av[hb][j] = ok ? rc[r * DK + i] : 0.f;
+            }
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
         {
-            const bool ok = c0 + j < nch;
-            const float* rc = rec0 + (size_t)(ok ? c0 + j : c0) * stride;
-            mv[j] = ok ? rc[a.R * DK + r] : -__builtin_inff();
-            lv[j] = ok ? rc[a.R * DK + 8 + r] : 0.f;
-            av[j] = ok ? rc[r * DK + i] : 0.f;
-        }
-        float Mb = M;
+            const int c0 = c00 + hb * kMergeBatch;
+            if (c0 >= nch) break;
+            float Mb = M;
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, mv[j]);
-        const float resc = expf(M - Mb);  // 0 on the first batch (M = -inf)
-        num = c0 == 0 ? 0.f : num * resc;
-        den = c0 == 0 ? 0.f : den * resc;
+            for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, mv[hb][j]);
+            const float resc = expf(M - Mb);  // 0 on the first batch (M = -inf)
+            num = c0 == 0 ? 0.f : num * resc;
+            den = c0 == 0 ? 0.f : den * resc;
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j)
-        {
-            const float e = c0 + j < nch ? expf(mv[j] - Mb) : 0.f;
-            num = __builtin_fmaf(e, av[j], num);
-            den = __builtin_fmaf(e, lv[j], den);
+            for (int j = 0; j < kMergeBatch; ++j)
+            {
+                const float e = c0 + j < nch ? expf(mv[hb][j] - Mb) : 0.f;
+                num = __builtin_fmaf(e, av[hb][j], num);
+                den = __builtin_fmaf(e, lv[hb][j], den);
+            }
+            M = Mb;
         }
-        M = Mb;
     }
     a.out[(size_t)(h * DK + i) * a.B + b] = num / den;
 }
