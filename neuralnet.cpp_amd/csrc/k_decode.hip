@@ -40,9 +40,6 @@ namespace
 
 constexpr int kAttnT = 128;        // cache positions per work-group
 constexpr int kAttnThreads = 256;  // 4 waves
-#ifndef NNHIP_ATTN_VEARLY
-#define NNHIP_ATTN_VEARLY 0  // value loads issued together with the key loads
-#endif
 #ifndef NNHIP_ATTN_MINW
 #define NNHIP_ATTN_MINW 5          // waves per SIMD the chunk kernel is compiled for (<= 96 VGPRs)
 #endif
@@ -296,9 +293,6 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
                 vv[u] = ld_f4(rv, row, 16u * vi);
             }
         };
-#if NNHIP_ATTN_VEARLY
-        load_values();
-#endif
 
         // ---- scores of the chunk, PB passes of 32 positions at a time
 #pragma unroll
@@ -349,10 +343,8 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         __syncthreads();
 
         // ---- value rows of the whole chunk: issued before the softmax so its latency hides
-        //      behind them (or with the keys, NNHIP_ATTN_VEARLY)
-#if !NNHIP_ATTN_VEARLY
+        //      behind them
         load_values();
-#endif
 
         // ---- chunk softmax statistics: one wave per head
         for (int r = w; r < R; r += 4)
