@@ -33,8 +33,11 @@ constexpr int kGemvMaxM = 16;
 //  * LDS: the group's activations are staged in LDS (they fit kGemvLdsBudget), one 16-row
 //    tile per wave item, 3 k-tile stages in flight, 16 waves per CU (M = 1 decode);
 //  * register: activations are loaded with the weights, 8 row tiles per item share them,
-//    3 stages, 8 waves per CU (larger M). At M = 16 the sweep measured 4505 GB/s with 4 tiles
-//    and 4 stages, 5038 with 8 and 3 (16 tiles: 2038, register-starved).
+//    3 stages (larger M). The kernel takes 481 VGPRs (accumulators, stages and epilogue
+//    operands of 8 row tiles), so one wave per SIMD is resident: the grid is 4 waves per CU
+//    (sized for 8, the launch ran as two rounds: 5018 against 5117 GB/s on the M = 16 sweep).
+//    At M = 16 the sweep measured 4505 GB/s with 4 tiles and 4 stages, 4635 with 4 tiles at
+//    two waves per SIMD (256 VGPRs), 5117 with 8 and 3.
 // Tuned on MI355X with the 30-layer BitNet-2B sweep (M = 1 and M = 16).
 #ifndef NNHIP_GEMV_LDS_DEPTH
 #define NNHIP_GEMV_LDS_DEPTH 3
@@ -49,7 +52,7 @@ constexpr int kGemvMaxM = 16;
 #define NNHIP_GEMV_REG_DEPTH 3
 #endif
 #ifndef NNHIP_GEMV_REG_WAVES
-#define NNHIP_GEMV_REG_WAVES 8
+#define NNHIP_GEMV_REG_WAVES 4
 #endif
 constexpr int kLdsRTW = 1, kLdsDepth = NNHIP_GEMV_LDS_DEPTH, kLdsWavesPerCu = NNHIP_GEMV_LDS_WAVES;
 constexpr int kRegRTW = NNHIP_GEMV_REG_RTW, kRegDepth = NNHIP_GEMV_REG_DEPTH, kRegWavesPerCu = NNHIP_GEMV_REG_WAVES;
