@@ -369,11 +369,13 @@ nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, si
 nnhip_status nnhip_group_run(nnhip_ctx* ctx, nnhip_group* group);
 nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group);
 
-/* What nnhip_group_create chose for a group: *lds_variant = 1 when the group's distinct
- * activation blocks fit the LDS budget and the kernel reads its B operands from LDS (one 16-row
- * tile per schedule item), 0 for the register variant (activations loaded with the weights);
- * *waves = waves launched; *lds_bytes = bytes of activations staged per block. Any output may be
- * NULL. No reference counterpart (introspection for tests and measurement). */
+/* What nnhip_group_create chose for a group: *lds_variant = 1 when every launch of the group
+ * stages its activation blocks in LDS and reads its B operands there (one 16-row tile per
+ * schedule item), 0 when the group runs the register variant only (activations loaded with the
+ * weights), 2 when blocks over the LDS budget put part of the problems on the register variant
+ * (one launch each, back to back); *waves = waves launched over all launches; *lds_bytes = the
+ * largest staging per block. Any output may be NULL. No reference counterpart (introspection for
+ * tests and measurement). */
 nnhip_status nnhip_group_info(const nnhip_group* group, int* lds_variant, size_t* waves, size_t* lds_bytes);
 
 /* Number of waves the decode GEMV launches for `items` row tiles (for roofline accounting). */

@@ -806,10 +806,12 @@ class Context:
         _check(lib().nnhip_group_destroy(self.h, h), "nnhip_group_destroy")
 
     def group_info(self, h) -> dict:
-        """The variant nnhip_group_create chose: {"lds": bool, "waves": int, "lds_bytes": int}."""
+        """What nnhip_group_create chose: {"lds": True (every launch stages its activations in LDS),
+        False (register variant only) or "mixed", "waves": int, "lds_bytes": int}."""
         v, w, b = ctypes.c_int(0), _sz(0), _sz(0)
         _check(lib().nnhip_group_info(h, ctypes.byref(v), ctypes.byref(w), ctypes.byref(b)), "nnhip_group_info")
-        return {"lds": bool(v.value), "waves": int(w.value), "lds_bytes": int(b.value)}
+        lds = {0: False, 1: True}.get(v.value, "mixed")
+        return {"lds": lds, "waves": int(w.value), "lds_bytes": int(b.value)}
 
     def gemv_grid_waves(self, items: int) -> int:
         return int(lib().nnhip_gemv_grid_waves(self.h, items))

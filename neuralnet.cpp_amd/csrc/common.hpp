@@ -128,10 +128,14 @@ struct XStage
     const int8_t* src;
     uint32_t bytes;   // multiple of 256
     uint32_t lds_off;
+    uint32_t row;     // bytes of one token row (Kp): the 16-byte units of row t are staged XOR-swizzled
 };
 
 // LDS budget per block for staged activations (3 blocks of 4 waves fit one CU).
 constexpr uint32_t kGemvLdsBudget = 48 * 1024;
+// A single activation block up to this size is staged by 1024-thread blocks (16 waves sharing
+// it, one block per CU); larger ones go to the register variant.
+constexpr uint32_t kGemvLdsBigBudget = 152 * 1024;
 
 // ---- reference-layout kernels (k_ref.hip)
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* dst, uint32_t value, size_t words);

@@ -43,7 +43,8 @@ struct Src
     __amdgpu_buffer_rsrc_t rw[kRTW];  // one resource per row tile (num_records = KT KiB, 0 past N)
     __amdgpu_buffer_rsrc_t rx;
     uint32_t voff_w, voff_x;
-    const uint8_t* xl;  // LDS path: this lane's activation row + 16 g
+    const uint8_t* xl;  // LDS path: this lane's activation row
+    uint32_t sw0, sw1;  // LDS path: byte offsets of this lane's units (g, 4 + g) in a 128-byte group
 };
 
 template <bool LDS, int kRTW>
@@ -62,7 +63,7 @@ template <int kRTW>
 __device__ __forceinline__ void read_x_lds(v4i (&x)[4], const Src<kRTW>& s, int kt)
 {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(s.xl + kt * 256 + 64 * j);
+    for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(s.xl + kt * 256 + (j >> 1) * 128 + ((j & 1) ? s.sw1 : s.sw0));
 }
 
 // Loads are unconditional: a stage past the last k tile reads beyond its resource
@@ -143,7 +144,12 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     s.voff_w = (uint32_t)lane * 16u;
     if constexpr (LDS)
     {
-        s.xl = lds + p.xlds + (t < p.M ? t : 0) * Kp + 16 * g;
+        // operand j of k tile kt is 16-byte column 16 kt + 4 j + g: unit (4 (j & 1) + g) ^ (tr & 7) of
+        // the 128-byte group 2 kt + (j >> 1) in the staged row tr (the identity for M = 1)
+        const int tr = t < p.M ? t : 0;
+        s.xl = lds + p.xlds + tr * Kp;
+        s.sw0 = 16u * (uint32_t)(g ^ (tr & 7));
+        s.sw1 = 16u * (uint32_t)((4 + g) ^ (tr & 7));
     }
     else
     {
@@ -199,14 +205,21 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     }
 }
 
-// Copy the listed activation blocks into LDS (whole block cooperates), then barrier.
+// Copy the listed activation blocks into LDS (whole block cooperates), then barrier. Unit u
+// (16 bytes) of token row t lands at unit u ^ (t & 7) of its 128-byte group, so the 16 token rows
+// an MFMA operand reads sit in 8 distinct bank groups (without it, rows Kp apart share banks).
+template <int kThreads = kBlock>
 __device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__ xs, int n_x)
 {
     for (int e = 0; e < n_x; ++e)
     {
         const XStage x = xs[e];
-        for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kBlock * 16u)
-            *reinterpret_cast<v4i*>(lds + x.lds_off + off) = *reinterpret_cast<const v4i*>(x.src + off);
+        for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kThreads * 16u)
+        {
+            const uint32_t t = off / x.row, u = (off - t * x.row) >> 4;
+            const uint32_t dst = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
+            *reinterpret_cast<v4i*>(lds + x.lds_off + dst) = *reinterpret_cast<const v4i*>(x.src + off);
+        }
     }
     __syncthreads();
 }
@@ -226,17 +239,19 @@ __global__ __launch_bounds__(kBlock) void k_gemv(GemvProblem p, int n_items, XSt
 // Grouped: wave w processes the items wave_items[wave_start[w] .. wave_start[w+1]) (each
 // item = problem << 20 | first row tile). The host balances the per-wave lists by cost
 // once, at group creation, so the kernel needs no atomics or memset and can be replayed.
-template <bool LDS, int kRTW, int kDepth>
-__global__ __launch_bounds__(kBlock) void k_gemv_grouped(const GemvProblem* __restrict__ probs,
-                                                         const uint32_t* __restrict__ wave_start,
-                                                         const uint32_t* __restrict__ wave_items,
-                                                         int n_waves, const XStage* __restrict__ xs,
-                                                         int n_x)
+// kThreads = 1024 (16 waves sharing one staging, one block per CU) for an activation block too
+// large for four 4-wave blocks per CU.
+template <bool LDS, int kRTW, int kDepth, int kThreads = kBlock>
+__global__ __launch_bounds__(kThreads) void k_gemv_grouped(const GemvProblem* __restrict__ probs,
+                                                           const uint32_t* __restrict__ wave_start,
+                                                           const uint32_t* __restrict__ wave_items,
+                                                           int n_waves, const XStage* __restrict__ xs,
+                                                           int n_x)
 {
     extern __shared__ __align__(16) uint8_t lds[];
-    if constexpr (LDS) stage_x(lds, xs, n_x);
+    if constexpr (LDS) stage_x<kThreads>(lds, xs, n_x);
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6));
+    const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6));
     if (w >= n_waves) return;
     const uint32_t b = wave_start[w], e = wave_start[w + 1];
     for (uint32_t i = b; i < e; ++i)
@@ -554,7 +569,14 @@ size_t gemv_grid_waves(size_t n_items, int num_cus, bool lds)
     const GemvVariant v = gemv_variant(lds);
     size_t blocks = ceil_div(n_items, (size_t)(kBlock / kWave));
     const size_t cap = (size_t)(num_cus > 0 ? num_cus : 256) * (v.waves_per_cu / (kBlock / kWave));
-    if (blocks > cap) blocks = cap;
+    if (blocks > cap)
+    {
+        blocks = cap;
+        // a few items per wave: as many waves as give every wave the same count (4800 items on
+        // 4096 waves would leave most waves idle while 704 run a second item)
+        const size_t per = ceil_div(n_items, cap * (kBlock / kWave));
+        if (per <= 4) blocks = ceil_div(ceil_div(n_items, per), (size_t)(kBlock / kWave));
+    }
     if (blocks < 1) blocks = 1;
     return blocks * (kBlock / kWave);
 }
@@ -615,7 +637,7 @@ hipError_t launch_gemv(hipStream_t st, const GemvProblem& p, int num_cus)
     if (lds)
     {
         q.xlds = 0;
-        const XStage xs{p.xi, xbytes, 0};
+        const XStage xs{p.xi, xbytes, 0, (uint32_t)p.KT * kTileK};
         hipLaunchKernelGGL((k_gemv<true, kLdsRTW, kLdsDepth>), dim3(blocks), dim3(kBlock), xbytes, st, q,
                            (int)items, xs);
     }
@@ -633,6 +655,24 @@ hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const
                                int n_xstage, uint32_t lds_bytes)
 {
     if (n_waves == 0) return hipSuccess;
+    if (n_xstage > 0 && lds_bytes > kGemvLdsBudget)
+    {
+        // one large activation block: 16 waves per block, one block per CU
+        constexpr int kBig = 1024;
+        static bool attr = false;
+        if (!attr)
+        {
+            const hipError_t e = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&k_gemv_grouped<true, kLdsRTW, kLdsDepth, kBig>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsBigBudget);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        const unsigned blocks = (unsigned)ceil_div(n_waves, (size_t)(kBig / kWave));
+        hipLaunchKernelGGL((k_gemv_grouped<true, kLdsRTW, kLdsDepth, kBig>), dim3(blocks), dim3(kBig), lds_bytes, st,
+                           d_probs, d_wave_start, d_wave_items, (int)n_waves, d_xstage, n_xstage);
+        return hipGetLastError();
+    }
     const unsigned blocks = (unsigned)ceil_div(n_waves, (size_t)(kBlock / kWave));
     if (n_xstage > 0)
         hipLaunchKernelGGL((k_gemv_grouped<true, kLdsRTW, kLdsDepth>), dim3(blocks), dim3(kBlock), lds_bytes,

@@ -46,13 +46,18 @@ struct nnhip_ctx
 
 struct nnhip_group
 {
-    GemvProblem* d_probs = nullptr;
-    uint32_t* d_wave_start = nullptr;  // n_waves + 1 offsets into d_wave_items
-    uint32_t* d_wave_items = nullptr;  // problem << 20 | row tile, grouped by wave
-    XStage* d_xstage = nullptr;        // activation blocks staged in LDS (if they fit)
-    int n_xstage = 0;
-    uint32_t lds_bytes = 0;
-    size_t n_waves = 0;
+    // one kernel launch over a subset of the group's problems
+    struct Launch
+    {
+        GemvProblem* d_probs = nullptr;
+        uint32_t* d_wave_start = nullptr;  // n_waves + 1 offsets into d_wave_items
+        uint32_t* d_wave_items = nullptr;  // problem << 20 | row tile, grouped by wave
+        XStage* d_xstage = nullptr;        // activation blocks staged in LDS (LDS variant)
+        int n_xstage = 0;
+        uint32_t lds_bytes = 0;
+        size_t n_waves = 0;
+    };
+    std::vector<Launch> launches;
 };
 
 namespace
@@ -1020,113 +1025,184 @@ nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, si
         p.xlds = -1;
     }
 
-    // Distinct activation blocks: if they fit the LDS budget together, every block of the
-    // kernel stages them once and the problems read their B operands from LDS (LDS variant);
-    // otherwise the register variant loads them with the weights.
-    std::vector<XStage> xstage;
+    // Distinct activation blocks. If they fit the LDS budget together, one launch stages them all
+    // and reads its B operands from LDS (LDS variant). Otherwise the blocks that fit are packed,
+    // first fit in order, into LDS launches of their own problems; a block over the budget but
+    // within kGemvLdsBigBudget gets an LDS launch of its own with 16-wave blocks (one per CU);
+    // the problems of still larger blocks go to one launch of the register variant (activations
+    // loaded with the weights). The launches run one after another on the stream.
+    struct Part
     {
+        std::vector<size_t> probs;  // indices into probs
+        std::vector<XStage> xstage;
         uint32_t lds = 0;
-        bool fits = true;
-        for (GemvProblem& p : probs)
+    };
+    std::vector<Part> parts;
+    {
+        std::vector<XStage> distinct;
+        std::vector<int> act_of(count);
+        for (size_t i = 0; i < count; ++i)
         {
+            const GemvProblem& p = probs[i];
             const uint32_t bytes = (uint32_t)p.M * (uint32_t)p.KT * kTileK;
             int found = -1;
-            for (size_t e = 0; e < xstage.size(); ++e)
-                if (xstage[e].src == p.xi && xstage[e].bytes == bytes) found = (int)e;
+            for (size_t e = 0; e < distinct.size(); ++e)
+                if (distinct[e].src == p.xi && distinct[e].bytes == bytes) found = (int)e;
             if (found < 0)
             {
-                if (lds + bytes > kGemvLdsBudget)
-                {
-                    fits = false;
-                    break;
-                }
-                xstage.push_back(XStage{p.xi, bytes, lds});
-                found = (int)xstage.size() - 1;
-                lds += bytes;
+                distinct.push_back(XStage{p.xi, bytes, 0, (uint32_t)p.KT * kTileK});
+                found = (int)distinct.size() - 1;
             }
-            p.xlds = (int32_t)xstage[found].lds_off;
+            act_of[i] = found;
         }
-        if (!fits)
+        std::vector<int> part_of(distinct.size(), -1);  // LDS part of each activation block
+        int reg_part = -1;
+        uint32_t total = 0;
+        for (const XStage& x : distinct) total += x.bytes;
+        for (size_t e = 0; e < distinct.size(); ++e)
         {
-            xstage.clear();
-            for (GemvProblem& p : probs) p.xlds = -1;
+            XStage x = distinct[e];
+            if (x.bytes > kGemvLdsBigBudget) continue;  // register variant
+            if (x.bytes > kGemvLdsBudget)
+            {
+                // a launch of its own with 16-wave blocks, one per CU
+                parts.push_back(Part{});
+                x.lds_off = 0;
+                parts.back().xstage.push_back(x);
+                parts.back().lds = x.bytes;
+                part_of[e] = (int)parts.size() - 1;
+                continue;
+            }
+            int target = -1;
+            if (total <= kGemvLdsBudget)
+                target = parts.empty() ? -1 : 0;
+            else
+                for (size_t q = 0; q < parts.size(); ++q)
+                    if (!parts[q].xstage.empty() && parts[q].lds <= kGemvLdsBudget &&
+                        parts[q].lds + x.bytes <= kGemvLdsBudget)
+                        target = (int)q;
+            if (target < 0)
+            {
+                parts.push_back(Part{});
+                target = (int)parts.size() - 1;
+            }
+            x.lds_off = parts[target].lds;
+            parts[target].xstage.push_back(x);
+            parts[target].lds += x.bytes;
+            part_of[e] = target;
         }
-    }
-    const bool use_lds = !xstage.empty();
-    const GemvVariant var = gemv_variant(use_lds);
-
-    std::vector<uint32_t> items;
-    for (size_t i = 0; i < count; ++i)
-    {
-        const size_t rts = ceil_div((size_t)probs[i].N, 16);
-        for (size_t rt = 0; rt < rts; rt += (size_t)var.row_tiles) items.push_back((uint32_t)((i << 20) | rt));
-    }
-    NNHIP_REQUIRE(items.size() < 0x7FFFFFFFull, fn, "too many row tiles");
-
-    // Longest-processing-time schedule: items (var.row_tiles row tiles of one problem) by
-    // decreasing cost (weight tiles + 1 for the epilogue), each to the currently
-    // least-loaded wave. Waves = the variant's resident wave slots.
-    const size_t n_waves = items.empty() ? 0 : gemv_grid_waves(items.size(), ctx->num_cus, use_lds);
-    std::vector<uint32_t> wave_start(n_waves + 1, 0), wave_items(items.size());
-    if (n_waves > 0)
-    {
-        auto cost = [&](uint32_t it) {
-            const GemvProblem& p = probs[it >> 20];
-            const uint64_t rts = std::min<uint64_t>((uint64_t)var.row_tiles, ceil_div(p.N, 16) - (it & 0xFFFFFu));
-            return (uint64_t)p.KT * rts + 1;
-        };
-        std::stable_sort(items.begin(), items.end(), [&](uint32_t a, uint32_t b) { return cost(a) > cost(b); });
-        using Slot = std::pair<uint64_t, uint32_t>;  // (load, wave)
-        std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> heap;
-        for (uint32_t w = 0; w < n_waves; ++w) heap.push({0, w});
-        std::vector<std::vector<uint32_t>> lists(n_waves);
-        for (const uint32_t it : items)
+        for (size_t i = 0; i < count; ++i)
         {
-            Slot sl = heap.top();
-            heap.pop();
-            lists[sl.second].push_back(it);
-            sl.first += cost(it);
-            heap.push(sl);
+            const int e = act_of[i];
+            if (part_of[e] >= 0)
+            {
+                Part& pt = parts[part_of[e]];
+                for (const XStage& x : pt.xstage)
+                    if (x.src == distinct[e].src && x.bytes == distinct[e].bytes) probs[i].xlds = (int32_t)x.lds_off;
+                pt.probs.push_back(i);
+            }
+            else
+            {
+                if (reg_part < 0)
+                {
+                    parts.push_back(Part{});
+                    reg_part = (int)parts.size() - 1;
+                }
+                parts[reg_part].probs.push_back(i);
+            }
         }
-        size_t pos = 0;
-        for (size_t w = 0; w < n_waves; ++w)
-        {
-            wave_start[w] = (uint32_t)pos;
-            for (const uint32_t it : lists[w]) wave_items[pos++] = it;
-        }
-        wave_start[n_waves] = (uint32_t)pos;
     }
 
     auto* grp = new nnhip_group;
-    grp->n_waves = n_waves;
-    grp->n_xstage = (int)xstage.size();
-    for (const XStage& x : xstage) grp->lds_bytes += x.bytes;
-    if (n_waves > 0)
+    auto release = [&]() {
+        for (nnhip_group::Launch& l : grp->launches)
+        {
+            (void)hipFree(l.d_probs);
+            (void)hipFree(l.d_wave_start);
+            (void)hipFree(l.d_wave_items);
+            (void)hipFree(l.d_xstage);
+        }
+        delete grp;
+    };
+    for (const Part& pt : parts)
     {
-        hipError_t e = hipMalloc(&grp->d_probs, sizeof(GemvProblem) * count);
-        if (e == hipSuccess && !xstage.empty()) e = hipMalloc(&grp->d_xstage, sizeof(XStage) * xstage.size());
-        if (e == hipSuccess && !xstage.empty())
-            e = hipMemcpyAsync(grp->d_xstage, xstage.data(), sizeof(XStage) * xstage.size(),
-                               hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess) e = hipMalloc(&grp->d_wave_start, sizeof(uint32_t) * wave_start.size());
-        if (e == hipSuccess) e = hipMalloc(&grp->d_wave_items, sizeof(uint32_t) * wave_items.size());
+        const bool use_lds = !pt.xstage.empty();
+        const GemvVariant var = gemv_variant(use_lds);
+        std::vector<GemvProblem> lp;
+        for (const size_t i : pt.probs) lp.push_back(probs[i]);
+        std::vector<uint32_t> items;
+        for (size_t i = 0; i < lp.size(); ++i)
+        {
+            const size_t rts = ceil_div((size_t)lp[i].N, 16);
+            for (size_t rt = 0; rt < rts; rt += (size_t)var.row_tiles) items.push_back((uint32_t)((i << 20) | rt));
+        }
+        if (items.size() >= 0x7FFFFFFFull)
+        {
+            release();
+            return fail(NNHIP_ERR_INVALID_ARG, fn, "too many row tiles");
+        }
+
+        // Longest-processing-time schedule: items (var.row_tiles row tiles of one problem) by
+        // decreasing cost (weight tiles + 1 for the epilogue), each to the currently
+        // least-loaded wave. Waves = the variant's resident wave slots.
+        const size_t n_waves = items.empty() ? 0 : gemv_grid_waves(items.size(), ctx->num_cus, use_lds);
+        std::vector<uint32_t> wave_start(n_waves + 1, 0), wave_items(items.size());
+        if (n_waves > 0)
+        {
+            auto cost = [&](uint32_t it) {
+                const GemvProblem& p = lp[it >> 20];
+                const uint64_t rts = std::min<uint64_t>((uint64_t)var.row_tiles, ceil_div(p.N, 16) - (it & 0xFFFFFu));
+                return (uint64_t)p.KT * rts + 1;
+            };
+            std::stable_sort(items.begin(), items.end(), [&](uint32_t a, uint32_t b) { return cost(a) > cost(b); });
+            using Slot = std::pair<uint64_t, uint32_t>;  // (load, wave)
+            std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> heap;
+            for (uint32_t w = 0; w < n_waves; ++w) heap.push({0, w});
+            std::vector<std::vector<uint32_t>> lists(n_waves);
+            for (const uint32_t it : items)
+            {
+                Slot sl = heap.top();
+                heap.pop();
+                lists[sl.second].push_back(it);
+                sl.first += cost(it);
+                heap.push(sl);
+            }
+            size_t pos = 0;
+            for (size_t w = 0; w < n_waves; ++w)
+            {
+                wave_start[w] = (uint32_t)pos;
+                for (const uint32_t it : lists[w]) wave_items[pos++] = it;
+            }
+            wave_start[n_waves] = (uint32_t)pos;
+        }
+        if (n_waves == 0) continue;
+
+        nnhip_group::Launch l;
+        l.n_waves = n_waves;
+        l.n_xstage = (int)pt.xstage.size();
+        l.lds_bytes = pt.lds;
+        grp->launches.push_back(l);
+        nnhip_group::Launch& L = grp->launches.back();
+        hipError_t e = hipMalloc(&L.d_probs, sizeof(GemvProblem) * lp.size());
+        if (e == hipSuccess && use_lds) e = hipMalloc(&L.d_xstage, sizeof(XStage) * pt.xstage.size());
+        if (e == hipSuccess && use_lds)
+            e = hipMemcpyAsync(L.d_xstage, pt.xstage.data(), sizeof(XStage) * pt.xstage.size(), hipMemcpyHostToDevice,
+                               ctx->stream);
+        if (e == hipSuccess) e = hipMalloc(&L.d_wave_start, sizeof(uint32_t) * wave_start.size());
+        if (e == hipSuccess) e = hipMalloc(&L.d_wave_items, sizeof(uint32_t) * wave_items.size());
         if (e == hipSuccess)
-            e = hipMemcpyAsync(grp->d_probs, probs.data(), sizeof(GemvProblem) * count,
+            e = hipMemcpyAsync(L.d_probs, lp.data(), sizeof(GemvProblem) * lp.size(), hipMemcpyHostToDevice,
+                               ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(L.d_wave_start, wave_start.data(), sizeof(uint32_t) * wave_start.size(),
                                hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess)
-            e = hipMemcpyAsync(grp->d_wave_start, wave_start.data(), sizeof(uint32_t) * wave_start.size(),
-                               hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(grp->d_wave_items, wave_items.data(), sizeof(uint32_t) * wave_items.size(),
+            e = hipMemcpyAsync(L.d_wave_items, wave_items.data(), sizeof(uint32_t) * wave_items.size(),
                                hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess)
         {
-            (void)hipFree(grp->d_probs);
-            (void)hipFree(grp->d_wave_start);
-            (void)hipFree(grp->d_wave_items);
-            (void)hipFree(grp->d_xstage);
-            delete grp;
+            release();
             return hip_fail(fn, "descriptor upload", e);
         }
     }
@@ -1139,9 +1215,9 @@ nnhip_status nnhip_group_run(nnhip_ctx* ctx, nnhip_group* group)
     const char* fn = "nnhip_group_run";
     NNHIP_CHECK_CTX(fn);
     NNHIP_REQUIRE(group != nullptr, fn, "null group");
-    NNHIP_LAUNCH(fn, launch_gemv_grouped(ctx->stream, group->d_probs, group->d_wave_start,
-                                         group->d_wave_items, group->n_waves, group->d_xstage,
-                                         group->n_xstage, group->lds_bytes));
+    for (const nnhip_group::Launch& l : group->launches)
+        NNHIP_LAUNCH(fn, launch_gemv_grouped(ctx->stream, l.d_probs, l.d_wave_start, l.d_wave_items, l.n_waves,
+                                             l.d_xstage, l.n_xstage, l.lds_bytes));
     return NNHIP_OK;
 }
 
@@ -1151,10 +1227,13 @@ nnhip_status nnhip_group_destroy(nnhip_ctx* ctx, nnhip_group* group)
     NNHIP_CHECK_CTX(fn);
     if (!group) return NNHIP_OK;
     const hipError_t e = hipStreamSynchronize(ctx->stream);
-    (void)hipFree(group->d_probs);
-    (void)hipFree(group->d_wave_start);
-    (void)hipFree(group->d_wave_items);
-    (void)hipFree(group->d_xstage);
+    for (const nnhip_group::Launch& l : group->launches)
+    {
+        (void)hipFree(l.d_probs);
+        (void)hipFree(l.d_wave_start);
+        (void)hipFree(l.d_wave_items);
+        (void)hipFree(l.d_xstage);
+    }
     delete group;
     if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
     return NNHIP_OK;
@@ -1164,9 +1243,16 @@ nnhip_status nnhip_group_info(const nnhip_group* group, int* lds_variant, size_t
 {
     const char* fn = "nnhip_group_info";
     NNHIP_REQUIRE(group != nullptr, fn, "null group");
-    if (lds_variant) *lds_variant = group->n_xstage > 0 ? 1 : 0;
-    if (waves) *waves = group->n_waves;
-    if (lds_bytes) *lds_bytes = group->lds_bytes;
+    size_t n_lds = 0, n_waves = 0, lds_max = 0;
+    for (const nnhip_group::Launch& l : group->launches)
+    {
+        n_lds += l.n_xstage > 0 ? 1 : 0;
+        n_waves += l.n_waves;
+        lds_max = std::max<size_t>(lds_max, l.lds_bytes);
+    }
+    if (lds_variant) *lds_variant = n_lds == 0 ? 0 : (n_lds == group->launches.size() ? 1 : 2);
+    if (waves) *waves = n_waves;
+    if (lds_bytes) *lds_bytes = lds_max;
     return NNHIP_OK;
 }
 

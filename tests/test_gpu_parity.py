@@ -446,7 +446,7 @@ STACK_SHAPES = [("q", 2560, 2560), ("k", 2560, 640), ("v", 2560, 640), ("o", 256
                 ("gate", 2560, 6912), ("up", 2560, 6912), ("down", 6912, 2560)]   # (name, K, N)
 
 
-def stack_group(ctx, orc, layers, M, seed, bias_layer=-1):
+def stack_group(ctx, orc, layers, M, seed, bias_layer=-1, shapes=None):
     """A reduced-depth copy of bench.py's headline group: `layers` x the seven BitNet-2B shapes,
     weights N(0, 0.02) ternarized by per-tensor absmean on the GPU (trit_pack is checked bit for
     bit elsewhere; the oracle below reads the same containers), one quantized activation block
@@ -454,7 +454,8 @@ def stack_group(ctx, orc, layers, M, seed, bias_layer=-1):
     import torch
     gen = torch.Generator(device="cuda")
     acts = {}
-    for K in (2560, 6912):
+    shapes = STACK_SHAPES if shapes is None else shapes
+    for K in sorted({K for (_, K, _) in shapes}):
         X = normal((K, M), seed + K)
         xi, s_d, rs = ctx.act_quant_i8(dev(X))
         s = orc.act_scale(X)
@@ -462,7 +463,7 @@ def stack_group(ctx, orc, layers, M, seed, bias_layer=-1):
         acts[K] = (xi, s_d, rs, orc.quantize_i8(X, s, True), s)
     probs, hosts = [], []
     for layer in range(layers):
-        for idx, (name, K, N) in enumerate(STACK_SHAPES):
+        for idx, (name, K, N) in enumerate(shapes):
             gen.manual_seed(seed * 131 + layer * 16 + idx)
             W = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
             tau = W.abs().double().mean().float().expand(N).contiguous()
@@ -506,12 +507,35 @@ def test_grouped_gemv_headline_group_lds(ctx, orc):
     check_stack_group(ctx, orc, probs, hosts, expect_lds=True)
 
 
-def test_grouped_gemv_m16_group_register(ctx, orc):
-    """bench.py's M=16 sweep group (2 layers x 7 shapes): its activations exceed the LDS budget, so
-    the register variant runs; every row of every problem bit for bit against the oracle."""
-    say("grouped gemv: M=16 group (register variant), 2 layers x 7 shapes")
+def test_grouped_gemv_m16_group_lds(ctx, orc):
+    """bench.py's M=16 sweep group (2 layers x 7 shapes): the K=2560 activations (40 KB) run in an
+    LDS launch of 4-wave blocks, the K=6912 ones (110 KB) in an LDS launch of 16-wave blocks (one
+    per CU), token rows XOR-swizzled; every row of every problem bit for bit against the oracle."""
+    say("grouped gemv: M=16 group (two LDS launches), 2 layers x 7 shapes")
     probs, hosts = stack_group(ctx, orc, 2, 16, 0xA2, bias_layer=0)
-    check_stack_group(ctx, orc, probs, hosts, expect_lds=False)
+    check_stack_group(ctx, orc, probs, hosts, expect_lds=True)
+
+
+@pytest.mark.parametrize("M", [16, 9, 2])
+def test_grouped_gemv_lds_swizzle_tokens(ctx, orc, M):
+    """The LDS variant with M tokens (rows staged with the unit swizzle u ^ (t & 7)): the K=2560
+    shapes of one layer share one activation block that fits the budget, every problem against
+    the oracle."""
+    say(f"grouped gemv: LDS variant at M={M}")
+    probs, hosts = stack_group(ctx, orc, 1, M, 0xA3 + M, bias_layer=0)
+    keep = [i for i, p in enumerate(probs) if p["K"] == 2560]
+    check_stack_group(ctx, orc, [probs[i] for i in keep], [hosts[i] for i in keep], expect_lds=True)
+
+
+def test_grouped_gemv_mixed_register(ctx, orc):
+    """An activation block over the 16-wave LDS budget (K=10240 at M=16: 160 KB) runs the register
+    variant in a launch of its own, beside an LDS launch for the K=2560 problems."""
+    say("grouped gemv: LDS + register launches (K=2560 and K=10240, M=16)")
+    shapes = [("a", 2560, 2560), ("b", 10240, 700), ("c", 2560, 640), ("d", 10240, 2560)]
+    probs, hosts = stack_group(ctx, orc, 1, 16, 0xA4, bias_layer=0, shapes=shapes)
+    check_stack_group(ctx, orc, probs, hosts, expect_lds="mixed")
+    keep = [i for i, p in enumerate(probs) if p["K"] == 10240]
+    check_stack_group(ctx, orc, [probs[i] for i in keep], [hosts[i] for i in keep], expect_lds=False)
 
 
 def test_invalid_arguments_raise(ctx, nnhip):
