@@ -1026,11 +1026,12 @@ nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, si
     }
 
     // Distinct activation blocks. If they fit the LDS budget together, one launch stages them all
-    // and reads its B operands from LDS (LDS variant). Otherwise the blocks that fit are packed,
-    // first fit in order, into LDS launches of their own problems; a block over the budget but
-    // within kGemvLdsBigBudget gets an LDS launch of its own with 16-wave blocks (one per CU);
-    // the problems of still larger blocks go to one launch of the register variant (activations
-    // loaded with the weights). The launches run one after another on the stream.
+    // and reads its B operands from LDS (LDS variant); if they fit kGemvLdsBigBudget together, one
+    // launch of 16-wave blocks (one per CU) does. Otherwise the blocks that fit are packed, first
+    // fit in order, into LDS launches of their own problems; a block over the budget but within
+    // kGemvLdsBigBudget gets an LDS launch of its own with 16-wave blocks; the problems of still
+    // larger blocks go to one launch of the register variant (activations loaded with the
+    // weights). The launches run one after another on the stream.
     struct Part
     {
         std::vector<size_t> probs;  // indices into probs
@@ -1059,9 +1060,20 @@ nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, si
         int reg_part = -1;
         uint32_t total = 0;
         for (const XStage& x : distinct) total += x.bytes;
+        // all blocks together within the 16-wave budget: one launch of 16-wave blocks stages them
+        const bool one_big = total > kGemvLdsBudget && total <= kGemvLdsBigBudget;
         for (size_t e = 0; e < distinct.size(); ++e)
         {
             XStage x = distinct[e];
+            if (one_big)
+            {
+                if (parts.empty()) parts.push_back(Part{});
+                x.lds_off = parts[0].lds;
+                parts[0].xstage.push_back(x);
+                parts[0].lds += x.bytes;
+                part_of[e] = 0;
+                continue;
+            }
             if (x.bytes > kGemvLdsBigBudget) continue;  // register variant
             if (x.bytes > kGemvLdsBudget)
             {

@@ -508,12 +508,22 @@ def test_grouped_gemv_headline_group_lds(ctx, orc):
 
 
 def test_grouped_gemv_m16_group_lds(ctx, orc):
-    """bench.py's M=16 sweep group (2 layers x 7 shapes): the K=2560 activations (40 KB) run in an
-    LDS launch of 4-wave blocks, the K=6912 ones (110 KB) in an LDS launch of 16-wave blocks (one
-    per CU), token rows XOR-swizzled; every row of every problem bit for bit against the oracle."""
-    say("grouped gemv: M=16 group (two LDS launches), 2 layers x 7 shapes")
+    """bench.py's M=16 sweep group (2 layers x 7 shapes): its two activation blocks (40 KB at
+    K=2560, 110 KB at K=6912) are staged together by 16-wave blocks (one per CU), token rows
+    XOR-swizzled; every row of every problem bit for bit against the oracle."""
+    say("grouped gemv: M=16 group (one LDS launch of 16-wave blocks), 2 layers x 7 shapes")
     probs, hosts = stack_group(ctx, orc, 2, 16, 0xA2, bias_layer=0)
     check_stack_group(ctx, orc, probs, hosts, expect_lds=True)
+
+
+def test_grouped_gemv_split_lds_launches(ctx, orc):
+    """Activation blocks over the 16-wave budget together (K=2560 and two K=6912 blocks at M=16:
+    261 KB): a launch of 4-wave blocks for the 40 KB block and one of 16-wave blocks for each
+    110 KB block, every problem against the oracle."""
+    say("grouped gemv: three LDS launches (M=16)")
+    p1, h1 = stack_group(ctx, orc, 1, 16, 0xA5, bias_layer=0)
+    p2, h2 = stack_group(ctx, orc, 1, 16, 0xA6, shapes=[("down2", 6912, 1000)])
+    check_stack_group(ctx, orc, p1 + p2, h1 + h2, expect_lds=True)
 
 
 @pytest.mark.parametrize("M", [16, 9, 2])
