@@ -412,6 +412,24 @@ nnhip_status nnhip_ternary_matmul_glu(nnhip_ctx* ctx, const void* rp, const floa
                                       const float* s, const int32_t* rowsum, const float* bias, size_t F,
                                       size_t K, size_t M, int act, float* h);
 
+/* nnhip_ternary_matmul_glu with h written token-major, (M, F): token m's F features contiguous,
+ * for a following per-token quantizer (nnhip_rmsnorm_quant_i8_tokens) that then reads each token
+ * as one contiguous row. Decode sizes only (the deep GEMV: M <= 16); other shapes return
+ * NNHIP_ERR_UNSUPPORTED. Same values as nnhip_ternary_matmul_glu, transposed. Replaces the fc1 +
+ * gated activation of FeedForward::forward (include/neuralnet.cpp/compute_layer_feedforward.hpp:
+ * 182-206; compute_layer_mlp.hpp:317-328, :405-414) inside the decode step. */
+nnhip_status nnhip_ternary_matmul_glu_tokens(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                             const float* s, const int32_t* rowsum, const float* bias, size_t F,
+                                             size_t K, size_t M, int act, float* h);
+
+/* nnhip_rmsnorm_quant_i8 (gamma != NULL) / nnhip_act_quant_i8 (gamma == NULL) on a token-major X
+ * (M, K): the same codes, scales and row sums as on X transposed, for 1 <= M <= 64 and K <= 11264
+ * (NNHIP_ERR_UNSUPPORTED otherwise). Replaces the SubLN RMSNorm -> quantize_i8 of the FFN's down
+ * projection (compute_layer_feedforward.hpp:201-206; compute_layer_mlp.hpp:686-707;
+ * compute_layer_bitlinear.hpp:443-448) in the decode step. */
+nnhip_status nnhip_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t K,
+                                           size_t M, int8_t* xi, float* s, int32_t* rowsum);
+
 /* Context scratch the block below uses (grown on demand, kept by the context). */
 size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M);
 

@@ -119,6 +119,9 @@ SIGNATURES = {
     "nnhip_glu_rows": (_sz, [_sz]),
     "nnhip_glu_interleave": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
     "nnhip_ternary_matmul_glu": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_int, _vp]),
+    "nnhip_ternary_matmul_glu_tokens": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_int,
+                                              _vp]),
+    "nnhip_rmsnorm_quant_i8_tokens": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _vp, _vp, _vp]),
     "nnhip_ffn_glu_workspace_bytes": (_sz, [_sz, _sz, _sz]),
     "nnhip_ffn_glu_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
                                _vp, _vp]),
@@ -752,6 +755,37 @@ class Context:
                                           self._dev(bias, torch.float32, "bias"), F, K, self._dev(wo), self._dev(to),
                                           self._dev(bo) if bo is not None else None), "nnhip_glu_interleave")
         return wo, to, bo
+
+    def ternary_matmul_glu_tokens(self, rp, tau, xi, s, rowsum, F: int, K: int, M: int, act: int = ACT_SWIGLU,
+                                  bias=None, out=None):
+        """ternary_matmul_glu with h token-major (M, F) (decode sizes)."""
+        torch = self._torch
+        h = self._empty((M, F), torch.float32) if out is None else out
+        self._bind_stream()
+        _check(lib().nnhip_ternary_matmul_glu_tokens(self.h, self._dev(rp, torch.int32, "rp"),
+                                                     self._dev(tau, torch.float32, "tau"),
+                                                     self._dev(xi, torch.int8, "xi"), self._dev(s, torch.float32, "s"),
+                                                     self._dev(rowsum, torch.int32, "rowsum"),
+                                                     self._dev(bias, torch.float32, "bias"), F, K, M, act,
+                                                     self._dev(h, torch.float32, "h")),
+               "nnhip_ternary_matmul_glu_tokens")
+        return h
+
+    def rmsnorm_quant_i8_tokens(self, X, gamma, eps: float, outs=None):
+        """[RMSNorm (gamma, or None) ->] absmax -> int8 of a token-major X (M, K); returns (xi, s, rowsum)."""
+        torch = self._torch
+        M, K = X.shape
+        if outs is None:
+            outs = (self._empty((M, kp(K)), torch.int8), self._empty((M,), torch.float32),
+                    self._empty((M,), torch.int32))
+        xi, s, rs = outs
+        self._bind_stream()
+        _check(lib().nnhip_rmsnorm_quant_i8_tokens(self.h, self._dev(X, torch.float32, "X"),
+                                                   self._dev(gamma, torch.float32, "gamma"), eps, K, M,
+                                                   self._dev(xi, torch.int8, "xi"), self._dev(s, torch.float32, "s"),
+                                                   self._dev(rs, torch.int32, "rowsum")),
+               "nnhip_rmsnorm_quant_i8_tokens")
+        return outs
 
     def ternary_matmul_glu(self, rp, tau, xi, s, rowsum, F: int, K: int, M: int, act: int = ACT_SWIGLU,
                            bias=None, out=None):

@@ -81,7 +81,7 @@ struct GemvProblem
     int32_t glu;          // prefill GEMM epilogue: 0 plain Y, else gated activation act = glu - 1
                           // (0 SwiGLU, 1 ReLU^2-GLU) of interleaved gate/up rows into y (glu_F, M)
     int32_t glu_F;        // features of the gated output (rows of y when glu != 0)
-    int32_t pad_;
+    int32_t ytm;          // deep decode GEMV with glu: h token-major (M, glu_F) instead of (glu_F, M)
     uint32_t* amax;       // prefill GEMM with glu: per-token max |h| (float bits, atomic max), or null
     const float* res;     // deep decode GEMV: residual (N, M) added after the epilogue (may alias y), or null
 };
@@ -192,6 +192,11 @@ struct EpiArgs
 bool epilogue_quant_ok(size_t N, size_t M);
 hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* gamma, bool norm, float eps, size_t N,
                                  size_t M, int8_t* xi, float* s, int32_t* rowsum);
+// The one-token [RMSNorm (gamma) ->] absmax -> int8 pass on a token-major X (M, K), decode sizes
+// (token_quant_tm_ok: M <= 64, K <= 11264); same bits as launch_act_quant on X transposed.
+bool token_quant_tm_ok(size_t K, size_t M);
+hipError_t launch_token_quant_tm(hipStream_t st, const float* X, const float* gamma, float eps, size_t K, size_t M,
+                                 int8_t* xi, float* s, int32_t* rowsum);
 hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, bool norm, float eps,
                             size_t K, size_t M, int8_t* xi, float* s, int32_t* rowsum,
                             uint32_t* xq_ref);

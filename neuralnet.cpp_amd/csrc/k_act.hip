@@ -595,7 +595,7 @@ __global__ __launch_bounds__(kOneThreads) void k_token_one(TokArgs a, const floa
     for (int r = 0; r < R; ++r)
     {
         const int f = t + kParts * r;
-        x[r] = f < a.K ? a.X[(size_t)f * a.M + m] : 0.0f;
+        x[r] = f < a.K ? a.X[a.xtm ? (size_t)m * a.K + f : (size_t)f * a.M + m] : 0.0f;
     }
     one_token_finish<R>(x, a, gamma, sh);
 }
@@ -898,6 +898,23 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
     const unsigned grid = (unsigned)ceil_div(M, kWave);
     hipLaunchKernelGGL(k_token_lanes, dim3(grid), dim3(kTW * kWave), 0, st, X, gamma, norm, eps,
                        inv_f, K, M, Kp, mode, xi, s, rowsum, xq_ref, fout);
+    return hipGetLastError();
+}
+
+bool token_quant_tm_ok(size_t K, size_t M)
+{
+    return M >= 1 && M <= kOneTokMaxM && K >= 1 && ceil_div(K, (size_t)512) <= 22;
+}
+
+hipError_t launch_token_quant_tm(hipStream_t st, const float* X, const float* gamma, float eps, size_t K, size_t M,
+                                 int8_t* xi, float* s, int32_t* rowsum)
+{
+    if (!token_quant_tm_ok(K, M)) return hipErrorInvalidValue;
+    const int rounds = (int)ceil_div(K, (size_t)512);
+    TokArgs a{X, gamma != nullptr, eps, 1.0f / (float)K, (int)K, (int)M, (int)round_up(K, kTileK), 0, xi, s, rowsum,
+              nullptr, nullptr, 1};
+    if (!launch_one_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, gamma))
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -400,8 +400,8 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvDeepArgs da)
             const int f = rt * 8 + 4 * g + i;
             const bool st = live && g < 2 && f < p.glu_F && t < p.M;
             const float hv = glu_one(y[i], up, p.glu - 1);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hv), rh,
-                                                  st ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u, 0, 0);
+            const uint32_t ho = p.ytm ? (uint32_t)t * (uint32_t)p.glu_F + (uint32_t)f : (uint32_t)f * (uint32_t)p.M + (uint32_t)t;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hv), rh, st ? ho * 4u : 0xFFFFFFF0u, 0, 0);
         }
     }
     (void)n_tiles;

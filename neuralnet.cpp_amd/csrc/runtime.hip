@@ -1378,6 +1378,54 @@ nnhip_status nnhip_ternary_matmul_glu(nnhip_ctx* ctx, const void* rp, const floa
     return run_matmul_glu(ctx, fn, rp, tau, xi, s, rowsum, bias, F, K, M, act, y1, h);
 }
 
+nnhip_status nnhip_ternary_matmul_glu_tokens(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                             const float* s, const int32_t* rowsum, const float* bias, size_t F,
+                                             size_t K, size_t M, int act, float* h)
+{
+    const char* fn = "nnhip_ternary_matmul_glu_tokens";
+    NNHIP_CHECK_CTX(fn);
+    if (F == 0 || M == 0) return NNHIP_OK;
+    const nnhip_status st = check_glu_args(fn, F, K, M, act);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && tau && xi && s && rowsum && h, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
+    GemvProblem p{};
+    p.rp = static_cast<const u32x4*>(rp);
+    p.tau = tau;
+    p.xi = xi;
+    p.s = s;
+    p.rowsum = rowsum;
+    p.bias = bias;
+    p.y = h;
+    p.N = (int32_t)nnhip_glu_rows(F);
+    p.K = (int32_t)K;
+    p.M = (int32_t)M;
+    p.KT = (int32_t)ceil_div(K, kTileK);
+    p.xlds = -1;
+    p.glu = act + 1;
+    p.glu_F = (int32_t)F;
+    p.ytm = 1;
+    if (M > (size_t)kGemvMaxM || !gemv_deep_ok(p, ctx->num_cus))
+        return fail(NNHIP_ERR_UNSUPPORTED, fn,
+                    "decode sizes only (M <= 16, K of 1024 / 2560 / 4096 / 6912 rounded to 256, at most 4 row tiles per CU)");
+    NNHIP_LAUNCH(fn, launch_gemv_deep(ctx->stream, p));
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t K,
+                                           size_t M, int8_t* xi, float* s, int32_t* rowsum)
+{
+    const char* fn = "nnhip_rmsnorm_quant_i8_tokens";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(X && xi && s && rowsum, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
+    if (!token_quant_tm_ok(K, M))
+        return fail(NNHIP_ERR_UNSUPPORTED, fn, "decode sizes only (1 <= M <= 64, 1 <= K <= 11264)");
+    NNHIP_LAUNCH(fn, launch_token_quant_tm(ctx->stream, X, gamma, eps, K, M, xi, s, rowsum));
+    return NNHIP_OK;
+}
+
 size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M)
 {
     size_t b = round_up(nnhip_act_i8_bytes(d, M), 256) + round_up(nnhip_act_i8_bytes(F, M), 256);

@@ -167,6 +167,7 @@ struct TokArgs
     int32_t* rowsum;
     uint32_t* xq_ref;
     float* fout;
+    int xtm;  // one-token kernel: X is token-major (M, K) instead of (K, M)
 };
 
 // LDS of the one-token kernels

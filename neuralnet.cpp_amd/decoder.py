@@ -234,6 +234,31 @@ class Decoder:
             self._h_buf = torch.empty((self.cfg.F, self.B), dtype=torch.float32, device=dev)
         return self._part_buf, self._h_buf
 
+    # h token-major between fc1 and the FFN SubLN quantizer: None until the first step tries it
+    _glu_tokens: Optional[bool] = None
+
+    def _ffn_gate_quant(self, blk: Block, h):
+        """fc1 + gated activation into h, then the FFN SubLN -> int8 into self.xi / s / rs. Where the
+        decode GEMV takes fc1 (the library reports the shape as unsupported otherwise) h is written
+        token-major, so the quantizer reads each token as one contiguous row; the bits are the
+        same either way."""
+        cfg, ctx, B, f1 = self.cfg, self.ctx, self.B, blk.fc1
+        if self._glu_tokens is not False:
+            try:
+                ctx.ternary_matmul_glu_tokens(f1.rp, f1.tau, self.xi, self.s, self.rs, cfg.F, cfg.d, B, act=cfg.act,
+                                              bias=f1.bias, out=h.view(B, cfg.F))
+                self._glu_tokens = True
+            except _pkg().NNHipError as e:
+                if e.status != 5:   # NNHIP_ERR_UNSUPPORTED
+                    raise
+                self._glu_tokens = False
+        if self._glu_tokens:
+            ctx.rmsnorm_quant_i8_tokens(h.view(B, cfg.F), blk.g_ffn_sub, cfg.eps, outs=(self.xi, self.s, self.rs))
+        else:
+            ctx.ternary_matmul_glu(f1.rp, f1.tau, self.xi, self.s, self.rs, cfg.F, cfg.d, B, act=cfg.act,
+                                   bias=f1.bias, out=h)
+            self._quant(h, blk.g_ffn_sub)
+
     def block_step_fused(self, i: int, pos, len_bound: int, attn_hook=None):
         """Block i with self.xi / s / rs holding int8(RMSNorm1(x)) on entry; on exit self.x holds the
         block output and self.xi / s / rs its quantization for the next block (gamma = next block's
@@ -256,9 +281,7 @@ class Decoder:
                                out=self.r)
         self._quant(self.r, blk.g2)
         part, h = self._scratch()
-        ctx.ternary_matmul_glu(blk.fc1.rp, blk.fc1.tau, self.xi, self.s, self.rs, cfg.F, d, B, act=cfg.act,
-                               bias=blk.fc1.bias, out=h)
-        self._quant(h, blk.g_ffn_sub)
+        self._ffn_gate_quant(blk, h)
         f2 = blk.fc2
         S = self._slices(f2.K, self.slices_fc2)
         pf = ctx.ternary_matmul_partial(f2.rp, self.xi, f2.N, f2.K, B, S, out=part[:S])

@@ -120,3 +120,57 @@ def test_partial_rejects(ctx, nnhip):
     with pytest.raises(nnhip.NNHipError):                       # M > 64
         ctx.partial_residual_quant_i8(part, f, torch.zeros(65, device="cuda"), i, 8, 65, x)
 
+
+
+# ---------------------------------------------------------------- token-major FFN intermediate
+
+@pytest.mark.parametrize("M,act,bias", [(16, 0, True), (1, 1, False), (7, 0, False)])
+def test_glu_tokens_equals_glu(ctx, orc, M, act, bias):
+    """nnhip_ternary_matmul_glu_tokens: h token-major (M, F), the transpose of
+    nnhip_ternary_matmul_glu's (F, M) bit for bit (C5's fc1: d=2560, F=6912)."""
+    say(f"glu tokens M={M} act={act} bias={bias}")
+    K, F = 2560, 6912
+    W = normal((2 * F, K), 61 + M, 0.0, 0.02)
+    tau = np.abs(W.astype(np.float64)).mean(axis=1).astype(np.float32)
+    wq = orc.trit_pack(W, tau)
+    b = dev(normal((2 * F,), 62)) if bias else None
+    wqi, taui, bi = ctx.glu_interleave(dev(wq), dev(tau), b, F, K)
+    rp = ctx.repack(wqi, K)
+    xi, s_d, rs = ctx.act_quant_i8(dev(normal((K, M), 63 + M)))
+    h = host(ctx.ternary_matmul_glu(rp, taui, xi, s_d, rs, F, K, M, act=act, bias=bi))
+    ht = host(ctx.ternary_matmul_glu_tokens(rp, taui, xi, s_d, rs, F, K, M, act=act, bias=bi))
+    assert ht.shape == (M, F)
+    assert np.array_equal(np.ascontiguousarray(ht.T).view(np.uint32), h.view(np.uint32))
+
+
+@pytest.mark.parametrize("K,M,norm", [(6912, 16, True), (6912, 16, False), (2560, 1, True), (1000, 64, True),
+                                      (11264, 5, False), (300, 3, True)])
+def test_quant_tokens_equals_quant(ctx, orc, K, M, norm):
+    """nnhip_rmsnorm_quant_i8_tokens on X (M, K) token-major: the codes, scales and row sums of
+    nnhip_rmsnorm_quant_i8 / nnhip_act_quant_i8 on X transposed, bit for bit."""
+    say(f"quant tokens K={K} M={M} norm={norm}")
+    X = normal((K, M), 71 + K + M) * np.float32(4.0)
+    X[3, 0] = np.float32(1e-3)
+    gamma = dev(1.0 + 0.2 * normal((K,), 72)) if norm else None
+    ref = ctx.rmsnorm_quant_i8(dev(X), gamma, 1e-5) if norm else ctx.act_quant_i8(dev(X))
+    got = ctx.rmsnorm_quant_i8_tokens(dev(np.ascontiguousarray(X.T)), gamma, 1e-5)
+    assert np.array_equal(host(got[0]), host(ref[0]))
+    assert np.array_equal(host(got[1]).view(np.uint32), host(ref[1]).view(np.uint32))
+    assert np.array_equal(host(got[2]), host(ref[2]))
+
+
+def test_token_major_rejects(ctx, nnhip):
+    import torch
+    with pytest.raises(nnhip.NNHipError) as e:     # M = 65: past the one-token kernel
+        ctx.rmsnorm_quant_i8_tokens(torch.zeros((65, 256), device="cuda"), None, 1e-5)
+    assert e.value.status == 5
+    with pytest.raises(nnhip.NNHipError) as e:     # K = 12000: more than 22 rounds of 512
+        ctx.rmsnorm_quant_i8_tokens(torch.zeros((4, 12000), device="cuda"), None, 1e-5)
+    assert e.value.status == 5
+    xi = torch.zeros((16, 256), dtype=torch.int8, device="cuda")
+    f = torch.ones(16, device="cuda")
+    i = torch.zeros(16, dtype=torch.int32, device="cuda")
+    rp = torch.zeros(64 * 64, dtype=torch.int32, device="cuda")
+    with pytest.raises(nnhip.NNHipError) as e:     # K = 256: not a decode GEMV width
+        ctx.ternary_matmul_glu_tokens(rp, torch.ones(32, device="cuda"), xi, f, i, 16, 256, 16)
+    assert e.value.status == 5
