@@ -335,22 +335,23 @@ __global__ __launch_bounds__(kTW * kWave) void k_token_lanes(
 }
 
 // ---------------------------------------------------------------------------------------
-// Large M: TPB tokens per block (4 or 8), 512 threads, X read from HBM exactly once.
+// Large M: TPB tokens per block (4 or 8) and 2*TPB waves, X read from HBM exactly once.
 // A thread holds 4 tokens of one row per round (16 B, a float4 when M % 4 == 0); LPR = TPB/4
-// lanes share a row, so a wave covers RPW = 64/LPR rows and a round RR = 8*RPW rows. Thread
-// (wave w, lane RPW*h + fl) loads rows f = RR*r + RPW*w + fl (r < R), tokens 4h..4h+3, keeps
-// them in registers, and owns sum-of-squares part f % 512 of its four tokens (one part when
-// RR = 512, two alternating parts when RR = 256). The butterfly levels down to offset RPW go
-// through LDS, the rest are lane shuffles.
-constexpr int kRegWaves = 8;  // 512 threads
+// lanes share a row (a 16- or 32-byte segment), so a wave covers RPW = 64/LPR rows and a round
+// RR = reg_waves*RPW = 512 rows. Thread (wave w, lane RPW*h + fl) loads rows f = RR*r + RPW*w + fl
+// (r < R), tokens 4h..4h+3, keeps them in registers, and owns sum-of-squares part f % 512 of its
+// four tokens. The butterfly levels down to offset RPW go through LDS, the rest are lane
+// shuffles.
+template <int TPB>
+constexpr int reg_waves = 2 * TPB;
 
 // Everything a block needs to load and finish token groups (uniform across the block).
 template <int TPB>
 struct TokShared
 {
     float red[kParts][TPB];  // sum-of-squares parts
-    float wred[kRegWaves][TPB];
-    int wsum[kRegWaves][TPB];
+    float wred[reg_waves<TPB>][TPB];
+    int wsum[reg_waves<TPB>][TPB];
     float tok_ri[TPB];
 };
 
@@ -359,7 +360,7 @@ struct TokShared
 template <int R, bool kVec, int TPB>
 __device__ __forceinline__ void load_group(float (&x)[R][4], const TokArgs& a, int g, int ro, int h)
 {
-    constexpr int RR = kRegWaves * kWave / (TPB / 4);
+    constexpr int RR = reg_waves<TPB> * kWave / (TPB / 4);
     const int mt = g * TPB + 4 * h;
     if (kVec)
     {
@@ -399,7 +400,8 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
 {
     constexpr int LPR = TPB / 4;          // lanes per row
     constexpr int RPW = kWave / LPR;      // rows per wave per round
-    constexpr int RR = kRegWaves * RPW;   // rows per round
+    constexpr int RW = reg_waves<TPB>;    // waves per block
+    constexpr int RR = RW * RPW;          // rows per round
     constexpr int NP = kParts / RR;       // parts per thread (1 or 2)
     const int mt = g * TPB + 4 * h;       // first of this thread's four tokens
 
@@ -485,7 +487,7 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
     {
         float t = sh.wred[0][4 * h + i];
 #pragma unroll
-        for (int v = 1; v < kRegWaves; ++v) t = fmaxf(t, sh.wred[v][4 * h + i]);
+        for (int v = 1; v < RW; ++v) t = fmaxf(t, sh.wred[v][4 * h + i]);
         sc[i] = __fmul_rn(t, 1.0f / 127.0f);
         rc[i] = quant_rcp(sc[i]);
     }
@@ -538,7 +540,7 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
         {
             int t = 0;
 #pragma unroll
-            for (int v = 0; v < kRegWaves; ++v) t += sh.wsum[v][4 * h + i];
+            for (int v = 0; v < RW; ++v) t += sh.wsum[v][4 * h + i];
             if (mt + i < a.M)
             {
                 a.s[mt + i] = sc[i];
@@ -552,11 +554,11 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
 // multiple of 8, so the blocks of one XCD take consecutive groups and the groups sharing a
 // 128-byte row segment of X meet in one L2.
 template <int R, bool kVec, int TPB>
-__global__ __launch_bounds__(kRegWaves * kWave) void k_token_regs(TokArgs a, const float* __restrict__ gamma,
+__global__ __launch_bounds__(reg_waves<TPB> * kWave) void k_token_regs(TokArgs a, const float* __restrict__ gamma,
                                                                   int n_groups)
 {
     constexpr int RPW = kWave / (TPB / 4);
-    constexpr int RR = kRegWaves * RPW;
+    constexpr int RR = reg_waves<TPB> * RPW;
     static_assert(TPB == 4 || TPB == 8, "tokens per block");
     __shared__ TokShared<TPB> sh;
 
@@ -835,6 +837,9 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_amax(const float* __res
     }
 }
 
+#ifndef NNHIP_TOK8_MAX_ROUNDS
+#define NNHIP_TOK8_MAX_ROUNDS 10  // largest K/512 rounds for the 8-token register kernel
+#endif
 constexpr size_t kSmallM = 32;
 constexpr size_t kOneTokMaxM = NNHIP_ONE_TOK_MAX_M;
 
@@ -842,7 +847,7 @@ template <int TPB, int R>
 void launch_regs_r(bool vec, hipStream_t st, int n_groups, const TokArgs& a, const float* gamma)
 {
     auto kern = vec ? k_token_regs<R, true, TPB> : k_token_regs<R, false, TPB>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)n_groups), dim3(kRegWaves * kWave), 0, st, a, gamma, n_groups);
+    hipLaunchKernelGGL(kern, dim3((unsigned)n_groups), dim3(reg_waves<TPB> * kWave), 0, st, a, gamma, n_groups);
 }
 
 // Launch the instantiation with the smallest R >= rounds from the ascending list Rs; false if
@@ -880,12 +885,17 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
         // rows are read as float4 when every row start is 16-byte aligned
         const bool vec = M % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
                          (fout == nullptr || reinterpret_cast<uintptr_t>(fout) % 16 == 0);
-        // 4 tokens per block: an 8-token layout (32-byte row segments) loads faster in isolation
-        // but measured no faster end to end, and halves the block count
-        const int n_groups = (int)ceil_div(M, (size_t)4);
+        // 8 tokens per block (32-byte row segments, 16 waves) while a thread's rows fit the
+        // 128 registers of a 1024-thread block and the grid is at most a few rounds (K=4096,
+        // M=2048: 14.2 against 15.7 us; 2560 x 32768, where the smaller blocks keep more waves
+        // resident: 193 against 159 us); 4 tokens (16-byte segments, 8 waves) otherwise
         TokArgs a{X, norm, eps, inv_f, (int)K, (int)M, (int)Kp, mode, xi, s, rowsum, xq_ref, fout};
-        const bool launched = launch_regs_pick<4, 1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(
-            rounds, vec, st, n_groups, a, gamma);
+        const bool tok8 = vec && rounds <= NNHIP_TOK8_MAX_ROUNDS && M <= 8192;
+        const int n_groups = (int)ceil_div(M, (size_t)(tok8 ? 8 : 4));
+        const bool launched =
+            tok8 ? launch_regs_pick<8, 1, 2, 3, 4, 5, 6, 8, 10>(rounds, vec, st, n_groups, a, gamma)
+                 : launch_regs_pick<4, 1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, vec, st, n_groups,
+                                                                                     a, gamma);
         if (launched) return hipGetLastError();
     }
     if (M <= kSmallM)

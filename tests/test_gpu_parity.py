@@ -228,11 +228,13 @@ def check_quant(ctx, orc, X, g=None, eps=1e-6):
     assert np.array_equal(host(rs), q.astype(np.int64).sum(axis=1))
 
 
-# M > 64 runs the register-resident kernel (rounds of 512 rows, 4 tokens per block; M % 4 != 0
-# takes the scalar-load path), M <= 64 the one-token kernel; K = 11264 is the largest
-# instantiation of both, K = 11265 the fallback.
+# M > 64 runs the register-resident kernel (rounds of 512 rows; 8 tokens per 16-wave block when
+# M % 4 == 0, M <= 8192 and K <= 5120, 4 tokens per 8-wave block otherwise; M % 4 != 0 takes the
+# scalar-load path), M <= 64 the one-token kernel; K = 11264 is the largest instantiation of
+# both, K = 11265 the fallback. M = 2052 and 1028 leave a half-empty last group of 8 tokens.
 @pytest.mark.parametrize("K,M", [(1, 36), (255, 37), (512, 40), (513, 128), (1000, 66), (2560, 2048),
-                                 (4096, 2048), (6912, 132), (11264, 40), (11265, 36)])
+                                 (4096, 2048), (2560, 2052), (5120, 1028), (5121, 1024), (512, 8196),
+                                 (6912, 132), (11264, 40), (11265, 36)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_token_kernel_shapes(ctx, orc, K, M, norm):
     say(f"token kernel K={K} M={M} norm={norm}")
