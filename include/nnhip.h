@@ -102,6 +102,16 @@ nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream);
 #define NNHIP_GEMM_TILE_64x64 3
 nnhip_status nnhip_ctx_set_gemm_tile(nnhip_ctx* ctx, int tile);
 
+/* A performance hint with no counterpart in the reference: the next call on this context of
+ * nnhip_act_quant_i8 / nnhip_rmsnorm_quant_i8 (at most 64 tokens), nnhip_rmsnorm_quant_i8_tokens
+ * or nnhip_partial_residual_quant_i8 also reads the given device ranges (count <= 4, each
+ * 16-byte aligned; whole 16-byte units inside each range, at most 64 MiB in all) in extra
+ * blocks, so that the kernel after it, which reads the same bytes (a decoder's next BitLinear
+ * weights), finds them in the GPU's memory-side cache. That call takes the ranges whether or
+ * not it can use them (M > 64 cannot); results never depend on them. The ranges must stay
+ * allocated until that call has run on the device. count = 0 clears them. */
+nnhip_status nnhip_ctx_prefetch_next(nnhip_ctx* ctx, size_t count, const void* const* ptrs, const size_t* bytes);
+
 /* Block the host until all work queued on the context's stream has finished.
  * Replaces ComputeEngine::end_batch()/flush_batch() waits (compute_layer_gpt.hpp:715-719). */
 nnhip_status nnhip_sync(nnhip_ctx* ctx);

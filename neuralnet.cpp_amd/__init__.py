@@ -65,6 +65,7 @@ SIGNATURES = {
     "nnhip_ctx_get_stream": (_st, [_vp, ctypes.POINTER(_vp)]),
     "nnhip_sync": (_st, [_vp]),
     "nnhip_ctx_set_gemm_tile": (_st, [_vp, _st]),
+    "nnhip_ctx_prefetch_next": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_sz)]),
     "nnhip_malloc": (_st, [_vp, _sz, ctypes.POINTER(_vp)]),
     "nnhip_free": (_st, [_vp, _vp]),
     "nnhip_memcpy_h2d": (_st, [_vp, _vp, _vp, _sz]),
@@ -269,6 +270,18 @@ class Context:
     def set_gemm_tile(self, tile: int) -> None:
         """Force the prefill GEMM block tile (GEMM_TILE_*); GEMM_TILE_AUTO picks per call."""
         _check(lib().nnhip_ctx_set_gemm_tile(self.h, tile), "nnhip_ctx_set_gemm_tile")
+
+    def prefetch_next(self, tensors) -> None:
+        """Device tensors (up to 4) that the next per-token quantizer call (act_quant_i8 /
+        rmsnorm_quant_i8 at M <= 64, rmsnorm_quant_i8_tokens, partial_residual_quant_i8) also
+        reads, so that the kernel after it finds them in the memory-side cache. Results are
+        unaffected; an empty list clears them."""
+        ts = [t for t in tensors if t is not None]
+        if len(ts) > 4:
+            raise NNHipError(1, "at most 4 ranges")
+        ptrs = (_vp * max(1, len(ts)))(*[self._dev(t, None, "range") for t in ts])
+        nb = (_sz * max(1, len(ts)))(*[t.numel() * t.element_size() for t in ts])
+        _check(lib().nnhip_ctx_prefetch_next(self.h, len(ts), ptrs, nb), "nnhip_ctx_prefetch_next")
 
     # -- reference-layout primitives
     def row_absmean(self, W):

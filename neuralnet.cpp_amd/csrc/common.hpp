@@ -174,6 +174,22 @@ hipError_t launch_matmul_q_t(hipStream_t st, const uint32_t* A, const float* tau
                              size_t M, size_t N, void* Y, bool y16, const MatqPlan& plan, float* scratch);
 
 // ---- activation kernels (k_act.hip)
+// Extra blocks of the one-token kernels (k_token_one, k_token_epi) that read up to kPfRanges
+// device ranges in whole 16-byte units with the default cache policy while the kernel's tokens
+// are processed, so that the next kernel, which reads the same bytes, finds them in the
+// memory-side cache (256 MB) instead of HBM. Outputs do not depend on it.
+constexpr int kPfRanges = 4;
+constexpr int kOneThreadsHost = 512;                  // threads of a one-token block
+// loads per prefetch thread: 4 and 2 measured alike in the decode step, 1 (more blocks to
+// dispatch) and 16 (prefetch blocks outlasting the quantizer) slower
+constexpr int kPfUnitsPerThread = 4;
+constexpr uint64_t kPfMaxUnits = (64ull << 20) / 16;  // at most 64 MiB per kernel
+struct Prefetch
+{
+    const void* p[kPfRanges];
+    uint32_t n16[kPfRanges];  // 16-byte units per range
+    int blocks;               // extra blocks of 512 threads (0: none)
+};
 hipError_t launch_rmsnorm(hipStream_t st, const float* X, const float* gamma, float eps, size_t F,
                           size_t M, float* out);
 // Epilogue of a split-k GEMV (part[S][M][N] slice sums) + residual, then [RMSNorm ->] absmax
@@ -191,15 +207,15 @@ struct EpiArgs
 };
 bool epilogue_quant_ok(size_t N, size_t M);
 hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* gamma, bool norm, float eps, size_t N,
-                                 size_t M, int8_t* xi, float* s, int32_t* rowsum);
+                                 size_t M, int8_t* xi, float* s, int32_t* rowsum, const Prefetch* pf = nullptr);
 // The one-token [RMSNorm (gamma) ->] absmax -> int8 pass on a token-major X (M, K), decode sizes
 // (token_quant_tm_ok: M <= 64, K <= 11264); same bits as launch_act_quant on X transposed.
 bool token_quant_tm_ok(size_t K, size_t M);
 hipError_t launch_token_quant_tm(hipStream_t st, const float* X, const float* gamma, float eps, size_t K, size_t M,
-                                 int8_t* xi, float* s, int32_t* rowsum);
+                                 int8_t* xi, float* s, int32_t* rowsum, const Prefetch* pf = nullptr);
 hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, bool norm, float eps,
                             size_t K, size_t M, int8_t* xi, float* s, int32_t* rowsum,
-                            uint32_t* xq_ref);
+                            uint32_t* xq_ref, const Prefetch* pf = nullptr);
 hipError_t launch_act_from_container(hipStream_t st, const uint32_t* xq, size_t K, size_t M,
                                      int8_t* xi, int32_t* rowsum);
 hipError_t launch_act_to_container(hipStream_t st, const int8_t* xi, size_t K, size_t M,

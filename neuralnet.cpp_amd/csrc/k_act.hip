@@ -591,6 +591,11 @@ template <int R>
 __global__ __launch_bounds__(kOneThreads) void k_token_one(TokArgs a, const float* __restrict__ gamma)
 {
     __shared__ OneShared sh;
+    if ((int)blockIdx.x >= a.M)
+    {
+        prefetch_block(a.pf, (int)blockIdx.x - a.M);
+        return;
+    }
     const int t = threadIdx.x, m = blockIdx.x;
     float x[R];
 #pragma unroll
@@ -610,6 +615,11 @@ template <int R, int kEpiMaxSlices>
 __global__ __launch_bounds__(kOneThreads) void k_token_epi(TokArgs a, EpiArgs e, const float* __restrict__ gamma)
 {
     __shared__ OneShared sh;
+    if ((int)blockIdx.x >= a.M)
+    {
+        prefetch_block(a.pf, (int)blockIdx.x - a.M);
+        return;
+    }
     const int t = threadIdx.x, m = blockIdx.x, N = a.K, M = a.M;
     const float sv = e.s_in[m];
     const int rs2 = 2 * e.rowsum_in[m];
@@ -658,9 +668,11 @@ template <int R>
 void launch_epi_r(hipStream_t st, const TokArgs& a, const EpiArgs& e, const float* gamma)
 {
     if (e.S <= 4)
-        hipLaunchKernelGGL((k_token_epi<R, 4>), dim3((unsigned)a.M), dim3(kOneThreads), 0, st, a, e, gamma);
+        hipLaunchKernelGGL((k_token_epi<R, 4>), dim3((unsigned)(a.M + a.pf.blocks)), dim3(kOneThreads), 0, st, a, e,
+                           gamma);
     else
-        hipLaunchKernelGGL((k_token_epi<R, 8>), dim3((unsigned)a.M), dim3(kOneThreads), 0, st, a, e, gamma);
+        hipLaunchKernelGGL((k_token_epi<R, 8>), dim3((unsigned)(a.M + a.pf.blocks)), dim3(kOneThreads), 0, st, a, e,
+                           gamma);
 }
 
 template <int... Rs>
@@ -674,7 +686,7 @@ bool launch_epi_pick(int rounds, hipStream_t st, const TokArgs& a, const EpiArgs
 template <int R>
 void launch_one_r(hipStream_t st, const TokArgs& a, const float* gamma)
 {
-    hipLaunchKernelGGL(k_token_one<R>, dim3((unsigned)a.M), dim3(kOneThreads), 0, st, a, gamma);
+    hipLaunchKernelGGL(k_token_one<R>, dim3((unsigned)(a.M + a.pf.blocks)), dim3(kOneThreads), 0, st, a, gamma);
 }
 
 template <int... Rs>
@@ -864,7 +876,7 @@ bool launch_regs_pick(int rounds, bool vec, hipStream_t st, int n_groups, const 
 
 static hipError_t launch_token_kernel(hipStream_t st, const float* X, const float* gamma, bool norm,
                                       float eps, size_t K, size_t M, int mode, int8_t* xi, float* s,
-                                      int32_t* rowsum, uint32_t* xq_ref, float* fout)
+                                      int32_t* rowsum, uint32_t* xq_ref, float* fout, const Prefetch* pf = nullptr)
 {
     if (M == 0) return hipSuccess;
     const float inv_f = 1.0f / (float)K;
@@ -877,6 +889,7 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
     if (M <= kOneTokMaxM && rounds <= 22)
     {
         TokArgs a{X, norm, eps, inv_f, (int)K, (int)M, (int)Kp, mode, xi, s, rowsum, xq_ref, fout};
+        if (pf) a.pf = *pf;
         if (launch_one_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, gamma))
             return hipGetLastError();
     }
@@ -917,12 +930,13 @@ bool token_quant_tm_ok(size_t K, size_t M)
 }
 
 hipError_t launch_token_quant_tm(hipStream_t st, const float* X, const float* gamma, float eps, size_t K, size_t M,
-                                 int8_t* xi, float* s, int32_t* rowsum)
+                                 int8_t* xi, float* s, int32_t* rowsum, const Prefetch* pf)
 {
     if (!token_quant_tm_ok(K, M)) return hipErrorInvalidValue;
     const int rounds = (int)ceil_div(K, (size_t)512);
     TokArgs a{X, gamma != nullptr, eps, 1.0f / (float)K, (int)K, (int)M, (int)round_up(K, kTileK), 0, xi, s, rowsum,
               nullptr, nullptr, 1};
+    if (pf) a.pf = *pf;
     if (!launch_one_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, gamma))
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -937,7 +951,7 @@ hipError_t launch_rmsnorm(hipStream_t st, const float* X, const float* gamma, fl
 
 hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, bool norm, float eps,
                             size_t K, size_t M, int8_t* xi, float* s, int32_t* rowsum,
-                            uint32_t* xq_ref)
+                            uint32_t* xq_ref, const Prefetch* pf)
 {
     if (xq_ref && M % 4 != 0)
     {
@@ -945,7 +959,7 @@ hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, 
         const hipError_t e = launch_fill_u32(st, xq_ref, 0u, K * ceil_div(M, 4));
         if (e != hipSuccess) return e;
     }
-    return launch_token_kernel(st, X, gamma, norm, eps, K, M, 0, xi, s, rowsum, xq_ref, nullptr);
+    return launch_token_kernel(st, X, gamma, norm, eps, K, M, 0, xi, s, rowsum, xq_ref, nullptr, pf);
 }
 
 bool epilogue_quant_ok(size_t N, size_t M)
@@ -954,12 +968,13 @@ bool epilogue_quant_ok(size_t N, size_t M)
 }
 
 hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* gamma, bool norm, float eps, size_t N,
-                                 size_t M, int8_t* xi, float* s, int32_t* rowsum)
+                                 size_t M, int8_t* xi, float* s, int32_t* rowsum, const Prefetch* pf)
 {
     if (M == 0) return hipSuccess;
     if (!epilogue_quant_ok(N, M)) return hipErrorInvalidValue;
-    const TokArgs a{nullptr, norm, eps, 1.0f / (float)N, (int)N, (int)M, (int)round_up(N, kTileK), 0, xi, s, rowsum,
-                    nullptr, nullptr};
+    TokArgs a{nullptr, norm, eps, 1.0f / (float)N, (int)N, (int)M, (int)round_up(N, kTileK), 0, xi, s, rowsum,
+              nullptr, nullptr};
+    if (pf) a.pf = *pf;
     const int rounds = (int)ceil_div(N, (size_t)kParts);
     if (!launch_epi_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, e, gamma))
         return hipErrorInvalidValue;

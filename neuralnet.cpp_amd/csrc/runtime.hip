@@ -42,7 +42,21 @@ struct nnhip_ctx
     float* ones = nullptr;  // 1.0f, the unit scales of the digit products
     size_t ones_words = 0;
     size_t ones_bytes_ = 0;
+    // ranges that the next per-token quantizer call reads in extra blocks (nnhip_ctx_prefetch_next)
+    Prefetch pf{};
 };
+
+namespace
+{
+// The pending prefetch ranges, cleared: every quantizer entry point takes them, whether or not
+// its launch can carry them (only the one-token kernels, M <= 64, do).
+Prefetch take_prefetch(nnhip_ctx* ctx)
+{
+    const Prefetch p = ctx->pf;
+    ctx->pf = Prefetch{};
+    return p;
+}
+}  // namespace
 
 struct nnhip_group
 {
@@ -353,6 +367,32 @@ nnhip_status nnhip_ctx_set_gemm_tile(nnhip_ctx* ctx, int tile)
     NNHIP_REQUIRE(tile >= NNHIP_GEMM_TILE_AUTO && tile <= NNHIP_GEMM_TILE_64x64, "nnhip_ctx_set_gemm_tile",
                   "tile must be one of NNHIP_GEMM_TILE_*");
     ctx->gemm_tile = tile;
+    return NNHIP_OK;
+}
+
+nnhip_status nnhip_ctx_prefetch_next(nnhip_ctx* ctx, size_t count, const void* const* ptrs, const size_t* bytes)
+{
+    const char* fn = "nnhip_ctx_prefetch_next";
+    NNHIP_CHECK_CTX(fn);
+    NNHIP_REQUIRE(count <= (size_t)kPfRanges, fn, "count must be at most 4");
+    NNHIP_REQUIRE(count == 0 || (ptrs && bytes), fn, "null pointer");
+    Prefetch p{};
+    uint64_t total = 0;
+    int k = 0;
+    for (size_t i = 0; i < count; ++i)
+    {
+        if (!ptrs[i] || bytes[i] < 16) continue;
+        NNHIP_REQUIRE(aligned16(ptrs[i]), fn, "ranges must be 16-byte aligned");
+        // whole 16-byte units inside the range, at most kPfMaxUnits over all ranges
+        const uint64_t n = std::min<uint64_t>(bytes[i] / 16, kPfMaxUnits - total);
+        if (n == 0) continue;
+        p.p[k] = ptrs[i];
+        p.n16[k] = (uint32_t)n;
+        total += n;
+        ++k;
+    }
+    p.blocks = (int)ceil_div((size_t)total, (size_t)kOneThreadsHost * kPfUnitsPerThread);
+    ctx->pf = p;
     return NNHIP_OK;
 }
 
@@ -754,12 +794,13 @@ static nnhip_status act_quant_common(nnhip_ctx* ctx, const char* fn, const float
                                      int32_t* rowsum, uint32_t* xq_ref)
 {
     NNHIP_CHECK_CTX(fn);
+    const Prefetch pf = take_prefetch(ctx);
     if (M == 0) return NNHIP_OK;
     NNHIP_REQUIRE(K >= 1 && K <= kMaxK && M <= kMaxDim, fn, "K must be in [1, 262144], M below 2^31");
     NNHIP_REQUIRE(X && xi && s && rowsum && (gamma || !norm), fn, "null pointer");
     NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
     NNHIP_REQUIRE(mul_ok(round_up(K, kTileK), M), fn, "size overflow");
-    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, norm, eps, K, M, xi, s, rowsum, xq_ref));
+    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, norm, eps, K, M, xi, s, rowsum, xq_ref, &pf));
     return NNHIP_OK;
 }
 
@@ -936,6 +977,7 @@ nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part
 {
     const char* fn = "nnhip_partial_residual_quant_i8";
     NNHIP_CHECK_CTX(fn);
+    const Prefetch pf = take_prefetch(ctx);
     if (N == 0 || M == 0) return NNHIP_OK;
     NNHIP_REQUIRE(part && tau && s_in && rowsum_in && x_out && xi && s && rowsum, fn, "null pointer");
     NNHIP_REQUIRE(slices >= 1 && slices <= 8, fn, "slices must be in [1, 8]");
@@ -943,7 +985,7 @@ nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part
     NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
     NNHIP_REQUIRE(!gamma || eps >= 0.0f, fn, "eps must be >= 0");
     const EpiArgs e{part, (int)slices, tau, s_in, rowsum_in, bias, res, x_out};
-    NNHIP_LAUNCH(fn, launch_epilogue_quant(ctx->stream, e, gamma, gamma != nullptr, eps, N, M, xi, s, rowsum));
+    NNHIP_LAUNCH(fn, launch_epilogue_quant(ctx->stream, e, gamma, gamma != nullptr, eps, N, M, xi, s, rowsum, &pf));
     return NNHIP_OK;
 }
 
@@ -1417,12 +1459,13 @@ nnhip_status nnhip_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* X, const
 {
     const char* fn = "nnhip_rmsnorm_quant_i8_tokens";
     NNHIP_CHECK_CTX(fn);
+    const Prefetch pf = take_prefetch(ctx);
     if (M == 0) return NNHIP_OK;
     NNHIP_REQUIRE(X && xi && s && rowsum, fn, "null pointer");
     NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
     if (!token_quant_tm_ok(K, M))
         return fail(NNHIP_ERR_UNSUPPORTED, fn, "decode sizes only (1 <= M <= 64, 1 <= K <= 11264)");
-    NNHIP_LAUNCH(fn, launch_token_quant_tm(ctx->stream, X, gamma, eps, K, M, xi, s, rowsum));
+    NNHIP_LAUNCH(fn, launch_token_quant_tm(ctx->stream, X, gamma, eps, K, M, xi, s, rowsum, &pf));
     return NNHIP_OK;
 }
 

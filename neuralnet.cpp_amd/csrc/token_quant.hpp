@@ -17,7 +17,7 @@ namespace
 {
 
 constexpr int kParts = 512;  // sum-of-squares parts
-constexpr int kOneThreads = 512;  // one-token kernels: thread t owns part t
+constexpr int kOneThreads = kOneThreadsHost;  // one-token kernels: thread t owns part t
 
 __device__ __forceinline__ int quantize_one(float x, float s)
 {
@@ -168,7 +168,30 @@ struct TokArgs
     uint32_t* xq_ref;
     float* fout;
     int xtm;  // one-token kernel: X is token-major (M, K) instead of (K, M)
+    Prefetch pf;  // one-token kernels: blocks M .. M + pf.blocks - 1 read these ranges
 };
+
+// Block b of a one-token kernel's prefetch blocks: thread t reads the 16-byte units
+// (k * blocks + b) * 512 + t (k < kPfUnitsPerThread) of the concatenated ranges, consecutive
+// threads consecutive units. The empty asm keeps the loads (their values are not used).
+__device__ __forceinline__ void prefetch_block(const Prefetch& pf, int b)
+{
+    const uint32_t e0 = pf.n16[0], e1 = e0 + pf.n16[1], e2 = e1 + pf.n16[2], e3 = e2 + pf.n16[3];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kPfUnitsPerThread; ++k)
+    {
+        const uint32_t u = (uint32_t)(k * pf.blocks + b) * kOneThreads + threadIdx.x;
+        if (u >= e3) break;
+        const uint4* q = u < e0   ? static_cast<const uint4*>(pf.p[0]) + u
+                         : u < e1 ? static_cast<const uint4*>(pf.p[1]) + (u - e0)
+                         : u < e2 ? static_cast<const uint4*>(pf.p[2]) + (u - e1)
+                                  : static_cast<const uint4*>(pf.p[3]) + (u - e2);
+        const uint4 v = *q;
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    asm volatile("" ::"v"(acc));
+}
 
 // LDS of the one-token kernels
 struct OneShared

@@ -174,3 +174,59 @@ def test_token_major_rejects(ctx, nnhip):
     with pytest.raises(nnhip.NNHipError) as e:     # K = 256: not a decode GEMV width
         ctx.ternary_matmul_glu_tokens(rp, torch.ones(32, device="cuda"), xi, f, i, 16, 256, 16)
     assert e.value.status == 5
+
+
+def test_prefetch_hint_leaves_results(ctx, orc, nnhip):
+    """nnhip_ctx_prefetch_next: the quantizer call that takes the ranges (its extra blocks read
+    them) gives the bits it gives without them, on every entry point that takes them; the hint
+    is consumed by that call, also where the launch cannot carry it (M > 64)."""
+    import torch
+    N, K, M, slices = 2560, 6912, 16, 4
+    W = normal((N, K), 81, 0.0, 0.02)
+    tau = np.full(N, np.abs(W.astype(np.float64)).mean(), np.float32)
+    rp = ctx.repack(dev(orc.trit_pack(W, tau)), K)
+    big = torch.arange(3 * 1024 * 1024 + 5, dtype=torch.int32, device="cuda")  # 12 MiB + 20 B
+    ranges = [rp, big[:1000], big, big[16:17]]
+    X = dev(normal((K, M), 82) * np.float32(3.0))
+    g = dev(1.0 + 0.2 * normal((K,), 83))
+    say("prefetch: rmsnorm_quant_i8 / act_quant_i8")
+    ref = [host(t) for t in ctx.rmsnorm_quant_i8(X, g, 1e-5)]
+    ctx.prefetch_next(ranges)
+    got = [host(t) for t in ctx.rmsnorm_quant_i8(X, g, 1e-5)]
+    assert all(np.array_equal(a.view(np.uint8), b.view(np.uint8)) for a, b in zip(got, ref))
+    ref = [host(t) for t in ctx.act_quant_i8(X)]
+    ctx.prefetch_next([big])
+    got = [host(t) for t in ctx.act_quant_i8(X)]
+    assert all(np.array_equal(a.view(np.uint8), b.view(np.uint8)) for a, b in zip(got, ref))
+    say("prefetch: rmsnorm_quant_i8_tokens")
+    Xt = dev(np.ascontiguousarray(host(X).T))
+    ref = [host(t) for t in ctx.rmsnorm_quant_i8_tokens(Xt, g, 1e-5)]
+    ctx.prefetch_next([rp, big])
+    got = [host(t) for t in ctx.rmsnorm_quant_i8_tokens(Xt, g, 1e-5)]
+    assert all(np.array_equal(a.view(np.uint8), b.view(np.uint8)) for a, b in zip(got, ref))
+    say("prefetch: partial_residual_quant_i8")
+    xi, s_d, rs = ctx.act_quant_i8(X)
+    part = ctx.ternary_matmul_partial(rp, xi, N, K, M, slices)
+    r = dev(normal((N, M), 84))
+    gn = dev(1.0 + 0.1 * normal((N,), 85))
+    x0 = torch.empty((N, M), device="cuda")
+    ref = [host(t) for t in ctx.partial_residual_quant_i8(part, dev(tau), s_d, rs, N, M, x0, res=r, gamma=gn,
+                                                          eps=1e-5)]
+    x1 = torch.empty((N, M), device="cuda")
+    ctx.prefetch_next(ranges)
+    got = [host(t) for t in ctx.partial_residual_quant_i8(part, dev(tau), s_d, rs, N, M, x1, res=r, gamma=gn,
+                                                          eps=1e-5)]
+    assert all(np.array_equal(a.view(np.uint8), b.view(np.uint8)) for a, b in zip(got, ref))
+    assert np.array_equal(host(x1).view(np.uint32), host(x0).view(np.uint32))
+    say("prefetch: taken by a call that cannot carry it, then cleared")
+    X2 = dev(normal((512, 128), 86))
+    ref = [host(t) for t in ctx.act_quant_i8(X2)]
+    ctx.prefetch_next([big])
+    got = [host(t) for t in ctx.act_quant_i8(X2)]      # M = 128: register kernel, hint dropped
+    assert all(np.array_equal(a.view(np.uint8), b.view(np.uint8)) for a, b in zip(got, ref))
+    ctx.prefetch_next([])
+    with pytest.raises(nnhip.NNHipError):
+        ctx.prefetch_next([big, big, big, big, big])    # more than 4 ranges
+    with pytest.raises(nnhip.NNHipError):
+        ctx.prefetch_next([big[1:]])                    # not 16-byte aligned
+    torch.cuda.synchronize()
