@@ -495,6 +495,17 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
                                     const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
                                     size_t max_len, float scale, float* out);
 
+/* nnhip_attention_decode with the output token-major: out (B, H*dk), row b = sequence b's
+ * H heads of dk values, the same bits as out transposed (same kernels, another store index).
+ * For a decode step whose next kernel works on whole tokens (nnhip_rmsnorm_quant_i8_tokens:
+ * each token's values are then one contiguous row instead of elements B*4 bytes apart). No
+ * separate counterpart in the reference: the same step 8 of AttentionBase::forward_step
+ * (compute_layer_attention.hpp:1022-1083), written in the layout the next step reads. */
+nnhip_status nnhip_attention_decode_tokens(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                           size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                           const float* rope_cos, const float* rope_sin, float* k_cache,
+                                           float* v_cache, size_t max_len, float scale, float* out);
+
 /* ---- batched prefill (config C5's 2048-token context): T new tokens of each of B sequences at
  *      positions pos0 .. pos0 + T - 1 in one pass. The reference fills the cache by running
  *      forward_step once per context token (GPTModel::generate, include/neuralnet.cpp/

@@ -130,6 +130,8 @@ SIGNATURES = {
     "nnhip_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz, _sz]),
     "nnhip_attention_decode": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _f,
                                      _vp]),
+    "nnhip_attention_decode_tokens": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _sz,
+                                            _f, _vp]),
     "nnhip_add": (_st, [_vp, _vp, _vp, _sz, _vp]),
     "nnhip_kv_cache_fill": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz]),
     "nnhip_attention_prefill": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _f, _vp]),
@@ -643,21 +645,24 @@ class Context:
 
     # -- batched decode step
     def attention_decode(self, q, k, v, H: int, Hkv: int, dk: int, pos, len_bound: int, k_cache, v_cache,
-                         scale: float, cos=None, sin=None, out=None):
+                         scale: float, cos=None, sin=None, out=None, out_tokens: bool = False):
         """q (H*dk, B), k/v (Hkv*dk, B), pos (B) int32 device, caches (B, max_len, Hkv*dk) updated in
-        place (row pos[b]); cos/sin (max_len, dk/2) device tables or None. Returns out (H*dk, B)."""
+        place (row pos[b]); cos/sin (max_len, dk/2) device tables or None. Returns out (H*dk, B), or
+        (B, H*dk) with out_tokens (nnhip_attention_decode_tokens)."""
         torch = self._torch
         B = q.shape[1]
         max_len = k_cache.shape[1]
         if out is None:
-            out = self._empty((H * dk, B), torch.float32)
+            out = self._empty((B, H * dk) if out_tokens else (H * dk, B), torch.float32)
         self._bind_stream()
-        _check(lib().nnhip_attention_decode(
+        entry = lib().nnhip_attention_decode_tokens if out_tokens else lib().nnhip_attention_decode
+        _check(entry(
             self.h, self._dev(q, torch.float32, "q"), self._dev(k, torch.float32, "k"),
             self._dev(v, torch.float32, "v"), B, H, Hkv, dk, self._dev(pos, torch.int32, "pos"), len_bound,
             self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
             self._dev(k_cache, torch.float32, "k_cache"), self._dev(v_cache, torch.float32, "v_cache"), max_len,
-            scale, self._dev(out, torch.float32, "out")), "nnhip_attention_decode")
+            scale, self._dev(out, torch.float32, "out")),
+               "nnhip_attention_decode_tokens" if out_tokens else "nnhip_attention_decode")
         return out
 
     def kv_cache_fill(self, k, v, B: int, T: int, Hkv: int, dk: int, pos0: int, k_cache, v_cache, cos=None, sin=None):

@@ -63,7 +63,14 @@ struct AttnArgs
     float* out;
     int B, H, Hkv, R, max_len, len_bound, nchunk;
     float scale;
+    int out_tm;  // out is token-major (B, H*dk) instead of (H*dk, B)
 };
+
+// Index of element i of head h, sequence b in the attention output
+__device__ __forceinline__ size_t attn_out_at(const AttnArgs& a, int h, int DKv, int i, int b)
+{
+    return a.out_tm ? ((size_t)b * a.H + h) * DKv + i : (size_t)(h * DKv + i) * a.B + b;
+}
 
 __device__ __forceinline__ float sum8(float v)
 {
@@ -169,7 +176,7 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             // out-of-range position: NaN output for this sequence's heads, cache untouched
             if (c == 0)
                 for (int e = tid; e < R * DK; e += kAttnThreads)
-                    a.out[(size_t)((g * R + e / DK) * DK + e % DK) * a.B + b] = __builtin_nanf("");
+                    a.out[attn_out_at(a, g * R + e / DK, DK, e % DK, b)] = __builtin_nanf("");
             continue;
         }
         const int len = p + 1;
@@ -429,11 +436,12 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             {
                 const int r = e / Q4, i = 4 * (e - r * Q4);
                 const float l = ml[1][r];
-                float* o = a.out + (size_t)((g * R + r) * DK + i) * a.B + b;
+                const size_t st = a.out_tm ? 1 : (size_t)a.B;
+                float* o = a.out + attn_out_at(a, g * R + r, DK, i, b);
                 o[0] = s4.x / l;
-                o[a.B] = s4.y / l;
-                o[2 * a.B] = s4.z / l;
-                o[3 * a.B] = s4.w / l;
+                o[st] = s4.y / l;
+                o[2 * st] = s4.z / l;
+                o[3 * st] = s4.w / l;
             }
             else
             {
@@ -507,7 +515,7 @@ __global__ __launch_bounds__(DK) void k_attn_merge(AttnArgs a)
             M = Mb;
         }
     }
-    a.out[(size_t)(h * DK + i) * a.B + b] = num / den;
+    a.out[attn_out_at(a, h, DK, i, b)] = num / den;
 }
 
 // Persistent grid: as many work-groups as fit the device at once (at most one per item).
@@ -659,10 +667,10 @@ size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t le
 hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
                               size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
                               const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
-                              float* out, int num_cus)
+                              float* out, int num_cus, bool out_tm)
 {
     AttnArgs a{q, k, v, pos, cosT, sinT, kc, vc, part, out, (int)B, (int)H, (int)Hkv, (int)(H / Hkv),
-               (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale};
+               (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale, out_tm ? 1 : 0};
     switch (dk)
     {
     case 64: return launch_attn_dk<64>(st, a, num_cus);

@@ -1618,12 +1618,12 @@ static nnhip_status attention_prep(nnhip_ctx* ctx, const char* fn, const float* 
     return NNHIP_OK;
 }
 
-nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
-                                    size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
-                                    const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
-                                    size_t max_len, float scale, float* out)
+static nnhip_status attention_decode_common(nnhip_ctx* ctx, const char* fn, const float* q, const float* k,
+                                            const float* v, size_t B, size_t H, size_t Hkv, size_t dk,
+                                            const int32_t* pos, size_t len_bound, const float* rope_cos,
+                                            const float* rope_sin, float* k_cache, float* v_cache, size_t max_len,
+                                            float scale, float* out, bool out_tm)
 {
-    const char* fn = "nnhip_attention_decode";
     NNHIP_CHECK_CTX(fn);
     if (B == 0) return NNHIP_OK;
     size_t wsb = 0;
@@ -1632,8 +1632,27 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
     if (st != NNHIP_OK) return st;
     NNHIP_LAUNCH(fn, launch_attn_decode(ctx->stream, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin,
                                         k_cache, v_cache, max_len, scale,
-                                        wsb ? static_cast<float*>(ctx->attn_ws) : nullptr, out, ctx->num_cus));
+                                        wsb ? static_cast<float*>(ctx->attn_ws) : nullptr, out, ctx->num_cus,
+                                        out_tm));
     return NNHIP_OK;
+}
+
+nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                    size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                    const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
+                                    size_t max_len, float scale, float* out)
+{
+    return attention_decode_common(ctx, "nnhip_attention_decode", q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos,
+                                   rope_sin, k_cache, v_cache, max_len, scale, out, false);
+}
+
+nnhip_status nnhip_attention_decode_tokens(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                           size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                           const float* rope_cos, const float* rope_sin, float* k_cache,
+                                           float* v_cache, size_t max_len, float scale, float* out)
+{
+    return attention_decode_common(ctx, "nnhip_attention_decode_tokens", q, k, v, B, H, Hkv, dk, pos, len_bound,
+                                   rope_cos, rope_sin, k_cache, v_cache, max_len, scale, out, true);
 }
 
 nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,

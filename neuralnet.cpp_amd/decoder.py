@@ -84,6 +84,8 @@ class Decoder:
     # whose quantizers absorb the extra reads (C5 step 2.519 -> 2.498 ms). Also available:
     # "fc1", "fc2" (their GEMVs gain 0.4 and 0 us, their quantizers lose 0.9 and 0.1 us).
     prefetch = ("qkv", "o")
+    # the fused step's attention writes its output token-major (nnhip_attention_decode_tokens)
+    attn_tokens = True
 
     def __init__(self, ctx, cfg: Config, blocks: List[Block], emb, g_final, head: Linear, B: int, caches=None):
         import torch
@@ -109,6 +111,10 @@ class Decoder:
         self.k = torch.empty((Hkv * dk, B), **f32)
         self.v = torch.empty((Hkv * dk, B), **f32)
         self.a = torch.empty((H * dk, B), **f32)
+        # the fused step's attention output, token-major, so that the SubLN quantizer reads each
+        # token as one contiguous row (decode sizes of the one-token quantizer)
+        self._attn_tokens = self.attn_tokens and B <= 64 and H * dk <= 11264
+        self.a_t = torch.empty((B, H * dk), **f32) if self._attn_tokens else None
         self.xi = torch.empty((B * kpd(max(d, H * dk, cfg.F)),), dtype=torch.int8, device=dev)
         self.s = torch.empty((B,), **f32)
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
@@ -285,13 +291,21 @@ class Decoder:
                               (blk.v.rp, blk.v.tau, blk.v.bias, blk.v.N, self.v)],
                              self.xi, self.s, self.rs, blk.q.K, B)
         kc, vc = self.caches[i]
-        ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
-                             self.cos, self.sin, out=self.a)
-        if attn_hook is not None:
-            attn_hook(i, self.a)
         o = blk.o
-        self._prefetch("o", o)
-        self._quant(self.a, blk.g_attn_sub)
+        if self._attn_tokens:
+            ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
+                                 self.cos, self.sin, out=self.a_t, out_tokens=True)
+            if attn_hook is not None:
+                attn_hook(i, self.a_t.t())
+            self._prefetch("o", o)
+            ctx.rmsnorm_quant_i8_tokens(self.a_t, blk.g_attn_sub, cfg.eps, outs=outs)
+        else:
+            ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
+                                 self.cos, self.sin, out=self.a)
+            if attn_hook is not None:
+                attn_hook(i, self.a)
+            self._prefetch("o", o)
+            self._quant(self.a, blk.g_attn_sub)
         ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x, bias=o.bias,
                                out=self.r)
         self._prefetch("fc1", blk.fc1)

@@ -137,6 +137,35 @@ def test_attention_decode_bad_position(ctx, nnhip):
                              dev(kc), dev(vc), 0.125)
 
 
+@pytest.mark.parametrize("B,H,Hkv,dk,pos,len_bound,rope", [
+    (3, 20, 5, 128, [127, 300, 2], 301, True),    # chunks and the merge
+    (2, 8, 2, 64, [5, 90], 100, True),            # one chunk: the chunk kernel writes the output
+    (4, 4, 1, 256, [40, -1, 3, 41], 42, False),   # dk 256, a bad position (NaN outputs)
+    (16, 20, 5, 128, [2000 + 7 * b for b in range(16)], 2106, True),
+])
+def test_attention_decode_tokens(ctx, nnhip, B, H, Hkv, dk, pos, len_bound, rope):
+    """nnhip_attention_decode_tokens: out (B, H*dk) is nnhip_attention_decode's out (H*dk, B)
+    transposed, bit for bit (NaN where the position is out of range), and both append the same
+    rows to the caches."""
+    say(f"attention tokens B={B} H={H} Hkv={Hkv} dk={dk} pos={pos[:4]} len_bound={len_bound}")
+    max_len = len_bound + 8
+    q = normal((H * dk, B), 91 + B)
+    k = normal((Hkv * dk, B), 92 + B)
+    v = normal((Hkv * dk, B), 93 + B)
+    kc = normal((B, max_len, Hkv * dk), 94 + B)
+    vc = normal((B, max_len, Hkv * dk), 95 + B)
+    cos, sin = nnhip.rope_table(dk, max_len) if rope else (None, None)
+    tabs = (dev(cos), dev(sin)) if rope else (None, None)
+    p = dev(np.array(pos, np.int32))
+    kc1, vc1, kc2, vc2 = dev(kc), dev(vc), dev(kc), dev(vc)
+    ref = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, p, len_bound, kc1, vc1, 0.1, *tabs))
+    got = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, p, len_bound, kc2, vc2, 0.1, *tabs,
+                                    out_tokens=True))
+    assert got.shape == (B, H * dk)
+    assert same_bits(np.ascontiguousarray(got.T), ref)
+    assert same_bits(host(kc2), host(kc1)) and same_bits(host(vc2), host(vc1))
+
+
 def test_attention_decode_c5_full_context(ctx, orc, nnhip):
     """Config C5's decode step at full context: 16 sequences at position 2048 of a 2176-row
     cache, sampled sequences checked against the oracle."""
