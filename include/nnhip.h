@@ -323,6 +323,15 @@ nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const floa
                                       const float* s, const int32_t* rowsum, const float* bias, const float* res,
                                       size_t N, size_t K, size_t M, float* Y);
 
+/* nnhip_ternary_matmul_add with res and Y token-major (M, N): the same bits transposed, for a
+ * decoder that keeps its residual stream token-major so that the next per-token quantizer
+ * (nnhip_rmsnorm_quant_i8_tokens) reads contiguous rows. Decode sizes only (the single-launch
+ * GEMV: M <= 16); NNHIP_ERR_UNSUPPORTED otherwise. Same reference step as
+ * nnhip_ternary_matmul_add (compute_layer_attention.hpp:1089; compute_layer_gpt.hpp:208-209). */
+nnhip_status nnhip_ternary_matmul_add_tokens(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                             const float* s, const int32_t* rowsum, const float* bias, const float* res,
+                                             size_t N, size_t K, size_t M, float* Y);
+
 /* Split-k partial sums of a decode ternary GEMV, without the epilogue: part[ks][m][n] (int32,
  * slices x M x N, token-major) = sum over slice ks of the k tiles of trit-code(n, k) * xi(m, k), the
  * integer dot products of nnhip_ternary_matmul's MFMAs, the K range cut into `slices` runs of
@@ -348,6 +357,14 @@ nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part
                                              const float* s_in, const int32_t* rowsum_in, const float* bias,
                                              const float* res, size_t N, size_t M, float* x_out,
                                              const float* gamma, float eps, int8_t* xi, float* s, int32_t* rowsum);
+
+/* nnhip_partial_residual_quant_i8 with res and x_out token-major (M, N); the same bits
+ * transposed (xi, s, rowsum identical). Same reference steps. */
+nnhip_status nnhip_partial_residual_quant_i8_tokens(nnhip_ctx* ctx, const int32_t* part, size_t slices,
+                                                    const float* tau, const float* s_in, const int32_t* rowsum_in,
+                                                    const float* bias, const float* res, size_t N, size_t M,
+                                                    float* x_out, const float* gamma, float eps, int8_t* xi, float* s,
+                                                    int32_t* rowsum);
 
 /* count (1..4) BitLinears on the same int8 input (xi, s, rowsum; shared K and M):
  * Y[i] (N[i], M) = nnhip_ternary_matmul(rp[i], tau[i], xi, s, rowsum, bias[i], N[i], K, M), as one
@@ -549,6 +566,12 @@ nnhip_status nnhip_add(nnhip_ctx* ctx, const float* x, const float* y, size_t n,
  * (compute_layer_gpt.hpp:700-704). */
 nnhip_status nnhip_embedding_gather(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
                                     size_t B, float* out);
+
+/* nnhip_embedding_gather with out token-major (B, d): row b = row ids[b] of the table (NaN row for
+ * an id outside [0, V)). Replaces gather_rows(token_emb, id) (compute_layer_gpt.hpp:700-704)
+ * without the transpose. */
+nnhip_status nnhip_embedding_gather_tokens(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
+                                           size_t B, float* out);
 
 /* ids[b] = greedy choice over column b of logits (V, B): the first index of the largest value,
  * NaN never chosen except that a NaN at index 0 keeps index 0 (the reference's

@@ -104,8 +104,11 @@ SIGNATURES = {
     "nnhip_stream_xor": (_st, [_vp, _vp, _sz, _vp]),
     "nnhip_device_info": (_st, [ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 4),
     "nnhip_ternary_matmul_add": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_ternary_matmul_add_tokens": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_ternary_matmul_partial": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     "nnhip_partial_residual_quant_i8": (_st, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _f, _vp,
+                                              _vp, _vp]),
+    "nnhip_partial_residual_quant_i8_tokens": (_st, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _f, _vp,
                                               _vp, _vp]),
     "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                      ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
@@ -137,6 +140,7 @@ SIGNATURES = {
     "nnhip_attention_prefill": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _f, _vp]),
     "nnhip_copy_columns": (_st, [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp]),
     "nnhip_embedding_gather": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "nnhip_embedding_gather_tokens": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_argmax_cols": (_st, [_vp, _vp, _sz, _sz, _vp]),
 }
 
@@ -567,18 +571,22 @@ class Context:
                "nnhip_ternary_matmul_t_f")
         return Y
 
-    def ternary_matmul_add(self, rp, tau, xi, s, rowsum, N: int, K: int, M: int, res, bias=None, out=None):
-        """Y = ternary_matmul(...) + res (res must not alias Y)."""
+    def ternary_matmul_add(self, rp, tau, xi, s, rowsum, N: int, K: int, M: int, res, bias=None, out=None,
+                           tokens: bool = False):
+        """Y = ternary_matmul(...) + res (res must not alias Y); with tokens, res and Y are (M, N)
+        (nnhip_ternary_matmul_add_tokens, decode sizes)."""
         torch = self._torch
-        Y = self._empty((N, M), torch.float32) if out is None else out
+        Y = self._empty((M, N) if tokens else (N, M), torch.float32) if out is None else out
         self._bind_stream()
-        _check(lib().nnhip_ternary_matmul_add(self.h, self._dev(rp, torch.int32, "rp"),
+        entry = lib().nnhip_ternary_matmul_add_tokens if tokens else lib().nnhip_ternary_matmul_add
+        _check(entry(self.h, self._dev(rp, torch.int32, "rp"),
                                               self._dev(tau, torch.float32, "tau"), self._dev(xi, torch.int8, "xi"),
                                               self._dev(s, torch.float32, "s"),
                                               self._dev(rowsum, torch.int32, "rowsum"),
                                               self._dev(bias, torch.float32, "bias"),
                                               self._dev(res, torch.float32, "res"), N, K, M,
-                                              self._dev(Y, torch.float32, "Y")), "nnhip_ternary_matmul_add")
+                                              self._dev(Y, torch.float32, "Y")),
+               "nnhip_ternary_matmul_add_tokens" if tokens else "nnhip_ternary_matmul_add")
         return Y
 
     def ternary_matmul_partial(self, rp, xi, N: int, K: int, M: int, slices: int, out=None):
@@ -593,12 +601,14 @@ class Context:
         return part
 
     def partial_residual_quant_i8(self, part, tau, s_in, rowsum_in, N: int, M: int, x_out, res=None, bias=None,
-                                  gamma=None, eps: float = 0.0, outs=None):
-        """x_out = epilogue(sum of part) [+ bias] [+ res], then [RMSNorm(gamma) ->] int8: returns (xi, s, rowsum)."""
+                                  gamma=None, eps: float = 0.0, outs=None, tokens: bool = False):
+        """x_out = epilogue(sum of part) [+ bias] [+ res], then [RMSNorm(gamma) ->] int8: returns (xi, s, rowsum).
+        With tokens, res and x_out are token-major (M, N)."""
         torch = self._torch
         xi, s, rs = self._act_out(N, M) if outs is None else outs
         self._bind_stream()
-        _check(lib().nnhip_partial_residual_quant_i8(self.h, self._dev(part, torch.int32, "part"), part.shape[0],
+        entry = lib().nnhip_partial_residual_quant_i8_tokens if tokens else lib().nnhip_partial_residual_quant_i8
+        _check(entry(self.h, self._dev(part, torch.int32, "part"), part.shape[0],
                                                      self._dev(tau, torch.float32, "tau"),
                                                      self._dev(s_in, torch.float32, "s_in"),
                                                      self._dev(rowsum_in, torch.int32, "rowsum_in"),
@@ -607,7 +617,7 @@ class Context:
                                                      self._dev(x_out, torch.float32, "x_out"),
                                                      self._dev(gamma, torch.float32, "gamma"), eps,
                                                      self._dev(xi), self._dev(s), self._dev(rs)),
-               "nnhip_partial_residual_quant_i8")
+               "nnhip_partial_residual_quant_i8_tokens" if tokens else "nnhip_partial_residual_quant_i8")
         return xi, s, rs
 
     def ternary_matmul_n(self, problems, xi, s, rowsum, K: int, M: int):
@@ -727,17 +737,19 @@ class Context:
                                x.numel(), self._dev(out, torch.float32, "out")), "nnhip_add")
         return out
 
-    def embedding_gather(self, table, ids, out=None):
-        """table (V, d), ids (B) int32 device -> (d, B)."""
+    def embedding_gather(self, table, ids, out=None, tokens: bool = False):
+        """table (V, d), ids (B) int32 device -> (d, B), or (B, d) with tokens."""
         torch = self._torch
         V, d = table.shape
         B = ids.shape[0]
         if out is None:
-            out = self._empty((d, B), torch.float32)
+            out = self._empty((B, d) if tokens else (d, B), torch.float32)
         self._bind_stream()
-        _check(lib().nnhip_embedding_gather(self.h, self._dev(table, torch.float32, "table"),
+        entry = lib().nnhip_embedding_gather_tokens if tokens else lib().nnhip_embedding_gather
+        _check(entry(self.h, self._dev(table, torch.float32, "table"),
                                             self._dev(ids, torch.int32, "ids"), V, d, B,
-                                            self._dev(out, torch.float32, "out")), "nnhip_embedding_gather")
+                                            self._dev(out, torch.float32, "out")),
+               "nnhip_embedding_gather_tokens" if tokens else "nnhip_embedding_gather")
         return out
 
     def argmax_cols(self, logits, out=None):

@@ -204,6 +204,7 @@ struct EpiArgs
     const float* bias;         // (N) or null
     const float* res;          // (N, M) residual or null
     float* xout;               // (N, M) epilogue + residual (may alias res)
+    int tm;                    // res and xout are token-major (M, N)
 };
 bool epilogue_quant_ok(size_t N, size_t M);
 hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* gamma, bool norm, float eps, size_t N,
@@ -304,7 +305,7 @@ hipError_t launch_kv_fill(hipStream_t st, const float* k, const float* v, size_t
 hipError_t launch_attn_prefill(hipStream_t st, const float* q, const float* kc, const float* vc, size_t B, size_t T,
                                size_t H, size_t Hkv, size_t dk, size_t pos0, const float* cosT, const float* sinT,
                                size_t max_len, float scale, float* out);
-hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B,
+hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B, bool tm,
                         float* out);
 hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids);
 

@@ -640,7 +640,7 @@ __global__ __launch_bounds__(kOneThreads) void k_token_epi(TokArgs a, EpiArgs e,
             ps[r][k] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
         }
         tv[r] = f < N ? e.tau[f] : 0.0f;
-        rv[r] = (f < N && e.res) ? e.res[(size_t)f * M + m] : 0.0f;
+        rv[r] = (f < N && e.res) ? e.res[e.tm ? (size_t)m * N + f : (size_t)f * M + m] : 0.0f;
     }
     float x[R];
 #pragma unroll
@@ -656,7 +656,7 @@ __global__ __launch_bounds__(kOneThreads) void k_token_epi(TokArgs a, EpiArgs e,
             float y = (tv[r] * sv) * (float)(acc - rs2);
             if (e.bias) y = y + e.bias[f];
             if (e.res) y = y + rv[r];
-            e.xout[(size_t)f * M + m] = y;
+            e.xout[e.tm ? (size_t)m * N + f : (size_t)f * M + m] = y;
             x[r] = y;
         }
     }

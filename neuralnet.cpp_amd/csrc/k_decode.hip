@@ -581,15 +581,16 @@ __global__ __launch_bounds__(kSmallBlock) void k_copy_cols(const float* __restri
     dst[i] = src[r * src_cols + col0 + j * stride];
 }
 
-// out (d, B): column b = row ids[b] of the (V, d) table (NaN column for an id outside [0, V))
+// out (d, B), or token-major (B, d) when tm: column (row) b = row ids[b] of the (V, d) table
+// (NaN for an id outside [0, V))
 __global__ __launch_bounds__(kSmallBlock) void k_embed(const float* __restrict__ table, const int32_t* __restrict__ ids,
-                                                       int V, int d, int B, float* __restrict__ out)
+                                                       int V, int d, int B, int tm, float* __restrict__ out)
 {
     const int b = blockIdx.y;
     const int i = blockIdx.x * kSmallBlock + threadIdx.x;
     if (i >= d) return;
     const int id = ids[b];
-    out[(size_t)i * B + b] = (id >= 0 && id < V) ? table[(size_t)id * d + i] : __builtin_nanf("");
+    out[tm ? (size_t)b * d + i : (size_t)i * B + b] = (id >= 0 && id < V) ? table[(size_t)id * d + i] : __builtin_nanf("");
 }
 
 // ids[b] = the reference greedy rule over column b of logits (V, B): best = l[0], then every
@@ -695,11 +696,11 @@ hipError_t launch_copy_cols(hipStream_t st, const float* src, size_t rows, size_
     return hipGetLastError();
 }
 
-hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B,
+hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B, bool tm,
                         float* out)
 {
     k_embed<<<dim3((unsigned)ceil_div(d, kSmallBlock), (unsigned)B), kSmallBlock, 0, st>>>(table, ids, (int)V, (int)d,
-                                                                                         (int)B, out);
+                                                                                         (int)B, tm ? 1 : 0, out);
     return hipGetLastError();
 }
 

@@ -327,7 +327,9 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvDeepArgs da)
         const uint32_t n = (uint32_t)(rt * 16 + 4 * g + i);
         tv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, n * 4u, 0, 0));
         bv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, n * 4u, 0, 0));
-        const uint32_t ro = (n < (uint32_t)p.N && t < p.M) ? (n * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u;
+        // residual (N, M), or token-major (M, N) when the output is
+        const uint32_t rix = p.ytm ? (uint32_t)t * (uint32_t)p.N + n : n * (uint32_t)p.M + (uint32_t)t;
+        const uint32_t ro = (n < (uint32_t)p.N && t < p.M) ? rix * 4u : 0xFFFFFFF0u;
         rv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, ro, 0, 0));
     }
 
@@ -386,7 +388,8 @@ __global__ __launch_bounds__(kBlock) void k_gemv_deep(GemvDeepArgs da)
         for (int i = 0; i < 4; ++i)
         {
             const int n = rt * 16 + 4 * g + i;
-            const uint32_t off = (live && n < p.N && t < p.M) ? ((uint32_t)n * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u;
+            const uint32_t yix = p.ytm ? (uint32_t)t * (uint32_t)p.N + (uint32_t)n : (uint32_t)n * (uint32_t)p.M + (uint32_t)t;
+            const uint32_t off = (live && n < p.N && t < p.M) ? yix * 4u : 0xFFFFFFF0u;
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[i]), ry, off, 0, 0);
         }
     }

@@ -929,6 +929,40 @@ nnhip_status nnhip_trit_transpose(nnhip_ctx* ctx, const uint32_t* A, size_t K, s
     return NNHIP_OK;
 }
 
+nnhip_status nnhip_ternary_matmul_add_tokens(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
+                                             const float* s, const int32_t* rowsum, const float* bias, const float* res,
+                                             size_t N, size_t K, size_t M, float* Y)
+{
+    const char* fn = "nnhip_ternary_matmul_add_tokens";
+    NNHIP_CHECK_CTX(fn);
+    if (N == 0 || M == 0) return NNHIP_OK;
+    const nnhip_status st = check_matmul_shape(fn, N, K, M);
+    if (st != NNHIP_OK) return st;
+    NNHIP_REQUIRE(rp && tau && xi && s && rowsum && res && Y, fn, "null pointer");
+    NNHIP_REQUIRE(res != Y, fn, "res must not alias Y");
+    NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
+    GemvProblem p{};
+    p.rp = static_cast<const u32x4*>(rp);
+    p.tau = tau;
+    p.xi = xi;
+    p.s = s;
+    p.rowsum = rowsum;
+    p.bias = bias;
+    p.y = Y;
+    p.N = (int32_t)N;
+    p.K = (int32_t)K;
+    p.M = (int32_t)M;
+    p.KT = (int32_t)ceil_div(K, kTileK);
+    p.xlds = -1;
+    p.res = res;
+    p.ytm = 1;
+    if (M > (size_t)kGemvMaxM || !gemv_deep_ok(p, ctx->num_cus))
+        return fail(NNHIP_ERR_UNSUPPORTED, fn,
+                    "decode sizes only (M <= 16, K of 1024 / 2560 / 4096 / 6912 rounded to 256, at most 4 row tiles per CU)");
+    NNHIP_LAUNCH(fn, launch_gemv_deep(ctx->stream, p));
+    return NNHIP_OK;
+}
+
 nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
                                       const float* s, const int32_t* rowsum, const float* bias, const float* res,
                                       size_t N, size_t K, size_t M, float* Y)
@@ -970,12 +1004,12 @@ nnhip_status nnhip_ternary_matmul_partial(nnhip_ctx* ctx, const void* rp, const 
     return NNHIP_OK;
 }
 
-nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part, size_t slices, const float* tau,
-                                             const float* s_in, const int32_t* rowsum_in, const float* bias,
-                                             const float* res, size_t N, size_t M, float* x_out,
-                                             const float* gamma, float eps, int8_t* xi, float* s, int32_t* rowsum)
+static nnhip_status partial_residual_common(nnhip_ctx* ctx, const char* fn, const int32_t* part, size_t slices,
+                                            const float* tau, const float* s_in, const int32_t* rowsum_in,
+                                            const float* bias, const float* res, size_t N, size_t M, float* x_out,
+                                            const float* gamma, float eps, int8_t* xi, float* s, int32_t* rowsum,
+                                            bool tm)
 {
-    const char* fn = "nnhip_partial_residual_quant_i8";
     NNHIP_CHECK_CTX(fn);
     const Prefetch pf = take_prefetch(ctx);
     if (N == 0 || M == 0) return NNHIP_OK;
@@ -984,9 +1018,28 @@ nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part
     NNHIP_REQUIRE(epilogue_quant_ok(N, M), fn, "needs M <= 64 and N <= 11264");
     NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
     NNHIP_REQUIRE(!gamma || eps >= 0.0f, fn, "eps must be >= 0");
-    const EpiArgs e{part, (int)slices, tau, s_in, rowsum_in, bias, res, x_out};
+    const EpiArgs e{part, (int)slices, tau, s_in, rowsum_in, bias, res, x_out, tm ? 1 : 0};
     NNHIP_LAUNCH(fn, launch_epilogue_quant(ctx->stream, e, gamma, gamma != nullptr, eps, N, M, xi, s, rowsum, &pf));
     return NNHIP_OK;
+}
+
+nnhip_status nnhip_partial_residual_quant_i8(nnhip_ctx* ctx, const int32_t* part, size_t slices, const float* tau,
+                                             const float* s_in, const int32_t* rowsum_in, const float* bias,
+                                             const float* res, size_t N, size_t M, float* x_out,
+                                             const float* gamma, float eps, int8_t* xi, float* s, int32_t* rowsum)
+{
+    return partial_residual_common(ctx, "nnhip_partial_residual_quant_i8", part, slices, tau, s_in, rowsum_in, bias,
+                                   res, N, M, x_out, gamma, eps, xi, s, rowsum, false);
+}
+
+nnhip_status nnhip_partial_residual_quant_i8_tokens(nnhip_ctx* ctx, const int32_t* part, size_t slices,
+                                                    const float* tau, const float* s_in, const int32_t* rowsum_in,
+                                                    const float* bias, const float* res, size_t N, size_t M,
+                                                    float* x_out, const float* gamma, float eps, int8_t* xi, float* s,
+                                                    int32_t* rowsum)
+{
+    return partial_residual_common(ctx, "nnhip_partial_residual_quant_i8_tokens", part, slices, tau, s_in, rowsum_in,
+                                   bias, res, N, M, x_out, gamma, eps, xi, s, rowsum, true);
 }
 
 nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* const* rp, const float* const* tau,
@@ -1720,16 +1773,27 @@ nnhip_status nnhip_add(nnhip_ctx* ctx, const float* x, const float* y, size_t n,
     return NNHIP_OK;
 }
 
-nnhip_status nnhip_embedding_gather(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
-                                    size_t B, float* out)
+static nnhip_status embedding_gather_common(nnhip_ctx* ctx, const char* fn, const float* table, const int32_t* ids,
+                                            size_t V, size_t d, size_t B, float* out, bool tm)
 {
-    const char* fn = "nnhip_embedding_gather";
     NNHIP_CHECK_CTX(fn);
     if (B == 0 || d == 0) return NNHIP_OK;
     NNHIP_REQUIRE(table && ids && out, fn, "null pointer");
     NNHIP_REQUIRE(V >= 1 && V <= kMaxDim && d <= kMaxDim && B <= 65535 && mul_ok(V, d), fn, "size out of range");
-    NNHIP_LAUNCH(fn, launch_embed(ctx->stream, table, ids, V, d, B, out));
+    NNHIP_LAUNCH(fn, launch_embed(ctx->stream, table, ids, V, d, B, tm, out));
     return NNHIP_OK;
+}
+
+nnhip_status nnhip_embedding_gather(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
+                                    size_t B, float* out)
+{
+    return embedding_gather_common(ctx, "nnhip_embedding_gather", table, ids, V, d, B, out, false);
+}
+
+nnhip_status nnhip_embedding_gather_tokens(nnhip_ctx* ctx, const float* table, const int32_t* ids, size_t V, size_t d,
+                                           size_t B, float* out)
+{
+    return embedding_gather_common(ctx, "nnhip_embedding_gather_tokens", table, ids, V, d, B, out, true);
 }
 
 nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids)

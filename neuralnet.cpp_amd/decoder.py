@@ -86,6 +86,10 @@ class Decoder:
     prefetch = ("qkv", "o")
     # the fused step's attention writes its output token-major (nnhip_attention_decode_tokens)
     attn_tokens = True
+    # the fused step keeps the residual stream x and the mid-block sum r token-major (B, d), so
+    # the RMSNorm quantizers read contiguous rows (nnhip_embedding_gather_tokens,
+    # nnhip_ternary_matmul_add_tokens, nnhip_partial_residual_quant_i8_tokens)
+    res_tokens = True
 
     def __init__(self, ctx, cfg: Config, blocks: List[Block], emb, g_final, head: Linear, B: int, caches=None):
         import torch
@@ -115,11 +119,28 @@ class Decoder:
         # token as one contiguous row (decode sizes of the one-token quantizer)
         self._attn_tokens = self.attn_tokens and B <= 64 and H * dk <= 11264
         self.a_t = torch.empty((B, H * dk), **f32) if self._attn_tokens else None
+        self._res_tokens = self.res_tokens and B <= 16 and d <= 11264
+        self.x_t = torch.empty((B, d), **f32) if self._res_tokens else None
+        self.r_t = torch.empty((B, d), **f32) if self._res_tokens else None
         self.xi = torch.empty((B * kpd(max(d, H * dk, cfg.F)),), dtype=torch.int8, device=dev)
         self.s = torch.empty((B,), **f32)
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
         self.logits = torch.empty((cfg.vocab, B), **f32)
         self.ids = torch.empty((B,), dtype=torch.int32, device=dev)
+        if self._res_tokens and blocks:
+            # the token-major o projection runs on the single-launch decode GEMV only: one call on
+            # the o shape (scratch in, scratch out) tells whether this model's shape is taken
+            o = blocks[0].o
+            self.xi.zero_()
+            self.s.zero_()
+            self.rs.zero_()
+            try:
+                ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x_t.zero_(),
+                                       out=self.r_t, tokens=True)
+            except _pkg().NNHipError as e:
+                if e.status != 5:   # NNHIP_ERR_UNSUPPORTED
+                    raise
+                self._res_tokens = False
 
     def _prefill_buffers(self, M: int):
         """Scratch of a prefill over M = B*T token columns (allocated once per M)."""
@@ -306,10 +327,15 @@ class Decoder:
                 attn_hook(i, self.a)
             self._prefetch("o", o)
             self._quant(self.a, blk.g_attn_sub)
-        ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x, bias=o.bias,
-                               out=self.r)
         self._prefetch("fc1", blk.fc1)
-        self._quant(self.r, blk.g2)
+        if self._res_tokens:
+            ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x_t, bias=o.bias,
+                                   out=self.r_t, tokens=True)
+            ctx.rmsnorm_quant_i8_tokens(self.r_t, blk.g2, cfg.eps, outs=outs)
+        else:
+            ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x, bias=o.bias,
+                                   out=self.r)
+            self._quant(self.r, blk.g2)
         part, h = self._scratch()
         self._ffn_gate_quant(blk, h)
         f2 = blk.fc2
@@ -321,17 +347,29 @@ class Decoder:
             self._prefetch("qkv", nb.q, nb.k, nb.v)
         else:
             self._prefetch("qkv", self.head)
-        ctx.partial_residual_quant_i8(pf, f2.tau, self.s, self.rs, d, B, self.x, res=self.r, bias=f2.bias,
-                                      gamma=g_next, eps=cfg.eps, outs=outs)
+        if self._res_tokens:
+            ctx.partial_residual_quant_i8(pf, f2.tau, self.s, self.rs, d, B, self.x_t, res=self.r_t, bias=f2.bias,
+                                          gamma=g_next, eps=cfg.eps, outs=outs, tokens=True)
+        else:
+            ctx.partial_residual_quant_i8(pf, f2.tau, self.s, self.rs, d, B, self.x, res=self.r, bias=f2.bias,
+                                          gamma=g_next, eps=cfg.eps, outs=outs)
 
     def step(self, ids, pos, len_bound: int, attn_hook=None):
         """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,))."""
         ctx = self.ctx
-        ctx.embedding_gather(self.emb, ids, out=self.x)
-        if self.fused_ok():
+        fused = self.fused_ok()
+        if fused and self._res_tokens:
+            ctx.embedding_gather(self.emb, ids, out=self.x_t, tokens=True)
+        else:
+            ctx.embedding_gather(self.emb, ids, out=self.x)
+        if fused:
             if self.blocks:
                 self._prefetch("qkv", self.blocks[0].q, self.blocks[0].k, self.blocks[0].v)
-            self._quant(self.x, self.blocks[0].g1 if self.blocks else self.g_final)
+            g0 = self.blocks[0].g1 if self.blocks else self.g_final
+            if self._res_tokens:
+                ctx.rmsnorm_quant_i8_tokens(self.x_t, g0, self.cfg.eps, outs=(self.xi, self.s, self.rs))
+            else:
+                self._quant(self.x, g0)
             for i in range(len(self.blocks)):
                 self.block_step_fused(i, pos, len_bound, attn_hook)
         else:

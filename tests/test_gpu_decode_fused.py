@@ -230,3 +230,52 @@ def test_prefetch_hint_leaves_results(ctx, orc, nnhip):
     with pytest.raises(nnhip.NNHipError):
         ctx.prefetch_next([big[1:]])                    # not 16-byte aligned
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_token_major_residual_entries(ctx, orc, bias):
+    """The token-major forms of the decoder's residual-stream entry points give the bits of the
+    feature-major ones transposed: nnhip_ternary_matmul_add_tokens (o + residual),
+    nnhip_partial_residual_quant_i8_tokens (fc2 epilogue + residual + next quantizer, also with
+    x_out aliasing res) and nnhip_embedding_gather_tokens (an id out of range gives a NaN row)."""
+    import torch
+    N, K, M = 2560, 2560, 16
+    say(f"token-major residual entries bias={bias}")
+    W = normal((N, K), 101, 0.0, 0.02)
+    tau = np.full(N, np.abs(W.astype(np.float64)).mean(), np.float32)
+    rp = ctx.repack(dev(orc.trit_pack(W, tau)), K)
+    xi, s_d, rs = ctx.act_quant_i8(dev(normal((K, M), 102)))
+    b = dev(normal((N,), 103)) if bias else None
+    res = normal((N, M), 104)
+    y = host(ctx.ternary_matmul_add(rp, dev(tau), xi, s_d, rs, N, K, M, dev(res), bias=b))
+    yt = host(ctx.ternary_matmul_add(rp, dev(tau), xi, s_d, rs, N, K, M, dev(np.ascontiguousarray(res.T)), bias=b,
+                                     tokens=True))
+    assert yt.shape == (M, N)
+    assert np.array_equal(np.ascontiguousarray(yt.T).view(np.uint32), y.view(np.uint32))
+    # fc2-shaped partial sums + epilogue + residual + next RMSNorm quantizer
+    N2, K2, S = 2560, 6912, 4
+    W2 = normal((N2, K2), 105, 0.0, 0.02)
+    tau2 = np.full(N2, np.abs(W2.astype(np.float64)).mean(), np.float32)
+    rp2 = ctx.repack(dev(orc.trit_pack(W2, tau2)), K2)
+    xi2, s2, rs2 = ctx.act_quant_i8(dev(normal((K2, M), 106)))
+    part = ctx.ternary_matmul_partial(rp2, xi2, N2, K2, M, S)
+    g = dev(1.0 + 0.1 * normal((N2,), 107))
+    b2 = dev(normal((N2,), 108)) if bias else None
+    x0 = torch.empty((N2, M), device="cuda")
+    ref = [host(t) for t in ctx.partial_residual_quant_i8(part, dev(tau2), s2, rs2, N2, M, x0, res=dev(res), bias=b2,
+                                                          gamma=g, eps=1e-5)]
+    x1 = dev(np.ascontiguousarray(res.T))            # in place: x_out aliases res
+    got = [host(t) for t in ctx.partial_residual_quant_i8(part, dev(tau2), s2, rs2, N2, M, x1, res=x1, bias=b2,
+                                                          gamma=g, eps=1e-5, tokens=True)]
+    assert all(np.array_equal(a.view(np.uint8), c.view(np.uint8)) for a, c in zip(got, ref))
+    assert np.array_equal(np.ascontiguousarray(host(x1).T).view(np.uint32), host(x0).view(np.uint32))
+    # embedding rows
+    V, d = 97, 2560
+    table = dev(normal((V, d), 109))
+    ids = dev(np.array([3, 96, 0, 97, 5, -1, 40, 41, 1, 2, 3, 4, 5, 6, 7, 8], np.int32))
+    e = host(ctx.embedding_gather(table, ids))
+    et = host(ctx.embedding_gather(table, ids, tokens=True))
+    assert et.shape == (16, d)
+    a, c = np.ascontiguousarray(et.T), e
+    assert np.array_equal(np.isnan(a), np.isnan(c)) and np.all(np.isnan(a[:, 3])) and np.all(np.isnan(a[:, 5]))
+    assert np.array_equal(a[~np.isnan(a)].view(np.uint32), c[~np.isnan(c)].view(np.uint32))
