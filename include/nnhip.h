@@ -376,6 +376,14 @@ nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* co
                                     const float* const* bias, const size_t* N, float* const* Y, const int8_t* xi,
                                     const float* s, const int32_t* rowsum, size_t K, size_t M);
 
+/* nnhip_ternary_matmul_n with each Y[i] token-major (M, N[i]): the same bits transposed, for a
+ * decoder whose attention takes token-major q, k, v (nnhip_attention_decode_tokens). Decode
+ * sizes only (the single-launch GEMV); NNHIP_ERR_UNSUPPORTED otherwise. Same reference calls. */
+nnhip_status nnhip_ternary_matmul_n_tokens(nnhip_ctx* ctx, size_t count, const void* const* rp,
+                                           const float* const* tau, const float* const* bias, const size_t* N,
+                                           float* const* Y, const int8_t* xi, const float* s, const int32_t* rowsum,
+                                           size_t K, size_t M);
+
 /* Grouped decode GEMV: many independent (weights, activations) problems with M <= 16 in one
  * launch, e.g. the q/k/v or gate/up projections of a layer, or a whole layer stack. The
  * descriptors are copied to the device once at creation; run() launches one kernel. */
@@ -512,12 +520,14 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
                                     const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
                                     size_t max_len, float scale, float* out);
 
-/* nnhip_attention_decode with the output token-major: out (B, H*dk), row b = sequence b's
- * H heads of dk values, the same bits as out transposed (same kernels, another store index).
- * For a decode step whose next kernel works on whole tokens (nnhip_rmsnorm_quant_i8_tokens:
- * each token's values are then one contiguous row instead of elements B*4 bytes apart). No
- * separate counterpart in the reference: the same step 8 of AttentionBase::forward_step
- * (compute_layer_attention.hpp:1022-1083), written in the layout the next step reads. */
+/* nnhip_attention_decode on token-major rows: q (B, H*dk), k / v (B, Hkv*dk) and out (B, H*dk),
+ * row b = sequence b's heads; the same bits as nnhip_attention_decode on the transposes (same
+ * kernels, other load and store indices), and the same cache rows. For a decode step whose
+ * producing and consuming kernels work on whole tokens (nnhip_ternary_matmul_n_tokens,
+ * nnhip_rmsnorm_quant_i8_tokens: each token's values are then one contiguous row instead of
+ * elements B*4 bytes apart). No separate counterpart in the reference: the same steps of
+ * AttentionBase::forward_step (compute_layer_attention.hpp:1022-1083) in the layout of the
+ * neighbouring steps. */
 nnhip_status nnhip_attention_decode_tokens(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
                                            size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
                                            const float* rope_cos, const float* rope_sin, float* k_cache,

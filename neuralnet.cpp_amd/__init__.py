@@ -112,6 +112,8 @@ SIGNATURES = {
                                               _vp, _vp]),
     "nnhip_ternary_matmul_n": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                      ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
+    "nnhip_ternary_matmul_n_tokens": (_st, [_vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                     ctypes.POINTER(_sz), ctypes.POINTER(_vp), _vp, _vp, _vp, _sz, _sz]),
     "nnhip_ffn_glu_i8_add": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
                                    _vp, _vp, _vp]),
     "nnhip_group_create": (_st, [_vp, ctypes.POINTER(GemvDesc), _sz, ctypes.POINTER(_vp)]),
@@ -620,20 +622,23 @@ class Context:
                "nnhip_partial_residual_quant_i8_tokens" if tokens else "nnhip_partial_residual_quant_i8")
         return xi, s, rs
 
-    def ternary_matmul_n(self, problems, xi, s, rowsum, K: int, M: int):
-        """problems: list of (rp, tau, bias or None, N, out or None) sharing the input; returns the outputs."""
+    def ternary_matmul_n(self, problems, xi, s, rowsum, K: int, M: int, tokens: bool = False):
+        """problems: list of (rp, tau, bias or None, N, out or None) sharing the input; returns the outputs
+        ((N, M) each, or token-major (M, N) with tokens: nnhip_ternary_matmul_n_tokens)."""
         torch = self._torch
         n = len(problems)
-        outs = [p[4] if p[4] is not None else self._empty((p[3], M), torch.float32) for p in problems]
+        outs = [p[4] if p[4] is not None else self._empty((M, p[3]) if tokens else (p[3], M), torch.float32)
+                for p in problems]
         rp = (_vp * n)(*[self._dev(p[0], torch.int32, "rp") for p in problems])
         tau = (_vp * n)(*[self._dev(p[1], torch.float32, "tau") for p in problems])
         bias = (_vp * n)(*[self._dev(p[2], torch.float32, "bias") for p in problems])
         Ns = (_sz * n)(*[p[3] for p in problems])
         Ys = (_vp * n)(*[self._dev(o, torch.float32, "Y") for o in outs])
         self._bind_stream()
-        _check(lib().nnhip_ternary_matmul_n(self.h, n, rp, tau, bias, Ns, Ys, self._dev(xi, torch.int8, "xi"),
-                                            self._dev(s, torch.float32, "s"), self._dev(rowsum, torch.int32, "rowsum"),
-                                            K, M), "nnhip_ternary_matmul_n")
+        entry = lib().nnhip_ternary_matmul_n_tokens if tokens else lib().nnhip_ternary_matmul_n
+        _check(entry(self.h, n, rp, tau, bias, Ns, Ys, self._dev(xi, torch.int8, "xi"),
+                     self._dev(s, torch.float32, "s"), self._dev(rowsum, torch.int32, "rowsum"), K, M),
+               "nnhip_ternary_matmul_n_tokens" if tokens else "nnhip_ternary_matmul_n")
         return outs
 
     def ffn_glu_i8_add(self, X, gamma, eps: float, F: int, rp1, tau1, b1, rp2, tau2, b2, res, act: int = ACT_SWIGLU,
@@ -655,24 +660,24 @@ class Context:
 
     # -- batched decode step
     def attention_decode(self, q, k, v, H: int, Hkv: int, dk: int, pos, len_bound: int, k_cache, v_cache,
-                         scale: float, cos=None, sin=None, out=None, out_tokens: bool = False):
+                         scale: float, cos=None, sin=None, out=None, tokens: bool = False):
         """q (H*dk, B), k/v (Hkv*dk, B), pos (B) int32 device, caches (B, max_len, Hkv*dk) updated in
-        place (row pos[b]); cos/sin (max_len, dk/2) device tables or None. Returns out (H*dk, B), or
-        (B, H*dk) with out_tokens (nnhip_attention_decode_tokens)."""
+        place (row pos[b]); cos/sin (max_len, dk/2) device tables or None. Returns out (H*dk, B).
+        With tokens, q (B, H*dk), k/v (B, Hkv*dk) and out (B, H*dk) (nnhip_attention_decode_tokens)."""
         torch = self._torch
-        B = q.shape[1]
+        B = q.shape[0] if tokens else q.shape[1]
         max_len = k_cache.shape[1]
         if out is None:
-            out = self._empty((B, H * dk) if out_tokens else (H * dk, B), torch.float32)
+            out = self._empty((B, H * dk) if tokens else (H * dk, B), torch.float32)
         self._bind_stream()
-        entry = lib().nnhip_attention_decode_tokens if out_tokens else lib().nnhip_attention_decode
+        entry = lib().nnhip_attention_decode_tokens if tokens else lib().nnhip_attention_decode
         _check(entry(
             self.h, self._dev(q, torch.float32, "q"), self._dev(k, torch.float32, "k"),
             self._dev(v, torch.float32, "v"), B, H, Hkv, dk, self._dev(pos, torch.int32, "pos"), len_bound,
             self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
             self._dev(k_cache, torch.float32, "k_cache"), self._dev(v_cache, torch.float32, "v_cache"), max_len,
             scale, self._dev(out, torch.float32, "out")),
-               "nnhip_attention_decode_tokens" if out_tokens else "nnhip_attention_decode")
+               "nnhip_attention_decode_tokens" if tokens else "nnhip_attention_decode")
         return out
 
     def kv_cache_fill(self, k, v, B: int, T: int, Hkv: int, dk: int, pos0: int, k_cache, v_cache, cos=None, sin=None):

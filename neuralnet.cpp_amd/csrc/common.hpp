@@ -292,7 +292,7 @@ size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t le
 hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
                               size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
                               const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
-                              float* out, int num_cus, bool out_tm = false);
+                              float* out, int num_cus, bool tm = false);  // tm: q, k, v and out token-major
 hipError_t launch_add(hipStream_t st, const float* x, const float* y, size_t n, float* out);
 // dst (rows, n) column j = src (rows, src_cols) column col0 + j * stride (k_decode.hip)
 hipError_t launch_copy_cols(hipStream_t st, const float* src, size_t rows, size_t src_cols, size_t col0, size_t stride,

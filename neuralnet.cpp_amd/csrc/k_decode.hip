@@ -64,6 +64,7 @@ struct AttnArgs
     int B, H, Hkv, R, max_len, len_bound, nchunk;
     float scale;
     int out_tm;  // out is token-major (B, H*dk) instead of (H*dk, B)
+    int in_tm;   // q, k, v are token-major (B, H*dk), (B, Hkv*dk) instead of (H*dk, B), (Hkv*dk, B)
 };
 
 // Index of element i of head h, sequence b in the attention output
@@ -190,10 +191,14 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         //      key/value), then the first PB passes of cached key rows. The queries' RoPE and
         //      LDS staging wait only for the query loads, so the key rows stream in meanwhile.
         // (buffer-resource loads: 32-bit offsets keep the address registers few)
-        const uint32_t qkv_rows = (uint32_t)a.B * 4u;  // bytes between features of one column
-        const __amdgpu_buffer_rsrc_t rq = attn_rsrc(a.q + b, (uint32_t)a.H * DK * qkv_rows);
-        const __amdgpu_buffer_rsrc_t rkn = attn_rsrc(a.k + b, (uint32_t)a.Hkv * DK * qkv_rows);
-        const __amdgpu_buffer_rsrc_t rvn = attn_rsrc(a.v + b, (uint32_t)a.Hkv * DK * qkv_rows);
+        // bytes between features of one token: 4 in token-major rows, B * 4 down a column
+        const uint32_t qkv_rows = a.in_tm ? 4u : (uint32_t)a.B * 4u;
+        const __amdgpu_buffer_rsrc_t rq =
+            attn_rsrc(a.in_tm ? a.q + (size_t)b * a.H * DK : a.q + b, (uint32_t)a.H * DK * qkv_rows);
+        const __amdgpu_buffer_rsrc_t rkn =
+            attn_rsrc(a.in_tm ? a.k + (size_t)b * a.Hkv * DK : a.k + b, (uint32_t)a.Hkv * DK * qkv_rows);
+        const __amdgpu_buffer_rsrc_t rvn =
+            attn_rsrc(a.in_tm ? a.v + (size_t)b * a.Hkv * DK : a.v + b, (uint32_t)a.Hkv * DK * qkv_rows);
         // the RoPE table rows of position p (unused without tables)
         const __amdgpu_buffer_rsrc_t rcs = attn_rsrc(a.cosT ? a.cosT + (size_t)p * HALF : a.q, HALF * 4u);
         const __amdgpu_buffer_rsrc_t rsn = attn_rsrc(a.sinT ? a.sinT + (size_t)p * HALF : a.q, HALF * 4u);
@@ -671,7 +676,7 @@ hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, co
                               float* out, int num_cus, bool out_tm)
 {
     AttnArgs a{q, k, v, pos, cosT, sinT, kc, vc, part, out, (int)B, (int)H, (int)Hkv, (int)(H / Hkv),
-               (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale, out_tm ? 1 : 0};
+               (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale, out_tm ? 1 : 0, out_tm ? 1 : 0};
     switch (dk)
     {
     case 64: return launch_attn_dk<64>(st, a, num_cus);

@@ -1042,11 +1042,11 @@ nnhip_status nnhip_partial_residual_quant_i8_tokens(nnhip_ctx* ctx, const int32_
                                    bias, res, N, M, x_out, gamma, eps, xi, s, rowsum, true);
 }
 
-nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* const* rp, const float* const* tau,
-                                    const float* const* bias, const size_t* N, float* const* Y, const int8_t* xi,
-                                    const float* s, const int32_t* rowsum, size_t K, size_t M)
+static nnhip_status matmul_n_common(nnhip_ctx* ctx, const char* fn, size_t count, const void* const* rp,
+                                    const float* const* tau, const float* const* bias, const size_t* N,
+                                    float* const* Y, const int8_t* xi, const float* s, const int32_t* rowsum, size_t K,
+                                    size_t M, bool tm)
 {
-    const char* fn = "nnhip_ternary_matmul_n";
     NNHIP_CHECK_CTX(fn);
     if (count == 0 || M == 0) return NNHIP_OK;
     NNHIP_REQUIRE(count <= (size_t)kGemvDeepMulti, fn, "count must be in [1, 4]");
@@ -1072,12 +1072,16 @@ nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* co
         p.M = (int32_t)M;
         p.KT = (int32_t)ceil_div(K, kTileK);
         p.xlds = -1;
+        p.ytm = tm ? 1 : 0;
     }
     if (M <= (size_t)kGemvMaxM && gemv_deep_multi_ok(ps, (int)count, ctx->num_cus))
     {
         NNHIP_LAUNCH(fn, launch_gemv_deep_multi(ctx->stream, ps, (int)count));
         return NNHIP_OK;
     }
+    if (tm)
+        return fail(NNHIP_ERR_UNSUPPORTED, fn,
+                    "decode sizes only (M <= 16, K of 1024 / 2560 / 4096 / 6912 rounded to 256, at most 4 row tiles per CU)");
     for (size_t i = 0; i < count; ++i)
     {
         const nnhip_status st = run_matmul(ctx, fn, rp[i], tau[i], xi, s, rowsum, bias ? bias[i] : nullptr, N[i], K, M,
@@ -1085,6 +1089,21 @@ nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* co
         if (st != NNHIP_OK) return st;
     }
     return NNHIP_OK;
+}
+
+nnhip_status nnhip_ternary_matmul_n(nnhip_ctx* ctx, size_t count, const void* const* rp, const float* const* tau,
+                                    const float* const* bias, const size_t* N, float* const* Y, const int8_t* xi,
+                                    const float* s, const int32_t* rowsum, size_t K, size_t M)
+{
+    return matmul_n_common(ctx, "nnhip_ternary_matmul_n", count, rp, tau, bias, N, Y, xi, s, rowsum, K, M, false);
+}
+
+nnhip_status nnhip_ternary_matmul_n_tokens(nnhip_ctx* ctx, size_t count, const void* const* rp,
+                                           const float* const* tau, const float* const* bias, const size_t* N,
+                                           float* const* Y, const int8_t* xi, const float* s, const int32_t* rowsum,
+                                           size_t K, size_t M)
+{
+    return matmul_n_common(ctx, "nnhip_ternary_matmul_n_tokens", count, rp, tau, bias, N, Y, xi, s, rowsum, K, M, true);
 }
 
 nnhip_status nnhip_group_create(nnhip_ctx* ctx, const nnhip_gemv_desc* descs, size_t count,

@@ -84,12 +84,12 @@ class Decoder:
     # whose quantizers absorb the extra reads (C5 step 2.519 -> 2.498 ms). Also available:
     # "fc1", "fc2" (their GEMVs gain 0.4 and 0 us, their quantizers lose 0.9 and 0.1 us).
     prefetch = ("qkv", "o")
-    # the fused step's attention writes its output token-major (nnhip_attention_decode_tokens)
-    attn_tokens = True
-    # the fused step keeps the residual stream x and the mid-block sum r token-major (B, d), so
-    # the RMSNorm quantizers read contiguous rows (nnhip_embedding_gather_tokens,
-    # nnhip_ternary_matmul_add_tokens, nnhip_partial_residual_quant_i8_tokens)
-    res_tokens = True
+    # the fused step keeps its activations token-major, (B, features): q/k/v, the attention
+    # output, the residual stream x and the mid-block sum r (nnhip_ternary_matmul_n_tokens,
+    # nnhip_attention_decode_tokens, nnhip_embedding_gather_tokens,
+    # nnhip_ternary_matmul_add_tokens, nnhip_partial_residual_quant_i8_tokens), so every
+    # per-token quantizer and the attention's query staging read contiguous rows
+    tokens = True
 
     def __init__(self, ctx, cfg: Config, blocks: List[Block], emb, g_final, head: Linear, B: int, caches=None):
         import torch
@@ -115,32 +115,35 @@ class Decoder:
         self.k = torch.empty((Hkv * dk, B), **f32)
         self.v = torch.empty((Hkv * dk, B), **f32)
         self.a = torch.empty((H * dk, B), **f32)
-        # the fused step's attention output, token-major, so that the SubLN quantizer reads each
-        # token as one contiguous row (decode sizes of the one-token quantizer)
-        self._attn_tokens = self.attn_tokens and B <= 64 and H * dk <= 11264
-        self.a_t = torch.empty((B, H * dk), **f32) if self._attn_tokens else None
-        self._res_tokens = self.res_tokens and B <= 16 and d <= 11264
-        self.x_t = torch.empty((B, d), **f32) if self._res_tokens else None
-        self.r_t = torch.empty((B, d), **f32) if self._res_tokens else None
+        # token-major buffers of the fused step (decode sizes of the one-token quantizer)
+        self._tok = self.tokens and B <= 16 and max(d, H * dk) <= 11264
+        if self._tok:
+            self.q_t = torch.empty((B, H * dk), **f32)
+            self.k_t = torch.empty((B, Hkv * dk), **f32)
+            self.v_t = torch.empty((B, Hkv * dk), **f32)
+            self.a_t = torch.empty((B, H * dk), **f32)
+            self.x_t = torch.empty((B, d), **f32)
+            self.r_t = torch.empty((B, d), **f32)
         self.xi = torch.empty((B * kpd(max(d, H * dk, cfg.F)),), dtype=torch.int8, device=dev)
         self.s = torch.empty((B,), **f32)
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
         self.logits = torch.empty((cfg.vocab, B), **f32)
         self.ids = torch.empty((B,), dtype=torch.int32, device=dev)
-        if self._res_tokens and blocks:
-            # the token-major o projection runs on the single-launch decode GEMV only: one call on
-            # the o shape (scratch in, scratch out) tells whether this model's shape is taken
-            o = blocks[0].o
+        if self._tok and blocks:
+            # the token-major q/k/v and o products run on the single-launch decode GEMV only: one
+            # call of each on scratch tells whether this model's shapes are taken
             self.xi.zero_()
             self.s.zero_()
             self.rs.zero_()
+            blk = blocks[0]
             try:
-                ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x_t.zero_(),
-                                       out=self.r_t, tokens=True)
+                self._qkv(blk, True)
+                ctx.ternary_matmul_add(blk.o.rp, blk.o.tau, self.xi, self.s, self.rs, blk.o.N, blk.o.K, B,
+                                       self.x_t.zero_(), out=self.r_t, tokens=True)
             except _pkg().NNHipError as e:
                 if e.status != 5:   # NNHIP_ERR_UNSUPPORTED
                     raise
-                self._res_tokens = False
+                self._tok = False
 
     def _prefill_buffers(self, M: int):
         """Scratch of a prefill over M = B*T token columns (allocated once per M)."""
@@ -212,6 +215,14 @@ class Decoder:
     def _mm(self, lin: Linear, out):
         return self.ctx.ternary_matmul(lin.rp, lin.tau, self.xi, self.s, self.rs, lin.N, lin.K, self.B,
                                        bias=lin.bias, out=out)
+
+    def _qkv(self, blk, tokens: bool):
+        """q, k, v of the quantized input in one launch (token-major rows with tokens)."""
+        outs = (self.q_t, self.k_t, self.v_t) if tokens else (self.q, self.k, self.v)
+        self.ctx.ternary_matmul_n([(blk.q.rp, blk.q.tau, blk.q.bias, blk.q.N, outs[0]),
+                                   (blk.k.rp, blk.k.tau, blk.k.bias, blk.k.N, outs[1]),
+                                   (blk.v.rp, blk.v.tau, blk.v.bias, blk.v.N, outs[2])],
+                                  self.xi, self.s, self.rs, blk.q.K, self.B, tokens=tokens)
 
     def _prefetch(self, kind: str, *lins):
         """Arm the next quantizer call to prefetch these BitLinears' packed weights."""
@@ -307,15 +318,12 @@ class Decoder:
         block_step followed by the next block's first quantizer."""
         cfg, blk, ctx, B, d = self.cfg, self.blocks[i], self.ctx, self.B, self.cfg.d
         outs = (self.xi, self.s, self.rs)
-        ctx.ternary_matmul_n([(blk.q.rp, blk.q.tau, blk.q.bias, blk.q.N, self.q),
-                              (blk.k.rp, blk.k.tau, blk.k.bias, blk.k.N, self.k),
-                              (blk.v.rp, blk.v.tau, blk.v.bias, blk.v.N, self.v)],
-                             self.xi, self.s, self.rs, blk.q.K, B)
+        self._qkv(blk, self._tok)
         kc, vc = self.caches[i]
         o = blk.o
-        if self._attn_tokens:
-            ctx.attention_decode(self.q, self.k, self.v, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc, cfg.scale,
-                                 self.cos, self.sin, out=self.a_t, out_tokens=True)
+        if self._tok:
+            ctx.attention_decode(self.q_t, self.k_t, self.v_t, cfg.H, cfg.Hkv, cfg.dk, pos, len_bound, kc, vc,
+                                 cfg.scale, self.cos, self.sin, out=self.a_t, tokens=True)
             if attn_hook is not None:
                 attn_hook(i, self.a_t.t())
             self._prefetch("o", o)
@@ -328,7 +336,7 @@ class Decoder:
             self._prefetch("o", o)
             self._quant(self.a, blk.g_attn_sub)
         self._prefetch("fc1", blk.fc1)
-        if self._res_tokens:
+        if self._tok:
             ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x_t, bias=o.bias,
                                    out=self.r_t, tokens=True)
             ctx.rmsnorm_quant_i8_tokens(self.r_t, blk.g2, cfg.eps, outs=outs)
@@ -347,7 +355,7 @@ class Decoder:
             self._prefetch("qkv", nb.q, nb.k, nb.v)
         else:
             self._prefetch("qkv", self.head)
-        if self._res_tokens:
+        if self._tok:
             ctx.partial_residual_quant_i8(pf, f2.tau, self.s, self.rs, d, B, self.x_t, res=self.r_t, bias=f2.bias,
                                           gamma=g_next, eps=cfg.eps, outs=outs, tokens=True)
         else:
@@ -358,7 +366,7 @@ class Decoder:
         """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,))."""
         ctx = self.ctx
         fused = self.fused_ok()
-        if fused and self._res_tokens:
+        if fused and self._tok:
             ctx.embedding_gather(self.emb, ids, out=self.x_t, tokens=True)
         else:
             ctx.embedding_gather(self.emb, ids, out=self.x)
@@ -366,7 +374,7 @@ class Decoder:
             if self.blocks:
                 self._prefetch("qkv", self.blocks[0].q, self.blocks[0].k, self.blocks[0].v)
             g0 = self.blocks[0].g1 if self.blocks else self.g_final
-            if self._res_tokens:
+            if self._tok:
                 ctx.rmsnorm_quant_i8_tokens(self.x_t, g0, self.cfg.eps, outs=(self.xi, self.s, self.rs))
             else:
                 self._quant(self.x, g0)

@@ -144,9 +144,9 @@ def test_attention_decode_bad_position(ctx, nnhip):
     (16, 20, 5, 128, [2000 + 7 * b for b in range(16)], 2106, True),
 ])
 def test_attention_decode_tokens(ctx, nnhip, B, H, Hkv, dk, pos, len_bound, rope):
-    """nnhip_attention_decode_tokens: out (B, H*dk) is nnhip_attention_decode's out (H*dk, B)
-    transposed, bit for bit (NaN where the position is out of range), and both append the same
-    rows to the caches."""
+    """nnhip_attention_decode_tokens on q, k, v as token-major rows: out (B, H*dk) is
+    nnhip_attention_decode's out (H*dk, B) on the columns, transposed, bit for bit (NaN where the
+    position is out of range), and both append the same rows to the caches."""
     say(f"attention tokens B={B} H={H} Hkv={Hkv} dk={dk} pos={pos[:4]} len_bound={len_bound}")
     max_len = len_bound + 8
     q = normal((H * dk, B), 91 + B)
@@ -159,8 +159,9 @@ def test_attention_decode_tokens(ctx, nnhip, B, H, Hkv, dk, pos, len_bound, rope
     p = dev(np.array(pos, np.int32))
     kc1, vc1, kc2, vc2 = dev(kc), dev(vc), dev(kc), dev(vc)
     ref = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, p, len_bound, kc1, vc1, 0.1, *tabs))
-    got = host(ctx.attention_decode(dev(q), dev(k), dev(v), H, Hkv, dk, p, len_bound, kc2, vc2, 0.1, *tabs,
-                                    out_tokens=True))
+    tr = lambda a: dev(np.ascontiguousarray(a.T))
+    got = host(ctx.attention_decode(tr(q), tr(k), tr(v), H, Hkv, dk, p, len_bound, kc2, vc2, 0.1, *tabs,
+                                    tokens=True))
     assert got.shape == (B, H * dk)
     assert same_bits(np.ascontiguousarray(got.T), ref)
     assert same_bits(host(kc2), host(kc1)) and same_bits(host(vc2), host(vc1))
