@@ -208,17 +208,49 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
 // Copy the listed activation blocks into LDS (whole block cooperates), then barrier. Unit u
 // (16 bytes) of token row t lands at unit u ^ (t & 7) of its 128-byte group, so the 16 token rows
 // an MFMA operand reads sit in 8 distinct bank groups (without it, rows Kp apart share banks).
+// The 16-wave blocks (up to 152 KiB of activations) copy by buffer->LDS DMA, one KiB of LDS per
+// instruction (lane l fills LDS unit 64q + l from the source unit that belongs there), all of a
+// block's instructions in flight together and one wait at the barrier: copied through
+// registers, each 16-byte load waited for its store, one memory round trip per 16 KiB of the
+// block's staging (M=16 sweep 5460 -> 5570 GB/s). The 4-wave blocks (at most 48 KiB, a few KiB
+// at M=1) keep the register copy, measured alike or slightly faster there.
 template <int kThreads = kBlock>
 __device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__ xs, int n_x)
 {
+    if constexpr (kThreads < 1024)
+    {
+        for (int e = 0; e < n_x; ++e)
+        {
+            const XStage x = xs[e];
+            for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kThreads * 16u)
+            {
+                const uint32_t t = off / x.row, u = (off - t * x.row) >> 4;
+                const uint32_t dst = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
+                *reinterpret_cast<v4i*>(lds + x.lds_off + dst) = *reinterpret_cast<const v4i*>(x.src + off);
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    typedef __attribute__((address_space(3))) void lds_void;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63u;
     for (int e = 0; e < n_x; ++e)
     {
         const XStage x = xs[e];
-        for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kThreads * 16u)
+        const __amdgpu_buffer_rsrc_t rx = rsrc(x.src, x.bytes);
+        const uint32_t upr = x.row >> 4;  // 16-byte units per token row
+        const uint32_t nq = (x.bytes + 1023u) >> 10;
+        for (uint32_t q = (uint32_t)wave; q < nq; q += kThreads / kWave)
         {
-            const uint32_t t = off / x.row, u = (off - t * x.row) >> 4;
-            const uint32_t dst = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
-            *reinterpret_cast<v4i*>(lds + x.lds_off + dst) = *reinterpret_cast<const v4i*>(x.src + off);
+            const uint32_t L = q * 64u + lane;  // LDS unit of this lane
+            if (L * 16u < x.bytes)              // lanes past the block leave the LDS after it alone
+            {
+                const uint32_t t = L / upr, u = L - t * upr;
+                const uint32_t src = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + x.lds_off + q * 1024u), 16, src, 0, 0,
+                                                         0);
+            }
         }
     }
     __syncthreads();
