@@ -66,16 +66,71 @@ __device__ __forceinline__ void read_x_lds(v4i (&x)[4], const Src<kRTW>& s, int 
     for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(s.xl + kt * 256 + (j >> 1) * 128 + ((j & 1) ? s.sw1 : s.sw0));
 }
 
+// Copy the listed activation blocks into LDS (whole block cooperates), then barrier. Unit u
+// (16 bytes) of token row t lands at unit u ^ (t & 7) of its 128-byte group, so the 16 token rows
+// an MFMA operand reads sit in 8 distinct bank groups (without it, rows Kp apart share banks).
+// The 16-wave blocks (up to 152 KiB of activations) copy by buffer->LDS DMA, one KiB of LDS per
+// instruction (lane l fills LDS unit 64q + l from the source unit that belongs there), all of a
+// block's instructions in flight together and one wait at the barrier: copied through
+// registers, each 16-byte load waited for its store, one memory round trip per 16 KiB of the
+// block's staging (M=16 sweep 5460 -> 5570 GB/s). The 4-wave blocks (at most 48 KiB, a few KiB
+// at M=1) keep the register copy, measured alike or slightly faster there.
+template <int kThreads = kBlock>
+__device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__ xs, int n_x)
+{
+    if constexpr (kThreads < 1024)
+    {
+        for (int e = 0; e < n_x; ++e)
+        {
+            const XStage x = xs[e];
+            for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kThreads * 16u)
+            {
+                const uint32_t t = off / x.row, u = (off - t * x.row) >> 4;
+                const uint32_t dst = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
+                *reinterpret_cast<v4i*>(lds + x.lds_off + dst) = *reinterpret_cast<const v4i*>(x.src + off);
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    typedef __attribute__((address_space(3))) void lds_void;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63u;
+    for (int e = 0; e < n_x; ++e)
+    {
+        const XStage x = xs[e];
+        const __amdgpu_buffer_rsrc_t rx = rsrc(x.src, x.bytes);
+        const uint32_t upr = x.row >> 4;  // 16-byte units per token row
+        const uint32_t nq = (x.bytes + 1023u) >> 10;
+        for (uint32_t q = (uint32_t)wave; q < nq; q += kThreads / kWave)
+        {
+            const uint32_t L = q * 64u + lane;  // LDS unit of this lane
+            if (L * 16u < x.bytes)              // lanes past the block leave the LDS after it alone
+            {
+                const uint32_t t = L / upr, u = L - t * upr;
+                const uint32_t src = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + x.lds_off + q * 1024u), 16, src, 0, 0,
+                                                         0);
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Loads are unconditional: a stage past the last k tile reads beyond its resource
 // (num_records = KT KiB), which returns zero words (code 0: no contribution). On the LDS
 // path the activations of stage kt+1 are read from LDS while stage kt computes (LDS reads
 // count on lgkmcnt, so they never wait behind the weight stream).
-template <bool LDS, int kRTW, int kDepth, int KT_FIXED>
-__device__ __forceinline__ void gemv_stream(int KT, const Src<kRTW>& s, Acc (&acc)[kRTW])
+template <bool LDS, int kRTW, int kDepth, int KT_FIXED, int kThreads = kBlock, bool kStage = false>
+__device__ __forceinline__ void gemv_stream(int KT, const Src<kRTW>& s, Acc (&acc)[kRTW], uint8_t* lds = nullptr,
+                                            const XStage* __restrict__ xs = nullptr, int n_x = 0)
 {
     Stage<kRTW> st[kDepth];
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) load_stage<LDS>(st[u], s, u);
+    // kStage: the block's activation staging (and its barrier) runs here, behind the first
+    // weight stages of the wave's first item, so their memory latency overlaps it
+    if constexpr (kStage) stage_x<kThreads>(lds, xs, n_x);
     v4i xc[4], xn[4];
     if constexpr (LDS) read_x_lds(xc, s, 0);
     if constexpr (KT_FIXED > 0)
@@ -128,8 +183,9 @@ __device__ __forceinline__ void gemv_stream(int KT, const Src<kRTW>& s, Acc (&ac
 // Item = row tiles rt0 .. rt0 + kRTW - 1 of problem p. LDS path: the problem's activations
 // were staged at lds + p.xlds; tokens t >= M read token 0's row (their columns are never
 // stored), so no lane needs zeros.
-template <bool LDS, int kRTW, int kDepth>
-__device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lane, const uint8_t* lds)
+template <bool LDS, int kRTW, int kDepth, int kThreads = kBlock, bool kStage = false>
+__device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lane, uint8_t* lds,
+                                          const XStage* __restrict__ xs = nullptr, int n_x = 0)
 {
     const int g = lane >> 4, t = lane & 15;
     const int RT = (p.N + 15) / 16;
@@ -180,11 +236,11 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     for (int r = 0; r < kRTW; ++r) acc[r].a0 = acc[r].a1 = acc[r].a2 = acc[r].a3 = v4i{0, 0, 0, 0};
     switch (p.KT)
     {
-    case 4: gemv_stream<LDS, kRTW, kDepth, 4>(4, s, acc); break;
-    case 10: gemv_stream<LDS, kRTW, kDepth, 10>(10, s, acc); break;
-    case 16: gemv_stream<LDS, kRTW, kDepth, 16>(16, s, acc); break;
-    case 27: gemv_stream<LDS, kRTW, kDepth, 27>(27, s, acc); break;
-    default: gemv_stream<LDS, kRTW, kDepth, 0>(p.KT, s, acc); break;
+    case 4: gemv_stream<LDS, kRTW, kDepth, 4, kThreads, kStage>(4, s, acc, lds, xs, n_x); break;
+    case 10: gemv_stream<LDS, kRTW, kDepth, 10, kThreads, kStage>(10, s, acc, lds, xs, n_x); break;
+    case 16: gemv_stream<LDS, kRTW, kDepth, 16, kThreads, kStage>(16, s, acc, lds, xs, n_x); break;
+    case 27: gemv_stream<LDS, kRTW, kDepth, 27, kThreads, kStage>(27, s, acc, lds, xs, n_x); break;
+    default: gemv_stream<LDS, kRTW, kDepth, 0, kThreads, kStage>(p.KT, s, acc, lds, xs, n_x); break;
     }
 
     // masked lanes (token >= M, row >= N) store out of range: dropped by the buffer unit
@@ -203,57 +259,6 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
         }
     }
-}
-
-// Copy the listed activation blocks into LDS (whole block cooperates), then barrier. Unit u
-// (16 bytes) of token row t lands at unit u ^ (t & 7) of its 128-byte group, so the 16 token rows
-// an MFMA operand reads sit in 8 distinct bank groups (without it, rows Kp apart share banks).
-// The 16-wave blocks (up to 152 KiB of activations) copy by buffer->LDS DMA, one KiB of LDS per
-// instruction (lane l fills LDS unit 64q + l from the source unit that belongs there), all of a
-// block's instructions in flight together and one wait at the barrier: copied through
-// registers, each 16-byte load waited for its store, one memory round trip per 16 KiB of the
-// block's staging (M=16 sweep 5460 -> 5570 GB/s). The 4-wave blocks (at most 48 KiB, a few KiB
-// at M=1) keep the register copy, measured alike or slightly faster there.
-template <int kThreads = kBlock>
-__device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__ xs, int n_x)
-{
-    if constexpr (kThreads < 1024)
-    {
-        for (int e = 0; e < n_x; ++e)
-        {
-            const XStage x = xs[e];
-            for (uint32_t off = threadIdx.x * 16u; off < x.bytes; off += kThreads * 16u)
-            {
-                const uint32_t t = off / x.row, u = (off - t * x.row) >> 4;
-                const uint32_t dst = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
-                *reinterpret_cast<v4i*>(lds + x.lds_off + dst) = *reinterpret_cast<const v4i*>(x.src + off);
-            }
-        }
-        __syncthreads();
-        return;
-    }
-    typedef __attribute__((address_space(3))) void lds_void;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const uint32_t lane = threadIdx.x & 63u;
-    for (int e = 0; e < n_x; ++e)
-    {
-        const XStage x = xs[e];
-        const __amdgpu_buffer_rsrc_t rx = rsrc(x.src, x.bytes);
-        const uint32_t upr = x.row >> 4;  // 16-byte units per token row
-        const uint32_t nq = (x.bytes + 1023u) >> 10;
-        for (uint32_t q = (uint32_t)wave; q < nq; q += kThreads / kWave)
-        {
-            const uint32_t L = q * 64u + lane;  // LDS unit of this lane
-            if (L * 16u < x.bytes)              // lanes past the block leave the LDS after it alone
-            {
-                const uint32_t t = L / upr, u = L - t * upr;
-                const uint32_t src = t * x.row + (((u & ~7u) | ((u ^ t) & 7u)) << 4);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(lds + x.lds_off + q * 1024u), 16, src, 0, 0,
-                                                         0);
-            }
-        }
-    }
-    __syncthreads();
 }
 
 // Single problem: static assignment of items to waves.
@@ -281,12 +286,28 @@ __global__ __launch_bounds__(kThreads) void k_gemv_grouped(const GemvProblem* __
                                                            int n_x)
 {
     extern __shared__ __align__(16) uint8_t lds[];
-    if constexpr (LDS) stage_x<kThreads>(lds, xs, n_x);
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6));
-    if (w >= n_waves) return;
-    const uint32_t b = wave_start[w], e = wave_start[w + 1];
-    for (uint32_t i = b; i < e; ++i)
+    const uint32_t b = w < n_waves ? wave_start[w] : 0u, e = w < n_waves ? wave_start[w + 1] : 0u;
+    // 16-wave blocks (DMA staging of up to 152 KiB): every wave joins the block's staging barrier
+    // once, inside its first item after that item's first weight loads are issued (or alone when
+    // it has no items), so the weights' memory latency overlaps the staging (M=16 sweep +1 %).
+    // 4-wave blocks stage first: there the register copy's waits also waited for the weights and
+    // left the pipeline empty after the barrier (M=1 sweep -3 % with the overlap).
+    constexpr bool kOverlap = LDS && kThreads >= 1024;
+    if constexpr (LDS && !kOverlap) stage_x<kThreads>(lds, xs, n_x);
+    if constexpr (kOverlap)
+    {
+        if (b == e)
+        {
+            stage_x<kThreads>(lds, xs, n_x);
+            return;
+        }
+        const uint32_t it = wave_items[b];
+        const GemvProblem p = probs[it >> 20];
+        gemv_item<LDS, kRTW, kDepth, kThreads, true>(p, (int)(it & 0xFFFFFu), lane, lds, xs, n_x);
+    }
+    for (uint32_t i = kOverlap ? b + 1 : b; i < e; ++i)
     {
         const uint32_t it = wave_items[i];
         const GemvProblem p = probs[it >> 20];
