@@ -399,9 +399,8 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     pos = torch.full((B,), ctx_len, device="cuda", dtype=torch.int32)
 
     def one_step():
-        dec.step(ids, pos, max_len)
-        ids.copy_(dec.ids)
-        pos.add_(1)
+        # the greedy ids land in ids and every position advances, in the step's last launch
+        dec.step(ids, pos, max_len, advance=True)
 
     one_step()                           # warm-up: context scratch grows outside the capture
     torch.cuda.synchronize()

@@ -590,6 +590,14 @@ nnhip_status nnhip_embedding_gather_tokens(nnhip_ctx* ctx, const float* table, c
  * merges two nearly equal logits). */
 nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids);
 
+/* nnhip_argmax_cols on token-major logits (B, V) (row b = sequence b's logits, read as one
+ * contiguous row): the same ids as on the transpose. When pos != NULL, pos[b] += 1 for every
+ * sequence after its choice, the position advance of the generation loop (GPTModel::generate,
+ * compute_layer_gpt.hpp:800-849: the chosen token is fed back at the next position), so that a
+ * captured decode step needs no separate position update; ids may then be the step's own input
+ * ids (the embedding gather that read them ran earlier on the stream). */
+nnhip_status nnhip_argmax_rows(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids, int32_t* pos);
+
 /* Y = res + the gated block of nnhip_ffn_glu_i8 on X (res (d, M) f32, must not alias Y): the second
  * residual add of GPTBlock::forward_step in fc2's launch on the decode path. Same bits as
  * nnhip_ffn_glu_i8 then nnhip_add(res, Y) (compute_layer_gpt.hpp:212-218). */

@@ -144,6 +144,7 @@ SIGNATURES = {
     "nnhip_embedding_gather": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_embedding_gather_tokens": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_argmax_cols": (_st, [_vp, _vp, _sz, _sz, _vp]),
+    "nnhip_argmax_rows": (_st, [_vp, _vp, _sz, _sz, _vp, _vp]),
 }
 
 ACT_SWIGLU, ACT_RELU2GLU = 0, 1
@@ -766,6 +767,21 @@ class Context:
         self._bind_stream()
         _check(lib().nnhip_argmax_cols(self.h, self._dev(logits, torch.float32, "logits"), V, B,
                                        self._dev(out, torch.int32, "out")), "nnhip_argmax_cols")
+        return out
+
+    def argmax_rows(self, logits, out=None, pos=None):
+        """token-major logits (B, V) -> (B) int32 greedy token ids; pos (B) int32, when given, is
+        advanced by one in the same launch."""
+        torch = self._torch
+        B, V = logits.shape
+        if out is None:
+            out = self._empty((B,), torch.int32)
+        if pos is not None and tuple(pos.shape) != (B,):
+            raise NNHipError(1, f"pos must have shape ({B},)")
+        self._bind_stream()
+        _check(lib().nnhip_argmax_rows(self.h, self._dev(logits, torch.float32, "logits"), V, B,
+                                       self._dev(out, torch.int32, "out"), self._dev(pos, torch.int32, "pos")),
+               "nnhip_argmax_rows")
         return out
 
     # -- gated feed-forward block

@@ -307,6 +307,7 @@ hipError_t launch_attn_prefill(hipStream_t st, const float* q, const float* kc, 
                                size_t max_len, float scale, float* out);
 hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B, bool tm,
                         float* out);
-hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids);
+hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids, bool rows = false,
+                         int32_t* pos = nullptr);
 
 }  // namespace nnhip

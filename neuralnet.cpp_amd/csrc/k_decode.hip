@@ -604,7 +604,11 @@ __global__ __launch_bounds__(kSmallBlock) void k_embed(const float* __restrict__
 constexpr int kArgThreads = 1024;
 constexpr int kArgBatch = 16;  // loads in flight per thread (V <= 16384 in one batch)
 
-__global__ __launch_bounds__(kArgThreads) void k_argmax(const float* __restrict__ L, int V, int B, int32_t* ids)
+// kRows: logits are token-major (B, V), row b contiguous; otherwise column b of (V, B). pos, when
+// given, is advanced by one for every sequence after its choice (the next decode position).
+template <bool kRows>
+__global__ __launch_bounds__(kArgThreads) void k_argmax(const float* __restrict__ L, int V, int B, int32_t* ids,
+                                                        int32_t* pos)
 {
     __shared__ float sv[kArgThreads / kWave];
     __shared__ int si[kArgThreads / kWave];
@@ -620,7 +624,7 @@ __global__ __launch_bounds__(kArgThreads) void k_argmax(const float* __restrict_
         for (int u = 0; u < kArgBatch; ++u)
         {
             const int v = v0 + u * kArgThreads;
-            x[u] = v < V ? L[(size_t)v * B + b] : __builtin_nanf("");
+            x[u] = v < V ? L[kRows ? (size_t)b * V + v : (size_t)v * B + b] : __builtin_nanf("");
         }
 #pragma unroll
         for (int u = 0; u < kArgBatch; ++u)
@@ -655,8 +659,9 @@ __global__ __launch_bounds__(kArgThreads) void k_argmax(const float* __restrict_
                 bi = si[w];
             }
         // the reference's loop starts from l[0]: a NaN there is never replaced
-        const float l0 = L[b];
+        const float l0 = L[kRows ? (size_t)b * V : (size_t)b];
         ids[b] = (l0 != l0 || bi < 0) ? 0 : bi;
+        if (pos) pos[b] = pos[b] + 1;
     }
 }
 
@@ -709,9 +714,12 @@ hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, 
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids)
+hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids, bool rows, int32_t* pos)
 {
-    k_argmax<<<dim3((unsigned)B), kArgThreads, 0, st>>>(L, (int)V, (int)B, ids);
+    if (rows)
+        k_argmax<true><<<dim3((unsigned)B), kArgThreads, 0, st>>>(L, (int)V, (int)B, ids, pos);
+    else
+        k_argmax<false><<<dim3((unsigned)B), kArgThreads, 0, st>>>(L, (int)V, (int)B, ids, pos);
     return hipGetLastError();
 }
 

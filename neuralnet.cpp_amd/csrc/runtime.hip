@@ -1826,4 +1826,15 @@ nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, si
     return NNHIP_OK;
 }
 
+nnhip_status nnhip_argmax_rows(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids, int32_t* pos)
+{
+    const char* fn = "nnhip_argmax_rows";
+    NNHIP_CHECK_CTX(fn);
+    if (B == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(logits && ids, fn, "null pointer");
+    NNHIP_REQUIRE(V >= 1 && V <= kMaxDim && B <= kMaxDim && mul_ok(V, B), fn, "size out of range");
+    NNHIP_LAUNCH(fn, launch_argmax(ctx->stream, logits, V, B, ids, true, pos));
+    return NNHIP_OK;
+}
+
 }  // extern "C"

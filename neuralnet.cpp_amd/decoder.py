@@ -127,7 +127,9 @@ class Decoder:
         self.xi = torch.empty((B * kpd(max(d, H * dk, cfg.F)),), dtype=torch.int8, device=dev)
         self.s = torch.empty((B,), **f32)
         self.rs = torch.empty((B,), dtype=torch.int32, device=dev)
-        self.logits = torch.empty((cfg.vocab, B), **f32)
+        self._logits_cols = torch.empty((cfg.vocab, B), **f32)
+        self._logits = self._logits_cols
+        self.logits_t = None    # token-major (B, vocab) logits of the step, when the head takes them
         self.ids = torch.empty((B,), dtype=torch.int32, device=dev)
         if self._tok and blocks:
             # the token-major q/k/v and o products run on the single-launch decode GEMV only: one
@@ -144,6 +146,23 @@ class Decoder:
                 if e.status != 5:   # NNHIP_ERR_UNSUPPORTED
                     raise
                 self._tok = False
+        if self._tok:
+            # the head with token-major logits, so that the greedy choice reads each sequence's
+            # logits as one row (and advances the positions in the same launch)
+            lt = torch.empty((B, cfg.vocab), **f32)
+            try:
+                ctx.ternary_matmul_n([(head.rp, head.tau, head.bias, head.N, lt)], self.xi, self.s, self.rs, head.K,
+                                     B, tokens=True)
+                self.logits_t = lt
+            except _pkg().NNHipError as e:
+                if e.status != 5:
+                    raise
+
+    @property
+    def logits(self):
+        """The last logits written (vocab, B): by prefill(), or by step() (a transposed view of the
+        token-major logits when the head produces those)."""
+        return self._logits
 
     def _prefill_buffers(self, M: int):
         """Scratch of a prefill over M = B*T token columns (allocated once per M)."""
@@ -208,9 +227,10 @@ class Decoder:
                 hook(i, "x", x)
         ctx.copy_columns(x, T - 1, T, B, out=self.x)
         self._quant(self.x, self.g_final)
-        self._mm(self.head, self.logits)
-        ctx.argmax_cols(self.logits, out=self.ids)
-        return self.logits, self.ids
+        self._mm(self.head, self._logits_cols)
+        ctx.argmax_cols(self._logits_cols, out=self.ids)
+        self._logits = self._logits_cols
+        return self._logits, self.ids
 
     def _mm(self, lin: Linear, out):
         return self.ctx.ternary_matmul(lin.rp, lin.tau, self.xi, self.s, self.rs, lin.N, lin.K, self.B,
@@ -362,8 +382,10 @@ class Decoder:
             ctx.partial_residual_quant_i8(pf, f2.tau, self.s, self.rs, d, B, self.x, res=self.r, bias=f2.bias,
                                           gamma=g_next, eps=cfg.eps, outs=outs)
 
-    def step(self, ids, pos, len_bound: int, attn_hook=None):
-        """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,))."""
+    def step(self, ids, pos, len_bound: int, attn_hook=None, advance: bool = False):
+        """ids / pos: (B,) int32 device tensors. Returns (logits (vocab, B), greedy ids (B,)).
+        advance: the greedy ids are written into ids itself and every pos is advanced by one, so
+        that the next call continues the generation (a captured step then replays as is)."""
         ctx = self.ctx
         fused = self.fused_ok()
         if fused and self._tok:
@@ -384,9 +406,20 @@ class Decoder:
             for i in range(len(self.blocks)):
                 self.block_step(i, pos, len_bound, attn_hook)
             self._quant(self.x, self.g_final)
-        self._mm(self.head, self.logits)
-        ctx.argmax_cols(self.logits, out=self.ids)
-        return self.logits, self.ids
+        out_ids = ids if advance else self.ids
+        if fused and self.logits_t is not None:
+            h = self.head
+            ctx.ternary_matmul_n([(h.rp, h.tau, h.bias, h.N, self.logits_t)], self.xi, self.s, self.rs, h.K, self.B,
+                                 tokens=True)
+            ctx.argmax_rows(self.logits_t, out=out_ids, pos=pos if advance else None)
+            self._logits = self.logits_t.t()
+            return self._logits, out_ids
+        self._mm(self.head, self._logits_cols)
+        ctx.argmax_cols(self._logits_cols, out=out_ids)
+        if advance:
+            pos.add_(1)
+        self._logits = self._logits_cols
+        return self._logits, out_ids
 
 
 def _pkg():

@@ -217,6 +217,35 @@ def test_add_gather_argmax_bitexact(ctx, orc):
     assert host(ctx.argmax_cols(dev(L))).tolist() == orc.argmax_cols(L).tolist() == [5, 39999, 0, 16385]
 
 
+@pytest.mark.parametrize("V,B", [(10000, 16), (40000, 4), (97, 3), (1, 2)])
+def test_argmax_rows_and_position_advance(ctx, orc, V, B):
+    """nnhip_argmax_rows on token-major logits (B, V): the oracle's greedy ids of the transpose
+    (ties, NaN at index 0 and elsewhere, all-NaN, +-inf, maxima in different load batches); with
+    pos the positions advance by one in the same launch, without it they are left alone."""
+    import torch
+    say(f"argmax_rows V={V} B={B}")
+    L = uniform((V, B), 26 + V)
+    L[:, 0] = 0.5                                  # all ties
+    if B > 1:
+        L[0, 1] = np.nan                           # NaN at index 0 keeps index 0
+    if B > 2 and V > 12:
+        L[7, 2] = np.nan
+        L[11, 2] = L[12, 2] = np.inf
+    if B > 3:
+        L[:, 3] = np.nan
+    if V > 20000 and B > 3:
+        L[5, 3] = L[20000, 3] = 3.0               # equal maxima in different load batches
+    want = orc.argmax_cols(L).tolist()
+    Lt = dev(np.ascontiguousarray(L.T))
+    assert host(ctx.argmax_rows(Lt)).tolist() == want == host(ctx.argmax_cols(dev(L))).tolist()
+    p0 = np.arange(B, dtype=np.int32) * 7 + 3
+    pos = dev(p0)
+    ids = dev(np.full(B, -1, np.int32))
+    ctx.argmax_rows(Lt, out=ids, pos=pos)
+    torch.cuda.synchronize()
+    assert host(ids).tolist() == want and host(pos).tolist() == (p0 + 1).tolist()
+
+
 # ---------------------------------------------------------------- the whole decode step
 
 def _linear(ctx, orc, N, K, seed, bias=True):

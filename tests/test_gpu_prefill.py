@@ -199,13 +199,14 @@ def _gpu_model(ctx, nnhip, cfg, L, B, seed, subln=True, bias=False):
     return dec, host_blocks, host(emb), host(gfin), (hostlin(ht)[0], hostlin(ht)[1], None)
 
 
-def _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, samp, steps, seed):
+def _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, samp, steps, seed, advance=False):
     """Decoder.prefill of T prompt tokens for B sequences, then `steps` decode steps, against the
     oracle chain on the sampled sequences: per block q / k / v and the block output bit for bit,
     the attention within tolerance (the GPU's attention output is fed to the oracle's next stage, so
     the int8 stages stay comparable bit for bit), the caches bit for bit, then the last tokens'
     logits and greedy ids; the decode steps continue from the prefilled caches (GPTBlock::
-    forward_step order, compute_layer_gpt.hpp:201-219)."""
+    forward_step order, compute_layer_gpt.hpp:201-219). advance: the last step runs with
+    advance=True and must leave its greedy ids in its own input ids and every position one ahead."""
     import torch
     rng = np.random.default_rng(seed)
     ids = rng.integers(0, cfg.vocab, size=(B, T)).astype(np.int32)
@@ -253,9 +254,14 @@ def _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, samp, steps, s
         pos = np.full(B, T + step, np.int32)
         say(f"prefill chain: decode step {step}")
         attn = {}
-        logits_d, next_d = dec.step(dev(cur), dev(pos), T + step + 1,
-                                    attn_hook=lambda i, a: attn.__setitem__(i, host(a[:, samp])))
+        adv = advance and step == steps - 1
+        cur_d, pos_d = dev(cur), dev(pos)
+        logits_d, next_d = dec.step(cur_d, pos_d, T + step + 1,
+                                    attn_hook=lambda i, a: attn.__setitem__(i, host(a[:, samp])), advance=adv)
         logits, nxt = host(logits_d), host(next_d)
+        if adv:
+            assert next_d.data_ptr() == cur_d.data_ptr()
+            assert host(pos_d).tolist() == (pos + 1).tolist()
         x = orc.embedding_gather(emb, cur[samp])
         for l, b in enumerate(hb):
             q = _orc_bitlinear(orc, x, b["q"], b["g1"], cfg.eps)
@@ -282,7 +288,7 @@ def test_decoder_prefill_chain_small(ctx, orc, nnhip, subln, bias, act):
     cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=64, act=act, eps=1e-5)
     B, T = 3, 45
     dec, hb, emb, gfin, head = _gpu_model(ctx, nnhip, cfg, 2, B, 0x9F + act, subln=subln, bias=bias)
-    _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, [0, 1, 2], 2, 11 + act)
+    _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, [0, 1, 2], 2, 11 + act, advance=True)
 
 
 def test_decoder_prefill_chain_c5(ctx, orc, nnhip):
@@ -295,4 +301,5 @@ def test_decoder_prefill_chain_c5(ctx, orc, nnhip):
     B, T = 16, 16
     say("building the 30-layer C5 model")
     dec, hb, emb, gfin, head = _gpu_model(ctx, nnhip, cfg, 30, B, 0xC5C5)
-    _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, [0, 13], 2, 5)
+    assert dec.logits_t is not None, "the C5 head should produce token-major logits"
+    _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, [0, 13], 2, 5, advance=True)
