@@ -279,6 +279,9 @@ class Decoder:
 
     # split-k slices of fc2 on the fused step path
     slices_fc2 = 4
+    # the o projection as split-k slice sums whose per-token epilogue kernel also adds the
+    # residual and quantizes for fc1 (0: the whole-K GEMV with the residual, then the quantizer)
+    slices_o = 4
 
     def fused_ok(self) -> bool:
         """The fused step path (fc2 split-k, its epilogue, the residual add and the next block's
@@ -356,7 +359,13 @@ class Decoder:
             self._prefetch("o", o)
             self._quant(self.a, blk.g_attn_sub)
         self._prefetch("fc1", blk.fc1)
-        if self._tok:
+        part, h = self._scratch()
+        if self._tok and self.slices_o > 0:
+            S = self._slices(o.K, min(self.slices_o, self.slices_fc2))
+            po = ctx.ternary_matmul_partial(o.rp, self.xi, o.N, o.K, B, S, out=part[:S])
+            ctx.partial_residual_quant_i8(po, o.tau, self.s, self.rs, d, B, self.r_t, res=self.x_t, bias=o.bias,
+                                          gamma=blk.g2, eps=cfg.eps, outs=outs, tokens=True)
+        elif self._tok:
             ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x_t, bias=o.bias,
                                    out=self.r_t, tokens=True)
             ctx.rmsnorm_quant_i8_tokens(self.r_t, blk.g2, cfg.eps, outs=outs)
@@ -364,7 +373,6 @@ class Decoder:
             ctx.ternary_matmul_add(o.rp, o.tau, self.xi, self.s, self.rs, o.N, o.K, B, self.x, bias=o.bias,
                                    out=self.r)
             self._quant(self.r, blk.g2)
-        part, h = self._scratch()
         self._ffn_gate_quant(blk, h)
         f2 = blk.fc2
         S = self._slices(f2.K, self.slices_fc2)
