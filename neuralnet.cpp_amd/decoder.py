@@ -80,10 +80,11 @@ class Decoder:
 
     # BitLinears whose packed weights the per-token quantizer before them also reads
     # (nnhip_ctx_prefetch_next), so that their GEMV finds them in the memory-side cache: q/k/v
-    # (in the fc2 epilogue kernel of the block before) and o (in the attention SubLN quantizer),
-    # whose quantizers absorb the extra reads (C5 step 2.519 -> 2.498 ms). Also available:
-    # "fc1", "fc2" (their GEMVs gain 0.4 and 0 us, their quantizers lose 0.9 and 0.1 us).
-    prefetch = ("qkv", "o")
+    # (in the fc2 epilogue kernel of the block before), o (in the attention SubLN quantizer) and
+    # fc2 (in the FFN SubLN quantizer), whose quantizers absorb the extra reads (C5 step
+    # 2.519 -> 2.498 ms for q/k/v and o; 2.340 -> 2.332 ms for fc2's split-k slices). Also
+    # available: "fc1" (in the o epilogue kernel: 2.340 -> 2.350 ms, so off).
+    prefetch = ("qkv", "o", "fc2")
     # the fused step keeps its activations token-major, (B, features): q/k/v, the attention
     # output, the residual stream x and the mid-block sum r (nnhip_ternary_matmul_n_tokens,
     # nnhip_attention_decode_tokens, nnhip_embedding_gather_tokens,
