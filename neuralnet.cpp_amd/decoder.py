@@ -304,7 +304,8 @@ class Decoder:
         import torch
         if getattr(self, "_part_buf", None) is None:
             dev = f"cuda:{self.ctx.device}"
-            self._part_buf = torch.empty((self.slices_fc2, self.B, self.cfg.d), dtype=torch.int32, device=dev)
+            S = max(self.slices_fc2, self.slices_o)
+            self._part_buf = torch.empty((S, self.B, self.cfg.d), dtype=torch.int32, device=dev)
             self._h_buf = torch.empty((self.cfg.F, self.B), dtype=torch.float32, device=dev)
         return self._part_buf, self._h_buf
 
@@ -362,7 +363,7 @@ class Decoder:
         self._prefetch("fc1", blk.fc1)
         part, h = self._scratch()
         if self._tok and self.slices_o > 0:
-            S = self._slices(o.K, min(self.slices_o, self.slices_fc2))
+            S = self._slices(o.K, self.slices_o)
             po = ctx.ternary_matmul_partial(o.rp, self.xi, o.N, o.K, B, S, out=part[:S])
             ctx.partial_residual_quant_i8(po, o.tau, self.s, self.rs, d, B, self.r_t, res=self.x_t, bias=o.bias,
                                           gamma=blk.g2, eps=cfg.eps, outs=outs, tokens=True)
