@@ -103,8 +103,8 @@ nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream);
 nnhip_status nnhip_ctx_set_gemm_tile(nnhip_ctx* ctx, int tile);
 
 /* A performance hint with no counterpart in the reference: the next call on this context of
- * nnhip_act_quant_i8 / nnhip_rmsnorm_quant_i8 (at most 64 tokens), nnhip_rmsnorm_quant_i8_tokens
- * or nnhip_partial_residual_quant_i8 also reads the given device ranges (count <= 4, each
+ * nnhip_act_quant_i8 / nnhip_rmsnorm_quant_i8 (at most 64 tokens), nnhip_rmsnorm_quant_i8_tokens,
+ * nnhip_embedding_rmsnorm_quant_i8_tokens or nnhip_partial_residual_quant_i8 also reads the given device ranges (count <= 4, each
  * 16-byte aligned; whole 16-byte units inside each range, at most 64 MiB in all) in extra
  * blocks, so that the kernel after it, which reads the same bytes (a decoder's next BitLinear
  * weights), finds them in the GPU's memory-side cache. That call takes the ranges whether or
@@ -464,6 +464,17 @@ nnhip_status nnhip_ternary_matmul_glu_tokens(nnhip_ctx* ctx, const void* rp, con
  * compute_layer_bitlinear.hpp:443-448) in the decode step. */
 nnhip_status nnhip_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t K,
                                            size_t M, int8_t* xi, float* s, int32_t* rowsum);
+
+/* nnhip_embedding_gather_tokens followed by nnhip_rmsnorm_quant_i8_tokens on its rows, in one
+ * launch: x (B, d) = rows ids[b] of table (V, d) (NaN rows for ids outside [0, V)), and xi / s /
+ * rowsum their [RMSNorm (gamma != NULL, eps) ->] absmax int8 quantization, the same bits as the
+ * two calls. 1 <= B <= 64 and d <= 11264 (NNHIP_ERR_UNSUPPORTED otherwise); takes the
+ * nnhip_ctx_prefetch_next ranges like the quantizer. The first steps of GPTModel::forward_step
+ * (token embedding, compute_layer_gpt.hpp:697-702) and the first block's RMSNorm1 ->
+ * quantize_i8 (compute_layer_gpt.hpp:203; compute_layer_bitlinear.hpp:443-448). */
+nnhip_status nnhip_embedding_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* table, const int32_t* ids,
+                                                     size_t V, size_t d, size_t B, const float* gamma, float eps,
+                                                     float* x, int8_t* xi, float* s, int32_t* rowsum);
 
 /* Context scratch the block below uses (grown on demand, kept by the context). */
 size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M);

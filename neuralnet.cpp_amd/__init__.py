@@ -128,6 +128,7 @@ SIGNATURES = {
     "nnhip_ternary_matmul_glu_tokens": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_int,
                                               _vp]),
     "nnhip_rmsnorm_quant_i8_tokens": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _vp, _vp, _vp]),
+    "nnhip_embedding_rmsnorm_quant_i8_tokens": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _f, _vp, _vp, _vp, _vp]),
     "nnhip_ffn_glu_workspace_bytes": (_sz, [_sz, _sz, _sz]),
     "nnhip_ffn_glu_i8": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp, _f, _vp, _vp,
                                _vp, _vp]),
@@ -837,6 +838,26 @@ class Context:
                                                    self._dev(rs, torch.int32, "rowsum")),
                "nnhip_rmsnorm_quant_i8_tokens")
         return outs
+
+    def embedding_rmsnorm_quant_i8_tokens(self, table, ids, gamma, eps: float, out=None, outs=None):
+        """Rows ids[b] of table (V, d) into out (B, d) and their [RMSNorm (gamma, or None) ->] absmax
+        -> int8 in the same launch; returns (out, (xi, s, rowsum))."""
+        torch = self._torch
+        V, d = table.shape
+        B = ids.shape[0]
+        if out is None:
+            out = self._empty((B, d), torch.float32)
+        if outs is None:
+            outs = (self._empty((B, kp(d)), torch.int8), self._empty((B,), torch.float32),
+                    self._empty((B,), torch.int32))
+        xi, s, rs = outs
+        self._bind_stream()
+        _check(lib().nnhip_embedding_rmsnorm_quant_i8_tokens(
+            self.h, self._dev(table, torch.float32, "table"), self._dev(ids, torch.int32, "ids"), V, d, B,
+            self._dev(gamma, torch.float32, "gamma"), eps, self._dev(out, torch.float32, "out"),
+            self._dev(xi, torch.int8, "xi"), self._dev(s, torch.float32, "s"), self._dev(rs, torch.int32, "rowsum")),
+            "nnhip_embedding_rmsnorm_quant_i8_tokens")
+        return out, outs
 
     def ternary_matmul_glu(self, rp, tau, xi, s, rowsum, F: int, K: int, M: int, act: int = ACT_SWIGLU,
                            bias=None, out=None):

@@ -214,6 +214,9 @@ hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* 
 bool token_quant_tm_ok(size_t K, size_t M);
 hipError_t launch_token_quant_tm(hipStream_t st, const float* X, const float* gamma, float eps, size_t K, size_t M,
                                  int8_t* xi, float* s, int32_t* rowsum, const Prefetch* pf = nullptr);
+hipError_t launch_embed_token_quant(hipStream_t st, const float* table, const int32_t* ids, size_t V, const float* gamma,
+                                   float eps, size_t K, size_t M, float* xout, int8_t* xi, float* s, int32_t* rowsum,
+                                   const Prefetch* pf);
 hipError_t launch_act_quant(hipStream_t st, const float* X, const float* gamma, bool norm, float eps,
                             size_t K, size_t M, int8_t* xi, float* s, int32_t* rowsum,
                             uint32_t* xq_ref, const Prefetch* pf = nullptr);

@@ -598,11 +598,26 @@ __global__ __launch_bounds__(kOneThreads) void k_token_one(TokArgs a, const floa
     }
     const int t = threadIdx.x, m = blockIdx.x;
     float x[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
+    if (a.gids)
     {
-        const int f = t + kParts * r;
-        x[r] = f < a.K ? a.X[a.xtm ? (size_t)m * a.K + f : (size_t)f * a.M + m] : 0.0f;
+        const int id = a.gids[m];
+        const bool ok = id >= 0 && id < a.gV;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = t + kParts * r;
+            x[r] = f < a.K ? (ok ? a.X[(size_t)id * a.K + f] : __builtin_nanf("")) : 0.0f;
+            if (f < a.K) a.gout[(size_t)m * a.K + f] = x[r];
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = t + kParts * r;
+            x[r] = f < a.K ? a.X[a.xtm ? (size_t)m * a.K + f : (size_t)f * a.M + m] : 0.0f;
+        }
     }
     one_token_finish<R>(x, a, gamma, sh);
 }
@@ -937,6 +952,23 @@ hipError_t launch_token_quant_tm(hipStream_t st, const float* X, const float* ga
     TokArgs a{X, gamma != nullptr, eps, 1.0f / (float)K, (int)K, (int)M, (int)round_up(K, kTileK), 0, xi, s, rowsum,
               nullptr, nullptr, 1};
     if (pf) a.pf = *pf;
+    if (!launch_one_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, gamma))
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_token_quant(hipStream_t st, const float* table, const int32_t* ids, size_t V, const float* gamma,
+                                   float eps, size_t K, size_t M, float* xout, int8_t* xi, float* s, int32_t* rowsum,
+                                   const Prefetch* pf)
+{
+    if (!token_quant_tm_ok(K, M)) return hipErrorInvalidValue;
+    const int rounds = (int)ceil_div(K, (size_t)512);
+    TokArgs a{table, gamma != nullptr, eps, 1.0f / (float)K, (int)K, (int)M, (int)round_up(K, kTileK), 0, xi, s, rowsum,
+              nullptr, nullptr, 1};
+    if (pf) a.pf = *pf;
+    a.gids = ids;
+    a.gV = (int)V;
+    a.gout = xout;
     if (!launch_one_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, gamma))
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -1541,6 +1541,23 @@ nnhip_status nnhip_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* X, const
     return NNHIP_OK;
 }
 
+nnhip_status nnhip_embedding_rmsnorm_quant_i8_tokens(nnhip_ctx* ctx, const float* table, const int32_t* ids,
+                                                     size_t V, size_t d, size_t B, const float* gamma, float eps,
+                                                     float* x, int8_t* xi, float* s, int32_t* rowsum)
+{
+    const char* fn = "nnhip_embedding_rmsnorm_quant_i8_tokens";
+    NNHIP_CHECK_CTX(fn);
+    const Prefetch pf = take_prefetch(ctx);
+    if (B == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(table && ids && x && xi && s && rowsum, fn, "null pointer");
+    NNHIP_REQUIRE(aligned16(xi), fn, "xi must be 16-byte aligned");
+    NNHIP_REQUIRE(V >= 1 && V <= kMaxDim && mul_ok(V, d) && V * d < 0x7FFFFFFFull, fn, "table must be below 2^31 elements");
+    if (!token_quant_tm_ok(d, B))
+        return fail(NNHIP_ERR_UNSUPPORTED, fn, "decode sizes only (1 <= B <= 64, 1 <= d <= 11264)");
+    NNHIP_LAUNCH(fn, launch_embed_token_quant(ctx->stream, table, ids, V, gamma, eps, d, B, x, xi, s, rowsum, &pf));
+    return NNHIP_OK;
+}
+
 size_t nnhip_ffn_glu_workspace_bytes(size_t d, size_t F, size_t M)
 {
     size_t b = round_up(nnhip_act_i8_bytes(d, M), 256) + round_up(nnhip_act_i8_bytes(F, M), 256);

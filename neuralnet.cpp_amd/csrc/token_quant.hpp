@@ -169,6 +169,11 @@ struct TokArgs
     float* fout;
     int xtm;  // one-token kernel: X is token-major (M, K) instead of (K, M)
     Prefetch pf;  // one-token kernels: blocks M .. M + pf.blocks - 1 read these ranges
+    // k_token_one gathering its rows: token m is row gids[m] of X (gV rows; NaN for an id outside
+    // [0, gV)), also stored as row m of gout (M, K)
+    const int32_t* gids;
+    int gV;
+    float* gout;
 };
 
 // Block b of a one-token kernel's prefetch blocks: thread t reads the 16-byte units

@@ -399,17 +399,19 @@ class Decoder:
         ctx = self.ctx
         fused = self.fused_ok()
         if fused and self._tok:
-            ctx.embedding_gather(self.emb, ids, out=self.x_t, tokens=True)
-        else:
-            ctx.embedding_gather(self.emb, ids, out=self.x)
-        if fused:
+            # the embedding rows and their first quantization in one launch
             if self.blocks:
                 self._prefetch("qkv", self.blocks[0].q, self.blocks[0].k, self.blocks[0].v)
             g0 = self.blocks[0].g1 if self.blocks else self.g_final
-            if self._tok:
-                ctx.rmsnorm_quant_i8_tokens(self.x_t, g0, self.cfg.eps, outs=(self.xi, self.s, self.rs))
-            else:
-                self._quant(self.x, g0)
+            ctx.embedding_rmsnorm_quant_i8_tokens(self.emb, ids, g0, self.cfg.eps, out=self.x_t,
+                                                  outs=(self.xi, self.s, self.rs))
+        else:
+            ctx.embedding_gather(self.emb, ids, out=self.x)
+        if fused:
+            if not self._tok:
+                if self.blocks:
+                    self._prefetch("qkv", self.blocks[0].q, self.blocks[0].k, self.blocks[0].v)
+                self._quant(self.x, self.blocks[0].g1 if self.blocks else self.g_final)
             for i in range(len(self.blocks)):
                 self.block_step_fused(i, pos, len_bound, attn_hook)
         else:

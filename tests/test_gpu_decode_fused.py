@@ -279,3 +279,40 @@ def test_token_major_residual_entries(ctx, orc, bias):
     a, c = np.ascontiguousarray(et.T), e
     assert np.array_equal(np.isnan(a), np.isnan(c)) and np.all(np.isnan(a[:, 3])) and np.all(np.isnan(a[:, 5]))
     assert np.array_equal(a[~np.isnan(a)].view(np.uint32), c[~np.isnan(c)].view(np.uint32))
+
+
+@pytest.mark.parametrize("d,B,gamma", [(2560, 16, True), (2560, 16, False), (256, 3, True), (6912, 5, True)])
+def test_embedding_rmsnorm_quant_fused(ctx, orc, d, B, gamma):
+    """nnhip_embedding_rmsnorm_quant_i8_tokens: the gathered rows against the oracle's embedding
+    gather, the codes / scales / row sums against the oracle's [RMSNorm ->] absmax int8 of those
+    rows, and, with ids out of range (NaN rows), the same bits as the two-launch form
+    (nnhip_embedding_gather_tokens, then nnhip_rmsnorm_quant_i8_tokens)."""
+    import torch
+    say(f"embedding + rmsnorm quant d={d} B={B} gamma={gamma}")
+    V, eps = 1000, 1e-5
+    table = normal((V, d), 120 + d)
+    ids = (np.arange(B, dtype=np.int32) * 37 + 5) % V
+    g = (1.0 + 0.1 * normal((d,), 121)).astype(np.float32) if gamma else None
+    gd = dev(g) if gamma else None
+    x, (xi, s, rs) = ctx.embedding_rmsnorm_quant_i8_tokens(dev(table), dev(ids), gd, eps)
+    X = orc.embedding_gather(table, ids)                       # (d, B)
+    assert np.array_equal(np.ascontiguousarray(host(x).T).view(np.uint32), X.view(np.uint32))
+    if gamma:
+        xq_o, s_o = orc.rmsnorm_quant_i8(X, g, eps)
+    else:
+        s_o = orc.act_scale(X)
+        xq_o = orc.quantize_i8(X, s_o, True)
+    q = orc.container_to_int8(xq_o, B).T                      # (B, d)
+    assert np.array_equal(host(s).view(np.uint32), np.asarray(s_o, np.float32).reshape(-1).view(np.uint32))
+    assert np.array_equal(host(xi)[:, :d], q)
+    assert np.array_equal(host(rs), q.astype(np.int64).sum(axis=1))
+    # NaN rows from ids outside [0, V): the two-launch form's bits
+    ids2 = ids.copy()
+    ids2[0], ids2[-1] = V, -1
+    got_x, got = ctx.embedding_rmsnorm_quant_i8_tokens(dev(table), dev(ids2), gd, eps)
+    ref_x = ctx.embedding_gather(dev(table), dev(ids2), tokens=True)
+    ref = ctx.rmsnorm_quant_i8_tokens(ref_x, gd, eps)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(got_x).view(np.uint32), host(ref_x).view(np.uint32))
+    assert np.all(np.isnan(host(got_x)[0])) and np.all(np.isnan(host(got_x)[-1]))
+    assert all(np.array_equal(host(a).view(np.uint8), host(c).view(np.uint8)) for a, c in zip(got, ref))
