@@ -376,6 +376,10 @@ struct Gemm
     {
         const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
         const uint32_t M4 = (uint32_t)p.M * 4u;
+        // p.res: y + res[row][token], the residual read at the output's own index, all of a row
+        // block's values requested in one round trip before the first add
+        const bool has_res = p.res != nullptr;
+        const __amdgpu_buffer_rsrc_t rres = rsrc(has_res ? p.res : p.y, has_res ? (uint32_t)p.N * (uint32_t)p.M * 4u : 0u);
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
         {
@@ -384,17 +388,35 @@ struct Gemm
             const uint32_t row0 = (uint32_t)(row_w + rb * 32 + 4 * h);
             const uint32_t vbase = (row0 * (uint32_t)p.M + (uint32_t)(tok_w + l32)) * 4u;
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
+            for (int i0 = 0; i0 < 16; i0 += 4)
             {
-                const int soff = (8 * (i >> 2) + (i & 3)) * (int)M4;
-#pragma unroll
-                for (int n = 0; n < kTB; ++n)
+                // the residuals of 4 rows x kTB token groups in one round trip
+                float rv[4][kTB];
+                if (has_res)
                 {
-                    const int a = acc[rb][n][i] - e.rs2[n];
-                    float y = (e.tv[r][i] * e.sv[n]) * (float)a;
-                    if (kBias) y = y + e.bv[r][i];
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, vbase + (uint32_t)(n * 128),
-                                                          soff, 0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int n = 0; n < kTB; ++n)
+                            rv[j][n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                     rres, vbase + (uint32_t)(n * 128),
+                                                                     (8 * (i0 >> 2) + j) * (int)M4, 0));
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    const int i = i0 + j;
+                    const int soff = (8 * (i >> 2) + (i & 3)) * (int)M4;
+#pragma unroll
+                    for (int n = 0; n < kTB; ++n)
+                    {
+                        const int a = acc[rb][n][i] - e.rs2[n];
+                        float y = (e.tv[r][i] * e.sv[n]) * (float)a;
+                        if (kBias) y = y + e.bv[r][i];
+                        if (has_res) y = y + rv[j][n];
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry,
+                                                              vbase + (uint32_t)(n * 128), soff, 0);
+                    }
                 }
             }
         }
@@ -406,6 +428,8 @@ struct Gemm
                                                int nrb, int row_w, int tok_w, int h, int l32)
     {
         const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+        // p.res: added per element (edge blocks are few; out-of-range lanes read 0 and store nothing)
+        const __amdgpu_buffer_rsrc_t rres = rsrc(p.res ? p.res : p.y, p.res ? (uint32_t)p.N * (uint32_t)p.M * 4u : 0u);
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
         {
@@ -425,6 +449,8 @@ struct Gemm
                     if (p.bias) y = y + e.bv[r][i];
                     const uint32_t off = (row < p.N && m < p.M) ? ((uint32_t)row * (uint32_t)p.M + (uint32_t)m) * 4u
                                                                  : 0xFFFFFFF0u;
+                    if (p.res)
+                        y = y + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, off, 0, 0));
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
                 }
             }

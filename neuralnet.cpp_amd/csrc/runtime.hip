@@ -244,7 +244,12 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     if (M <= (size_t)kGemvMaxM)
         NNHIP_LAUNCH(fn, launch_gemv(ctx->stream, p, ctx->num_cus));
     else
+    {
+        // the prefill GEMM adds the residual in its plain epilogue (not in the gated one)
+        if (res && glu == 0) p.res = res;
         NNHIP_LAUNCH(fn, launch_gemm(ctx->stream, p, ctx->num_cus, ctx->gemm_tile));
+        if (p.res) return NNHIP_OK;
+    }
     if (res) NNHIP_LAUNCH(fn, launch_add(ctx->stream, res, Y, N * M, Y));
     return NNHIP_OK;
 }

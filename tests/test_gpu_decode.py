@@ -419,6 +419,27 @@ def test_ternary_matmul_add_equals_unfused(ctx, orc, N, K, M):
         ctx.ternary_matmul_add(rp, tau, xi, s, rs, N, K, M, out, out=out)   # aliasing is refused
 
 
+@pytest.mark.parametrize("N,K,M", [(2560, 2560, 256), (2560, 2560, 2048), (300, 520, 200), (1000, 6912, 130)])
+def test_gemm_residual_epilogue_every_tile(ctx, orc, nnhip, N, K, M):
+    """The prefill GEMM's residual epilogue (M > 16: y + res added where y is stored), for every
+    block tile, interior and edge blocks: the same bits as ternary_matmul (checked against the
+    oracle in the parity tests) followed by add."""
+    say(f"gemm residual N={N} K={K} M={M}")
+    rp, tau, b = _fast_linear(ctx, orc, N, K, 30 + N + K, True)
+    X = normal((K, M), 31)
+    xi, s, rs = ctx.act_quant_i8(dev(X))
+    resh = normal((N, M), 32)
+    res = dev(resh)
+    ref = host(ctx.add(res, ctx.ternary_matmul(rp, tau, xi, s, rs, N, K, M, bias=b)))
+    try:
+        for tile in (nnhip.GEMM_TILE_256x128, nnhip.GEMM_TILE_128x128, nnhip.GEMM_TILE_64x64, nnhip.GEMM_TILE_AUTO):
+            ctx.set_gemm_tile(tile)
+            y = host(ctx.ternary_matmul_add(rp, tau, xi, s, rs, N, K, M, res, bias=b))
+            assert same_bits(y, ref), tile
+    finally:
+        ctx.set_gemm_tile(nnhip.GEMM_TILE_AUTO)
+
+
 @pytest.mark.parametrize("K,M,Ns", [(2560, 16, (2560, 640, 640)), (2560, 1, (2560, 2560, 2560, 17)),
                                     (520, 5, (100, 30)), (1024, 40, (64, 64, 64))])
 def test_ternary_matmul_n_equals_separate(ctx, orc, K, M, Ns):
