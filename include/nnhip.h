@@ -316,7 +316,7 @@ nnhip_status nnhip_stream_xor(nnhip_ctx* ctx, const void* src, size_t bytes, uin
 nnhip_status nnhip_trit_transpose(nnhip_ctx* ctx, const uint32_t* A, size_t K, size_t M, uint32_t* At);
 
 /* Y = nnhip_ternary_matmul(...) + res: the decoder's residual add in the same launch on the decode
- * path (res (N, M) f32, must not alias Y). Same bits as nnhip_ternary_matmul then nnhip_add(res, Y).
+ * path and on the prefill GEMM (M > 16: added in its epilogue) (res (N, M) f32, must not alias Y). Same bits as nnhip_ternary_matmul then nnhip_add(res, Y).
  * Replaces w_o's BitLinear::forward followed by the residual add of GPTBlock::forward_step
  * (include/neuralnet.cpp/compute_layer_attention.hpp:1089; compute_layer_gpt.hpp:208-209). */
 nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const float* tau, const int8_t* xi,
@@ -610,7 +610,7 @@ nnhip_status nnhip_argmax_cols(nnhip_ctx* ctx, const float* logits, size_t V, si
 nnhip_status nnhip_argmax_rows(nnhip_ctx* ctx, const float* logits, size_t V, size_t B, int32_t* ids, int32_t* pos);
 
 /* Y = res + the gated block of nnhip_ffn_glu_i8 on X (res (d, M) f32, must not alias Y): the second
- * residual add of GPTBlock::forward_step in fc2's launch on the decode path. Same bits as
+ * residual add of GPTBlock::forward_step in fc2's launch (decode GEMV or prefill GEMM epilogue). Same bits as
  * nnhip_ffn_glu_i8 then nnhip_add(res, Y) (compute_layer_gpt.hpp:212-218). */
 nnhip_status nnhip_ffn_glu_i8_add(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,
                                   size_t M, int act, const void* rp1, const float* tau1, const float* b1,
