@@ -553,8 +553,10 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
 // One block per token group; block b takes group slot(b), XCD-aware when the group count is a
 // multiple of 8, so the blocks of one XCD take consecutive groups and the groups sharing a
 // 128-byte row segment of X meet in one L2.
+// (R = 12 and 14 with 4-token blocks: at least 3 waves per SIMD, 168 registers; left to itself the
+// compiler took 171 for R = 14, i.e. 2 waves per SIMD, too few loads in flight at prefill sizes)
 template <int R, bool kVec, int TPB>
-__global__ __launch_bounds__(reg_waves<TPB> * kWave) void k_token_regs(TokArgs a, const float* __restrict__ gamma,
+__global__ __launch_bounds__(reg_waves<TPB> * kWave, ((R == 12 || R == 14) && TPB == 4) ? 3 : 1) void k_token_regs(TokArgs a, const float* __restrict__ gamma,
                                                                   int n_groups)
 {
     constexpr int RPW = kWave / (TPB / 4);
