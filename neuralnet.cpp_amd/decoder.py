@@ -284,10 +284,24 @@ class Decoder:
     # residual and quantizes for fc1 (0: the whole-K GEMV with the residual, then the quantizer)
     slices_o = 4
 
+    # widest residual stream of the per-token epilogue + quantizer kernel (epilogue_quant_ok)
+    fused_max_d = 11264
+
     def fused_ok(self) -> bool:
         """The fused step path (fc2 split-k, its epilogue, the residual add and the next block's
-        RMSNorm -> int8 as one per-token kernel) applies to batches of at most 16 sequences."""
-        return self.B <= 16
+        RMSNorm -> int8 as one per-token kernel) applies to batches of at most 16 sequences whose
+        residual stream fits the per-token kernel (d <= fused_max_d) and whose fc2 (and, on the
+        token-major path, o) reductions have a split-k slicing; otherwise step() runs block_step."""
+        cfg = self.cfg
+        if self.B > 16 or cfg.d > self.fused_max_d:
+            return False
+        try:
+            self._slices(cfg.F, self.slices_fc2)
+            if self._tok and self.slices_o > 0:
+                self._slices(cfg.H * cfg.dk, self.slices_o)
+        except ValueError:
+            return False
+        return True
 
     @staticmethod
     def _slices(K: int, want: int) -> int:

@@ -312,24 +312,72 @@ def test_decode_step_chain(ctx, orc, nnhip, subln):
     forward_step order), with the GPU's attention output fed to the oracle's next step so the
     int8 stages stay bit-exact: q/k/v, o, FFN, residuals, final norm + head, greedy ids bit for
     bit; attention within tolerance; the KV caches bit for bit."""
+    from nnhip_py import decoder as dmod
+    cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=200, act=0, eps=1e-5)
+    _decode_chain(ctx, orc, nnhip, cfg, B=3, start=np.array([0, 7, 126], np.int32),
+                  ids=np.array([3, 50, 96], np.int32), subln=subln, seed=0x5EC + subln, expect_fused=True)
+
+
+def test_decode_step_chain_unfused_b17(ctx, orc, nnhip):
+    """17 sequences take the unfused step (block_step, then the column argmax): the same oracle
+    chain bit for bit, the last step with advance=True (ids written into the input, every
+    position advanced by one)."""
+    from nnhip_py import decoder as dmod
+    cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=200, act=0, eps=1e-5)
+    B = 17
+    start = (np.arange(B, dtype=np.int32) * 11) % 150
+    ids = (np.arange(B, dtype=np.int32) * 13 + 5) % cfg.vocab
+    _decode_chain(ctx, orc, nnhip, cfg, B=B, start=start, ids=ids, subln=True, seed=0x5F0, expect_fused=False,
+                  advance_last=True)
+
+
+def test_decode_fused_ok_limits_fall_back(ctx, orc, nnhip):
+    """A model past the fused step's limits (residual stream wider than the per-token kernel
+    takes, or no split-k slicing of fc2) is stepped by block_step instead of failing; the two
+    paths give the same bits."""
     import torch
     from nnhip_py import decoder as dmod
     cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=200, act=0, eps=1e-5)
-    L, B = 2, 3
-    dec, hb, emb, gfin, head = _build_model(ctx, orc, nnhip, cfg, L, B, 0x5EC + subln, subln)
+    B = 4
+    dec, hb, emb, gfin, head = _build_model(ctx, orc, nnhip, cfg, 2, B, 0x5F1, True)
+    ref, _, _, _, _ = _build_model(ctx, orc, nnhip, cfg, 2, B, 0x5F1, True)
+    assert ref.fused_ok()
+    dec.fused_max_d = 128          # below d: the per-token kernel would refuse the residual stream
+    assert not dec.fused_ok()
+    dec2, _, _, _, _ = _build_model(ctx, orc, nnhip, cfg, 2, B, 0x5F1, True)
+    dec2.slices_fc2 = 0            # no split-k slicing of fc2
+    assert not dec2.fused_ok()
+    ids = np.array([1, 2, 3, 4], np.int32)
+    pos = np.array([0, 5, 9, 130], np.int32)
+    outs = []
+    for d_ in (ref, dec, dec2):
+        say(f"fused_ok fallback: fused={d_.fused_ok()}")
+        lg, nx = d_.step(dev(ids), dev(pos), int(pos.max()) + 1)
+        outs.append((host(lg), host(nx)))
+        torch.cuda.synchronize()
+    for lg, nx in outs[1:]:
+        assert same_bits(lg, outs[0][0]) and nx.tolist() == outs[0][1].tolist()
+
+
+def _decode_chain(ctx, orc, nnhip, cfg, B, start, ids, subln, seed, expect_fused, advance_last=False):
+    import torch
+    L = 2
+    dec, hb, emb, gfin, head = _build_model(ctx, orc, nnhip, cfg, L, B, seed, subln)
+    assert dec.fused_ok() == expect_fused
     cos, sin = orc.rope_table(cfg.dk, cfg.max_len)
     kc_o = [np.zeros((B, cfg.max_len, cfg.Hkv * cfg.dk), np.float32) for _ in range(L)]
     vc_o = [np.zeros_like(kc_o[0]) for _ in range(L)]
-    start = np.array([0, 7, 126], np.int32)
-    ids = np.array([3, 50, 96], np.int32)
     for step in range(3):
         pos = start + step
-        say(f"decode chain subln={subln} step {step} pos={pos.tolist()}")
+        advance = advance_last and step == 2
+        say(f"decode chain B={B} subln={subln} step {step} advance={advance}")
         attn_gpu = {}
-        dec_ids = dev(ids)
-        logits_d, next_d = dec.step(dec_ids, dev(pos), int(pos.max()) + 1,
-                                    attn_hook=lambda i, a: attn_gpu.__setitem__(i, a.cpu().numpy()))
+        dec_ids, dec_pos = dev(ids), dev(pos)
+        logits_d, next_d = dec.step(dec_ids, dec_pos, int(pos.max()) + 1,
+                                    attn_hook=lambda i, a: attn_gpu.__setitem__(i, a.cpu().numpy()), advance=advance)
         logits, nxt = host(logits_d), host(next_d)
+        if advance:
+            assert host(dec_ids).tolist() == nxt.tolist() and host(dec_pos).tolist() == (pos + 1).tolist()
         # oracle chain
         x = orc.embedding_gather(emb, ids)
         for l in range(L):

@@ -357,8 +357,8 @@ def c3_case(ctx, orc, N, K, M, seed):
     return host(wq_d, np.uint32), host(tau_d), xq, s, rp, tau_d, xi, s_d, rs
 
 
-@pytest.mark.parametrize("N,K,M", [(4096, 4096, 256), (11008, 4096, 1024), (4096, 4096, 2048),
-                                   (11008, 4096, 2048), (4096, 4096, 4096), (11008, 4096, 4096),
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 256), (11008, 4096, 256), (4096, 4096, 1024), (11008, 4096, 1024),
+                                   (4096, 4096, 2048), (11008, 4096, 2048), (4096, 4096, 4096), (11008, 4096, 4096),
                                    (2560, 2560, 100)])
 def test_prefill_gemm_shapes(ctx, orc, N, K, M):
     """BASELINE config 2 (K=4096, N in {4096, 11008}, M up to 4096; 0.1% activation outliers at 20x):

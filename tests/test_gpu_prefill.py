@@ -303,3 +303,53 @@ def test_decoder_prefill_chain_c5(ctx, orc, nnhip):
     dec, hb, emb, gfin, head = _gpu_model(ctx, nnhip, cfg, 30, B, 0xC5C5)
     assert dec.logits_t is not None, "the C5 head should produce token-major logits"
     _prefill_chain(ctx, orc, cfg, dec, hb, emb, gfin, head, B, T, [0, 13], 2, 5, advance=True)
+
+
+@pytest.mark.parametrize("N,K,gated", [(2560, 2560, False), (2560, 6912, False), (6912, 2560, True)])
+def test_prefill_gemm_c5_token_count(ctx, orc, nnhip, N, K, gated):
+    """The prefill GEMM at config C5's size: 16 sequences x 2048 tokens = 32768 tokens per call, the
+    o / q and fc2 shapes (2560 x 2560, 2560 x 6912) and fc1 with the gated epilogue (13824 fused
+    gate/up rows over d = 2560 into 6912 features). Against the oracle's CpuEngine restatement
+    (src/int8_act_test.cpp:210-236 order): every row on a band of 256 tokens in the middle of the
+    call and sampled rows (every 97th, the last) over all 32768 tokens; the scales bit for bit."""
+    import torch
+    M = 32768
+    say(f"prefill GEMM at C5 size N={N} K={K} M={M} gated={gated}")
+    rows_w = 2 * N if gated else N
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xC5 + N + K)
+    W = torch.randn((rows_w, K), generator=gen, device="cuda") * 0.02
+    tau_d = W.abs().mean(dim=1).contiguous()           # per-row absmean, as a converted checkpoint has
+    wq_d = ctx.trit_pack(W, tau_d)
+    del W
+    b = normal((rows_w,), 0xC6 + N, 0.0, 0.1)
+    X_d = torch.randn((K, M), generator=gen, device="cuda")
+    xi, s_d, rs = ctx.act_quant_i8(X_d)
+    X = host(X_d)
+    del X_d
+    s = orc.act_scale(X)
+    assert np.array_equal(host(s_d), s)
+    xq = orc.quantize_i8(X, s, True)
+    del X
+    wq, tau = host(wq_d).view(np.uint32), host(tau_d)
+    if gated:
+        wo, to, bo = ctx.glu_interleave(wq_d, tau_d, dev(b), N, K)
+        Y = host(ctx.ternary_matmul_glu(ctx.repack(wo, K), to, xi, s_d, rs, N, K, M, 0, bias=bo))
+    else:
+        Y = host(ctx.ternary_matmul(ctx.repack(wq_d, K), tau_d, xi, s_d, rs, N, K, M, bias=dev(b)))
+
+    def ref(rows, m0, m1):
+        """oracle output rows `rows` (features when gated) for tokens [m0, m1), m0 % 4 == 0"""
+        xs = np.ascontiguousarray(xq[:, m0 // 4:(m1 + 3) // 4])
+        if not gated:
+            y = orc.matmul_q_i8_rowblock(wq[rows], tau[rows], xs, s[m0:m1], K, m1 - m0)
+            return orc.add_row_broadcast(y, b[rows])
+        both = np.concatenate([rows, rows + N])           # gate rows, then their up rows
+        y1 = orc.add_row_broadcast(orc.matmul_q_i8_rowblock(wq[both], tau[both], xs, s[m0:m1], K, m1 - m0), b[both])
+        return orc.glu(y1, 0)
+
+    m0 = 16384 + 128
+    band = ref(np.arange(N), m0, m0 + 256)
+    assert same_bits(Y[:, m0:m0 + 256], band), "band of 256 tokens differs"
+    rows = np.unique(np.concatenate([np.arange(0, N, 97), [N - 1]]))
+    assert same_bits(Y[rows], ref(rows, 0, M)), "sampled rows differ"
