@@ -242,7 +242,8 @@ constexpr int kGemvDeepMulti = 4;
 bool gemv_deep_multi_ok(const GemvProblem* ps, int count, int num_cus);
 hipError_t launch_gemv_deep_multi(hipStream_t st, const GemvProblem* ps, int count);
 // Split-k partial sums (no epilogue): part[ks][t][n] int32, S slices of ceil(KT / S) k tiles
-// (each slice non-empty, S <= 8, M <= 16); the epilogue runs in the per-token kernel that follows.
+// (each slice non-empty and at most 14 tiles long, S <= 32, M <= 16); the epilogue runs in the
+// kernel that follows (the decoder's per-token kernel takes S <= 8).
 bool gemv_part_ok(const GemvProblem& p, int S);
 hipError_t launch_gemv_part(hipStream_t st, const GemvProblem& p, int S, int32_t* part);
 // Grouped GEMV over a precomputed per-wave schedule: wave w runs the items
@@ -275,6 +276,15 @@ hipError_t launch_digits(hipStream_t st, const void* B, bool b16, const float* k
 hipError_t launch_digit_combine(hipStream_t st, const float* Yp, const float* tau, const int32_t* ex,
                                 const uint32_t* rp, const void* B, bool b16, const float* kscale, size_t N, size_t K,
                                 size_t M, void* Y, bool y16);
+// split-k form for a few long tokens (M <= 4): digits in chunks of 4096 columns (P =
+// digit_chunks(K) partial digit sums per token), the slice sums of k_gemv_part, and a combine
+// that adds both exactly (bit-identical to the unit-scale GEMV path)
+size_t digit_chunks(size_t K);
+hipError_t launch_digits_chunks(hipStream_t st, const void* B, bool b16, const float* kscale, size_t K, size_t M,
+                                int8_t* xi, int32_t* rsp, int32_t* ex);
+hipError_t launch_digit_combine_parts(hipStream_t st, const int32_t* part, int S, const int32_t* rsp, size_t P,
+                                      const float* tau, const int32_t* ex, const uint32_t* rp, const void* B, bool b16,
+                                      const float* kscale, size_t N, size_t K, size_t M, void* Y, bool y16);
 // the same product in one launch at decode sizes (f32 activations, M <= 4, K % 4 == 0, 16-byte
 // aligned B, the compiled k-tile counts): digits in LDS per block, int64 combine in the
 // epilogue; bit-identical to the three launches

@@ -143,6 +143,102 @@ __global__ __launch_bounds__(kDigThreads) void k_digits(const void* __restrict__
     if (tid == 0) ex[m] = bad ? kSpecialToken : E;
 }
 
+// The same digits for a few long tokens (the split-k path, M <= 4): block (c, m) takes columns
+// [c * kChunk, (c + 1) * kChunk) of token m. Each block first reduces the absmax and the
+// non-finite flag over the whole token (every chunk of a token sees the same E, so the digits are
+// k_digits' bit for bit), then writes its chunk's digit rows and its partial digit sums
+// rsp[(m * P + c) * 4 + p] (the combine adds the P partials: integers, exact in any order).
+constexpr int kChunk = 4096;
+constexpr int kChunkThreads = 256;
+
+__global__ __launch_bounds__(kChunkThreads) void k_digits_chunks(const void* __restrict__ B, bool f16,
+                                                                 const float* __restrict__ kscale, int K, int M, int Kp,
+                                                                 int8_t* __restrict__ xi, int32_t* __restrict__ rsp,
+                                                                 int32_t* __restrict__ ex)
+{
+    constexpr int NW = kChunkThreads / kWave;
+    __shared__ float smax[NW];
+    __shared__ int sbad[NW];
+    __shared__ int ssum[4][NW];
+    const int c = blockIdx.x, m = blockIdx.y, P = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    constexpr int STEP = kChunkThreads * kDigUnroll;
+    float mx = 0.0f;
+    int bad = 0;
+    for (int k0 = tid; k0 < K; k0 += STEP)
+    {
+        float v[kDigUnroll];
+#pragma unroll
+        for (int u = 0; u < kDigUnroll; ++u)
+        {
+            const int k = k0 + u * kChunkThreads;
+            v[u] = k < K ? load_bk(B, kscale, k, M, m, f16) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kDigUnroll; ++u)
+        {
+            const float a = fabsf(v[u]);
+            bad |= !(a <= 3.4028234663852886e38f);  // NaN or inf
+            mx = fmaxf(mx, a);
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1)
+    {
+        mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        bad |= __shfl_xor(bad, off, kWave);
+    }
+    if (lane == 0)
+    {
+        smax[w] = mx;
+        sbad[w] = bad;
+    }
+    __syncthreads();
+    for (int i = 0; i < NW; ++i)
+    {
+        mx = fmaxf(mx, smax[i]);
+        bad |= sbad[i];
+    }
+    int E = 0;
+    (void)frexpf(mx, &E);  // mx < 2^E (E = 0 for mx = 0: every digit is 0)
+    const int shift = 30 - E;
+    int s[4] = {0, 0, 0, 0};
+    int8_t* row = xi + (size_t)4 * m * Kp;
+    const int kend = min(Kp, (c + 1) * kChunk);
+    for (int k = c * kChunk + tid; k < kend; k += kChunkThreads)
+    {
+        const float v = (k < K && !bad) ? load_bk(B, kscale, k, M, m, f16) : 0.0f;
+        int X = (int)__builtin_rintf(ldexpf(v, shift));
+        int d[4];
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+        {
+            d[p] = ((X + 128) & 255) - 128;
+            X = (X - d[p]) >> 8;  // exact: X - d is a multiple of 256
+        }
+        d[3] = X;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+        {
+            row[(size_t)p * Kp + k] = (int8_t)d[p];
+            s[p] += d[p];
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+    {
+        for (int off = 32; off >= 1; off >>= 1) s[p] += __shfl_xor(s[p], off, kWave);
+        if (lane == 0) ssum[p][w] = s[p];
+    }
+    __syncthreads();
+    if (tid < 4)
+    {
+        int t = 0;
+        for (int i = 0; i < NW; ++i) t += ssum[tid][i];
+        rsp[((size_t)m * P + c) * 4 + tid] = t;
+    }
+    if (c == 0 && tid == 0) ex[m] = bad ? kSpecialToken : E;
+}
+
 // Code (trit + 2) of row n, column k in the T16K256 layout.
 __device__ __forceinline__ int code_at(const uint32_t* rp, int KT, int n, int k)
 {
@@ -201,6 +297,48 @@ __global__ __launch_bounds__(kDigBlock) void k_digit_combine(const float* __rest
         reinterpret_cast<_Float16*>(Y)[idx] = (_Float16)y;
     else
         reinterpret_cast<float*>(Y)[idx] = y;
+}
+
+// k_digit_combine on the split-k path: the digit products come as S int32 slice sums of
+// sum(code * d) (part[ks][4m + p][n], k_gemv_part) and P partial digit sums per token; their
+// exact total A_p = sum_ks part - 2 sum_c rsp is the integer the unit-scale GEMV would have given,
+// so Y is k_digit_combine's bit for bit.
+__global__ __launch_bounds__(kDigBlock) void k_digit_combine_parts(const int32_t* __restrict__ part, int S,
+                                                                   const int32_t* __restrict__ rsp, int P,
+                                                                   const float* __restrict__ tau,
+                                                                   const int32_t* __restrict__ ex,
+                                                                   const uint32_t* __restrict__ rp, int KT,
+                                                                   const void* __restrict__ B, bool b16,
+                                                                   const float* __restrict__ kscale, int N, int K, int M,
+                                                                   void* __restrict__ Y, bool y16)
+{
+    const size_t idx = (size_t)blockIdx.x * kDigBlock + threadIdx.x;
+    if (idx >= (size_t)N * M) return;
+    const int n = (int)(idx % N), m = (int)(idx / N);  // consecutive threads: consecutive n
+    const int E = ex[m];
+    const float tn = tau ? tau[n] : 1.0f;
+    float y;
+    if (E != kSpecialToken)
+    {
+        long long T = 0;
+#pragma unroll
+        for (int p = 3; p >= 0; --p)
+        {
+            int a = 0;
+            for (int ks = 0; ks < S; ++ks) a += part[((size_t)ks * 4 * M + 4 * m + p) * N + n];
+            int r = 0;
+            for (int c = 0; c < P; ++c) r += rsp[((size_t)m * P + c) * 4 + p];
+            T = (T << 8) + (long long)(a - 2 * r);
+        }
+        y = tn * ldexpf((float)T, E - 30);
+    }
+    else
+        y = special_dot(B, b16, kscale, rp, KT, K, M, n, m, tn);
+    const size_t o = (size_t)n * M + m;
+    if (y16)
+        reinterpret_cast<_Float16*>(Y)[o] = (_Float16)y;
+    else
+        reinterpret_cast<float*>(Y)[o] = y;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -485,6 +623,27 @@ hipError_t launch_digits(hipStream_t st, const void* B, bool b16, const float* k
 {
     const size_t Kp = round_up(K, kTileK);
     k_digits<<<dim3((unsigned)M), kDigThreads, 0, st>>>(B, b16, kscale, (int)K, (int)M, (int)Kp, xi, rowsum, ex);
+    return hipGetLastError();
+}
+
+size_t digit_chunks(size_t K) { return ceil_div(round_up(K, kTileK), (size_t)kChunk); }
+
+hipError_t launch_digits_chunks(hipStream_t st, const void* B, bool b16, const float* kscale, size_t K, size_t M,
+                                int8_t* xi, int32_t* rsp, int32_t* ex)
+{
+    const size_t Kp = round_up(K, kTileK);
+    k_digits_chunks<<<dim3((unsigned)digit_chunks(K), (unsigned)M), kChunkThreads, 0, st>>>(B, b16, kscale, (int)K, (int)M,
+                                                                                           (int)Kp, xi, rsp, ex);
+    return hipGetLastError();
+}
+
+hipError_t launch_digit_combine_parts(hipStream_t st, const int32_t* part, int S, const int32_t* rsp, size_t P,
+                                      const float* tau, const int32_t* ex, const uint32_t* rp, const void* B, bool b16,
+                                      const float* kscale, size_t N, size_t K, size_t M, void* Y, bool y16)
+{
+    const size_t n = N * M;
+    k_digit_combine_parts<<<dim3((unsigned)ceil_div(n, kDigBlock)), kDigBlock, 0, st>>>(
+        part, S, rsp, (int)P, tau, ex, rp, (int)ceil_div(K, kTileK), B, b16, kscale, (int)N, (int)K, (int)M, Y, y16);
     return hipGetLastError();
 }
 

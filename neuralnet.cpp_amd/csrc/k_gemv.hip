@@ -595,7 +595,7 @@ static int gemv_part_width(int KT, int S)
 
 bool gemv_part_ok(const GemvProblem& p, int S)
 {
-    if (S < 1 || S > 8 || p.M < 1 || p.M > kGemvMaxM || p.N < 1) return false;
+    if (S < 1 || S > 32 || p.M < 1 || p.M > kGemvMaxM || p.N < 1) return false;
     const int kts = (p.KT + S - 1) / S;
     if ((S - 1) * kts >= p.KT) return false;  // every slice holds at least one k tile
     const int w = gemv_part_width(p.KT, S);

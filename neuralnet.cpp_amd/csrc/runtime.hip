@@ -862,6 +862,30 @@ nnhip_status nnhip_ternary_matmul(nnhip_ctx* ctx, const void* rp, const float* t
     return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y);
 }
 
+// Slices of the split-k digit path, or 0 for the unit-scale GEMV / GEMM. It takes a few long
+// tokens (M <= 4, so the 4M digit tokens are one GEMV column block) with a long reduction
+// (K >= 6144) over few output rows (at most 2048 row tiles): there the whole-K GEMV runs one wave
+// per 16-row tile through K / 256 sequential k tiles, too few waves to hide memory latency. The
+// slices keep every slice within 14 k tiles and give at least two blocks of four row tiles per CU.
+static int digit_split_slices(size_t N, size_t K, size_t M, int num_cus)
+{
+    const size_t KT = ceil_div(K, kTileK), RT = ceil_div(N, 16);
+    if (M < 1 || M > 4 || KT < 24 || RT > 2048) return 0;
+    const size_t row_groups = ceil_div(RT, 4);
+    const size_t cus = num_cus > 0 ? (size_t)num_cus : 256;
+    size_t S = ceil_div(KT, 14);
+    if (row_groups * S < 2 * cus) S = ceil_div(2 * cus, row_groups);
+    if (S > 32) S = 32;
+    if (S > KT) S = KT;
+    GemvProblem p{};
+    p.N = (int32_t)N;
+    p.M = (int32_t)(4 * M);
+    p.KT = (int32_t)KT;
+    for (; S >= 1; --S)
+        if (gemv_part_ok(p, (int)S)) return (int)S;
+    return 0;
+}
+
 static nnhip_status matmul_digits(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
                                   const float* kscale, const void* B, int b_f16, size_t N, size_t K, size_t M, void* Y,
                                   int y_f16)
@@ -882,6 +906,35 @@ static nnhip_status matmul_digits(nnhip_ctx* ctx, const char* fn, const void* rp
         return NNHIP_OK;
     }
     const size_t Kp = round_up(K, kTileK), M4 = 4 * M;
+    const int S = digit_split_slices(N, K, M, ctx->num_cus);
+    if (S > 0)
+    {
+        // a few long tokens: the digits in column chunks, the GEMV as split-k int32 slice sums, and
+        // a combine that adds both (exact integers: the same bits as the path below)
+        const size_t P = digit_chunks(K);
+        const size_t b_xi = round_up(M4 * Kp, 256), b_rsp = round_up(M * P * 16, 256), b_ex = round_up(M * 4, 256);
+        const size_t b_part = (size_t)S * M4 * N * 4;
+        st = ensure_ws(ctx, b_xi + b_rsp + b_ex + b_part, fn);
+        if (st != NNHIP_OK) return st;
+        uint8_t* w = static_cast<uint8_t*>(ctx->ws);
+        int8_t* xi = reinterpret_cast<int8_t*>(w);
+        int32_t* rsp = reinterpret_cast<int32_t*>(w + b_xi);
+        int32_t* ex = reinterpret_cast<int32_t*>(w + b_xi + b_rsp);
+        int32_t* part = reinterpret_cast<int32_t*>(w + b_xi + b_rsp + b_ex);
+        NNHIP_LAUNCH(fn, launch_digits_chunks(ctx->stream, B, b_f16 != 0, kscale, K, M, xi, rsp, ex));
+        GemvProblem p{};
+        p.rp = static_cast<const u32x4*>(rp);
+        p.xi = xi;
+        p.N = (int32_t)N;
+        p.K = (int32_t)K;
+        p.M = (int32_t)M4;
+        p.KT = (int32_t)ceil_div(K, kTileK);
+        p.xlds = -1;
+        NNHIP_LAUNCH(fn, launch_gemv_part(ctx->stream, p, S, part));
+        NNHIP_LAUNCH(fn, launch_digit_combine_parts(ctx->stream, part, S, rsp, P, tau, ex, static_cast<const uint32_t*>(rp),
+                                                    B, b_f16 != 0, kscale, N, K, M, Y, y_f16 != 0));
+        return NNHIP_OK;
+    }
     const size_t b_xi = round_up(M4 * Kp, 256), b_rs = round_up(M4 * 4, 256), b_ex = round_up(M * 4, 256);
     const size_t b_yp = N * M4 * 4;
     st = ensure_ws(ctx, b_xi + b_rs + b_ex + b_yp, fn);

@@ -327,3 +327,49 @@ def test_matmul_t_f_one_launch_bits(ctx, orc, K, M, N):
     assert same_bits(one, three)
     trT = orc.trits_of(At.cpu().numpy().view(np.uint32), K)
     assert same_bits(one, digit_model(trT, B, kscale=tau))
+
+
+@pytest.mark.parametrize("N,K,M", [(640, 12000, 3), (1000, 8192, 2), (2048, 7000, 4), (48, 30000, 1)])
+def test_matmul_f_split_k_bits(ctx, orc, N, K, M):
+    """A few long tokens over few rows (M <= 4, K >= 6144, at most 2048 row tiles, beyond the
+    one-launch kernel's shapes) run split-k: digits in column chunks, int32 slice sums, and a
+    combine adding both; bit for bit the exact digit model, and within the f32 tolerance of the
+    oracle's float64 product."""
+    say(f"ternary_matmul_f split-k N={N} K={K} M={M}")
+    wq, tau, rp = case(ctx, orc, N, K, seed=N + K + M)
+    X = normal((K, M), 70 + M)
+    X[::3, :] *= 17.0
+    got = host(ctx.ternary_matmul_f(rp, dev(tau), dev(X), N, K))
+    assert same_bits(got, digit_model(orc.trits_of(wq, K), X, tau=tau))
+    check(got, orc.matmul_q(wq, tau, X, K), TOL)
+
+
+def test_matmul_t_f_split_k_long_reduction(ctx, orc):
+    """The dX product with a long reduction (16384 k over 1024 outputs, one token), on the split-k
+    path: bit for bit the digit model on the transposed trits with tau folded per k."""
+    K, M, N = 16384, 1024, 1
+    say(f"ternary_matmul_t_f split-k K={K} M={M} N={N}")
+    A, tau, At, rpT = transposed_case(ctx, orc, K, M, seed=77)
+    B = normal((K, N), 78)
+    got = host(ctx.ternary_matmul_t_f(rpT, dev(tau), dev(B), M))
+    trT = orc.trits_of(At.cpu().numpy().view(np.uint32), K)
+    assert same_bits(got, digit_model(trT, B, kscale=tau))
+
+
+def test_matmul_f_split_k_specials(ctx, orc):
+    """Non-finite and zero tokens on the split-k path: the IEEE results of the exact path, and the
+    finite token beside them the digit model's bits."""
+    N, K, M = 300, 9000, 4
+    W = normal((N, K), 81, 0.0, 0.02)
+    W[::2, 20] = 1.0
+    W[1::2, 20] = -1.0
+    W[:, 10] = 0.0
+    wq, tau, rp = case(ctx, orc, N, K, W=W)
+    X = normal((K, M), 82)
+    X[20, 0] = np.inf
+    X[10, 1] = -np.inf
+    X[:, 2] = 0.0
+    got = host(ctx.ternary_matmul_f(rp, dev(tau), dev(X), N, K))
+    assert np.all(got[::2, 0] == np.inf) and np.all(got[1::2, 0] == -np.inf) and np.all(np.isnan(got[:, 1]))
+    assert np.all(got[:, 2] == 0.0)
+    assert same_bits(got[:, 3:], digit_model(orc.trits_of(wq, K), X[:, 3:], tau=tau))
