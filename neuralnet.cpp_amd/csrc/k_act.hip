@@ -85,15 +85,18 @@ __device__ __forceinline__ void bfly_fsum(float (&v)[4])
     for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], o[i]);
     if constexpr (OFF > 1) bfly_fsum<OFF / 2>(v);
 }
+// Max over the same lanes of values that are never NaN and never negative (absolute values,
+// +0 included): their bit patterns order as unsigned integers, so one integer max per level
+// replaces a float compare and select.
 template <int OFF>
-__device__ __forceinline__ void bfly_fmax(float (&v)[4])
+__device__ __forceinline__ void bfly_umax(uint32_t (&v)[4])
 {
-    float o[4];
+    uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = lane_xor<OFF>(v[i]);
+    for (int i = 0; i < 4; ++i) o[i] = (uint32_t)lane_xor<OFF>((int)v[i]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = o[i] > v[i] ? o[i] : v[i];
-    if constexpr (OFF > 1) bfly_fmax<OFF / 2>(v);
+    if constexpr (OFF > 1) bfly_umax<OFF / 2>(v);
 }
 template <int OFF>
 __device__ __forceinline__ void bfly_isum(int (&v)[4])
@@ -353,6 +356,8 @@ struct TokShared
     float wred[reg_waves<TPB>][TPB];
     int wsum[reg_waves<TPB>][TPB];
     float tok_ri[TPB];
+    float tok_sc[TPB], tok_rc[TPB];  // per-token scale and its reciprocal
+    float4 tok_ex[TPB];              // exact path: prescale xs, s * xs, fl(1 / (s * xs))
 };
 
 // Issue the loads of group g into x (vector path: one buffer resource over X, K*M*4 < 2^31
@@ -470,65 +475,109 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
         return;
     }
 
-    // ---- pass 2: per-token absmax -> scale (fmaxf ignores NaN, as `a > m ? a : m` from 0 does)
-    float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // ---- pass 2: per-token absmax -> scale (fmaxf ignores NaN, as `a > m ? a : m` from 0 does).
+    // The waves' maxima meet in LDS; TPB lanes of wave 0 reduce them, one token each, and post
+    // the scale and its reciprocal for the block.
+    uint32_t mx[4];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int i = 0; i < 4; ++i)
+    {
+        float m = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], fabsf(x[r][i]));
-    bfly_fmax<RPW / 2>(mx);
+        for (int r = 0; r < R; ++r) m = fmaxf(m, fabsf(x[r][i]));
+        mx[i] = __builtin_bit_cast(uint32_t, m);
+    }
+    bfly_umax<RPW / 2>(mx);
     if (fl == 0)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sh.wred[w][4 * h + i] = mx[i];
+        for (int i = 0; i < 4; ++i) sh.wred[w][4 * h + i] = __builtin_bit_cast(float, mx[i]);
+    __syncthreads();
+    if (threadIdx.x < TPB)
+    {
+        float t = sh.wred[0][threadIdx.x];
+#pragma unroll
+        for (int v = 1; v < RW; ++v) t = fmaxf(t, sh.wred[v][threadIdx.x]);
+        const float scv = __fmul_rn(t, 1.0f / 127.0f);
+        sh.tok_sc[threadIdx.x] = scv;
+        sh.tok_rc[threadIdx.x] = quant_rcp(scv);
+        const float xs = scv < 0x1p-100f ? 0x1p100f : 1.0f;
+        const float se = __fmul_rn(scv, xs);
+        sh.tok_ex[threadIdx.x] = make_float4(xs, se, quant_rcp(se), 0.0f);
+    }
     __syncthreads();
     float sc[4], rc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
     {
-        float t = sh.wred[0][4 * h + i];
-#pragma unroll
-        for (int v = 1; v < RW; ++v) t = fmaxf(t, sh.wred[v][4 * h + i]);
-        sc[i] = __fmul_rn(t, 1.0f / 127.0f);
-        rc[i] = quant_rcp(sc[i]);
+        sc[i] = sh.tok_sc[4 * h + i];
+        rc[i] = sh.tok_rc[4 * h + i];
     }
 
-    // ---- pass 3: quantize; codes on the fast path with one flag for the thread. Rows past K
-    // hold x = 0 (or NaN when rms_inv is infinite), which both paths turn into code 0.
+    // ---- pass 3: quantize; codes on the fast path with one flag per round. Rows past K hold
+    // x = 0 (or NaN when rms_inv is infinite), which every path turns into code 0. A round with a
+    // flagged element (a product near a tie, NaN or inf, or any product of a token whose
+    // reciprocal overflowed) is recomputed by the exact division-free code for its four elements,
+    // on x * xs / (s * xs) with the token's power-of-two prescale xs (2^100 below s = 2^-100, else
+    // 1): the same quotient, with s * xs in quantize_exact's range.
     uint32_t pk[R];
-    bool amb = isinf(rc[0]) || isinf(rc[1]) || isinf(rc[2]) || isinf(rc[3]);
+    uint32_t amb = 0;  // bit r: round r holds a flagged element
 #pragma unroll
     for (int r = 0; r < R; ++r)
     {
+        bool f = false;
         int qv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qv[i] = quantize_guess(x[r][i], rc[i], amb);
+        for (int i = 0; i < 4; ++i) qv[i] = quantize_code(x[r][i], rc[i], f);
         pk[r] = pack4(qv[0], qv[1], qv[2], qv[3]);
+        amb |= f ? 1u << r : 0u;
     }
     if (amb)
     {
+        float4 ex[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ex[i] = sh.tok_ex[4 * h + i];
 #pragma unroll
         for (int r = 0; r < R; ++r)
-        {
-            int qv[4];
+            if (amb >> r & 1u)
+            {
+                int qv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) qv[i] = quantize_fast(x[r][i], sc[i], rc[i]);
-            pk[r] = pack4(qv[0], qv[1], qv[2], qv[3]);
-        }
+                for (int i = 0; i < 4; ++i) qv[i] = quantize_exact(__fmul_rn(x[r][i], ex[i].x), ex[i].y, ex[i].z);
+                pk[r] = pack4(qv[0], qv[1], qv[2], qv[3]);
+            }
     }
     // xi: after a quad transpose lane (quad q, position j) holds token 4h+j for the four rows
     // 4q..4q+3 of its wave's slice, one dword store each; dot4 against 1s sums those codes.
+    // Stores go through one buffer resource over xi (M * Kp < 2^31 at launch) from one offset per
+    // thread; a token past M gets an offset past the range, which the buffer store drops. Rows
+    // past Kp (the next token's bytes otherwise) are never stored: rounds below Kp / RR are whole,
+    // the round at Kp / RR holds rows below Kp in the threads whose first row of a round is below
+    // Kp % RR (Kp % 256 == 0, so a thread's four rows are all in or all out), later rounds none.
     const int wpr = (a.M + 3) / 4;
     const int j = lane_j(fl);
+    const int q0 = RPW * w + (fl & ~3);  // first of the thread's four rows in a round
+    const __amdgpu_buffer_rsrc_t rxi =
+        __builtin_amdgcn_make_buffer_rsrc(a.xi, (short)0, a.M * a.Kp, 0x00020000);
+    const uint32_t xoff = mt + j < a.M ? (uint32_t)((mt + j) * a.Kp + q0) : 0x80000000u;
+    const uint32_t xpart = q0 < a.Kp % RR ? xoff : 0x80000000u;
+    const int whole = a.Kp / RR;
+    if (a.xq_ref && g * LPR + h < wpr)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            const int f = RR * r + ro;
+            if (f < a.K) a.xq_ref[(size_t)f * wpr + g * LPR + h] = pk[r];
+        }
     int tsum = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r)
     {
-        const int f = RR * r + ro;
-        if (a.xq_ref && f < a.K && g * LPR + h < wpr) a.xq_ref[(size_t)f * wpr + g * LPR + h] = pk[r];
         const uint32_t col = quad_transpose(pk[r], j);
         tsum = __builtin_amdgcn_sdot4((int)col, 0x01010101, tsum, false);
-        const int f0 = RR * r + RPW * w + (fl & ~3);  // first of the four rows (Kp % 256 == 0)
-        if (f0 < a.Kp && mt + j < a.M) *reinterpret_cast<uint32_t*>(a.xi + (size_t)(mt + j) * a.Kp + f0) = col;
+        if (r < whole)
+            __builtin_amdgcn_raw_buffer_store_b32(col, rxi, xoff + (uint32_t)(RR * r), 0, 0);
+        else if (r == whole)
+            __builtin_amdgcn_raw_buffer_store_b32(col, rxi, xpart + (uint32_t)(RR * r), 0, 0);
     }
     tsum = bfly_isum1<RPW / 2, 4>(tsum);  // over the quads of the wave's slice
     if (fl < 4) sh.wsum[w][4 * h + j] = tsum;

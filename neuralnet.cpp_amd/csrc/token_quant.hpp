@@ -59,6 +59,40 @@ __device__ __forceinline__ int quantize_guess(float x, float r, bool& amb)
     return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
 }
 
+// quantize_guess without the clamp and with half its margin, for callers whose scale comes from
+// the same elements. Range: with s = fl(amax * fl(1/127)) over them and r = fl(1/s) finite, every
+// |x| <= amax gives |fl(x * r)| <= 127 * (1 + 2^-20) < 127.5 (four roundings, one of them of s,
+// which is at least 2^-128 whenever 1/s is finite and so keeps 22 significant bits even when
+// subnormal), so rint(y) is already in [-127, 127]. Margin: |y - x/s| <= |x/s| * (2^-23 + 2^-48)
+// < 2^-16 and |fl(x/s) - x/s| <= 2^-17 below 128, so |y - fl(x/s)| < 3 * 2^-17; when y is
+// 2^-15 or more from every half-integer, fl(x/s) is on the same side of each, and rint(y) is
+// quantize_one's code. NaN, inf and near-tie products set `amb`.
+__device__ __forceinline__ int quantize_code(float x, float r, bool& amb)
+{
+    const float y = __fmul_rn(x, r);
+    const float t = __builtin_rintf(y);
+    amb |= !(fabsf(y - t) < 0.5f - 0x1p-15f);
+    return (int)t;
+}
+
+// quantize_one(x, s) without a division and without branches, for s >= 2^-100 and r = fl(1/s)
+// (the correctly rounded reciprocal). q0 = fl(x * r) is within one ulp of x/s, the residual
+// x - q0 * s is exact under one FMA, and fl(q0 + residual * r) is then the correctly rounded
+// quotient fl(x/s) (Markstein's theorem; the bound on s keeps the residual out of the subnormal
+// range wherever the code can be nonzero). Clamped to 127 in magnitude and rounded half away
+// from zero as roundf; a NaN quotient (NaN x, or 0 * inf when s is 0) gives 0.
+__device__ __forceinline__ int quantize_exact(float x, float s, float r)
+{
+    const float q0 = __fmul_rn(x, r);
+    const float e = __builtin_fmaf(-q0, s, x);
+    const float v = __builtin_fmaf(e, r, q0);
+    const float a = fminf(fabsf(v), 127.0f);
+    float t = __builtin_rintf(a);
+    t = (__fsub_rn(a, t) == 0.5f) ? __fadd_rn(t, 1.0f) : t;
+    const int c = (int)t;
+    return v != v ? 0 : (__builtin_signbit(v) ? -c : c);
+}
+
 // Correctly rounded fp32 square root. v_sqrt_f32 alone is accurate to 1 ulp; the two
 // fma residuals pick between its neighbours (the same correction LLVM's IEEE fsqrt
 // lowering applies), so the result matches a host sqrtf bit for bit. Inputs here are

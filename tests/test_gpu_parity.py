@@ -294,6 +294,49 @@ def test_quant_near_ties(ctx, orc):
     check_quant(ctx, orc, np.ascontiguousarray(X[:, :16]))
 
 
+@pytest.mark.parametrize("K,M", [(1024, 2048), (6912, 132), (2560, 100)])
+def test_quant_near_ties_register_kernel(ctx, orc, K, M):
+    """The same near-tie values through the register kernel (M > 64: 8 tokens per block at
+    K = 1024, 4 per block at K = 6912, the scalar-load path at M = 100): a flagged round is
+    recomputed by the exact division-free code, bit for bit the division's."""
+    say(f"act_quant near ties, register kernel K={K} M={M}")
+    rng = np.random.default_rng(K + M)
+    n = rng.integers(-126, 126, size=(K, M)).astype(np.float64)
+    d = rng.choice([0.0, 2.0 ** -23, -2.0 ** -23, 2.0 ** -17, -2.0 ** -17, 2.0 ** -15, -2.0 ** -15, 2.0 ** -14,
+                    -2.0 ** -14], size=(K, M))
+    X = ((n + 0.5) * (1.0 + d)).astype(np.float32)
+    X[0, :] = 127.0
+    X[1, ::3] = -127.0
+    check_quant(ctx, orc, X)
+    check_quant(ctx, orc, (X * np.float32(0.0371)).astype(np.float32))
+    g = normal((K,), K + 1, 1.0, 0.2)
+    check_quant(ctx, orc, X, g)
+
+
+@pytest.mark.parametrize("K,M", [(2560, 2048), (6912, 132)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_token_regs_special_values(ctx, orc, K, M, norm):
+    """NaN, infinities, all-zero tokens, and tokens whose scale is below 2^-100 (prescaled exact
+    path), subnormal (its reciprocal overflows) or made of subnormals, through the register
+    kernel (M > 64)."""
+    say(f"register kernel special values K={K} M={M} norm={norm}")
+    X = normal((K, M), K + M, 0.0, 1.0)
+    X[5, 0] = np.nan
+    X[7, 1] = np.inf
+    X[9, 2] = -np.inf
+    X[:, 3] = 0.0
+    X[:, 4] *= np.float32(1e-30)
+    X[:, 5] *= np.float32(1e30)
+    X[:, 6] *= np.float32(1e-37)
+    X[:, 7] *= np.float32(1e-43)
+    X[:, 8] = np.float32(1e-45)
+    X[11, 9] = np.nan
+    X[11, 10] = -np.inf
+    X[12, 10] = np.inf
+    g = normal((K,), 4, 1.0, 0.2) if norm else None
+    check_quant(ctx, orc, X, g)
+
+
 # ------------------------------------------------------------------ fast-path GEMV / GEMM
 
 def fast_case(ctx, orc, N, K, M, seed, outliers=False):
