@@ -399,7 +399,7 @@ __device__ __forceinline__ void load_group(float (&x)[R][4], const TokArgs& a, i
 
 // The three passes over one group held in registers: sum of squares -> rms_inv (RMSNorm),
 // per-token absmax -> scale, quantize -> xi / s / rowsum (and the reference container).
-template <int R, bool kVec, int TPB>
+template <int R, bool kVec, int TPB, bool kNormOK>
 __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)[R], const TokArgs& a,
                                              TokShared<TPB>& sh, int g, int w, int fl, int h, int ro)
 {
@@ -411,7 +411,7 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
     const int mt = g * TPB + 4 * h;       // first of this thread's four tokens
 
     // ---- pass 1: sum of squares -> rms_inv, then normalize in place
-    if (a.norm)
+    if (kNormOK && a.norm)
     {
         float acc[NP][4];
 #pragma unroll
@@ -604,7 +604,7 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
 // 128-byte row segment of X meet in one L2.
 // (R = 12 and 14 with 4-token blocks: at least 3 waves per SIMD, 168 registers; left to itself the
 // compiler took 171 for R = 14, i.e. 2 waves per SIMD, too few loads in flight at prefill sizes)
-template <int R, bool kVec, int TPB>
+template <int R, bool kVec, int TPB, bool kNormOK>
 __global__ __launch_bounds__(reg_waves<TPB> * kWave, ((R == 12 || R == 14) && TPB == 4) ? 3 : 1) void k_token_regs(TokArgs a, const float* __restrict__ gamma,
                                                                   int n_groups)
 {
@@ -622,7 +622,7 @@ __global__ __launch_bounds__(reg_waves<TPB> * kWave, ((R == 12 || R == 14) && TP
     float x[R][4];
     load_group<R, kVec, TPB>(x, a, g, ro, h);
     float gm[R];
-    if (a.norm)
+    if (kNormOK && a.norm)
     {
         const __amdgpu_buffer_rsrc_t rg =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(gamma), (short)0, a.K * 4, 0x00020000);
@@ -630,7 +630,7 @@ __global__ __launch_bounds__(reg_waves<TPB> * kWave, ((R == 12 || R == 14) && TP
         for (int r = 0; r < R; ++r)
             gm[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, (uint32_t)(RR * r + ro) * 4u, 0, 0));
     }
-    finish_group<R, kVec, TPB>(x, gm, a, sh, g, w, fl, h, ro);
+    finish_group<R, kVec, TPB, kNormOK>(x, gm, a, sh, g, w, fl, h, ro);
 }
 
 // Decode-sized M (up to 64 tokens): one token per block, 512 threads. Thread t owns sum-of-squares
@@ -921,10 +921,10 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_amax(const float* __res
 constexpr size_t kSmallM = 32;
 constexpr size_t kOneTokMaxM = NNHIP_ONE_TOK_MAX_M;
 
-template <int TPB, int R>
+template <int TPB, int R, bool kNormOK = true>
 void launch_regs_r(bool vec, hipStream_t st, int n_groups, const TokArgs& a, const float* gamma)
 {
-    auto kern = vec ? k_token_regs<R, true, TPB> : k_token_regs<R, false, TPB>;
+    auto kern = vec ? k_token_regs<R, true, TPB, kNormOK> : k_token_regs<R, false, TPB, kNormOK>;
     hipLaunchKernelGGL(kern, dim3((unsigned)n_groups), dim3(reg_waves<TPB> * kWave), 0, st, a, gamma, n_groups);
 }
 
@@ -969,12 +969,22 @@ static hipError_t launch_token_kernel(hipStream_t st, const float* X, const floa
         // M=2048: 14.2 against 15.7 us; 2560 x 32768, where the smaller blocks keep more waves
         // resident: 193 against 159 us); 4 tokens (16-byte segments, 8 waves) otherwise
         TokArgs a{X, norm, eps, inv_f, (int)K, (int)M, (int)Kp, mode, xi, s, rowsum, xq_ref, fout};
-        const bool tok8 = vec && rounds <= NNHIP_TOK8_MAX_ROUNDS && M <= 8192;
+        // Without RMSNorm the 8-token layout also serves 11 to 14 rounds (K <= 7168: the FFN
+        // width 6912): those instantiations leave the norm passes out, which keeps them within
+        // the 128 registers (K=6912, M=2048: 16-byte segments read the 56 MB at ~4 TB/s).
+        const bool tok8 = vec && M <= 8192 && (rounds <= NNHIP_TOK8_MAX_ROUNDS || (!norm && mode == 0 && rounds <= 14));
         const int n_groups = (int)ceil_div(M, (size_t)(tok8 ? 8 : 4));
-        const bool launched =
-            tok8 ? launch_regs_pick<8, 1, 2, 3, 4, 5, 6, 8, 10>(rounds, vec, st, n_groups, a, gamma)
-                 : launch_regs_pick<4, 1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, vec, st, n_groups,
-                                                                                     a, gamma);
+        bool launched;
+        if (tok8 && rounds > NNHIP_TOK8_MAX_ROUNDS)
+        {
+            if (rounds <= 12) launch_regs_r<8, 12, false>(vec, st, n_groups, a, gamma);
+            else launch_regs_r<8, 14, false>(vec, st, n_groups, a, gamma);
+            launched = true;
+        }
+        else
+            launched = tok8 ? launch_regs_pick<8, 1, 2, 3, 4, 5, 6, 8, 10>(rounds, vec, st, n_groups, a, gamma)
+                            : launch_regs_pick<4, 1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, vec, st,
+                                                                                                n_groups, a, gamma);
         if (launched) return hipGetLastError();
     }
     if (M <= kSmallM)
