@@ -841,13 +841,18 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_amax(const float* __res
     const int row = w * 32 + rq * 4 + j;  // row within a chunk
     const int mq = m0 + 4 * hq;           // first of the lane's four tokens
 
-    float sc[4], rc[4];
+    // per token: s, fl(1/s) for the fast codes, and the exact path's prescale xs (2^100 below
+    // s = 2^-100, else 1), s * xs and its reciprocal
+    float sc[4], rc[4], xs[4], se[4], re[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
     {
         const float mx = mq + i < M ? __builtin_bit_cast(float, amax[mq + i]) : 0.0f;
         sc[i] = __fmul_rn(mx, 1.0f / 127.0f);
         rc[i] = quant_rcp(sc[i]);
+        xs[i] = sc[i] < 0x1p-100f ? 0x1p100f : 1.0f;
+        se[i] = __fmul_rn(sc[i], xs[i]);
+        re[i] = quant_rcp(se[i]);
     }
     const bool rc_inf = isinf(rc[0]) || isinf(rc[1]) || isinf(rc[2]) || isinf(rc[3]);
 
@@ -893,7 +898,7 @@ __global__ __launch_bounds__(kQuantThreads) void k_quant_amax(const float* __res
             for (int i = 0; i < 4; ++i) q[i] = quantize_guess(x[u][i], rc[i], amb);
             if (amb)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) q[i] = quantize_fast(x[u][i], sc[i], rc[i]);
+                for (int i = 0; i < 4; ++i) q[i] = quantize_exact(__fmul_rn(x[u][i], xs[i]), se[i], re[i]);
             if (c + kQuantU < n_chunks) load(x[u], c + kQuantU);
             const uint32_t col = quad_transpose(pack4(q[0], q[1], q[2], q[3]), j);
             tsum = __builtin_amdgcn_sdot4((int)col, 0x01010101, tsum, false);

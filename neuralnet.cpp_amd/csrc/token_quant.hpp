@@ -28,8 +28,8 @@ __device__ __forceinline__ int quantize_one(float x, float s)
     return (int)roundf(v);
 }
 
-// Per-token reciprocal for quantize_fast: fl(1/s), 0 when s == 0 (every code is then 0, as
-// quantize_one gives), +inf when 1/s overflows (the caller then takes the exact path).
+// Per-token reciprocal for the division-free codes: fl(1/s), 0 when s == 0 (every code is then
+// 0, as quantize_one gives), +inf when 1/s overflows (every product is then flagged).
 __device__ __forceinline__ float quant_rcp(float s)
 {
     return s == 0.0f ? 0.0f : __fdiv_rn(1.0f, s);
@@ -40,17 +40,8 @@ __device__ __forceinline__ float quant_rcp(float s)
 // |x/s| <= 128. Unless y lies within 2^-14 of a half-integer, round-to-nearest-even of y then
 // equals round-half-away-from-zero of fl(x/s) (no tie and no integer boundary in between), and
 // clamping after rounding equals clamping before (127 is an integer, and values past 127.5
-// round to 127 or more either way). Near a half-integer, for NaN inputs and when 1/s
-// overflowed, the exact quantize_one decides; the result is the same code bit for bit.
-__device__ __forceinline__ int quantize_fast(float x, float s, float r)
-{
-    const float y = __fmul_rn(x, r);
-    const float t = __builtin_rintf(y);
-    if (!(fabsf(y - t) < 0.5f - 0x1p-14f) || isinf(r)) return quantize_one(x, s);
-    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
-}
-
-// The fast-path code alone; `amb` is set when the exact path must decide (see quantize_fast).
+// round to 127 or more either way). Near a half-integer, for NaN and inf products and when 1/s
+// overflowed, `amb` is set and the caller takes quantize_exact; the code is the same bit for bit.
 __device__ __forceinline__ int quantize_guess(float x, float r, bool& amb)
 {
     const float y = __fmul_rn(x, r);
@@ -305,10 +296,16 @@ __device__ __forceinline__ void one_token_finish(float (&x)[R], const TokArgs& a
     int q[R];
     bool amb = isinf(rc);
 #pragma unroll
-    for (int r = 0; r < R; ++r) q[r] = quantize_guess(x[r], rc, amb);
+    for (int r = 0; r < R; ++r) q[r] = quantize_code(x[r], rc, amb);
     if (amb)
+    {
+        // a flagged element: the thread's codes again through the exact division-free path, on
+        // x * xs / (s * xs) with the power-of-two prescale that keeps s * xs >= 2^-100
+        const float xs = sc < 0x1p-100f ? 0x1p100f : 1.0f;
+        const float se = __fmul_rn(sc, xs), re = quant_rcp(se);
 #pragma unroll
-        for (int r = 0; r < R; ++r) q[r] = quantize_fast(x[r], sc, rc);
+        for (int r = 0; r < R; ++r) q[r] = quantize_exact(__fmul_rn(x[r], xs), se, re);
+    }
     int tsum = 0;
     const int wpr = (a.M + 3) / 4;
 #pragma unroll
