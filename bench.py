@@ -460,15 +460,30 @@ def decode_c5_line(ctx, torch, stream, steps, out):
 
 
 def profiled_traffic():
-    """Calibrated HBM bytes per headline launch from the committed PMC summary, or None."""
+    """Calibrated HBM bytes per headline launch from the committed PMC summary, or None when the
+    summary is missing or was taken on other kernel sources: it records the sha256 of the grouped
+    GEMV's source files, recomputed here (the .git history does not travel to the GPU box)."""
+    import hashlib
     import re
     path = os.path.join(ROOT, "profiles", "k_gemv_grouped_m1_layerstack_pmc.md")
     try:
         with open(path) as f:
-            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read())
-        return int(m.group(1)) if m else None
+            text = f.read()
+        h = hashlib.sha256()
+        for src in ("k_gemv.hip", "gemv_tile.hpp"):
+            with open(os.path.join(ROOT, "neuralnet.cpp_amd", "csrc", src), "rb") as f:
+                h.update(f.read())
     except OSError:
         return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
+    k = re.search(r"kernel_source_sha256:\s*([0-9a-f]+)", text)
+    if not m or not k:
+        return None
+    if k.group(1) != h.hexdigest()[:len(k.group(1))]:
+        print("bench.py: the PMC summary was taken on other k_gemv sources; roofline.traffic omitted "
+              "(re-take profiles/k_gemv_grouped_m1_layerstack_pmc.md)", file=sys.stderr)
+        return None
+    return int(m.group(1))
 
 
 def copy_probe(mib):

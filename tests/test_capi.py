@@ -6,6 +6,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -84,3 +85,23 @@ def test_fnv1a64_output_hash(nnhip):
     # f32 values hash their little-endian bytes
     x = np.array([1.0, -2.5], np.float32)
     assert nnhip.fnv1a64(x) == nnhip.fnv1a64(x.view(np.uint8))
+
+
+def test_bench_traffic_needs_matching_kernel_sources(tmp_path, monkeypatch, capsys):
+    """bench.py's roofline.traffic comes from the committed PMC summary only while the grouped
+    GEMV's sources hash to the value the summary records; after any change it is omitted."""
+    import shutil
+    sys.path.insert(0, ROOT)
+    import bench
+    assert bench.profiled_traffic() is not None  # the committed summary matches the tree
+    (tmp_path / "profiles").mkdir()
+    (tmp_path / "neuralnet.cpp_amd" / "csrc").mkdir(parents=True)
+    shutil.copy(os.path.join(ROOT, "profiles", "k_gemv_grouped_m1_layerstack_pmc.md"), tmp_path / "profiles")
+    for src in ("k_gemv.hip", "gemv_tile.hpp"):
+        shutil.copy(os.path.join(ROOT, "neuralnet.cpp_amd", "csrc", src), tmp_path / "neuralnet.cpp_amd" / "csrc")
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    assert bench.profiled_traffic() is not None
+    with open(tmp_path / "neuralnet.cpp_amd" / "csrc" / "k_gemv.hip", "a") as f:
+        f.write("\n// changed\n")
+    assert bench.profiled_traffic() is None
+    assert "other k_gemv sources" in capsys.readouterr().err
