@@ -544,6 +544,23 @@ nnhip_status nnhip_attention_decode_tokens(nnhip_ctx* ctx, const float* q, const
                                            const float* rope_cos, const float* rope_sin, float* k_cache,
                                            float* v_cache, size_t max_len, float scale, float* out);
 
+/* KV caches of IEEE binary16 elements (compute = F16): the reference creates each layer's KV
+ * caches in the profile's compute precision, engine.create_tensor(seq_len_, d_model_, p_.compute)
+ * (include/neuralnet.cpp/compute_layer_gpt.hpp:764-765), F16 under the t1_58 preset
+ * (src/t1_58_test.cpp:668-690). The same attention as nnhip_attention_decode /
+ * nnhip_attention_decode_tokens with k_cache / v_cache holding f16 bit patterns: the appended
+ * rotated key and value are rounded to the nearest f16 (ties to even) and this call's scores use
+ * the rounded values, as every later call reads them; cached elements are widened exactly and
+ * q, k, v, out and the arithmetic stay f32. Half the cache bytes per call. */
+nnhip_status nnhip_attention_decode_h(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                      size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                      const float* rope_cos, const float* rope_sin, uint16_t* k_cache,
+                                      uint16_t* v_cache, size_t max_len, float scale, float* out);
+nnhip_status nnhip_attention_decode_tokens_h(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                             size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                             const float* rope_cos, const float* rope_sin, uint16_t* k_cache,
+                                             uint16_t* v_cache, size_t max_len, float scale, float* out);
+
 /* ---- batched prefill (config C5's 2048-token context): T new tokens of each of B sequences at
  *      positions pos0 .. pos0 + T - 1 in one pass. The reference fills the cache by running
  *      forward_step once per context token (GPTModel::generate, include/neuralnet.cpp/
@@ -560,6 +577,12 @@ nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v,
                                  size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin, float* k_cache,
                                  float* v_cache, size_t max_len);
 
+/* nnhip_kv_cache_fill into f16 caches (compute = F16, compute_layer_gpt.hpp:764-765): each rotated
+ * key and value rounded to the nearest f16, the rows nnhip_attention_decode_h would append. */
+nnhip_status nnhip_kv_cache_fill_h(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,
+                                   size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin,
+                                   uint16_t* k_cache, uint16_t* v_cache, size_t max_len);
+
 /* Causal attention of the T tokens over caches already holding rows [0, pos0 + T) (after
  * nnhip_kv_cache_fill): out (H*dk, B*T), column b*T + t = per query head h the softmax
  * ((rot(q_h) . K^T) * scale) . V over cache rows [0, pos0 + t] of sequence b, KV head h / (H/Hkv),
@@ -571,6 +594,13 @@ nnhip_status nnhip_attention_prefill(nnhip_ctx* ctx, const float* q, const float
                                      size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0,
                                      const float* rope_cos, const float* rope_sin, size_t max_len, float scale,
                                      float* out);
+
+/* nnhip_attention_prefill over f16 caches (compute = F16, compute_layer_gpt.hpp:764-765): the
+ * cached elements widened exactly, everything else as nnhip_attention_prefill. */
+nnhip_status nnhip_attention_prefill_h(nnhip_ctx* ctx, const float* q, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, size_t B, size_t T, size_t H, size_t Hkv, size_t dk,
+                                       size_t pos0, const float* rope_cos, const float* rope_sin, size_t max_len,
+                                       float scale, float* out);
 
 /* dst (rows, n): column j = column col0 + j * stride of src (rows, src_cols), e.g. the last token of
  * each sequence after a prefill (col0 = T - 1, stride = T) for the LM head. Replaces the reference's

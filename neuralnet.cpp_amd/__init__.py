@@ -138,9 +138,15 @@ SIGNATURES = {
                                      _vp]),
     "nnhip_attention_decode_tokens": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _sz,
                                             _f, _vp]),
+    "nnhip_attention_decode_h": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _f,
+                                       _vp]),
+    "nnhip_attention_decode_tokens_h": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp,
+                                              _sz, _f, _vp]),
     "nnhip_add": (_st, [_vp, _vp, _vp, _sz, _vp]),
     "nnhip_kv_cache_fill": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz]),
+    "nnhip_kv_cache_fill_h": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _sz]),
     "nnhip_attention_prefill": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _f, _vp]),
+    "nnhip_attention_prefill_h": (_st, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _f, _vp]),
     "nnhip_copy_columns": (_st, [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp]),
     "nnhip_embedding_gather": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "nnhip_embedding_gather_tokens": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -665,46 +671,56 @@ class Context:
                          scale: float, cos=None, sin=None, out=None, tokens: bool = False):
         """q (H*dk, B), k/v (Hkv*dk, B), pos (B) int32 device, caches (B, max_len, Hkv*dk) updated in
         place (row pos[b]); cos/sin (max_len, dk/2) device tables or None. Returns out (H*dk, B).
-        With tokens, q (B, H*dk), k/v (B, Hkv*dk) and out (B, H*dk) (nnhip_attention_decode_tokens)."""
+        With tokens, q (B, H*dk), k/v (B, Hkv*dk) and out (B, H*dk) (nnhip_attention_decode_tokens).
+        float16 caches (compute = F16) run the _h entry points; both caches have one dtype."""
         torch = self._torch
         B = q.shape[0] if tokens else q.shape[1]
         max_len = k_cache.shape[1]
+        ct = self._cache_dtype(k_cache, v_cache)
         if out is None:
             out = self._empty((B, H * dk) if tokens else (H * dk, B), torch.float32)
         self._bind_stream()
-        entry = lib().nnhip_attention_decode_tokens if tokens else lib().nnhip_attention_decode
-        _check(entry(
+        name = ("nnhip_attention_decode_tokens" if tokens else "nnhip_attention_decode") + \
+            ("_h" if ct == torch.float16 else "")
+        _check(getattr(lib(), name)(
             self.h, self._dev(q, torch.float32, "q"), self._dev(k, torch.float32, "k"),
             self._dev(v, torch.float32, "v"), B, H, Hkv, dk, self._dev(pos, torch.int32, "pos"), len_bound,
             self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
-            self._dev(k_cache, torch.float32, "k_cache"), self._dev(v_cache, torch.float32, "v_cache"), max_len,
-            scale, self._dev(out, torch.float32, "out")),
-               "nnhip_attention_decode_tokens" if tokens else "nnhip_attention_decode")
+            self._dev(k_cache, ct, "k_cache"), self._dev(v_cache, ct, "v_cache"), max_len,
+            scale, self._dev(out, torch.float32, "out")), name)
         return out
 
-    def kv_cache_fill(self, k, v, B: int, T: int, Hkv: int, dk: int, pos0: int, k_cache, v_cache, cos=None, sin=None):
-        """Append T tokens of each of B sequences (k / v (Hkv*dk, B*T)) to the caches at rows pos0 + t."""
+    def _cache_dtype(self, k_cache, v_cache):
+        """The caches' element type: float32, or float16 under compute = F16 (both alike)."""
         torch = self._torch
+        if k_cache.dtype != v_cache.dtype or k_cache.dtype not in (torch.float32, torch.float16):
+            raise NNHipError(1, f"caches must both be float32 or both float16 (got {k_cache.dtype}, {v_cache.dtype})")
+        return k_cache.dtype
+
+    def kv_cache_fill(self, k, v, B: int, T: int, Hkv: int, dk: int, pos0: int, k_cache, v_cache, cos=None, sin=None):
+        """Append T tokens of each of B sequences (k / v (Hkv*dk, B*T)) to the caches at rows pos0 + t
+        (float16 caches: nnhip_kv_cache_fill_h)."""
+        torch = self._torch
+        ct = self._cache_dtype(k_cache, v_cache)
+        name = "nnhip_kv_cache_fill" + ("_h" if ct == torch.float16 else "")
         self._bind_stream()
-        _check(lib().nnhip_kv_cache_fill(self.h, self._dev(k, torch.float32, "k"), self._dev(v, torch.float32, "v"),
-                                         B, T, Hkv, dk, pos0, self._dev(cos, torch.float32, "cos"),
-                                         self._dev(sin, torch.float32, "sin"),
-                                         self._dev(k_cache, torch.float32, "k_cache"),
-                                         self._dev(v_cache, torch.float32, "v_cache"), k_cache.shape[1]),
-               "nnhip_kv_cache_fill")
+        _check(getattr(lib(), name)(self.h, self._dev(k, torch.float32, "k"), self._dev(v, torch.float32, "v"),
+                                    B, T, Hkv, dk, pos0, self._dev(cos, torch.float32, "cos"),
+                                    self._dev(sin, torch.float32, "sin"), self._dev(k_cache, ct, "k_cache"),
+                                    self._dev(v_cache, ct, "v_cache"), k_cache.shape[1]), name)
 
     def attention_prefill(self, q, k_cache, v_cache, B: int, T: int, H: int, Hkv: int, dk: int, pos0: int,
                           scale: float, cos=None, sin=None, out=None):
         """Causal attention of T tokens per sequence (q (H*dk, B*T)) over caches holding rows [0, pos0 + T)."""
         torch = self._torch
+        ct = self._cache_dtype(k_cache, v_cache)
+        name = "nnhip_attention_prefill" + ("_h" if ct == torch.float16 else "")
         Y = out if out is not None else self._empty((H * dk, B * T), torch.float32)
         self._bind_stream()
-        _check(lib().nnhip_attention_prefill(self.h, self._dev(q, torch.float32, "q"),
-                                             self._dev(k_cache, torch.float32, "k_cache"),
-                                             self._dev(v_cache, torch.float32, "v_cache"), B, T, H, Hkv, dk, pos0,
-                                             self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
-                                             k_cache.shape[1], scale, self._dev(Y, torch.float32, "out")),
-               "nnhip_attention_prefill")
+        _check(getattr(lib(), name)(self.h, self._dev(q, torch.float32, "q"), self._dev(k_cache, ct, "k_cache"),
+                                    self._dev(v_cache, ct, "v_cache"), B, T, H, Hkv, dk, pos0,
+                                    self._dev(cos, torch.float32, "cos"), self._dev(sin, torch.float32, "sin"),
+                                    k_cache.shape[1], scale, self._dev(Y, torch.float32, "out")), name)
         return Y
 
     def copy_columns(self, src, col0: int, stride: int, n: int, out=None):

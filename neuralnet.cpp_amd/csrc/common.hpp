@@ -302,10 +302,11 @@ hipError_t launch_trit_transpose(hipStream_t st, const uint32_t* A, size_t K, si
 // ---- batched decode step (k_decode.hip)
 size_t attn_chunks(size_t len_bound);
 size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t len_bound);
+// caches of f32, or of f16 elements when cache_f16 (compute = F16); tm: q, k, v and out token-major
 hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
                               size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
-                              const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
-                              float* out, int num_cus, bool tm = false);  // tm: q, k, v and out token-major
+                              const float* sinT, void* kc, void* vc, bool cache_f16, size_t max_len, float scale,
+                              float* part, float* out, int num_cus, bool tm = false);
 hipError_t launch_add(hipStream_t st, const float* x, const float* y, size_t n, float* out);
 // dst (rows, n) column j = src (rows, src_cols) column col0 + j * stride (k_decode.hip)
 hipError_t launch_copy_cols(hipStream_t st, const float* src, size_t rows, size_t src_cols, size_t col0, size_t stride,
@@ -314,10 +315,11 @@ hipError_t launch_copy_cols(hipStream_t st, const float* src, size_t rows, size_
 // ---- batched prefill (k_prefill.hip): T tokens of each of B sequences at positions pos0 + t
 bool prefill_dk_supported(size_t dk);
 hipError_t launch_kv_fill(hipStream_t st, const float* k, const float* v, size_t B, size_t T, size_t Hkv, size_t dk,
-                          size_t pos0, const float* cosT, const float* sinT, float* kc, float* vc, size_t max_len);
-hipError_t launch_attn_prefill(hipStream_t st, const float* q, const float* kc, const float* vc, size_t B, size_t T,
-                               size_t H, size_t Hkv, size_t dk, size_t pos0, const float* cosT, const float* sinT,
-                               size_t max_len, float scale, float* out);
+                          size_t pos0, const float* cosT, const float* sinT, void* kc, void* vc, bool cache_f16,
+                          size_t max_len);
+hipError_t launch_attn_prefill(hipStream_t st, const float* q, const void* kc, const void* vc, bool cache_f16,
+                               size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0, const float* cosT,
+                               const float* sinT, size_t max_len, float scale, float* out);
 hipError_t launch_embed(hipStream_t st, const float* table, const int32_t* ids, size_t V, size_t d, size_t B, bool tm,
                         float* out);
 hipError_t launch_argmax(hipStream_t st, const float* L, size_t V, size_t B, int32_t* ids, bool rows = false,

@@ -57,8 +57,8 @@ struct AttnArgs
     const int32_t* pos;
     const float* cosT;
     const float* sinT;
-    float* kc;
-    float* vc;
+    void* kc;  // caches of CT elements (float, or _Float16 under compute = F16)
+    void* vc;
     float* part;
     float* out;
     int B, H, Hkv, R, max_len, len_bound, nchunk;
@@ -107,6 +107,28 @@ __device__ __forceinline__ float4 ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff,
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
 }
 
+// Four cache elements at byte offset voff + soff as floats: 16 bytes of f32, or 8 bytes of f16
+// widened exactly (the same cache policy).
+template <typename CT>
+__device__ __forceinline__ float4 ld_c4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    if constexpr (sizeof(CT) == 4) return ld_f4(r, voff, soff);
+    else
+    {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 h = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
+        return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    }
+}
+
+// x as the cache stores it: itself in an f32 cache, the nearest f16 (ties to even) in an f16 one
+template <typename CT>
+__device__ __forceinline__ float cache_round(float x)
+{
+    if constexpr (sizeof(CT) == 4) return x;
+    else return (float)(_Float16)x;
+}
+
 // 4 bytes at byte offset off of the resource (0 when out of range), default cache policy
 __device__ __forceinline__ float ld_f1(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
@@ -125,7 +147,7 @@ __device__ __forceinline__ void lds_only_barrier()
     asm volatile("" ::: "memory");
 }
 
-template <int DK, int RT, bool kFinal>
+template <int DK, int RT, bool kFinal, typename CT>
 __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_MINW : 1) void k_attn_chunk(AttnArgs a)
 {
     constexpr int HALF = DK / 2;
@@ -234,7 +256,9 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         // chunk or on the new position read zeros without a branch, so every load of a pass
         // group is in flight at once; the new position's key is selected from LDS afterwards.
         const int pg = tid >> 3, j8 = tid & 7;
-        const __amdgpu_buffer_rsrc_t rk = attn_rsrc(a.kc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
+        constexpr uint32_t ES = sizeof(CT);  // bytes per cache element
+        const __amdgpu_buffer_rsrc_t rk =
+            attn_rsrc(static_cast<const CT*>(a.kc) + seq_off, (uint32_t)((size_t)a.max_len * rstride * ES));
         float4 kv[PB][F4];
         auto load_keys = [&](int pass0) {
 #pragma unroll
@@ -242,9 +266,9 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             {
                 const int tl = (pass0 + u) * 32 + pg;
                 const int t = t0 + tl;
-                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
+                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * ES : 0x80000000u;
 #pragma unroll
-                for (int i = 0; i < F4; ++i) kv[u][i] = ld_f4(rk, row, 16u * (j8 + 8 * i));
+                for (int i = 0; i < F4; ++i) kv[u][i] = ld_c4<CT>(rk, row, 4u * ES * (j8 + 8 * i));
             }
         };
         load_keys(0);
@@ -272,21 +296,31 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             {
                 float y0 = kx0, y1 = kx1;
                 if (a.cosT) rope_pair(kx0, kx1, kcs, ksn, y0, y1);
-                kf[tid] = y0;
-                kf[tid + HALF] = y1;
+                kf[tid] = cache_round<CT>(y0);
+                kf[tid + HALF] = cache_round<CT>(y1);
             }
-            if (tid < DK) vf[tid] = vx;
+            if (tid < DK) vf[tid] = cache_round<CT>(vx);
         }
         // LDS-only barrier: a workgroup fence (__syncthreads) would also wait for the key loads
         lds_only_barrier();
         if (has_new)
         {
-            float4* krow = reinterpret_cast<float4*>(a.kc + seq_off + (size_t)p * rstride);
-            float4* vrow = reinterpret_cast<float4*>(a.vc + seq_off + (size_t)p * rstride);
+            CT* krow = static_cast<CT*>(a.kc) + seq_off + (size_t)p * rstride;
+            CT* vrow = static_cast<CT*>(a.vc) + seq_off + (size_t)p * rstride;
             for (int i = tid; i < Q4; i += kAttnThreads)
             {
-                krow[i] = kn_s[i];
-                vrow[i] = vn_s[i];
+                if constexpr (sizeof(CT) == 4)
+                {
+                    reinterpret_cast<float4*>(krow)[i] = kn_s[i];
+                    reinterpret_cast<float4*>(vrow)[i] = vn_s[i];
+                }
+                else
+                {
+                    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                    const float4 kq = kn_s[i], vq = vn_s[i];
+                    reinterpret_cast<h4*>(krow)[i] = h4{(_Float16)kq.x, (_Float16)kq.y, (_Float16)kq.z, (_Float16)kq.w};
+                    reinterpret_cast<h4*>(vrow)[i] = h4{(_Float16)vq.x, (_Float16)vq.y, (_Float16)vq.z, (_Float16)vq.w};
+                }
             }
         }
 
@@ -294,15 +328,16 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         constexpr int VR = kAttnT / NG;
         const int vg = tid / VL, vi = tid % VL;
         float4 vv[VR];
-        const __amdgpu_buffer_rsrc_t rv = attn_rsrc(a.vc + seq_off, (uint32_t)((size_t)a.max_len * rstride * 4));
+        const __amdgpu_buffer_rsrc_t rv =
+            attn_rsrc(static_cast<const CT*>(a.vc) + seq_off, (uint32_t)((size_t)a.max_len * rstride * ES));
         auto load_values = [&]() {
 #pragma unroll
             for (int u = 0; u < VR; ++u)
             {
                 const int tl = vg + u * NG;
                 const int t = t0 + tl;
-                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * 4u : 0x80000000u;
-                vv[u] = ld_f4(rv, row, 16u * vi);
+                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * ES : 0x80000000u;
+                vv[u] = ld_c4<CT>(rv, row, 4u * ES * vi);
             }
         };
 
@@ -524,14 +559,14 @@ __global__ __launch_bounds__(DK) void k_attn_merge(AttnArgs a)
 }
 
 // Persistent grid: as many work-groups as fit the device at once (at most one per item).
-template <int DK, int RT, bool kFinal>
+template <int DK, int RT, bool kFinal, typename CT>
 hipError_t launch_attn_variant(hipStream_t st, const AttnArgs& a, int num_cus)
 {
     static int per_cu = 0;
     if (per_cu == 0)
     {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_chunk<DK, RT, kFinal>, kAttnThreads, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_chunk<DK, RT, kFinal, CT>, kAttnThreads, 0) !=
                 hipSuccess ||
             n < 1)
             n = 1;
@@ -540,26 +575,26 @@ hipError_t launch_attn_variant(hipStream_t st, const AttnArgs& a, int num_cus)
     const long total = (long)a.nchunk * a.Hkv * a.B;
     const long cap = (long)per_cu * (num_cus > 0 ? num_cus : 256);
     const unsigned grid = (unsigned)(total < cap ? total : cap);
-    k_attn_chunk<DK, RT, kFinal><<<dim3(grid), kAttnThreads, 0, st>>>(a);
+    k_attn_chunk<DK, RT, kFinal, CT><<<dim3(grid), kAttnThreads, 0, st>>>(a);
     return hipGetLastError();
 }
 
 // query heads per KV head: 1, 2, 4 or 8 at compile time (3, 5, 6, 7 run as the next power of two
 // with the extra heads masked)
-template <int DK, bool kFinal>
+template <int DK, bool kFinal, typename CT>
 hipError_t launch_attn_r(hipStream_t st, const AttnArgs& a, int num_cus)
 {
-    if (a.R == 1) return launch_attn_variant<DK, 1, kFinal>(st, a, num_cus);
-    if (a.R == 2) return launch_attn_variant<DK, 2, kFinal>(st, a, num_cus);
-    if (a.R <= 4) return launch_attn_variant<DK, 4, kFinal>(st, a, num_cus);
-    return launch_attn_variant<DK, 8, kFinal>(st, a, num_cus);
+    if (a.R == 1) return launch_attn_variant<DK, 1, kFinal, CT>(st, a, num_cus);
+    if (a.R == 2) return launch_attn_variant<DK, 2, kFinal, CT>(st, a, num_cus);
+    if (a.R <= 4) return launch_attn_variant<DK, 4, kFinal, CT>(st, a, num_cus);
+    return launch_attn_variant<DK, 8, kFinal, CT>(st, a, num_cus);
 }
 
-template <int DK>
+template <int DK, typename CT>
 hipError_t launch_attn_dk(hipStream_t st, const AttnArgs& a, int num_cus)
 {
-    if (a.nchunk == 1) return launch_attn_r<DK, true>(st, a, num_cus);
-    const hipError_t e = launch_attn_r<DK, false>(st, a, num_cus);
+    if (a.nchunk == 1) return launch_attn_r<DK, true, CT>(st, a, num_cus);
+    const hipError_t e = launch_attn_r<DK, false, CT>(st, a, num_cus);
     if (e != hipSuccess) return e;
     k_attn_merge<DK><<<dim3(a.B * a.H), DK, 0, st>>>(a);
     return hipGetLastError();
@@ -677,16 +712,26 @@ size_t attn_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk, size_t le
 
 hipError_t launch_attn_decode(hipStream_t st, const float* q, const float* k, const float* v, size_t B, size_t H,
                               size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound, const float* cosT,
-                              const float* sinT, float* kc, float* vc, size_t max_len, float scale, float* part,
-                              float* out, int num_cus, bool out_tm)
+                              const float* sinT, void* kc, void* vc, bool cache_f16, size_t max_len, float scale,
+                              float* part, float* out, int num_cus, bool out_tm)
 {
     AttnArgs a{q, k, v, pos, cosT, sinT, kc, vc, part, out, (int)B, (int)H, (int)Hkv, (int)(H / Hkv),
                (int)max_len, (int)len_bound, (int)attn_chunks(len_bound), scale, out_tm ? 1 : 0, out_tm ? 1 : 0};
+    if (cache_f16)
+    {
+        switch (dk)
+        {
+        case 64: return launch_attn_dk<64, _Float16>(st, a, num_cus);
+        case 128: return launch_attn_dk<128, _Float16>(st, a, num_cus);
+        case 256: return launch_attn_dk<256, _Float16>(st, a, num_cus);
+        default: return hipErrorInvalidValue;
+        }
+    }
     switch (dk)
     {
-    case 64: return launch_attn_dk<64>(st, a, num_cus);
-    case 128: return launch_attn_dk<128>(st, a, num_cus);
-    case 256: return launch_attn_dk<256>(st, a, num_cus);
+    case 64: return launch_attn_dk<64, float>(st, a, num_cus);
+    case 128: return launch_attn_dk<128, float>(st, a, num_cus);
+    case 256: return launch_attn_dk<256, float>(st, a, num_cus);
     default: return hipErrorInvalidValue;
     }
 }

@@ -28,7 +28,9 @@
 // padded to dk + 4 floats in LDS, so the 16-byte reads of 8 consecutive rows cover all banks.
 // Work-groups are issued heaviest first (the last query blocks attend over the most keys).
 // f32 throughout; the accumulation order differs from a sequential dot product (results within
-// 2e-6 relative of a float64 evaluation on the test data).
+// 2e-6 relative of a float64 evaluation on the test data). Caches of f16 elements (compute = F16)
+// are widened exactly when a tile is staged; the fill rounds the rotated keys and the values to
+// the nearest f16 (ties to even), as the decode append does.
 #include "common.hpp"
 
 #include <cmath>
@@ -58,6 +60,19 @@ __device__ __forceinline__ float4 ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t off)
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Four cache elements at byte offset off as floats (f32, or f16 widened exactly)
+template <typename CT>
+__device__ __forceinline__ float4 ld_c4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    if constexpr (sizeof(CT) == 4) return ld_f4(r, off);
+    else
+    {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 h = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+        return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    }
+}
+
 // (x0, x1) = (x[j], x[j + dk/2]) -> x*cos + rotate_half(x)*sin: two rounded products and a
 // rounded sum per output, as the decode append does.
 __device__ __forceinline__ void pf_rope(float x0, float x1, float cs, float sn, float& y0, float& y1)
@@ -71,11 +86,11 @@ __device__ __forceinline__ void pf_rope(float x0, float x1, float cs, float sn, 
 // Block = (32 tokens, KV head g): the head's dk feature rows of k and v for the 32 tokens are
 // read along tokens (coalesced), transposed through LDS and written as cache rows (coalesced
 // along features), the keys rotated at their positions.
-template <int DK>
+template <int DK, typename CT>
 __global__ __launch_bounds__(256) void k_kv_fill(const float* __restrict__ k, const float* __restrict__ v, int B, int T,
                                                  int Hkv, int pos0, const float* __restrict__ cosT,
-                                                 const float* __restrict__ sinT, float* __restrict__ kc,
-                                                 float* __restrict__ vc, int max_len)
+                                                 const float* __restrict__ sinT, CT* __restrict__ kc,
+                                                 CT* __restrict__ vc, int max_len)
 {
     constexpr int HALF = DK / 2;
     __shared__ float sk[DK][kPQ + 1];
@@ -101,14 +116,14 @@ __global__ __launch_bounds__(256) void k_kv_fill(const float* __restrict__ k, co
         if (m >= M) continue;
         const int b = m / T, t = m % T;
         const int p = pos0 + t;
-        float* kr = kc + ((size_t)b * (size_t)max_len + (size_t)p) * (size_t)row + (size_t)g * DK;
-        float* vr = vc + ((size_t)b * (size_t)max_len + (size_t)p) * (size_t)row + (size_t)g * DK;
+        CT* kr = kc + ((size_t)b * (size_t)max_len + (size_t)p) * (size_t)row + (size_t)g * DK;
+        CT* vr = vc + ((size_t)b * (size_t)max_len + (size_t)p) * (size_t)row + (size_t)g * DK;
         float y0 = sk[j][c], y1 = sk[j + HALF][c];
         if (cosT) pf_rope(sk[j][c], sk[j + HALF][c], cosT[(size_t)p * HALF + j], sinT[(size_t)p * HALF + j], y0, y1);
-        kr[j] = y0;
-        kr[j + HALF] = y1;
-        vr[j] = sv[j][c];
-        vr[j + HALF] = sv[j + HALF][c];
+        kr[j] = (CT)y0;
+        kr[j + HALF] = (CT)y1;
+        vr[j] = (CT)sv[j][c];
+        vr[j + HALF] = (CT)sv[j + HALF][c];
     }
 }
 
@@ -117,8 +132,8 @@ __global__ __launch_bounds__(256) void k_kv_fill(const float* __restrict__ k, co
 struct PrefillArgs
 {
     const float* q;
-    const float* kc;
-    const float* vc;
+    const void* kc;  // caches of CT elements
+    const void* vc;
     const float* cosT;
     const float* sinT;
     float* out;
@@ -134,7 +149,7 @@ struct PrefillTile
     static constexpr int kBytes = 2 * kFloats * 4;  // double-buffered
 };
 
-template <int DK>
+template <int DK, typename CT>
 __global__ __launch_bounds__(512) void k_attn_prefill(PrefillArgs a)
 {
     constexpr int HALF = DK / 2;
@@ -204,9 +219,9 @@ __global__ __launch_bounds__(512) void k_attn_prefill(PrefillArgs a)
     const size_t seq_off = (size_t)b * (size_t)a.max_len * (size_t)row;
     // rows at or past `valid` (and past max_len) read as zeros: their scores are masked and their
     // zero values keep 0 * v finite
-    const uint32_t seq_bytes = (uint32_t)((size_t)min(valid, a.max_len) * (size_t)row * 4u);
-    const __amdgpu_buffer_rsrc_t rk = pf_rsrc(a.kc + seq_off, seq_bytes);
-    const __amdgpu_buffer_rsrc_t rv = pf_rsrc(a.vc + seq_off, seq_bytes);
+    const uint32_t seq_bytes = (uint32_t)((size_t)min(valid, a.max_len) * (size_t)row * sizeof(CT));
+    const __amdgpu_buffer_rsrc_t rk = pf_rsrc(static_cast<const CT*>(a.kc) + seq_off, seq_bytes);
+    const __amdgpu_buffer_rsrc_t rv = pf_rsrc(static_cast<const CT*>(a.vc) + seq_off, seq_bytes);
 
     // staging: float4 units of a 32 x DK tile, spread over the work-group's threads
     constexpr int kUnits = kPK * DK / 4;
@@ -216,9 +231,10 @@ __global__ __launch_bounds__(512) void k_attn_prefill(PrefillArgs a)
         for (int u = tid; u < kUnits; u += nthreads)
         {
             const int key = u / (DK / 4), c4 = u % (DK / 4);
-            const uint32_t off = (uint32_t)(((size_t)(kb * kPK + key) * (size_t)row + (size_t)g * DK + 4 * c4) * 4u);
-            const float4 kk = ld_f4(rk, off);
-            const float4 vv = ld_f4(rv, off);
+            const uint32_t off =
+                (uint32_t)(((size_t)(kb * kPK + key) * (size_t)row + (size_t)g * DK + 4 * c4) * sizeof(CT));
+            const float4 kk = ld_c4<CT>(rk, off);
+            const float4 vv = ld_c4<CT>(rv, off);
             *reinterpret_cast<float4*>(ks + key * KROW + 4 * c4) = kk;
             *reinterpret_cast<float4*>(vs + key * KROW + 4 * c4) = vv;
         }
@@ -305,19 +321,19 @@ __global__ __launch_bounds__(512) void k_attn_prefill(PrefillArgs a)
     }
 }
 
-template <int DK>
+template <int DK, typename CT>
 hipError_t launch_prefill_dk(hipStream_t st, const PrefillArgs& a)
 {
     static bool attr_set = false;
     if (!attr_set)
     {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_prefill<DK>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_prefill<DK, CT>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<DK>::kBytes);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const unsigned blocks = (unsigned)(a.nqb * a.B * a.Hkv);
-    hipLaunchKernelGGL(k_attn_prefill<DK>, dim3(blocks), dim3(a.R * 64), PrefillTile<DK>::kBytes, st, a);
+    hipLaunchKernelGGL((k_attn_prefill<DK, CT>), dim3(blocks), dim3(a.R * 64), PrefillTile<DK>::kBytes, st, a);
     return hipGetLastError();
 }
 
@@ -325,32 +341,49 @@ hipError_t launch_prefill_dk(hipStream_t st, const PrefillArgs& a)
 
 bool prefill_dk_supported(size_t dk) { return dk == 64 || dk == 128; }
 
-hipError_t launch_kv_fill(hipStream_t st, const float* k, const float* v, size_t B, size_t T, size_t Hkv, size_t dk,
-                          size_t pos0, const float* cosT, const float* sinT, float* kc, float* vc, size_t max_len)
+template <typename CT>
+hipError_t launch_kv_fill_ct(hipStream_t st, const float* k, const float* v, size_t B, size_t T, size_t Hkv, size_t dk,
+                             size_t pos0, const float* cosT, const float* sinT, CT* kc, CT* vc, size_t max_len)
 {
-    const size_t M = B * T;
-    if (M == 0) return hipSuccess;
-    const dim3 grid((unsigned)ceil_div(M, kPQ), (unsigned)Hkv);
+    const dim3 grid((unsigned)ceil_div(B * T, kPQ), (unsigned)Hkv);
     if (dk == 64)
-        hipLaunchKernelGGL(k_kv_fill<64>, grid, dim3(256), 0, st, k, v, (int)B, (int)T, (int)Hkv, (int)pos0, cosT, sinT,
-                           kc, vc, (int)max_len);
+        hipLaunchKernelGGL((k_kv_fill<64, CT>), grid, dim3(256), 0, st, k, v, (int)B, (int)T, (int)Hkv, (int)pos0, cosT,
+                           sinT, kc, vc, (int)max_len);
     else if (dk == 128)
-        hipLaunchKernelGGL(k_kv_fill<128>, grid, dim3(256), 0, st, k, v, (int)B, (int)T, (int)Hkv, (int)pos0, cosT,
+        hipLaunchKernelGGL((k_kv_fill<128, CT>), grid, dim3(256), 0, st, k, v, (int)B, (int)T, (int)Hkv, (int)pos0, cosT,
                            sinT, kc, vc, (int)max_len);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t launch_attn_prefill(hipStream_t st, const float* q, const float* kc, const float* vc, size_t B, size_t T,
-                               size_t H, size_t Hkv, size_t dk, size_t pos0, const float* cosT, const float* sinT,
-                               size_t max_len, float scale, float* out)
+hipError_t launch_kv_fill(hipStream_t st, const float* k, const float* v, size_t B, size_t T, size_t Hkv, size_t dk,
+                          size_t pos0, const float* cosT, const float* sinT, void* kc, void* vc, bool cache_f16,
+                          size_t max_len)
+{
+    if (B * T == 0) return hipSuccess;
+    if (cache_f16)
+        return launch_kv_fill_ct(st, k, v, B, T, Hkv, dk, pos0, cosT, sinT, static_cast<_Float16*>(kc),
+                                 static_cast<_Float16*>(vc), max_len);
+    return launch_kv_fill_ct(st, k, v, B, T, Hkv, dk, pos0, cosT, sinT, static_cast<float*>(kc),
+                             static_cast<float*>(vc), max_len);
+}
+
+hipError_t launch_attn_prefill(hipStream_t st, const float* q, const void* kc, const void* vc, bool cache_f16,
+                               size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0, const float* cosT,
+                               const float* sinT, size_t max_len, float scale, float* out)
 {
     if (B * T == 0) return hipSuccess;
     PrefillArgs a{q, kc, vc, cosT, sinT, out, (int)B, (int)T, (int)H, (int)Hkv, (int)(H / Hkv), (int)pos0,
                   (int)max_len, (int)ceil_div(T, kPQ), scale};
-    if (dk == 64) return launch_prefill_dk<64>(st, a);
-    if (dk == 128) return launch_prefill_dk<128>(st, a);
+    if (cache_f16)
+    {
+        if (dk == 64) return launch_prefill_dk<64, _Float16>(st, a);
+        if (dk == 128) return launch_prefill_dk<128, _Float16>(st, a);
+        return hipErrorInvalidValue;
+    }
+    if (dk == 64) return launch_prefill_dk<64, float>(st, a);
+    if (dk == 128) return launch_prefill_dk<128, float>(st, a);
     return hipErrorInvalidValue;
 }
 

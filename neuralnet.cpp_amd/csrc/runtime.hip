@@ -1741,8 +1741,8 @@ size_t nnhip_attention_workspace_bytes(size_t B, size_t H, size_t Hkv, size_t dk
 // Shared argument checks of the decode attention entry points; grows the chunk workspace.
 static nnhip_status attention_prep(nnhip_ctx* ctx, const char* fn, const float* q, const float* k, const float* v,
                                    size_t B, size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
-                                   const float* rope_cos, const float* rope_sin, float* k_cache, float* v_cache,
-                                   size_t max_len, float* out, size_t& wsb)
+                                   const float* rope_cos, const float* rope_sin, const void* k_cache,
+                                   const void* v_cache, size_t max_len, float* out, size_t& wsb)
 {
     NNHIP_REQUIRE(q && k && v && pos && k_cache && v_cache && out, fn, "null pointer");
     NNHIP_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), fn, "rope_cos and rope_sin go together");
@@ -1768,8 +1768,8 @@ static nnhip_status attention_prep(nnhip_ctx* ctx, const char* fn, const float* 
 static nnhip_status attention_decode_common(nnhip_ctx* ctx, const char* fn, const float* q, const float* k,
                                             const float* v, size_t B, size_t H, size_t Hkv, size_t dk,
                                             const int32_t* pos, size_t len_bound, const float* rope_cos,
-                                            const float* rope_sin, float* k_cache, float* v_cache, size_t max_len,
-                                            float scale, float* out, bool out_tm)
+                                            const float* rope_sin, void* k_cache, void* v_cache, bool cache_f16,
+                                            size_t max_len, float scale, float* out, bool out_tm)
 {
     NNHIP_CHECK_CTX(fn);
     if (B == 0) return NNHIP_OK;
@@ -1778,7 +1778,7 @@ static nnhip_status attention_decode_common(nnhip_ctx* ctx, const char* fn, cons
                                            v_cache, max_len, out, wsb);
     if (st != NNHIP_OK) return st;
     NNHIP_LAUNCH(fn, launch_attn_decode(ctx->stream, q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos, rope_sin,
-                                        k_cache, v_cache, max_len, scale,
+                                        k_cache, v_cache, cache_f16, max_len, scale,
                                         wsb ? static_cast<float*>(ctx->attn_ws) : nullptr, out, ctx->num_cus,
                                         out_tm));
     return NNHIP_OK;
@@ -1790,7 +1790,16 @@ nnhip_status nnhip_attention_decode(nnhip_ctx* ctx, const float* q, const float*
                                     size_t max_len, float scale, float* out)
 {
     return attention_decode_common(ctx, "nnhip_attention_decode", q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos,
-                                   rope_sin, k_cache, v_cache, max_len, scale, out, false);
+                                   rope_sin, k_cache, v_cache, false, max_len, scale, out, false);
+}
+
+nnhip_status nnhip_attention_decode_h(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                      size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                      const float* rope_cos, const float* rope_sin, uint16_t* k_cache,
+                                      uint16_t* v_cache, size_t max_len, float scale, float* out)
+{
+    return attention_decode_common(ctx, "nnhip_attention_decode_h", q, k, v, B, H, Hkv, dk, pos, len_bound, rope_cos,
+                                   rope_sin, k_cache, v_cache, true, max_len, scale, out, false);
 }
 
 nnhip_status nnhip_attention_decode_tokens(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
@@ -1799,14 +1808,23 @@ nnhip_status nnhip_attention_decode_tokens(nnhip_ctx* ctx, const float* q, const
                                            float* v_cache, size_t max_len, float scale, float* out)
 {
     return attention_decode_common(ctx, "nnhip_attention_decode_tokens", q, k, v, B, H, Hkv, dk, pos, len_bound,
-                                   rope_cos, rope_sin, k_cache, v_cache, max_len, scale, out, true);
+                                   rope_cos, rope_sin, k_cache, v_cache, false, max_len, scale, out, true);
 }
 
-nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,
-                                 size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin, float* k_cache,
-                                 float* v_cache, size_t max_len)
+nnhip_status nnhip_attention_decode_tokens_h(nnhip_ctx* ctx, const float* q, const float* k, const float* v, size_t B,
+                                             size_t H, size_t Hkv, size_t dk, const int32_t* pos, size_t len_bound,
+                                             const float* rope_cos, const float* rope_sin, uint16_t* k_cache,
+                                             uint16_t* v_cache, size_t max_len, float scale, float* out)
 {
-    const char* fn = "nnhip_kv_cache_fill";
+    return attention_decode_common(ctx, "nnhip_attention_decode_tokens_h", q, k, v, B, H, Hkv, dk, pos, len_bound,
+                                   rope_cos, rope_sin, k_cache, v_cache, true, max_len, scale, out, true);
+}
+
+static nnhip_status kv_cache_fill_common(nnhip_ctx* ctx, const char* fn, const float* k, const float* v, size_t B,
+                                         size_t T, size_t Hkv, size_t dk, size_t pos0, const float* rope_cos,
+                                         const float* rope_sin, void* k_cache, void* v_cache, bool cache_f16,
+                                         size_t max_len)
+{
     NNHIP_CHECK_CTX(fn);
     if (B == 0 || T == 0) return NNHIP_OK;
     NNHIP_REQUIRE(k && v && k_cache && v_cache, fn, "null pointer");
@@ -1815,16 +1833,32 @@ nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v,
     NNHIP_REQUIRE(Hkv >= 1 && pos0 + T <= max_len && mul_ok(B, T), fn, "need Hkv >= 1 and pos0 + T <= max_len");
     NNHIP_REQUIRE(B * T <= kMaxDim && mul_ok(Hkv * dk, B * T) && Hkv * dk * B * T < 0x7FFFFFFFull, fn,
                   "k / v must be below 2^31 elements");
-    NNHIP_LAUNCH(fn, launch_kv_fill(ctx->stream, k, v, B, T, Hkv, dk, pos0, rope_cos, rope_sin, k_cache, v_cache, max_len));
+    NNHIP_LAUNCH(fn, launch_kv_fill(ctx->stream, k, v, B, T, Hkv, dk, pos0, rope_cos, rope_sin, k_cache, v_cache,
+                                    cache_f16, max_len));
     return NNHIP_OK;
 }
 
-nnhip_status nnhip_attention_prefill(nnhip_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
-                                     size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0,
-                                     const float* rope_cos, const float* rope_sin, size_t max_len, float scale,
-                                     float* out)
+nnhip_status nnhip_kv_cache_fill(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,
+                                 size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin, float* k_cache,
+                                 float* v_cache, size_t max_len)
 {
-    const char* fn = "nnhip_attention_prefill";
+    return kv_cache_fill_common(ctx, "nnhip_kv_cache_fill", k, v, B, T, Hkv, dk, pos0, rope_cos, rope_sin, k_cache,
+                                v_cache, false, max_len);
+}
+
+nnhip_status nnhip_kv_cache_fill_h(nnhip_ctx* ctx, const float* k, const float* v, size_t B, size_t T, size_t Hkv,
+                                   size_t dk, size_t pos0, const float* rope_cos, const float* rope_sin,
+                                   uint16_t* k_cache, uint16_t* v_cache, size_t max_len)
+{
+    return kv_cache_fill_common(ctx, "nnhip_kv_cache_fill_h", k, v, B, T, Hkv, dk, pos0, rope_cos, rope_sin, k_cache,
+                                v_cache, true, max_len);
+}
+
+static nnhip_status attention_prefill_common(nnhip_ctx* ctx, const char* fn, const float* q, const void* k_cache,
+                                             const void* v_cache, bool cache_f16, size_t B, size_t T, size_t H,
+                                             size_t Hkv, size_t dk, size_t pos0, const float* rope_cos,
+                                             const float* rope_sin, size_t max_len, float scale, float* out)
+{
     NNHIP_CHECK_CTX(fn);
     if (B == 0 || T == 0) return NNHIP_OK;
     NNHIP_REQUIRE(q && k_cache && v_cache && out, fn, "null pointer");
@@ -1839,9 +1873,27 @@ nnhip_status nnhip_attention_prefill(nnhip_ctx* ctx, const float* q, const float
     NNHIP_REQUIRE(B * T <= kMaxDim && mul_ok(H * dk, B * T) && H * dk * B * T < 0x3FFFFFFFull, fn,
                   "q / out must be below 2^30 elements");
     NNHIP_REQUIRE(max_len * Hkv * dk < 0x3FFFFFFFull, fn, "one sequence's cache must be below 2^30 elements");
-    NNHIP_LAUNCH(fn, launch_attn_prefill(ctx->stream, q, k_cache, v_cache, B, T, H, Hkv, dk, pos0, rope_cos, rope_sin,
-                                         max_len, scale, out));
+    NNHIP_LAUNCH(fn, launch_attn_prefill(ctx->stream, q, k_cache, v_cache, cache_f16, B, T, H, Hkv, dk, pos0, rope_cos,
+                                         rope_sin, max_len, scale, out));
     return NNHIP_OK;
+}
+
+nnhip_status nnhip_attention_prefill(nnhip_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
+                                     size_t B, size_t T, size_t H, size_t Hkv, size_t dk, size_t pos0,
+                                     const float* rope_cos, const float* rope_sin, size_t max_len, float scale,
+                                     float* out)
+{
+    return attention_prefill_common(ctx, "nnhip_attention_prefill", q, k_cache, v_cache, false, B, T, H, Hkv, dk, pos0,
+                                    rope_cos, rope_sin, max_len, scale, out);
+}
+
+nnhip_status nnhip_attention_prefill_h(nnhip_ctx* ctx, const float* q, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, size_t B, size_t T, size_t H, size_t Hkv, size_t dk,
+                                       size_t pos0, const float* rope_cos, const float* rope_sin, size_t max_len,
+                                       float scale, float* out)
+{
+    return attention_prefill_common(ctx, "nnhip_attention_prefill_h", q, k_cache, v_cache, true, B, T, H, Hkv, dk,
+                                    pos0, rope_cos, rope_sin, max_len, scale, out);
 }
 
 nnhip_status nnhip_copy_columns(nnhip_ctx* ctx, const float* src, size_t rows, size_t src_cols, size_t col0,

@@ -680,9 +680,47 @@ void orc_rope_apply(const float* x, size_t dk, const float* cos_row, const float
  * ascending i), softmax exp(s - max) / sum (compute_layer_softmax.hpp:56-66, sum ascending in t),
  * out_i = sum_t attn_t * V_t[i] (ascending t). Layouts as nnhip_attention_decode. cosT == NULL:
  * no rotation. */
+/* x rounded to the nearest IEEE binary16 value (ties to even), returned as the float it equals:
+ * what a cache of f16 elements stores (compute = F16). Overflow past 65504 gives inf, NaN stays
+ * NaN, and below 2^-14 the f16 subnormal quantum 2^-24 applies. */
+float orc_round_f16(float x)
+{
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    const uint32_t sign = b & 0x80000000u, a = b & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return x;  /* inf, NaN */
+    if (a >= 0x477FF000u)            /* at or past the midpoint of 65504 and 2^16 */
+        return sign ? -INFINITY : INFINITY;
+    if (a < 0x38800000u)             /* below 2^-14: multiples of 2^-24, exact scaling */
+    {
+        const float r = rintf(fabsf(x) * 16777216.0f) / 16777216.0f;
+        return sign ? -r : r;
+    }
+    uint32_t r = (a + 0xFFFu + ((a >> 13) & 1u)) & ~0x1FFFu;  /* 10 mantissa bits, ties to even */
+    r |= sign;
+    float f;
+    memcpy(&f, &r, 4);
+    return f;
+}
+
+void orc_round_f16_n(const float* x, size_t n, float* out)
+{
+    for (size_t i = 0; i < n; ++i) out[i] = orc_round_f16(x[i]);
+}
+
 void orc_attention_decode(const float* q, const float* k, const float* v, size_t B, size_t H, size_t Hkv,
                           size_t dk, const int32_t* pos, const float* cosT, const float* sinT, float* k_cache,
                           float* v_cache, size_t max_len, float scale, float* out)
+{
+    orc_attention_decode_ct(q, k, v, B, H, Hkv, dk, pos, cosT, sinT, k_cache, v_cache, max_len, scale, 0, out);
+}
+
+/* cache_f16: the appended key and value rows are rounded to f16 (orc_round_f16) before they are
+ * used, the caches then hold f16 values (as floats), as under compute = F16
+ * (include/neuralnet.cpp/compute_layer_gpt.hpp:764-765). */
+void orc_attention_decode_ct(const float* q, const float* k, const float* v, size_t B, size_t H, size_t Hkv,
+                             size_t dk, const int32_t* pos, const float* cosT, const float* sinT, float* k_cache,
+                             float* v_cache, size_t max_len, float scale, int cache_f16, float* out)
 {
     const size_t R = H / Hkv, half = dk / 2, row = Hkv * dk;
     float* xbuf = (float*)malloc(dk * sizeof(float));
@@ -706,6 +744,12 @@ void orc_attention_decode(const float* q, const float* k, const float* v, size_t
             else
                 memcpy(kc + (size_t)p * row + g * dk, xbuf, dk * sizeof(float));
             for (size_t i = 0; i < dk; ++i) vc[(size_t)p * row + g * dk + i] = v[(g * dk + i) * B + b];
+            if (cache_f16)
+                for (size_t i = 0; i < dk; ++i)
+                {
+                    kc[(size_t)p * row + g * dk + i] = orc_round_f16(kc[(size_t)p * row + g * dk + i]);
+                    vc[(size_t)p * row + g * dk + i] = orc_round_f16(vc[(size_t)p * row + g * dk + i]);
+                }
         }
         for (size_t h = 0; h < H; ++h)
         {

@@ -48,6 +48,9 @@
  *                       (compute_layer_softmax.hpp:56-66); checked against a float64 numpy
  *                       attention, and exactly on the closed forms (one position -> v; equal keys
  *                       -> mean of v) and on a GQA head map with distinct KV heads
+ *   orc_round_f16      : the f16 element of a compute = F16 cache (compute_layer_gpt.hpp:764-765);
+ *                       checked bit for bit against numpy's float16 conversion over sampled
+ *                       float32 bit patterns and every boundary class (overflow, subnormal, ties)
  *   orc_argmax        : the greedy loop of sample_next_token_ (compute_layer_base.hpp:1152-1160)
  */
 #ifndef NN_ORACLE_H
@@ -125,6 +128,11 @@ void orc_rope_apply(const float* x, size_t dk, const float* cos_row, const float
 void orc_attention_decode(const float* q, const float* k, const float* v, size_t B, size_t H, size_t Hkv,
                           size_t dk, const int32_t* pos, const float* cosT, const float* sinT, float* k_cache,
                           float* v_cache, size_t max_len, float scale, float* out);
+float orc_round_f16(float x);
+void orc_round_f16_n(const float* x, size_t n, float* out);
+void orc_attention_decode_ct(const float* q, const float* k, const float* v, size_t B, size_t H, size_t Hkv,
+                             size_t dk, const int32_t* pos, const float* cosT, const float* sinT, float* k_cache,
+                             float* v_cache, size_t max_len, float scale, int cache_f16, float* out);
 void orc_embedding_gather(const float* table, const int32_t* ids, size_t V, size_t d, size_t B, float* out);
 int32_t orc_argmax(const float* logits, size_t V, size_t stride);
 

@@ -101,6 +101,10 @@ def _load(path) -> ctypes.CDLL:
         "orc_rope_apply": (None, [_f32p, _sz, _f32p, _f32p, _f32p]),
         "orc_attention_decode": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _i32p, _f32p, _f32p, _f32p,
                                         _f32p, _sz, ctypes.c_float, _f32p]),
+        "orc_attention_decode_ct": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _i32p, _f32p, _f32p, _f32p,
+                                           _f32p, _sz, ctypes.c_float, ctypes.c_int, _f32p]),
+        "orc_round_f16": (ctypes.c_float, [ctypes.c_float]),
+        "orc_round_f16_n": (None, [_f32p, _sz, _f32p]),
         "orc_embedding_gather": (None, [_f32p, _i32p, _sz, _sz, _sz, _f32p]),
         "orc_argmax": (ctypes.c_int32, [_f32p, _sz, _sz]),
         "orc_repacked_words": (_sz, [_sz, _sz]),
@@ -383,9 +387,10 @@ def rope_apply(x: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.nd
 
 
 def attention_decode(q, k, v, H: int, Hkv: int, dk: int, pos, k_cache, v_cache, scale: float,
-                     cos=None, sin=None):
+                     cos=None, sin=None, cache_f16: bool = False):
     """One decode step for B sequences; q (H*dk, B), k/v (Hkv*dk, B), caches (B, max_len, Hkv*dk)
-    are updated IN PLACE (row pos[b] written). Returns out (H*dk, B)."""
+    are updated IN PLACE (row pos[b] written). Returns out (H*dk, B). cache_f16: the appended rows
+    are rounded to f16 before use (the caches of compute = F16, held here as float32 values)."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     B = q.shape[1]
     pos = np.ascontiguousarray(pos, dtype=np.int32)
@@ -396,9 +401,18 @@ def attention_decode(q, k, v, H: int, Hkv: int, dk: int, pos, k_cache, v_cache, 
     keep = (None if cos is None else _f32(cos), None if sin is None else _f32(sin))
     cp = None if keep[0] is None else _p(keep[0], ctypes.c_float)
     sp = None if keep[1] is None else _p(keep[1], ctypes.c_float)
-    lib().orc_attention_decode(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(v, ctypes.c_float), B, H, Hkv, dk,
-                               _p(pos, ctypes.c_int32), cp, sp, _p(k_cache, ctypes.c_float),
-                               _p(v_cache, ctypes.c_float), max_len, scale, _p(out, ctypes.c_float))
+    lib().orc_attention_decode_ct(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(v, ctypes.c_float), B, H, Hkv,
+                                  dk, _p(pos, ctypes.c_int32), cp, sp, _p(k_cache, ctypes.c_float),
+                                  _p(v_cache, ctypes.c_float), max_len, scale, 1 if cache_f16 else 0,
+                                  _p(out, ctypes.c_float))
+    return out
+
+
+def round_f16(x) -> np.ndarray:
+    """Elementwise orc_round_f16: the nearest f16 value of each float32 (ties to even), as float32."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_round_f16_n(_p(x, ctypes.c_float), x.size, _p(out, ctypes.c_float))
     return out
 
 

@@ -190,3 +190,24 @@ def test_argmax_greedy_rule(orc):
     L[:, 3] = -np.inf                            # all equal -> 0
     L[:, 4] = [-1, -2, np.inf, np.inf, 0, 0]
     assert orc.argmax_cols(L).tolist() == [1, 0, 2, 0, 2]
+
+
+def test_round_f16_matches_numpy(orc):
+    """orc_round_f16 (the element of a compute = F16 KV cache) bit for bit against numpy's
+    float32 -> float16 conversion (round to nearest, ties to even): every 1031st float32 bit
+    pattern, plus every pattern around the f16 overflow threshold, the normal/subnormal boundary
+    and the f16 ties of a range of exponents."""
+    bits = np.arange(0, 1 << 32, 1031, dtype=np.uint64).astype(np.uint32)
+    extra = [np.arange(0x477F0000, 0x47810000, dtype=np.uint32),   # 65280 .. 66048 (overflow)
+             np.arange(0x38700000, 0x38900000, dtype=np.uint32),   # around 2^-14
+             np.arange(0x33000000, 0x33800000, 997, dtype=np.uint32)]  # around 2^-25
+    ties = (np.arange(0x38800000, 0x477FF000, 0x2000, dtype=np.uint64) + 0x1000).astype(np.uint32)  # exact ties
+    allb = np.concatenate([bits] + extra + [ties, ties + 1, ties - 1])
+    allb = np.concatenate([allb, allb | np.uint32(0x80000000)])
+    x = allb.view(np.float32)
+    got = orc.round_f16(x)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = x.astype(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
