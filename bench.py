@@ -349,13 +349,15 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     The decode steps continue from those caches and tokens: the step is captured once in a graph and
     replayed 128 times. Reported separately: prefill time and tokens/s, decode ms per step and
     tokens/s, the end-to-end time, one layer's prefill attention against the fp32 MFMA peak, and one
-    layer's decode attention call against HBM bandwidth."""
+    layer's decode attention call against HBM bandwidth. The same weights and prompt run twice:
+    "decode_c5" with f32 KV caches and "decode_c5_f16_cache" with f16 ones (compute = F16: the
+    reference creates its caches in the profile's compute precision, compute_layer_gpt.hpp:764-765,
+    F16 under the t1_58 preset), the arithmetic f32 in both."""
     nn = load_pkg()
     from nnhip_py import decoder as dm
     L, d, H, Hkv, F, V, B, ctx_len, new = 30, D, 20, 5, FFN, 10000, 16, 2048, 128
     max_len = ctx_len + new
-    cfg = dm.Config(d=d, H=H, Hkv=Hkv, F=F, vocab=V, max_len=max_len, act=0, eps=1e-5)
-    dk = cfg.dk
+    dk = d // H
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xB17AC500)
 
@@ -385,9 +387,21 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     head = dm.Linear(ctx.repack(hq, d), ht, None, V, d)
     wbytes += V * d // 4
     emb = torch.randn((V, d), generator=gen, device="cuda")
-    dec = dm.Decoder(ctx, cfg, blocks, emb, ones_d, head, B)
     prompt = torch.randint(0, V, (B * ctx_len,), generator=gen, device="cuda", dtype=torch.int32)
+    for key, f16 in (("decode_c5", False), ("decode_c5_f16_cache", True)):
+        cfg = dm.Config(d=d, H=H, Hkv=Hkv, F=F, vocab=V, max_len=max_len, act=0, eps=1e-5, cache_f16=f16)
+        dec = dm.Decoder(ctx, cfg, blocks, emb, ones_d, head, B)
+        res = _c5_measure(ctx, torch, stream, steps, nn, dm, dec, cfg, prompt, wbytes)
+        out[key] = res
+        log(f"C5 ({'f16' if f16 else 'f32'} KV caches): {res}")
+        del dec
+        torch.cuda.empty_cache()
 
+
+def _c5_measure(ctx, torch, stream, steps, nn, dm, dec, cfg, prompt, wbytes):
+    """Prefill, graph-replayed decode steps and lone attention calls of one C5 Decoder."""
+    L, B, ctx_len, new = len(dec.blocks), dec.B, 2048, 128
+    max_len, H, Hkv, dk = cfg.max_len, cfg.H, cfg.Hkv, cfg.dk
     # ---- prefill: 2048 prompt tokens per sequence in one pass (repeatable: it rewrites rows 0..2047)
     dec.prefill(prompt, ctx_len)                    # warm-up: the prefill scratch is allocated here
     torch.cuda.synchronize()
@@ -435,7 +449,7 @@ def decode_c5_line(ctx, torch, stream, steps, out):
     fn = lambda: ctx.attention_decode(dec.q, dec.k, dec.v, H, Hkv, dk, pos, max_len, kc, vc, cfg.scale, dec.cos,
                                       dec.sin, out=dec.a)
     t_att, _ = time_launches(torch, stream, fn, max(10, steps // 2), 3)
-    att_bytes = dm.attention_bytes(B, [mid + 1] * B, Hkv, dk, H)
+    att_bytes = dm.attention_bytes(B, [mid + 1] * B, Hkv, dk, H, 2 if cfg.cache_f16 else 4)
     kv_bytes = L * att_bytes
     res = {
         "prefill_ms": round(t_prefill * 1e3, 3), "prefill_tokens_per_s": round(B * ctx_len / t_prefill, 1),
@@ -451,12 +465,10 @@ def decode_c5_line(ctx, torch, stream, steps, out):
         "attention_one_layer": {"us": round(t_att * 1e6, 2), "bytes": att_bytes,
                                 "GB/s": round(att_bytes / t_att / 1e9, 1),
                                 "frac_hbm": round(att_bytes / t_att / 1e9 / HBM_PEAK_GBS, 4)},
+        "kv_cache": "f16" if cfg.cache_f16 else "f32",
         "hash": {"prefill_last_logits": prefill_hash, "last_ids": tokens_hash},
     }
-    out["decode_c5"] = res
-    log(f"C5: {res}")
-    del dec
-    torch.cuda.empty_cache()
+    return res
 
 
 def profiled_traffic():

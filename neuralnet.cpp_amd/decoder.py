@@ -63,6 +63,9 @@ class Config:
     act: int = 0            # ACT_SWIGLU / ACT_RELU2GLU
     eps: float = 1e-5
     rope: bool = True
+    # KV caches in f16 (compute = F16: the reference creates them in the profile's compute
+    # precision, compute_layer_gpt.hpp:764-765); the arithmetic stays f32
+    cache_f16: bool = False
 
     @property
     def dk(self) -> int:
@@ -101,7 +104,8 @@ class Decoder:
         f32 = dict(dtype=torch.float32, device=dev)
         d, H, Hkv, dk = cfg.d, cfg.H, cfg.Hkv, cfg.dk
         if caches is None:
-            caches = [(torch.zeros((B, cfg.max_len, Hkv * dk), **f32), torch.zeros((B, cfg.max_len, Hkv * dk), **f32))
+            cdt = dict(dtype=torch.float16 if cfg.cache_f16 else torch.float32, device=dev)
+            caches = [(torch.zeros((B, cfg.max_len, Hkv * dk), **cdt), torch.zeros((B, cfg.max_len, Hkv * dk), **cdt))
                       for _ in blocks]
         self.caches = caches
         if cfg.rope:
@@ -453,8 +457,10 @@ def _pkg():
     return sys.modules[__name__.rsplit(".", 1)[0]]
 
 
-def attention_bytes(B: int, lens, Hkv: int, dk: int, H: int) -> int:
+def attention_bytes(B: int, lens, Hkv: int, dk: int, H: int, cache_elem: int = 4) -> int:
     """Algorithmic HBM bytes of one decode attention call: the cached keys and values read
-    (lens[b] - 1 rows each, f32), the new key/value rows written, q read and the output written."""
+    (lens[b] - 1 rows each, cache_elem bytes per element: 4 in f32 caches, 2 in f16 ones), the
+    new key/value (f32) read and their cache rows written, q read and the output written."""
     rows = sum(int(L) - 1 for L in lens)
-    return 2 * rows * Hkv * dk * 4 + 2 * B * Hkv * dk * 4 + 2 * B * Hkv * dk * 4 + 2 * B * H * dk * 4
+    return (2 * rows * Hkv * dk * cache_elem + 2 * B * Hkv * dk * 4 + 2 * B * Hkv * dk * cache_elem +
+            2 * B * H * dk * 4)

@@ -318,6 +318,20 @@ def test_decode_step_chain(ctx, orc, nnhip, subln):
                   ids=np.array([3, 50, 96], np.int32), subln=subln, seed=0x5EC + subln, expect_fused=True)
 
 
+@pytest.mark.parametrize("B", [3, 17])
+def test_decode_step_chain_f16_cache(ctx, orc, nnhip, B):
+    """The decode chain with the KV caches in f16 (compute = F16, Config.cache_f16): the fused step
+    (B = 3) and the unfused one (B = 17), against the oracle chain on the same f16 caches: every
+    int8 stage, the logits and the greedy ids bit for bit, attention within tolerance, the caches'
+    f16 elements bit for bit."""
+    from nnhip_py import decoder as dmod
+    cfg = dmod.Config(d=256, H=4, Hkv=2, F=320, vocab=97, max_len=200, act=0, eps=1e-5, cache_f16=True)
+    start = (np.arange(B, dtype=np.int32) * 11 + 120) % 190
+    ids = (np.arange(B, dtype=np.int32) * 13 + 5) % cfg.vocab
+    _decode_chain(ctx, orc, nnhip, cfg, B=B, start=start, ids=ids, subln=True, seed=0x5F1 + B,
+                  expect_fused=B <= 16)
+
+
 def test_decode_step_chain_unfused_b17(ctx, orc, nnhip):
     """17 sequences take the unfused step (block_step, then the column argmax): the same oracle
     chain bit for bit, the last step with advance=True (ids written into the input, every
@@ -363,6 +377,7 @@ def _decode_chain(ctx, orc, nnhip, cfg, B, start, ids, subln, seed, expect_fused
     import torch
     L = 2
     dec, hb, emb, gfin, head = _build_model(ctx, orc, nnhip, cfg, L, B, seed, subln)
+    assert dec.caches[0][0].dtype == (torch.float16 if cfg.cache_f16 else torch.float32)
     assert dec.fused_ok() == expect_fused
     cos, sin = orc.rope_table(cfg.dk, cfg.max_len)
     kc_o = [np.zeros((B, cfg.max_len, cfg.Hkv * cfg.dk), np.float32) for _ in range(L)]
@@ -385,7 +400,8 @@ def _decode_chain(ctx, orc, nnhip, cfg, B, start, ids, subln, seed, expect_fused
             q = _orc_bitlinear(orc, x, b["q"], b["g1"], cfg.eps)
             k = _orc_bitlinear(orc, x, b["k"], b["g1"], cfg.eps)
             v = _orc_bitlinear(orc, x, b["v"], b["g1"], cfg.eps)
-            a = orc.attention_decode(q, k, v, cfg.H, cfg.Hkv, cfg.dk, pos, kc_o[l], vc_o[l], cfg.scale, cos, sin)
+            a = orc.attention_decode(q, k, v, cfg.H, cfg.Hkv, cfg.dk, pos, kc_o[l], vc_o[l], cfg.scale, cos, sin,
+                                     cache_f16=cfg.cache_f16)
             ag = attn_gpu[l]
             assert np.max(np.abs(ag - a)) <= ATOL * max(1.0, float(np.max(np.abs(a))))
             o = _orc_bitlinear(orc, ag, b["o"], b["ga"], cfg.eps)
@@ -398,7 +414,8 @@ def _decode_chain(ctx, orc, nnhip, cfg, B, start, ids, subln, seed, expect_fused
         assert nxt.tolist() == orc.argmax_cols(lg).tolist()
         torch.cuda.synchronize()
         for l in range(L):
-            assert same_bits(host(dec.caches[l][0]), kc_o[l]) and same_bits(host(dec.caches[l][1]), vc_o[l])
+            assert same_bits(host(dec.caches[l][0].float()), kc_o[l])
+            assert same_bits(host(dec.caches[l][1].float()), vc_o[l])
         ids = nxt.astype(np.int32)
 
 
@@ -522,3 +539,4 @@ def test_ffn_glu_i8_add_equals_unfused(ctx, orc, nnhip, d, F, M):
     y = host(ctx.ffn_glu_i8_add(X, g, 1e-5, F, rp1, to, None, rp2, t2, b2, res, gamma_sub=gs))
     ref = host(ctx.add(res, ctx.ffn_glu_i8(X, g, 1e-5, F, rp1, to, None, rp2, t2, b2, gamma_sub=gs)))
     assert same_bits(y, ref)
+
