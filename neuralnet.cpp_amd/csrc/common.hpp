@@ -16,6 +16,13 @@ namespace nnhip
 
 constexpr int kWave = 64;
 
+// Cache-policy operands of buffer loads and stores (gfx950 bits: sc0 = 1, nt = 2, sc1 = 16).
+// A store with sc0 sc1 (system scope) is written through the L2 as it is issued; with the default
+// policy a large output sits dirty in the L2 and is written back at the end of the kernel, after
+// the last wave, where nothing overlaps it.
+constexpr int kPolicyNT = 2;
+constexpr int kPolicySys = 17;
+
 // T16K256 repacked-weight geometry (see include/nnhip.h and oracle/nn_oracle.c).
 constexpr int kTileRows = 16;
 constexpr int kTileK = 256;
@@ -54,7 +61,14 @@ constexpr int kGemvMaxM = 16;
 #ifndef NNHIP_GEMV_REG_WAVES
 #define NNHIP_GEMV_REG_WAVES 4
 #endif
+#ifndef NNHIP_GEMV_BIG_DEPTH
+#define NNHIP_GEMV_BIG_DEPTH 2
+#endif
 constexpr int kLdsRTW = 1, kLdsDepth = NNHIP_GEMV_LDS_DEPTH, kLdsWavesPerCu = NNHIP_GEMV_LDS_WAVES;
+// The 16-wave blocks (one per CU, activation sets beyond 48 KiB) keep 2 stages in flight: with
+// 16 waves per CU that holds as many bytes in flight, and the M = 16 sweep measured 102.6-102.7
+// against 103.6-104.5 us at 3 stages (97.9-98.8 against 101.2-101.8 us with write-through stores).
+constexpr int kBigDepth = NNHIP_GEMV_BIG_DEPTH;
 constexpr int kRegRTW = NNHIP_GEMV_REG_RTW, kRegDepth = NNHIP_GEMV_REG_DEPTH, kRegWavesPerCu = NNHIP_GEMV_REG_WAVES;
 
 struct GemvVariant

@@ -9,7 +9,10 @@
 //   j=2: w & 0x30303030 (16 * codes)     -> a2      j=3: (w >> 6) & 0x03030303       -> a3
 //   acc = a0 + a3 + (a1 >> 2) + (a2 >> 4) - 2 * rowsum       (shifts divide exact multiples)
 // Output layout of the 16x16 MFMA: lane l = 16 g + t holds rows 4g + i (i = 0..3) of column
-// (token) t.
+// (token) t. The A and B operands share one lane layout (lane l: row / column l % 16, k block
+// l / 16), so passing the activations as A and the codes as B (kT) computes the transposed
+// tile from the same registers: lane 16 g + r then holds tokens 4g + i of row r, four
+// consecutive floats of a feature-major (N, M) output.
 #pragma once
 
 #include "common.hpp"
@@ -50,17 +53,23 @@ struct Acc
     v4i a0, a1, a2, a3;
 };
 
-template <int kRTW>
+template <bool kT>
+__device__ __forceinline__ v4i mfma_wx(v4i w, v4i x, v4i c)
+{
+    return kT ? mfma16(x, w, c) : mfma16(w, x, c);
+}
+
+template <int kRTW, bool kT = false>
 __device__ __forceinline__ void compute_stage(const v4i (&w4)[kRTW], const v4i (&x)[4], Acc (&acc)[kRTW])
 {
 #pragma unroll
     for (int r = 0; r < kRTW; ++r)
     {
         const v4i w = w4[r];
-        acc[r].a0 = mfma16(w & (int)kM3, x[0], acc[r].a0);
-        acc[r].a1 = mfma16(w & (int)(kM3 << 2), x[1], acc[r].a1);
-        acc[r].a2 = mfma16(w & (int)(kM3 << 4), x[2], acc[r].a2);
-        acc[r].a3 = mfma16((v4i)((__builtin_bit_cast(u32x4, w) >> 6) & kM3), x[3], acc[r].a3);
+        acc[r].a0 = mfma_wx<kT>(w & (int)kM3, x[0], acc[r].a0);
+        acc[r].a1 = mfma_wx<kT>(w & (int)(kM3 << 2), x[1], acc[r].a1);
+        acc[r].a2 = mfma_wx<kT>(w & (int)(kM3 << 4), x[2], acc[r].a2);
+        acc[r].a3 = mfma_wx<kT>((v4i)((__builtin_bit_cast(u32x4, w) >> 6) & kM3), x[3], acc[r].a3);
     }
 }
 

@@ -29,6 +29,13 @@ namespace
 {
 
 constexpr int kBlock = 256;
+// Cache-policy operand of the register quantizer's xi stores. The 8-token blocks (M <= 8192: a
+// grid of one or a few resident rounds) write the codes through the L2 (kPolicySys) as they are
+// produced: at M = 2048, K = 4096 12.1 -> 10.9 us, RMSNorm 2560 9.35 -> 9.0 us, K = 6912 21.1 ->
+// 20.9 us. The 4-token blocks (larger M, many rounds) keep the default policy, 1-2 % faster
+// there (2560 x 32768: 157.6-159.2 against 160.4-161.0 us).
+template <int TPB>
+constexpr int kXiPolicy = TPB >= 8 ? kPolicySys : 0;
 #ifndef NNHIP_ONE_TOK_MAX_M
 #define NNHIP_ONE_TOK_MAX_M 64  // largest M for k_token_one (K=6912, M=64: 6.8 us per call, the
                                 // 4-token kernel 11.0; equal at K=2560)
@@ -575,9 +582,9 @@ __device__ __forceinline__ void finish_group(float (&x)[R][4], const float (&gm)
         const uint32_t col = quad_transpose(pk[r], j);
         tsum = __builtin_amdgcn_sdot4((int)col, 0x01010101, tsum, false);
         if (r < whole)
-            __builtin_amdgcn_raw_buffer_store_b32(col, rxi, xoff + (uint32_t)(RR * r), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(col, rxi, xoff + (uint32_t)(RR * r), 0, kXiPolicy<TPB>);
         else if (r == whole)
-            __builtin_amdgcn_raw_buffer_store_b32(col, rxi, xpart + (uint32_t)(RR * r), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(col, rxi, xpart + (uint32_t)(RR * r), 0, kXiPolicy<TPB>);
     }
     tsum = bfly_isum1<RPW / 2, 4>(tsum);  // over the quads of the wave's slice
     if (fl < 4) sh.wsum[w][4 * h + j] = tsum;

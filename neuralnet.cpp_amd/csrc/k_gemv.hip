@@ -117,6 +117,51 @@ __device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__
     __syncthreads();
 }
 
+// One item's outputs (the transposed tile: lane 16 g + r holds tokens 4 g + i of row r).
+template <int kRTW>
+struct TileOut
+{
+    float y[kRTW][4];
+    uint32_t base[kRTW];  // element index of (row n, token 4 g), kNone past N or M
+    __amdgpu_buffer_rsrc_t ry;
+    int M;
+};
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+
+// Masked lanes store out of range (the output is below 2 GiB, so kOOB + 16 is past it): dropped
+// by the buffer unit. With M a multiple of 4 a lane's four tokens are one 16-byte store (the 16
+// lanes of a row tile write its 16 x 16 block as 1 KiB contiguous), written through the L2
+// (kPolicySys): the M = 16 sweep writes 44 MB of outputs beside 527 MB of weights, and left
+// dirty in the L2 they cost 101.2-101.8 against 97.9-98.8 us. Otherwise (M = 1: 64 bytes per
+// row tile) one store per token with the default policy.
+template <int kRTW>
+__device__ __forceinline__ void store_tile(const TileOut<kRTW>& q)
+{
+    const uint32_t tb = 4u * ((threadIdx.x & 63u) >> 4);
+#pragma unroll
+    for (int r = 0; r < kRTW; ++r)
+    {
+        if ((q.M & 3) == 0)
+        {
+            const uint32_t off = q.base[r] != kNone ? q.base[r] * 4u : kOOB;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__builtin_bit_cast(uint32_t, q.y[r][0]), __builtin_bit_cast(uint32_t, q.y[r][1]),
+                      __builtin_bit_cast(uint32_t, q.y[r][2]), __builtin_bit_cast(uint32_t, q.y[r][3])},
+                q.ry, off, 0, kPolicySys);
+        }
+        else
+        {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                if (i >= q.M) break;  // uniform: no store that every lane would drop
+                const uint32_t off = (q.base[r] != kNone && tb + i < (uint32_t)q.M) ? (q.base[r] + i) * 4u : kOOB;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, q.y[r][i]), q.ry, off, 0, 0);
+            }
+        }
+    }
+}
+
 // Loads are unconditional: a stage past the last k tile reads beyond its resource
 // (num_records = KT KiB), which returns zero words (code 0: no contribution). On the LDS
 // path the activations of stage kt+1 are read from LDS while stage kt computes (LDS reads
@@ -141,13 +186,13 @@ __device__ __forceinline__ void gemv_stream(int KT, const Src<kRTW>& s, Acc (&ac
             if constexpr (LDS)
             {
                 if (kt + 1 < KT_FIXED) read_x_lds(xn, s, kt + 1);
-                compute_stage(st[kt % kDepth].w, xc, acc);
+                compute_stage<kRTW, true>(st[kt % kDepth].w, xc, acc);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) xc[j] = xn[j];
             }
             else
             {
-                compute_stage(st[kt % kDepth].w, st[kt % kDepth].x, acc);
+                compute_stage<kRTW, true>(st[kt % kDepth].w, st[kt % kDepth].x, acc);
             }
             if (kt + kDepth < KT_FIXED) load_stage<LDS>(st[kt % kDepth], s, kt + kDepth);
             // keep the stage order: later stages' MFMAs must not be hoisted above these loads
@@ -165,13 +210,13 @@ __device__ __forceinline__ void gemv_stream(int KT, const Src<kRTW>& s, Acc (&ac
                 if constexpr (LDS)
                 {
                     if (kt + u + 1 < KT) read_x_lds(xn, s, kt + u + 1);
-                    compute_stage(st[u].w, xc, acc);
+                    compute_stage<kRTW, true>(st[u].w, xc, acc);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) xc[j] = xn[j];
                 }
                 else
                 {
-                    compute_stage(st[u].w, st[u].x, acc);
+                    compute_stage<kRTW, true>(st[u].w, st[u].x, acc);
                 }
                 load_stage<LDS>(st[u], s, kt + u + kDepth);
                 __builtin_amdgcn_sched_barrier(0);
@@ -214,22 +259,30 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     }
 
     // Epilogue operands: unconditional buffer loads issued before the weight stream (rows
-    // past N and tokens past M read 0), so they have landed by the end of the item.
+    // past N and tokens past M read 0), so they have landed by the end of the item. The tile
+    // is computed transposed (compute_stage<kT>): lane 16 g + r holds tokens tb + i (tb = 4 g,
+    // i = 0..3) of row r of each row tile.
+    const uint32_t tb = 4u * (uint32_t)g, rl = (uint32_t)t;
     const __amdgpu_buffer_rsrc_t rtau = rsrc(p.tau, (uint32_t)p.N * 4u);
     const __amdgpu_buffer_rsrc_t rbias = rsrc(p.bias ? p.bias : p.tau, p.bias ? (uint32_t)p.N * 4u : 0u);
-    const uint32_t tok = t < p.M ? (uint32_t)t : 0x40000000u;
-    const int rs2 = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.rowsum, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
-    const float sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(p.s, (uint32_t)p.M * 4u), tok * 4u, 0, 0));
-    float tv[kRTW][4], bv[kRTW][4];
+    const __amdgpu_buffer_rsrc_t rrs = rsrc(p.rowsum, (uint32_t)p.M * 4u), rs = rsrc(p.s, (uint32_t)p.M * 4u);
+    int rs2[4];
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const uint32_t to = tb + i < (uint32_t)p.M ? (tb + i) * 4u : kOOB;
+        rs2[i] = 2 * __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rrs, to, 0, 0));
+        sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, to, 0, 0));
+    }
+    float tv[kRTW], bv[kRTW];
 #pragma unroll
     for (int r = 0; r < kRTW; ++r)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            const uint32_t n = (uint32_t)((rt0 + r) * 16 + 4 * g + i);
-            tv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, n * 4u, 0, 0));
-            bv[r][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, n * 4u, 0, 0));
-        }
+    {
+        const uint32_t n = (uint32_t)(rt0 + r) * 16u + rl;
+        tv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rtau, n * 4u, 0, 0));
+        bv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbias, n * 4u, 0, 0));
+    }
 
     Acc acc[kRTW];
 #pragma unroll
@@ -243,22 +296,24 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     default: gemv_stream<LDS, kRTW, kDepth, 0, kThreads, kStage>(p.KT, s, acc, lds, xs, n_x); break;
     }
 
-    // masked lanes (token >= M, row >= N) store out of range: dropped by the buffer unit
-    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+    TileOut<kRTW> q;
+    q.ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
+    q.M = p.M;
 #pragma unroll
     for (int r = 0; r < kRTW; ++r)
     {
+        const uint32_t n = (uint32_t)(rt0 + r) * 16u + rl;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
         {
-            const int n = (rt0 + r) * 16 + 4 * g + i;
-            const int a = acc[r].a0[i] + acc[r].a3[i] + (acc[r].a1[i] >> 2) + (acc[r].a2[i] >> 4) - rs2;
-            float y = (tv[r][i] * sv) * (float)a;
-            if (p.bias) y = y + bv[r][i];
-            const uint32_t off = (n < p.N && t < p.M) ? ((uint32_t)n * (uint32_t)p.M + (uint32_t)t) * 4u : 0xFFFFFFF0u;
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, 0);
+            const int a = acc_sum(acc[r], i) - rs2[i];
+            float y = (tv[r] * sv[i]) * (float)a;
+            if (p.bias) y = y + bv[r];
+            q.y[r][i] = y;
         }
+        q.base[r] = (n < (uint32_t)p.N && tb < (uint32_t)p.M) ? n * (uint32_t)p.M + tb : kNone;
     }
+    store_tile(q);
 }
 
 // Single problem: static assignment of items to waves.
@@ -719,13 +774,13 @@ hipError_t launch_gemv_grouped(hipStream_t st, const GemvProblem* d_probs, const
         if (!attr)
         {
             const hipError_t e = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&k_gemv_grouped<true, kLdsRTW, kLdsDepth, kBig>),
+                reinterpret_cast<const void*>(&k_gemv_grouped<true, kLdsRTW, kBigDepth, kBig>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsBigBudget);
             if (e != hipSuccess) return e;
             attr = true;
         }
         const unsigned blocks = (unsigned)ceil_div(n_waves, (size_t)(kBig / kWave));
-        hipLaunchKernelGGL((k_gemv_grouped<true, kLdsRTW, kLdsDepth, kBig>), dim3(blocks), dim3(kBig), lds_bytes, st,
+        hipLaunchKernelGGL((k_gemv_grouped<true, kLdsRTW, kBigDepth, kBig>), dim3(blocks), dim3(kBig), lds_bytes, st,
                            d_probs, d_wave_start, d_wave_items, (int)n_waves, d_xstage, n_xstage);
         return hipGetLastError();
     }
