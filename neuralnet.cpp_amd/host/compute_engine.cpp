@@ -402,6 +402,11 @@ Result<Tensor> ComputeEngine::attention_decode(const Tensor& q, const Tensor& k,
         v_cache.rows() != k_cache.rows() || v_cache.cols() != k_cache.cols())
         return Error{"attention_decode: caches must be (B * max_len, kv_heads * d_k), got " + shape(k_cache) + " / " +
                      shape(v_cache)};
+    if (k_cache.precision() != v_cache.precision() ||
+        (k_cache.precision() != Precision::F32 && k_cache.precision() != Precision::F16))
+        return Error{"attention_decode: caches must both be f32 or both f16"};
+    for (const Tensor* t : {&q, &k, &v})
+        if (t->precision() != Precision::F32) return Error{"attention_decode: q, k and v must be f32"};
     if (positions.rows() != B || positions.cols() != 1)
         return Error{"attention_decode: positions must be (B, 1), got " + shape(positions)};
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return Error{"attention_decode: rope tables go together"};

@@ -504,10 +504,20 @@ protected:
                                        const Tensor& out) override
     {
         const std::size_t dk = q.rows() / heads;
-        NNHIP_TRY(nnhip_attention_decode(ctx_->h, fp(q), fp(k), fp(v), q.cols(), heads, kv_heads, dk,
-                                         static_cast<const int32_t*>(TensorAccess::ptr(positions)), len_bound,
-                                         rope_cos ? fp(*rope_cos) : nullptr, rope_sin ? fp(*rope_sin) : nullptr,
-                                         fpw(k_cache), fpw(v_cache), max_len, scale, fpw(out)),
+        const auto* pos = static_cast<const int32_t*>(TensorAccess::ptr(positions));
+        const float* cs = rope_cos ? fp(*rope_cos) : nullptr;
+        const float* sn = rope_sin ? fp(*rope_sin) : nullptr;
+        if (k_cache.precision() == Precision::F16)  // compute = F16: f16 storage, f32 arithmetic
+        {
+            NNHIP_TRY(nnhip_attention_decode_h(ctx_->h, fp(q), fp(k), fp(v), q.cols(), heads, kv_heads, dk, pos,
+                                               len_bound, cs, sn, static_cast<uint16_t*>(TensorAccess::ptr(k_cache)),
+                                               static_cast<uint16_t*>(TensorAccess::ptr(v_cache)), max_len, scale,
+                                               fpw(out)),
+                      "attention_decode");
+            return {};
+        }
+        NNHIP_TRY(nnhip_attention_decode(ctx_->h, fp(q), fp(k), fp(v), q.cols(), heads, kv_heads, dk, pos, len_bound,
+                                         cs, sn, fpw(k_cache), fpw(v_cache), max_len, scale, fpw(out)),
                   "attention_decode");
         return {};
     }

@@ -89,6 +89,11 @@ inline PrecisionProfile float_part(PrecisionProfile p)
     p.param = Precision::F32;
     return p;
 }
+// The decoder's block activations, residual stream and KV caches are f32: init refuses a
+// compute = F16 profile (the reference's t1_58 preset, src/t1_58_test.cpp:668-690) rather than
+// hand f16 BitLinear outputs to f32 kernels. The engine's attention itself takes f16 caches
+// (ComputeEngine::attention_decode, nnhip_attention_decode_h).
+inline PrecisionSet decoder_compute() { return PrecisionSet::of({Precision::F32}); }
 }  // namespace detail
 
 // KV cache of one attention layer for B sequences: rows [b*max_len, (b+1)*max_len) of k / v
@@ -179,6 +184,7 @@ public:
     {
         PrecisionSupport sup = PrecisionSupport::rounding_all_slots();
         sup.param.mask |= PrecisionSet::of({Precision::T1_58}).mask;
+        sup.compute = detail::decoder_compute();
         return sup;
     }
 
@@ -220,7 +226,8 @@ public:
                      "decode with forward_step"};
     }
 
-    // Zero-filled caches for `batch` sequences.
+    // Zero-filled caches for `batch` sequences, in the compute precision as the reference creates
+    // them (compute_layer_gpt.hpp:764-765): f32, the only compute precision this decoder takes.
     [[nodiscard]] Result<KVCache> make_cache(std::size_t batch)
     {
         KVCache c;
@@ -329,6 +336,7 @@ public:
     {
         PrecisionSupport sup = PrecisionSupport::rounding_all_slots();
         sup.param.mask |= PrecisionSet::of({Precision::T1_58}).mask;
+        sup.compute = detail::decoder_compute();
         return sup;
     }
     void set_activation_quant(bool enabled) noexcept
@@ -419,6 +427,7 @@ public:
     {
         PrecisionSupport sup = PrecisionSupport::rounding_all_slots();
         sup.param.mask |= PrecisionSet::of({Precision::T1_58}).mask;
+        sup.compute = detail::decoder_compute();
         return sup;
     }
     void set_activation_quant(bool enabled) noexcept

@@ -91,6 +91,9 @@ public:
         if (!sup.param.has(p_.param))
             return Error{std::string(layer_name()) + ": param precision " + precision_name(p_.param) +
                          " not supported (supported: " + sup.param.to_string() + ")"};
+        if (!sup.compute.has(p_.compute))
+            return Error{std::string(layer_name()) + ": compute precision " + precision_name(p_.compute) +
+                         " not supported (supported: " + sup.compute.to_string() + ")"};
         engine_ = &engine;
         return init_impl(engine);
     }

@@ -1118,6 +1118,63 @@ void test_decoder(nn::ComputeEngine& e)
         CHECK(rows_ok, "appended cache rows: rotated key (vs double) and the exact value");
         CHECK(ok && err < 1e-5, "attention_decode within 1e-5 of a host double evaluation");
     }
+    // f16 caches (the reference's caches under compute = F16, compute_layer_gpt.hpp:764-765): the same
+    // call on f16 caches holding kc0 / vc0 rounded to f16 appends the f16 rounding of the f32 call's
+    // rows (the same f32 arithmetic, one rounding), leaves every other row alone, and returns the
+    // host double evaluation over the f16 cache contents it ends with
+    {
+        auto q = attn.w_q().forward(xt);
+        auto k = attn.w_k().forward(xt);
+        auto v = attn.w_v().forward(xt);
+        const auto F16 = nn::Precision::F16;
+        nn::KVCache ch{e.create_tensor(B * max_len, Hkv * dk, F16), e.create_tensor(B * max_len, Hkv * dk, F16), B,
+                       max_len};
+        nn::KVCache cf{e.create_tensor(B * max_len, Hkv * dk), e.create_tensor(B * max_len, Hkv * dk), B, max_len};
+        (void)e.copy_from(ch.k, kc0);
+        (void)e.copy_from(ch.v, vc0);
+        (void)e.copy_from(cf.k, kc0);
+        (void)e.copy_from(cf.v, vc0);
+        auto a16 = e.attention_decode(*q, *k, *v, ch.k, ch.v, max_len, *pos, 64, &attn.rotary()->cos(),
+                                      &attn.rotary()->sin(), H, Hkv, attn.scale());
+        auto a32 = e.attention_decode(*q, *k, *v, cf.k, cf.v, max_len, *pos, 64, &attn.rotary()->cos(),
+                                      &attn.rotary()->sin(), H, Hkv, attn.scale());
+        bool ok = a16.has_value() && a32.has_value();
+        bool rows_ok = ok;
+        double err = 0;
+        if (ok)
+        {
+            const nn::Matrix A = download(e, *a16), Q = download(e, *q);
+            const nn::Matrix KH = download(e, ch.k), VH = download(e, ch.v);  // f16 widened exactly
+            auto kr = e.to_matrix(cf.k, F16), vr = e.to_matrix(cf.v, F16);  // the f32 caches rounded
+            rows_ok = kr.has_value() && vr.has_value() && bitwise_equal(KH, *kr) && bitwise_equal(VH, *vr);
+            const nn::Matrix cosT = download(e, attn.rotary()->cos()), sinT = download(e, attn.rotary()->sin());
+            for (std::size_t b = 0; b < B; ++b)
+            {
+                const std::size_t p = posv[b];
+                std::vector<float> qb(H * dk), kcb((p + 1) * Hkv * dk), vcb((p + 1) * Hkv * dk);
+                for (std::size_t i = 0; i < H * dk; ++i) qb[i] = Q.at(i, b);
+                for (std::size_t t = 0; t <= p; ++t)
+                    for (std::size_t i = 0; i < Hkv * dk; ++i)
+                    {
+                        kcb[t * Hkv * dk + i] = KH.at(b * max_len + t, i);
+                        vcb[t * Hkv * dk + i] = VH.at(b * max_len + t, i);
+                    }
+                const auto ref = host_attention(qb, kcb, vcb, p + 1, H, Hkv, dk, attn.scale(), cosT, sinT);
+                for (std::size_t i = 0; i < H * dk; ++i) err = std::max(err, std::abs(A.at(i, b) - ref[i]));
+            }
+        }
+        CHECK(rows_ok, "f16 caches: every row == the f32 call's cache rounded to f16 (appended rows included)");
+        CHECK(ok && err < 1e-5, "f16 caches: attention_decode within 1e-5 of a host double evaluation of their contents");
+        auto mixed = e.attention_decode(*q, *k, *v, ch.k, cf.v, max_len, *pos, 64, &attn.rotary()->cos(),
+                                        &attn.rotary()->sin(), H, Hkv, attn.scale());
+        auto q16 = e.to_matrix(*q, F16);
+        nn::Tensor qh = e.create_tensor(q->rows(), q->cols(), F16);
+        const bool qh_ok = q16.has_value() && e.copy_from(qh, *q16).has_value();
+        auto half_q = e.attention_decode(qh, *k, *v, ch.k, ch.v, max_len, *pos, 64, &attn.rotary()->cos(),
+                                         &attn.rotary()->sin(), H, Hkv, attn.scale());
+        CHECK(!mixed.has_value() && qh_ok && !half_q.has_value(),
+              "attention_decode refuses an f16 / f32 cache pair and f16 queries");
+    }
     // batched == the reference single-sequence signature, per sequence (same kernels, same chunking)
     {
         bool same = true;
@@ -1162,6 +1219,14 @@ void test_decoder(nn::ComputeEngine& e)
                  bitwise_equal(download(e, c1->k), download(e, c2->k));
         }
         CHECK(ok, "GPTBlock::forward_step == norm1 -> attention -> add -> norm2 -> FeedForward -> add, bit for bit");
+    }
+    // compute = F16 (the t1_58 preset) is refused at init: the decoder's activations are f32
+    {
+        nn::GPTModel g16(97, d, 32, H, F, 1, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
+        g16.set_precision_profile(nn::profile_t1_58());
+        auto r = g16.init(e);
+        CHECK(!r.has_value() && r.error().message.find("compute precision") != std::string::npos,
+              "GPTModel refuses compute = F16 at init with a clear error");
     }
     // GPTModel: greedy generation == forward_step + the reference greedy loop on the host
     {
