@@ -231,6 +231,15 @@ nnhip_status nnhip_add_row_broadcast(nnhip_ctx* ctx, float* Y, const float* b, s
 nnhip_status nnhip_rmsnorm(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t F,
                            size_t M, float* out);
 
+/* out (F, M) = LayerNorm(X (F, M)) with gain gamma (F) and shift beta (F): mean = sum_f x * fl(1/F),
+ * d = x - mean, sinv = 1/sqrt(sum_f d*d * fl(1/F) + eps), out = (d * sinv) * gamma[f] + beta[f], each
+ * step rounded to fp32 (both sums in one fixed order: 8 strided parts f % 8, each ascending, then
+ * ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))).
+ * Replaces LayerNorm::forward (include/neuralnet.cpp/compute_layer_mlp.hpp:529-545), the SubLN
+ * norm type FeedForward takes by default (include/neuralnet.cpp/compute_layer_feedforward.hpp:50-65). */
+nnhip_status nnhip_layernorm(nnhip_ctx* ctx, const float* X, const float* gamma, const float* beta, float eps,
+                             size_t F, size_t M, float* out);
+
 /* --------------------------------------------- MI355X-native fast path */
 
 /* Repacked ternary weights, layout T16K256: rows padded to 16, k padded to 256; one

@@ -89,6 +89,7 @@ SIGNATURES = {
     "nnhip_matmul_q": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_matmul_q_t": (_st, [_vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp, ctypes.c_int]),
     "nnhip_rmsnorm": (_st, [_vp, _vp, _vp, _f, _sz, _sz, _vp]),
+    "nnhip_layernorm": (_st, [_vp, _vp, _vp, _vp, _f, _sz, _sz, _vp]),
     "nnhip_repacked_bytes": (_sz, [_sz, _sz]),
     "nnhip_repack_ternary": (_st, [_vp, _vp, _sz, _sz, _vp]),
     "nnhip_unrepack_ternary": (_st, [_vp, _vp, _sz, _sz, _vp]),
@@ -451,6 +452,23 @@ class Context:
         _check(lib().nnhip_rmsnorm(self.h, self._dev(X, torch.float32, "X"),
                                    self._dev(gamma, torch.float32, "gamma"), eps, F, M,
                                    self._dev(out)), "nnhip_rmsnorm")
+        return out
+
+    def layernorm(self, X, gamma, beta, eps: float = 1e-5):
+        """LayerNorm of each token (column) of X (F, M) with gain gamma (F) and shift beta (F):
+        LayerNorm::forward (include/neuralnet.cpp/compute_layer_mlp.hpp:529-545), the SubLN norm type
+        FeedForward takes by default. Returns (F, M) float32."""
+        torch = self._torch
+        F, M = X.shape
+        if gamma.numel() != F or beta.numel() != F:
+            raise NNHipError(1, f"layernorm: gamma and beta must hold F={F} values "
+                                f"(got {gamma.numel()}, {beta.numel()})")
+        out = self._empty((F, M), torch.float32)
+        self._bind_stream()
+        _check(lib().nnhip_layernorm(self.h, self._dev(X, torch.float32, "X"),
+                                     self._dev(gamma, torch.float32, "gamma"),
+                                     self._dev(beta, torch.float32, "beta"), eps, F, M,
+                                     self._dev(out)), "nnhip_layernorm")
         return out
 
     # -- fast path

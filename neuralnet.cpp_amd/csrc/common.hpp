@@ -206,6 +206,8 @@ struct Prefetch
 };
 hipError_t launch_rmsnorm(hipStream_t st, const float* X, const float* gamma, float eps, size_t F,
                           size_t M, float* out);
+hipError_t launch_layernorm(hipStream_t st, const float* X, const float* gamma, const float* beta, float eps,
+                            size_t F, size_t M, float* out);
 // Epilogue of a split-k GEMV (part[S][M][N] slice sums) + residual, then [RMSNorm ->] absmax
 // int8 quantization, one token per block (epilogue_quant_ok: M <= 64, N <= 11264).
 struct EpiArgs

@@ -762,6 +762,18 @@ nnhip_status nnhip_rmsnorm(nnhip_ctx* ctx, const float* X, const float* gamma, f
     return NNHIP_OK;
 }
 
+nnhip_status nnhip_layernorm(nnhip_ctx* ctx, const float* X, const float* gamma, const float* beta, float eps,
+                             size_t F, size_t M, float* out)
+{
+    const char* fn = "nnhip_layernorm";
+    NNHIP_CHECK_CTX(fn);
+    if (M == 0 || F == 0) return NNHIP_OK;
+    NNHIP_REQUIRE(X && gamma && beta && out, fn, "null pointer");
+    NNHIP_REQUIRE(F <= kMaxDim && M <= kMaxDim && mul_ok(F, M), fn, "size overflow");
+    NNHIP_LAUNCH(fn, launch_layernorm(ctx->stream, X, gamma, beta, eps, F, M, out));
+    return NNHIP_OK;
+}
+
 // ------------------------------------------------------------- MI355X-native fast path
 
 size_t nnhip_repacked_bytes(size_t N, size_t K)

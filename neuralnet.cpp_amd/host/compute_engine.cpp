@@ -313,6 +313,21 @@ Result<Tensor> ComputeEngine::rmsnorm(const Tensor& x, const Tensor& gamma, Scal
     return *out;
 }
 
+Result<Tensor> ComputeEngine::layernorm(const Tensor& x, const Tensor& gamma, const Tensor& beta, Scalar eps)
+{
+    EX_TRY_CHECK(check_owned(x, "layernorm: x"));
+    EX_TRY_CHECK(check_owned(gamma, "layernorm: gamma"));
+    EX_TRY_CHECK(check_owned(beta, "layernorm: beta"));
+    if (x.precision() != Precision::F32) return Error{"layernorm: x must be f32"};
+    for (const Tensor* t : {&gamma, &beta})
+        if (t->rows() != x.rows() || t->cols() != 1 || t->precision() != Precision::F32)
+            return Error{"layernorm: gamma and beta must be f32 (" + std::to_string(x.rows()) + ",1), got " +
+                         shape(*t)};
+    EX_TRY(out, alloc_impl(x.rows(), x.cols(), Precision::F32));
+    EX_TRY_CHECK(layernorm_impl(x, gamma, beta, eps, *out));
+    return *out;
+}
+
 Result<Tensor> ComputeEngine::bitlinear_i8_forward(const Tensor& x, const Tensor& wq, const Tensor& tau,
                                                    const Tensor& b, Precision p, Tensor* xq_out, Tensor* s_out)
 {

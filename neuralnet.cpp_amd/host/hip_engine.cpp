@@ -401,6 +401,14 @@ protected:
         return {};
     }
 
+    Result<void> layernorm_impl(const Tensor& x, const Tensor& gamma, const Tensor& beta, Scalar eps,
+                                const Tensor& out) override
+    {
+        NNHIP_TRY(nnhip_layernorm(ctx_->h, fp(x), fp(gamma), fp(beta), eps, x.rows(), x.cols(), fpw(out)),
+                  "layernorm");
+        return {};
+    }
+
     // The last input quantized into the activation scratch. Another BitLinear on the same input
     // (same storage, same write epoch, same shape; e.g. the q / k / v projections of one
     // attention input) reuses it instead of quantizing again. The storage is held weakly, so a

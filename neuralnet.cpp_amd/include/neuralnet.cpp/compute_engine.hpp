@@ -173,6 +173,9 @@ public:
     [[nodiscard]] Result<Tensor> add_row_broadcast(const Tensor& y, const Tensor& b);
     // RMSNorm forward: (x * rsqrt(mean_f x^2 + eps)) * gamma, per column (token)
     [[nodiscard]] Result<Tensor> rmsnorm(const Tensor& x, const Tensor& gamma, Scalar eps);
+    // LayerNorm forward: ((x - mean) * rsqrt(var + eps)) * gamma + beta, per column (token), with
+    // the biased variance (include/neuralnet.cpp/compute_layer_mlp.hpp:529-545); x f32
+    [[nodiscard]] Result<Tensor> layernorm(const Tensor& x, const Tensor& gamma, const Tensor& beta, Scalar eps);
 
     // Fused BitLinear int8 forward, the sequence of compute_layer_bitlinear.hpp:443-456:
     // s = col_reduce_max(|x|) * fl(1/127); xq = quantize_i8(x, s); y = matmul_q_i8(wq, tau, xq, s, p);
@@ -249,6 +252,8 @@ protected:
     [[nodiscard]] virtual Result<void> add_row_broadcast_impl(const Tensor& y, const Tensor& b, const Tensor& out) = 0;
     [[nodiscard]] virtual Result<void> rmsnorm_impl(const Tensor& x, const Tensor& gamma, Scalar eps,
                                                     const Tensor& out) = 0;
+    [[nodiscard]] virtual Result<void> layernorm_impl(const Tensor& x, const Tensor& gamma, const Tensor& beta,
+                                                      Scalar eps, const Tensor& out) = 0;
     // b may be null (no bias); x is f32 here (the public entry casts f16 inputs)
     [[nodiscard]] virtual Result<Tensor> bitlinear_i8_impl(const Tensor& x, const Tensor& wq, const Tensor& tau,
                                                            const Tensor* b, Tensor* xq_out, Tensor* s_out);

@@ -327,7 +327,8 @@ public:
              std::size_t n_head_kv = 0, ActivationType activation = ActivationType::SwiGLU, bool subln = false,
              Scalar norm_eps = 1e-5f, bool inference_only = false)
         : attn_(d_model, num_heads, max_len, n_head_kv, true, subln, inference_only), norm1_(d_model, norm_eps),
-          ff_(d_model, d_ff, activation, subln, inference_only), norm2_(d_model, norm_eps)
+          ff_(d_model, d_ff, activation, subln, NormType::RMSNorm, WeightQuant::T1_58, inference_only),
+          norm2_(d_model, norm_eps)
     {
     }
 

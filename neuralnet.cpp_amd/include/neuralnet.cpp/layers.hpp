@@ -398,6 +398,43 @@ private:
     Tensor gamma_;
 };
 
+// LayerNorm over the features of each token (include/neuralnet.cpp/compute_layer_mlp.hpp:462-545):
+// gain gamma (initialized to 1) and shift beta (0), both f32; forward is ComputeEngine::layernorm,
+// ((x - mean) * rsqrt(var + eps)) * gamma + beta with the biased variance.
+class LayerNorm final : public Layer
+{
+public:
+    explicit LayerNorm(std::size_t normalized_shape, Scalar epsilon = 1e-5f)
+        : normalized_shape_(normalized_shape), epsilon_(epsilon)
+    {
+    }
+    [[nodiscard]] const char* layer_name() const noexcept override { return "LayerNorm"; }
+    [[nodiscard]] std::vector<TensorRef> parameters() override { return {gamma_, beta_}; }
+    [[nodiscard]] Tensor& gamma() noexcept { return gamma_; }
+    [[nodiscard]] Tensor& beta() noexcept { return beta_; }
+    [[nodiscard]] Scalar epsilon() const noexcept { return epsilon_; }
+
+    [[nodiscard]] Result<Tensor> forward(const Tensor& input) override
+    {
+        if (input.rows() != normalized_shape_) return Error{"layernorm forward: input shape mismatch"};
+        return engine_ref().layernorm(input, gamma_, beta_, epsilon_);
+    }
+
+protected:
+    [[nodiscard]] Result<void> init_impl(ComputeEngine& engine) override
+    {
+        gamma_ = engine.create_tensor(normalized_shape_, 1, Precision::F32, InitSpec::constant(1.0f));
+        beta_ = engine.create_tensor(normalized_shape_, 1, Precision::F32, InitSpec::zero());
+        if (!gamma_.valid() || !beta_.valid()) return Error{"LayerNorm: parameter init failed"};
+        return {};
+    }
+
+private:
+    std::size_t normalized_shape_;
+    Scalar epsilon_;
+    Tensor gamma_, beta_;
+};
+
 // Activation of the feed-forward block (include/neuralnet.cpp/model_spec.hpp:47-54).
 enum class ActivationType : std::uint32_t
 {
@@ -406,24 +443,54 @@ enum class ActivationType : std::uint32_t
     ReLU2 = 2,
 };
 
+// Normalization layer type (include/neuralnet.cpp/model_spec.hpp:56-62). FeedForward's SubLN
+// takes LayerNorm (the reference's default) or RMSNorm (BitNet b1.58's); BatchNorm is refused.
+enum class NormType : std::uint32_t
+{
+    LayerNorm = 0,
+    RMSNorm = 1,
+    BatchNorm = 2,
+};
+
+// Weight quantization of the linear sublayers (include/neuralnet.cpp/model_spec.hpp:112-116):
+// T1_58 = BitLinear projections, the only kind this engine provides; None = float Linear.
+enum class WeightQuant : std::uint32_t
+{
+    None = 0,
+    T1_58 = 1,
+};
+
 // Gated feed-forward block with ternary BitLinear projections
-// (include/neuralnet.cpp/compute_layer_feedforward.hpp:22-206, WeightQuant::T1_58):
-// fc1 = BitLinear(d_model -> 2*d_ff) whose rows [0, d_ff) are the gate and [d_ff, 2*d_ff) the
-// up projection, the gated activation (SwiGLU or ReLU^2-GLU), optionally SubLN (an RMSNorm of
-// width d_ff with the RMSNorm default eps, BitNet b1.58's norm type; :37-45, :65, :201-206),
-// fc2 = BitLinear(d_ff -> d_model). With int8 activation quantization on both projections,
-// forward() is one ComputeEngine::ffn_glu_i8_forward (the HIP engine fuses the block);
-// otherwise it chains the layers. Only the gated activations are provided (GeLU is outside
-// this path), and SubLN is an RMSNorm (the reference's LayerNorm variant is not provided).
+// (include/neuralnet.cpp/compute_layer_feedforward.hpp:22-206, WeightQuant::T1_58), with the
+// reference's constructor (:50-65): fc1 = BitLinear(d_model -> 2*d_ff) whose rows [0, d_ff) are
+// the gate and [d_ff, 2*d_ff) the up projection, the gated activation (SwiGLU or ReLU^2-GLU),
+// optionally SubLN of width d_ff (:37-45, :201-206; LayerNorm by default as in the reference,
+// RMSNorm for BitNet b1.58), fc2 = BitLinear(d_ff -> d_model). With int8 activation
+// quantization on both projections and an RMSNorm (or no) SubLN, forward() is one
+// ComputeEngine::ffn_glu_i8_forward (the HIP engine fuses the block); otherwise it chains the
+// layers. Only the gated activations and BitLinear projections are provided: init refuses
+// GeLU, WeightQuant::None (float Linear projections) and a BatchNorm SubLN.
 class FeedForward final : public Layer
 {
 public:
-    FeedForward(std::size_t d_model, std::size_t d_ff, ActivationType activation = ActivationType::SwiGLU,
-                bool subln = false, bool inference_only = false)
-        : d_model_(d_model), d_ff_(d_ff), activation_(activation), fc1_(d_model, 2 * d_ff, inference_only),
-          fc2_(d_ff, d_model, inference_only)
+    FeedForward(std::size_t d_model, std::size_t d_ff, ActivationType activation = ActivationType::GeLU,
+                bool subln = false, NormType subln_norm_type = NormType::LayerNorm,
+                WeightQuant weight_quant = WeightQuant::None, bool inference_only = false)
+        : d_model_(d_model), d_ff_(d_ff), activation_(activation), subln_(subln), norm_type_(subln_norm_type),
+          weight_quant_(weight_quant), fc1_(d_model, 2 * d_ff, inference_only), fc2_(d_ff, d_model, inference_only)
     {
-        if (subln) sub_norm_ = std::make_unique<RMSNorm>(d_ff);
+        if (subln && subln_norm_type == NormType::RMSNorm)
+        {
+            auto n = std::make_unique<RMSNorm>(d_ff);
+            sub_rms_ = n.get();
+            sub_norm_ = std::move(n);
+        }
+        else if (subln && subln_norm_type == NormType::LayerNorm)
+        {
+            auto n = std::make_unique<LayerNorm>(d_ff);
+            sub_ln_ = n.get();
+            sub_norm_ = std::move(n);
+        }
     }
 
     [[nodiscard]] const char* layer_name() const noexcept override { return "FeedForward"; }
@@ -445,11 +512,16 @@ public:
 
     [[nodiscard]] BitLinear& fc1() noexcept { return fc1_; }
     [[nodiscard]] BitLinear& fc2() noexcept { return fc2_; }
-    [[nodiscard]] RMSNorm* sub_norm() noexcept { return sub_norm_.get(); }
+    // the SubLN layer (nullptr without one), and the same as its type
+    [[nodiscard]] Layer* sub_norm() noexcept { return sub_norm_.get(); }
+    [[nodiscard]] RMSNorm* sub_rmsnorm() noexcept { return sub_rms_; }
+    [[nodiscard]] LayerNorm* sub_layernorm() noexcept { return sub_ln_; }
+    [[nodiscard]] NormType subln_norm_type() const noexcept { return norm_type_; }
+    [[nodiscard]] WeightQuant weight_quant() const noexcept { return weight_quant_; }
     [[nodiscard]] std::size_t d_model() const noexcept { return d_model_; }
     [[nodiscard]] std::size_t d_ff() const noexcept { return d_ff_; }
 
-    // fc1, fc2, then the SubLN gamma (compute_layer_feedforward.hpp:87-105)
+    // fc1, fc2, then the SubLN's gamma [and beta] (compute_layer_feedforward.hpp:87-105)
     [[nodiscard]] std::vector<TensorRef> parameters() override
     {
         auto r = fc1_.parameters();
@@ -463,7 +535,7 @@ public:
         return r;
     }
 
-    // entries: fc1 (weights, bias), fc2 (weights, bias), [SubLN gamma] (same order)
+    // entries: fc1 (weights, bias), fc2 (weights, bias), [SubLN gamma [, beta]] (same order)
     [[nodiscard]] std::size_t param_count() override
     {
         return fc1_.param_count() + fc2_.param_count() + (sub_norm_ ? sub_norm_->param_count() : 0);
@@ -505,15 +577,16 @@ private:
         if (input.rows() != d_model_) return Error{"feedforward forward: input shape mismatch"};
         ComputeEngine& engine = engine_ref();
         const int act = activation_ == ActivationType::ReLU2 ? 1 : 0;
-        if (fc1_.activation_quant() && fc2_.activation_quant())
+        // the fused block takes an RMSNorm SubLN; a LayerNorm SubLN runs the chain below
+        if (fc1_.activation_quant() && fc2_.activation_quant() && sub_ln_ == nullptr)
         {
             EX_TRY_CHECK(fc1_.ensure_quantized());
             EX_TRY_CHECK(fc2_.ensure_quantized());
             return engine.ffn_glu_i8_forward(input, norm ? &norm->gamma() : nullptr, norm ? norm->epsilon() : 0.0f,
                                              fc1_.quantized_weights_packed(), fc1_.row_scales(),
                                              fc1_.bias(), fc2_.quantized_weights_packed(), fc2_.row_scales(),
-                                             fc2_.bias(), act, sub_norm_ ? &sub_norm_->gamma() : nullptr,
-                                             sub_norm_ ? sub_norm_->epsilon() : 0.0f);
+                                             fc2_.bias(), act, sub_rms_ ? &sub_rms_->gamma() : nullptr,
+                                             sub_rms_ ? sub_rms_->epsilon() : 0.0f);
         }
         Tensor in = input;
         if (norm)
@@ -537,6 +610,10 @@ protected:
     {
         if (activation_ == ActivationType::GeLU)
             return Error{"FeedForward: only the gated activations (SwiGLU, ReLU2) are provided by this engine"};
+        if (weight_quant_ != WeightQuant::T1_58)
+            return Error{"FeedForward: only BitLinear projections (WeightQuant::T1_58) are provided by this engine"};
+        if (subln_ && !sub_norm_)
+            return Error{"FeedForward: the SubLN norm type must be LayerNorm or RMSNorm (BatchNorm is not provided)"};
         PrecisionProfile linear = p_;
         linear.param = Precision::T1_58;
         fc1_.set_precision_profile(linear);
@@ -556,8 +633,13 @@ protected:
 private:
     std::size_t d_model_, d_ff_;
     ActivationType activation_;
+    bool subln_;
+    NormType norm_type_;
+    WeightQuant weight_quant_;
     BitLinear fc1_, fc2_;
-    std::unique_ptr<RMSNorm> sub_norm_;  // SubLN, or none
+    std::unique_ptr<Layer> sub_norm_;  // SubLN, or none
+    RMSNorm* sub_rms_ = nullptr;       // sub_norm_ as its type
+    LayerNorm* sub_ln_ = nullptr;
 };
 
 }  // namespace nn

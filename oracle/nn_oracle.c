@@ -423,6 +423,58 @@ void orc_rmsnorm(const float* X, const float* gamma, float eps, size_t F, size_t
     }
 }
 
+/* LayerNorm forward: include/neuralnet.cpp/compute_layer_mlp.hpp:529-545 (the SubLN norm type
+ * FeedForward defaults to, compute_layer_feedforward.hpp:50-65):
+ * mean = sum_f x * fl(1/F); d = x - mean; sinv = rsqrt(sum_f d*d * fl(1/F) + eps);
+ * out = (d * sinv) * gamma + beta, rsqrt as 1/sqrtf (the RMSNorm convention above). The two sums
+ * use the order of the GPU kernel: 8 strided parts (f % 8), each ascending, then the tree
+ * ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)). The reference's engine order is not
+ * available; tests pin this restatement against a float64 evaluation and exact special cases. */
+static float orc_tree8(const float* v)
+{
+    const float a = (v[0] + v[1]) + (v[2] + v[3]);
+    const float b = (v[4] + v[5]) + (v[6] + v[7]);
+    return a + b;
+}
+
+void orc_layernorm(const float* X, const float* gamma, const float* beta, float eps, size_t F, size_t M,
+                   float* out)
+{
+    const float inv_f = 1.0f / (float)F;
+    for (size_t m = 0; m < M; ++m)
+    {
+        float p[8];
+        for (int l = 0; l < 8; ++l)
+        {
+            float part = 0.0f;
+            for (size_t f = (size_t)l; f < F; f += 8) part = part + X[f * M + m];
+            p[l] = part;
+        }
+        const float mean = orc_tree8(p) * inv_f;
+        for (int l = 0; l < 8; ++l)
+        {
+            float part = 0.0f;
+            for (size_t f = (size_t)l; f < F; f += 8)
+            {
+                const float d = X[f * M + m] - mean;
+                const float sq = d * d;
+                part = part + sq;
+            }
+            p[l] = part;
+        }
+        const float var = orc_tree8(p) * inv_f;
+        const float v = var + eps;
+        const float sinv = 1.0f / sqrtf(v);
+        for (size_t f = 0; f < F; ++f)
+        {
+            const float d = X[f * M + m] - mean;
+            const float nrm = d * sinv;
+            const float g = nrm * gamma[f];
+            out[f * M + m] = g + beta[f];
+        }
+    }
+}
+
 /* RMSNorm -> per-token absmax scale -> int8, the three steps of
  * include/neuralnet.cpp/compute_layer_mlp.hpp:686-707 followed by
  * include/neuralnet.cpp/compute_layer_bitlinear.hpp:443-448, on the normed values.

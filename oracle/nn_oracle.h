@@ -25,6 +25,9 @@
  *                       reference test's own patterns (:253-334)
  *   orc_rmsnorm*      : textbook formula include/neuralnet.cpp/compute_layer_mlp.hpp:615-619,
  *                       checked against a float64 recomputation within tolerance
+ *   orc_layernorm     : LayerNorm::forward (include/neuralnet.cpp/compute_layer_mlp.hpp:529-545),
+ *                       checked against a float64 recomputation within tolerance and exact
+ *                       special cases (constant token -> beta, F = 1)
  *   orc_repack*       : the MI355X tile layout is this build's own format; pinned by
  *                       the round trip repack -> unrepack == identity
  *   orc_exp           : this build's own fp32 exp (the reference's exp lives in the absent
@@ -106,6 +109,8 @@ void orc_matmul_q_t(const uint32_t* A, const float* tau, const float* B, size_t 
 
 /* ---- RMSNorm and the fused RMSNorm -> absmax -> int8 path ---- */
 void orc_rmsnorm(const float* X, const float* gamma, float eps, size_t F, size_t M, float* out);
+void orc_layernorm(const float* X, const float* gamma, const float* beta, float eps, size_t F, size_t M,
+                   float* out);
 void orc_rmsnorm_quant_i8(const float* X, const float* gamma, float eps, size_t F, size_t M,
                           uint32_t* xq, float* s);
 

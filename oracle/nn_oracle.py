@@ -87,6 +87,7 @@ def _load(path) -> ctypes.CDLL:
         "orc_matmul_q": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
         "orc_matmul_q_t": (None, [_u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p]),
         "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
+        "orc_layernorm": (None, [_f32p, _f32p, _f32p, ctypes.c_float, _sz, _sz, _f32p]),
         "orc_rmsnorm_quant_i8": (None, [_f32p, _f32p, ctypes.c_float, _sz, _sz, _u32p, _f32p]),
         "orc_exp": (ctypes.c_float, [ctypes.c_float]),
         "orc_exp_array": (None, [_f32p, _sz, _f32p]),
@@ -276,6 +277,18 @@ def rmsnorm(X: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
     gamma = _f32(gamma).reshape(F)
     out = np.empty((F, M), np.float32)
     lib().orc_rmsnorm(_p(X, ctypes.c_float), _p(gamma, ctypes.c_float), eps, F, M, _p(out, ctypes.c_float))
+    return out
+
+
+def layernorm(X: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float) -> np.ndarray:
+    """LayerNorm of each token (column) of X (F, M), include/neuralnet.cpp/compute_layer_mlp.hpp:529-545."""
+    X = _f32(X)
+    F, M = X.shape
+    gamma = _f32(gamma).reshape(F)
+    beta = _f32(beta).reshape(F)
+    out = np.empty((F, M), np.float32)
+    lib().orc_layernorm(_p(X, ctypes.c_float), _p(gamma, ctypes.c_float), _p(beta, ctypes.c_float), eps, F, M,
+                        _p(out, ctypes.c_float))
     return out
 
 

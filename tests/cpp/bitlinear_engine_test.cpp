@@ -640,7 +640,7 @@ void test_feedforward(nn::ComputeEngine& e)
     for (const auto act : {nn::ActivationType::SwiGLU, nn::ActivationType::ReLU2})
     {
         const int a = act == nn::ActivationType::ReLU2 ? 1 : 0;
-        nn::FeedForward ff(D, F, act);
+        nn::FeedForward ff(D, F, act, false, nn::NormType::LayerNorm, nn::WeightQuant::T1_58);
         nn::PrecisionProfile prof;
         prof.param = nn::Precision::T1_58;
         ff.set_precision_profile(prof);
@@ -667,7 +667,8 @@ void test_feedforward(nn::ComputeEngine& e)
         // with RMSNorm in front (config C4's block): Model of two layers vs the fused call
         nn::Model model(e);  // default f32 profile: the FeedForward gives its projections T1_58
         CHECK(model.add<nn::RMSNorm>(D, 1e-6f).has_value(), "Model::add<RMSNorm>");
-        CHECK(model.add<nn::FeedForward>(D, F, act).has_value(), "Model::add<FeedForward>");
+        CHECK(model.add<nn::FeedForward>(D, F, act, false, nn::NormType::LayerNorm, nn::WeightQuant::T1_58).has_value(),
+              "Model::add<FeedForward>");
         if (model.num_layers() != 2) return;
         auto& mff = static_cast<nn::FeedForward&>(model.layer_at(1));
         auto mp = mff.parameters();
@@ -693,7 +694,7 @@ void test_feedforward(nn::ComputeEngine& e)
     }
     // SubLN: RMSNorm(d_ff, eps 1e-5) of the gated output before fc2; its gamma is the fifth entry
     {
-        nn::FeedForward sf(D, F, nn::ActivationType::SwiGLU, true);
+        nn::FeedForward sf(D, F, nn::ActivationType::SwiGLU, true, nn::NormType::RMSNorm, nn::WeightQuant::T1_58);
         CHECK(sf.init(e).has_value(), "FeedForward(SwiGLU, SubLN) init");
         auto sp = sf.parameters();  // fc1 latent, fc1 bias, fc2 latent, fc2 bias, SubLN gamma
         CHECK(sp.size() == 5 && sf.param_count() == 5 && sf.sub_norm() != nullptr, "SubLN adds one parameter");
@@ -718,11 +719,71 @@ void test_feedforward(nn::ComputeEngine& e)
             CHECK(g.has_value() && g->kind == nn::ParamKind::Dense && g->rows == F, "SubLN gamma exports Dense");
         }
     }
-    nn::FeedForward gelu(8, 8, nn::ActivationType::GeLU);
+    // SubLN of the reference's default norm type, LayerNorm(d_ff, eps 1e-5): gamma and beta are the
+    // fifth and sixth entries; the block runs fc1 -> glu -> LayerNorm -> fc2 (no fused form)
+    {
+        nn::FeedForward lf(D, F, nn::ActivationType::SwiGLU, true, nn::NormType::LayerNorm, nn::WeightQuant::T1_58);
+        CHECK(lf.init(e).has_value() && lf.sub_layernorm() != nullptr && lf.sub_rmsnorm() == nullptr,
+              "FeedForward(SwiGLU, LayerNorm SubLN) init");
+        auto lp = lf.parameters();  // fc1 latent, fc1 bias, fc2 latent, fc2 bias, SubLN gamma, SubLN beta
+        CHECK(lp.size() == 6 && lf.param_count() == 6, "LayerNorm SubLN adds two parameters");
+        if (lp.size() == 6 && lf.sub_layernorm())
+        {
+            const nn::Matrix gm = download(e, lp[4].get()), bm = download(e, lp[5].get());
+            bool init_ok = gm.rows() == F && bm.rows() == F;
+            for (std::size_t i = 0; init_ok && i < F; ++i) init_ok = gm.at(i, 0) == 1.0f && bm.at(i, 0) == 0.0f;
+            CHECK(init_ok, "LayerNorm gamma starts at 1, beta at 0");
+            CHECK(e.copy_from(lp[0].get(), random_matrix(2 * F, D, 291)).has_value() &&
+                      e.copy_from(lp[1].get(), random_matrix(2 * F, 1, 292)).has_value() &&
+                      e.copy_from(lp[2].get(), random_matrix(D, F, 293)).has_value() &&
+                      e.copy_from(lp[3].get(), random_matrix(D, 1, 294)).has_value() &&
+                      e.copy_from(lp[4].get(), random_matrix(F, 1, 295)).has_value() &&
+                      e.copy_from(lp[5].get(), random_matrix(F, 1, 296)).has_value(),
+                  "write LayerNorm SubLN block parameters");
+            lf.set_activation_quant(true);
+            const nn::Tensor x = upload(e, random_matrix(D, B, 297));
+            auto y = lf.forward(x);
+            auto h1 = lf.fc1().forward(x);
+            auto h2 = h1 ? e.glu(*h1, 0) : nn::Result<nn::Tensor>(nn::Error{"fc1 failed"});
+            auto h3 = h2 ? lf.sub_layernorm()->forward(*h2) : nn::Result<nn::Tensor>(nn::Error{"glu failed"});
+            auto y2 = h3 ? lf.fc2().forward(*h3) : nn::Result<nn::Tensor>(nn::Error{"sub_norm failed"});
+            CHECK(y.has_value() && y2.has_value() && bitwise_equal(download(e, *y), download(e, *y2)),
+                  "LayerNorm SubLN block bit-identical to fc1 -> glu -> LayerNorm -> fc2");
+            // the LayerNorm itself against a host double evaluation of the reference formula
+            bool ln_ok = h2.has_value() && h3.has_value();
+            double err = 0;
+            if (ln_ok)
+            {
+                const nn::Matrix H = download(e, *h2), O = download(e, *h3);
+                const nn::Matrix G = download(e, lp[4].get()), Bt = download(e, lp[5].get());
+                for (std::size_t b = 0; b < B; ++b)
+                {
+                    double mean = 0, var = 0;
+                    for (std::size_t f = 0; f < F; ++f) mean += H.at(f, b);
+                    mean /= F;
+                    for (std::size_t f = 0; f < F; ++f) var += (H.at(f, b) - mean) * (H.at(f, b) - mean);
+                    var /= F;
+                    for (std::size_t f = 0; f < F; ++f)
+                    {
+                        const double r = (H.at(f, b) - mean) / std::sqrt(var + 1e-5) * G.at(f, 0) + Bt.at(f, 0);
+                        err = std::max(err, std::abs(O.at(f, b) - r) / std::max(1.0, std::abs(r)));
+                    }
+                }
+            }
+            CHECK(ln_ok && err < 1e-5, "LayerNorm forward within 1e-5 of a host double evaluation");
+            auto bt = lf.export_param(5, nn::ModelRole::Model);
+            CHECK(bt.has_value() && bt->kind == nn::ParamKind::Dense && bt->rows == F, "SubLN beta exports Dense");
+        }
+    }
+    nn::FeedForward gelu(8, 8, nn::ActivationType::GeLU, false, nn::NormType::LayerNorm, nn::WeightQuant::T1_58);
     nn::PrecisionProfile prof;
     prof.param = nn::Precision::T1_58;
     gelu.set_precision_profile(prof);
     CHECK(!gelu.init(e).has_value(), "GeLU FeedForward is refused (only gated activations)");
+    nn::FeedForward lin(8, 8, nn::ActivationType::SwiGLU);  // the reference's defaults: WeightQuant::None
+    CHECK(!lin.init(e).has_value(), "WeightQuant::None (float Linear projections) is refused");
+    nn::FeedForward bn(8, 8, nn::ActivationType::SwiGLU, true, nn::NormType::BatchNorm, nn::WeightQuant::T1_58);
+    CHECK(!bn.init(e).has_value(), "a BatchNorm SubLN is refused");
 }
 
 // ---------------------------------------------------------------- [14]

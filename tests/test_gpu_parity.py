@@ -209,6 +209,29 @@ def test_rmsnorm_quant(ctx, orc, F, M, eps):
     assert np.array_equal(host(xi)[:, :F], orc.container_to_int8(xq_o, M).T)
 
 
+@pytest.mark.parametrize("F,M,loc", [(2560, 33, 0.0), (6912, 64, 3.0), (1, 5, 0.0), (17, 1, -1.0), (300, 1000, 0.5),
+                                     (13, 2048, 0.0), (2560, 31, 0.0)])
+def test_layernorm(ctx, orc, F, M, loc):
+    say(f"layernorm F={F} M={M}")
+    X = normal((F, M), F + M, loc, 1.0)
+    if M > 2:
+        X[:, 2] = 0.625          # a constant token: beta exactly
+    g = normal((F,), 3, 1.0, 0.1)
+    b = normal((F,), 4, 0.0, 0.5)
+    out = host(ctx.layernorm(dev(X), dev(g), dev(b), 1e-5))
+    ref = orc.layernorm(X, g, b, 1e-5)
+    assert np.array_equal(out, ref)
+    if M > 2:
+        assert np.array_equal(out[:, 2], b)
+
+
+def test_layernorm_rejects_short_gain(ctx, nnhip):
+    import torch
+    X = torch.zeros((8, 3), device="cuda")
+    with pytest.raises(nnhip.NNHipError):
+        ctx.layernorm(X, torch.ones(7, device="cuda"), torch.zeros(8, device="cuda"))
+
+
 def check_quant(ctx, orc, X, g=None, eps=1e-6):
     """act_quant_i8 (g None) or rmsnorm_quant_i8 on X (K, M) against the oracle, all outputs."""
     K, M = X.shape

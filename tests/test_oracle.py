@@ -203,6 +203,54 @@ def test_rmsnorm_close_to_float64(orc):
     assert np.max(np.abs(out - ref) / np.maximum(np.abs(ref), 1e-3)) < 2e-6
 
 
+# ---------------------------------------------------------------- LayerNorm
+
+def _layernorm64(X, g, b, eps):
+    x64 = X.astype(np.float64)
+    d = x64 - x64.mean(axis=0)
+    return d / np.sqrt((d ** 2).mean(axis=0) + eps) * g.astype(np.float64)[:, None] + b.astype(np.float64)[:, None]
+
+
+@pytest.mark.parametrize("F,M,loc,eps", [(2560, 33, 0.0, 1e-5), (6912, 5, 4.0, 1e-5), (300, 17, -2.5, 1e-6),
+                                         (4, 9, 1.0, 1e-2)])
+def test_layernorm_close_to_float64(orc, F, M, loc, eps):
+    """The mean is subtracted (loc != 0), the variance is the biased one (a 1/(F-1) variance is
+    2e-4 off at F=2560), eps sits inside the square root (F=4, eps=1e-2 moves every value), and
+    beta is added after the gain."""
+    X = normal((F, M), F + M, loc, 1.0)
+    g = normal((F,), 10, 1.0, 0.1)
+    b = normal((F,), 11, 0.0, 0.5)
+    out = orc.layernorm(X, g, b, eps)
+    ref = _layernorm64(X, g, b, eps)
+    # fp32 sums of F values around a mean of |loc| leave ~1e-6 absolute in d = x - mean
+    assert np.max(np.abs(out - ref) - 1e-5 * np.abs(ref)) < 5e-6
+
+
+def test_layernorm_exact_cases(orc):
+    """A constant token (every deviation 0) and F = 1 give beta exactly, whatever gamma and eps."""
+    F, M = 257, 4
+    X = normal((F, M), 5)
+    X[:, 1] = 3.25
+    X[:, 3] = -1e30
+    g = normal((F,), 6, 1.0, 0.1)
+    b = normal((F,), 7)
+    out = orc.layernorm(X, g, b, 1e-5)
+    assert np.array_equal(out[:, 1], b) and np.array_equal(out[:, 3], b)
+    X1 = normal((1, 6), 8)
+    g1, b1 = np.array([2.0], np.float32), np.array([-0.75], np.float32)
+    assert np.array_equal(orc.layernorm(X1, g1, b1, 1e-5), np.full((1, 6), -0.75, np.float32))
+
+
+def test_layernorm_unit_gain_standardizes(orc):
+    """gamma = 1, beta = 0: every token has mean ~0 and variance ~1 / (1 + eps / var)."""
+    X = normal((1024, 8), 9, 2.0, 3.0)
+    out = orc.layernorm(X, np.ones(1024, np.float32), np.zeros(1024, np.float32), 1e-5)
+    o64 = out.astype(np.float64)
+    assert np.max(np.abs(o64.mean(axis=0))) < 1e-6
+    var = X.astype(np.float64).var(axis=0)
+    assert np.allclose(o64.var(axis=0), var / (var + 1e-5), rtol=0, atol=1e-5)
+
+
 def test_rmsnorm_quant_is_the_sequence(orc):
     X = normal((700, 21), 12)
     g = np.ones(700, np.float32)
