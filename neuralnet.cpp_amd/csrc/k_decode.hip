@@ -47,6 +47,10 @@ constexpr int kAttnThreads = 256;  // 4 waves
 #define NNHIP_ATTN_PB 2            // score passes (32 positions each) whose loads are in flight together
                                    // (2: 136.0 us at 16 x 8192 positions, 4: 141.6; equal at 2112)
 #endif
+#ifndef NNHIP_ATTN_PB_H
+#define NNHIP_ATTN_PB_H 4          // the same over f16 caches (rows held packed: every pass at once;
+                                   // C5 30.9-31.3 us with the merge against 31.5-32.0 at 2 passes)
+#endif
 constexpr int kRecPad = 16;        // record tail: max[8], sum[8]
 
 struct AttnArgs
@@ -107,26 +111,47 @@ __device__ __forceinline__ float4 ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff,
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
 }
 
-// Four cache elements at byte offset voff + soff as floats: 16 bytes of f32, or 8 bytes of f16
-// widened exactly (the same cache policy).
-template <typename CT>
-__device__ __forceinline__ float4 ld_c4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
-{
-    if constexpr (sizeof(CT) == 4) return ld_f4(r, voff, soff);
-    else
-    {
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-        const h4 h = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
-        return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
-    }
-}
-
 // x as the cache stores it: itself in an f32 cache, the nearest f16 (ties to even) in an f16 one
 template <typename CT>
 __device__ __forceinline__ float cache_round(float x)
 {
     if constexpr (sizeof(CT) == 4) return x;
     else return (float)(_Float16)x;
+}
+
+// Four cache elements as they are held between their load and their use: a float4 from an f32
+// cache, or the four halves of an f16 one packed in two registers (half the registers, so twice
+// the rows can be in flight), widened by widen4 where they are used.
+template <typename CT>
+struct CacheQuad
+{
+    using type = float4;
+};
+template <>
+struct CacheQuad<_Float16>
+{
+    typedef uint32_t type __attribute__((ext_vector_type(2)));
+};
+
+template <typename CT>
+__device__ __forceinline__ typename CacheQuad<CT>::type ld_q4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    if constexpr (sizeof(CT) == 4) return ld_f4(r, voff, soff);
+    else
+        return __builtin_bit_cast(typename CacheQuad<CT>::type,
+                                  __builtin_amdgcn_raw_buffer_load_b64(r, voff + soff, 0, NNHIP_ATTN_LOAD_AUX));
+}
+
+template <typename CT>
+__device__ __forceinline__ float4 widen4(typename CacheQuad<CT>::type v)
+{
+    if constexpr (sizeof(CT) == 4) return v;
+    else
+    {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 h = __builtin_bit_cast(h4, v);
+        return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    }
 }
 
 // 4 bytes at byte offset off of the resource (0 when out of range), default cache policy
@@ -153,7 +178,9 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
     constexpr int HALF = DK / 2;
     constexpr int Q4 = DK / 4;         // float4 per row
     constexpr int F4 = DK / 32;        // float4 per lane in the score phase (8 lanes per position)
-    constexpr int PB = DK <= 128 ? NNHIP_ATTN_PB : 2;  // position passes whose loads are issued together
+    constexpr bool kH = sizeof(CT) == 2;  // f16 cache rows, held packed until use
+    constexpr int PB = DK <= 128 ? (kH ? NNHIP_ATTN_PB_H : NNHIP_ATTN_PB) : 2;  // passes whose loads go together
+    using Quad = typename CacheQuad<CT>::type;
     constexpr int VL = DK / 4;         // lanes per row in the value phase
     constexpr int NG = kAttnThreads / VL;  // rows per value step
     constexpr int QI = (RT * HALF + kAttnThreads - 1) / kAttnThreads;  // query pairs per thread
@@ -259,7 +286,7 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         constexpr uint32_t ES = sizeof(CT);  // bytes per cache element
         const __amdgpu_buffer_rsrc_t rk =
             attn_rsrc(static_cast<const CT*>(a.kc) + seq_off, (uint32_t)((size_t)a.max_len * rstride * ES));
-        float4 kv[PB][F4];
+        Quad kv[PB][F4];
         auto load_keys = [&](int pass0) {
 #pragma unroll
             for (int u = 0; u < PB; ++u)
@@ -268,10 +295,27 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
                 const int t = t0 + tl;
                 const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * ES : 0x80000000u;
 #pragma unroll
-                for (int i = 0; i < F4; ++i) kv[u][i] = ld_c4<CT>(rk, row, 4u * ES * (j8 + 8 * i));
+                for (int i = 0; i < F4; ++i) kv[u][i] = ld_q4<CT>(rk, row, 4u * ES * (j8 + 8 * i));
             }
         };
         load_keys(0);
+
+        // value-row geometry: VL lanes per row (one quad each), NG rows per step, VR rows per thread
+        constexpr int VR = kAttnT / NG;
+        const int vg = tid / VL, vi = tid % VL;
+        Quad vv[VR];
+        const __amdgpu_buffer_rsrc_t rv =
+            attn_rsrc(static_cast<const CT*>(a.vc) + seq_off, (uint32_t)((size_t)a.max_len * rstride * ES));
+        auto load_values = [&]() {
+#pragma unroll
+            for (int u = 0; u < VR; ++u)
+            {
+                const int tl = vg + u * NG;
+                const int t = t0 + tl;
+                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * ES : 0x80000000u;
+                vv[u] = ld_q4<CT>(rv, row, 4u * ES * vi);
+            }
+        };
 
         // ---- stage the rotated queries (R heads) and, in the chunk holding p, the new key/value
         float* qf = reinterpret_cast<float*>(q_s);
@@ -324,23 +368,6 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             }
         }
 
-        // value-row geometry: VL lanes per row (one float4 each), NG rows per step, VR rows per thread
-        constexpr int VR = kAttnT / NG;
-        const int vg = tid / VL, vi = tid % VL;
-        float4 vv[VR];
-        const __amdgpu_buffer_rsrc_t rv =
-            attn_rsrc(static_cast<const CT*>(a.vc) + seq_off, (uint32_t)((size_t)a.max_len * rstride * ES));
-        auto load_values = [&]() {
-#pragma unroll
-            for (int u = 0; u < VR; ++u)
-            {
-                const int tl = vg + u * NG;
-                const int t = t0 + tl;
-                const uint32_t row = (tl < n && t < p) ? (uint32_t)t * (uint32_t)rstride * ES : 0x80000000u;
-                vv[u] = ld_c4<CT>(rv, row, 4u * ES * vi);
-            }
-        };
-
         // ---- scores of the chunk, PB passes of 32 positions at a time
 #pragma unroll
         for (int pass0 = 0; pass0 < kAttnT / 32; pass0 += PB)
@@ -350,16 +377,28 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             for (int u = 0; u < PB; ++u)
             {
                 const int tl = (pass0 + u) * 32 + pg;
-                if (t0 + tl == p)
+                // the row widened; the new position's key comes from LDS (in place over f32)
+                float4 kk[F4];
+                if constexpr (kH)
                 {
 #pragma unroll
-                    for (int i = 0; i < F4; ++i) kv[u][i] = kn_s[j8 + 8 * i];
-                }
-            }
+                    for (int i = 0; i < F4; ++i) kk[i] = widen4<CT>(kv[u][i]);
+                    if (t0 + tl == p)
+                    {
 #pragma unroll
-            for (int u = 0; u < PB; ++u)
-            {
-                const int tl = (pass0 + u) * 32 + pg;
+                        for (int i = 0; i < F4; ++i) kk[i] = kn_s[j8 + 8 * i];
+                    }
+                }
+                else
+                {
+                    if (t0 + tl == p)
+                    {
+#pragma unroll
+                        for (int i = 0; i < F4; ++i) kv[u][i] = kn_s[j8 + 8 * i];
+                    }
+#pragma unroll
+                    for (int i = 0; i < F4; ++i) kk[i] = kv[u][i];
+                }
                 float d[RT];
 #pragma unroll
                 for (int r = 0; r < RT; ++r)
@@ -371,10 +410,10 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
                         for (int i = 0; i < F4; ++i)
                         {
                             const float4 qq = q_s[r * Q4 + j8 + 8 * i];
-                            d[r] = __builtin_fmaf(kv[u][i].x, qq.x, d[r]);
-                            d[r] = __builtin_fmaf(kv[u][i].y, qq.y, d[r]);
-                            d[r] = __builtin_fmaf(kv[u][i].z, qq.z, d[r]);
-                            d[r] = __builtin_fmaf(kv[u][i].w, qq.w, d[r]);
+                            d[r] = __builtin_fmaf(kk[i].x, qq.x, d[r]);
+                            d[r] = __builtin_fmaf(kk[i].y, qq.y, d[r]);
+                            d[r] = __builtin_fmaf(kk[i].z, qq.z, d[r]);
+                            d[r] = __builtin_fmaf(kk[i].w, qq.w, d[r]);
                         }
                         d[r] = sum8(d[r]);
                     }
@@ -390,7 +429,8 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         __syncthreads();
 
         // ---- value rows of the whole chunk: issued before the softmax so its latency hides
-        //      behind them
+        //      behind them (with the first key rows instead, over f16 caches: 8 VGPRs of spills
+        //      at 96, 38.7 against 31.1 us)
         load_values();
 
         // ---- chunk softmax statistics: one wave per head
@@ -416,9 +456,12 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
         __syncthreads();
 
         // ---- weighted values (the new position's value from LDS)
+        if constexpr (!kH)
+        {
 #pragma unroll
-        for (int u = 0; u < VR; ++u)
-            if (t0 + vg + u * NG == p) vv[u] = vn_s[vi];
+            for (int u = 0; u < VR; ++u)
+                if (t0 + vg + u * NG == p) vv[u] = vn_s[vi];
+        }
         float4 acc[RT];
 #pragma unroll
         for (int r = 0; r < RT; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -428,15 +471,18 @@ __global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_M
             const int tl = vg + u * NG;
             if (tl < n)
             {
+                float4 vf = widen4<CT>(vv[u]);
+                if constexpr (kH)
+                    if (t0 + tl == p) vf = vn_s[vi];
 #pragma unroll
                 for (int r = 0; r < RT; ++r)
                     if (r < R)
                     {
                         const float pr = S[r][tl];
-                        acc[r].x = __builtin_fmaf(pr, vv[u].x, acc[r].x);
-                        acc[r].y = __builtin_fmaf(pr, vv[u].y, acc[r].y);
-                        acc[r].z = __builtin_fmaf(pr, vv[u].z, acc[r].z);
-                        acc[r].w = __builtin_fmaf(pr, vv[u].w, acc[r].w);
+                        acc[r].x = __builtin_fmaf(pr, vf.x, acc[r].x);
+                        acc[r].y = __builtin_fmaf(pr, vf.y, acc[r].y);
+                        acc[r].z = __builtin_fmaf(pr, vf.z, acc[r].z);
+                        acc[r].w = __builtin_fmaf(pr, vf.w, acc[r].w);
                     }
             }
         }
