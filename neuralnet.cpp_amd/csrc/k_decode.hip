@@ -43,6 +43,11 @@ constexpr int kAttnThreads = 256;  // 4 waves
 #ifndef NNHIP_ATTN_MINW
 #define NNHIP_ATTN_MINW 5          // waves per SIMD the chunk kernel is compiled for (<= 96 VGPRs)
 #endif
+#ifndef NNHIP_ATTN_MINW_H
+#define NNHIP_ATTN_MINW_H 5        // over f16 caches. 6 (80 VGPRs, no spills) takes C5's 1360 items
+                                   // in one round: the lone call 28.7-29.1 against 31.2-31.3 us, but
+                                   // the decode step 2.045 against 2.031 ms (A/B, same ids)
+#endif
 #ifndef NNHIP_ATTN_PB
 #define NNHIP_ATTN_PB 2            // score passes (32 positions each) whose loads are in flight together
                                    // (2: 136.0 us at 16 x 8192 positions, 4: 141.6; equal at 2112)
@@ -173,7 +178,7 @@ __device__ __forceinline__ void lds_only_barrier()
 }
 
 template <int DK, int RT, bool kFinal, typename CT>
-__global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? NNHIP_ATTN_MINW : 1) void k_attn_chunk(AttnArgs a)
+__global__ __launch_bounds__(kAttnThreads, (DK <= 128 && RT <= 4) ? (sizeof(CT) == 2 ? NNHIP_ATTN_MINW_H : NNHIP_ATTN_MINW) : 1) void k_attn_chunk(AttnArgs a)
 {
     constexpr int HALF = DK / 2;
     constexpr int Q4 = DK / 4;         // float4 per row
