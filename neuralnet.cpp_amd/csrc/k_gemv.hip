@@ -117,51 +117,6 @@ __device__ __forceinline__ void stage_x(uint8_t* lds, const XStage* __restrict__
     __syncthreads();
 }
 
-// One item's outputs (the transposed tile: lane 16 g + r holds tokens 4 g + i of row r).
-template <int kRTW>
-struct TileOut
-{
-    float y[kRTW][4];
-    uint32_t base[kRTW];  // element index of (row n, token 4 g), kNone past N or M
-    __amdgpu_buffer_rsrc_t ry;
-    int M;
-};
-constexpr uint32_t kNone = 0xFFFFFFFFu;
-
-// Masked lanes store out of range (the output is below 2 GiB, so kOOB + 16 is past it): dropped
-// by the buffer unit. With M a multiple of 4 a lane's four tokens are one 16-byte store (the 16
-// lanes of a row tile write its 16 x 16 block as 1 KiB contiguous), written through the L2
-// (kPolicySys): the M = 16 sweep writes 44 MB of outputs beside 527 MB of weights, and left
-// dirty in the L2 they cost 101.2-101.8 against 97.9-98.8 us. Otherwise (M = 1: 64 bytes per
-// row tile) one store per token with the default policy.
-template <int kRTW>
-__device__ __forceinline__ void store_tile(const TileOut<kRTW>& q)
-{
-    const uint32_t tb = 4u * ((threadIdx.x & 63u) >> 4);
-#pragma unroll
-    for (int r = 0; r < kRTW; ++r)
-    {
-        if ((q.M & 3) == 0)
-        {
-            const uint32_t off = q.base[r] != kNone ? q.base[r] * 4u : kOOB;
-            __builtin_amdgcn_raw_buffer_store_b128(
-                u32x4{__builtin_bit_cast(uint32_t, q.y[r][0]), __builtin_bit_cast(uint32_t, q.y[r][1]),
-                      __builtin_bit_cast(uint32_t, q.y[r][2]), __builtin_bit_cast(uint32_t, q.y[r][3])},
-                q.ry, off, 0, kPolicySys);
-        }
-        else
-        {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                if (i >= q.M) break;  // uniform: no store that every lane would drop
-                const uint32_t off = (q.base[r] != kNone && tb + i < (uint32_t)q.M) ? (q.base[r] + i) * 4u : kOOB;
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, q.y[r][i]), q.ry, off, 0, 0);
-            }
-        }
-    }
-}
-
 // Loads are unconditional: a stage past the last k tile reads beyond its resource
 // (num_records = KT KiB), which returns zero words (code 0: no contribution). On the LDS
 // path the activations of stage kt+1 are read from LDS while stage kt computes (LDS reads
@@ -296,24 +251,45 @@ __device__ __forceinline__ void gemv_item(const GemvProblem& p, int rt0, int lan
     default: gemv_stream<LDS, kRTW, kDepth, 0, kThreads, kStage>(p.KT, s, acc, lds, xs, n_x); break;
     }
 
-    TileOut<kRTW> q;
-    q.ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
-    q.M = p.M;
+    // Masked lanes store out of range (the output is below 2 GiB, so kOOB + 16 is past it): dropped
+    // by the buffer unit. With M a multiple of 4 a lane's four tokens are one 16-byte store (the 16
+    // lanes of a row tile write its 16 x 16 block as 1 KiB contiguous), written through the L2
+    // (kPolicySys): the M = 16 sweep writes 44 MB of outputs beside 527 MB of weights, and left
+    // dirty in the L2 they cost 101.2-101.8 against 97.9-98.8 us. Otherwise (M = 1: 64 bytes per
+    // row tile) one store per token with the default policy.
+    const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.N * (uint32_t)p.M * 4u);
 #pragma unroll
     for (int r = 0; r < kRTW; ++r)
     {
         const uint32_t n = (uint32_t)(rt0 + r) * 16u + rl;
+        float y[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
         {
             const int a = acc_sum(acc[r], i) - rs2[i];
-            float y = (tv[r] * sv[i]) * (float)a;
-            if (p.bias) y = y + bv[r];
-            q.y[r][i] = y;
+            y[i] = (tv[r] * sv[i]) * (float)a;
+            if (p.bias) y[i] = y[i] + bv[r];
         }
-        q.base[r] = (n < (uint32_t)p.N && tb < (uint32_t)p.M) ? n * (uint32_t)p.M + tb : kNone;
+        const bool live = n < (uint32_t)p.N && tb < (uint32_t)p.M;
+        const uint32_t base = n * (uint32_t)p.M + tb;
+        if ((p.M & 3) == 0)
+        {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__builtin_bit_cast(uint32_t, y[0]), __builtin_bit_cast(uint32_t, y[1]),
+                      __builtin_bit_cast(uint32_t, y[2]), __builtin_bit_cast(uint32_t, y[3])},
+                ry, live ? base * 4u : kOOB, 0, kPolicySys);
+        }
+        else
+        {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                if (i >= p.M) break;  // uniform: no store that every lane would drop
+                const uint32_t off = (live && tb + i < (uint32_t)p.M) ? (base + i) * 4u : kOOB;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[i]), ry, off, 0, 0);
+            }
+        }
     }
-    store_tile(q);
 }
 
 // Single problem: static assignment of items to waves.
