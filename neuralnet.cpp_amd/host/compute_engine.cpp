@@ -306,6 +306,7 @@ Result<Tensor> ComputeEngine::rmsnorm(const Tensor& x, const Tensor& gamma, Scal
 {
     EX_TRY_CHECK(check_owned(x, "rmsnorm: x"));
     EX_TRY_CHECK(check_owned(gamma, "rmsnorm: gamma"));
+    EX_TRY_CHECK(require_f32(x, "rmsnorm", "x"));
     if (gamma.rows() != x.rows() || gamma.cols() != 1)
         return Error{"rmsnorm: gamma must be (" + std::to_string(x.rows()) + ",1), got " + shape(gamma)};
     EX_TRY(out, alloc_impl(x.rows(), x.cols(), Precision::F32));
@@ -440,10 +441,22 @@ Result<Tensor> ComputeEngine::attention_decode(const Tensor& q, const Tensor& k,
     return *out;
 }
 
+Result<Tensor> ComputeEngine::cast(const Tensor& t, Precision p)
+{
+    EX_TRY_CHECK(check_owned(t, "cast"));
+    if (t.precision() == p) return t;
+    if (p == Precision::F32 && t.precision() == Precision::F16) return widen_f32(t);
+    if (p == Precision::F16 && t.precision() == Precision::F32) return narrow_to(t, Precision::F16);
+    return Error{std::string("cast: only f32 <-> f16 (") + precision_name(t.precision()) + " -> " + precision_name(p) +
+                 ")"};
+}
+
 Result<Tensor> ComputeEngine::add(const Tensor& x, const Tensor& y)
 {
     EX_TRY_CHECK(check_owned(x, "add: x"));
     EX_TRY_CHECK(check_owned(y, "add: y"));
+    EX_TRY_CHECK(require_f32(x, "add", "x"));
+    EX_TRY_CHECK(require_f32(y, "add", "y"));
     if (x.rows() != y.rows() || x.cols() != y.cols()) return Error{"add: shape mismatch " + shape(x) + " vs " + shape(y)};
     EX_TRY(out, alloc_impl(x.rows(), x.cols(), Precision::F32));
     EX_TRY_CHECK(add_impl(x, y, *out));
@@ -463,6 +476,7 @@ Result<Tensor> ComputeEngine::embedding_gather(const Tensor& table, const Tensor
 Result<Tensor> ComputeEngine::argmax_cols(const Tensor& logits)
 {
     EX_TRY_CHECK(check_owned(logits, "argmax_cols"));
+    EX_TRY_CHECK(require_f32(logits, "argmax_cols", "logits"));
     if (logits.rows() == 0) return Error{"argmax_cols: empty logits"};
     EX_TRY(out, alloc_impl(logits.cols(), 1, Precision::F32));
     EX_TRY_CHECK(argmax_cols_impl(logits, *out));

@@ -216,6 +216,9 @@ public:
                                                   std::size_t heads, std::size_t kv_heads, Scalar scale);
     // x + y (the residual adds of GPTBlock::forward_step, compute_layer_gpt.hpp:208-218)
     [[nodiscard]] Result<Tensor> add(const Tensor& x, const Tensor& y);
+    // t in precision p (F32 or F16): f16 -> f32 widens exactly, f32 -> f16 rounds to nearest even
+    // (the reference's boundary cast); t itself when it already has p
+    [[nodiscard]] Result<Tensor> cast(const Tensor& t, Precision p);
     // gather_rows(table, ids) + transpose (compute_layer_gpt.hpp:700-704): table (V, d) -> (d, B)
     [[nodiscard]] Result<Tensor> embedding_gather(const Tensor& table, const Tensor& ids);
     // greedy token per column of logits (V, B) (compute_layer_base.hpp:1152-1160) -> (B, 1) ids

@@ -23,7 +23,14 @@
 //     (B*max_len, Hkv*d_k) instead of (max_len, H*d_k);
 //   * norms are RMSNorm and position encoding is RoPE or none (BitNet b1.58's choices); the
 //     full-sequence training forward and the sliding-window cache rebuild are not provided
-//     (decode only: generate_greedy refuses prompts + tokens beyond max_len).
+//     (decode only: generate_greedy refuses prompts + tokens beyond max_len);
+//   * under compute = F16 (the t1_58 preset) the tensors the reference hands between layers in
+//     the compute precision are f16 here too: the BitLinear outputs, the attention output, the
+//     residual sums (x + a, r2 + f) and the KV caches; the norms (stable = F32) and the LM head
+//     (compute = stable, compute_layer_gpt.hpp:335-337) give f32. Inside the attention the
+//     scores, softmax and weighted sums run in f32 on the widened f16 operands (the reference
+//     rounds them to f16 too), as do the gated activation and the residual additions before
+//     their results are rounded.
 
 #include <algorithm>
 #include <cmath>
@@ -89,11 +96,13 @@ inline PrecisionProfile float_part(PrecisionProfile p)
     p.param = Precision::F32;
     return p;
 }
-// The decoder's block activations, residual stream and KV caches are f32: init refuses a
-// compute = F16 profile (the reference's t1_58 preset, src/t1_58_test.cpp:668-690) rather than
-// hand f16 BitLinear outputs to f32 kernels. The engine's attention itself takes f16 caches
-// (ComputeEngine::attention_decode, nnhip_attention_decode_h).
-inline PrecisionSet decoder_compute() { return PrecisionSet::of({Precision::F32}); }
+// The decoder takes compute = F32 or F16 (the reference's t1_58 preset, src/t1_58_test.cpp:668-690);
+// act_precision is the precision of the activations handed between its layers.
+inline PrecisionSet decoder_compute() { return PrecisionSet::of({Precision::F32, Precision::F16}); }
+inline Precision act_precision(const PrecisionProfile& p)
+{
+    return p.compute == Precision::F16 ? Precision::F16 : Precision::F32;
+}
 }  // namespace detail
 
 // KV cache of one attention layer for B sequences: rows [b*max_len, (b+1)*max_len) of k / v
@@ -227,14 +236,15 @@ public:
     }
 
     // Zero-filled caches for `batch` sequences, in the compute precision as the reference creates
-    // them (compute_layer_gpt.hpp:764-765): f32, the only compute precision this decoder takes.
+    // them (compute_layer_gpt.hpp:764-765): f16 under compute = F16, else f32.
     [[nodiscard]] Result<KVCache> make_cache(std::size_t batch)
     {
         KVCache c;
         c.batch = batch;
         c.max_len = max_len_;
-        c.k = engine_ref().create_tensor(batch * max_len_, n_head_kv_ * d_k_, Precision::F32, InitSpec::zero());
-        c.v = engine_ref().create_tensor(batch * max_len_, n_head_kv_ * d_k_, Precision::F32, InitSpec::zero());
+        const Precision cp = detail::act_precision(p_);
+        c.k = engine_ref().create_tensor(batch * max_len_, n_head_kv_ * d_k_, cp, InitSpec::zero());
+        c.v = engine_ref().create_tensor(batch * max_len_, n_head_kv_ * d_k_, cp, InitSpec::zero());
         if (!c.k.valid() || !c.v.valid()) return Error{"CausalSelfAttention: KV cache allocation failed"};
         return c;
     }
@@ -254,17 +264,30 @@ public:
         EX_TRY(q, w_q_.forward(x_new));
         EX_TRY(k, w_k_.forward(x_new));
         EX_TRY(v, w_v_.forward(x_new));
-        // 1.5-8. RoPE, cache append, scores, softmax, weighted values
+        // 1.5-8. RoPE, cache append, scores, softmax, weighted values (f32 arithmetic; under
+        // compute = F16 on the widened f16 projections and f16 caches, the output rounded to f16)
         const RotaryTable* rt = rotary();
-        EX_TRY(a, engine.attention_decode(*q, *k, *v, cache.k, cache.v, max_len_, positions, len_bound,
-                                          rt ? &rt->cos() : nullptr, rt ? &rt->sin() : nullptr, num_heads_,
-                                          n_head_kv_, scale_));
-        // 9. SubLN, output projection
+        const Precision P = detail::act_precision(p_);
+        EX_TRY(q32, engine.cast(*q, Precision::F32));
+        EX_TRY(k32, engine.cast(*k, Precision::F32));
+        EX_TRY(v32, engine.cast(*v, Precision::F32));
+        EX_TRY(a32, engine.attention_decode(*q32, *k32, *v32, cache.k, cache.v, max_len_, positions, len_bound,
+                                            rt ? &rt->cos() : nullptr, rt ? &rt->sin() : nullptr, num_heads_,
+                                            n_head_kv_, scale_));
+        // 9. SubLN (f32 in, f32 out), output projection
         if (sub_norm_)
         {
-            EX_TRY(n, sub_norm_->forward(*a));
+            if (P == Precision::F32)
+            {
+                EX_TRY(n, sub_norm_->forward(*a32));
+                return w_o_.forward(*n);
+            }
+            EX_TRY(a16, engine.cast(*a32, P));
+            EX_TRY(aw, engine.cast(*a16, Precision::F32));
+            EX_TRY(n, sub_norm_->forward(*aw));
             return w_o_.forward(*n);
         }
+        EX_TRY(a, engine.cast(*a32, P));
         return w_o_.forward(*a);
     }
 
@@ -376,12 +399,30 @@ public:
     [[nodiscard]] Result<Tensor> forward_step(ComputeEngine& engine, const Tensor& x, KVCache& cache,
                                               const Tensor& positions, std::size_t len_bound)
     {
-        EX_TRY(n1, norm1_.forward(x));
+        const Precision P = detail::act_precision(p_);
+        if (P == Precision::F32)
+        {
+            EX_TRY(n1, norm1_.forward(x));
+            EX_TRY(a, attn_.forward_step(engine, *n1, cache, positions, len_bound));
+            EX_TRY(r2, engine.add(x, *a));
+            // norm2 -> FFN; with int8 activations the engine runs the norm inside the fused block
+            EX_TRY(f, ff_.forward_with_norm(*r2, norm2_));
+            return engine.add(*r2, *f);
+        }
+        // compute = F16: x, the attention and FFN outputs and both residual sums are f16; each sum
+        // is taken in f32 on the widened operands and rounded once (:208-216)
+        EX_TRY(xw, engine.cast(x, Precision::F32));
+        EX_TRY(n1, norm1_.forward(*xw));
         EX_TRY(a, attn_.forward_step(engine, *n1, cache, positions, len_bound));
-        EX_TRY(r2, engine.add(x, *a));
-        // norm2 -> FFN; with int8 activations the engine runs the norm inside the fused block
-        EX_TRY(f, ff_.forward_with_norm(*r2, norm2_));
-        return engine.add(*r2, *f);
+        EX_TRY(aw, engine.cast(*a, Precision::F32));
+        EX_TRY(s1, engine.add(*xw, *aw));
+        EX_TRY(r2, engine.cast(*s1, P));
+        EX_TRY(r2w, engine.cast(*r2, Precision::F32));
+        EX_TRY(n2, norm2_.forward(*r2w));
+        EX_TRY(f, ff_.forward(*n2));
+        EX_TRY(fw, engine.cast(*f, Precision::F32));
+        EX_TRY(s2, engine.add(*r2w, *fw));
+        return engine.cast(*s2, P);
     }
 
 protected:
@@ -488,7 +529,8 @@ public:
             if (!r) return Error{"GPTBlock " + std::to_string(i) + ": " + r.error().message};
             x = *r;
         }
-        EX_TRY(n, ln_f_.forward(x));
+        EX_TRY(xw, engine.cast(x, Precision::F32));
+        EX_TRY(n, ln_f_.forward(*xw));
         return head_.forward(*n);
     }
 
@@ -535,7 +577,8 @@ public:
             EX_TRY(ids, upload_indices(engine, cur.data(), B));
             EX_TRY(pt, upload_indices(engine, pos.data(), B));
             EX_TRY(logits, forward_step(engine, *ids, *pt, s + 1, *caches));
-            EX_TRY(next_t, engine.argmax_cols(*logits));
+            EX_TRY(lw, engine.cast(*logits, Precision::F32));
+            EX_TRY(next_t, engine.argmax_cols(*lw));
             EX_TRY(next, download_indices(engine, *next_t));
             for (std::size_t b = 0; b < B; ++b)
             {
@@ -559,7 +602,11 @@ protected:
         }
         ln_f_.set_precision_profile(detail::float_part(p_));
         EX_TRY_CHECK(ln_f_.init(engine));
-        head_.set_precision_profile(detail::ternary_part(p_));
+        // the LM head computes in the stable precision (f32 logits under t1_58), as the
+        // reference's head profile does (compute_layer_gpt.hpp:335-337)
+        PrecisionProfile hp = detail::ternary_part(p_);
+        hp.compute = p_.stable;
+        head_.set_precision_profile(hp);
         EX_TRY_CHECK(head_.init(engine));
         return {};
     }

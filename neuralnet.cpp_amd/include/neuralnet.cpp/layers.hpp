@@ -577,8 +577,11 @@ private:
         if (input.rows() != d_model_) return Error{"feedforward forward: input shape mismatch"};
         ComputeEngine& engine = engine_ref();
         const int act = activation_ == ActivationType::ReLU2 ? 1 : 0;
-        // the fused block takes an RMSNorm SubLN; a LayerNorm SubLN runs the chain below
-        if (fc1_.activation_quant() && fc2_.activation_quant() && sub_ln_ == nullptr)
+        // compute = F16: the projections and the gated activation give f16 (the reference's
+        // compute precision), the SubLN f32 (stable); the chain below rounds where they do
+        const Precision P = p_.compute == Precision::F16 ? Precision::F16 : Precision::F32;
+        // the fused block takes an RMSNorm SubLN in f32; a LayerNorm SubLN runs the chain below
+        if (fc1_.activation_quant() && fc2_.activation_quant() && sub_ln_ == nullptr && P == Precision::F32)
         {
             EX_TRY_CHECK(fc1_.ensure_quantized());
             EX_TRY_CHECK(fc2_.ensure_quantized());
@@ -591,14 +594,18 @@ private:
         Tensor in = input;
         if (norm)
         {
-            EX_TRY(n, norm->forward(input));
+            EX_TRY(iw, engine.cast(input, Precision::F32));
+            EX_TRY(n, norm->forward(*iw));
             in = *n;
         }
         EX_TRY(h1, fc1_.forward(in));
-        EX_TRY(h2, engine.glu(*h1, act));
+        EX_TRY(h1w, engine.cast(*h1, Precision::F32));
+        EX_TRY(g32, engine.glu(*h1w, act));
+        EX_TRY(h2, engine.cast(*g32, P));
         if (sub_norm_)
         {
-            EX_TRY(h3, sub_norm_->forward(*h2));
+            EX_TRY(h2w, engine.cast(*h2, Precision::F32));
+            EX_TRY(h3, sub_norm_->forward(*h2w));
             return fc2_.forward(*h3);
         }
         return fc2_.forward(*h2);

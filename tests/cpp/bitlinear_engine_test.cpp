@@ -1281,25 +1281,15 @@ void test_decoder(nn::ComputeEngine& e)
         }
         CHECK(ok, "GPTBlock::forward_step == norm1 -> attention -> add -> norm2 -> FeedForward -> add, bit for bit");
     }
-    // compute = F16 (the t1_58 preset) is refused at init: the decoder's activations are f32
-    {
-        nn::GPTModel g16(97, d, 32, H, F, 1, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
-        g16.set_precision_profile(nn::profile_t1_58());
-        auto r = g16.init(e);
-        CHECK(!r.has_value() && r.error().message.find("compute precision") != std::string::npos,
-              "GPTModel refuses compute = F16 at init with a clear error");
-    }
-    // GPTModel: greedy generation == forward_step + the reference greedy loop on the host
-    {
-        const std::size_t V = 97;
-        nn::GPTModel gm(V, d, 32, H, F, 2, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
-        CHECK(gm.init(e).has_value(), "GPTModel (2 blocks, vocab 97) initialized");
-        gm.set_activation_quant(true);
-        const std::vector<std::vector<std::int32_t>> prompts = {{5, 9, 2}, {1}, {40, 41, 42, 43, 44}};
+    // GPTModel: greedy generation == forward_step + the reference greedy loop on the host, under
+    // the default f32 profile and under compute = F16 (the t1_58 preset)
+    const std::size_t V = 97;
+    const std::vector<std::vector<std::int32_t>> prompts = {{5, 9, 2}, {1}, {40, 41, 42, 43, 44}};
+    auto greedy_checks = [&](nn::GPTModel& gm, const char* tag) {
         auto gen = gm.generate_greedy(e, prompts, 6);
         auto gen2 = gm.generate_greedy(e, prompts, 6);
         CHECK(gen.has_value() && gen2.has_value() && *gen == *gen2 && (*gen)[0].size() == 6 && (*gen)[1].size() == 6,
-              "generate_greedy: 6 tokens per sequence, deterministic");
+              (std::string(tag) + "generate_greedy: 6 tokens per sequence, deterministic").c_str());
         // manual lockstep loop with host-side greedy choice
         bool same = gen.has_value();
         auto caches = gm.make_caches(prompts.size());
@@ -1333,9 +1323,87 @@ void test_decoder(nn::ComputeEngine& e)
                 cur[b] = static_cast<std::int32_t>(next);
             }
         }
-        CHECK(same && manual == *gen, "generate_greedy == forward_step + the reference greedy loop on downloaded logits");
-        auto too_long = gm.generate_greedy(e, prompts, 40);
-        CHECK(!too_long.has_value(), "prompt + new tokens beyond max_len is refused");
+        CHECK(same && manual == *gen,
+              (std::string(tag) + "generate_greedy == forward_step + the reference greedy loop on downloaded logits").c_str());
+    };
+    nn::GPTModel gm(V, d, 32, H, F, 2, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
+    CHECK(gm.init(e).has_value(), "GPTModel (2 blocks, vocab 97) initialized");
+    gm.set_activation_quant(true);
+    greedy_checks(gm, "");
+    auto too_long = gm.generate_greedy(e, prompts, 40);
+    CHECK(!too_long.has_value(), "prompt + new tokens beyond max_len is refused");
+
+    // compute = F16: the same weights (every layer initializes from fixed seeds), f16 activations
+    // between the layers, f16 caches, f32 logits (the head computes in the stable precision)
+    nn::GPTModel g16(V, d, 32, H, F, 2, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
+    g16.set_precision_profile(nn::profile_t1_58());
+    CHECK(g16.init(e).has_value(), "GPTModel under compute = F16 (profile_t1_58) initialized");
+    g16.set_activation_quant(true);
+    {
+        auto c16 = g16.make_caches(prompts.size());
+        CHECK(c16.has_value() && (*c16)[0].k.precision() == nn::Precision::F16 &&
+                  (*c16)[1].v.precision() == nn::Precision::F16,
+              "compute = F16: the KV caches are f16 (compute_layer_gpt.hpp:764-765)");
+    }
+    greedy_checks(g16, "compute = F16: ");
+    // one step of both models on the same tokens: f32 logits, within a few percent of the f32 model's
+    {
+        auto ca = gm.make_caches(3), cb = g16.make_caches(3);
+        const std::int32_t idv[3] = {5, 1, 40}, pz[3] = {0, 0, 0};
+        auto ids = nn::upload_indices(e, idv, 3);
+        auto pt = nn::upload_indices(e, pz, 3);
+        auto la = gm.forward_step(e, *ids, *pt, 1, *ca);
+        auto lb = g16.forward_step(e, *ids, *pt, 1, *cb);
+        bool ok = la.has_value() && lb.has_value() && lb->precision() == nn::Precision::F32;
+        double mx = 0, dm = 0;
+        if (ok)
+        {
+            const nn::Matrix A = download(e, *la), Bm = download(e, *lb);
+            for (std::size_t i = 0; i < A.size(); ++i)
+            {
+                mx = std::max(mx, (double)std::abs(A.span()[i]));
+                dm = std::max(dm, (double)std::abs(A.span()[i] - Bm.span()[i]));
+            }
+        }
+        CHECK(ok && mx > 0 && dm <= 0.05 * mx && dm > 0,
+              "compute = F16 logits within 5 % (of the largest) of the f32 model's, and not identical");
+    }
+    // GPTBlock::forward_step under compute = F16 == its composition with the f16 roundings
+    {
+        nn::GPTBlock blk(d, H, F, max_len, Hkv, nn::ActivationType::SwiGLU, true, 1e-5f);
+        blk.set_precision_profile(nn::profile_t1_58());
+        CHECK(blk.init(e).has_value(), "GPTBlock under compute = F16 initialized");
+        blk.set_activation_quant(true);
+        auto c1 = blk.attention().make_cache(B);
+        auto c2 = blk.attention().make_cache(B);
+        bool ok = c1.has_value() && c2.has_value();
+        if (ok)
+        {
+            (void)e.copy_from(c1->k, kc0);
+            (void)e.copy_from(c1->v, vc0);
+            (void)e.copy_from(c2->k, kc0);
+            (void)e.copy_from(c2->v, vc0);
+            auto x16 = e.cast(xt, nn::Precision::F16);  // the residual stream between blocks is f16
+            auto yb = x16 ? blk.forward_step(e, *x16, *c1, *pos, 64) : nn::Result<nn::Tensor>(nn::Error{"x16"});
+            const auto F32 = nn::Precision::F32, F16 = nn::Precision::F16;
+            auto xw = e.cast(*x16, F32);
+            auto n1 = blk.norm1().forward(*xw);
+            auto a = n1 ? blk.attention().forward_step(e, *n1, *c2, *pos, 64) : nn::Result<nn::Tensor>(nn::Error{"n1"});
+            auto aw = a ? e.cast(*a, F32) : nn::Result<nn::Tensor>(nn::Error{"a"});
+            auto s1 = aw ? e.add(*xw, *aw) : nn::Result<nn::Tensor>(nn::Error{"aw"});
+            auto r2 = s1 ? e.cast(*s1, F16) : nn::Result<nn::Tensor>(nn::Error{"s1"});
+            auto r2w = r2 ? e.cast(*r2, F32) : nn::Result<nn::Tensor>(nn::Error{"r2"});
+            auto n2 = r2w ? blk.norm2().forward(*r2w) : nn::Result<nn::Tensor>(nn::Error{"r2w"});
+            auto f = n2 ? blk.feed_forward().forward(*n2) : nn::Result<nn::Tensor>(nn::Error{"n2"});
+            auto fw = f ? e.cast(*f, F32) : nn::Result<nn::Tensor>(nn::Error{"f"});
+            auto s2 = fw ? e.add(*r2w, *fw) : nn::Result<nn::Tensor>(nn::Error{"fw"});
+            auto out = s2 ? e.cast(*s2, F16) : nn::Result<nn::Tensor>(nn::Error{"s2"});
+            ok = yb.has_value() && out.has_value() && yb->precision() == F16 && a.has_value() && a->precision() == F16 &&
+                 f.has_value() && f->precision() == F16 && bitwise_equal(download(e, *yb), download(e, *out)) &&
+                 bitwise_equal(download(e, c1->k), download(e, c2->k)) && c1->k.precision() == F16;
+        }
+        CHECK(ok, "compute = F16: GPTBlock::forward_step == norm1 -> attention (f16 out) -> f32 add rounded to f16 -> "
+                  "norm2 -> FeedForward (f16 out) -> f32 add rounded to f16, bit for bit");
     }
 }
 // ---------------------------------------------------------------- [15]
