@@ -265,16 +265,29 @@ __global__ __launch_bounds__(512) void k_attn_prefill(PrefillArgs a)
         }
         // the next tile's loads overlap this tile's softmax and products
         if (kb + 1 < nkb) stage_tile(kb + 1, smem + ((kb + 1) & 1) * TILE);
-        // online softmax over this tile's keys (element v: key 32kb + 8(v/4) + 4h + v%4)
+        // online softmax over this tile's keys (element v: key 32kb + 8(v/4) + 4h + v%4); the
+        // causal mask only where the tile reaches past the wave's first query
         float sc[16];
         float mx = -__builtin_inff();
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
+        if (kb * kPK + kPK - 1 <= a.pos0 + t0)
         {
-            const int key = kb * kPK + 8 * (v >> 2) + 4 * h + (v & 3);
-            const float x = s[v] * a.scale;
-            sc[v] = key <= qpos ? x : -__builtin_inff();
-            mx = fmaxf(mx, sc[v]);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+            {
+                sc[v] = s[v] * a.scale;
+                mx = fmaxf(mx, sc[v]);
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+            {
+                const int key = kb * kPK + 8 * (v >> 2) + 4 * h + (v & 3);
+                const float x = s[v] * a.scale;
+                sc[v] = key <= qpos ? x : -__builtin_inff();
+                mx = fmaxf(mx, sc[v]);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
@@ -290,10 +303,15 @@ __global__ __launch_bounds__(512) void k_attn_prefill(PrefillArgs a)
         ls += __shfl_xor(ls, 32);
         l_run = l_run * corr + ls;
         m_run = m_new;
+        // corr is exactly 1 where the running maximum did not move: skip the rescale when that
+        // holds for every lane (multiplying by 1 would change no bit)
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0)
+        {
 #pragma unroll
-        for (int d = 0; d < ND; ++d)
+            for (int d = 0; d < ND; ++d)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[d][v] *= corr;
+                for (int v = 0; v < 16; ++v) o[d][v] *= corr;
+        }
         // O^T += V^T . P^T: product s takes key 8(s/4) + 4h + s%4 (the lane's score element s)
 #pragma unroll
         for (int d = 0; d < ND; ++d)
