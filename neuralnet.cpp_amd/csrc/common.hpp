@@ -277,6 +277,16 @@ int gemm_tile_choice(const GemvProblem& p, int num_cus);
 // measured over M = 128..4096, K = 2560..6912, N = 2560..13824 (with these the automatic choice
 // picked the fastest tile on every measured shape).
 constexpr double kGemmRelB = 0.6, kGemmRelC = 0.45;
+// The automatic choice may split the rows: 256 x 128 blocks over the longest row prefix that
+// fills whole rounds of the CUs, then the remaining rows in a second launch (tail_tile), when the
+// estimate (rounds, plus kGemmSplitCost of a 256 x 128 round for the second launch) is lower
+// than every single-launch tile's. rows = 0: one launch of tile.
+struct GemmSplit
+{
+    int tile, rows, tail_tile;
+};
+constexpr double kGemmSplitCost = 0.1;
+GemmSplit gemm_split_choice(const GemvProblem& p, int num_cus);
 
 // ---- gated activations (k_glu.hip)
 hipError_t launch_glu(hipStream_t st, const float* Y1, size_t F, size_t M, int act, bool interleaved, float* h);

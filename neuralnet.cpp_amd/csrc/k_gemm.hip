@@ -768,10 +768,74 @@ int gemm_tile_choice(const GemvProblem& p, int num_cus)
     return b <= c ? NNHIP_GEMM_TILE_128x128 : NNHIP_GEMM_TILE_64x64;
 }
 
+namespace
+{
+
+// The rows [rows0, N) of p as a problem of their own: the weight row tiles, the per-row scales,
+// bias and residual, and the output rows move; the per-token inputs (codes, scales, row sums, the
+// absmax slots) are shared. rows0 is a multiple of 256 (16 row tiles; 128 gated features).
+GemvProblem gemm_rows_from(const GemvProblem& p, int rows0)
+{
+    GemvProblem q = p;
+    const size_t rt0 = (size_t)rows0 / 16;
+    q.rp = p.rp + rt0 * (size_t)p.KT * 64;  // 1024 bytes = 64 x 16 per (row tile, k tile)
+    q.tau = p.tau + rows0;
+    if (p.bias) q.bias = p.bias + rows0;
+    q.N = p.N - rows0;
+    if (p.glu)
+    {
+        q.glu_F = p.glu_F - rows0 / 2;
+        q.y = p.y + (size_t)(rows0 / 2) * (size_t)p.M;
+    }
+    else
+    {
+        q.y = p.y + (size_t)rows0 * (size_t)p.M;
+        if (p.res) q.res = p.res + (size_t)rows0 * (size_t)p.M;
+    }
+    return q;
+}
+
+}  // namespace
+
+GemmSplit gemm_split_choice(const GemvProblem& p, int num_cus)
+{
+    GemmSplit s{gemm_tile_choice(p, num_cus), 0, 0};
+    const int cus = num_cus > 0 ? num_cus : 256;
+    const int n_mb = (int)ceil_div((size_t)p.M, (size_t)GemmA::kBM);
+    const int n_nb = (int)ceil_div((size_t)p.N, (size_t)GemmA::kBN);
+    // the longest row-block prefix whose 256 x 128 blocks fill whole rounds of the CUs
+    int r1 = n_nb - 1;
+    while (r1 > 0 && ((long)r1 * n_mb) % cus != 0) --r1;
+    if (r1 <= 0) return s;
+    const double best = s.tile == NNHIP_GEMM_TILE_256x128   ? gemm_cost(p, cus, GemmA::kBN, GemmA::kBM, 1.0)
+                        : s.tile == NNHIP_GEMM_TILE_128x128 ? gemm_cost(p, cus, GemmB::kBN, GemmB::kBM, kGemmRelB)
+                                                            : gemm_cost(p, cus, GemmC::kBN, GemmC::kBM, kGemmRelC);
+    const GemvProblem tail = gemm_rows_from(p, r1 * GemmA::kBN);
+    const double tb = gemm_cost(tail, cus, GemmB::kBN, GemmB::kBM, kGemmRelB);
+    const double tc = gemm_cost(tail, cus, GemmC::kBN, GemmC::kBM, kGemmRelC);
+    const double split = (double)((long)r1 * n_mb / cus) + (tb <= tc ? tb : tc) + kGemmSplitCost;
+    if (split < best) s = GemmSplit{NNHIP_GEMM_TILE_256x128, r1 * GemmA::kBN,
+                                    tb <= tc ? NNHIP_GEMM_TILE_128x128 : NNHIP_GEMM_TILE_64x64};
+    return s;
+}
+
 hipError_t launch_gemm(hipStream_t st, const GemvProblem& p, int num_cus, int tile)
 {
     if (p.N == 0 || p.M == 0) return hipSuccess;
-    if (tile == NNHIP_GEMM_TILE_AUTO) tile = gemm_tile_choice(p, num_cus);
+    if (tile == NNHIP_GEMM_TILE_AUTO)
+    {
+        const GemmSplit s = gemm_split_choice(p, num_cus);
+        if (s.rows > 0)
+        {
+            GemvProblem head = p;
+            head.N = s.rows;
+            if (p.glu) head.glu_F = s.rows / 2;
+            const hipError_t e = launch_cfg<GemmA>(st, head);
+            if (e != hipSuccess) return e;
+            return launch_gemm(st, gemm_rows_from(p, s.rows), num_cus, s.tail_tile);
+        }
+        tile = s.tile;
+    }
     if (tile == NNHIP_GEMM_TILE_128x128) return launch_cfg<GemmB>(st, p);
     if (tile == NNHIP_GEMM_TILE_64x64) return launch_cfg<GemmC>(st, p);
     return launch_cfg<GemmA>(st, p);

@@ -223,6 +223,31 @@ def test_ffn_block_each_tile(ctx, orc, tile):
     assert same_bits(Y, Y_ref)
 
 
+def test_ffn_block_split_rows(ctx, orc):
+    """fc1 of 2F = 4608 interleaved rows at 2048 tokens: on a 256-CU device the automatic tile
+    choice runs 256 x 128 blocks over the first 4096 rows (features 0..2047) and 128 x 128 blocks
+    over the rest, the per-token absmax of h folded by both launches. The block against the
+    oracle on every token, h the same bits as under the 256 x 128 tile alone."""
+    d, F, M = 256, 2304, 2048
+    say(f"ffn_glu_i8 split rows d={d} F={F} M={M}")
+    wq1, t1, b1, wq2, t2, b2 = block_case(orc, d, F, 960)
+    X = normal((d, M), 961, 0.0, 1.0)
+    gamma = normal((d,), 962, 1.0, 0.1)
+    Y_ref, _ = orc.ffn_glu_i8(X, gamma, 1e-6, F, wq1, t1, b1, wq2, t2, b2, 0)
+    rp1, to, bo = prepare_fc1(ctx, wq1, t1, b1, F, d)
+    rp2 = ctx.repack(dev(wq2), F)
+    Y = host(ctx.ffn_glu_i8(dev(X), dev(gamma), 1e-6, F, rp1, to, bo, rp2, dev(t2), dev(b2), 0))
+    assert same_bits(Y, Y_ref)
+    xi, s, rs = ctx.act_quant_i8(dev(X))
+    h = host(ctx.ternary_matmul_glu(rp1, to, xi, s, rs, F, d, M, bias=bo))
+    ctx.set_gemm_tile(1)
+    try:
+        h1 = host(ctx.ternary_matmul_glu(rp1, to, xi, s, rs, F, d, M, bias=bo))
+    finally:
+        ctx.set_gemm_tile(0)
+    assert same_bits(h, h1)
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 300])
 @pytest.mark.parametrize("act", [0, 1])
 def test_ffn_block_subln(ctx, orc, M, act):

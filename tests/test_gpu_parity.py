@@ -483,6 +483,31 @@ def test_prefill_gemm_each_tile(ctx, orc, tile, N, K, M):
     assert np.array_equal(Y[rows], ref)
 
 
+@pytest.mark.parametrize("N,K,M", [(4608, 768, 2048), (11008, 1024, 1024), (2560, 520, 4096)])
+def test_prefill_gemm_split_rows(ctx, orc, N, K, M):
+    """Shapes on which the automatic tile choice splits the rows on a 256-CU device: 256 x 128
+    blocks over the rows that fill whole rounds (4096, 8192 and 2048 rows here), the rest in a
+    second launch of 128 x 128 blocks. Every row against the oracle, with a bias; the same bits
+    as the 256 x 128 tile over all rows; and the residual epilogue (the rows' residual moves
+    with them) the same bits as add(res, ternary_matmul)."""
+    say(f"gemm split N={N} K={K} M={M}")
+    tau, s, wq, xq, rp, xi, s_d, rs = fast_case(ctx, orc, N, K, M, 23 + N + M, outliers=True)
+    b = normal((N,), 99)
+    Y = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M, bias=dev(b)))
+    ref = orc.add_row_broadcast(orc.matmul_q_i8_rowblock(wq, tau, xq, s, K, M), b)
+    assert np.array_equal(Y, ref)
+    ctx.set_gemm_tile(1)
+    try:
+        Y1 = host(ctx.ternary_matmul(rp, dev(tau), xi, s_d, rs, N, K, M, bias=dev(b)))
+    finally:
+        ctx.set_gemm_tile(0)
+    assert np.array_equal(Y1.view(np.uint32), Y.view(np.uint32))
+    res = normal((N, M), 100)
+    Yr = host(ctx.ternary_matmul_add(rp, dev(tau), xi, s_d, rs, N, K, M, dev(res), bias=dev(b)))
+    Yr_ref = host(ctx.add(dev(res), dev(Y)))
+    assert np.array_equal(Yr.view(np.uint32), Yr_ref.view(np.uint32))
+
+
 def test_gemm_tile_setter_rejects(ctx, nnhip):
     with pytest.raises(nnhip.NNHipError):
         ctx.set_gemm_tile(4)
