@@ -252,9 +252,11 @@ def check_quant(ctx, orc, X, g=None, eps=1e-6):
 
 
 # M > 64 runs the register-resident kernel (rounds of 512 rows; 8 tokens per 16-wave block when
-# M % 4 == 0, M <= 8192 and K <= 5120, 4 tokens per 8-wave block otherwise; M % 4 != 0 takes the
-# scalar-load path), M <= 64 the one-token kernel; K = 11264 is the largest instantiation of
-# both, K = 11265 the fallback. M = 2052 and 1028 leave a half-empty last group of 8 tokens.
+# M % 4 == 0, M <= 8192 and K <= 5120, or K <= 7168 without RMSNorm, where each wave reads one
+# contiguous band of rows; 4 tokens per 8-wave block otherwise; M % 4 != 0 takes the scalar-load
+# path), M <= 64 the one-token kernel; K = 11264 is the largest instantiation of both, K = 11265
+# the fallback. M = 2052 and 1028 leave a half-empty last group of 8 tokens; K = 5121 and 6912
+# end inside a band.
 @pytest.mark.parametrize("K,M", [(1, 36), (255, 37), (512, 40), (513, 128), (1000, 66), (2560, 2048),
                                  (4096, 2048), (2560, 2052), (5120, 1028), (5121, 1024), (512, 8196),
                                  (6912, 132), (11264, 40), (11265, 36)])
