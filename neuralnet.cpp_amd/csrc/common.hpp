@@ -96,7 +96,6 @@ struct GemvProblem
                           // (0 SwiGLU, 1 ReLU^2-GLU) of interleaved gate/up rows into y (glu_F, M)
     int32_t glu_F;        // features of the gated output (rows of y when glu != 0)
     int32_t ytm;          // deep decode GEMV with glu: h token-major (M, glu_F) instead of (glu_F, M)
-    uint32_t* amax;       // prefill GEMM with glu: per-token max |h| (float bits, atomic max), or null
     const float* res;     // deep decode GEMV: residual (N, M) added after the epilogue (may alias y), or null
 };
 
@@ -155,10 +154,6 @@ constexpr uint32_t kGemvLdsBigBudget = 152 * 1024;
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* dst, uint32_t value, size_t words);
 hipError_t launch_f32_to_f16(hipStream_t st, const float* src, size_t n, uint16_t* dst);
 hipError_t launch_f16_to_f32(hipStream_t st, const uint16_t* src, size_t n, float* dst);
-// Quantize X (K, M) f32 with a known per-token absmax (float bits in amax[M], as the gated GEMM
-// epilogue leaves them) into token-major xi (M, Kp) + s + rowsum; resets amax to 0.
-hipError_t launch_quant_amax(hipStream_t st, const float* X, size_t K, size_t M, uint32_t* amax, int8_t* xi,
-                             float* s, int32_t* rowsum);
 hipError_t launch_row_absmean(hipStream_t st, const float* W, size_t N, size_t K, float* tau);
 hipError_t launch_trit_pack(hipStream_t st, const float* W, const float* tau, size_t N, size_t K,
                             uint32_t* wq);

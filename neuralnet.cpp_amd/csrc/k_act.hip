@@ -847,112 +847,6 @@ __global__ __launch_bounds__(kBlock) void k_to_container(const int8_t* __restric
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// Quantization with a known per-token absmax (amax: float bits, left by the gated GEMM
-// epilogue): no reduction pass, so X is streamed once. 8 tokens per block (32-byte row
-// segments, two lanes per row), 512 threads, 256 rows per chunk, kQuantU chunks of loads in
-// flight per thread (a load is issued as soon as its registers are free). Lane l holds row
-// 4*(l/8) + l%4 of its wave's 32, tokens 4*((l/4)%2) .. +3; a byte transpose inside each lane
-// quad turns the four codes of one row into four rows of one token, stored as one dword of the
-// token-major xi. Blocks are XCD-aware (the 4 blocks sharing a 128-byte row line meet in one
-// L2). s = fl(absmax * fl(1/127)) and the codes are those of the absmax kernels above; amax is
-// reset to 0 for the next producer.
-constexpr int kQuantTok = 8, kQuantThreads = 512, kQuantChunk = 256, kQuantU = 8;
-
-template <bool kVec>
-__global__ __launch_bounds__(kQuantThreads) void k_quant_amax(const float* __restrict__ X, int K, int M, int Kp,
-                                                              uint32_t* __restrict__ amax, int8_t* __restrict__ xi,
-                                                              float* __restrict__ s_out, int32_t* __restrict__ rowsum,
-                                                              int n_groups)
-{
-    __shared__ int wsum[kQuantThreads / kWave][kQuantTok];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int b = blockIdx.x;
-    const int g = n_groups % 8 == 0 ? (b & 7) * (n_groups >> 3) + (b >> 3) : b;
-    const int m0 = g * kQuantTok;
-    const int j = lane & 3, hq = (lane >> 2) & 1, rq = lane >> 3;
-    const int row = w * 32 + rq * 4 + j;  // row within a chunk
-    const int mq = m0 + 4 * hq;           // first of the lane's four tokens
-
-    // per token: s, fl(1/s) for the fast codes, and the exact path's prescale xs (2^100 below
-    // s = 2^-100, else 1), s * xs and its reciprocal
-    float sc[4], rc[4], xs[4], se[4], re[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-    {
-        const float mx = mq + i < M ? __builtin_bit_cast(float, amax[mq + i]) : 0.0f;
-        sc[i] = __fmul_rn(mx, 1.0f / 127.0f);
-        rc[i] = quant_rcp(sc[i]);
-        xs[i] = sc[i] < 0x1p-100f ? 0x1p100f : 1.0f;
-        se[i] = __fmul_rn(sc[i], xs[i]);
-        re[i] = quant_rcp(se[i]);
-    }
-    const bool rc_inf = isinf(rc[0]) || isinf(rc[1]) || isinf(rc[2]) || isinf(rc[3]);
-
-    const __amdgpu_buffer_rsrc_t rx =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X), (short)0, kVec ? K * M * 4 : 0, 0x00020000);
-    const uint32_t moff = mq < M ? (uint32_t)mq * 4u : 0x80000000u;
-    const int n_chunks = Kp / kQuantChunk;
-    auto load = [&](float (&x)[4], int c) {
-        const int f = c * kQuantChunk + row;  // rows past K read 0 (past the buffer)
-        if (kVec)
-        {
-            typedef float v4f __attribute__((ext_vector_type(4)));
-            const v4f v = __builtin_bit_cast(
-                v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, moff + (uint32_t)f * (uint32_t)M * 4u, 0, 0));
-            x[0] = v[0];
-            x[1] = v[1];
-            x[2] = v[2];
-            x[3] = v[3];
-        }
-        else
-        {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = (f < K && mq + i < M) ? X[(size_t)f * M + mq + i] : 0.0f;
-        }
-    };
-
-    float x[kQuantU][4];
-#pragma unroll
-    for (int u = 0; u < kQuantU; ++u)
-        if (u < n_chunks) load(x[u], u);
-    int tsum = 0;
-    int8_t* dst = mq + j < M ? xi + (size_t)(mq + j) * Kp + w * 32 + rq * 4 : nullptr;
-    for (int c0 = 0; c0 < n_chunks; c0 += kQuantU)
-    {
-#pragma unroll
-        for (int u = 0; u < kQuantU; ++u)
-        {
-            const int c = c0 + u;
-            if (c >= n_chunks) break;
-            bool amb = rc_inf;
-            int q[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) q[i] = quantize_guess(x[u][i], rc[i], amb);
-            if (amb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) q[i] = quantize_exact(__fmul_rn(x[u][i], xs[i]), se[i], re[i]);
-            if (c + kQuantU < n_chunks) load(x[u], c + kQuantU);
-            const uint32_t col = quad_transpose(pack4(q[0], q[1], q[2], q[3]), j);
-            tsum = __builtin_amdgcn_sdot4((int)col, 0x01010101, tsum, false);
-            if (dst) *reinterpret_cast<uint32_t*>(dst + (size_t)c * kQuantChunk) = col;
-        }
-    }
-    // rowsum: lanes with the same token differ in lane bits 3..5 (row quads), then the waves
-    tsum = bfly_isum1<32, 8>(tsum);
-    if (rq == 0) wsum[w][4 * hq + j] = tsum;
-    __syncthreads();  // also: every thread has read its scales before the reset below
-    if (t < kQuantTok && m0 + t < M)
-    {
-        int sum = 0;
-#pragma unroll
-        for (int v = 0; v < kQuantThreads / kWave; ++v) sum += wsum[v][t];
-        rowsum[m0 + t] = sum;
-        s_out[m0 + t] = __fmul_rn(__builtin_bit_cast(float, amax[m0 + t]), 1.0f / 127.0f);
-        amax[m0 + t] = 0u;
-    }
-}
-
 #ifndef NNHIP_TOK8_MAX_ROUNDS
 #define NNHIP_TOK8_MAX_ROUNDS 10  // largest K/512 rounds for the 8-token register kernel
 #endif
@@ -1118,23 +1012,6 @@ hipError_t launch_epilogue_quant(hipStream_t st, const EpiArgs& e, const float* 
     const int rounds = (int)ceil_div(N, (size_t)kParts);
     if (!launch_epi_pick<1, 2, 3, 4, 5, 6, 8, 10, 12, 14, 16, 18, 20, 22>(rounds, st, a, e, gamma))
         return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-hipError_t launch_quant_amax(hipStream_t st, const float* X, size_t K, size_t M, uint32_t* amax, int8_t* xi,
-                             float* s, int32_t* rowsum)
-{
-    if (M == 0) return hipSuccess;
-    const size_t Kp = round_up(K, kTileK);
-    const int n_groups = (int)ceil_div(M, (size_t)kQuantTok);
-    // vector loads need 16-byte aligned rows and offsets that stay below 2^31 (rows up to Kp)
-    const bool vec = M % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0 && (K + kQuantChunk) * M * 4 < 0x7FFFFFFFull;
-    if (vec)
-        hipLaunchKernelGGL(k_quant_amax<true>, dim3((unsigned)n_groups), dim3(kQuantThreads), 0, st, X, (int)K, (int)M,
-                           (int)Kp, amax, xi, s, rowsum, n_groups);
-    else
-        hipLaunchKernelGGL(k_quant_amax<false>, dim3((unsigned)n_groups), dim3(kQuantThreads), 0, st, X, (int)K, (int)M,
-                           (int)Kp, amax, xi, s, rowsum, n_groups);
     return hipGetLastError();
 }
 

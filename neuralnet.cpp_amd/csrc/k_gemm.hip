@@ -151,8 +151,7 @@ struct Gemm
     static constexpr int kRingBytes = kSlots * kSlotBytes;
     static constexpr int kLdsMain = kKSplit == 2 && kWaves * kPartBytes > kRingBytes ? kWaves * kPartBytes : kRingBytes;
     // gated epilogue: per-token max |h| of each (wn, ks) wave row, reduced across the block
-    static constexpr int kAmaxRows = kWavesN * kKSplit;
-    static constexpr int kLdsBytes = kLdsMain + kAmaxRows * kBM * 4;
+    static constexpr int kLdsBytes = kLdsMain;
     // DMA instructions per wave per stage: A one row tile (1 KiB) each, B four token rows each
     // Waves 0 .. kDmaWaves-1 issue the DMA (with the default k split, the first wave of each pair:
     // the older wave of its SIMD, which the issue arbiter favours and which reaches the stage
@@ -472,19 +471,12 @@ struct Gemm
     // i (row 8*(i/4) + 4h + i%4 of the 32-row block) and element i + 4 (8 rows below) are gate and
     // up of one feature when i/4 is even. Each is rescaled exactly as the plain epilogue does
     // ((tau * s) * float(acc) [+ bias]), then combined by glu_one; h (glu_F, M) gets the result.
-    // With p.amax, the block also folds max |h| per token (NaN ignored, as `a > m ? a : m` from 0
-    // does) into p.amax (float bits; non-negative floats order as unsigned integers) with one
-    // atomic max per token: the absmax of the next activation quantization, order-independent.
     template <int kHPolicy>
     static __device__ __forceinline__ void store_glu(const GemvProblem& p, const v16i (&acc)[kRB][kTB], const EpiOps& e, int rb0,
-                                              int nrb, int row_w, int tok_w, int h, int l32, uint8_t* lds, int amax_row,
-                                              int tok_local, int m0)
+                                              int nrb, int row_w, int tok_w, int h, int l32)
     {
         const __amdgpu_buffer_rsrc_t ry = rsrc(p.y, (uint32_t)p.glu_F * (uint32_t)p.M * 4u);
         const int act = p.glu - 1;
-        float mx[kTB];
-#pragma unroll
-        for (int n = 0; n < kTB; ++n) mx[n] = 0.0f;
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
         {
@@ -512,30 +504,8 @@ struct Gemm
                     const bool in = f < p.glu_F && m < p.M;
                     const uint32_t off = in ? ((uint32_t)f * (uint32_t)p.M + (uint32_t)m) * 4u : 0xFFFFFFF0u;
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ry, off, 0, kHPolicy);
-                    const float a = fabsf(y);
-                    if (in && a > mx[n]) mx[n] = a;
                 }
             }
-        }
-        if (!p.amax) return;
-        // lanes l and l ^ 32 hold the same tokens (other rows); then one row of LDS per wave
-        float* red = reinterpret_cast<float*>(lds + kLdsMain);
-#pragma unroll
-        for (int n = 0; n < kTB; ++n)
-        {
-            mx[n] = fmaxf(mx[n], __shfl_xor(mx[n], 32));
-            if (h == 0) red[amax_row * kBM + tok_local + n * 32 + l32] = mx[n];
-        }
-        wait_lgkm0();   // this wave's LDS writes are done; the h stores stay in flight
-        lds_barrier();
-        const int t = threadIdx.x;
-        if (t < kBM && m0 + t < p.M)
-        {
-            float v = red[t];
-#pragma unroll
-            for (int w = 1; w < kAmaxRows; ++w) v = fmaxf(v, red[w * kBM + t]);
-            __hip_atomic_fetch_max(p.amax + m0 + t, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 
@@ -703,12 +673,8 @@ struct Gemm
         if (p.glu)
         {
             // one uniform branch over the whole epilogue (the store policy is an immediate)
-            if (h_keep)
-                store_glu<kPolicySys>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32, lds, wn * kKSplit + ks,
-                                      wm * kWaveToks, m0);
-            else
-                store_glu<kGemmYPolicy>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32, lds, wn * kKSplit + ks,
-                                        wm * kWaveToks, m0);
+            if (h_keep) store_glu<kPolicySys>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
+            else store_glu<kGemmYPolicy>(p, acc, e, rb0, nrb, row_w, tok_w, h, l32);
         }
         else if (full)
         {

@@ -34,8 +34,6 @@ struct nnhip_ctx
     size_t ws_bytes = 0;
     // per-token absmax between the gated GEMM epilogue and the next quantization of the fused
     // FFN block: zero between calls (zero-filled when allocated, reset by its consumer)
-    uint32_t* amax = nullptr;
-    size_t amax_words = 0;
     int gemm_tile = NNHIP_GEMM_TILE_AUTO;
     void* attn_ws = nullptr;  // per-chunk partial results of the decode attention
     size_t attn_ws_bytes = 0;
@@ -174,31 +172,6 @@ nnhip_status ensure_ws(nnhip_ctx* ctx, size_t bytes, const char* fn)
     return ensure_buf(ctx, ctx->ws, ctx->ws_bytes, bytes, fn, "workspace");
 }
 
-nnhip_status ensure_amax(nnhip_ctx* ctx, size_t words, const char* fn)
-{
-    if (ctx->amax_words >= words) return NNHIP_OK;
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return hip_fail(fn, "hipStreamSynchronize", e);
-    if (ctx->amax)
-    {
-        e = hipFree(ctx->amax);
-        ctx->amax = nullptr;
-        ctx->amax_words = 0;
-        if (e != hipSuccess) return hip_fail(fn, "hipFree", e);
-    }
-    e = hipMalloc(reinterpret_cast<void**>(&ctx->amax), words * 4);
-    if (e != hipSuccess)
-    {
-        ctx->amax = nullptr;
-        (void)hipGetLastError();
-        return fail(NNHIP_ERR_OOM, fn, "absmax buffer allocation of " + std::to_string(words * 4) + " bytes failed");
-    }
-    e = launch_fill_u32(ctx->stream, ctx->amax, 0u, words);
-    if (e != hipSuccess) return hip_fail(fn, "launch_fill_u32", e);
-    ctx->amax_words = words;
-    return NNHIP_OK;
-}
-
 nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
 {
     NNHIP_REQUIRE(N <= kMaxDim && M <= kMaxDim, fn, "N and M must be below 2^31");
@@ -216,7 +189,7 @@ nnhip_status check_matmul_shape(const char* fn, size_t N, size_t K, size_t M)
 nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const float* tau,
                         const int8_t* xi, const float* s, const int32_t* rowsum, const float* bias,
                         size_t N, size_t K, size_t M, float* Y, int glu = 0, size_t glu_F = 0,
-                        uint32_t* amax = nullptr, const float* res = nullptr)
+                        const float* res = nullptr)
 {
     GemvProblem p{};
     p.rp = static_cast<const u32x4*>(rp);
@@ -233,7 +206,6 @@ nnhip_status run_matmul(nnhip_ctx* ctx, const char* fn, const void* rp, const fl
     p.xlds = -1;
     p.glu = glu;
     p.glu_F = (int32_t)glu_F;
-    p.amax = amax;
     if (res && glu == 0 && M <= (size_t)kGemvMaxM && gemv_deep_ok(p, ctx->num_cus))
     {
         // the residual in the deep GEMV's epilogue
@@ -335,7 +307,6 @@ nnhip_status nnhip_ctx_destroy(nnhip_ctx* ctx)
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->amax) (void)hipFree(ctx->amax);
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
     if (ctx->ones) (void)hipFree(ctx->ones);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
@@ -1045,7 +1016,7 @@ nnhip_status nnhip_ternary_matmul_add(nnhip_ctx* ctx, const void* rp, const floa
     NNHIP_REQUIRE(rp && tau && xi && s && rowsum && res && Y, fn, "null pointer");
     NNHIP_REQUIRE(res != Y, fn, "res must not alias Y");
     NNHIP_REQUIRE(aligned16(rp) && aligned16(xi), fn, "rp and xi must be 16-byte aligned");
-    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y, 0, 0, nullptr, res);
+    return run_matmul(ctx, fn, rp, tau, xi, s, rowsum, bias, N, K, M, Y, 0, 0, res);
 }
 
 nnhip_status nnhip_ternary_matmul_partial(nnhip_ctx* ctx, const void* rp, const int8_t* xi, size_t N, size_t K,
@@ -1666,38 +1637,16 @@ static nnhip_status ffn_glu_i8(nnhip_ctx* ctx, const char* fn, const float* X, c
     int32_t* rs2 = reinterpret_cast<int32_t*>(take(M * 4));
     float* h = reinterpret_cast<float*>(take(F * M * 4));
     float* y1 = M <= (size_t)kGemvMaxM ? reinterpret_cast<float*>(take(nnhip_glu_rows(F) * M * 4)) : nullptr;
-    // prefill without SubLN: the gated GEMM epilogue leaves max |h| per token, so h is quantized
-    // in one streaming pass (the same scale and codes as the absmax kernel); with SubLN the
-    // fused RMSNorm -> absmax -> int8 kernel quantizes h
-    const bool fold = M > (size_t)kGemvMaxM && gamma_sub == nullptr;
-    if (fold)
-    {
-        st = ensure_amax(ctx, M, fn);
-        if (st != NNHIP_OK) return st;
-    }
+    // h is quantized by the fused [RMSNorm ->] absmax -> int8 kernel. (A per-token max |h| folded
+    // into fc1's epilogue, with h then quantized in one streaming pass, was slower once the
+    // absmax kernel read its rows in contiguous bands: C4 185.4 against 183.3 us, M=64 53.0
+    // against 46.6 us, M=16384 1192 against 1182 us, the same outputs.)
     NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, X, gamma, gamma != nullptr, eps, d, M, xi1, s1, rs1, nullptr));
-    if (fold)
-    {
-        st = run_matmul(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, nnhip_glu_rows(F), d, M, h, act + 1, F, ctx->amax);
-        if (st == NNHIP_OK)
-        {
-            const hipError_t e = launch_quant_amax(ctx->stream, h, F, M, ctx->amax, xi2, s2, rs2);
-            if (e != hipSuccess) st = hip_fail(fn, "kernel launch", e);
-        }
-        if (st != NNHIP_OK)
-        {
-            ctx->amax_words = 0;  // contents unknown: re-allocated and zero-filled by the next call
-            return st;
-        }
-    }
-    else
-    {
-        st = run_matmul_glu(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, F, d, M, act, y1, h);
-        if (st != NNHIP_OK) return st;
-        NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, gamma_sub, gamma_sub != nullptr, eps_sub, F, M, xi2, s2, rs2,
-                                          nullptr));
-    }
-    return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y, 0, 0, nullptr, res);
+    st = run_matmul_glu(ctx, fn, rp1, tau1, xi1, s1, rs1, b1, F, d, M, act, y1, h);
+    if (st != NNHIP_OK) return st;
+    NNHIP_LAUNCH(fn, launch_act_quant(ctx->stream, h, gamma_sub, gamma_sub != nullptr, eps_sub, F, M, xi2, s2, rs2,
+                                      nullptr));
+    return run_matmul(ctx, fn, rp2, tau2, xi2, s2, rs2, b2, d, F, M, Y, 0, 0, res);
 }
 
 nnhip_status nnhip_ffn_glu_i8(nnhip_ctx* ctx, const float* X, const float* gamma, float eps, size_t d, size_t F,

@@ -35,29 +35,15 @@ __device__ __forceinline__ float quant_rcp(float s)
     return s == 0.0f ? 0.0f : __fdiv_rn(1.0f, s);
 }
 
-// quantize_one(x, s) without a division in the common case. With r = fl(1/s) and
-// y = fl(x * r), |y - x/s| <= |x/s| * 2^-23 (two roundings), so |y - fl(x/s)| < 2^-15 for
-// |x/s| <= 128. Unless y lies within 2^-14 of a half-integer, round-to-nearest-even of y then
-// equals round-half-away-from-zero of fl(x/s) (no tie and no integer boundary in between), and
-// clamping after rounding equals clamping before (127 is an integer, and values past 127.5
-// round to 127 or more either way). Near a half-integer, for NaN and inf products and when 1/s
-// overflowed, `amb` is set and the caller takes quantize_exact; the code is the same bit for bit.
-__device__ __forceinline__ int quantize_guess(float x, float r, bool& amb)
-{
-    const float y = __fmul_rn(x, r);
-    const float t = __builtin_rintf(y);
-    amb |= !(fabsf(y - t) < 0.5f - 0x1p-14f);
-    return (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
-}
-
-// quantize_guess without the clamp and with half its margin, for callers whose scale comes from
-// the same elements. Range: with s = fl(amax * fl(1/127)) over them and r = fl(1/s) finite, every
-// |x| <= amax gives |fl(x * r)| <= 127 * (1 + 2^-20) < 127.5 (four roundings, one of them of s,
-// which is at least 2^-128 whenever 1/s is finite and so keeps 22 significant bits even when
-// subnormal), so rint(y) is already in [-127, 127]. Margin: |y - x/s| <= |x/s| * (2^-23 + 2^-48)
-// < 2^-16 and |fl(x/s) - x/s| <= 2^-17 below 128, so |y - fl(x/s)| < 3 * 2^-17; when y is
-// 2^-15 or more from every half-integer, fl(x/s) is on the same side of each, and rint(y) is
-// quantize_one's code. NaN, inf and near-tie products set `amb`.
+// quantize_one(x, s) without a division in the common case, for callers whose scale comes from
+// the same elements: with r = fl(1/s) and y = fl(x * r), when y is 2^-15 or more from every
+// half-integer, rint(y) is quantize_one's code (no tie and no integer boundary between y and
+// fl(x/s)), and no clamp is needed. Range: with s = fl(amax * fl(1/127)) over the elements and r
+// finite, every |x| <= amax gives |fl(x * r)| <= 127 * (1 + 2^-20) < 127.5 (four roundings, one of
+// them of s, which is at least 2^-128 whenever 1/s is finite and so keeps 22 significant bits even
+// when subnormal), so rint(y) is already in [-127, 127]. Margin: |y - x/s| <= |x/s| * (2^-23 +
+// 2^-48) < 2^-16 and |fl(x/s) - x/s| <= 2^-17 below 128, so |y - fl(x/s)| < 3 * 2^-17. NaN, inf
+// and near-tie products set `amb`, and the caller takes quantize_exact (the same code bit for bit).
 __device__ __forceinline__ int quantize_code(float x, float r, bool& amb)
 {
     const float y = __fmul_rn(x, r);
