@@ -93,9 +93,10 @@ nnhip_status nnhip_ctx_reset_stream(nnhip_ctx* ctx);
 nnhip_status nnhip_ctx_get_stream(nnhip_ctx* ctx, void** stream);
 
 /* Block tile of the prefill GEMM (M > 16 tokens): automatic (the default) picks, per call, the
- * tile with the fewest estimated block rounds over the CUs; the others force one tile. A tuning
- * control of this library (the reference's GEMM shader has a single 64 x 64 tile); results are
- * bit-identical whichever tile runs. */
+ * tile with the fewest estimated block rounds over the CUs, and may split the rows over two
+ * launches (256 x 128 blocks over whole rounds of the CUs, a smaller tile over the rest); the
+ * others force one tile for all rows. A tuning control of this library (the reference's GEMM
+ * shader has a single 64 x 64 tile); results are bit-identical whichever tile runs. */
 #define NNHIP_GEMM_TILE_AUTO 0
 #define NNHIP_GEMM_TILE_256x128 1
 #define NNHIP_GEMM_TILE_128x128 2
