@@ -62,9 +62,9 @@ constexpr int kRsrcFlags = 0x00020000;
 constexpr int kGemmYPolicy = kPolicyNT;
 // The gated epilogue's h is read by the next quantizer. When h fits well inside the 256 MiB
 // memory-side cache (kGemmHKeepBytes) it is written through (sc0 sc1) so that it stays there:
-// C4's h (6912 x 2048, 57 MB) then quantizes in 21.1-21.2 instead of 30.6-30.8 us and the block
-// takes 188-189 instead of 197 us, fc1 unchanged within noise. Larger h (C5's prefill at 32768
-// tokens, 906 MB) stays non-temporal: written through, the prefill took 0.5 ms longer.
+// the quantization of C4's h (6912 x 2048, 57 MB) took 21.1-21.2 instead of 30.6-30.8 us after
+// it (same-box A/B), fc1 unchanged within noise. Larger h (C5's prefill at 32768 tokens, 906 MB)
+// stays non-temporal: written through, the prefill took 0.5 ms longer.
 constexpr size_t kGemmHKeepBytes = size_t(128) << 20;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -150,7 +150,6 @@ struct Gemm
     static constexpr int kPartBytes = kRB / 2 * kTB * 4096;
     static constexpr int kRingBytes = kSlots * kSlotBytes;
     static constexpr int kLdsMain = kKSplit == 2 && kWaves * kPartBytes > kRingBytes ? kWaves * kPartBytes : kRingBytes;
-    // gated epilogue: per-token max |h| of each (wn, ks) wave row, reduced across the block
     static constexpr int kLdsBytes = kLdsMain;
     // DMA instructions per wave per stage: A one row tile (1 KiB) each, B four token rows each
     // Waves 0 .. kDmaWaves-1 issue the DMA (with the default k split, the first wave of each pair:
@@ -752,8 +751,8 @@ namespace
 {
 
 // The rows [rows0, N) of p as a problem of their own: the weight row tiles, the per-row scales,
-// bias and residual, and the output rows move; the per-token inputs (codes, scales, row sums, the
-// absmax slots) are shared. rows0 is a multiple of 256 (16 row tiles; 128 gated features).
+// bias and residual, and the output rows move; the per-token inputs (codes, scales, row sums) are
+// shared. rows0 is a multiple of 256 (16 row tiles; 128 gated features).
 GemvProblem gemm_rows_from(const GemvProblem& p, int rows0)
 {
     GemvProblem q = p;
