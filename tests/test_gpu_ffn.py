@@ -177,11 +177,10 @@ def test_ffn_block_c4_sampled_tokens(ctx, orc):
 
 
 def test_ffn_block_repeat_and_special_h(ctx, orc):
-    """The prefill block carries max |h| per token from the fc1 epilogue to the second
-    quantization in a buffer of the context that each call must leave at zero: consecutive
-    calls on one context (a smaller M after a larger one, inputs of other magnitudes) each
-    match the oracle. The last call has a fc1 bias with NaN and inf entries, so h holds NaN
-    (ignored by the absmax, quantized to 0) and inf (scale inf, codes 0)."""
+    """Consecutive prefill-block calls on one context (a smaller M after a larger one, inputs of
+    other magnitudes; the context's workspace is reused) each match the oracle. The last call
+    has a fc1 bias with NaN and inf entries, so h holds NaN (ignored by the absmax, quantized to
+    0) and inf (scale inf, codes 0)."""
     d, F = 256, 136
     wq1, t1, b1, wq2, t2, b2 = block_case(orc, d, F, 900)
     rp1, to, bo = prepare_fc1(ctx, wq1, t1, b1, F, d)
@@ -223,12 +222,14 @@ def test_ffn_block_each_tile(ctx, orc, tile):
     assert same_bits(Y, Y_ref)
 
 
-def test_ffn_block_split_rows(ctx, orc):
-    """fc1 of 2F = 4608 interleaved rows at 2048 tokens: on a 256-CU device the automatic tile
-    choice runs 256 x 128 blocks over the first 4096 rows (features 0..2047) and 128 x 128 blocks
-    over the rest, the per-token absmax of h folded by both launches. The block against the
-    oracle on every token, h the same bits as under the 256 x 128 tile alone."""
-    d, F, M = 256, 2304, 2048
+@pytest.mark.parametrize("F,M", [(2304, 2048), (2300, 2000)])
+def test_ffn_block_split_rows(ctx, orc, F, M):
+    """fc1 of F gated features (2F interleaved rows) at about 2048 tokens: on a 256-CU device the
+    automatic tile choice runs 256 x 128 blocks over the first 4096 rows (features 0..2047) and a
+    smaller tile over the rest (F = 2300, M = 2000: the last features and tokens end inside a
+    block). The block against the oracle on every token, h the same bits as under the 256 x 128
+    tile alone."""
+    d = 256
     say(f"ffn_glu_i8 split rows d={d} F={F} M={M}")
     wq1, t1, b1, wq2, t2, b2 = block_case(orc, d, F, 960)
     X = normal((d, M), 961, 0.0, 1.0)

@@ -485,11 +485,13 @@ def test_prefill_gemm_each_tile(ctx, orc, tile, N, K, M):
     assert np.array_equal(Y[rows], ref)
 
 
-@pytest.mark.parametrize("N,K,M", [(4608, 768, 2048), (11008, 1024, 1024), (2560, 520, 4096)])
+@pytest.mark.parametrize("N,K,M", [(4608, 768, 2048), (11008, 1024, 1024), (2560, 520, 4096), (4615, 520, 2000)])
 def test_prefill_gemm_split_rows(ctx, orc, N, K, M):
     """Shapes on which the automatic tile choice splits the rows on a 256-CU device: 256 x 128
-    blocks over the rows that fill whole rounds (4096, 8192 and 2048 rows here), the rest in a
-    second launch of 128 x 128 blocks. Every row against the oracle, with a bias; the same bits
+    blocks over the rows that fill whole rounds (4096, 8192, 2048 and 4096 rows here), the rest in
+    a second launch of 64 x 64 (the first) or 128 x 128 blocks; (4615, 520, 2000) ends both
+    launches' last blocks inside the tile (rows and tokens). Every row against the oracle, with a
+    bias; the same bits
     as the 256 x 128 tile over all rows; and the residual epilogue (the rows' residual moves
     with them) the same bits as add(res, ternary_matmul)."""
     say(f"gemm split N={N} K={K} M={M}")
